@@ -1,0 +1,202 @@
+"""GPU parity of the GGUF dequant / GEMV path against the CPU oracle.
+
+Tolerances: block dequantization bit-exact; GEMV
+outputs within 1e-3 relative error, measured as max|gpu-ref| / max|ref| per
+activation row (fp32 accumulation on both sides; only the summation order
+differs).  The Q8_0 activation codes are additionally required to be
+bit-identical, since the GPU restates the CPU coding exactly.
+"""
+import numpy as np
+import pytest
+
+import zg_oracle as O
+from zerogravity_amd import _lib as L
+from zerogravity_amd import regions as R
+from zerogravity_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(3584, 1024), (1024, 3584), (6144, 2048), (2048, 6144), (151936, 2048)]
+KINDS = [synth.Q8_0, synth.Q4_K]
+REL_TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def kern():
+    k = R.HipMatVecKernel(0)
+    yield k
+    k.ctx.close()
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    assert torch.cuda.is_available()
+    return torch
+
+
+_weights = {}
+_streams = []
+
+
+def _stream(torch):
+    """A non-null torch stream (default priority) shared with the launches."""
+    if not _streams:
+        _streams.append(torch.cuda.Stream())
+    s = _streams[0]
+    torch.cuda.set_stream(s)
+    return s.cuda_stream
+
+
+def weight(kern, kind, N, K, seed=1):
+    key = (kind, N, K, seed)
+    if key not in _weights:
+        rng = np.random.default_rng(seed * 1000 + N + K + kind)
+        w = synth.random_matrix(rng, kind, N, K)
+        h = kern.register(77, f"w.{kind}.{N}.{K}.{seed}", kind, K, N, w)
+        _weights[key] = (w, h)
+    return _weights[key]
+
+
+def rel_err(got, ref):
+    return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def row_subset(N):
+    if N <= 8192:
+        return [np.arange(N)]
+    return [np.arange(2048), np.arange(N - 2048, N)]
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("N,K", [(64, 1024), (3584, 1024), (256, 6144)])
+def test_dequantize_bit_exact(kern, kind, N, K):
+    w, h = weight(kern, kind, N, K)
+    dev = h.dequantize()
+    ref = O.dequantize(kind, w.reshape(-1), N * K).reshape(N, K)
+    assert np.array_equal(dev.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("N,K", SHAPES)
+def test_matvec_region_matches_oracle(kern, kind, N, K):
+    w, _ = weight(kern, kind, N, K)
+    x = np.random.default_rng(N + K).standard_normal(K).astype(np.float32)
+    region = R.MatVecRegion(R.SourceIdentity(77), f"w.{kind}.{N}.{K}.1", kind, K, N, w.reshape(-1), x)
+    res = kern.try_execute(region)
+    assert isinstance(res, R.Completed)
+    R.validate_completed(region, res.values)
+    for rows in row_subset(N):
+        ref = O.matvec(kind, w[rows].reshape(-1), rows.size, K, x)
+        assert rel_err(res.values[rows], ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("N,K", SHAPES)
+@pytest.mark.parametrize("M", [1, 4, 16, 32])
+def test_gemv_device_rms_prologue_bf16(kern, torch_cuda, kind, N, K, M):
+    torch = torch_cuda
+    w, h = weight(kern, kind, N, K)
+    rng = np.random.default_rng(M * 7 + N)
+    xf, xb = synth.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    gamma = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    x_d = torch.from_numpy(xb.view(np.int16)).cuda()
+    g_d = torch.from_numpy(gamma).cuda()
+    y_d = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    stream = _stream(torch)
+    rc = L.lib().zg_gemv_device(kern.ctx.h, h.h, x_d.data_ptr(), L.BF16, M, g_d.data_ptr(), 1e-6,
+                                y_d.data_ptr(), stream)
+    kern.ctx.check(rc)
+    torch.cuda.synchronize()
+    y = y_d.cpu().numpy()
+    assert np.isfinite(y).all()
+    worst = 0.0
+    for m in range(M):
+        xn = O.rms_norm(xf[m], gamma, 1e-6)
+        for rows in row_subset(N):
+            ref = O.matvec(kind, w[rows].reshape(-1), rows.size, K, xn)
+            worst = max(worst, rel_err(y[m, rows], ref))
+    assert worst <= REL_TOL, worst
+
+
+def test_q8_activation_codes_bit_exact(kern, torch_cuda):
+    torch = torch_cuda
+    rng = np.random.default_rng(5)
+    M, K = 4, 2048
+    xf, xb = synth.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    gamma = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    x_d = torch.from_numpy(xb.view(np.int16)).cuda()
+    g_d = torch.from_numpy(gamma).cuda()
+    xn_d = torch.empty((M, K), dtype=torch.float32, device="cuda")
+    q_d = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    s_d = torch.empty((M, K // 32), dtype=torch.float32, device="cuda")
+    stream = _stream(torch)
+    kern.ctx.check(L.lib().zg_act_prepare_device(kern.ctx.h, x_d.data_ptr(), L.BF16, M, K, g_d.data_ptr(), 1e-6,
+                                                 xn_d.data_ptr(), q_d.data_ptr(), s_d.data_ptr(), stream))
+    torch.cuda.synchronize()
+    for m in range(M):
+        xn = O.rms_norm(xf[m], gamma, 1e-6)
+        qs, d, _ = O.q8_activation(xn)
+        assert np.array_equal(xn_d[m].cpu().numpy().view(np.uint32), xn.view(np.uint32))
+        assert np.array_equal(q_d[m].cpu().numpy(), qs)
+        assert np.array_equal(s_d[m].cpu().numpy().view(np.uint32), d.view(np.uint32))
+
+
+def test_region_refusals(kern):
+    x = np.ones(32, np.float32)
+    w = np.zeros(34, np.uint8)
+    # unsupported codec -> Unsupported (caller may use its CPU path)
+    r = R.MatVecRegion(R.SourceIdentity(5), "t.q6k", 14, 256, 1, np.zeros(210, np.uint8), np.ones(256, np.float32))
+    assert kern.try_execute(r) is R.UNSUPPORTED
+    # nonfinite activation -> error
+    bad = R.MatVecRegion(R.SourceIdentity(5), "t.q8", synth.Q8_0, 32, 1, w, np.full(32, np.nan, np.float32))
+    with pytest.raises(L.ZgError):
+        kern.try_execute(bad)
+    # nonfinite block scale -> error (codecs/q8.rs:6-15)
+    w2 = w.copy()
+    w2[0:2] = [0x00, 0x7C]
+    with pytest.raises(L.ZgError):
+        kern.try_execute(R.MatVecRegion(R.SourceIdentity(0), "t.q8inf", synth.Q8_0, 32, 1, w2, x))
+    # byte length mismatch -> error
+    with pytest.raises(L.ZgError):
+        kern.try_execute(R.MatVecRegion(R.SourceIdentity(5), "t.q8short", synth.Q8_0, 32, 1, w[:33], x))
+    # unbound identity cannot key a resident weight
+    with pytest.raises(L.ZgError):
+        kern.register(0, "t.unbound", synth.Q8_0, 32, 1, w)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_embedding_region_matches_codec(kern, kind):
+    rng = np.random.default_rng(3)
+    V, H = 1000, 1024 if kind == synth.Q8_0 else 2048
+    w = synth.random_matrix(rng, kind, V, H)
+    for sid in (0, 91):
+        for token in (0, 17, V - 1):
+            r = R.EmbeddingRegion(R.SourceIdentity(sid), "token_embd.weight", kind, w.reshape(-1), token, H, V)
+            res = kern.try_embedding(r)
+            ref = O.dequantize(kind, w[token], H)
+            assert np.array_equal(res.values.view(np.uint32), ref.view(np.uint32))
+    with pytest.raises(L.ZgError):
+        kern.try_embedding(R.EmbeddingRegion(R.SourceIdentity(91), "token_embd.weight", kind, w.reshape(-1), V, H, V))
+
+
+def test_pointwise_regions_match_oracle(kern):
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal(2048).astype(np.float32) * 3
+    m = rng.standard_normal(2048).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    # RMS: bit-exact (same f32 rounding points; f64 sum of 2048 f32 squares)
+    r = kern.try_rms_norm(R.RmsNormRegion(R.SourceIdentity(1), "n", x, np.ones(2048, np.float32), 1e-6))
+    assert np.array_equal(r.values.view(np.uint32), O.rms_norm(x, np.ones(2048, np.float32), 1e-6).view(np.uint32))
+    r = kern.try_grouped_rms_norm(R.GroupedRmsNormRegion(R.SourceIdentity(1), "g", x, g, 128, 16, 1e-6))
+    assert np.array_equal(r.values.view(np.uint32), O.grouped_rms_norm(x, g, 16, 1e-6).view(np.uint32))
+    # SiLU: polynomial exp with explicit FMAs -> bit-exact
+    r = kern.try_silu(R.SiluRegion(R.SourceIdentity(1), "s", x, m))
+    assert np.array_equal(r.values.view(np.uint32), O.silu(x, m).view(np.uint32))
+    r = kern.try_silu(R.SiluRegion(R.SourceIdentity(1), "s", x))
+    assert np.array_equal(r.values.view(np.uint32), O.silu(x).view(np.uint32))
+    # Add bit-exact; SigmoidGate uses device expf (1e-6 relative)
+    r = kern.try_binary(R.BinaryRegion(R.SourceIdentity(1), "a", 0, x, m))
+    assert np.array_equal(r.values.view(np.uint32), O.binary(0, x, m).view(np.uint32))
+    r = kern.try_binary(R.BinaryRegion(R.SourceIdentity(1), "b", 1, x, m))
+    np.testing.assert_allclose(r.values, O.binary(1, x, m), rtol=2e-6, atol=1e-30)

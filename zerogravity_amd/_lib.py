@@ -1,0 +1,102 @@
+"""ctypes binding of libzg_hip.so (the gfx950 backend).
+
+There is no CPU fallback anywhere in this package: if the HIP library is not
+built, or no GPU is visible, these functions raise.
+"""
+import ctypes as C
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libzg_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "zg_hip.h")
+
+COMPLETED, UNSUPPORTED = 0, 1
+E_MALFORMED, E_UNSUPPORTED, E_RESOURCE, E_LIMIT, E_STATE, E_DEVICE = -1, -2, -3, -4, -5, -6
+F32, F16, Q8_0, Q4_K, BF16 = 0, 1, 8, 12, 30
+
+_lib = None
+P = C.c_void_p
+SZ = C.c_size_t
+FP = C.POINTER(C.c_float)
+
+_SIGS = {
+    "zg_version": (C.c_char_p, []),
+    "zg_ctx_create": (C.c_int, [C.c_int, C.POINTER(P)]),
+    "zg_ctx_destroy": (None, [P]),
+    "zg_last_error": (C.c_char_p, [P]),
+    "zg_weight_register": (C.c_int, [P, C.c_uint64, C.c_char_p, C.c_int, SZ, SZ, P, SZ, C.POINTER(P)]),
+    "zg_source_release": (C.c_int, [P, C.c_uint64]),
+    "zg_weight_device_bytes": (SZ, [P]),
+    "zg_weight_dequantize": (C.c_int, [P, P, P, SZ]),
+    "zg_matvec": (C.c_int, [P, C.c_uint64, C.c_char_p, C.c_int, SZ, SZ, P, SZ, P, SZ, P, SZ]),
+    "zg_embedding": (C.c_int, [P, C.c_uint64, C.c_char_p, C.c_int, P, SZ, C.c_uint32, SZ, SZ, P, SZ]),
+    "zg_rms_norm": (C.c_int, [P, P, P, SZ, C.c_float, P]),
+    "zg_grouped_rms_norm": (C.c_int, [P, P, P, SZ, SZ, C.c_float, P]),
+    "zg_silu": (C.c_int, [P, P, P, SZ, P]),
+    "zg_binary": (C.c_int, [P, C.c_int, P, P, SZ, P]),
+    "zg_gemv_device": (C.c_int, [P, P, P, C.c_int, SZ, P, C.c_float, P, P]),
+    "zg_act_prepare_device": (C.c_int, [P, P, C.c_int, SZ, SZ, P, C.c_float, P, P, P, P]),
+    "zg_gemv_prepared_device": (C.c_int, [P, P, SZ, P, P, P, P, P]),
+}
+
+
+def header_symbols():
+    """Every function the public header declares."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(zg_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        # One HIP runtime per process: when torch (which ships its own
+        # libamdhip64) is importable, load it first so this library binds to
+        # the same runtime instead of pulling in a second one.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build the HIP backend first (python -c 'import __graft_entry__ as g; g.build()')")
+        _lib = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(_lib, name)
+            fn.restype = res
+            fn.argtypes = args
+    return _lib
+
+
+class ZgError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"zg status {code}: {msg}")
+        self.code = code
+
+
+class Context:
+    """One device context (zg_ctx) with its own stream and weight cache."""
+
+    def __init__(self, device=0):
+        h = P()
+        rc = lib().zg_ctx_create(device, C.byref(h))
+        if rc != COMPLETED:
+            raise ZgError(rc, "zg_ctx_create failed (no usable HIP device?)")
+        self.h = h
+
+    def error(self):
+        return lib().zg_last_error(self.h).decode()
+
+    def check(self, rc):
+        if rc < 0:
+            raise ZgError(rc, self.error())
+        return rc
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().zg_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()

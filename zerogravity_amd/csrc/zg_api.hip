@@ -1,0 +1,453 @@
+// C ABI of the gfx950 backend (include/zg_hip.h): context, resident weight
+// cache, boundary-A region entry points and the device GEMV API.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "zg_hip.h"
+#include "zg_internal.hpp"
+
+struct zg_weight {
+    zg::DeviceWeight dw;
+    uint64_t source = 0;
+    std::string name;
+};
+
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+struct zg_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::mutex mu;
+    std::string err;
+    std::map<std::tuple<uint64_t, std::string, int, size_t, size_t>, std::unique_ptr<zg_weight>> weights;
+    DeviceBuffer scratch;    // region calls: inputs/outputs staged here
+    DeviceBuffer actbuf;     // zg_gemv_device: prepared activations
+    int* d_flag = nullptr;
+};
+
+namespace {
+
+int fail(zg_ctx* ctx, int code, const std::string& msg) {
+    if (ctx) ctx->err = msg;
+    return code;
+}
+
+#define ZG_HIP(expr)                                                                               \
+    do {                                                                                           \
+        hipError_t e_ = (expr);                                                                    \
+        if (e_ != hipSuccess)                                                                      \
+            return fail(ctx, ZG_E_DEVICE, std::string(#expr) + " failed: " + hipGetErrorString(e_)); \
+    } while (0)
+
+bool all_finite(const float* x, size_t n) {
+    for (size_t i = 0; i < n; ++i)
+        if (!std::isfinite(x[i])) return false;
+    return true;
+}
+
+int ensure(zg_ctx* ctx, DeviceBuffer& b, size_t bytes) {
+    if (b.bytes >= bytes) return ZG_COMPLETED;
+    if (b.ptr) {
+        ZG_HIP(hipStreamSynchronize(ctx->stream));
+        ZG_HIP(hipFree(b.ptr));
+        b.ptr = nullptr;
+        b.bytes = 0;
+    }
+    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+    ZG_HIP(hipMalloc(&b.ptr, want));
+    b.bytes = want;
+    return ZG_COMPLETED;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+void free_weight(zg_weight* w) {
+    if (!w) return;
+    if (w->dw.qs) (void)hipFree(w->dw.qs);
+    if (w->dw.hdr) (void)hipFree(w->dw.hdr);
+    w->dw.qs = w->dw.hdr = nullptr;
+}
+
+bool supported_type(int t) { return t == ZG_Q8_0 || t == ZG_Q4_K || t == ZG_F32; }
+
+size_t block_elems(int t) { return t == ZG_Q8_0 ? 32 : t == ZG_Q4_K ? 256 : 1; }
+
+// Upload and split one GGUF matrix.  Caller holds the ctx lock.
+int build_weight(zg_ctx* ctx, int type, size_t cols, size_t rows, const void* bytes, size_t len,
+                 std::unique_ptr<zg_weight>& out) {
+    auto w = std::make_unique<zg_weight>();
+    w->dw.type = type;
+    w->dw.K = cols;
+    w->dw.N = rows;
+    if (type == ZG_Q8_0) {
+        w->dw.qs_bytes = rows * cols;
+        w->dw.hdr_bytes = rows * (cols / 32) * 2;
+    } else if (type == ZG_Q4_K) {
+        w->dw.qs_bytes = rows * (cols / 2);
+        w->dw.hdr_bytes = rows * (cols / 256) * 16;
+    } else {
+        w->dw.qs_bytes = rows * cols * 4;
+        w->dw.hdr_bytes = 0;
+    }
+    void* staging = nullptr;
+    ZG_HIP(hipMalloc(&w->dw.qs, w->dw.qs_bytes));
+    if (w->dw.hdr_bytes) ZG_HIP(hipMalloc(&w->dw.hdr, w->dw.hdr_bytes));
+    hipError_t e = hipMalloc(&staging, len);
+    if (e != hipSuccess) {
+        free_weight(w.get());
+        return fail(ctx, ZG_E_RESOURCE, std::string("weight staging allocation: ") + hipGetErrorString(e));
+    }
+    ZG_HIP(hipMemsetAsync(ctx->d_flag, 0, sizeof(int), ctx->stream));
+    ZG_HIP(hipMemcpyAsync(staging, bytes, len, hipMemcpyHostToDevice, ctx->stream));
+    ZG_HIP(zg::repack_weight((const uint8_t*)staging, w->dw, ctx->d_flag, ctx->stream));
+    int bad = 0;
+    ZG_HIP(hipMemcpyAsync(&bad, ctx->d_flag, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
+    ZG_HIP(hipStreamSynchronize(ctx->stream));
+    ZG_HIP(hipFree(staging));
+    if (bad) {
+        free_weight(w.get());
+        return fail(ctx, ZG_E_MALFORMED, "nonfinite GGUF block scale");
+    }
+    out = std::move(w);
+    return ZG_COMPLETED;
+}
+
+int check_matrix(zg_ctx* ctx, int type, size_t cols, size_t rows, const void* bytes, size_t len) {
+    if (!bytes || cols == 0 || rows == 0 || rows > 1000000)
+        return fail(ctx, ZG_E_MALFORMED, "invalid matrix geometry");
+    if (!supported_type(type)) return fail(ctx, ZG_UNSUPPORTED, "ggml type not offered by this backend");
+    if (cols % block_elems(type)) return fail(ctx, ZG_E_MALFORMED, "row not aligned to whole blocks");
+    if (zg::gguf_row_bytes(type, cols) * rows != len) return fail(ctx, ZG_E_MALFORMED, "packed byte length mismatch");
+    return ZG_COMPLETED;
+}
+
+int lookup_or_register(zg_ctx* ctx, uint64_t source, const char* name, int type, size_t cols, size_t rows,
+                       const void* bytes, size_t len, zg_weight** out) {
+    auto key = std::make_tuple(source, std::string(name), type, cols, rows);
+    auto it = ctx->weights.find(key);
+    if (it != ctx->weights.end()) {
+        *out = it->second.get();
+        return ZG_COMPLETED;
+    }
+    std::unique_ptr<zg_weight> w;
+    int rc = build_weight(ctx, type, cols, rows, bytes, len, w);
+    if (rc != ZG_COMPLETED) return rc;
+    w->source = source;
+    w->name = name;
+    *out = w.get();
+    ctx->weights.emplace(key, std::move(w));
+    return ZG_COMPLETED;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* zg_version(void) { return "zerogravity_amd 0.1.0 (gfx950)"; }
+
+int zg_ctx_create(int device, zg_ctx** out) {
+    if (!out) return ZG_E_MALFORMED;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return ZG_E_DEVICE;
+    if (hipSetDevice(device) != hipSuccess) return ZG_E_DEVICE;
+    auto ctx = new zg_ctx();
+    ctx->device = device;
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipMalloc(&ctx->d_flag, sizeof(int)) != hipSuccess) {
+        delete ctx;
+        return ZG_E_DEVICE;
+    }
+    *out = ctx;
+    return ZG_COMPLETED;
+}
+
+void zg_ctx_destroy(zg_ctx* ctx) {
+    if (!ctx) return;
+    {
+        std::lock_guard<std::mutex> g(ctx->mu);
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+        for (auto& kv : ctx->weights) free_weight(kv.second.get());
+        ctx->weights.clear();
+        if (ctx->scratch.ptr) (void)hipFree(ctx->scratch.ptr);
+        if (ctx->actbuf.ptr) (void)hipFree(ctx->actbuf.ptr);
+        if (ctx->d_flag) (void)hipFree(ctx->d_flag);
+        (void)hipStreamDestroy(ctx->stream);
+    }
+    delete ctx;
+}
+
+const char* zg_last_error(const zg_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+int zg_weight_register(zg_ctx* ctx, uint64_t source_id, const char* name, int ggml_type, size_t columns,
+                       size_t rows, const void* bytes, size_t len, zg_weight** out) {
+    if (!ctx || !out || !name || !*name) return fail(ctx, ZG_E_MALFORMED, "invalid registration arguments");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (source_id == 0) return fail(ctx, ZG_E_MALFORMED, "unbound source identity cannot key a resident weight");
+    int rc = check_matrix(ctx, ggml_type, columns, rows, bytes, len);
+    if (rc == ZG_UNSUPPORTED) return fail(ctx, ZG_E_UNSUPPORTED, ctx->err);
+    if (rc != ZG_COMPLETED) return rc;
+    return lookup_or_register(ctx, source_id, name, ggml_type, columns, rows, bytes, len, out);
+}
+
+int zg_source_release(zg_ctx* ctx, uint64_t source_id) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    ZG_HIP(hipStreamSynchronize(ctx->stream));
+    for (auto it = ctx->weights.begin(); it != ctx->weights.end();) {
+        if (std::get<0>(it->first) == source_id) {
+            free_weight(it->second.get());
+            it = ctx->weights.erase(it);
+        } else {
+            ++it;
+        }
+    }
+    return ZG_COMPLETED;
+}
+
+size_t zg_weight_device_bytes(const zg_weight* w) { return w ? w->dw.qs_bytes + w->dw.hdr_bytes : 0; }
+
+int zg_weight_dequantize(zg_ctx* ctx, const zg_weight* w, float* out, size_t out_len) {
+    if (!ctx || !w || !out) return fail(ctx, ZG_E_MALFORMED, "invalid arguments");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    const size_t n = w->dw.N * w->dw.K;
+    if (out_len != n) return fail(ctx, ZG_E_MALFORMED, "output length mismatch");
+    int rc = ensure(ctx, ctx->scratch, n * 4);
+    if (rc) return rc;
+    ZG_HIP(zg::dequantize_rows(w->dw, 0, w->dw.N, (float*)ctx->scratch.ptr, ctx->stream));
+    ZG_HIP(hipMemcpyAsync(out, ctx->scratch.ptr, n * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ZG_HIP(hipStreamSynchronize(ctx->stream));
+    return ZG_COMPLETED;
+}
+
+int zg_matvec(zg_ctx* ctx, uint64_t source_id, const char* tensor_name, int ggml_type, size_t columns, size_t rows,
+              const void* packed_weights, size_t packed_len, const float* activation, size_t activation_len,
+              float* out, size_t out_len) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!tensor_name || !*tensor_name || !activation || !out || activation_len != columns || out_len != rows)
+        return fail(ctx, ZG_E_MALFORMED, "invalid matvec region");
+    int rc = check_matrix(ctx, ggml_type, columns, rows, packed_weights, packed_len);
+    if (rc != ZG_COMPLETED) return rc;
+    if (!all_finite(activation, columns)) return fail(ctx, ZG_E_MALFORMED, "nonfinite GEMV input");
+    if (!zg::gemv_supported(ggml_type, columns, 1)) return fail(ctx, ZG_UNSUPPORTED, "geometry not offered");
+    zg_weight* w = nullptr;
+    std::unique_ptr<zg_weight> temp;
+    if (source_id != 0) {
+        rc = lookup_or_register(ctx, source_id, tensor_name, ggml_type, columns, rows, packed_weights, packed_len, &w);
+        if (rc) return rc;
+    } else {
+        rc = build_weight(ctx, ggml_type, columns, rows, packed_weights, packed_len, temp);
+        if (rc) return rc;
+        w = temp.get();
+    }
+    const size_t ox = 0, oq = align256(columns * 4), od = oq + align256(columns), oy = od + align256(columns / 32 * 4 + 4);
+    rc = ensure(ctx, ctx->scratch, oy + align256(rows * 4));
+    if (rc) {
+        free_weight(temp.get());
+        return rc;
+    }
+    char* base = (char*)ctx->scratch.ptr;
+    float* xf = (float*)(base + ox);
+    int8_t* aq = (int8_t*)(base + oq);
+    float* ad = (float*)(base + od);
+    float* y = (float*)(base + oy);
+    ZG_HIP(hipMemcpyAsync(xf, activation, columns * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (ggml_type == ZG_Q8_0) ZG_HIP(zg::act_prep(xf, 0, 1, columns, nullptr, 0.0f, nullptr, aq, ad, ctx->stream));
+    ZG_HIP(zg::gemv(w->dw, 1, xf, aq, ad, y, ctx->stream));
+    ZG_HIP(hipMemcpyAsync(out, y, rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ZG_HIP(hipStreamSynchronize(ctx->stream));
+    free_weight(temp.get());
+    if (!all_finite(out, rows)) return fail(ctx, ZG_E_STATE, std::string("nonfinite result from matrix '") + tensor_name + "'");
+    return ZG_COMPLETED;
+}
+
+int zg_embedding(zg_ctx* ctx, uint64_t source_id, const char* tensor_name, int ggml_type, const void* packed_weights,
+                 size_t packed_len, uint32_t token, size_t width, size_t vocabulary, float* out, size_t out_len) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!tensor_name || !*tensor_name || !out || out_len != width || width == 0 || vocabulary == 0 || token >= vocabulary)
+        return fail(ctx, ZG_E_MALFORMED, "invalid original source embedding region");
+    int rc = check_matrix(ctx, ggml_type, width, vocabulary, packed_weights, packed_len);
+    if (rc != ZG_COMPLETED) return rc;
+    zg_weight* w = nullptr;
+    std::unique_ptr<zg_weight> temp;
+    if (source_id != 0) {
+        rc = lookup_or_register(ctx, source_id, tensor_name, ggml_type, width, vocabulary, packed_weights, packed_len, &w);
+        if (rc) return rc;
+    } else {
+        // Unbound: upload only the selected row.
+        const size_t rb = zg::gguf_row_bytes(ggml_type, width);
+        rc = build_weight(ctx, ggml_type, width, 1, (const char*)packed_weights + (size_t)token * rb, rb, temp);
+        if (rc) return rc;
+        w = temp.get();
+        token = 0;
+    }
+    rc = ensure(ctx, ctx->scratch, width * 4);
+    if (rc) return rc;
+    ZG_HIP(zg::dequantize_rows(w->dw, token, 1, (float*)ctx->scratch.ptr, ctx->stream));
+    ZG_HIP(hipMemcpyAsync(out, ctx->scratch.ptr, width * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ZG_HIP(hipStreamSynchronize(ctx->stream));
+    free_weight(temp.get());
+    if (!all_finite(out, width)) return fail(ctx, ZG_E_STATE, "incomplete/nonfinite source embedding proposal");
+    return ZG_COMPLETED;
+}
+
+}  // extern "C"
+
+// Shared driver for the pointwise regions: upload n-float inputs, run, read back.
+namespace {
+template <typename F>
+int run_pointwise(zg_ctx* ctx, size_t n_in, const float* const* ins, const size_t* lens, size_t n_out, float* out,
+                  F launch) {
+    size_t off[4] = {0, 0, 0, 0}, total = 0;
+    for (size_t i = 0; i < n_in; ++i) {
+        off[i] = total;
+        total += align256(lens[i] * 4);
+    }
+    const size_t oo = total;
+    total += align256(n_out * 4);
+    int rc = ensure(ctx, ctx->scratch, total);
+    if (rc) return rc;
+    char* base = (char*)ctx->scratch.ptr;
+    const float* dev[4] = {nullptr, nullptr, nullptr, nullptr};
+    for (size_t i = 0; i < n_in; ++i) {
+        if (ins[i]) {
+            ZG_HIP(hipMemcpyAsync(base + off[i], ins[i], lens[i] * 4, hipMemcpyHostToDevice, ctx->stream));
+            dev[i] = (const float*)(base + off[i]);
+        }
+    }
+    ZG_HIP(launch(dev, (float*)(base + oo)));
+    ZG_HIP(hipMemcpyAsync(out, base + oo, n_out * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ZG_HIP(hipStreamSynchronize(ctx->stream));
+    return ZG_COMPLETED;
+}
+}  // namespace
+
+extern "C" {
+
+int zg_rms_norm(zg_ctx* ctx, const float* input, const float* weights, size_t n, float eps, float* out) {
+    return zg_grouped_rms_norm(ctx, input, weights, n, 1, eps, out);
+}
+
+int zg_grouped_rms_norm(zg_ctx* ctx, const float* input, const float* weights, size_t width, size_t groups, float eps,
+                        float* out) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!input || !weights || !out || width == 0 || groups == 0 || !std::isfinite(eps) || eps <= 0.0f)
+        return fail(ctx, ZG_E_MALFORMED, "invalid grouped RMS normalization dimensions");
+    if (!all_finite(input, width * groups)) return fail(ctx, ZG_E_MALFORMED, "nonfinite RMSNorm input");
+    const float* ins[2] = {input, weights};
+    const size_t lens[2] = {width * groups, width};
+    int rc = run_pointwise(ctx, 2, ins, lens, width * groups, out, [&](const float* const* d, float* o) {
+        return zg::rms_groups(d[0], d[1], width, groups, eps, o, ctx->stream);
+    });
+    if (rc) return rc;
+    if (!all_finite(out, width * groups)) return fail(ctx, ZG_E_STATE, "physical normalization output malformed");
+    return ZG_COMPLETED;
+}
+
+int zg_silu(zg_ctx* ctx, const float* input, const float* multiplier, size_t n, float* out) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!input || !out || n == 0 || !all_finite(input, n) || (multiplier && !all_finite(multiplier, n)))
+        return fail(ctx, ZG_E_MALFORMED, "invalid source SiLU inputs");
+    const float* ins[2] = {input, multiplier};
+    const size_t lens[2] = {n, multiplier ? n : 0};
+    int rc = run_pointwise(ctx, 2, ins, lens, n, out, [&](const float* const* d, float* o) {
+        return zg::silu(d[0], d[1], n, o, ctx->stream);
+    });
+    if (rc) return rc;
+    if (!all_finite(out, n)) return fail(ctx, ZG_E_STATE, "physical SiLU output malformed");
+    return ZG_COMPLETED;
+}
+
+int zg_binary(zg_ctx* ctx, int kind, const float* left, const float* right, size_t n, float* out) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!left || !right || !out || n == 0 || (kind != 0 && kind != 1) || !all_finite(left, n) || !all_finite(right, n))
+        return fail(ctx, ZG_E_MALFORMED, "invalid source binary region");
+    const float* ins[2] = {left, right};
+    const size_t lens[2] = {n, n};
+    int rc = run_pointwise(ctx, 2, ins, lens, n, out, [&](const float* const* d, float* o) {
+        return zg::binary(kind, d[0], d[1], n, o, ctx->stream);
+    });
+    if (rc) return rc;
+    if (!all_finite(out, n)) return fail(ctx, ZG_E_STATE, "incomplete/nonfinite source binary proposal");
+    return ZG_COMPLETED;
+}
+
+// ------------------------------------------------------------- device API
+
+int zg_act_prepare_device(zg_ctx* ctx, const void* x, int x_dtype, size_t m_rows, size_t columns, const float* gamma,
+                          float eps, float* xf, int8_t* codes, float* scales, void* stream) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!x || m_rows == 0 || (x_dtype != ZG_BF16 && x_dtype != ZG_F32) || (!xf && !codes) || (codes && !scales))
+        return fail(ctx, ZG_E_MALFORMED, "invalid activation preparation");
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    ZG_HIP(zg::act_prep(x, x_dtype == ZG_BF16, m_rows, columns, gamma, eps, xf, codes, scales, s));
+    return ZG_COMPLETED;
+}
+
+int zg_gemv_prepared_device(zg_ctx* ctx, const zg_weight* w, size_t m_rows, const float* xf, const int8_t* codes,
+                            const float* scales, float* y, void* stream) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!w || !y) return fail(ctx, ZG_E_MALFORMED, "invalid gemv arguments");
+    if (!zg::gemv_supported(w->dw.type, w->dw.K, m_rows)) return fail(ctx, ZG_UNSUPPORTED, "geometry not offered");
+    if (w->dw.type == ZG_Q8_0 ? (!codes || !scales) : !xf) return fail(ctx, ZG_E_MALFORMED, "missing activation");
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    ZG_HIP(zg::gemv(w->dw, m_rows, xf, codes, scales, y, s));
+    return ZG_COMPLETED;
+}
+
+int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows, const float* gamma,
+                   float eps, float* y, void* stream) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!w || !x || !y || (x_dtype != ZG_BF16 && x_dtype != ZG_F32)) return fail(ctx, ZG_E_MALFORMED, "invalid gemv arguments");
+    if (!zg::gemv_supported(w->dw.type, w->dw.K, m_rows)) return fail(ctx, ZG_UNSUPPORTED, "geometry not offered");
+    const size_t K = w->dw.K, M = m_rows;
+    const size_t oq = align256(M * K * 4), od = oq + align256(M * K), end = od + align256(M * (K / 32 + 1) * 4);
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    if (ctx->actbuf.bytes < end) {
+        // Growing the buffer must not race work still queued on the caller stream.
+        ZG_HIP(hipStreamSynchronize(s));
+    }
+    int rc = ensure(ctx, ctx->actbuf, end);
+    if (rc) return rc;
+    char* base = (char*)ctx->actbuf.ptr;
+    float* xf = (float*)base;
+    int8_t* aq = (int8_t*)(base + oq);
+    float* ad = (float*)(base + od);
+    const bool q8 = w->dw.type == ZG_Q8_0;
+    ZG_HIP(zg::act_prep(x, x_dtype == ZG_BF16, M, K, gamma, eps, q8 ? nullptr : xf, q8 ? aq : nullptr,
+                        q8 ? ad : nullptr, s));
+    ZG_HIP(zg::gemv(w->dw, M, xf, aq, ad, y, s));
+    return ZG_COMPLETED;
+}
+
+}  // extern "C"

@@ -1,0 +1,71 @@
+// Device-side helpers shared by every zerogravity_amd kernel (gfx950 only).
+// All HIP code is compiled with -ffp-contract=off: a fused multiply-add only
+// appears where a kernel calls fmaf() explicitly.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace zg {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// IEEE binary16 -> binary32 (exact, subnormals included); the hardware
+// conversion is exact for every finite code, which is all a registered
+// tensor may hold (nonfinite scales are refused at registration).
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return (float)v;
+}
+
+// binary32 -> binary16, round to nearest even, restated bit by bit so the
+// dynamic Q8_0 activation scale rounds exactly as the CPU path does.
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float value) {
+    uint32_t bits = __float_as_uint(value);
+    uint32_t sign = (bits >> 16) & 0x8000u;
+    int exponent = (int)((bits >> 23) & 0xff);
+    uint32_t fraction = bits & 0x7fffffu;
+    if (exponent == 255) return (uint16_t)(sign | 0x7c00u | (fraction ? (((fraction >> 13) & 0xffffu) | 0x200u) : 0u));
+    int half_exp = exponent - 127 + 15;
+    if (half_exp >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (half_exp <= 0) {
+        if (half_exp < -10) return (uint16_t)sign;
+        uint32_t mantissa = fraction | 0x800000u;
+        uint32_t shift = (uint32_t)(14 - half_exp);
+        uint32_t half = (mantissa + ((1u << (shift - 1)) - 1) + ((mantissa >> shift) & 1)) >> shift;
+        return (uint16_t)(sign | half);
+    }
+    uint32_t rounded = fraction + 0x0fffu + ((fraction >> 13) & 1);
+    if (rounded >= 0x800000u) return (uint16_t)(sign | ((uint32_t)(half_exp + 1) << 10));
+    return (uint16_t)(sign | ((uint32_t)half_exp << 10) | (rounded >> 13));
+}
+
+__device__ __forceinline__ float f16_roundtrip(float v) { return f16_to_f32(f32_to_f16_rne(v)); }
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+__device__ __forceinline__ bool finite_f32(float v) {
+    return (__float_as_uint(v) & 0x7f800000u) != 0x7f800000u;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum_xor(T v, int width) {
+    for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+// Streaming 16-byte load that bypasses cache retention (weights are read
+// exactly once per launch).
+__device__ __forceinline__ v4i load_nt(const void* p) {
+    return __builtin_nontemporal_load((const v4i*)p);
+}
+
+}  // namespace zg

@@ -1,0 +1,576 @@
+// GGUF block-quantized GEMV / skinny GEMM for gfx950, plus the weight repack,
+// exact dequantization and activation-preparation kernels it depends on.
+//
+// Reference semantics (zerogravity repository):
+//   Q8_0 x dynamic-Q8_0 activation: cpu/src/source/quantization.rs:37-61,171-196
+//   Q4_K x f32 activation (dot_row): cpu/src/source.rs:431-459
+//   codecs: artifacts/src/codecs/q8.rs:6-15, q4.rs:39-70
+//   RMSNorm prologue: model-qwen35/src/lib.rs:263-284
+//
+// Design: memory-bound.  Each wavefront owns `64/lpr` weight rows at a time,
+// `lpr` lanes per row, every lane streaming 16-byte nontemporal loads of the
+// row payload.  A lane always covers the same K positions, so its share of
+// the activation lives in registers for the whole launch and is reused by
+// every row it visits; the only per-row reduction is a log2(lpr)-step XOR
+// shuffle tree.
+#include "zg_device.hpp"
+#include "zg_internal.hpp"
+
+namespace zg {
+
+size_t gguf_row_bytes(int type, size_t K) {
+    switch (type) {
+    case kQ8_0: return K / 32 * 34;
+    case kQ4_K: return K / 256 * 144;
+    case kF32: return K * 4;
+    default: return 0;
+    }
+}
+
+// ------------------------------------------------------------------ repack
+
+__global__ void repack_q8_0_kernel(const uint8_t* __restrict__ src, int8_t* __restrict__ qs,
+                                   uint16_t* __restrict__ hdr, size_t nblocks, int* bad) {
+    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint8_t* blk = src + b * 34;
+    uint16_t d = (uint16_t)(blk[0] | (blk[1] << 8));
+    if ((d & 0x7c00u) == 0x7c00u) atomicOr(bad, 1);
+    hdr[b] = d;
+    int8_t* out = qs + b * 32;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) out[i] = (int8_t)blk[2 + i];
+}
+
+__device__ __forceinline__ void q4k_scale_min(const uint8_t* s, int g, uint32_t& sc, uint32_t& mn) {
+    if (g < 4) {
+        sc = s[g] & 63;
+        mn = s[g + 4] & 63;
+    } else {
+        sc = (s[g + 4] & 15) | ((s[g - 4] >> 6) << 4);
+        mn = (s[g + 4] >> 4) | ((s[g] >> 6) << 4);
+    }
+}
+
+// Q4_K header relayout.  GGUF packs 8 six-bit scales and 8 six-bit mins into
+// 12 bytes (codecs/q4.rs:58-65), which forces a lane-dependent multi-byte
+// gather per group.  The device header keeps d and dmin (bytes 0-3) and
+// stores the four values of group pair p (sc[2p], mn[2p], sc[2p+1],
+// mn[2p+1]) in byte p of dwords 1..3:
+//   dw1.byte[p] = sc[2p]   | (mn[2p+1] & 3) << 6
+//   dw2.byte[p] = mn[2p]   | ((mn[2p+1] >> 2) & 3) << 6
+//   dw3.byte[p] = sc[2p+1] | ((mn[2p+1] >> 4) & 3) << 6
+// so a lane decodes its pair with three fixed-offset byte extracts.  The
+// mapping is a bijection of the same 96 bits: no information is added or lost.
+__device__ __forceinline__ void q4k_dev_scale_min(const v4u h, int g, uint32_t& sc, uint32_t& mn) {
+    const int sh = 8 * (g >> 1);
+    const uint32_t b1 = (h.y >> sh) & 0xffu, b2 = (h.z >> sh) & 0xffu, b3 = (h.w >> sh) & 0xffu;
+    if ((g & 1) == 0) {
+        sc = b1 & 63;
+        mn = b2 & 63;
+    } else {
+        sc = b3 & 63;
+        mn = (b1 >> 6) | ((b2 >> 6) << 2) | ((b3 >> 6) << 4);
+    }
+}
+
+__global__ void repack_q4k_kernel(const v4i* __restrict__ src, v4i* __restrict__ qs, v4u* __restrict__ hdr,
+                                  size_t nblocks, int* bad) {
+    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const v4i* blk = src + b * 9;  // 144 bytes = 9 x 16
+    v4i h = blk[0];
+    uint32_t w0 = (uint32_t)h.x;
+    if ((w0 & 0x7c00u) == 0x7c00u || ((w0 >> 16) & 0x7c00u) == 0x7c00u) atomicOr(bad, 1);
+    uint8_t s[12];
+    const uint32_t hw[3] = {(uint32_t)h.y, (uint32_t)h.z, (uint32_t)h.w};
+#pragma unroll
+    for (int i = 0; i < 12; ++i) s[i] = (uint8_t)(hw[i >> 2] >> (8 * (i & 3)));
+    uint32_t d1 = 0, d2 = 0, d3 = 0;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        uint32_t sc0, mn0, sc1, mn1;
+        q4k_scale_min(s, 2 * p, sc0, mn0);
+        q4k_scale_min(s, 2 * p + 1, sc1, mn1);
+        d1 |= (sc0 | ((mn1 & 3u) << 6)) << (8 * p);
+        d2 |= (mn0 | (((mn1 >> 2) & 3u) << 6)) << (8 * p);
+        d3 |= (sc1 | (((mn1 >> 4) & 3u) << 6)) << (8 * p);
+    }
+    hdr[b] = v4u{w0, d1, d2, d3};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qs[b * 8 + i] = blk[1 + i];
+}
+
+hipError_t repack_weight(const uint8_t* d_gguf, DeviceWeight& w, int* d_bad, hipStream_t s) {
+    if (w.type == kQ8_0) {
+        size_t nb = w.N * (w.K / 32);
+        unsigned grid = (unsigned)((nb + 255) / 256);
+        hipLaunchKernelGGL(repack_q8_0_kernel, dim3(grid), dim3(256), 0, s, d_gguf, (int8_t*)w.qs,
+                           (uint16_t*)w.hdr, nb, d_bad);
+    } else if (w.type == kQ4_K) {
+        size_t nb = w.N * (w.K / 256);
+        unsigned grid = (unsigned)((nb + 255) / 256);
+        hipLaunchKernelGGL(repack_q4k_kernel, dim3(grid), dim3(256), 0, s, (const v4i*)d_gguf, (v4i*)w.qs,
+                           (v4u*)w.hdr, nb, d_bad);
+    } else if (w.type == kF32) {
+        return hipMemcpyAsync(w.qs, d_gguf, w.qs_bytes, hipMemcpyDeviceToDevice, s);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------- dequantize
+
+__global__ void dequant_q8_0_kernel(const int8_t* __restrict__ qs, const uint16_t* __restrict__ hdr,
+                                    float* __restrict__ out, size_t nblocks) {
+    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    float scale = f16_to_f32(hdr[b]);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) out[b * 32 + i] = (float)qs[b * 32 + i] * scale;
+}
+
+__global__ void dequant_q4k_kernel(const uint8_t* __restrict__ qs, const v4u* __restrict__ hdr,
+                                   float* __restrict__ out, size_t nblocks) {
+    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const v4u h = hdr[b];
+    float d = f16_to_f32((uint16_t)(h.x & 0xffffu));
+    float dmin = f16_to_f32((uint16_t)(h.x >> 16));
+    const uint8_t* q = qs + b * 128;
+    for (int g = 0; g < 8; ++g) {
+        uint32_t sc, mn;
+        q4k_dev_scale_min(h, g, sc, mn);
+        float scale = d * (float)sc;
+        float mnf = dmin * (float)mn;
+        for (int i = 0; i < 32; ++i) {
+            uint8_t byte = q[(g >> 1) * 32 + i];
+            uint32_t v = (g & 1) ? (byte >> 4) : (byte & 15);
+            out[b * 256 + g * 32 + i] = scale * (float)v - mnf;
+        }
+    }
+}
+
+hipError_t dequantize_rows(const DeviceWeight& w, size_t row0, size_t rows, float* out, hipStream_t s) {
+    if (row0 + rows > w.N) return hipErrorInvalidValue;
+    if (w.type == kQ8_0) {
+        const size_t bpr = w.K / 32, nb = rows * bpr;
+        hipLaunchKernelGGL(dequant_q8_0_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, s,
+                           (const int8_t*)w.qs + row0 * w.K, (const uint16_t*)w.hdr + row0 * bpr, out, nb);
+    } else if (w.type == kQ4_K) {
+        const size_t bpr = w.K / 256, nb = rows * bpr;
+        hipLaunchKernelGGL(dequant_q4k_kernel, dim3((unsigned)((nb + 63) / 64)), dim3(64), 0, s,
+                           (const uint8_t*)w.qs + row0 * (w.K / 2), (const v4u*)w.hdr + row0 * bpr, out, nb);
+    } else if (w.type == kF32) {
+        return hipMemcpyAsync(out, (const float*)w.qs + row0 * w.K, rows * w.K * 4, hipMemcpyDeviceToDevice, s);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// --------------------------------------------------------- activation prep
+
+// One workgroup per activation row.  RMS: f64 sum of f32-rounded squares
+// (order-free to within f64 rounding), mean rounded to f32, inv = 1/sqrtf,
+// y = (x*inv)*gamma.  Q8_0 coding per 32-block: amax, d = amax/127,
+// inv = 127/amax, code = clamp(rint(y*inv)), scale stored f16-rounded.
+template <bool XBF16>
+__global__ __launch_bounds__(256) void act_prep_kernel(const void* __restrict__ x, int K,
+                                                       const float* __restrict__ gamma, float eps,
+                                                       float* __restrict__ xf, int8_t* __restrict__ aq,
+                                                       float* __restrict__ ad) {
+    extern __shared__ float sx[];
+    __shared__ double red[4];
+    __shared__ float inv_s;
+    const size_t m = blockIdx.x;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < K; i += 256) {
+        sx[i] = XBF16 ? bf16_to_f32(((const uint16_t*)x)[m * K + i]) : ((const float*)x)[m * K + i];
+    }
+    __syncthreads();
+    if (gamma) {
+        double s = 0.0;
+        for (int i = tid; i < K; i += 256) {
+            float v = sx[i];
+            float sq = v * v;
+            s += (double)sq;
+        }
+        s = wave_sum_xor<double>(s, 64);
+        if ((tid & 63) == 0) red[tid >> 6] = s;
+        __syncthreads();
+        if (tid == 0) {
+            double total = (red[0] + red[1]) + (red[2] + red[3]);
+            float mean = (float)(total / (double)K);
+            float root = sqrtf(mean + eps);
+            inv_s = 1.0f / root;
+        }
+        __syncthreads();
+        const float inv = inv_s;
+        for (int i = tid; i < K; i += 256) {
+            float t = sx[i] * inv;
+            sx[i] = t * gamma[i];
+        }
+        __syncthreads();
+    }
+    if (xf) {
+        for (int i = tid; i < K; i += 256) xf[m * K + i] = sx[i];
+    }
+    if (aq) {
+        const int nb = K >> 5;
+        const int l = tid & 31;
+        for (int b = tid >> 5; b < nb; b += 8) {
+            float v = sx[b * 32 + l];
+            float amax = fabsf(v);
+            for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+            float d = amax / 127.0f;
+            float inv = amax == 0.0f ? 0.0f : 127.0f / amax;
+            float r = rintf(v * inv);
+            r = fminf(fmaxf(r, -128.0f), 127.0f);
+            aq[m * K + b * 32 + l] = (int8_t)(int)r;
+            if (l == 0) ad[m * nb + b] = f16_roundtrip(d);
+        }
+    }
+}
+
+hipError_t act_prep(const void* x, int x_bf16, size_t M, size_t K, const float* gamma, float eps,
+                    float* xf, int8_t* aq, float* ad, hipStream_t s) {
+    if (M == 0 || K == 0 || K > 8192 || (aq && K % 32)) return hipErrorInvalidValue;
+    size_t lds = K * sizeof(float);
+    if (x_bf16)
+        hipLaunchKernelGGL(act_prep_kernel<true>, dim3((unsigned)M), dim3(256), lds, s, x, (int)K, gamma, eps, xf, aq, ad);
+    else
+        hipLaunchKernelGGL(act_prep_kernel<false>, dim3((unsigned)M), dim3(256), lds, s, x, (int)K, gamma, eps, xf, aq, ad);
+    return hipGetLastError();
+}
+
+// ----------------------------------------------------------------- GEMV Q8_0
+
+// MT activation rows per pass (grid.y covers ceil(M/MT) passes), CH 16-byte
+// chunks per lane.  Integer block dots via v_dot4_i32_i8; each half block's
+// int32 sum is scaled once by f16(w.d) * act.d in f32.
+template <int CH, int MT>
+__global__ __launch_bounds__(256) void gemv_q8_0_kernel(const int8_t* __restrict__ qs,
+                                                        const uint16_t* __restrict__ hdr,
+                                                        const int8_t* __restrict__ aq,
+                                                        const float* __restrict__ ad, float* __restrict__ y,
+                                                        int N, int K, int M, int lpr_log2) {
+    const int lane = threadIdx.x & 63;
+    const int lpr = 1 << lpr_log2;
+    const int sub = lane & (lpr - 1);
+    const int rsub = lane >> lpr_log2;
+    const int rpw = 64 >> lpr_log2;
+    const int nchunk = K >> 4;
+    const int nb = K >> 5;
+    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int nwaves = gridDim.x * (blockDim.x >> 6);
+    const int m0 = blockIdx.y * MT;
+
+    v4i a[MT][CH];
+    float as[MT][CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        const int c = sub + i * lpr;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (c < nchunk && m0 + m < M) {
+                a[m][i] = *(const v4i*)(aq + (size_t)(m0 + m) * K + (size_t)c * 16);
+                as[m][i] = ad[(size_t)(m0 + m) * nb + (c >> 1)];
+            } else {
+                a[m][i] = v4i{0, 0, 0, 0};
+                as[m][i] = 0.0f;
+            }
+        }
+    }
+    for (int rg = wave; rg * rpw < N; rg += nwaves) {
+        const int row = rg * rpw + rsub;
+        const bool rv = row < N;
+        v4i w[CH];
+        float sc[CH];
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = sub + i * lpr;
+            if (rv && c < nchunk) {
+                w[i] = load_nt(qs + (size_t)row * K + (size_t)c * 16);
+                sc[i] = f16_to_f32(hdr[(size_t)row * nb + (c >> 1)]);
+            } else {
+                w[i] = v4i{0, 0, 0, 0};
+                sc[i] = 0.0f;
+            }
+        }
+        float acc[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                int d = __builtin_amdgcn_sdot4(w[i].x, a[m][i].x, 0, false);
+                d = __builtin_amdgcn_sdot4(w[i].y, a[m][i].y, d, false);
+                d = __builtin_amdgcn_sdot4(w[i].z, a[m][i].z, d, false);
+                d = __builtin_amdgcn_sdot4(w[i].w, a[m][i].w, d, false);
+                acc[m] = fmaf((float)d, sc[i] * as[m][i], acc[m]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = wave_sum_xor(acc[m], lpr);
+        if (rv && sub == 0) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                if (m0 + m < M) y[(size_t)(m0 + m) * N + row] = acc[m];
+        }
+    }
+}
+
+// ----------------------------------------------------------------- GEMV Q4_K
+
+// A lane owns whole "pair chunks": 32 payload bytes = all 64 elements of the
+// group pair (2p, 2p+1) of one 256-element block (low nibbles -> group 2p,
+// high nibbles -> group 2p+1).  With lpr a multiple of 4 every chunk of a lane
+// has the same p, so one header decode serves 64 elements.  The activation
+// is carried as int16 fixed point per (lane, group): xq = rint(x * 32767/amax),
+// relative precision 2^-15 of the group's max; nibble pairs are spread into
+// int16 pairs with one mask (and a shift) and reduced with v_dot2_i32_i16 into
+// an exact int32 group sum.  Per group:
+//   acc += (d*sc) * (xs * isum) - (dmin*mn) * sum(x)        (f32)
+// where sum(x) is the exact f32 sum of the group's activations.  MT
+// activation rows share every converted weight dword.
+template <int CH, int MT>
+__global__ __launch_bounds__(256) void gemv_q4k_kernel(const uint8_t* __restrict__ qs,
+                                                       const v4u* __restrict__ hdr,
+                                                       const float* __restrict__ x, float* __restrict__ y,
+                                                       int N, int K, int M, int lpr_log2) {
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    const int lane = threadIdx.x & 63;
+    const int lpr = 1 << lpr_log2;
+    const int sub = lane & (lpr - 1);
+    const int rsub = lane >> lpr_log2;
+    const int rpw = 64 >> lpr_log2;
+    const int nchunk = K >> 6;  // pair chunks per row
+    const int nbk = K >> 8;
+    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int nwaves = gridDim.x * (blockDim.x >> 6);
+    const int m0 = blockIdx.y * MT;
+    const int p = sub & 3;
+
+    // activation: packed int16 pairs matching the weight pair order
+    int xl0[MT][CH][8], xl1[MT][CH][8], xh0[MT][CH][8], xh1[MT][CH][8];
+    float xs_lo[MT][CH], xs_hi[MT][CH], sx_lo[MT][CH], sx_hi[MT][CH];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = sub + i * lpr;
+            const bool ok = c < nchunk && m0 + m < M;
+            const float* lo = x + (size_t)(ok ? m0 + m : 0) * K + (size_t)(ok ? c >> 2 : 0) * 256 + 64 * p;
+            const float* hi = lo + 32;
+            float alo = 0.0f, ahi = 0.0f, slo = 0.0f, shi = 0.0f;
+            if (ok) {
+#pragma unroll
+                for (int t = 0; t < 32; ++t) {
+                    alo = fmaxf(alo, fabsf(lo[t]));
+                    ahi = fmaxf(ahi, fabsf(hi[t]));
+                    slo += lo[t];
+                    shi += hi[t];
+                }
+            }
+            const float ilo = alo == 0.0f ? 0.0f : 32767.0f / alo;
+            const float ihi = ahi == 0.0f ? 0.0f : 32767.0f / ahi;
+            xs_lo[m][i] = alo / 32767.0f;
+            xs_hi[m][i] = ahi / 32767.0f;
+            sx_lo[m][i] = slo;
+            sx_hi[m][i] = shi;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                int a0 = 0, a1 = 0, a2 = 0, a3 = 0, b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+                if (ok) {
+                    a0 = (int)rintf(lo[4 * q + 0] * ilo);
+                    a1 = (int)rintf(lo[4 * q + 1] * ilo);
+                    a2 = (int)rintf(lo[4 * q + 2] * ilo);
+                    a3 = (int)rintf(lo[4 * q + 3] * ilo);
+                    b0 = (int)rintf(hi[4 * q + 0] * ihi);
+                    b1 = (int)rintf(hi[4 * q + 1] * ihi);
+                    b2 = (int)rintf(hi[4 * q + 2] * ihi);
+                    b3 = (int)rintf(hi[4 * q + 3] * ihi);
+                }
+                xl0[m][i][q] = (a0 & 0xffff) | (a2 << 16);
+                xl1[m][i][q] = (a1 & 0xffff) | (a3 << 16);
+                xh0[m][i][q] = (b0 & 0xffff) | (b2 << 16);
+                xh1[m][i][q] = (b1 & 0xffff) | (b3 << 16);
+            }
+        }
+    }
+    for (int rg = wave; rg * rpw < N; rg += nwaves) {
+        const int row = rg * rpw + rsub;
+        const bool rv = row < N;
+        v4i w0[CH], w1[CH];
+        v4u h[CH];
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = sub + i * lpr;
+            if (rv && c < nchunk) {
+                const uint8_t* base = qs + (size_t)row * (K >> 1) + (size_t)c * 32;
+                w0[i] = load_nt(base);
+                w1[i] = load_nt(base + 16);
+                h[i] = hdr[(size_t)row * nbk + (c >> 2)];
+            } else {
+                w0[i] = v4i{0, 0, 0, 0};
+                w1[i] = v4i{0, 0, 0, 0};
+                h[i] = v4u{0u, 0u, 0u, 0u};
+            }
+        }
+        float acc[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const uint32_t ww[8] = {(uint32_t)w0[i].x, (uint32_t)w0[i].y, (uint32_t)w0[i].z, (uint32_t)w0[i].w,
+                                    (uint32_t)w1[i].x, (uint32_t)w1[i].y, (uint32_t)w1[i].z, (uint32_t)w1[i].w};
+            int ilo[MT], ihi[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) ilo[m] = ihi[m] = 0;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const uint32_t d = ww[q];
+                const v2s L0 = __builtin_bit_cast(v2s, d & 0x000f000fu);
+                const v2s L1 = __builtin_bit_cast(v2s, (d >> 8) & 0x000f000fu);
+                const v2s H0 = __builtin_bit_cast(v2s, (d >> 4) & 0x000f000fu);
+                const v2s H1 = __builtin_bit_cast(v2s, (d >> 12) & 0x000f000fu);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    ilo[m] = __builtin_amdgcn_sdot2(L0, __builtin_bit_cast(v2s, xl0[m][i][q]), ilo[m], false);
+                    ilo[m] = __builtin_amdgcn_sdot2(L1, __builtin_bit_cast(v2s, xl1[m][i][q]), ilo[m], false);
+                    ihi[m] = __builtin_amdgcn_sdot2(H0, __builtin_bit_cast(v2s, xh0[m][i][q]), ihi[m], false);
+                    ihi[m] = __builtin_amdgcn_sdot2(H1, __builtin_bit_cast(v2s, xh1[m][i][q]), ihi[m], false);
+                }
+            }
+            uint32_t sc0, mn0, sc1, mn1;
+            q4k_dev_scale_min(h[i], 2 * p, sc0, mn0);
+            q4k_dev_scale_min(h[i], 2 * p + 1, sc1, mn1);
+            const float d = f16_to_f32((uint16_t)(h[i].x & 0xffffu));
+            const float dmin = f16_to_f32((uint16_t)(h[i].x >> 16));
+            const float s0 = d * (float)sc0, n0 = dmin * (float)mn0;
+            const float s1 = d * (float)sc1, n1 = dmin * (float)mn1;
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                acc[m] = fmaf(s0, xs_lo[m][i] * (float)ilo[m], acc[m]);
+                acc[m] = fmaf(-n0, sx_lo[m][i], acc[m]);
+                acc[m] = fmaf(s1, xs_hi[m][i] * (float)ihi[m], acc[m]);
+                acc[m] = fmaf(-n1, sx_hi[m][i], acc[m]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = wave_sum_xor(acc[m], lpr);
+        if (rv && sub == 0) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                if (m0 + m < M) y[(size_t)(m0 + m) * N + row] = acc[m];
+        }
+    }
+}
+
+// ----------------------------------------------------------------- GEMV F32
+
+__global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__ w, const float* __restrict__ x,
+                                                       float* __restrict__ y, int N, int K) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const size_t m = blockIdx.y;
+    if (row >= N) return;
+    float acc = 0.0f;
+    for (int k = lane; k < K; k += 64) acc = fmaf(w[(size_t)row * K + k], x[m * K + k], acc);
+    acc = wave_sum_xor(acc, 64);
+    if (lane == 0) y[m * N + row] = acc;
+}
+
+// ------------------------------------------------------------- dispatch
+
+static int pick_lpr_log2(int nchunk, int target) {
+    int l = 3;  // 8 lanes minimum: Q4_K needs lpr % 8 == 0
+    while (l < 6 && (nchunk + (1 << l) - 1) / (1 << l) > target) ++l;
+    return l;
+}
+
+static unsigned grid_for(size_t N, int lpr_log2) {
+    const size_t rpw = 64u >> lpr_log2;
+    size_t waves = (N + rpw - 1) / rpw;
+    size_t wgs = (waves + 3) / 4;
+    const size_t cap = 256 * 8;  // 8 workgroups per CU on 256 CUs, grid-stride beyond
+    return (unsigned)(wgs < cap ? wgs : cap);
+}
+
+bool gemv_supported(int type, size_t K, size_t M) {
+    if (M == 0 || M > 64 || K == 0) return false;
+    switch (type) {
+    case kQ8_0: return K % 32 == 0 && K <= 8192;
+    case kQ4_K: return K % 256 == 0 && K <= 16384;
+    case kF32: return K <= (1u << 20);
+    default: return false;
+    }
+}
+
+template <int MT>
+static void launch_q8(int ch, dim3 g, hipStream_t s, const DeviceWeight& w, const int8_t* aq, const float* ad,
+                      float* y, int M, int l) {
+    const int8_t* q = (const int8_t*)w.qs;
+    const uint16_t* h = (const uint16_t*)w.hdr;
+    const int N = (int)w.N, K = (int)w.K;
+    switch (ch) {
+#define ZG_Q8(C) case C: hipLaunchKernelGGL((gemv_q8_0_kernel<C, MT>), g, dim3(256), 0, s, q, h, aq, ad, y, N, K, M, l); break;
+        ZG_Q8(1) ZG_Q8(2) ZG_Q8(3) ZG_Q8(4) ZG_Q8(5) ZG_Q8(6) ZG_Q8(7) ZG_Q8(8)
+#undef ZG_Q8
+    }
+}
+
+hipError_t gemv(const DeviceWeight& w, size_t M, const float* xf, const int8_t* aq, const float* ad, float* y,
+                hipStream_t s) {
+    if (!gemv_supported(w.type, w.K, M)) return hipErrorInvalidValue;
+    const int K = (int)w.K, N = (int)w.N;
+    if (w.type == kQ8_0) {
+        const int nchunk = K / 16;
+        const int l = pick_lpr_log2(nchunk, 4);
+        const int ch = (nchunk + (1 << l) - 1) >> l;
+        const int mt = M == 1 ? 1 : (M == 2 ? 2 : 4);
+        dim3 g(grid_for(w.N, l), (unsigned)((M + mt - 1) / mt));
+        if (mt == 1) launch_q8<1>(ch, g, s, w, aq, ad, y, (int)M, l);
+        else if (mt == 2) launch_q8<2>(ch, g, s, w, aq, ad, y, (int)M, l);
+        else launch_q8<4>(ch, g, s, w, aq, ad, y, (int)M, l);
+    } else if (w.type == kQ4_K) {
+        const int nchunk = K / 64;
+        int mt = M == 1 ? 1 : (M == 2 ? 2 : 4);
+        const int minch = (nchunk + 63) / 64;  // chunks per lane at 64 lanes per row
+        while (mt > 1 && minch * mt > 4) mt >>= 1;
+        const int chmax = 4 / mt;
+        // Fewer chunks per lane keeps VGPRs (and so occupancy) in check; more
+        // only when the row is too long for 64 lanes.
+        const int target = minch > (2 / mt) ? minch : (mt == 1 ? 2 : 1);
+        int l = 2;
+        while (l < 6 && (nchunk + (1 << l) - 1) / (1 << l) > target) ++l;
+        const int ch = (nchunk + (1 << l) - 1) >> l;
+        if (ch > chmax) return hipErrorInvalidValue;
+        dim3 g(grid_for(w.N, l), (unsigned)((M + mt - 1) / mt));
+        const uint8_t* q = (const uint8_t*)w.qs;
+        const v4u* h = (const v4u*)w.hdr;
+#define ZG_Q4(C, T) hipLaunchKernelGGL((gemv_q4k_kernel<C, T>), g, dim3(256), 0, s, q, h, xf, y, N, K, (int)M, l)
+        if (mt == 1) {
+            switch (ch) {
+            case 1: ZG_Q4(1, 1); break;
+            case 2: ZG_Q4(2, 1); break;
+            case 3: ZG_Q4(3, 1); break;
+            default: ZG_Q4(4, 1); break;
+            }
+        } else if (mt == 2) {
+            if (ch == 1) ZG_Q4(1, 2); else ZG_Q4(2, 2);
+        } else {
+            ZG_Q4(1, 4);
+        }
+#undef ZG_Q4
+    } else {
+        dim3 g((unsigned)((w.N + 3) / 4), (unsigned)M);
+        hipLaunchKernelGGL(gemv_f32_kernel, g, dim3(256), 0, s, (const float*)w.qs, xf, y, N, K);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace zg
