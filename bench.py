@@ -48,20 +48,18 @@ def bench_gemv(kern, torch, handles, kind, N, K, M, steps, warmup, rng):
     gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
     x_d = torch.from_numpy(xb.view(np.int16)).cuda()
     g_d = torch.from_numpy(gamma).cuda()
-    xn = torch.empty((M, K), dtype=torch.float32, device="cuda")
-    aq = torch.empty((M, K), dtype=torch.int8, device="cuda")
-    ad = torch.empty((M, K // 32), dtype=torch.float32, device="cuda")
     y = torch.empty((M, N), dtype=torch.float32, device="cuda")
     s = torch.cuda.current_stream()
     assert s.cuda_stream != 0, "launch and event stream must be a real stream"
     lib, ctx = L.lib(), kern.ctx
-    ctx.check(lib.zg_act_prepare_device(ctx.h, x_d.data_ptr(), L.BF16, M, K, g_d.data_ptr(), 1e-6, xn.data_ptr(),
-                                        aq.data_ptr(), ad.data_ptr(), s.cuda_stream))
+    nbytes = lib.zg_act_prepared_bytes(handles[0].h, M)
+    prep = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    ctx.check(lib.zg_act_prepare_device(ctx.h, handles[0].h, x_d.data_ptr(), L.BF16, M, g_d.data_ptr(), 1e-6,
+                                        prep.data_ptr(), nbytes, s.cuda_stream))
 
     def launch(i):
         h = handles[i % copies]
-        ctx.check(lib.zg_gemv_prepared_device(ctx.h, h.h, M, xn.data_ptr(), aq.data_ptr(), ad.data_ptr(),
-                                              y.data_ptr(), s.cuda_stream))
+        ctx.check(lib.zg_gemv_prepared_device(ctx.h, h.h, M, prep.data_ptr(), y.data_ptr(), s.cuda_stream))
 
     for i in range(warmup):
         launch(i)

@@ -126,6 +126,119 @@ int zg_silu(zg_ctx* ctx, const float* input, const float* multiplier, size_t n, 
  * (lib.rs:1258-1271).  kind 0 = Add, 1 = SigmoidGate. out[n]. */
 int zg_binary(zg_ctx* ctx, int kind, const float* left, const float* right, size_t n, float* out);
 
+/* GdnConvRegion (accelerator.rs:106-117) -> try_gdn_conv; gdn_conv_step
+ * (cpu/src/ops/gdn.rs:7-44): raw_out[channels] and history_out[channels*3]
+ * (oldest -> newest per channel); weights [channels][4]. */
+int zg_gdn_conv(zg_ctx* ctx, const float* activation, const float* weights, const float* history,
+                size_t channels, float* raw_out, float* history_out);
+
+/* GdnCoefficientRegion (accelerator.rs:135-189) -> try_gdn_coefficients;
+ * source_gdn_coefficients (model-qwen35/src/lib.rs:339-362).  The caller
+ * attaches the immutable `scale` to each head's coefficients. */
+int zg_gdn_coefficients(zg_ctx* ctx, const float* alpha, const float* beta, const float* dt, const float* a,
+                        size_t heads, float scale, float* gain_out, float* beta_out, float* softplus_out,
+                        float* gate_raw_out);
+
+/* GdnRecurrentRegion (accelerator.rs:592-633) -> try_gdn_recurrent;
+ * source_gdn_recurrent_step per head (lib.rs:1446-1499).  q, k, v [heads][width];
+ * coefficients [heads][3] = {gain, beta, scale}; state value-major
+ * [heads][width][width].  Offered for width 128. */
+int zg_gdn_recurrent(zg_ctx* ctx, size_t width, size_t heads, const float* q, const float* k, const float* v,
+                     const float* coefficients, const float* state, float* output, float* state_out);
+
+/* RopeKvRegion (accelerator.rs:205-296) -> try_rope_kv; source_rope_kv
+ * (lib.rs:1552-1577).  Returns the rotated query and key and the unchanged
+ * value slab. */
+int zg_rope_kv(zg_ctx* ctx, const float* query, const float* key, const float* value, size_t head_width,
+               size_t query_heads, size_t kv_heads, size_t rotate, size_t position, float theta_scale,
+               float* query_out, float* key_out, float* value_out);
+
+/* AttentionQkRegion (accelerator.rs:302-362) -> try_attention_qk;
+ * source_attention_qk (lib.rs:1427-1441).  keys [tokens][kv_heads*head_width];
+ * dots and scores [query_heads][tokens]. Offered for head width 256. */
+int zg_attention_qk(zg_ctx* ctx, const float* query, const float* keys, size_t tokens, size_t head_width,
+                    size_t query_heads, size_t kv_heads, float scale, float* dots, float* scores);
+
+/* AttentionSoftmaxRegion (accelerator.rs:368-453) -> try_attention_softmax;
+ * source_attention_softmax (lib.rs:1352-1387). probabilities [heads][width]. */
+int zg_attention_softmax(zg_ctx* ctx, const float* scores, size_t heads, size_t width, float* probabilities);
+
+/* AttentionValueRegion (accelerator.rs:450-500) -> try_attention_value;
+ * source_attention_value (lib.rs:1276-1305); the reference's +0 padding of
+ * the FMA schedule has no arithmetic effect beyond the sign of an exact zero.
+ * values [tokens][kv_heads*head_width]; out [query_heads][head_width]. */
+int zg_attention_value(zg_ctx* ctx, const float* probabilities, const float* values, size_t tokens,
+                       size_t head_width, size_t query_heads, size_t kv_heads, float* out);
+
+/* --------------------------------------------- boundary B: whole program */
+
+/* Replaces RegionExecutionProvider::prepare(ModelProgram) for the Qwen3.5
+ * GGUF forward plan (core/src/provider.rs:10-42, engine/src/prepare.rs:11-26):
+ * the model is loaded once from a tensor table (names and GGML shapes of
+ * model-qwen35/src/source/binding.rs:43-91, checked as in
+ * LoadedQwenModel::from_checked_source, lib.rs:386-507) and sessions run
+ * forward::forward_token (forward.rs:451-755) on the device. */
+typedef struct zg_model zg_model;
+typedef struct zg_session zg_session;
+
+typedef struct zg_tensor_desc {
+    const char* name;  /* GGUF tensor name, e.g. "blk.0.attn_qkv.weight" */
+    int ggml_type;     /* ZG_F32, ZG_Q8_0 or ZG_Q4_K */
+    uint64_t shape0;   /* GGML ne0: inner (columns / vector length) */
+    uint64_t shape1;   /* GGML ne1: rows (1 for vectors) */
+    const void* data;  /* host bytes, only read during zg_model_load */
+    uint64_t nbytes;
+} zg_tensor_desc;
+
+typedef struct zg_geometry { /* ModelGeometry, model-qwen35/src/config.rs:51-182 */
+    uint32_t hidden, layers, ffn, vocab;
+    uint32_t gdn_heads, gdn_dim;          /* linear_num_value_heads, head width (128) */
+    uint32_t q_heads, kv_heads, head_dim; /* full attention (head_dim 256) */
+    uint32_t full_attention_interval;     /* layer i is full attention iff (i+1) % interval == 0 */
+    uint32_t max_context;
+    float eps;                            /* 1e-6 (lib.rs:505) */
+} zg_geometry;
+
+int zg_model_load(zg_ctx* ctx, uint64_t source_id, const zg_geometry* geometry, const zg_tensor_desc* tensors,
+                  size_t n_tensors, zg_model** out);
+void zg_model_destroy(zg_model* model);
+
+/* A session holds max_batch independent rows (continuous batch), each with
+ * its own position, GDN conv/recurrent state and KV cache (kv_dtype ZG_BF16
+ * or ZG_F32) of max_context tokens.  QwenDenseCpu's per-session state
+ * (lib.rs:76-150). */
+int zg_session_create(zg_model* model, size_t max_batch, size_t max_context, int kv_dtype, zg_session** out);
+void zg_session_destroy(zg_session* s);
+/* All rows back to position 0 with zero state (QwenDenseCpu::reset). */
+int zg_session_reset(zg_session* s);
+int zg_session_position(const zg_session* s, size_t row);
+
+/* One forward_token for rows [0, rows): tokens[rows] host ids, logits
+ * [rows][vocab] and/or greedy [rows] (first maximum, numerics.rs:126-140)
+ * written to host memory when non-NULL.  Each row advances one position
+ * (QwenDenseCpu::forward, lib.rs:1227-1232).  A nonfinite layer or logit is
+ * ZG_E_STATE and poisons the session until reset or state import. */
+int zg_decode_step(zg_session* s, size_t rows, const uint32_t* tokens, float* logits, uint32_t* greedy);
+/* n tokens per row (tokens[row*n + t]), logits of the last only
+ * (QwenDenseCpu::prefill_transaction, lib.rs:1119-1187). */
+int zg_prefill(zg_session* s, size_t rows, size_t n, const uint32_t* tokens, float* logits);
+/* Device-side step: d_tokens/d_logits/d_greedy are device pointers, no host
+ * synchronisation (zg_session_check reads the device status word). */
+int zg_decode_step_device(zg_session* s, size_t rows, const uint32_t* d_tokens, float* d_logits, uint32_t* d_greedy,
+                          void* stream);
+int zg_session_check(zg_session* s, void* stream);
+
+/* State domains of one row in the reference order (lib.rs:112-150): per layer,
+ * GDN conv history then recurrent state (value-major), or attention keys then
+ * values (token-major, f32). */
+size_t zg_state_floats(const zg_session* s, size_t row);
+int zg_state_export(zg_session* s, size_t row, float* out, size_t n);
+int zg_state_import(zg_session* s, size_t row, const float* in, size_t n, int position);
+/* Seeded synthetic prefix for benchmarking: rows [0, rows) get `prefix`
+ * random tokens of KV (N(0,1)), recurrent state N(0,0.02) and conv history
+ * N(0,0.5), and position `prefix`.  No reference counterpart. */
+int zg_session_fill_random(zg_session* s, size_t rows, size_t prefix, uint64_t seed);
+
 /* ------------------------------------------------------------- device API */
 
 /* y[M][rows] = W . rmsnorm(x)[M][columns] on device memory, the fused
@@ -138,14 +251,21 @@ int zg_binary(zg_ctx* ctx, int kind, const float* left, const float* right, size
 int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows,
                    const float* gamma, float eps, float* y, void* stream);
 
-/* Only the GEMV kernel of zg_gemv_device, on activations already prepared by
- * zg_act_prepare_device (for timing the kernel alone).  For Q8_0 pass the
- * codes/scales, for Q4_K and F32 the f32 activation. */
-int zg_act_prepare_device(zg_ctx* ctx, const void* x, int x_dtype, size_t m_rows, size_t columns,
-                          const float* gamma, float eps, float* xf, int8_t* codes, float* scales,
-                          void* stream);
-int zg_gemv_prepared_device(zg_ctx* ctx, const zg_weight* w, size_t m_rows, const float* xf,
-                            const int8_t* codes, const float* scales, float* y, void* stream);
+/* The two halves of zg_gemv_device, for callers that prepare one activation
+ * and reuse it (and for timing the GEMV kernel alone).  The prepared buffer
+ * is device memory of zg_act_prepared_bytes(w, m_rows) bytes holding the
+ * activation in the format w's codec consumes:
+ *   Q8_0: int8 codes [M][columns], then f32 scales [M][columns/32]: the
+ *         dynamic Q8_0 coding of cpu/src/source/quantization.rs:37-61;
+ *   Q4_K: int16 fixed-point group-pair records [M][columns/64][64], then f32
+ *         {scale_lo, scale_hi, sum_lo, sum_hi} [M][columns/64];
+ *   F32 : f32 [M][columns];
+ * each part starting on a 256-byte boundary. */
+size_t zg_act_prepared_bytes(const zg_weight* w, size_t m_rows);
+int zg_act_prepare_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows,
+                          const float* gamma, float eps, void* prepared, size_t prepared_len, void* stream);
+int zg_gemv_prepared_device(zg_ctx* ctx, const zg_weight* w, size_t m_rows, const void* prepared, float* y,
+                            void* stream);
 
 #ifdef __cplusplus
 }

@@ -120,26 +120,31 @@ def test_gemv_device_rms_prologue_bf16(kern, torch_cuda, kind, N, K, M):
 
 
 def test_q8_activation_codes_bit_exact(kern, torch_cuda):
+    # The prepared Q8_0 activation (RMSNorm + dynamic coding) must equal the
+    # oracle's codes and f16-rounded scales bit for bit.
     torch = torch_cuda
     rng = np.random.default_rng(5)
     M, K = 4, 2048
+    _, h = weight(kern, synth.Q8_0, 64, K)
     xf, xb = synth.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
     gamma = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
     x_d = torch.from_numpy(xb.view(np.int16)).cuda()
     g_d = torch.from_numpy(gamma).cuda()
-    xn_d = torch.empty((M, K), dtype=torch.float32, device="cuda")
-    q_d = torch.empty((M, K), dtype=torch.int8, device="cuda")
-    s_d = torch.empty((M, K // 32), dtype=torch.float32, device="cuda")
+    nbytes = L.lib().zg_act_prepared_bytes(h.h, M)
+    prep = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
     stream = _stream(torch)
-    kern.ctx.check(L.lib().zg_act_prepare_device(kern.ctx.h, x_d.data_ptr(), L.BF16, M, K, g_d.data_ptr(), 1e-6,
-                                                 xn_d.data_ptr(), q_d.data_ptr(), s_d.data_ptr(), stream))
+    kern.ctx.check(L.lib().zg_act_prepare_device(kern.ctx.h, h.h, x_d.data_ptr(), L.BF16, M, g_d.data_ptr(), 1e-6,
+                                                 prep.data_ptr(), nbytes, stream))
     torch.cuda.synchronize()
+    raw = prep.cpu().numpy()
+    codes = raw[:M * K].view(np.int8).reshape(M, K)
+    off = (M * K + 255) // 256 * 256
+    scales = raw[off:off + M * (K // 32) * 4].view(np.float32).reshape(M, K // 32)
     for m in range(M):
         xn = O.rms_norm(xf[m], gamma, 1e-6)
         qs, d, _ = O.q8_activation(xn)
-        assert np.array_equal(xn_d[m].cpu().numpy().view(np.uint32), xn.view(np.uint32))
-        assert np.array_equal(q_d[m].cpu().numpy(), qs)
-        assert np.array_equal(s_d[m].cpu().numpy().view(np.uint32), d.view(np.uint32))
+        assert np.array_equal(codes[m], qs)
+        assert np.array_equal(scales[m].view(np.uint32), d.view(np.uint32))
 
 
 def test_region_refusals(kern):

@@ -36,8 +36,30 @@ _SIGS = {
     "zg_silu": (C.c_int, [P, P, P, SZ, P]),
     "zg_binary": (C.c_int, [P, C.c_int, P, P, SZ, P]),
     "zg_gemv_device": (C.c_int, [P, P, P, C.c_int, SZ, P, C.c_float, P, P]),
-    "zg_act_prepare_device": (C.c_int, [P, P, C.c_int, SZ, SZ, P, C.c_float, P, P, P, P]),
-    "zg_gemv_prepared_device": (C.c_int, [P, P, SZ, P, P, P, P, P]),
+    "zg_gdn_conv": (C.c_int, [P, P, P, P, SZ, P, P]),
+    "zg_gdn_coefficients": (C.c_int, [P, P, P, P, P, SZ, C.c_float, P, P, P, P]),
+    "zg_gdn_recurrent": (C.c_int, [P, SZ, SZ, P, P, P, P, P, P, P]),
+    "zg_rope_kv": (C.c_int, [P, P, P, P, SZ, SZ, SZ, SZ, SZ, C.c_float, P, P, P]),
+    "zg_attention_qk": (C.c_int, [P, P, P, SZ, SZ, SZ, SZ, C.c_float, P, P]),
+    "zg_attention_softmax": (C.c_int, [P, P, SZ, SZ, P]),
+    "zg_attention_value": (C.c_int, [P, P, P, SZ, SZ, SZ, SZ, P]),
+    "zg_model_load": (C.c_int, [P, C.c_uint64, P, P, SZ, C.POINTER(P)]),
+    "zg_model_destroy": (None, [P]),
+    "zg_session_create": (C.c_int, [P, SZ, SZ, C.c_int, C.POINTER(P)]),
+    "zg_session_destroy": (None, [P]),
+    "zg_session_reset": (C.c_int, [P]),
+    "zg_session_position": (C.c_int, [P, SZ]),
+    "zg_decode_step": (C.c_int, [P, SZ, P, P, P]),
+    "zg_prefill": (C.c_int, [P, SZ, SZ, P, P]),
+    "zg_decode_step_device": (C.c_int, [P, SZ, P, P, P, P]),
+    "zg_session_check": (C.c_int, [P, P]),
+    "zg_state_floats": (SZ, [P, SZ]),
+    "zg_state_export": (C.c_int, [P, SZ, P, SZ]),
+    "zg_state_import": (C.c_int, [P, SZ, P, SZ, C.c_int]),
+    "zg_session_fill_random": (C.c_int, [P, SZ, SZ, C.c_uint64]),
+    "zg_act_prepared_bytes": (SZ, [P, SZ]),
+    "zg_act_prepare_device": (C.c_int, [P, P, P, C.c_int, SZ, P, C.c_float, P, SZ, P]),
+    "zg_gemv_prepared_device": (C.c_int, [P, P, SZ, P, P, P]),
 }
 
 

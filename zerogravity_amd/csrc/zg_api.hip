@@ -10,44 +10,15 @@
 #include <tuple>
 #include <vector>
 
-#include "zg_hip.h"
-#include "zg_internal.hpp"
+#include "zg_context.hpp"
 
-struct zg_weight {
-    zg::DeviceWeight dw;
-    uint64_t source = 0;
-    std::string name;
-};
-
-struct DeviceBuffer {
-    void* ptr = nullptr;
-    size_t bytes = 0;
-};
-
-struct zg_ctx {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    std::mutex mu;
-    std::string err;
-    std::map<std::tuple<uint64_t, std::string, int, size_t, size_t>, std::unique_ptr<zg_weight>> weights;
-    DeviceBuffer scratch;    // region calls: inputs/outputs staged here
-    DeviceBuffer actbuf;     // zg_gemv_device: prepared activations
-    int* d_flag = nullptr;
-};
-
-namespace {
+namespace zgc {
 
 int fail(zg_ctx* ctx, int code, const std::string& msg) {
     if (ctx) ctx->err = msg;
     return code;
 }
 
-#define ZG_HIP(expr)                                                                               \
-    do {                                                                                           \
-        hipError_t e_ = (expr);                                                                    \
-        if (e_ != hipSuccess)                                                                      \
-            return fail(ctx, ZG_E_DEVICE, std::string(#expr) + " failed: " + hipGetErrorString(e_)); \
-    } while (0)
 
 bool all_finite(const float* x, size_t n) {
     for (size_t i = 0; i < n; ++i)
@@ -149,7 +120,9 @@ int lookup_or_register(zg_ctx* ctx, uint64_t source, const char* name, int type,
     return ZG_COMPLETED;
 }
 
-}  // namespace
+}  // namespace zgc
+
+using namespace zgc;
 
 extern "C" {
 
@@ -175,7 +148,7 @@ int zg_ctx_create(int device, zg_ctx** out) {
 void zg_ctx_destroy(zg_ctx* ctx) {
     if (!ctx) return;
     {
-        std::lock_guard<std::mutex> g(ctx->mu);
+        std::lock_guard<std::recursive_mutex> g(ctx->mu);
         (void)hipSetDevice(ctx->device);
         (void)hipStreamSynchronize(ctx->stream);
         for (auto& kv : ctx->weights) free_weight(kv.second.get());
@@ -193,7 +166,7 @@ const char* zg_last_error(const zg_ctx* ctx) { return ctx ? ctx->err.c_str() : "
 int zg_weight_register(zg_ctx* ctx, uint64_t source_id, const char* name, int ggml_type, size_t columns,
                        size_t rows, const void* bytes, size_t len, zg_weight** out) {
     if (!ctx || !out || !name || !*name) return fail(ctx, ZG_E_MALFORMED, "invalid registration arguments");
-    std::lock_guard<std::mutex> g(ctx->mu);
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
     if (source_id == 0) return fail(ctx, ZG_E_MALFORMED, "unbound source identity cannot key a resident weight");
     int rc = check_matrix(ctx, ggml_type, columns, rows, bytes, len);
@@ -204,7 +177,7 @@ int zg_weight_register(zg_ctx* ctx, uint64_t source_id, const char* name, int gg
 
 int zg_source_release(zg_ctx* ctx, uint64_t source_id) {
     if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::mutex> g(ctx->mu);
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
     ZG_HIP(hipStreamSynchronize(ctx->stream));
     for (auto it = ctx->weights.begin(); it != ctx->weights.end();) {
@@ -222,7 +195,7 @@ size_t zg_weight_device_bytes(const zg_weight* w) { return w ? w->dw.qs_bytes + 
 
 int zg_weight_dequantize(zg_ctx* ctx, const zg_weight* w, float* out, size_t out_len) {
     if (!ctx || !w || !out) return fail(ctx, ZG_E_MALFORMED, "invalid arguments");
-    std::lock_guard<std::mutex> g(ctx->mu);
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
     const size_t n = w->dw.N * w->dw.K;
     if (out_len != n) return fail(ctx, ZG_E_MALFORMED, "output length mismatch");
@@ -238,7 +211,7 @@ int zg_matvec(zg_ctx* ctx, uint64_t source_id, const char* tensor_name, int ggml
               const void* packed_weights, size_t packed_len, const float* activation, size_t activation_len,
               float* out, size_t out_len) {
     if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::mutex> g(ctx->mu);
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
     if (!tensor_name || !*tensor_name || !activation || !out || activation_len != columns || out_len != rows)
         return fail(ctx, ZG_E_MALFORMED, "invalid matvec region");
@@ -256,20 +229,20 @@ int zg_matvec(zg_ctx* ctx, uint64_t source_id, const char* tensor_name, int ggml
         if (rc) return rc;
         w = temp.get();
     }
-    const size_t ox = 0, oq = align256(columns * 4), od = oq + align256(columns), oy = od + align256(columns / 32 * 4 + 4);
+    const size_t prep = zg::prepared_bytes(ggml_type, 1, columns);
+    const size_t oy = align256(columns * 4) + align256(prep);
     rc = ensure(ctx, ctx->scratch, oy + align256(rows * 4));
     if (rc) {
         free_weight(temp.get());
         return rc;
     }
     char* base = (char*)ctx->scratch.ptr;
-    float* xf = (float*)(base + ox);
-    int8_t* aq = (int8_t*)(base + oq);
-    float* ad = (float*)(base + od);
+    float* xf = (float*)base;
+    void* prepared = base + align256(columns * 4);
     float* y = (float*)(base + oy);
     ZG_HIP(hipMemcpyAsync(xf, activation, columns * 4, hipMemcpyHostToDevice, ctx->stream));
-    if (ggml_type == ZG_Q8_0) ZG_HIP(zg::act_prep(xf, 0, 1, columns, nullptr, 0.0f, nullptr, aq, ad, ctx->stream));
-    ZG_HIP(zg::gemv(w->dw, 1, xf, aq, ad, y, ctx->stream));
+    ZG_HIP(zg::act_prepare_for(ggml_type, xf, 0, 1, columns, nullptr, 0.0f, prepared, ctx->stream));
+    ZG_HIP(zg::gemv(w->dw, 1, prepared, y, ctx->stream));
     ZG_HIP(hipMemcpyAsync(out, y, rows * 4, hipMemcpyDeviceToHost, ctx->stream));
     ZG_HIP(hipStreamSynchronize(ctx->stream));
     free_weight(temp.get());
@@ -280,7 +253,7 @@ int zg_matvec(zg_ctx* ctx, uint64_t source_id, const char* tensor_name, int ggml
 int zg_embedding(zg_ctx* ctx, uint64_t source_id, const char* tensor_name, int ggml_type, const void* packed_weights,
                  size_t packed_len, uint32_t token, size_t width, size_t vocabulary, float* out, size_t out_len) {
     if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::mutex> g(ctx->mu);
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
     if (!tensor_name || !*tensor_name || !out || out_len != width || width == 0 || vocabulary == 0 || token >= vocabulary)
         return fail(ctx, ZG_E_MALFORMED, "invalid original source embedding region");
@@ -349,7 +322,7 @@ int zg_rms_norm(zg_ctx* ctx, const float* input, const float* weights, size_t n,
 int zg_grouped_rms_norm(zg_ctx* ctx, const float* input, const float* weights, size_t width, size_t groups, float eps,
                         float* out) {
     if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::mutex> g(ctx->mu);
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
     if (!input || !weights || !out || width == 0 || groups == 0 || !std::isfinite(eps) || eps <= 0.0f)
         return fail(ctx, ZG_E_MALFORMED, "invalid grouped RMS normalization dimensions");
@@ -366,7 +339,7 @@ int zg_grouped_rms_norm(zg_ctx* ctx, const float* input, const float* weights, s
 
 int zg_silu(zg_ctx* ctx, const float* input, const float* multiplier, size_t n, float* out) {
     if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::mutex> g(ctx->mu);
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
     if (!input || !out || n == 0 || !all_finite(input, n) || (multiplier && !all_finite(multiplier, n)))
         return fail(ctx, ZG_E_MALFORMED, "invalid source SiLU inputs");
@@ -382,7 +355,7 @@ int zg_silu(zg_ctx* ctx, const float* input, const float* multiplier, size_t n, 
 
 int zg_binary(zg_ctx* ctx, int kind, const float* left, const float* right, size_t n, float* out) {
     if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::mutex> g(ctx->mu);
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
     if (!left || !right || !out || n == 0 || (kind != 0 && kind != 1) || !all_finite(left, n) || !all_finite(right, n))
         return fail(ctx, ZG_E_MALFORMED, "invalid source binary region");
@@ -398,55 +371,54 @@ int zg_binary(zg_ctx* ctx, int kind, const float* left, const float* right, size
 
 // ------------------------------------------------------------- device API
 
-int zg_act_prepare_device(zg_ctx* ctx, const void* x, int x_dtype, size_t m_rows, size_t columns, const float* gamma,
-                          float eps, float* xf, int8_t* codes, float* scales, void* stream) {
+size_t zg_act_prepared_bytes(const zg_weight* w, size_t m_rows) {
+    return w ? zg::prepared_bytes(w->dw.type, m_rows, w->dw.K) : 0;
+}
+
+int zg_act_prepare_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows,
+                          const float* gamma, float eps, void* prepared, size_t prepared_len, void* stream) {
     if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::mutex> g(ctx->mu);
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
-    if (!x || m_rows == 0 || (x_dtype != ZG_BF16 && x_dtype != ZG_F32) || (!xf && !codes) || (codes && !scales))
+    if (!w || !x || !prepared || m_rows == 0 || (x_dtype != ZG_BF16 && x_dtype != ZG_F32))
         return fail(ctx, ZG_E_MALFORMED, "invalid activation preparation");
+    if (prepared_len < zg::prepared_bytes(w->dw.type, m_rows, w->dw.K))
+        return fail(ctx, ZG_E_MALFORMED, "prepared activation buffer too small");
+    if (!zg::gemv_supported(w->dw.type, w->dw.K, m_rows)) return fail(ctx, ZG_UNSUPPORTED, "geometry not offered");
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    ZG_HIP(zg::act_prep(x, x_dtype == ZG_BF16, m_rows, columns, gamma, eps, xf, codes, scales, s));
+    ZG_HIP(zg::act_prepare_for(w->dw.type, x, x_dtype == ZG_BF16, m_rows, w->dw.K, gamma, eps, prepared, s));
     return ZG_COMPLETED;
 }
 
-int zg_gemv_prepared_device(zg_ctx* ctx, const zg_weight* w, size_t m_rows, const float* xf, const int8_t* codes,
-                            const float* scales, float* y, void* stream) {
+int zg_gemv_prepared_device(zg_ctx* ctx, const zg_weight* w, size_t m_rows, const void* prepared, float* y,
+                            void* stream) {
     if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::mutex> g(ctx->mu);
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
-    if (!w || !y) return fail(ctx, ZG_E_MALFORMED, "invalid gemv arguments");
+    if (!w || !y || !prepared) return fail(ctx, ZG_E_MALFORMED, "invalid gemv arguments");
     if (!zg::gemv_supported(w->dw.type, w->dw.K, m_rows)) return fail(ctx, ZG_UNSUPPORTED, "geometry not offered");
-    if (w->dw.type == ZG_Q8_0 ? (!codes || !scales) : !xf) return fail(ctx, ZG_E_MALFORMED, "missing activation");
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    ZG_HIP(zg::gemv(w->dw, m_rows, xf, codes, scales, y, s));
+    ZG_HIP(zg::gemv(w->dw, m_rows, prepared, y, s));
     return ZG_COMPLETED;
 }
 
 int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows, const float* gamma,
                    float eps, float* y, void* stream) {
     if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::mutex> g(ctx->mu);
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
     if (!w || !x || !y || (x_dtype != ZG_BF16 && x_dtype != ZG_F32)) return fail(ctx, ZG_E_MALFORMED, "invalid gemv arguments");
     if (!zg::gemv_supported(w->dw.type, w->dw.K, m_rows)) return fail(ctx, ZG_UNSUPPORTED, "geometry not offered");
-    const size_t K = w->dw.K, M = m_rows;
-    const size_t oq = align256(M * K * 4), od = oq + align256(M * K), end = od + align256(M * (K / 32 + 1) * 4);
+    const size_t need = zg::prepared_bytes(w->dw.type, m_rows, w->dw.K);
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
-    if (ctx->actbuf.bytes < end) {
+    if (ctx->actbuf.bytes < need) {
         // Growing the buffer must not race work still queued on the caller stream.
         ZG_HIP(hipStreamSynchronize(s));
     }
-    int rc = ensure(ctx, ctx->actbuf, end);
+    int rc = ensure(ctx, ctx->actbuf, need);
     if (rc) return rc;
-    char* base = (char*)ctx->actbuf.ptr;
-    float* xf = (float*)base;
-    int8_t* aq = (int8_t*)(base + oq);
-    float* ad = (float*)(base + od);
-    const bool q8 = w->dw.type == ZG_Q8_0;
-    ZG_HIP(zg::act_prep(x, x_dtype == ZG_BF16, M, K, gamma, eps, q8 ? nullptr : xf, q8 ? aq : nullptr,
-                        q8 ? ad : nullptr, s));
-    ZG_HIP(zg::gemv(w->dw, M, xf, aq, ad, y, s));
+    ZG_HIP(zg::act_prepare_for(w->dw.type, x, x_dtype == ZG_BF16, m_rows, w->dw.K, gamma, eps, ctx->actbuf.ptr, s));
+    ZG_HIP(zg::gemv(w->dw, m_rows, ctx->actbuf.ptr, y, s));
     return ZG_COMPLETED;
 }
 

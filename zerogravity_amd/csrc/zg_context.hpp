@@ -1,0 +1,54 @@
+// Context and resident-weight types shared by the C ABI translation units.
+#pragma once
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <tuple>
+
+#include "zg_hip.h"
+#include "zg_internal.hpp"
+
+struct zg_weight {
+    zg::DeviceWeight dw;
+    uint64_t source = 0;
+    std::string name;
+};
+
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+struct zg_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::recursive_mutex mu;
+    std::string err;
+    std::map<std::tuple<uint64_t, std::string, int, size_t, size_t>, std::unique_ptr<zg_weight>> weights;
+    DeviceBuffer scratch;    // region calls: inputs/outputs staged here
+    DeviceBuffer actbuf;     // zg_gemv_device: prepared activations
+    int* d_flag = nullptr;
+};
+
+namespace zgc {
+
+int fail(zg_ctx* ctx, int code, const std::string& msg);
+int ensure(zg_ctx* ctx, DeviceBuffer& b, size_t bytes);
+size_t align256(size_t n);
+void free_weight(zg_weight* w);
+int check_matrix(zg_ctx* ctx, int type, size_t cols, size_t rows, const void* bytes, size_t len);
+int lookup_or_register(zg_ctx* ctx, uint64_t source, const char* name, int type, size_t cols, size_t rows,
+                       const void* bytes, size_t len, zg_weight** out);
+int build_weight(zg_ctx* ctx, int type, size_t cols, size_t rows, const void* bytes, size_t len,
+                 std::unique_ptr<zg_weight>& out);
+bool all_finite(const float* x, size_t n);
+
+}  // namespace zgc
+
+#define ZG_HIP(expr)                                                                                     \
+    do {                                                                                                 \
+        hipError_t e_ = (expr);                                                                          \
+        if (e_ != hipSuccess)                                                                            \
+            return zgc::fail(ctx, ZG_E_DEVICE, std::string(#expr) + " failed: " + hipGetErrorString(e_)); \
+    } while (0)

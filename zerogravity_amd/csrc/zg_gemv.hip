@@ -180,7 +180,8 @@ template <bool XBF16>
 __global__ __launch_bounds__(256) void act_prep_kernel(const void* __restrict__ x, int K,
                                                        const float* __restrict__ gamma, float eps,
                                                        float* __restrict__ xf, int8_t* __restrict__ aq,
-                                                       float* __restrict__ ad) {
+                                                       float* __restrict__ ad, int16_t* __restrict__ x4,
+                                                       float* __restrict__ m4) {
     extern __shared__ float sx[];
     __shared__ double red[4];
     __shared__ float inv_s;
@@ -232,17 +233,63 @@ __global__ __launch_bounds__(256) void act_prep_kernel(const void* __restrict__ 
             if (l == 0) ad[m * nb + b] = f16_roundtrip(d);
         }
     }
+    if (x4) {
+        // Q4_K record per 64-element group pair (see gemv_q4k_kernel): 32
+        // dwords of int16 pairs ordered XL0[8] XL1[8] XH0[8] XH1[8] where for
+        // element t of a group, dword = (t&1 ? 8 : 0) + (t>>2), half = (t>>1)&1,
+        // plus {xs_lo, xs_hi, sum_lo, sum_hi}.
+        const int npc = K >> 6;
+        const int l = tid & 31;
+        for (int gi = tid >> 5; gi < 2 * npc; gi += 8) {  // one 32-lane group per 32 elements
+            const int pc = gi >> 1, hi = gi & 1;
+            const float v = sx[gi * 32 + l];
+            float amax = fabsf(v), sum = v;
+            for (int off = 16; off > 0; off >>= 1) {
+                amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+                sum += __shfl_xor(sum, off, 32);
+            }
+            const float inv = amax == 0.0f ? 0.0f : 32767.0f / amax;
+            const int q = (int)rintf(v * inv);
+            const int dw = hi * 16 + ((l & 1) ? 8 : 0) + (l >> 2);
+            const int half = (l >> 1) & 1;
+            x4[((size_t)m * npc + pc) * 64 + dw * 2 + half] = (int16_t)q;
+            if (l == 0) {
+                m4[((size_t)m * npc + pc) * 4 + hi] = amax / 32767.0f;
+                m4[((size_t)m * npc + pc) * 4 + 2 + hi] = sum;
+            }
+        }
+    }
 }
 
 hipError_t act_prep(const void* x, int x_bf16, size_t M, size_t K, const float* gamma, float eps,
-                    float* xf, int8_t* aq, float* ad, hipStream_t s) {
-    if (M == 0 || K == 0 || K > 8192 || (aq && K % 32)) return hipErrorInvalidValue;
+                    float* xf, int8_t* aq, float* ad, int16_t* x4, float* m4, hipStream_t s) {
+    if (M == 0 || K == 0 || K > 8192 || (aq && K % 32) || (x4 && K % 256)) return hipErrorInvalidValue;
     size_t lds = K * sizeof(float);
     if (x_bf16)
-        hipLaunchKernelGGL(act_prep_kernel<true>, dim3((unsigned)M), dim3(256), lds, s, x, (int)K, gamma, eps, xf, aq, ad);
+        hipLaunchKernelGGL(act_prep_kernel<true>, dim3((unsigned)M), dim3(256), lds, s, x, (int)K, gamma, eps, xf,
+                           aq, ad, x4, m4);
     else
-        hipLaunchKernelGGL(act_prep_kernel<false>, dim3((unsigned)M), dim3(256), lds, s, x, (int)K, gamma, eps, xf, aq, ad);
+        hipLaunchKernelGGL(act_prep_kernel<false>, dim3((unsigned)M), dim3(256), lds, s, x, (int)K, gamma, eps, xf,
+                           aq, ad, x4, m4);
     return hipGetLastError();
+}
+
+size_t prepared_bytes(int type, size_t M, size_t K) {
+    auto a = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    if (type == kQ8_0) return a(M * K) + a(M * (K / 32) * 4);
+    if (type == kQ4_K) return a(M * K * 2) + a(M * (K / 64) * 16);
+    return a(M * K * 4);
+}
+
+hipError_t act_prepare_for(int type, const void* x, int x_bf16, size_t M, size_t K, const float* gamma, float eps,
+                           void* prepared, hipStream_t s) {
+    auto a = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    char* base = (char*)prepared;
+    if (type == kQ8_0) return act_prep(x, x_bf16, M, K, gamma, eps, nullptr, (int8_t*)base, (float*)(base + a(M * K)),
+                                       nullptr, nullptr, s);
+    if (type == kQ4_K) return act_prep(x, x_bf16, M, K, gamma, eps, nullptr, nullptr, nullptr, (int16_t*)base,
+                                       (float*)(base + a(M * K * 2)), s);
+    return act_prep(x, x_bf16, M, K, gamma, eps, (float*)base, nullptr, nullptr, nullptr, nullptr, s);
 }
 
 // ----------------------------------------------------------------- GEMV Q8_0
@@ -339,8 +386,8 @@ __global__ __launch_bounds__(256) void gemv_q8_0_kernel(const int8_t* __restrict
 template <int CH, int MT>
 __global__ __launch_bounds__(256) void gemv_q4k_kernel(const uint8_t* __restrict__ qs,
                                                        const v4u* __restrict__ hdr,
-                                                       const float* __restrict__ x, float* __restrict__ y,
-                                                       int N, int K, int M, int lpr_log2) {
+                                                       const int16_t* __restrict__ xq, const float* __restrict__ xm,
+                                                       float* __restrict__ y, int N, int K, int M, int lpr_log2) {
     typedef short v2s __attribute__((ext_vector_type(2)));
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << lpr_log2;
@@ -354,7 +401,8 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(const uint8_t* __restrict
     const int m0 = blockIdx.y * MT;
     const int p = sub & 3;
 
-    // activation: packed int16 pairs matching the weight pair order
+    // activation records prepared by act_prep_kernel (int16 pairs in the
+    // weight pair order, group scales and exact f32 group sums)
     int xl0[MT][CH][8], xl1[MT][CH][8], xh0[MT][CH][8], xh1[MT][CH][8];
     float xs_lo[MT][CH], xs_hi[MT][CH], sx_lo[MT][CH], sx_hi[MT][CH];
 #pragma unroll
@@ -363,41 +411,25 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(const uint8_t* __restrict
         for (int i = 0; i < CH; ++i) {
             const int c = sub + i * lpr;
             const bool ok = c < nchunk && m0 + m < M;
-            const float* lo = x + (size_t)(ok ? m0 + m : 0) * K + (size_t)(ok ? c >> 2 : 0) * 256 + 64 * p;
-            const float* hi = lo + 32;
-            float alo = 0.0f, ahi = 0.0f, slo = 0.0f, shi = 0.0f;
             if (ok) {
+                const v4i* rec = (const v4i*)(xq + ((size_t)(m0 + m) * nchunk + c) * 64);
+                const v4f mt4 = *(const v4f*)(xm + ((size_t)(m0 + m) * nchunk + c) * 4);
 #pragma unroll
-                for (int t = 0; t < 32; ++t) {
-                    alo = fmaxf(alo, fabsf(lo[t]));
-                    ahi = fmaxf(ahi, fabsf(hi[t]));
-                    slo += lo[t];
-                    shi += hi[t];
+                for (int j = 0; j < 2; ++j) {
+                    const v4i r0 = rec[j], r1 = rec[2 + j], r2 = rec[4 + j], r3 = rec[6 + j];
+                    xl0[m][i][4 * j + 0] = r0.x; xl0[m][i][4 * j + 1] = r0.y; xl0[m][i][4 * j + 2] = r0.z; xl0[m][i][4 * j + 3] = r0.w;
+                    xl1[m][i][4 * j + 0] = r1.x; xl1[m][i][4 * j + 1] = r1.y; xl1[m][i][4 * j + 2] = r1.z; xl1[m][i][4 * j + 3] = r1.w;
+                    xh0[m][i][4 * j + 0] = r2.x; xh0[m][i][4 * j + 1] = r2.y; xh0[m][i][4 * j + 2] = r2.z; xh0[m][i][4 * j + 3] = r2.w;
+                    xh1[m][i][4 * j + 0] = r3.x; xh1[m][i][4 * j + 1] = r3.y; xh1[m][i][4 * j + 2] = r3.z; xh1[m][i][4 * j + 3] = r3.w;
                 }
-            }
-            const float ilo = alo == 0.0f ? 0.0f : 32767.0f / alo;
-            const float ihi = ahi == 0.0f ? 0.0f : 32767.0f / ahi;
-            xs_lo[m][i] = alo / 32767.0f;
-            xs_hi[m][i] = ahi / 32767.0f;
-            sx_lo[m][i] = slo;
-            sx_hi[m][i] = shi;
+                xs_lo[m][i] = mt4.x;
+                xs_hi[m][i] = mt4.y;
+                sx_lo[m][i] = mt4.z;
+                sx_hi[m][i] = mt4.w;
+            } else {
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                int a0 = 0, a1 = 0, a2 = 0, a3 = 0, b0 = 0, b1 = 0, b2 = 0, b3 = 0;
-                if (ok) {
-                    a0 = (int)rintf(lo[4 * q + 0] * ilo);
-                    a1 = (int)rintf(lo[4 * q + 1] * ilo);
-                    a2 = (int)rintf(lo[4 * q + 2] * ilo);
-                    a3 = (int)rintf(lo[4 * q + 3] * ilo);
-                    b0 = (int)rintf(hi[4 * q + 0] * ihi);
-                    b1 = (int)rintf(hi[4 * q + 1] * ihi);
-                    b2 = (int)rintf(hi[4 * q + 2] * ihi);
-                    b3 = (int)rintf(hi[4 * q + 3] * ihi);
-                }
-                xl0[m][i][q] = (a0 & 0xffff) | (a2 << 16);
-                xl1[m][i][q] = (a1 & 0xffff) | (a3 << 16);
-                xh0[m][i][q] = (b0 & 0xffff) | (b2 << 16);
-                xh1[m][i][q] = (b1 & 0xffff) | (b3 << 16);
+                for (int q = 0; q < 8; ++q) xl0[m][i][q] = xl1[m][i][q] = xh0[m][i][q] = xh1[m][i][q] = 0;
+                xs_lo[m][i] = xs_hi[m][i] = sx_lo[m][i] = sx_hi[m][i] = 0.0f;
             }
         }
     }
@@ -523,10 +555,16 @@ static void launch_q8(int ch, dim3 g, hipStream_t s, const DeviceWeight& w, cons
     }
 }
 
-hipError_t gemv(const DeviceWeight& w, size_t M, const float* xf, const int8_t* aq, const float* ad, float* y,
-                hipStream_t s) {
+hipError_t gemv(const DeviceWeight& w, size_t M, const void* prepared, float* y, hipStream_t s) {
     if (!gemv_supported(w.type, w.K, M)) return hipErrorInvalidValue;
     const int K = (int)w.K, N = (int)w.N;
+    auto a = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    const char* base = (const char*)prepared;
+    const float* xf = (const float*)base;
+    const int8_t* aq = (const int8_t*)base;
+    const float* ad = (const float*)(base + a(M * w.K));
+    const int16_t* x4 = (const int16_t*)base;
+    const float* m4 = (const float*)(base + a(M * w.K * 2));
     if (w.type == kQ8_0) {
         const int nchunk = K / 16;
         const int l = pick_lpr_log2(nchunk, 4);
@@ -552,7 +590,7 @@ hipError_t gemv(const DeviceWeight& w, size_t M, const float* xf, const int8_t* 
         dim3 g(grid_for(w.N, l), (unsigned)((M + mt - 1) / mt));
         const uint8_t* q = (const uint8_t*)w.qs;
         const v4u* h = (const v4u*)w.hdr;
-#define ZG_Q4(C, T) hipLaunchKernelGGL((gemv_q4k_kernel<C, T>), g, dim3(256), 0, s, q, h, xf, y, N, K, (int)M, l)
+#define ZG_Q4(C, T) hipLaunchKernelGGL((gemv_q4k_kernel<C, T>), g, dim3(256), 0, s, q, h, x4, m4, y, N, K, (int)M, l)
         if (mt == 1) {
             switch (ch) {
             case 1: ZG_Q4(1, 1); break;

@@ -35,16 +35,25 @@ hipError_t repack_weight(const uint8_t* d_gguf, DeviceWeight& w, int* d_bad, hip
 hipError_t dequantize_rows(const DeviceWeight& w, size_t row0, size_t rows, float* out, hipStream_t s);
 
 // Activation preparation for M rows of width K: optional RMSNorm with gamma
-// (f64 sum of f32 squares, f32 mean, 1/sqrtf, (x*inv)*gamma), then either
-// f32 output (xf) and/or the dynamic Q8_0 coding (aq codes, ad f16-rounded
-// scales).  x is bf16 when x_bf16 != 0, else f32.
+// (f64 sum of f32 squares, f32 mean, 1/sqrtf, (x*inv)*gamma), then any of:
+// f32 output (xf); the dynamic Q8_0 coding (aq codes, ad f16-rounded
+// scales); the Q4_K int16 group-pair records (x4, m4).  x is bf16 when
+// x_bf16 != 0, else f32.
 hipError_t act_prep(const void* x, int x_bf16, size_t M, size_t K, const float* gamma, float eps,
-                    float* xf, int8_t* aq, float* ad, hipStream_t s);
+                    float* xf, int8_t* aq, float* ad, int16_t* x4, float* m4, hipStream_t s);
 
-// y[M][N] = W x for a registered weight.  Q8_0 consumes (aq, ad); Q4_K and
-// F32 consume xf.  Returns hipErrorInvalidValue for unsupported geometry.
-hipError_t gemv(const DeviceWeight& w, size_t M, const float* xf, const int8_t* aq, const float* ad,
-                float* y, hipStream_t s);
+// The activation format a weight type consumes, in one device buffer:
+//   Q8_0: int8 codes [M][K], then f32 scales [M][K/32]
+//   Q4_K: int16 records [M][K/64][64], then f32 {xs_lo, xs_hi, sum_lo, sum_hi} [M][K/64]
+//   F32 : f32 [M][K]
+// (each part 256-byte aligned).
+size_t prepared_bytes(int type, size_t M, size_t K);
+hipError_t act_prepare_for(int type, const void* x, int x_bf16, size_t M, size_t K, const float* gamma, float eps,
+                           void* prepared, hipStream_t s);
+
+// y[M][N] = W x for a registered weight over a prepared activation.
+// Returns hipErrorInvalidValue for unsupported geometry.
+hipError_t gemv(const DeviceWeight& w, size_t M, const void* prepared, float* y, hipStream_t s);
 bool gemv_supported(int type, size_t K, size_t M);
 
 // Pointwise / normalisation kernels (zg_elementwise.hip).
@@ -52,5 +61,59 @@ hipError_t rms_groups(const float* x, const float* w, size_t width, size_t group
                       hipStream_t s);
 hipError_t silu(const float* x, const float* m, size_t n, float* out, hipStream_t s);
 hipError_t binary(int kind, const float* a, const float* b, size_t n, float* out, hipStream_t s);
+
+// Gated DeltaNet decode (zg_gdn.hip).  Strides are in floats per row.
+hipError_t gdn_conv(const float* x, const float* w, float* hist, float* out, size_t C, size_t rows, int apply_silu,
+                    size_t x_stride, size_t hist_stride, size_t out_stride, hipStream_t s);
+hipError_t gdn_coefficients(const float* alpha, const float* beta, const float* dt, const float* a, size_t H,
+                            float* gain, float* beta_out, float* sp, float* gr, hipStream_t s);
+// fused: q/k L2 + coefficients from raw alpha/beta projections (model path);
+// otherwise alpha/beta carry gain/beta and scale_h (nullable) the per-head scale.
+hipError_t gdn_recurrent(bool fused, const float* q, const float* k, const float* v, size_t src_stride,
+                         const float* alpha, const float* beta, size_t coef_stride, const float* dt, const float* a,
+                         float eps, float scale, const float* scale_h, float* state, float* out, size_t out_stride,
+                         size_t H, size_t D, size_t rows, hipStream_t s);
+
+// GQA decode attention (zg_attn.hip), d = 256, <= 8 query heads, <= 4 per kv
+// head.  Scores/probs are compact per row: [h][ntok[b]] at b*score_stride.
+struct AttnArgs {
+    int B = 0, nq = 0, nkv = 0, d = 0, rotate = 64, tmax = 0, splits = 1;
+    int kv_bf16 = 0, do_prep = 0, prep_only = 0, norm = 1;
+    const float* qproj = nullptr;  // [B][nq*2d] (q | gate per head)
+    size_t q_stride = 0;
+    const float *kproj = nullptr, *vproj = nullptr;
+    size_t kv_stride = 0;
+    const float *qnorm = nullptr, *knorm = nullptr;
+    const int* pos = nullptr;   // [B] position written by this step
+    const int* ntok = nullptr;  // [B] valid tokens
+    float theta_scale = 0.0f, eps = 0.0f, scale = 0.0f;
+    float* qr = nullptr;  // [B][nq*d] roped query
+    size_t qr_stride = 0;
+    void *kcache = nullptr, *vcache = nullptr;  // [B][tmax][nkv*d] KV
+    size_t cache_row_stride = 0;                // elements per row
+    float *kout = nullptr, *vout = nullptr;     // direct f32 k/v outputs (region path)
+    float *dots = nullptr, *scores = nullptr, *exps = nullptr, *probs = nullptr;
+    double* sums = nullptr;
+    size_t score_stride = 0;
+    float* part = nullptr;  // [B][splits][nq][d]
+    const float* gate = nullptr;
+    size_t gate_stride = 0;
+    float* out = nullptr;
+    size_t out_stride = 0;
+};
+hipError_t attention(const AttnArgs& a, hipStream_t s);            // prep (if do_prep) + all parts
+hipError_t rope_prep(const AttnArgs& a, hipStream_t s);            // norm + RoPE + KV append only
+hipError_t attention_parts(const AttnArgs& a, bool qk, bool softmax, bool pv, hipStream_t s);
+hipError_t softmax_rows(const float* scores, size_t score_stride, const int* ntok, float* probs, size_t heads, size_t B,
+                        hipStream_t s);
+
+// Model-step helpers (zg_model.hip).  `status` is a device word: bit 0
+// nonfinite residual, bit 1 out-of-vocabulary token, bit 2 nonfinite logits.
+hipError_t embed(const DeviceWeight& w, const uint32_t* tokens, float* x, size_t B, int* status, hipStream_t s);
+hipError_t residual_add(float* x, const float* y, size_t n, int* status, hipStream_t s);
+hipError_t argmax(const float* logits, size_t V, size_t B, uint32_t* out, int* status, hipStream_t s);
+hipError_t fill_normal(void* p, size_t n, bool bf16, uint64_t seed, float sigma, hipStream_t s);
+hipError_t convert_kv(const void* in, void* out, size_t n, bool to_f32, hipStream_t s);
+hipError_t fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
 
 }  // namespace zg

@@ -1,0 +1,237 @@
+// Resident Qwen3.5 hybrid model and decode sessions (boundary B).
+//
+// Schedule: forward::forward_token (model-qwen35/src/forward.rs:451-516)
+// with gdn_layer (:518-632) and attention_layer (:634-755), run for B
+// independent rows at once (continuous batch).  Each row keeps its own
+// position; weights stream from HBM once per step for all rows.
+//
+// Per layer (B rows):
+//   GDN:  prep(rms attn_norm) -> GEMV qkv, z, alpha, beta -> conv+SiLU ->
+//         recurrence (L2 + coefficients fused) -> grouped RMS(ssm_norm) * silu(z)
+//         -> prep -> GEMV ssm_out -> residual add
+//   ATTN: prep(rms attn_norm) -> GEMV q|gate, k, v -> norm+RoPE+KV append ->
+//         QK -> softmax -> PV -> sigmoid gate -> prep -> GEMV attn_output -> add
+//   FFN:  prep(rms post_attention_norm) -> GEMV gate, up -> up*silu(gate) ->
+//         prep -> GEMV down -> residual add
+// Final: prep(rms output_norm) -> GEMV token_embd (tied LM head) -> argmax.
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "zg_device.hpp"
+#include "zg_hip.h"
+#include "zg_internal.hpp"
+
+namespace zg {
+
+// --------------------------------------------------------------- kernels
+
+// Dequantize embedding rows: x[b] = token_embd[tokens[b]] (codecs/mod.rs:36-88).
+__global__ void embed_q8_0_kernel(const int8_t* __restrict__ qs, const uint16_t* __restrict__ hdr,
+                                  const uint32_t* __restrict__ tokens, float* __restrict__ x, int K, int V,
+                                  int* __restrict__ status) {
+    const int b = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= K) return;
+    const uint32_t t = tokens[b];
+    if (t >= (uint32_t)V) {
+        if (i == 0) atomicOr(status, 2);
+        x[(size_t)b * K + i] = 0.0f;
+        return;
+    }
+    x[(size_t)b * K + i] = (float)qs[(size_t)t * K + i] * f16_to_f32(hdr[(size_t)t * (K / 32) + i / 32]);
+}
+
+__global__ void embed_q4k_kernel(const uint8_t* __restrict__ qs, const v4u* __restrict__ hdr,
+                                 const uint32_t* __restrict__ tokens, float* __restrict__ x, int K, int V,
+                                 int* __restrict__ status) {
+    const int b = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= K) return;
+    const uint32_t t = tokens[b];
+    if (t >= (uint32_t)V) {
+        if (i == 0) atomicOr(status, 2);
+        x[(size_t)b * K + i] = 0.0f;
+        return;
+    }
+    const size_t blk = (size_t)t * (K / 256) + i / 256;
+    const v4u h = hdr[blk];
+    const int e = i % 256, g = e / 32, pos = e % 32;
+    const int sh = 8 * (g >> 1);
+    const uint32_t b1 = (h.y >> sh) & 0xffu, b2 = (h.z >> sh) & 0xffu, b3 = (h.w >> sh) & 0xffu;
+    uint32_t sc, mn;
+    if ((g & 1) == 0) {
+        sc = b1 & 63;
+        mn = b2 & 63;
+    } else {
+        sc = b3 & 63;
+        mn = (b1 >> 6) | ((b2 >> 6) << 2) | ((b3 >> 6) << 4);
+    }
+    const float d = f16_to_f32((uint16_t)(h.x & 0xffffu)), dmin = f16_to_f32((uint16_t)(h.x >> 16));
+    const float scale = d * (float)sc, mnf = dmin * (float)mn;
+    const uint8_t byte = qs[blk * 128 + (g >> 1) * 32 + pos];
+    const uint32_t v = (g & 1) ? (byte >> 4) : (byte & 15);
+    x[(size_t)b * K + i] = scale * (float)v - mnf;
+}
+
+__global__ void embed_f32_kernel(const float* __restrict__ w, const uint32_t* __restrict__ tokens,
+                                 float* __restrict__ x, int K, int V, int* __restrict__ status) {
+    const int b = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= K) return;
+    const uint32_t t = tokens[b];
+    if (t >= (uint32_t)V) {
+        if (i == 0) atomicOr(status, 2);
+        x[(size_t)b * K + i] = 0.0f;
+        return;
+    }
+    x[(size_t)b * K + i] = w[(size_t)t * K + i];
+}
+
+// Residual add that also flags nonfinite values (forward.rs:502 assert_finite).
+__global__ void residual_add_kernel(float* __restrict__ x, const float* __restrict__ y, size_t n,
+                                    int* __restrict__ status) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i] + y[i];
+    x[i] = v;
+    if (!finite_f32(v)) atomicOr(status, 1);
+}
+
+// Greedy readout per row: first maximum wins; nonfinite logits flag status
+// (core/src/numerics.rs:126-140).
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ logits, int V, uint32_t* __restrict__ out,
+                                                     int* __restrict__ status) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const float* row = logits + (size_t)b * V;
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    bool bad = false;
+    for (int i = tid; i < V; i += 256) {
+        const float v = row[i];
+        if (!finite_f32(v)) bad = true;
+        if (v > best) {
+            best = v;
+            bi = i;
+        }
+    }
+    if (bad) atomicOr(status, 4);
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (ov > best || (ov == best && oi < bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = best;
+        si[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        best = sv[0];
+        bi = si[0];
+        for (int w = 1; w < 4; ++w)
+            if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
+                best = sv[w];
+                bi = si[w];
+            }
+        out[b] = (uint32_t)bi;
+    }
+}
+
+// Seeded counter-based normal samples (splitmix64 + Box-Muller) for the
+// synthetic decode prefix.
+__device__ __forceinline__ uint64_t splitmix(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+__device__ __forceinline__ float normal_at(uint64_t seed, uint64_t i) {
+    const uint64_t r = splitmix(seed ^ splitmix(i));
+    const float u1 = ((float)(r >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    const float u2 = ((float)((r >> 16) & 0xffffff) + 0.5f) * (1.0f / 16777216.0f);
+    return sqrtf(-2.0f * logf(u1)) * cosf(6.28318530718f * u2);
+}
+__global__ void fill_normal_f32(float* __restrict__ p, size_t n, uint64_t seed, float sigma) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = sigma * normal_at(seed, i);
+}
+__global__ void fill_normal_bf16(uint16_t* __restrict__ p, size_t n, uint64_t seed, float sigma) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        uint32_t b = __float_as_uint(sigma * normal_at(seed, i));
+        b += 0x7fffu + ((b >> 16) & 1u);
+        p[i] = (uint16_t)(b >> 16);
+    }
+}
+__global__ void bf16_to_f32_kernel(const uint16_t* __restrict__ in, float* __restrict__ out, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = bf16_to_f32(in[i]);
+}
+__global__ void f32_to_bf16_kernel(const float* __restrict__ in, uint16_t* __restrict__ out, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    uint32_t b = __float_as_uint(in[i]);
+    b += 0x7fffu + ((b >> 16) & 1u);
+    out[i] = (uint16_t)(b >> 16);
+}
+__global__ void fill_u32_kernel(uint32_t* __restrict__ p, size_t n, uint32_t v) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+static unsigned blocks_for(size_t n, unsigned t = 256) { return (unsigned)((n + t - 1) / t); }
+
+hipError_t embed(const DeviceWeight& w, const uint32_t* tokens, float* x, size_t B, int* status, hipStream_t s) {
+    dim3 g(blocks_for(w.K), (unsigned)B);
+    if (w.type == kQ8_0)
+        hipLaunchKernelGGL(embed_q8_0_kernel, g, dim3(256), 0, s, (const int8_t*)w.qs, (const uint16_t*)w.hdr, tokens,
+                           x, (int)w.K, (int)w.N, status);
+    else if (w.type == kQ4_K)
+        hipLaunchKernelGGL(embed_q4k_kernel, g, dim3(256), 0, s, (const uint8_t*)w.qs, (const v4u*)w.hdr, tokens, x,
+                           (int)w.K, (int)w.N, status);
+    else
+        hipLaunchKernelGGL(embed_f32_kernel, g, dim3(256), 0, s, (const float*)w.qs, tokens, x, (int)w.K, (int)w.N,
+                           status);
+    return hipGetLastError();
+}
+
+hipError_t residual_add(float* x, const float* y, size_t n, int* status, hipStream_t s) {
+    hipLaunchKernelGGL(residual_add_kernel, dim3(blocks_for(n)), dim3(256), 0, s, x, y, n, status);
+    return hipGetLastError();
+}
+
+hipError_t argmax(const float* logits, size_t V, size_t B, uint32_t* out, int* status, hipStream_t s) {
+    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)B), dim3(256), 0, s, logits, (int)V, out, status);
+    return hipGetLastError();
+}
+
+hipError_t fill_normal(void* p, size_t n, bool bf16, uint64_t seed, float sigma, hipStream_t s) {
+    const unsigned g = (unsigned)std::min<size_t>(blocks_for(n), 4096);
+    if (bf16)
+        hipLaunchKernelGGL(fill_normal_bf16, dim3(g), dim3(256), 0, s, (uint16_t*)p, n, seed, sigma);
+    else
+        hipLaunchKernelGGL(fill_normal_f32, dim3(g), dim3(256), 0, s, (float*)p, n, seed, sigma);
+    return hipGetLastError();
+}
+
+hipError_t convert_kv(const void* in, void* out, size_t n, bool to_f32, hipStream_t s) {
+    if (to_f32)
+        hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(blocks_for(n)), dim3(256), 0, s, (const uint16_t*)in, (float*)out, n);
+    else
+        hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(blocks_for(n)), dim3(256), 0, s, (const float*)in, (uint16_t*)out, n);
+    return hipGetLastError();
+}
+
+hipError_t fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s) {
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks_for(n)), dim3(256), 0, s, p, n, v);
+    return hipGetLastError();
+}
+
+}  // namespace zg

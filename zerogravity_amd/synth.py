@@ -33,7 +33,8 @@ def random_q4_k(rng, rows, cols, d_scale=None):
     assert cols % 256 == 0
     nb = rows * (cols // 256)
     if d_scale is None:
-        d_scale = 3.4 / (31.0 * 7.5 * np.sqrt(cols))
+        # std(sc*q - 7.5*mn) is ~258 for uniform 6-bit sc/mn and 4-bit q
+        d_scale = 1.0 / (258.0 * np.sqrt(cols))
     out = np.empty((nb, 144), np.uint8)
     out[:, 16:] = rng.integers(0, 256, size=(nb, 128), dtype=np.uint8)
     out[:, 4:16] = rng.integers(0, 256, size=(nb, 12), dtype=np.uint8)
