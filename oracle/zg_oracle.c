@@ -364,6 +364,18 @@ int zgo_grouped_rms_norm(const float* x, const float* w, size_t width, size_t gr
 
 /* --------------------------------------------------------- exp / SiLU / misc */
 
+/* f32 transcendentals of the reference's platform libm (Rust f32::exp, ln,
+ * sin_cos, lib.rs:324-336, 357, 1566) evaluated in double and rounded once:
+ * the correctly rounded f32 value (double exp/log/sin/cos are within an ulp
+ * of double, far inside the f32 rounding interval except in measure-zero
+ * ties).  glibc's f32 versions are not correctly rounded, and no reference
+ * test pins their last bit; the HIP kernels use the same definition so the
+ * two agree bit for bit. */
+static float cr_expf(float x) { return (float)exp((double)x); }
+static float cr_logf(float x) { return (float)log((double)x); }
+static float cr_sinf(float x) { return (float)sin((double)x); }
+static float cr_cosf(float x) { return (float)cos((double)x); }
+
 /* cpu/src/ops.rs:317-350: GGML Haswell vector exp, scalar form. */
 float zgo_ggml_exp(float x) {
     if (!isfinite(x)) return expf(x);
@@ -399,13 +411,13 @@ int zgo_silu(const float* x, const float* m, size_t n, float* out) {
 }
 
 /* lib.rs:324-326 */
-float zgo_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+float zgo_sigmoid(float x) { return 1.0f / (1.0f + cr_expf(-x)); }
 
 /* lib.rs:328-336 */
 float zgo_softplus(float x) {
     if (x > 20.0f) return x;
-    if (x < -20.0f) return expf(x);
-    return logf(1.0f + expf(x));
+    if (x < -20.0f) return cr_expf(x);
+    return cr_logf(1.0f + cr_expf(x));
 }
 
 /* lib.rs:1258-1271: kind 0 = Add, 1 = SigmoidGate a*sigmoid(b). */
@@ -454,7 +466,7 @@ int zgo_gdn_coefficients(const float* alpha, const float* beta, const float* dt,
         float gr = sp * a[h];
         if (softplus_out) softplus_out[h] = sp;
         if (gate_raw_out) gate_raw_out[h] = gr;
-        gain[h] = expf(gr);
+        gain[h] = cr_expf(gr);
         beta_out[h] = zgo_sigmoid(beta[h]);
         if (!isfinite(sp) || !isfinite(gr) || !isfinite(gain[h]) || !isfinite(beta_out[h]))
             return ZGO_E_STATE;
@@ -520,7 +532,7 @@ int zgo_rope_kv(float* q, float* k, size_t hw, size_t qh, size_t kvh, size_t rot
         float* head = hd < qh ? q + hd * hw : k + (hd - qh) * hw;
         float angle = (float)pos;
         for (size_t i = 0; i < half; ++i) {
-            float s = sinf(angle), c = cosf(angle);
+            float s = cr_sinf(angle), c = cr_cosf(angle);
             float a = head[i], b = head[i + half];
             head[i] = fmaf(a, c, -(b * s));
             head[i + half] = fmaf(a, s, b * c);
@@ -699,13 +711,13 @@ static void chunk_head(const float* qn, const float* kn, const float* v, const f
     mm(qp, kp, intra, C, C, W, 0, 1);
     for (size_t t = 0; t < C; ++t)
         for (size_t s = 0; s < C; ++s) {
-            float decay = s <= t ? expf(g[t] - g[s]) : 0.0f;
+            float decay = s <= t ? cr_expf(g[t] - g[s]) : 0.0f;
             A[t * C + s] *= decay;
             intra[t * C + s] *= decay;
         }
     /* decayed beta key (in W2) and new values (in vb) */
     for (size_t t = 0; t < C; ++t) {
-        float e = expf(g[t]);
+        float e = cr_expf(g[t]);
         for (size_t d = 0; d < W; ++d) W2[t * W + d] = kb[t * W + d] * e;
         for (size_t d = 0; d < W; ++d) dq[t * W + d] = qp[t * W + d] * e;
     }
@@ -713,10 +725,10 @@ static void chunk_head(const float* qn, const float* kn, const float* v, const f
     solve_unit_lower(A, W2, C, W);
     float last = g[C - 1];
     for (size_t t = 0; t < C; ++t) {
-        float e = expf(last - g[t]);
+        float e = cr_expf(last - g[t]);
         for (size_t d = 0; d < W; ++d) dk[t * W + d] = kp[t * W + d] * e;
     }
-    float chunk_decay = expf(last);
+    float chunk_decay = cr_expf(last);
     float* pred = core; /* reuse: predicted = W2 * S */
     memset(pred, 0, sizeof(float) * C * W);
     mm(W2, S, pred, C, W, W, 0, 0);
@@ -812,6 +824,7 @@ struct zgo_session {
     float** rec;      /* per layer [H][d][d] value-major or NULL */
     float** keys;     /* per layer [max_ctx][kvw] or NULL */
     float** values;
+    int kv_bf16;      /* round appended K/V to bf16 (device cache storage) */
 };
 
 static const zgo_tensor* find(const zgo_tensor* ts, size_t n, const char* name) {
@@ -881,6 +894,16 @@ const char* zgo_model_error(const zgo_model* m) { return m->err[0] ? m->err : NU
 
 static size_t conv_ch(const zgo_model* m) { return (size_t)m->g.gdn_heads * m->g.gdn_dim * 3; }
 static size_t kvw(const zgo_model* m) { return (size_t)m->g.kv_heads * m->g.head_dim; }
+
+/* Round to the nearest bf16 (ties to even), kept as f32.  Models a device
+ * KV cache stored in bf16; the reference itself keeps f32 keys and values. */
+static float bf16_round(float x) {
+    uint32_t b = f32_bits(x);
+    b += 0x7fffu + ((b >> 16) & 1u);
+    return bits_f32(b & 0xffff0000u);
+}
+
+void zgo_session_set_kv_bf16(zgo_session* s, int on) { s->kv_bf16 = on != 0; }
 
 zgo_session* zgo_session_create(zgo_model* m) {
     if (m->err[0]) return NULL;
@@ -999,6 +1022,14 @@ int zgo_forward_token(zgo_session* s, uint32_t token, float* logits) {
             size_t T = (size_t)s->position + 1;
             memcpy(s->keys[i] + (size_t)s->position * kvw(m), kn, sizeof(float) * kvw(m));
             memcpy(s->values[i] + (size_t)s->position * kvw(m), vp, sizeof(float) * kvw(m));
+            if (s->kv_bf16) {
+                float* kr = s->keys[i] + (size_t)s->position * kvw(m);
+                float* vr = s->values[i] + (size_t)s->position * kvw(m);
+                for (size_t e = 0; e < kvw(m); ++e) {
+                    kr[e] = bf16_round(kr[e]);
+                    vr[e] = bf16_round(vr[e]);
+                }
+            }
             float* scores = (float*)malloc(sizeof(float) * nq * T);
             probs = (float*)malloc(sizeof(float) * nq * T);
             int r2 = zgo_attention_qk(qn, s->keys[i], T, hd, nq, nkv, 1.0f / sqrtf((float)hd), NULL, scores);

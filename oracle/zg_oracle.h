@@ -129,6 +129,9 @@ zgo_model*   zgo_model_create(const zgo_geometry* g, const zgo_tensor* tensors, 
 void         zgo_model_destroy(zgo_model* m);
 const char*  zgo_model_error(const zgo_model* m);
 zgo_session* zgo_session_create(zgo_model* m);
+/* Test hook (no reference counterpart): store appended K/V rounded to bf16,
+ * as a device session with a bf16 KV cache does. */
+void         zgo_session_set_kv_bf16(zgo_session* s, int on);
 void         zgo_session_destroy(zgo_session* s);
 int          zgo_session_position(const zgo_session* s);
 /* One forward_token: logits (vocab floats) written when logits != NULL. */

@@ -83,6 +83,7 @@ def _declare(L):
         "zgo_model_destroy": (None, [P]),
         "zgo_model_error": (C.c_char_p, [P]),
         "zgo_session_create": (P, [P]),
+        "zgo_session_set_kv_bf16": (None, [P, C.c_int]),
         "zgo_session_destroy": (None, [P]),
         "zgo_session_position": (C.c_int, [P]),
         "zgo_forward_token": (C.c_int, [P, C.c_uint32, P]),
@@ -296,8 +297,8 @@ class Model:
         if err:
             raise OracleError(-1, err.decode())
 
-    def session(self):
-        return Session(self)
+    def session(self, kv_bf16=False):
+        return Session(self, kv_bf16)
 
     def __del__(self):
         if getattr(self, "m", None):
@@ -306,9 +307,11 @@ class Model:
 
 
 class Session:
-    def __init__(self, model):
+    def __init__(self, model, kv_bf16=False):
         self.model = model
         self.s = lib().zgo_session_create(model.m)
+        if kv_bf16:
+            lib().zgo_session_set_kv_bf16(self.s, 1)
 
     @property
     def position(self):

@@ -106,6 +106,13 @@ class Context:
         if rc != COMPLETED:
             raise ZgError(rc, "zg_ctx_create failed (no usable HIP device?)")
         self.h = h
+        self._dependents = []  # weakrefs to models/sessions living on this ctx
+
+    def adopt(self, obj):
+        """Register an object whose native handle lives on this context; it is
+        closed before the context is destroyed, whatever the teardown order."""
+        import weakref
+        self._dependents.append(weakref.ref(obj))
 
     def error(self):
         return lib().zg_last_error(self.h).decode()
@@ -117,6 +124,11 @@ class Context:
 
     def close(self):
         if getattr(self, "h", None):
+            for ref in reversed(self._dependents):
+                obj = ref()
+                if obj is not None:
+                    obj.close()
+            self._dependents = []
             lib().zg_ctx_destroy(self.h)
             self.h = None
 

@@ -61,8 +61,9 @@ int build_weight(zg_ctx* ctx, int type, size_t cols, size_t rows, const void* by
     w->dw.K = cols;
     w->dw.N = rows;
     if (type == ZG_Q8_0) {
-        w->dw.qs_bytes = rows * cols;
-        w->dw.hdr_bytes = rows * (cols / 32) * 2;
+        const size_t nbc = (cols / 32 + 3) / 4;
+        w->dw.qs_bytes = (rows + 7) / 8 * nbc * 1024;
+        w->dw.hdr_bytes = rows * nbc * 4 * 2;
     } else if (type == ZG_Q4_K) {
         w->dw.qs_bytes = rows * (cols / 2);
         w->dw.hdr_bytes = rows * (cols / 256) * 16;

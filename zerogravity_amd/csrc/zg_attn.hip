@@ -8,6 +8,9 @@
 //   QK dot * scale                       lib.rs:1427-1441
 //   softmax (GGML exp, f64 sum)          lib.rs:1352-1387
 //   PV                                   lib.rs:1276-1305
+// Every f32 sum is formed in the reference's own order (the 32-accumulator
+// FMA tree of its dot and value loops, the 8-wide softmax partials), so the
+// outputs equal the CPU path's bit for bit.
 //   sigmoid output gate                  forward.rs:751, lib.rs:1258-1271
 //
 // KV cache: [row][token][kv_head * d] in the element type KV (bf16 for the
@@ -85,7 +88,7 @@ __global__ __launch_bounds__(64) void attn_prep_kernel(const float* __restrict__
     if (lane < half) {
         float angle = (float)p;
         for (int t = 0; t < lane; ++t) angle *= theta_scale;
-        const float sn = sinf(angle), cs = cosf(angle);
+        const float sn = cr_sinf(angle), cs = cr_cosf(angle);
         const float a = head[lane], bb = head[lane + half];
         head[lane] = fmaf(a, cs, -(bb * sn));
         head[lane + half] = fmaf(a, sn, bb * cs);
@@ -112,58 +115,89 @@ __global__ __launch_bounds__(64) void attn_prep_kernel(const float* __restrict__
 
 // -------------------------------------------------------------------- QK
 
-// Grid (ceil(Tmax/16), B); 4 waves x 4 tokens, 16 lanes per token, 16 dims
-// per lane (d = 256).  Lane keeps its 16 dims of every query head in
-// registers; the 16-lane dot partials reduce with a 4-step XOR tree.
 template <typename KV>
+__device__ __forceinline__ void kv_load4(const KV* p, float (&o)[4]);
+template <>
+__device__ __forceinline__ void kv_load4<float>(const float* p, float (&o)[4]) {
+    const v4f v = *(const v4f*)p;
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+}
+template <>
+__device__ __forceinline__ void kv_load4<uint16_t>(const uint16_t* p, float (&o)[4]) {
+    const uint2 v = *(const uint2*)p;
+    o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xffff0000u);
+    o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xffff0000u);
+}
+
+// The reference dot (source_dot_f32, lib.rs:1394-1423) gives element i to
+// accumulator i % 32 (chained FMA over i, i+32, ...) and reduces the 32
+// accumulators with a fixed tree.  Eight lanes share one token: lane s holds
+// accumulators 4s..4s+3 (a float4 at 32c + 4s for c = 0..7), XOR 4/2/1
+// shuffles form the tree's first three levels, the last two are local.
+//
+// Grid (ceil(Tmax/32), kv_heads, B), 4 waves x 8 tokens; the G query heads
+// of one kv head share each key load.  q is [B][nq][256] (roped).
+template <typename KV, int G>
 __global__ __launch_bounds__(256) void attn_qk_kernel(const float* __restrict__ q, size_t q_stride,
                                                       const KV* __restrict__ kcache, size_t cache_row_stride,
-                                                      const int* __restrict__ ntok, int nq, int nkv, float scale,
+                                                      const int* __restrict__ ntok, int nkv, float scale,
                                                       float* __restrict__ dots, float* __restrict__ scores,
                                                       size_t score_stride) {
-    constexpr int D = 256, NQ = 8;
-    const int b = blockIdx.y;
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4, sub = lane & 15;
-    const int t = blockIdx.x * 16 + (threadIdx.x >> 6) * 4 + g;
+    constexpr int D = 256;
+    const int b = blockIdx.z, kvh = blockIdx.y;
+    const int s = threadIdx.x & 7;
+    const int t = blockIdx.x * 32 + (threadIdx.x >> 3);
     const int T = ntok[b];
-    float qv[NQ][16];
+    if (blockIdx.x * 32 >= T) return;  // uniform over the workgroup
+    float acc[G][4];
 #pragma unroll
-    for (int h = 0; h < NQ; ++h)
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) qv[h][e] = h < nq ? q[(size_t)b * q_stride + (size_t)h * D + sub * 16 + e] : 0.0f;
-    const int group = nq / nkv;
-    float acc[NQ];
-#pragma unroll
-    for (int h = 0; h < NQ; ++h) acc[h] = 0.0f;
+        for (int e = 0; e < 4; ++e) acc[g][e] = 0.0f;
     if (t < T) {
-        const KV* krow = kcache + (size_t)b * cache_row_stride + (size_t)t * nkv * D;
+        const float* qb = q + (size_t)b * q_stride + (size_t)kvh * G * D + 4 * s;
+        const KV* krow = kcache + (size_t)b * cache_row_stride + ((size_t)t * nkv + kvh) * D + 4 * s;
 #pragma unroll
-        for (int h = 0; h < NQ; ++h) {
-            if (h < nq) {
-                const KV* kk = krow + (size_t)(h / group) * D + sub * 16;
+        for (int c = 0; c < D / 32; ++c) {
+            float kk[4];
+            kv_load4<KV>(krow + 32 * c, kk);
 #pragma unroll
-                for (int e = 0; e < 16; ++e) acc[h] = fmaf(qv[h][e], kv_load<KV>(kk + e), acc[h]);
+            for (int g = 0; g < G; ++g) {
+                const v4f qq = *(const v4f*)(qb + (size_t)g * D + 32 * c);
+                acc[g][0] = fmaf(qq.x, kk[0], acc[g][0]);
+                acc[g][1] = fmaf(qq.y, kk[1], acc[g][1]);
+                acc[g][2] = fmaf(qq.z, kk[2], acc[g][2]);
+                acc[g][3] = fmaf(qq.w, kk[3], acc[g][3]);
             }
         }
     }
 #pragma unroll
-    for (int h = 0; h < NQ; ++h) acc[h] = wave_sum_xor(acc[h], 16);
-    if (t < T && sub == 0) {
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int h = 0; h < NQ; ++h) {
-            if (h < nq) {
-                if (dots) dots[(size_t)b * score_stride + (size_t)h * T + t] = acc[h];
-                scores[(size_t)b * score_stride + (size_t)h * T + t] = acc[h] * scale;
-            }
+        for (int e = 0; e < 4; ++e) {
+            float v = acc[g][e];
+            v = v + __shfl_xor(v, 4, 64);
+            v = v + __shfl_xor(v, 2, 64);
+            v = v + __shfl_xor(v, 1, 64);
+            acc[g][e] = v;
+        }
+    if (t < T && s == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float dot = (acc[g][0] + acc[g][1]) + (acc[g][2] + acc[g][3]);
+            const size_t at = (size_t)b * score_stride + (size_t)(kvh * G + g) * T + t;
+            if (dots) dots[at] = dot;
+            scores[at] = dot * scale;
         }
     }
 }
 
 // --------------------------------------------------------------- softmax
 
-// One workgroup per (head, row): max, e = ggml_exp(x - max), f64 sum,
-// inv = (float)(1/sum), p = e * inv.
+// One workgroup per (head, row), lib.rs:1352-1387: max, e = ggml_exp(x -
+// max) in blocks of 8 (zero past the end), block partial
+// ((e0+e4)+(e2+e6))+((e1+e5)+(e3+e7)) in f32, partials summed in f64,
+// inv = (float)(1/sum), p = e * inv.  Thread i owns blocks i, i+256, ...
 __global__ __launch_bounds__(256) void attn_softmax_kernel(const float* __restrict__ scores, size_t score_stride,
                                                            const int* __restrict__ ntok, float* __restrict__ exps,
                                                            float* __restrict__ probs, double* __restrict__ sums) {
@@ -180,11 +214,24 @@ __global__ __launch_bounds__(256) void attn_softmax_kernel(const float* __restri
     m = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
     double s = 0.0;
     float* prow = probs + (size_t)b * score_stride + (size_t)h * T;
-    for (int i = tid; i < T; i += 256) {
-        const float e = ggml_exp(row[i] - m);
-        prow[i] = e;
-        if (exps) exps[(size_t)b * score_stride + (size_t)h * T + i] = e;
-        s += (double)e;
+    float* erow = exps ? exps + (size_t)b * score_stride + (size_t)h * T : nullptr;
+    for (int blk = tid; blk * 8 < T; blk += 256) {
+        float e[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int at = blk * 8 + i;
+            e[i] = at < T ? ggml_exp(row[at] - m) : 0.0f;
+        }
+        const float partial = ((e[0] + e[4]) + (e[2] + e[6])) + ((e[1] + e[5]) + (e[3] + e[7]));
+        s += (double)partial;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int at = blk * 8 + i;
+            if (at < T) {
+                prow[at] = e[i];
+                if (erow) erow[at] = e[i];
+            }
+        }
     }
     s = wave_sum_xor<double>(s, 64);
     if ((tid & 63) == 0) ssum[tid >> 6] = s;
@@ -192,75 +239,65 @@ __global__ __launch_bounds__(256) void attn_softmax_kernel(const float* __restri
     const double total = (ssum[0] + ssum[1]) + (ssum[2] + ssum[3]);
     const float inv = (float)(1.0 / total);
     if (sums && tid == 0) sums[(size_t)b * gridDim.x + h] = total;
-    for (int i = tid; i < T; i += 256) prow[i] = prow[i] * inv;
+    for (int blk = tid; blk * 8 < T; blk += 256) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int at = blk * 8 + i;
+            if (at < T) prow[at] = prow[at] * inv;
+        }
+    }
 }
 
 // -------------------------------------------------------------------- PV
 
-// Grid (splits, kv_heads, B).  Each workgroup covers a contiguous token
-// range for the `group` query heads of one kv head; lanes own 4 of the 256
-// value dims, waves interleave tokens.  Partial sums go to
-// part[b][split][h][d]; attn_combine adds the splits in order.
-template <typename KV>
+// lib.rs:1276-1305: out[h][j] = tree over 32 accumulators, accumulator a
+// chaining fmaf(v[t][j], p[h][t], acc) over tokens t = a, a+32, ... (the
+// reference's zero padding adds +0*+0 terms, which change nothing).
+//
+// Grid (256/8, kv_heads, B), 4 waves: wave w holds accumulators 8w..8w+7 of
+// 8 value channels (lane = channel*8 + a%8) for the G query heads of one kv
+// head, so each value load feeds G chains.  The tree runs from LDS, then
+// the sigmoid output gate (forward.rs:751) is applied when given.
+template <typename KV, int G>
 __global__ __launch_bounds__(256) void attn_pv_kernel(const float* __restrict__ probs, size_t score_stride,
                                                       const KV* __restrict__ vcache, size_t cache_row_stride,
-                                                      const int* __restrict__ ntok, int nq, int nkv, int splits,
-                                                      float* __restrict__ part) {
-    constexpr int D = 256, G = 4;
-    __shared__ float red[4][G][D];
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int T = ntok[b];
-    const int per = (T + splits - 1) / splits;
-    const int t0 = split * per, t1 = min(T, t0 + per);
-    const int group = nq / nkv;
-    float acc[G][4];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[g][e] = 0.0f;
-    const float* pb = probs + (size_t)b * score_stride;
-    for (int t = t0 + wave; t < t1; t += 4) {
-        const KV* v = vcache + (size_t)b * cache_row_stride + (size_t)t * nkv * D + (size_t)kvh * D + lane * 4;
-        float vv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) vv[e] = kv_load<KV>(v + e);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            if (g < group) {
-                const float p = pb[(size_t)(kvh * group + g) * T + t];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(vv[e], p, acc[g][e]);
-            }
-        }
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) red[wave][g][lane * 4 + e] = acc[g][e];
-    __syncthreads();
-    for (int i = threadIdx.x; i < group * D; i += 256) {
-        const int g = i / D, dd = i % D;
-        const float sum = (red[0][g][dd] + red[1][g][dd]) + (red[2][g][dd] + red[3][g][dd]);
-        part[(((size_t)b * splits + split) * nq + kvh * group + g) * D + dd] = sum;
-    }
-}
-
-// out[b][h][d] = sum over splits (in order), times sigmoid(gate) when gate.
-__global__ void attn_combine_kernel(const float* __restrict__ part, int splits, int nq,
-                                    const float* __restrict__ gate, size_t gate_stride, float* __restrict__ out,
-                                    size_t out_stride, int B) {
+                                                      const int* __restrict__ ntok, int nkv,
+                                                      const float* __restrict__ gate, size_t gate_stride,
+                                                      float* __restrict__ out, size_t out_stride) {
     constexpr int D = 256;
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)B * nq * D) return;
-    const size_t b = i / (nq * D), hd = i % (nq * D);
-    float s = 0.0f;
-    for (int k = 0; k < splits; ++k) s += part[((size_t)b * splits + k) * nq * D + hd];
-    if (gate) {
-        const size_t h = hd / D, dd = hd % D;
-        s = s * source_sigmoid(gate[b * gate_stride + h * 2 * D + D + dd]);
+    __shared__ float red[G][8][33];
+    const int kvh = blockIdx.y, b = blockIdx.z;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int ch = lane >> 3, a = w * 8 + (lane & 7);
+    const int j = blockIdx.x * 8 + ch;
+    const int T = ntok[b];
+    float acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+    const float* pb = probs + (size_t)b * score_stride + (size_t)kvh * G * T;
+    const KV* vb = vcache + (size_t)b * cache_row_stride + (size_t)kvh * D + j;
+    const size_t vstep = (size_t)nkv * D;
+    for (int t = a; t < T; t += 32) {
+        const float v = kv_load<KV>(vb + (size_t)t * vstep);
+#pragma unroll
+        for (int g = 0; g < G; ++g) acc[g] = fmaf(v, pb[(size_t)g * T + t], acc[g]);
     }
-    out[b * out_stride + hd] = s;
+#pragma unroll
+    for (int g = 0; g < G; ++g) red[g][ch][a] = acc[g];
+    __syncthreads();
+    if (threadIdx.x < G * 8) {
+        const int g = threadIdx.x >> 3, c = threadIdx.x & 7;
+        const float* r = red[g][c];
+        float comb[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) comb[l] = (r[l] + r[16 + l]) + (r[8 + l] + r[24 + l]);
+        const float h0 = comb[0] + comb[4], h1 = comb[1] + comb[5], h2 = comb[2] + comb[6], h3 = comb[3] + comb[7];
+        float v = (h0 + h1) + (h2 + h3);
+        const int jj = blockIdx.x * 8 + c;
+        const int h = kvh * G + g;
+        if (gate) v = v * source_sigmoid(gate[(size_t)b * gate_stride + (size_t)h * 2 * D + D + jj]);
+        out[(size_t)b * out_stride + (size_t)h * D + jj] = v;
+    }
 }
 
 // ------------------------------------------------------------------ host
@@ -274,23 +311,31 @@ static hipError_t launch_prep(const AttnArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <typename KV>
-static hipError_t launch_parts(const AttnArgs& a, bool qk, bool softmax, bool pv, hipStream_t s) {
-    const int D = a.d;
-    if (D != 256 || a.nq > 8 || a.nq % a.nkv || a.nq / a.nkv > 4) return hipErrorInvalidValue;
+template <typename KV, int G>
+static void launch_group(const AttnArgs& a, bool qk, bool softmax, bool pv, hipStream_t s) {
+    constexpr int D = 256;
     if (qk)
-        hipLaunchKernelGGL(attn_qk_kernel<KV>, dim3((a.tmax + 15) / 16, a.B), dim3(256), 0, s, a.qr, a.qr_stride,
-                           (const KV*)a.kcache, a.cache_row_stride, a.ntok, a.nq, a.nkv, a.scale, a.dots, a.scores,
-                           a.score_stride);
+        hipLaunchKernelGGL((attn_qk_kernel<KV, G>), dim3((a.tmax + 31) / 32, a.nkv, a.B), dim3(256), 0, s, a.qr,
+                           a.qr_stride, (const KV*)a.kcache, a.cache_row_stride, a.ntok, a.nkv, a.scale, a.dots,
+                           a.scores, a.score_stride);
     if (softmax)
         hipLaunchKernelGGL(attn_softmax_kernel, dim3(a.nq, a.B), dim3(256), 0, s, a.scores, a.score_stride, a.ntok,
                            a.exps, a.probs, a.sums);
-    if (pv) {
-        hipLaunchKernelGGL(attn_pv_kernel<KV>, dim3(a.splits, a.nkv, a.B), dim3(256), 0, s, a.probs, a.score_stride,
-                           (const KV*)a.vcache, a.cache_row_stride, a.ntok, a.nq, a.nkv, a.splits, a.part);
-        const size_t n = (size_t)a.B * a.nq * D;
-        hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.part, a.splits,
-                           a.nq, a.gate, a.gate_stride, a.out, a.out_stride, a.B);
+    if (pv)
+        hipLaunchKernelGGL((attn_pv_kernel<KV, G>), dim3(D / 8, a.nkv, a.B), dim3(256), 0, s, a.probs,
+                           a.score_stride, (const KV*)a.vcache, a.cache_row_stride, a.ntok, a.nkv, a.gate,
+                           a.gate_stride, a.out, a.out_stride);
+}
+
+template <typename KV>
+static hipError_t launch_parts(const AttnArgs& a, bool qk, bool softmax, bool pv, hipStream_t s) {
+    if (a.d != 256 || a.nkv <= 0 || a.nq % a.nkv || a.tmax <= 0) return hipErrorInvalidValue;
+    switch (a.nq / a.nkv) {
+        case 1: launch_group<KV, 1>(a, qk, softmax, pv, s); break;
+        case 2: launch_group<KV, 2>(a, qk, softmax, pv, s); break;
+        case 3: launch_group<KV, 3>(a, qk, softmax, pv, s); break;
+        case 4: launch_group<KV, 4>(a, qk, softmax, pv, s); break;
+        default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }

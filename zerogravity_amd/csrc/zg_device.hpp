@@ -69,4 +69,12 @@ __device__ __forceinline__ v4i load_nt(const void* p) {
     return __builtin_nontemporal_load((const v4i*)p);
 }
 
+// Q8_0 device layout: tiles of 8 rows x 4 blocks, one 16-byte slot per
+// (row % 8, lane-of-block l) holding bytes 4l..4l+3 of the 4 blocks, so the
+// 64 lanes of a wavefront read one contiguous 1 KB tile.  Byte offset of
+// the 4-byte group l of block b of row `row`:
+__device__ __forceinline__ size_t q8_tile_offset(size_t row, size_t b, int l, size_t nbc) {
+    return (((row >> 3) * nbc + (b >> 2)) * 64 + (row & 7) * 8 + l) * 16 + (b & 3) * 4;
+}
+
 }  // namespace zg

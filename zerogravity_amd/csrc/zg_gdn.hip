@@ -62,7 +62,7 @@ __device__ __forceinline__ void gdn_coef(float alpha, float beta_p, float dt, fl
     const float biased = alpha + dt;
     sp = source_softplus(biased);
     gate_raw = sp * a;
-    gain = expf(gate_raw);
+    gain = cr_expf(gate_raw);
     beta = source_sigmoid(beta_p);
 }
 
@@ -89,14 +89,40 @@ hipError_t gdn_coefficients(const float* alpha, const float* beta, const float* 
 
 // ------------------------------------------------------------- recurrence
 
+// Eight lanes own one value column j.  The reference dot (source_dot_f32,
+// model-qwen35/src/lib.rs:1394-1423) keeps 32 f32 accumulators, accumulator
+// a = 8i + l taking elements a, a+32, a+64, a+96 in that order, then reduces
+// combined[l] = (s[0][l]+s[2][l]) + (s[1][l]+s[3][l]),
+// halves[m] = combined[m] + combined[m+4], (h0+h1)+(h2+h3).
+// Lane s of the column holds accumulators 4s..4s+3, i.e. elements
+// 32c + 4s + t (c, t in 0..3): one float4 per c, coalesced across the 8
+// lanes.  XOR-4 then XOR-2 shuffles form `combined`, XOR-1 forms `halves`
+// and the last two levels are local: the dot is bit-identical to the CPU.
+__device__ __forceinline__ float column_dot(const float (&a)[4][4], const float (&b)[4][4]) {
+    float acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        float v = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v = fmaf(a[c][t], b[c][t], v);
+        acc[t] = v;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        acc[t] = acc[t] + __shfl_xor(acc[t], 4, 64);
+        acc[t] = acc[t] + __shfl_xor(acc[t], 2, 64);
+        acc[t] = acc[t] + __shfl_xor(acc[t], 1, 64);
+    }
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+}
+
 // Grid: x = heads * (d/8) / 4 workgroups of 4 waves, y = rows.  Wave w of
-// the grid owns columns j0..j0+7 of one head; lane = (j - j0) * 8 + s holds
-// keys s*16 .. s*16+15 of column j.
+// the grid owns columns j0..j0+7 of one head (lane = (j - j0) * 8 + s).
 //
 // FUSED (model path): q, k, v come from the conv+SiLU output
 // mixed[row] = [q (H*d) | k (H*d) | v (H*d)], q and k are L2-normalised here
 // (f64 sum of f32 squares over the head, f32 mean, 1/sqrtf(mean + eps/d),
-// then x*inv*(1/sqrt d)), and gain/beta come from the raw alpha/beta
+// then (x*inv)*(1/sqrt d)), and gain/beta come from the raw alpha/beta
 // projections, ssm_dt and ssm_a.
 // Not FUSED (region path): q, k, v are given, as are gain and beta per head.
 template <bool FUSED>
@@ -114,27 +140,29 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(
     const size_t row = blockIdx.y;
     if (h >= H) return;
 
-    const float* qrow = qsrc + row * src_stride + (size_t)h * D;
-    const float* krow = ksrc + row * src_stride + (size_t)h * D;
-    float q[16], k[16];
+    const float* qrow = qsrc + row * src_stride + (size_t)h * D + 4 * s;
+    const float* krow = ksrc + row * src_stride + (size_t)h * D + 4 * s;
+    float q[4][4], k[4][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const v4f qa = *(const v4f*)(qrow + s * 16 + 4 * t);
-        const v4f ka = *(const v4f*)(krow + s * 16 + 4 * t);
-        q[4 * t] = qa.x; q[4 * t + 1] = qa.y; q[4 * t + 2] = qa.z; q[4 * t + 3] = qa.w;
-        k[4 * t] = ka.x; k[4 * t + 1] = ka.y; k[4 * t + 2] = ka.z; k[4 * t + 3] = ka.w;
+    for (int c = 0; c < 4; ++c) {
+        const v4f qa = *(const v4f*)(qrow + 32 * c);
+        const v4f ka = *(const v4f*)(krow + 32 * c);
+        q[c][0] = qa.x; q[c][1] = qa.y; q[c][2] = qa.z; q[c][3] = qa.w;
+        k[c][0] = ka.x; k[c][1] = ka.y; k[c][2] = ka.z; k[c][3] = ka.w;
     }
     float gain, beta;
     if (FUSED) {
         // two-stage L2 (forward.rs:564-576): the 8 lanes of a column cover the head
         double sq = 0.0, sk = 0.0;
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            const float a2 = q[t] * q[t];
-            const float b2 = k[t] * k[t];
-            sq += (double)a2;
-            sk += (double)b2;
-        }
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float a2 = q[c][t] * q[c][t];
+                const float b2 = k[c][t] * k[c][t];
+                sq += (double)a2;
+                sk += (double)b2;
+            }
         sq = wave_sum_xor<double>(sq, 8);
         sk = wave_sum_xor<double>(sk, 8);
         const float dsq = 1.0f / sqrtf((float)D);
@@ -142,12 +170,14 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(
         const float iq = 1.0f / sqrtf((float)(sq / (double)D) + eps_d);
         const float ik = 1.0f / sqrtf((float)(sk / (double)D) + eps_d);
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            const float tq = q[t] * iq;
-            q[t] = tq * dsq;
-            const float tk = k[t] * ik;
-            k[t] = tk * dsq;
-        }
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float tq = q[c][t] * iq;
+                q[c][t] = tq * dsq;
+                const float tk = k[c][t] * ik;
+                k[c][t] = tk * dsq;
+            }
         float sp, gr;
         gdn_coef(alpha[row * coef_stride + h], beta_p[row * coef_stride + h], dt[h], a[h], gain, beta, sp, gr);
     } else {
@@ -156,30 +186,22 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(
         if (scale_h) scale = scale_h[row * coef_stride + h];
     }
     const float vj = vsrc[row * src_stride + (size_t)h * D + j];
-    float* col = state + ((row * H + h) * D + j) * D + s * 16;
-    float c[16];
+    float* col = state + ((row * H + h) * D + j) * D + 4 * s;
+    float cv[4][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const v4f v = *(const v4f*)(col + 4 * t);
-        c[4 * t] = v.x; c[4 * t + 1] = v.y; c[4 * t + 2] = v.z; c[4 * t + 3] = v.w;
+    for (int c = 0; c < 4; ++c) {
+        const v4f v = *(const v4f*)(col + 32 * c);
+        cv[c][0] = v.x * gain; cv[c][1] = v.y * gain; cv[c][2] = v.z * gain; cv[c][3] = v.w * gain;
     }
-    float prev = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        c[t] = c[t] * gain;
-        prev = fmaf(c[t], k[t], prev);
-    }
-    prev = wave_sum_xor(prev, 8);
+    const float prev = column_dot(cv, k);
     const float delta = (vj - prev) * beta;
-    float o = 0.0f;
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        c[t] = fmaf(k[t], delta, c[t]);
-        o = fmaf(c[t], q[t], o);
-    }
-    o = wave_sum_xor(o, 8);
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) *(v4f*)(col + 4 * t) = v4f{c[4 * t], c[4 * t + 1], c[4 * t + 2], c[4 * t + 3]};
+        for (int t = 0; t < 4; ++t) cv[c][t] = fmaf(k[c][t], delta, cv[c][t]);
+    const float o = column_dot(cv, q);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) *(v4f*)(col + 32 * c) = v4f{cv[c][0], cv[c][1], cv[c][2], cv[c][3]};
     if (s == 0) out[row * out_stride + (size_t)h * D + j] = o * scale;
 }
 

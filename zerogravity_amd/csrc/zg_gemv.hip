@@ -13,6 +13,8 @@
 // the activation lives in registers for the whole launch and is reused by
 // every row it visits; the only per-row reduction is a log2(lpr)-step XOR
 // shuffle tree.
+#include <algorithm>
+
 #include "zg_device.hpp"
 #include "zg_internal.hpp"
 
@@ -30,18 +32,24 @@ size_t gguf_row_bytes(int type, size_t K) {
 // ------------------------------------------------------------------ repack
 
 __global__ void repack_q8_0_kernel(const uint8_t* __restrict__ src, int8_t* __restrict__ qs,
-                                   uint16_t* __restrict__ hdr, size_t nblocks, int* bad) {
-    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nblocks) return;
-    const uint8_t* blk = src + b * 34;
+                                   uint16_t* __restrict__ hdr, size_t N, size_t nb, int* bad) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N * nb) return;
+    const size_t row = i / nb, b = i % nb;
+    const uint8_t* blk = src + i * 34;
     uint16_t d = (uint16_t)(blk[0] | (blk[1] << 8));
     if ((d & 0x7c00u) == 0x7c00u) atomicOr(bad, 1);
-    hdr[b] = d;
-    int8_t* out = qs + b * 32;
+    const size_t nbc = (nb + 3) / 4;
+    hdr[row * nbc * 4 + b] = d;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) out[i] = (int8_t)blk[2 + i];
+    for (int l = 0; l < 8; ++l) {
+        uint32_t word = (uint32_t)blk[2 + 4 * l] | ((uint32_t)blk[3 + 4 * l] << 8) | ((uint32_t)blk[4 + 4 * l] << 16) |
+                        ((uint32_t)blk[5 + 4 * l] << 24);
+        *(uint32_t*)(qs + q8_tile_offset(row, b, l, nbc)) = word;
+    }
 }
 
+// GGUF Q4_K 6-bit scale/min unpack (artifacts/src/codecs/q4.rs:58-65).
 __device__ __forceinline__ void q4k_scale_min(const uint8_t* s, int g, uint32_t& sc, uint32_t& mn) {
     if (g < 4) {
         sc = s[g] & 63;
@@ -103,10 +111,12 @@ __global__ void repack_q4k_kernel(const v4i* __restrict__ src, v4i* __restrict__
 
 hipError_t repack_weight(const uint8_t* d_gguf, DeviceWeight& w, int* d_bad, hipStream_t s) {
     if (w.type == kQ8_0) {
-        size_t nb = w.N * (w.K / 32);
-        unsigned grid = (unsigned)((nb + 255) / 256);
-        hipLaunchKernelGGL(repack_q8_0_kernel, dim3(grid), dim3(256), 0, s, d_gguf, (int8_t*)w.qs,
-                           (uint16_t*)w.hdr, nb, d_bad);
+        const size_t nb = w.K / 32, n = w.N * nb;
+        hipError_t e = hipMemsetAsync(w.qs, 0, w.qs_bytes, s);
+        if (e == hipSuccess) e = hipMemsetAsync(w.hdr, 0, w.hdr_bytes, s);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(repack_q8_0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, d_gguf,
+                           (int8_t*)w.qs, (uint16_t*)w.hdr, w.N, nb, d_bad);
     } else if (w.type == kQ4_K) {
         size_t nb = w.N * (w.K / 256);
         unsigned grid = (unsigned)((nb + 255) / 256);
@@ -123,12 +133,14 @@ hipError_t repack_weight(const uint8_t* d_gguf, DeviceWeight& w, int* d_bad, hip
 // ------------------------------------------------------------- dequantize
 
 __global__ void dequant_q8_0_kernel(const int8_t* __restrict__ qs, const uint16_t* __restrict__ hdr,
-                                    float* __restrict__ out, size_t nblocks) {
-    size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nblocks) return;
-    float scale = f16_to_f32(hdr[b]);
+                                    float* __restrict__ out, size_t row0, size_t rows, size_t nb) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * nb) return;
+    const size_t row = row0 + i / nb, b = i % nb, nbc = (nb + 3) / 4;
+    const float scale = f16_to_f32(hdr[row * nbc * 4 + b]);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) out[b * 32 + i] = (float)qs[b * 32 + i] * scale;
+    for (int e = 0; e < 32; ++e)
+        out[i * 32 + e] = (float)qs[q8_tile_offset(row, b, e >> 2, nbc) + (e & 3)] * scale;
 }
 
 __global__ void dequant_q4k_kernel(const uint8_t* __restrict__ qs, const v4u* __restrict__ hdr,
@@ -155,9 +167,9 @@ __global__ void dequant_q4k_kernel(const uint8_t* __restrict__ qs, const v4u* __
 hipError_t dequantize_rows(const DeviceWeight& w, size_t row0, size_t rows, float* out, hipStream_t s) {
     if (row0 + rows > w.N) return hipErrorInvalidValue;
     if (w.type == kQ8_0) {
-        const size_t bpr = w.K / 32, nb = rows * bpr;
-        hipLaunchKernelGGL(dequant_q8_0_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, s,
-                           (const int8_t*)w.qs + row0 * w.K, (const uint16_t*)w.hdr + row0 * bpr, out, nb);
+        const size_t nb = w.K / 32, n = rows * nb;
+        hipLaunchKernelGGL(dequant_q8_0_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                           (const int8_t*)w.qs, (const uint16_t*)w.hdr, out, row0, rows, nb);
     } else if (w.type == kQ4_K) {
         const size_t bpr = w.K / 256, nb = rows * bpr;
         hipLaunchKernelGGL(dequant_q4k_kernel, dim3((unsigned)((nb + 63) / 64)), dim3(64), 0, s,
@@ -294,75 +306,72 @@ hipError_t act_prepare_for(int type, const void* x, int x_bf16, size_t M, size_t
 
 // ----------------------------------------------------------------- GEMV Q8_0
 
-// MT activation rows per pass (grid.y covers ceil(M/MT) passes), CH 16-byte
-// chunks per lane.  Integer block dots via v_dot4_i32_i8; each half block's
-// int32 sum is scaled once by f16(w.d) * act.d in f32.
-template <int CH, int MT>
-__global__ __launch_bounds__(256) void gemv_q8_0_kernel(const int8_t* __restrict__ qs,
-                                                        const uint16_t* __restrict__ hdr,
-                                                        const int8_t* __restrict__ aq,
-                                                        const float* __restrict__ ad, float* __restrict__ y,
-                                                        int N, int K, int M, int lpr_log2) {
-    const int lane = threadIdx.x & 63;
-    const int lpr = 1 << lpr_log2;
-    const int sub = lane & (lpr - 1);
-    const int rsub = lane >> lpr_log2;
-    const int rpw = 64 >> lpr_log2;
-    const int nchunk = K >> 4;
-    const int nb = K >> 5;
-    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int nwaves = gridDim.x * (blockDim.x >> 6);
+// Reference order (cpu/src/source/quantization.rs:171-196): for every row,
+// eight f32 accumulators; accumulator l takes, block after block, the int32
+// dot of elements 4l..4l+3 with the activation codes, fused-multiply-added
+// with scale = f16(w.d) * act.d; the row value is
+// ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7)).  Here lane (row%8)*8 + l of a
+// wavefront IS accumulator l of row (8 rows per wave), it walks the blocks
+// in order, and the final tree is the XOR-4/2/1 shuffle tree (IEEE addition
+// commutes, so each step reproduces the reference sum exactly): the result
+// is bit-identical to the CPU.  The tile layout gives the wavefront one
+// contiguous 1 KB load per 4 blocks; the MT activation rows (codes and
+// scales) sit in LDS and every weight word is reused MT times.
+template <int MT>
+__global__ __launch_bounds__(256) void gemv_q8_0_kernel(const v4i* __restrict__ qs, const uint16_t* __restrict__ hdr,
+                                                        const int8_t* __restrict__ aq, const float* __restrict__ ad,
+                                                        float* __restrict__ y, int N, int K, int M) {
+    extern __shared__ int lds_q8[];
+    const int nb = K >> 5, nbc = (nb + 3) >> 2;
+    int* codes = lds_q8;                          // [MT][K/4] words
+    float* scales = (float*)(lds_q8 + MT * (K >> 2));  // [MT][nb]
     const int m0 = blockIdx.y * MT;
-
-    v4i a[MT][CH];
-    float as[MT][CH];
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-        const int c = sub + i * lpr;
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            if (c < nchunk && m0 + m < M) {
-                a[m][i] = *(const v4i*)(aq + (size_t)(m0 + m) * K + (size_t)c * 16);
-                as[m][i] = ad[(size_t)(m0 + m) * nb + (c >> 1)];
-            } else {
-                a[m][i] = v4i{0, 0, 0, 0};
-                as[m][i] = 0.0f;
-            }
-        }
+    for (int i = threadIdx.x; i < MT * (K >> 2); i += blockDim.x) {
+        const int m = i / (K >> 2), w = i % (K >> 2);
+        codes[i] = m0 + m < M ? ((const int*)aq)[(size_t)(m0 + m) * (K >> 2) + w] : 0;
     }
-    for (int rg = wave; rg * rpw < N; rg += nwaves) {
-        const int row = rg * rpw + rsub;
-        const bool rv = row < N;
-        v4i w[CH];
-        float sc[CH];
-#pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const int c = sub + i * lpr;
-            if (rv && c < nchunk) {
-                w[i] = load_nt(qs + (size_t)row * K + (size_t)c * 16);
-                sc[i] = f16_to_f32(hdr[(size_t)row * nb + (c >> 1)]);
-            } else {
-                w[i] = v4i{0, 0, 0, 0};
-                sc[i] = 0.0f;
-            }
-        }
+    for (int i = threadIdx.x; i < MT * nb; i += blockDim.x) {
+        const int m = i / nb, b = i % nb;
+        scales[i] = m0 + m < M ? ad[(size_t)(m0 + m) * nb + b] : 0.0f;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int rl = lane >> 3, l = lane & 7;
+    const int groups = (N + 7) >> 3;
+    const int nwaves = gridDim.x * (blockDim.x >> 6);
+    for (int R = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); R < groups; R += nwaves) {
+        const int row = R * 8 + rl;
+        const uint16_t* hrow = hdr + (size_t)(row < N ? row : N - 1) * nbc * 4;
+        const v4i* tile = qs + (size_t)R * nbc * 64 + lane;
         float acc[MT];
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+        for (int c = 0; c < nbc; ++c) {
+            const v4i w4 = load_nt(tile + (size_t)c * 64);
+            const uint2 h2 = *(const uint2*)(hrow + 4 * c);
+            const int ww[4] = {w4.x, w4.y, w4.z, w4.w};
+            const uint32_t hw[4] = {h2.x & 0xffffu, h2.x >> 16, h2.y & 0xffffu, h2.y >> 16};
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
+            for (int bi = 0; bi < 4; ++bi) {
+                const int b = 4 * c + bi;
+                if (b < nb) {
+                    const float wd = f16_to_f32((uint16_t)hw[bi]);
 #pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                int d = __builtin_amdgcn_sdot4(w[i].x, a[m][i].x, 0, false);
-                d = __builtin_amdgcn_sdot4(w[i].y, a[m][i].y, d, false);
-                d = __builtin_amdgcn_sdot4(w[i].z, a[m][i].z, d, false);
-                d = __builtin_amdgcn_sdot4(w[i].w, a[m][i].w, d, false);
-                acc[m] = fmaf((float)d, sc[i] * as[m][i], acc[m]);
+                    for (int m = 0; m < MT; ++m) {
+                        const int pair = __builtin_amdgcn_sdot4(ww[bi], codes[m * (K >> 2) + b * 8 + l], 0, false);
+                        const float scale = wd * scales[m * nb + b];
+                        acc[m] = fmaf((float)pair, scale, acc[m]);
+                    }
+                }
             }
         }
 #pragma unroll
-        for (int m = 0; m < MT; ++m) acc[m] = wave_sum_xor(acc[m], lpr);
-        if (rv && sub == 0) {
+        for (int m = 0; m < MT; ++m) {
+            acc[m] = acc[m] + __shfl_xor(acc[m], 4, 64);
+            acc[m] = acc[m] + __shfl_xor(acc[m], 2, 64);
+            acc[m] = acc[m] + __shfl_xor(acc[m], 1, 64);
+        }
+        if (l == 0 && row < N) {
 #pragma unroll
             for (int m = 0; m < MT; ++m)
                 if (m0 + m < M) y[(size_t)(m0 + m) * N + row] = acc[m];
@@ -542,19 +551,6 @@ bool gemv_supported(int type, size_t K, size_t M) {
     }
 }
 
-template <int MT>
-static void launch_q8(int ch, dim3 g, hipStream_t s, const DeviceWeight& w, const int8_t* aq, const float* ad,
-                      float* y, int M, int l) {
-    const int8_t* q = (const int8_t*)w.qs;
-    const uint16_t* h = (const uint16_t*)w.hdr;
-    const int N = (int)w.N, K = (int)w.K;
-    switch (ch) {
-#define ZG_Q8(C) case C: hipLaunchKernelGGL((gemv_q8_0_kernel<C, MT>), g, dim3(256), 0, s, q, h, aq, ad, y, N, K, M, l); break;
-        ZG_Q8(1) ZG_Q8(2) ZG_Q8(3) ZG_Q8(4) ZG_Q8(5) ZG_Q8(6) ZG_Q8(7) ZG_Q8(8)
-#undef ZG_Q8
-    }
-}
-
 hipError_t gemv(const DeviceWeight& w, size_t M, const void* prepared, float* y, hipStream_t s) {
     if (!gemv_supported(w.type, w.K, M)) return hipErrorInvalidValue;
     const int K = (int)w.K, N = (int)w.N;
@@ -566,14 +562,18 @@ hipError_t gemv(const DeviceWeight& w, size_t M, const void* prepared, float* y,
     const int16_t* x4 = (const int16_t*)base;
     const float* m4 = (const float*)(base + a(M * w.K * 2));
     if (w.type == kQ8_0) {
-        const int nchunk = K / 16;
-        const int l = pick_lpr_log2(nchunk, 4);
-        const int ch = (nchunk + (1 << l) - 1) >> l;
-        const int mt = M == 1 ? 1 : (M == 2 ? 2 : 4);
-        dim3 g(grid_for(w.N, l), (unsigned)((M + mt - 1) / mt));
-        if (mt == 1) launch_q8<1>(ch, g, s, w, aq, ad, y, (int)M, l);
-        else if (mt == 2) launch_q8<2>(ch, g, s, w, aq, ad, y, (int)M, l);
-        else launch_q8<4>(ch, g, s, w, aq, ad, y, (int)M, l);
+        int mt = M == 1 ? 1 : (M == 2 ? 2 : (M <= 4 ? 4 : 8));
+        while (mt > 1 && (size_t)mt * (K + (K / 32) * 4) > 65536) mt >>= 1;
+        const size_t lds = (size_t)mt * (K + (K / 32) * 4);
+        const size_t groups = (w.N + 7) / 8;
+        const unsigned wgs = (unsigned)std::min<size_t>((groups + 3) / 4, 256 * 8);
+        dim3 g(wgs, (unsigned)((M + mt - 1) / mt));
+        const v4i* q = (const v4i*)w.qs;
+        const uint16_t* h = (const uint16_t*)w.hdr;
+        if (mt == 1) hipLaunchKernelGGL(gemv_q8_0_kernel<1>, g, dim3(256), lds, s, q, h, aq, ad, y, N, K, (int)M);
+        else if (mt == 2) hipLaunchKernelGGL(gemv_q8_0_kernel<2>, g, dim3(256), lds, s, q, h, aq, ad, y, N, K, (int)M);
+        else if (mt == 4) hipLaunchKernelGGL(gemv_q8_0_kernel<4>, g, dim3(256), lds, s, q, h, aq, ad, y, N, K, (int)M);
+        else hipLaunchKernelGGL(gemv_q8_0_kernel<8>, g, dim3(256), lds, s, q, h, aq, ad, y, N, K, (int)M);
     } else if (w.type == kQ4_K) {
         const int nchunk = K / 64;
         int mt = M == 1 ? 1 : (M == 2 ? 2 : 4);

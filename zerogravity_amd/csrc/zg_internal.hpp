@@ -77,7 +77,7 @@ hipError_t gdn_recurrent(bool fused, const float* q, const float* k, const float
 // GQA decode attention (zg_attn.hip), d = 256, <= 8 query heads, <= 4 per kv
 // head.  Scores/probs are compact per row: [h][ntok[b]] at b*score_stride.
 struct AttnArgs {
-    int B = 0, nq = 0, nkv = 0, d = 0, rotate = 64, tmax = 0, splits = 1;
+    int B = 0, nq = 0, nkv = 0, d = 0, rotate = 64, tmax = 0;
     int kv_bf16 = 0, do_prep = 0, prep_only = 0, norm = 1;
     const float* qproj = nullptr;  // [B][nq*2d] (q | gate per head)
     size_t q_stride = 0;
@@ -95,7 +95,6 @@ struct AttnArgs {
     float *dots = nullptr, *scores = nullptr, *exps = nullptr, *probs = nullptr;
     double* sums = nullptr;
     size_t score_stride = 0;
-    float* part = nullptr;  // [B][splits][nq][d]
     const float* gate = nullptr;
     size_t gate_stride = 0;
     float* out = nullptr;

@@ -41,7 +41,9 @@ __global__ void embed_q8_0_kernel(const int8_t* __restrict__ qs, const uint16_t*
         x[(size_t)b * K + i] = 0.0f;
         return;
     }
-    x[(size_t)b * K + i] = (float)qs[(size_t)t * K + i] * f16_to_f32(hdr[(size_t)t * (K / 32) + i / 32]);
+    const size_t nbc = ((size_t)K / 32 + 3) / 4;
+    const float scale = f16_to_f32(hdr[(size_t)t * nbc * 4 + i / 32]);
+    x[(size_t)b * K + i] = (float)qs[q8_tile_offset(t, i / 32, (i % 32) >> 2, nbc) + (i & 3)] * scale;
 }
 
 __global__ void embed_q4k_kernel(const uint8_t* __restrict__ qs, const v4u* __restrict__ hdr,

@@ -31,14 +31,23 @@ __device__ __forceinline__ float ggml_exp(float x) {
 // cpu/src/ops.rs:353-355
 __device__ __forceinline__ float ggml_silu(float x) { return x / (1.0f + ggml_exp(0.0f - x)); }
 
-// model-qwen35/src/lib.rs:324-326 (device expf, within 1 ulp of libm)
-__device__ __forceinline__ float source_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+// f32 transcendentals, correctly rounded: evaluated in double and rounded
+// once.  The reference calls the platform libm (Rust f32::exp/ln/sin_cos) and
+// no reference test pins their last bit; both this device code and the CPU
+// oracle use the correctly rounded value, so they agree bit for bit.
+__device__ __forceinline__ float cr_expf(float x) { return (float)exp((double)x); }
+__device__ __forceinline__ float cr_logf(float x) { return (float)log((double)x); }
+__device__ __forceinline__ float cr_sinf(float x) { return (float)sin((double)x); }
+__device__ __forceinline__ float cr_cosf(float x) { return (float)cos((double)x); }
+
+// model-qwen35/src/lib.rs:324-326
+__device__ __forceinline__ float source_sigmoid(float x) { return 1.0f / (1.0f + cr_expf(-x)); }
 
 // lib.rs:328-336
 __device__ __forceinline__ float source_softplus(float x) {
     if (x > 20.0f) return x;
-    if (x < -20.0f) return expf(x);
-    return logf(1.0f + expf(x));
+    if (x < -20.0f) return cr_expf(x);
+    return cr_logf(1.0f + cr_expf(x));
 }
 
 }  // namespace zg

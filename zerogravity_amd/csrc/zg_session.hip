@@ -45,10 +45,9 @@ struct zg_session {
     int *d_pos = nullptr, *d_ntok = nullptr, *d_status = nullptr;
     uint32_t *d_tokens = nullptr, *d_greedy = nullptr;
     float *x = nullptr, *y0 = nullptr, *y1 = nullptr, *y2 = nullptr, *y3 = nullptr, *mixed = nullptr, *core = nullptr,
-          *gated = nullptr, *out = nullptr, *logits = nullptr, *qr = nullptr, *scores = nullptr, *probs = nullptr,
-          *part = nullptr;
+          *gated = nullptr, *out = nullptr, *logits = nullptr, *qr = nullptr, *scores = nullptr, *probs = nullptr;
     void* prep = nullptr;
-    size_t prep_bytes = 0, y0w = 0, y1w = 0, y2w = 0, gatedw = 0, max_splits = 64;
+    size_t prep_bytes = 0, y0w = 0, y1w = 0, y2w = 0, gatedw = 0;
     std::vector<float*> conv, rec;   // per GDN layer
     std::vector<void*> kc, vc;       // per attention layer
     std::vector<int> layer_slot;     // layer -> index into conv/rec or kc/vc
@@ -188,12 +187,7 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             a.score_stride = (size_t)g.q_heads * s->max_ctx;
             int maxpos = 0;
             for (size_t b = 0; b < B; ++b) maxpos = std::max(maxpos, s->pos[b] + 1);
-            size_t splits = std::max<size_t>(1, 512 / (B * g.kv_heads));
-            splits = std::min(splits, std::max<size_t>(1, (size_t)(maxpos + 15) / 16));
-            splits = std::min(splits, s->max_splits);
-            a.splits = (int)splits;
             a.tmax = maxpos;
-            a.part = s->part;
             a.gate = s->y0;
             a.gate_stride = 2 * (size_t)g.q_heads * g.head_dim;
             a.out = s->gated;
@@ -378,7 +372,6 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     A((void**)&s->qr, B * QD * 4);
     A((void**)&s->scores, B * g.q_heads * max_context * 4);
     A((void**)&s->probs, B * g.q_heads * max_context * 4);
-    A((void**)&s->part, B * s->max_splits * QD * 4);
     A(&s->prep, prep);
     s->layer_slot.resize(g.layers);
     for (size_t i = 0; i < m->layers.size() && !rc; ++i) {
@@ -793,8 +786,8 @@ static int attention_region(zg_ctx* ctx, const float* query, const float* keys, 
                             float* scores, float* probs, float* out) {
     const size_t nq = query_heads * head_width, kw = kv_heads * head_width, ns = query_heads * tokens;
     const size_t oq = 0, ok = align256(nq * 4), ov = ok + align256(tokens * kw * 4), on = ov + align256(values ? tokens * kw * 4 : 4),
-                 od = on + 256, osc = od + align256(ns * 4), opr = osc + align256(ns * 4), opa = opr + align256(ns * 4),
-                 oo = opa + align256(64 * nq * 4);
+                 od = on + 256, osc = od + align256(ns * 4), opr = osc + align256(ns * 4),
+                 oo = opr + align256(ns * 4);
     int rc = ensure(ctx, ctx->scratch, oo + align256(nq * 4));
     if (rc) return rc;
     char* b = (char*)ctx->scratch.ptr;
@@ -823,8 +816,6 @@ static int attention_region(zg_ctx* ctx, const float* query, const float* keys, 
     a.scores = (float*)(b + osc);
     a.probs = (float*)(b + opr);
     a.score_stride = ns;
-    a.part = (float*)(b + opa);
-    a.splits = (int)std::min<size_t>(64, std::max<size_t>(1, tokens / 16));
     a.out = out ? (float*)(b + oo) : nullptr;
     a.out_stride = nq;
     ZG_HIP(zg::attention_parts(a, keys != nullptr, keys != nullptr, out != nullptr, st));
@@ -845,8 +836,8 @@ int zg_attention_qk(zg_ctx* ctx, const float* query, const float* keys, size_t t
         query_heads % kv_heads || tokens == 0 || !std::isfinite(scale) || scale <= 0.0f ||
         !all_finite(query, query_heads * head_width) || !all_finite(keys, tokens * kv_heads * head_width))
         return fail(ctx, ZG_E_MALFORMED, "invalid source attention QK region");
-    if (head_width != 256 || query_heads > 8 || query_heads / kv_heads > 4)
-        return fail(ctx, ZG_UNSUPPORTED, "attention offered for head width 256, <= 8 query heads");
+    if (head_width != 256 || query_heads / kv_heads > 4)
+        return fail(ctx, ZG_UNSUPPORTED, "attention offered for head width 256, GQA group <= 4");
     const size_t ns = query_heads * tokens;
     std::vector<float> probs(ns);
     int rc = attention_region(ctx, query, keys, nullptr, tokens, head_width, query_heads, kv_heads, scale, dots, scores,
@@ -893,8 +884,8 @@ int zg_attention_value(zg_ctx* ctx, const float* probabilities, const float* val
     for (size_t i = 0; i < query_heads * tokens; ++i)
         if (!std::isfinite(probabilities[i]) || std::signbit(probabilities[i]) || probabilities[i] > 1.0f)
             return fail(ctx, ZG_E_MALFORMED, "invalid source attention value region");
-    if (head_width != 256 || query_heads > 8 || query_heads / kv_heads > 4)
-        return fail(ctx, ZG_UNSUPPORTED, "attention offered for head width 256, <= 8 query heads");
+    if (head_width != 256 || query_heads / kv_heads > 4)
+        return fail(ctx, ZG_UNSUPPORTED, "attention offered for head width 256, GQA group <= 4");
     std::vector<float> dummy(query_heads * head_width);
     int rc = attention_region(ctx, dummy.data(), nullptr, values, tokens, head_width, query_heads, kv_heads, 1.0f,
                               nullptr, nullptr, const_cast<float*>(probabilities), out);

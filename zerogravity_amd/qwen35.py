@@ -184,14 +184,15 @@ class QwenModelHip:
         self.ctx.check(L.lib().zg_model_load(self.ctx.h, self.source_id, C.byref(geo), descs, len(tensors),
                                              C.byref(h)))
         self.h = h
+        self.ctx.adopt(self)
 
     def session(self, max_batch=1, max_context=4096, kv_dtype=L.BF16):
         return QwenDenseHip(self, max_batch, max_context, kv_dtype)
 
     def close(self):
-        if getattr(self, "h", None):
+        if getattr(self, "h", None) and getattr(self.ctx, "h", None):
             L.lib().zg_model_destroy(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):
         self.close()
@@ -207,6 +208,7 @@ class QwenDenseHip:
         h = C.c_void_p()
         model.ctx.check(L.lib().zg_session_create(model.h, max_batch, max_context, kv_dtype, C.byref(h)))
         self.h = h
+        model.ctx.adopt(self)
 
     @property
     def position(self):
@@ -259,9 +261,9 @@ class QwenDenseHip:
         self.model.ctx.check(L.lib().zg_session_fill_random(self.h, rows, prefix, seed))
 
     def close(self):
-        if getattr(self, "h", None):
+        if getattr(self, "h", None) and getattr(self.model, "h", None):
             L.lib().zg_session_destroy(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):
         self.close()
