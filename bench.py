@@ -1,12 +1,18 @@
-"""Benchmark of the MI355X Qwen3.5 GGUF hot path.
+"""Benchmark of the MI355X Qwen3.5 GGUF decode hot path.
 
-Workloads:
-  gemv   BASELINE config 2: dequant-GEMV sweep (Q8_0/Q4_K, M in {1,4,16,32}),
-         bf16 activations with the RMSNorm prologue; weights rotate across
-         distinct buffers totalling > 2x the 256 MB Infinity Cache so every
-         launch streams from HBM.  Timed with HIP events on the launch stream.
+Workloads (synthetic, seeded random-init weights in the named GGUF codec):
+  decode (default)  2B-shaped Q4_K hybrid model (hidden 2048, 24 layers at
+         3:1 GDN:attention, FFN 6144, vocab 151936), continuous-batch greedy
+         decode at B=1 and B=32, each row holding a 2048-token random prefix in
+         the bf16 KV cache and a random GDN state.  A step is one decode
+         position for every row: embedding, 24 layers, LM head, device argmax
+         feeding the next step's tokens.  value = B=1 tokens/s.
+  gemv   dequant-GEMV sweep (Q8_0/Q4_K, M in {1,4,16,32}) with the RMSNorm
+         prologue; weights rotate across distinct buffers totalling > 2x the
+         256 MB Infinity Cache.
 
-The default workload is the one BASELINE.json's metric is quoted on.
+Every timed region uses HIP events recorded on the stream the kernels are
+launched on (a non-null torch stream at default priority).
 """
 import argparse
 import json
@@ -21,16 +27,226 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 << 20
+Q8_0, Q4_K = 8, 12
+BPE = {Q8_0: 34 / 32, Q4_K: 144 / 256}
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def gemv_bytes(kind, N, K, M):
-    bpe = 34 / 32 if kind == 8 else 144 / 256
-    return N * K * bpe + M * K * 2 + M * N * 4
+def host_threads():
+    """Host cores for the CPU baseline: this process's affinity, capped by
+    OMP_NUM_THREADS when set (the GPU box gives one GPU a 16-core share)."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    return max(1, min(n, int(env))) if env and env.isdigit() else n
 
+
+def gemv_bytes(kind, N, K, M):
+    """Algorithmic bytes of one GEMV launch: weights once, bf16 activation
+    rows in, f32 outputs out."""
+    return N * K * BPE[kind] + M * K * 2 + M * N * 4
+
+
+# ------------------------------------------------------------------ decode
+
+def decode_matrices(g):
+    """(name, K, N) of every quantized matrix one decode step streams, in
+    launch order (model-qwen35/src/forward.rs layer schedule + tied LM head)."""
+    H, F, V = g["hidden"], g["ffn"], g["vocab"]
+    W = g["gdn_heads"] * g["gdn_dim"]
+    QD, KD = g["q_heads"] * g["head_dim"], g["kv_heads"] * g["head_dim"]
+    out = []
+    for i in range(g["layers"]):
+        p = f"blk.{i}."
+        if (i + 1) % g["full_attention_interval"] == 0:
+            out += [(p + "attn_q.weight", H, 2 * QD), (p + "attn_k.weight", H, KD), (p + "attn_v.weight", H, KD),
+                    (p + "attn_output.weight", QD, H)]
+        else:
+            out += [(p + "attn_qkv.weight", H, 3 * W), (p + "attn_gate.weight", H, W),
+                    (p + "ssm_alpha.weight", H, g["gdn_heads"]), (p + "ssm_beta.weight", H, g["gdn_heads"]),
+                    (p + "ssm_out.weight", W, H)]
+        out += [(p + "ffn_gate.weight", H, F), (p + "ffn_up.weight", H, F), (p + "ffn_down.weight", F, H)]
+    out.append(("token_embd.weight", H, V))
+    return out
+
+
+def step_bytes(g, kind, B, T):
+    """Algorithmic HBM bytes of one decode step at B rows, T cached tokens:
+    every weight once, GDN state read+write and conv history per row, K and
+    V of T tokens (bf16) per attention layer and row, activations ignored."""
+    w = sum(N * K * BPE[kind] for _, K, N in decode_matrices(g))
+    W = g["gdn_heads"] * g["gdn_dim"]
+    n_attn = g["layers"] // g["full_attention_interval"]
+    n_gdn = g["layers"] - n_attn
+    state = n_gdn * (g["gdn_heads"] * g["gdn_dim"] ** 2 * 4 * 2 + 3 * W * 3 * 4 * 2)
+    kv = n_attn * 2 * T * g["kv_heads"] * g["head_dim"] * 2
+    return w + B * (state + kv)
+
+
+def run_decode(model, torch, B, prefix, steps, warmup, seed):
+    """Greedy decode of `steps` positions for B rows after `warmup` untimed
+    ones; tokens stay on the device (argmax output feeds the next step)."""
+    from zerogravity_amd import _lib as L
+    lib = L.lib()
+    sess = model.session(max_batch=B, max_context=prefix + warmup + steps + 1, kv_dtype=L.BF16)
+    sess.fill_random_prefix(B, prefix, seed)
+    s = torch.cuda.current_stream()
+    assert s.cuda_stream != 0, "launch and event stream must be a real stream"
+    toks = torch.from_numpy(np.random.default_rng(seed).integers(0, model.g["vocab"], B).astype(np.int32)).cuda()
+    ptr = toks.data_ptr()
+
+    def step():
+        model.ctx.check(lib.zg_decode_step_device(sess.h, B, ptr, None, ptr, s.cuda_stream))
+
+    for _ in range(warmup):
+        step()
+    model.ctx.check(lib.zg_session_check(sess.h, s.cuda_stream))
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(s)
+    for i in range(steps):
+        step()
+        ev[i + 1].record(s)
+    torch.cuda.synchronize()
+    model.ctx.check(lib.zg_session_check(sess.h, s.cuda_stream))
+    per = np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(steps)])
+    total_ms = ev[0].elapsed_time(ev[-1])
+    assert sess.positions()[:B] == [prefix + warmup + steps] * B
+    sess.close()
+    return total_ms, per
+
+
+def gemv_leg(kern, torch, g, tensors, kind, reps):
+    """The dominant kernel: the Q4_K dequant-GEMV launches of one B=1 decode
+    step (every quantized matrix of the model in launch order, ~0.95 GB, so
+    nothing is served from the 256 MB Infinity Cache), replayed `reps` times
+    with HIP events around each replay."""
+    from zerogravity_amd import _lib as L
+    lib, ctx = L.lib(), kern.ctx
+    mats = decode_matrices(g)
+    handles = []
+    for name, K, N in mats:
+        ty, s0, s1, data = tensors[name]
+        assert ty == kind and s0 == K and s1 == N, name
+        handles.append((kern.register(4243, "leg." + name, kind, K, N, data), K, N))
+    s = torch.cuda.current_stream()
+    rng = np.random.default_rng(7)
+    preps = {}
+    for h, K, N in handles:
+        if K not in preps:
+            from zerogravity_amd import synth
+            _, xb = synth.bf16_round(rng.standard_normal((1, K)).astype(np.float32))
+            x_d = torch.from_numpy(xb.view(np.int16)).cuda()
+            g_d = torch.ones(K, dtype=torch.float32, device="cuda")
+            nb = lib.zg_act_prepared_bytes(h.h, 1)
+            prep = torch.empty(nb, dtype=torch.uint8, device="cuda")
+            ctx.check(lib.zg_act_prepare_device(ctx.h, h.h, x_d.data_ptr(), L.BF16, 1, g_d.data_ptr(), 1e-6,
+                                                prep.data_ptr(), nb, s.cuda_stream))
+            preps[K] = (prep, x_d, g_d)
+    y = torch.empty(max(N for _, _, N in handles), dtype=torch.float32, device="cuda")
+
+    def replay():
+        for h, K, N in handles:
+            ctx.check(lib.zg_gemv_prepared_device(ctx.h, h.h, 1, preps[K][0].data_ptr(), y.data_ptr(), s.cuda_stream))
+
+    replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(reps):
+        replay()
+    e1.record(s)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    byts = sum(gemv_bytes(kind, N, K, 1) for _, K, N in handles)
+    kern.release_source(4243)
+    return dict(launches=len(handles), us_per_step=us, us_per_launch=us / len(handles),
+                bytes_per_launch=byts / len(handles), gbs=byts / us / 1e3)
+
+
+def cpu_decode_baseline(g, tensors, prefix, seconds):
+    """The oracle (C restatement of the reference CPU path, OpenMP over GEMV
+    rows on every host core) decoding greedily at B=1 after importing a random
+    state of `prefix` tokens."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import zg_oracle as O
+    threads = host_threads()
+    cap = 256  # decode steps at most; the sample is bounded by `seconds` first
+    model = O.Model(dict(g, max_context=prefix + cap + 2), tensors, threads)
+    sess = model.session()
+    n = int(sess_state_floats(g, prefix))
+    rng = np.random.default_rng(3)
+    sess.load_state((0.02 * rng.standard_normal(n)).astype(np.float32), prefix)
+    tok = 1
+    sess.forward(tok)  # first touch
+    t0 = time.perf_counter()
+    steps = 0
+    while (time.perf_counter() - t0 < seconds or steps < 2) and steps < cap:
+        tok = int(np.argmax(sess.forward(tok)))
+        steps += 1
+    dt = time.perf_counter() - t0
+    return steps / dt, threads, f"{steps} greedy decode steps at B=1 from a random {prefix}-token state"
+
+
+def sess_state_floats(g, T):
+    W = g["gdn_heads"] * g["gdn_dim"]
+    n_attn = g["layers"] // g["full_attention_interval"]
+    n_gdn = g["layers"] - n_attn
+    return n_gdn * (3 * W * 3 + g["gdn_heads"] * g["gdn_dim"] ** 2) + n_attn * 2 * T * g["kv_heads"] * g["head_dim"]
+
+
+def bench_decode(args):
+    import torch
+    from zerogravity_amd import gguf, qwen35
+    from zerogravity_amd import regions as R
+    kern = R.HipMatVecKernel(0)
+    torch.cuda.set_stream(torch.cuda.Stream())  # default priority, non-null
+    g = dict(qwen35.QWEN35_2B)
+    t0 = time.perf_counter()
+    tensors = qwen35.synthetic_tensors(g, gguf.Q4_K, seed=2026)
+    model = qwen35.QwenModelHip(g, tensors, kernel=kern)
+    log(f"2B Q4_K model resident ({time.perf_counter() - t0:.1f} s)")
+    prefix = args.prefix
+    res = {}
+    for B in (1, 32):
+        total_ms, per = run_decode(model, torch, B, prefix, args.steps, args.warmup, seed=B)
+        tps = B * args.steps / (total_ms / 1e3)
+        byts = step_bytes(g, gguf.Q4_K, B, prefix + args.warmup + args.steps // 2)
+        res[B] = dict(tok_s=tps, ms_per_step=total_ms / args.steps, p10_ms=float(np.percentile(per, 10)),
+                      p50_ms=float(np.median(per)), p90_ms=float(np.percentile(per, 90)),
+                      step_gb=byts / 1e9, step_hbm_frac=byts / (total_ms / args.steps * 1e-3) / 1e9 / HBM_PEAK_GBS)
+        log(f"decode B={B:2d}: {total_ms / args.steps:.3f} ms/step  {tps:9.1f} tok/s  "
+            f"(p10 {res[B]['p10_ms']:.3f} p50 {res[B]['p50_ms']:.3f} p90 {res[B]['p90_ms']:.3f} ms; "
+            f"{res[B]['step_gb']:.3f} GB/step = {res[B]['step_hbm_frac']:.1%} of HBM roofline)")
+    model.close()
+    leg = gemv_leg(kern, torch, g, tensors, gguf.Q4_K, args.leg_reps)
+    log(f"Q4_K GEMV leg: {leg['launches']} launches {leg['us_per_step']:.1f} us/step, "
+        f"{leg['us_per_launch']:.2f} us/launch, {leg['gbs']:.0f} GB/s")
+    line = {
+        "metric": "decode tok/s @B=1 (2B-shaped Q4_K, 2048-token prefix, bf16 KV)",
+        "value": round(res[1]["tok_s"], 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(res[1]["ms_per_step"], 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q4_k weights, f32 accumulate",
+        "data": "synthetic (seeded random-init Q4_K GGUF weights, random prefix state)",
+        "config": {"workload": "2B-shaped Q4_K continuous-batch greedy decode", "prefix": prefix,
+                   "kv_cache": "bf16", "b1": res[1], "b32": res[32],
+                   "b32_tok_s": round(res[32]["tok_s"], 1)},
+        "roofline": {"bound": "hbm", "achieved": round(leg["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(leg["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_q4k_kernel (decode-step launches, B=1)",
+                     "bytes_per_launch": round(leg["bytes_per_launch"]), "us_per_launch": round(leg["us_per_launch"], 3)},
+    }
+    if not args.no_cpu:
+        v, cores, sample = cpu_decode_baseline(g, tensors, prefix, args.cpu_seconds)
+        line["cpu_baseline"] = {"value": round(v, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+                                "sample": sample}
+    kern.ctx.close()
+    return line
+
+
+# -------------------------------------------------------------------- gemv
 
 def register_copies(kern, kind, N, K, rng):
     """Distinct device copies totalling > 2.2x the Infinity Cache."""
@@ -40,7 +256,7 @@ def register_copies(kern, kind, N, K, rng):
     return [kern.register(4242, f"bench.{kind}.{N}.{K}.{i}", kind, K, N, w) for i in range(copies)]
 
 
-def bench_gemv(kern, torch, handles, kind, N, K, M, steps, warmup, rng):
+def bench_gemv_one(kern, torch, handles, kind, N, K, M, steps, warmup, rng):
     from zerogravity_amd import _lib as L
     from zerogravity_amd import synth
     copies = len(handles)
@@ -71,11 +287,10 @@ def bench_gemv(kern, torch, handles, kind, N, K, M, steps, warmup, rng):
     e1.record(s)
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / steps
-    byts = gemv_bytes(kind, N, K, M)
-    return us, byts / us / 1e3  # GB/s
+    return us, gemv_bytes(kind, N, K, M) / us / 1e3
 
 
-def cpu_gemv_baseline(kind, N, K, seconds=10.0):
+def cpu_gemv_baseline(kind, N, K, seconds):
     """Oracle GEMV (OpenMP over rows, all host cores) on a bounded row sample."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import zg_oracle as O
@@ -84,7 +299,7 @@ def cpu_gemv_baseline(kind, N, K, seconds=10.0):
     rows = min(N, 32768)
     w = synth.random_matrix(rng, kind, rows, K)
     x = rng.standard_normal(K).astype(np.float32)
-    threads = os.cpu_count() or 1
+    threads = host_threads()
     O.matvec(kind, w.reshape(-1), rows, K, x, threads)
     t0 = time.perf_counter()
     n = 0
@@ -92,55 +307,63 @@ def cpu_gemv_baseline(kind, N, K, seconds=10.0):
         O.matvec(kind, w.reshape(-1), rows, K, x, threads)
         n += 1
     dt = (time.perf_counter() - t0) / n
-    byts = rows * K * (34 / 32 if kind == 8 else 144 / 256) + K * 4 + rows * 4
+    byts = rows * K * BPE[kind] + K * 4 + rows * 4
     return byts / dt / 1e9, threads, f"{rows}x{K} rows of the {N}x{K} matrix, {n} passes"
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="gemv", choices=["gemv"])
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(data-parallel sharding is described in DESIGN.md)", file=sys.stderr)
-        sys.exit(2)
+def bench_gemv(args):
     import torch
     from zerogravity_amd import regions as R
     kern = R.HipMatVecKernel(0)
-    torch.cuda.set_stream(torch.cuda.Stream())  # default priority, non-null
+    torch.cuda.set_stream(torch.cuda.Stream())
     rng = np.random.default_rng(2026)
     results = []
     shapes = [(3584, 1024), (1024, 3584), (6144, 2048), (2048, 6144), (151936, 2048)]
-    for kind in (12, 8):
+    for kind in (Q4_K, Q8_0):
         for (N, K) in shapes:
             handles = register_copies(kern, kind, N, K, rng)
             for M in (1, 4, 16, 32):
-                us, gbs = bench_gemv(kern, torch, handles, kind, N, K, M, args.steps, args.warmup, rng)
-                name = "Q4_K" if kind == 12 else "Q8_0"
+                us, gbs = bench_gemv_one(kern, torch, handles, kind, N, K, M, args.steps, args.warmup, rng)
+                name = "Q4_K" if kind == Q4_K else "Q8_0"
                 log(f"gemv {name} N={N:6d} K={K:5d} M={M:2d}: {us:9.2f} us  {gbs:8.1f} GB/s  "
                     f"({gbs / HBM_PEAK_GBS:.1%} of HBM)")
-                results.append(dict(kind=name, N=N, K=K, M=M, us=us, gbs=gbs))
+                results.append(dict(kind=name, N=N, K=K, M=M, us=round(us, 3), gbs=round(gbs, 1)))
             del handles
             kern.release_source(4242)
     head = next(r for r in results if r["kind"] == "Q4_K" and r["N"] == 151936 and r["M"] == 1)
     line = {
         "metric": "dequant-GEMV achieved HBM GB/s (Q4_K 151936x2048, M=1, RMSNorm-prepared bf16 activation)",
-        "value": round(head["gbs"], 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "value": head["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": head["us"] / 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "q4_k x f32", "data": "synthetic (seeded random GGUF blocks)",
-        "config": {"workload": "BASELINE config 2: GEMV sweep", "sweep": results},
-        "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "config": {"workload": "dequant-GEMV sweep", "sweep": results},
+        "roofline": {"bound": "hbm", "achieved": head["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
     }
     if not args.no_cpu:
-        v, cores, sample = cpu_gemv_baseline(12, 151936, 2048, args.cpu_seconds)
+        v, cores, sample = cpu_gemv_baseline(Q4_K, 151936, 2048, args.cpu_seconds)
         line["cpu_baseline"] = {"value": round(v, 2), "unit": "GB/s", "cores": cores, "kind": "port",
                                 "sample": sample}
+    kern.ctx.close()
+    return line
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--workload", default="decode", choices=["decode", "gemv"])
+    ap.add_argument("--prefix", type=int, default=2048)
+    ap.add_argument("--leg-reps", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each GPU would run its own "
+              "sessions; see the sharding notes in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    line = bench_decode(args) if args.workload == "decode" else bench_gemv(args)
     print(json.dumps(line), flush=True)
 
 

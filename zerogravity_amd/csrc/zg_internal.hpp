@@ -114,5 +114,6 @@ hipError_t argmax(const float* logits, size_t V, size_t B, uint32_t* out, int* s
 hipError_t fill_normal(void* p, size_t n, bool bf16, uint64_t seed, float sigma, hipStream_t s);
 hipError_t convert_kv(const void* in, void* out, size_t n, bool to_f32, hipStream_t s);
 hipError_t fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
+hipError_t advance_positions(int* pos, int* ntok, size_t B, hipStream_t s);  // B <= 64
 
 }  // namespace zg

@@ -231,6 +231,21 @@ hipError_t convert_kv(const void* in, void* out, size_t n, bool to_f32, hipStrea
     return hipGetLastError();
 }
 
+// Rows [0, B) move one token on: pos += 1, ntok = pos + 1.
+__global__ void advance_positions_kernel(int* __restrict__ pos, int* __restrict__ ntok, int B) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b < B) {
+        const int p = pos[b] + 1;
+        pos[b] = p;
+        ntok[b] = p + 1;
+    }
+}
+
+hipError_t advance_positions(int* pos, int* ntok, size_t B, hipStream_t s) {
+    hipLaunchKernelGGL(advance_positions_kernel, dim3(1), dim3(64), 0, s, pos, ntok, (int)B);
+    return hipGetLastError();
+}
+
 hipError_t fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s) {
     hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks_for(n)), dim3(256), 0, s, p, n, v);
     return hipGetLastError();

@@ -40,6 +40,7 @@ struct zg_session {
     int kv_bf16 = 1;
     std::vector<int> pos;  // host copy of each row's next position
     bool poisoned = false;
+    bool pos_dirty = true;  // device positions must be re-uploaded from pos
     // device buffers
     std::vector<void*> allocs;
     int *d_pos = nullptr, *d_ntok = nullptr, *d_status = nullptr;
@@ -225,8 +226,14 @@ int read_status(zg_session* s, hipStream_t st) {
     return ZG_COMPLETED;
 }
 
-int upload_positions(zg_session* s, size_t B, hipStream_t st) {
+// Device positions follow the host copy: steps advance both (a one-wave
+// kernel on the stream, so device-driven decode loops never wait on the
+// host); reset, import and random fill mark them dirty and the next step
+// uploads them once.
+int sync_positions(zg_session* s, hipStream_t st) {
+    if (!s->pos_dirty) return ZG_COMPLETED;
     zg_ctx* ctx = s->m->ctx;
+    const size_t B = s->max_batch;
     std::vector<int> p(B), t(B);
     for (size_t b = 0; b < B; ++b) {
         p[b] = s->pos[b];
@@ -236,6 +243,14 @@ int upload_positions(zg_session* s, size_t B, hipStream_t st) {
     ZG_HIP(hipMemcpyAsync(s->d_ntok, t.data(), B * sizeof(int), hipMemcpyHostToDevice, st));
     // pageable source: make the copy complete before the vectors go away
     ZG_HIP(hipStreamSynchronize(st));
+    s->pos_dirty = false;
+    return ZG_COMPLETED;
+}
+
+int advance(zg_session* s, size_t rows, hipStream_t st) {
+    zg_ctx* ctx = s->m->ctx;
+    ZG_HIP(zg::advance_positions(s->d_pos, s->d_ntok, rows, st));
+    for (size_t b = 0; b < rows; ++b) s->pos[b] += 1;
     return ZG_COMPLETED;
 }
 
@@ -427,6 +442,7 @@ int zg_session_reset(zg_session* s) {
     ZG_HIP(hipMemsetAsync(s->d_status, 0, 4, ctx->stream));
     ZG_HIP(hipStreamSynchronize(ctx->stream));
     std::fill(s->pos.begin(), s->pos.end(), 0);
+    s->pos_dirty = true;
     s->poisoned = false;
     return ZG_COMPLETED;
 }
@@ -446,7 +462,7 @@ int zg_decode_step(zg_session* s, size_t rows, const uint32_t* tokens, float* lo
     for (size_t b = 0; b < rows; ++b)
         if (tokens[b] >= s->m->g.vocab) return fail(ctx, ZG_E_MALFORMED, "decode step contains an out-of-vocabulary token id");
     hipStream_t st = ctx->stream;
-    if ((rc = upload_positions(s, rows, st))) return rc;
+    if ((rc = sync_positions(s, st))) return rc;
     ZG_HIP(hipMemcpyAsync(s->d_tokens, tokens, rows * 4, hipMemcpyHostToDevice, st));
     ZG_HIP(hipStreamSynchronize(st));
     const bool want = logits || greedy;
@@ -454,11 +470,11 @@ int zg_decode_step(zg_session* s, size_t rows, const uint32_t* tokens, float* lo
         s->poisoned = true;
         return rc;
     }
+    if ((rc = advance(s, rows, st))) return rc;
     if ((rc = read_status(s, st))) return rc;
     if (logits) ZG_HIP(hipMemcpyAsync(logits, s->logits, rows * s->m->g.vocab * 4, hipMemcpyDeviceToHost, st));
     if (greedy) ZG_HIP(hipMemcpyAsync(greedy, s->d_greedy, rows * 4, hipMemcpyDeviceToHost, st));
     ZG_HIP(hipStreamSynchronize(st));
-    for (size_t b = 0; b < rows; ++b) s->pos[b] += 1;
     return ZG_COMPLETED;
 }
 
@@ -484,13 +500,12 @@ int zg_decode_step_device(zg_session* s, size_t rows, const uint32_t* d_tokens, 
     int rc = check_rows(s, rows);
     if (rc) return rc;
     hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
-    if ((rc = upload_positions(s, rows, st))) return rc;
+    if ((rc = sync_positions(s, st))) return rc;
     if ((rc = step(s, rows, d_tokens, d_logits ? d_logits : (d_greedy ? s->logits : nullptr), d_greedy, st))) {
         s->poisoned = true;
         return rc;
     }
-    for (size_t b = 0; b < rows; ++b) s->pos[b] += 1;
-    return ZG_COMPLETED;
+    return advance(s, rows, st);
 }
 
 int zg_session_check(zg_session* s, void* stream) {
@@ -588,6 +603,7 @@ int zg_state_import(zg_session* s, size_t row, const float* in, size_t n, int po
         }
     }
     ZG_HIP(hipStreamSynchronize(st));
+    s->pos_dirty = true;
     s->poisoned = false;
     return ZG_COMPLETED;
 }
@@ -616,6 +632,7 @@ int zg_session_fill_random(zg_session* s, size_t rows, size_t prefix, uint64_t s
     }
     ZG_HIP(hipStreamSynchronize(st));
     for (size_t b = 0; b < rows; ++b) s->pos[b] = (int)prefix;
+    s->pos_dirty = true;
     s->poisoned = false;
     return ZG_COMPLETED;
 }
