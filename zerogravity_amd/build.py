@@ -19,6 +19,9 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # loops marked `#pragma unroll` index register arrays and must unroll
+    # fully even when long (else the arrays go to scratch memory)
+    "-mllvm", "-pragma-unroll-threshold=100000",
     "-munsafe-fp-atomics", "-Wall", "-Wno-unused-function",
     "-I" + os.path.join(ROOT, "include"), "-I" + CSRC,
 ]

@@ -1,0 +1,1057 @@
+// Fused kernels of the resident decode step (gfx950).
+//
+// A decode step is a chain of dependent launches; at batch 1 each launch is
+// latency-bound, so the step is built from as few launches as the data
+// dependencies allow:
+//   GDN layer:  [RMS + in-proj (qkv|z|alpha|beta)] [conv + L2 + gates +
+//               recurrence] [gated RMS + ssm_out + residual]
+//   attention:  [RMS + in-proj (q|gate, k, v)] [q/k norm + RoPE + KV append
+//               + QK] [softmax + PV + sigmoid gate] [o-proj + residual]
+//   FFN:        [RMS + gate|up] [SiLU product + down + residual]
+//   head:       [RMS + LM head] [argmax + position advance]
+// Each GEMV launch prepares its own activation in its prologue and adds the
+// residual in its epilogue.  Every rounding point is the reference's
+// (model-qwen35/src/forward.rs:451-755, lib.rs:263-362,1276-1577), in the
+// reference's order, so the Q8_0 path is bit-identical to the CPU.
+#include <algorithm>
+
+#include "zg_device.hpp"
+#include "zg_internal.hpp"
+#include "zg_pointwise.hpp"
+
+namespace zg {
+
+// ======================================================= activation values
+
+__device__ __forceinline__ float rms_inv(double total, int n, float eps) {
+    const float mean = (float)(total / (double)n);
+    const float root = sqrtf(mean + eps);
+    return 1.0f / root;
+}
+
+__device__ __forceinline__ void epilogue(const FusedGemvArgs& a, int m, int row, float acc, int epi) {
+    float* p = a.y + (size_t)m * a.ldy + row;
+    if (epi == EPI_RESID) {
+        const float v = *p + acc;  // source_binary Add, lib.rs:1258-1271
+        *p = v;
+        if (!finite_f32(v)) atomicOr(a.status, 1);
+    } else {
+        *p = acc;
+    }
+}
+
+// ================================================ workgroup prologue
+
+constexpr int kCodecQ4K = 0, kCodecQ8 = 1;
+constexpr int kRecWords = 36;  // Q4_K record: 32 dwords of int16 pairs + {xs_lo, xs_hi, sum_lo, sum_hi}
+
+// Activation row m prepared once per workgroup.  Thread t holds the float4
+// slabs k = 4t + 1024j (all loads issued together), so the 8 threads of a
+// 32-element group are adjacent lanes and the group statistics are 3-step
+// XOR shuffles.  The values are coded straight into LDS:
+//   Q8_0 (cpu/src/source/quantization.rs:37-61): per 32-block amax,
+//     d = amax/127, code = clamp(rint(v*127/amax)), d rounded to f16;
+//     codes [K/4] words, scales [K/32].
+//   Q4_K: per 32-group int16 fixed point, xq = rint(v*32767/amax), with the
+//     group's scale amax/32767 and its f32 sum; records [K/64][36] dwords in
+//     the pairing gemv_q4k_kernel expects (element e of a group goes to
+//     dword (e&1 ? 8 : 0) + e/4, half (e>>1)&1; high group +16).
+// Ends with a barrier.  K <= 1024 * JMAX, K % 32 == 0.
+template <int PRO, int CODEC, int JMAX>
+__device__ void wg_prologue(const FusedGemvArgs& a, int m, bool valid, uint32_t* rec, int* codes, float* scales) {
+    __shared__ double red[4];
+    const int tid = threadIdx.x, lane = tid & 63, K = a.K;
+    v4f v[JMAX], w[JMAX];
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) {
+        const int k = 4 * tid + 1024 * j;
+        v[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        w[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (valid && k < K) {
+            v[j] = *(const v4f*)(a.x + (size_t)m * a.ldx + k);
+            if (PRO == PRO_RMS) w[j] = *(const v4f*)(a.gamma + k);
+            if (PRO == PRO_GATED || PRO == PRO_SILU_MUL) w[j] = *(const v4f*)(a.x2 + (size_t)m * a.ldx2 + k);
+        }
+    }
+    float inv = 1.0f;
+    if (PRO == PRO_RMS) {
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < JMAX; ++j) {
+            const float q0 = v[j].x * v[j].x, q1 = v[j].y * v[j].y, q2 = v[j].z * v[j].z, q3 = v[j].w * v[j].w;
+            s += (double)q0;
+            s += (double)q1;
+            s += (double)q2;
+            s += (double)q3;
+        }
+        s = wave_sum_xor<double>(s, 64);
+        if (lane == 0) red[tid >> 6] = s;
+        __syncthreads();
+        inv = rms_inv((red[0] + red[1]) + (red[2] + red[3]), K, a.eps);
+    }
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) {
+        const int k = 4 * tid + 1024 * j;
+        if (1024 * j >= K) break;  // uniform
+        float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        const float o[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+        if (PRO == PRO_RMS) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) e[t] = (e[t] * inv) * o[t];
+        } else if (PRO == PRO_GATED) {
+            // per 128-element group (32 adjacent lanes): f64 sum of f32 squares
+            double s = 0.0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float q = e[t] * e[t];
+                s += (double)q;
+            }
+            s = wave_sum_xor<double>(s, 32);
+            const float gi = rms_inv(s, a.group, a.eps);
+            const v4f g = k < K ? *(const v4f*)(a.gamma + (k & (a.group - 1))) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            const float gg[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) e[t] = ((e[t] * gi) * gg[t]) * ggml_silu(o[t]);
+        } else if (PRO == PRO_SILU_MUL) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) e[t] = o[t] * ggml_silu(e[t]);
+        }
+        if (!(valid && k < K)) e[0] = e[1] = e[2] = e[3] = 0.0f;
+        float amax = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
+        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        const int l = tid & 7;
+        if (k < K) {
+            if (CODEC == kCodecQ8) {
+                const float d = amax / 127.0f;
+                const float qi = amax == 0.0f ? 0.0f : 127.0f / amax;
+                uint32_t word = 0;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    float r = rintf(e[t] * qi);
+                    r = fminf(fmaxf(r, -128.0f), 127.0f);
+                    word |= ((uint32_t)(int)r & 0xffu) << (8 * t);
+                }
+                codes[k >> 2] = (int)word;
+                if (l == 0) scales[k >> 5] = f16_roundtrip(d);
+            }
+        }
+        if (CODEC == kCodecQ4K) {
+            float sum = ((e[0] + e[1]) + e[2]) + e[3];
+            sum += __shfl_xor(sum, 4, 64);
+            sum += __shfl_xor(sum, 2, 64);
+            sum += __shfl_xor(sum, 1, 64);
+            if (k < K) {
+                const float qi = amax == 0.0f ? 0.0f : 32767.0f / amax;
+                const int q0 = (int)rintf(e[0] * qi), q1 = (int)rintf(e[1] * qi);
+                const int q2 = (int)rintf(e[2] * qi), q3 = (int)rintf(e[3] * qi);
+                const int g = k >> 5, hi = g & 1;
+                uint32_t* r = rec + (size_t)(g >> 1) * kRecWords;
+                r[hi * 16 + l] = ((uint32_t)q0 & 0xffffu) | ((uint32_t)q2 << 16);
+                r[hi * 16 + 8 + l] = ((uint32_t)q1 & 0xffffu) | ((uint32_t)q3 << 16);
+                if (l == 0) {
+                    r[32 + hi] = __float_as_uint(amax / 32767.0f);
+                    r[34 + hi] = __float_as_uint(sum);
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// ============================================================= Q4_K GEMV
+
+// Lanes: `lpr` per row, chunk c = sub + i*lpr (i < CH) is the group pair
+// (2p, 2p+1) of block c/4: elements 64c .. 64c+63; the nibble/int16 pairing
+// and the per-group epilogue are gemv_q4k_kernel's.  The workgroup codes the
+// activation into LDS once (its weight loads for the first row group are
+// already in flight), each lane copies its chunk records to registers.
+template <int CH, int MT, int J, int RG, int PRO, int EPI>
+__global__ __launch_bounds__(256) void fused_q4k_kernel(FusedGemvArgs a, int lpr_log2) {
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    extern __shared__ uint32_t lds_q4[];
+    const int lane = threadIdx.x & 63;
+    const int lpr = 1 << lpr_log2;
+    const int sub = lane & (lpr - 1);
+    const int rsub = lane >> lpr_log2;
+    const int rpw = 64 >> lpr_log2;
+    const int K = a.K, N = a.N;
+    const int nchunk = K >> 6, nbk = K >> 8;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nwaves = gridDim.x * 4;
+    const int m0 = blockIdx.y * MT;
+    const int p = sub & 3;
+    const uint8_t* qs = (const uint8_t*)a.qs;
+    const v4u* hdr = (const v4u*)a.hdr;
+
+    // RG consecutive row groups per wave, all their loads issued together
+    v4i w0[RG][CH], w1[RG][CH];
+    v4u h[RG][CH];
+    auto load_rows = [&](int rg0) {
+#pragma unroll
+        for (int r = 0; r < RG; ++r) {
+            const int row = (rg0 + r) * rpw + rsub;
+#pragma unroll
+            for (int i = 0; i < CH; ++i) {
+                const int c = sub + i * lpr;
+                if (row < N && c < nchunk) {
+                    const uint8_t* base = qs + (size_t)row * (K >> 1) + (size_t)c * 32;
+                    w0[r][i] = load_nt(base);
+                    w1[r][i] = load_nt(base + 16);
+                    h[r][i] = hdr[(size_t)row * nbk + (c >> 2)];
+                } else {
+                    w0[r][i] = v4i{0, 0, 0, 0};
+                    w1[r][i] = v4i{0, 0, 0, 0};
+                    h[r][i] = v4u{0u, 0u, 0u, 0u};
+                }
+            }
+        }
+    };
+    if (wave * RG * rpw < N) load_rows(wave * RG);
+
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+        wg_prologue<PRO, kCodecQ4K, J>(a, m0 + m, m0 + m < a.M, lds_q4 + (size_t)m * nchunk * kRecWords, nullptr,
+                                    nullptr);
+
+    int xl0[MT][CH][8], xl1[MT][CH][8], xh0[MT][CH][8], xh1[MT][CH][8];
+    float xs_lo[MT][CH], xs_hi[MT][CH], sx_lo[MT][CH], sx_hi[MT][CH];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int c = sub + i * lpr;
+            if (c < nchunk) {
+                const v4u* r = (const v4u*)(lds_q4 + ((size_t)m * nchunk + c) * kRecWords);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const v4u r0 = r[j], r1 = r[2 + j], r2 = r[4 + j], r3 = r[6 + j];
+                    xl0[m][i][4 * j + 0] = r0.x; xl0[m][i][4 * j + 1] = r0.y; xl0[m][i][4 * j + 2] = r0.z; xl0[m][i][4 * j + 3] = r0.w;
+                    xl1[m][i][4 * j + 0] = r1.x; xl1[m][i][4 * j + 1] = r1.y; xl1[m][i][4 * j + 2] = r1.z; xl1[m][i][4 * j + 3] = r1.w;
+                    xh0[m][i][4 * j + 0] = r2.x; xh0[m][i][4 * j + 1] = r2.y; xh0[m][i][4 * j + 2] = r2.z; xh0[m][i][4 * j + 3] = r2.w;
+                    xh1[m][i][4 * j + 0] = r3.x; xh1[m][i][4 * j + 1] = r3.y; xh1[m][i][4 * j + 2] = r3.z; xh1[m][i][4 * j + 3] = r3.w;
+                }
+                const v4u mt = r[8];
+                xs_lo[m][i] = __uint_as_float(mt.x);
+                xs_hi[m][i] = __uint_as_float(mt.y);
+                sx_lo[m][i] = __uint_as_float(mt.z);
+                sx_hi[m][i] = __uint_as_float(mt.w);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) xl0[m][i][q] = xl1[m][i][q] = xh0[m][i][q] = xh1[m][i][q] = 0;
+                xs_lo[m][i] = xs_hi[m][i] = sx_lo[m][i] = sx_hi[m][i] = 0.0f;
+            }
+        }
+
+    bool first = true;
+    for (int rg0 = wave * RG; rg0 * rpw < N; rg0 += nwaves * RG) {
+        if (!first) load_rows(rg0);
+        first = false;
+#pragma unroll
+        for (int r = 0; r < RG; ++r) {
+            const int row = (rg0 + r) * rpw + rsub;
+            float acc[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < CH; ++i) {
+                const uint32_t ww[8] = {(uint32_t)w0[r][i].x, (uint32_t)w0[r][i].y, (uint32_t)w0[r][i].z,
+                                        (uint32_t)w0[r][i].w, (uint32_t)w1[r][i].x, (uint32_t)w1[r][i].y,
+                                        (uint32_t)w1[r][i].z, (uint32_t)w1[r][i].w};
+                int ilo[MT], ihi[MT];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) ilo[m] = ihi[m] = 0;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const uint32_t d = ww[q];
+                    const v2s L0 = __builtin_bit_cast(v2s, d & 0x000f000fu);
+                    const v2s L1 = __builtin_bit_cast(v2s, (d >> 8) & 0x000f000fu);
+                    const v2s H0 = __builtin_bit_cast(v2s, (d >> 4) & 0x000f000fu);
+                    const v2s H1 = __builtin_bit_cast(v2s, (d >> 12) & 0x000f000fu);
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        ilo[m] = __builtin_amdgcn_sdot2(L0, __builtin_bit_cast(v2s, xl0[m][i][q]), ilo[m], false);
+                        ilo[m] = __builtin_amdgcn_sdot2(L1, __builtin_bit_cast(v2s, xl1[m][i][q]), ilo[m], false);
+                        ihi[m] = __builtin_amdgcn_sdot2(H0, __builtin_bit_cast(v2s, xh0[m][i][q]), ihi[m], false);
+                        ihi[m] = __builtin_amdgcn_sdot2(H1, __builtin_bit_cast(v2s, xh1[m][i][q]), ihi[m], false);
+                    }
+                }
+                uint32_t sc0, mn0, sc1, mn1;
+                q4k_dev_scale_min(h[r][i], 2 * p, sc0, mn0);
+                q4k_dev_scale_min(h[r][i], 2 * p + 1, sc1, mn1);
+                const float d = f16_to_f32((uint16_t)(h[r][i].x & 0xffffu));
+                const float dmin = f16_to_f32((uint16_t)(h[r][i].x >> 16));
+                const float s0 = d * (float)sc0, n0 = dmin * (float)mn0;
+                const float s1 = d * (float)sc1, n1 = dmin * (float)mn1;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    acc[m] = fmaf(s0, xs_lo[m][i] * (float)ilo[m], acc[m]);
+                    acc[m] = fmaf(-n0, sx_lo[m][i], acc[m]);
+                    acc[m] = fmaf(s1, xs_hi[m][i] * (float)ihi[m], acc[m]);
+                    acc[m] = fmaf(-n1, sx_hi[m][i], acc[m]);
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < MT; ++m) acc[m] = wave_sum_xor(acc[m], lpr);
+            if (row < N && sub == 0) {
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    if (m0 + m < a.M) epilogue(a, m0 + m, row, acc[m], EPI);
+            }
+        }
+    }
+}
+
+// ============================================================= Q8_0 GEMV
+
+// The workgroup codes MT activation rows into LDS (wg_prologue), then runs
+// gemv_q8_0_kernel's row loop: the bit-exact reference order.
+template <int MT, int J, int PRO, int EPI>
+__global__ __launch_bounds__(256) void fused_q8_kernel(FusedGemvArgs a) {
+    extern __shared__ int lds_f8[];
+    const int K = a.K, N = a.N;
+    const int nb = K >> 5, nbc = (nb + 3) >> 2;
+    int* codes = lds_f8;                               // [MT][K/4] words
+    float* scales = (float*)(lds_f8 + MT * (K >> 2));  // [MT][nb]
+    const int m0 = blockIdx.y * MT;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+        wg_prologue<PRO, kCodecQ8, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * (K >> 2), scales + m * nb);
+    const v4i* qs = (const v4i*)a.qs;
+    const uint16_t* hdr = (const uint16_t*)a.hdr;
+    const int lane = threadIdx.x & 63;
+    const int rl = lane >> 3, l = lane & 7;
+    const int groups = (N + 7) >> 3;
+    const int nwaves = gridDim.x * 4;
+    for (int R = blockIdx.x * 4 + (threadIdx.x >> 6); R < groups; R += nwaves) {
+        const int row = R * 8 + rl;
+        const uint16_t* hrow = hdr + (size_t)(row < N ? row : N - 1) * nbc * 4;
+        const v4i* tile = qs + (size_t)R * nbc * 64 + lane;
+        float acc[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+        for (int c = 0; c < nbc; ++c) {
+            const v4i w4 = load_nt(tile + (size_t)c * 64);
+            const uint2 h2 = *(const uint2*)(hrow + 4 * c);
+            const int ww[4] = {w4.x, w4.y, w4.z, w4.w};
+            const uint32_t hw[4] = {h2.x & 0xffffu, h2.x >> 16, h2.y & 0xffffu, h2.y >> 16};
+#pragma unroll
+            for (int bi = 0; bi < 4; ++bi) {
+                const int b = 4 * c + bi;
+                if (b < nb) {
+                    const float wd = f16_to_f32((uint16_t)hw[bi]);
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        const int pair = __builtin_amdgcn_sdot4(ww[bi], codes[m * (K >> 2) + b * 8 + l], 0, false);
+                        const float scale = wd * scales[m * nb + b];
+                        acc[m] = fmaf((float)pair, scale, acc[m]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            acc[m] = acc[m] + __shfl_xor(acc[m], 4, 64);
+            acc[m] = acc[m] + __shfl_xor(acc[m], 2, 64);
+            acc[m] = acc[m] + __shfl_xor(acc[m], 1, 64);
+        }
+        if (row < N && l == 0) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                if (m0 + m < a.M) epilogue(a, m0 + m, row, acc[m], EPI);
+        }
+    }
+}
+
+// ============================================================ dispatch
+
+template <int PRO, int EPI>
+static hipError_t launch_q4k(const FusedGemvArgs& a, hipStream_t s) {
+    // one 64-element chunk per lane while the row fits 64 lanes (K <= 4096),
+    // else two; activation slabs J = ceil(K / 1024) rounded to 2, 4, 8
+    const int nchunk = a.K / 64;
+    int l = 2;
+    while (l < 6 && (1 << l) < nchunk) ++l;
+    const int ch = (nchunk + (1 << l) - 1) >> l;
+    if (ch > 2) return hipErrorInvalidValue;
+    int mt = a.M == 1 ? 1 : (a.M == 2 ? 2 : 4);
+    while (mt > 1 && ch * mt > 4) mt >>= 1;
+    // B=1: up to 4 row groups per wave so that ~2048 waves cover the matrix
+    // (fewer workgroups repeating the prologue, more loads in flight)
+    const size_t rpw = 64u >> l, groups = (a.N + rpw - 1) / rpw;
+    int rg = 1;
+    if (mt == 1) {
+        while (rg < 4 && groups > (size_t)2048 * rg) rg *= 2;
+    }
+    const size_t waves = (groups + rg - 1) / rg;
+    const unsigned wgs = (unsigned)std::min<size_t>((waves + 3) / 4, 256 * 8);
+    dim3 g(wgs, (unsigned)((a.M + mt - 1) / mt));
+    const size_t lds = (size_t)mt * nchunk * kRecWords * 4;
+#define ZG_F4(C, T, JJ, R) hipLaunchKernelGGL((fused_q4k_kernel<C, T, JJ, R, PRO, EPI>), g, dim3(256), lds, s, a, l)
+#define ZG_F4R(C, JJ)                \
+    if (rg == 1) ZG_F4(C, 1, JJ, 1);      \
+    else if (rg == 2) ZG_F4(C, 1, JJ, 2); \
+    else ZG_F4(C, 1, JJ, 4);
+    if (ch == 2) {
+        if (mt == 1) {
+            ZG_F4R(2, 8)
+        } else {
+            ZG_F4(2, 2, 8, 1);
+        }
+    } else if (a.K <= 2048) {
+        if (mt == 1) {
+            ZG_F4R(1, 2)
+        } else if (mt == 2) {
+            ZG_F4(1, 2, 2, 1);
+        } else {
+            ZG_F4(1, 4, 2, 1);
+        }
+    } else {
+        if (mt == 1) {
+            ZG_F4R(1, 4)
+        } else if (mt == 2) {
+            ZG_F4(1, 2, 4, 1);
+        } else {
+            ZG_F4(1, 4, 4, 1);
+        }
+    }
+#undef ZG_F4R
+#undef ZG_F4
+    return hipGetLastError();
+}
+
+template <int PRO, int EPI>
+static hipError_t launch_q8(const FusedGemvArgs& a, hipStream_t s) {
+    const int K = a.K;
+    int mt = a.M == 1 ? 1 : (a.M == 2 ? 2 : 4);
+    auto lds = [&](int t) { return (size_t)t * (K + (K / 32) * 4); };
+    const size_t groups = (a.N + 7) / 8;
+    const unsigned wgs = (unsigned)std::min<size_t>((groups + 3) / 4, 256 * 8);
+    dim3 g(wgs, (unsigned)((a.M + mt - 1) / mt));
+#define ZG_F8(T, JJ) hipLaunchKernelGGL((fused_q8_kernel<T, JJ, PRO, EPI>), g, dim3(256), lds(T), s, a)
+#define ZG_F8J(JJ)                  \
+    if (mt == 1) ZG_F8(1, JJ);      \
+    else if (mt == 2) ZG_F8(2, JJ); \
+    else ZG_F8(4, JJ);
+    if (K <= 1024) {
+        ZG_F8J(1)
+    } else if (K <= 2048) {
+        ZG_F8J(2)
+    } else if (K <= 4096) {
+        ZG_F8J(4)
+    } else {
+        ZG_F8J(8)
+    }
+#undef ZG_F8J
+#undef ZG_F8
+    return hipGetLastError();
+}
+
+template <int PRO>
+static hipError_t launch_pro(const FusedGemvArgs& a, int type, hipStream_t s) {
+    if (type == kQ4_K) return a.epi == EPI_RESID ? launch_q4k<PRO, EPI_RESID>(a, s) : launch_q4k<PRO, EPI_STORE>(a, s);
+    if (type == kQ8_0) return a.epi == EPI_RESID ? launch_q8<PRO, EPI_RESID>(a, s) : launch_q8<PRO, EPI_STORE>(a, s);
+    return hipErrorInvalidValue;
+}
+
+bool fused_gemv_supported(int type, size_t K, size_t N, int pro) {
+    if (N == 0 || K == 0 || N > (1u << 30)) return false;
+    if (pro == PRO_GATED && (K % 128 || K / 128 > 256 || 256 % (K / 128))) return false;
+    if (K > 8192) return false;  // prologue slabs
+    if (type == kQ4_K) return K % 256 == 0;
+    if (type == kQ8_0) return K % 32 == 0;
+    return false;
+}
+
+hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& args, hipStream_t s) {
+    if (!fused_gemv_supported(w.type, w.K, w.N, args.pro) || args.M <= 0) return hipErrorInvalidValue;
+    if (args.pro == PRO_GATED && args.group != 128) return hipErrorInvalidValue;  // 32 lanes x 4 per group
+    FusedGemvArgs a = args;
+    a.qs = w.qs;
+    a.hdr = w.hdr;
+    a.K = (int)w.K;
+    a.N = (int)w.N;
+    switch (a.pro) {
+    case PRO_RMS: return launch_pro<PRO_RMS>(a, w.type, s);
+    case PRO_GATED: return launch_pro<PRO_GATED>(a, w.type, s);
+    case PRO_SILU_MUL: return launch_pro<PRO_SILU_MUL>(a, w.type, s);
+    case PRO_PLAIN: return launch_pro<PRO_PLAIN>(a, w.type, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// ============================================================ GDN decode
+
+// Grid (H * 4, B), 256 threads: workgroup (h, quarter) owns value columns
+// quarter*32 .. +31 of head h.  The causal conv keeps a 4-slot ring per
+// channel: the token at position p is written to slot p%4 while the taps
+// x[p-3], x[p-2], x[p-1] are read from the other three slots, so the
+// workgroups of one head that all read the q/k channels never race with the
+// one (quarter 0) that writes them.  conv: cpu/src/ops/gdn.rs:7-44 (left to
+// right, no FMA) + SiLU (forward.rs:548); L2, gates and recurrence as
+// gdn_recurrent_kernel<true>.
+__global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
+    constexpr int D = 128;
+    __shared__ float qk[2 * D];
+    __shared__ float vv[32];
+    const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3, b = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int W = a.H * D;
+    const int p = a.pos[b];
+    const int s0 = (p + 1) & 3, s1 = (p + 2) & 3, s2 = (p + 3) & 3, sw = p & 3;
+    const float* xin = a.proj + (size_t)b * a.proj_stride;
+    float* ring = a.ring + (size_t)b * 3 * W * 4;
+    auto conv = [&](int ch) {
+        const v4f r = *(const v4f*)(ring + (size_t)ch * 4);
+        const float hv[4] = {r.x, r.y, r.z, r.w};
+        const v4f w = *(const v4f*)(a.conv_w + (size_t)ch * 4);
+        const float x = xin[ch];
+        const float t0 = hv[s0] * w.x;
+        const float t1 = hv[s1] * w.y;
+        const float t2 = hv[s2] * w.z;
+        const float t3 = x * w.w;
+        float acc = t0 + t1;
+        acc = acc + t2;
+        acc = acc + t3;
+        return acc;
+    };
+    {
+        const int ch = tid < D ? h * D + tid : W + h * D + (tid - D);
+        qk[tid] = ggml_silu(conv(ch));
+        if (quarter == 0) ring[(size_t)ch * 4 + sw] = xin[ch];
+    }
+    if (tid < 32) {
+        const int ch = 2 * W + h * D + quarter * 32 + tid;
+        vv[tid] = ggml_silu(conv(ch));
+        ring[(size_t)ch * 4 + sw] = xin[ch];
+    }
+    __syncthreads();
+
+    const int lane = tid & 63, wv = tid >> 6;
+    const int jl = wv * 8 + (lane >> 3);  // column within the quarter
+    const int j = quarter * 32 + jl;
+    const int s = lane & 7;
+    float q[4][4], k[4][4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            q[c][t] = qk[32 * c + 4 * s + t];
+            k[c][t] = qk[D + 32 * c + 4 * s + t];
+        }
+    // two-stage L2 (forward.rs:564-576)
+    double sq = 0.0, sk = 0.0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float a2 = q[c][t] * q[c][t];
+            const float b2 = k[c][t] * k[c][t];
+            sq += (double)a2;
+            sk += (double)b2;
+        }
+    sq = wave_sum_xor<double>(sq, 8);
+    sk = wave_sum_xor<double>(sk, 8);
+    const float dsq = 1.0f / sqrtf((float)D);
+    const float eps_d = a.eps / (float)D;
+    const float iq = 1.0f / sqrtf((float)(sq / (double)D) + eps_d);
+    const float ik = 1.0f / sqrtf((float)(sk / (double)D) + eps_d);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float tq = q[c][t] * iq;
+            q[c][t] = tq * dsq;
+            const float tk = k[c][t] * ik;
+            k[c][t] = tk * dsq;
+        }
+    float gain, beta, sp, gr;
+    gdn_coef(xin[4 * W + h], xin[4 * W + a.H + h], a.dt[h], a.ssm_a[h], gain, beta, sp, gr);
+    const float vj = vv[jl];
+    float* col = a.state + (((size_t)b * a.H + h) * D + j) * D + 4 * s;
+    float cv[4][4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const v4f v = *(const v4f*)(col + 32 * c);
+        cv[c][0] = v.x * gain; cv[c][1] = v.y * gain; cv[c][2] = v.z * gain; cv[c][3] = v.w * gain;
+    }
+    const float prev = column_dot(cv, k);
+    const float delta = (vj - prev) * beta;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) cv[c][t] = fmaf(k[c][t], delta, cv[c][t]);
+    const float o = column_dot(cv, q);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) *(v4f*)(col + 32 * c) = v4f{cv[c][0], cv[c][1], cv[c][2], cv[c][3]};
+    if (s == 0) a.core[(size_t)b * W + h * D + j] = o * a.scale;
+}
+
+hipError_t gdn_decode(const GdnDecodeArgs& a, size_t B, hipStream_t s) {
+    if (a.H <= 0 || B == 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gdn_decode_kernel, dim3((unsigned)(a.H * 4), (unsigned)B), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+// ===================================================== attention decode
+
+template <typename KV>
+__device__ __forceinline__ float kv_ld(const KV* p);
+template <>
+__device__ __forceinline__ float kv_ld<float>(const float* p) { return *p; }
+template <>
+__device__ __forceinline__ float kv_ld<uint16_t>(const uint16_t* p) { return bf16_to_f32(*p); }
+template <typename KV>
+__device__ __forceinline__ KV kv_st(float v);
+template <>
+__device__ __forceinline__ float kv_st<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ uint16_t kv_st<uint16_t>(float v) {
+    uint32_t b = __float_as_uint(v);
+    b += 0x7fffu + ((b >> 16) & 1u);
+    return (uint16_t)(b >> 16);
+}
+template <typename KV>
+__device__ __forceinline__ void kv_ld4(const KV* p, float (&o)[4]);
+template <>
+__device__ __forceinline__ void kv_ld4<float>(const float* p, float (&o)[4]) {
+    const v4f v = *(const v4f*)p;
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+}
+template <>
+__device__ __forceinline__ void kv_ld4<uint16_t>(const uint16_t* p, float (&o)[4]) {
+    const uint2 v = *(const uint2*)p;
+    o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xffff0000u);
+    o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xffff0000u);
+}
+
+// RoPE of one 256-wide head held in LDS, lanes < 32 of a wave
+// (lib.rs:1552-1577: pairs (i, i+32), angle starts at the position and is
+// multiplied by theta_scale per pair, FMA form).
+__device__ __forceinline__ void head_rope(float* hv, const float* sn, const float* cs, int lane) {
+    if (lane < 32) {
+        const float a = hv[lane], bb = hv[lane + 32];
+        hv[lane] = fmaf(a, cs[lane], -(bb * sn[lane]));
+        hv[lane + 32] = fmaf(a, sn[lane], bb * cs[lane]);
+    }
+}
+
+// Grid (nblk, kv_heads, B).  Each workgroup: (1) issues the key loads of its
+// first token block, (2) normalises (forward.rs:680-695) and ropes
+// (lib.rs:1552-1577) the G query heads of its kv head and the new key (one
+// head per wave, redundant across workgroups: ~1 KB of work), (3) appends
+// K/V at the row's position if it owns that token block, (4) scores its token
+// blocks blockIdx.x, +nblk, ... in the reference's 32-accumulator dot order
+// (see attn_qk_kernel), the position's own token from its copy of the stored
+// key.  The last workgroup of a (row, kv head) to finish (one atomic ticket
+// each, no waiting) reduces the softmax statistics of the G heads
+// (lib.rs:1352-1387: max, GGML exp, 8-wide f32 partials summed in f64,
+// inv = (float)(1/sum)) and resets the ticket.
+template <typename KV, int G>
+__global__ __launch_bounds__(256) void attn_decode_qk_kernel(AttnDecodeArgs a) {
+    constexpr int D = 256;
+    __shared__ float hv[G + 1][D];
+    __shared__ float rsin[32], rcos[32];
+    __shared__ float wmax[4][G];
+    __shared__ double wsum[4][G];
+    __shared__ bool last;
+    const int kvh = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int p = a.pos[b], T = p + 1;
+    const int nblk = gridDim.x;
+    const int s = tid & 7;
+    const float* proj = a.proj + (size_t)b * a.proj_stride;
+    const int QD2 = a.nq * 2 * D;
+    KV* kc = (KV*)a.kcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D;
+    KV* vc = (KV*)a.vcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D;
+    const size_t tstep = (size_t)a.nkv * D;
+
+    float kk[8][4];
+    auto load_keys = [&](int tb) {
+        const int t = tb * 32 + (tid >> 3);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            if (t < T && t != p) {
+                kv_ld4<KV>(kc + (size_t)t * tstep + 32 * c + 4 * s, kk[c]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) kk[c][e] = 0.0f;
+            }
+        }
+    };
+    if (blockIdx.x * 32 < T) load_keys(blockIdx.x);
+
+    // rotation angles of this position, shared by every head
+    if (tid < 32) {
+        float angle = (float)p;
+        for (int t = 0; t < tid; ++t) angle *= a.theta_scale;
+        rsin[tid] = cr_sinf(angle);
+        rcos[tid] = cr_cosf(angle);
+    }
+    // q heads (tasks 0..G-1) and the key (task G): wave w takes tasks w, w+4
+#pragma unroll
+    for (int task0 = 0; task0 <= G; task0 += 4) {
+        const int task = task0 + wv;
+        if (task <= G) {
+            const float* src = task < G ? proj + (size_t)(kvh * G + task) * 2 * D : proj + QD2 + (size_t)kvh * D;
+            const float* gamma = task < G ? a.qnorm : a.knorm;
+            float v[4], gm[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                v[r] = src[lane + 64 * r];
+                gm[r] = gamma[lane + 64 * r];
+            }
+            double sq = 0.0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float q = v[r] * v[r];
+                sq += (double)q;
+            }
+            sq = wave_sum_xor<double>(sq, 64);
+            const float inv = rms_inv(sq, D, a.eps);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float t = v[r] * inv;
+                hv[task][lane + 64 * r] = t * gm[r];
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int task0 = 0; task0 <= G; task0 += 4) {
+        const int task = task0 + wv;
+        if (task <= G) head_rope(hv[task], rsin, rcos, lane);
+    }
+    __syncthreads();
+    {
+        const KV st = kv_st<KV>(hv[G][tid]);
+        if (((p >> 5) % nblk) == (int)blockIdx.x) {
+            const float* vsrc = proj + QD2 + (size_t)a.nkv * D + (size_t)kvh * D;
+            kc[(size_t)p * tstep + tid] = st;
+            vc[(size_t)p * tstep + tid] = kv_st<KV>(vsrc[tid]);
+        }
+        __syncthreads();
+        hv[G][tid] = kv_ld<KV>(&st);
+        __syncthreads();
+    }
+    float qv[G][8][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qv[g][c][e] = hv[g][32 * c + 4 * s + e];
+    float* sb = a.scores + (size_t)b * a.score_stride + (size_t)kvh * G * a.head_stride;
+    bool first = true;
+    for (int tb = blockIdx.x; tb * 32 < T; tb += nblk) {
+        if (!first) load_keys(tb);
+        first = false;
+        const int t = tb * 32 + (tid >> 3);
+        if (t == p) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) kk[c][e] = hv[G][32 * c + 4 * s + e];
+        }
+        float acc[G][4];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[g][e] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(qv[g][c][e], kk[c][e], acc[g][e]);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float v = acc[g][e];
+                v = v + __shfl_xor(v, 4, 64);
+                v = v + __shfl_xor(v, 2, 64);
+                v = v + __shfl_xor(v, 1, 64);
+                acc[g][e] = v;
+            }
+        if (t < T && s == 0) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float dot = (acc[g][0] + acc[g][1]) + (acc[g][2] + acc[g][3]);
+                sb[(size_t)g * a.head_stride + t] = dot * a.scale;
+            }
+        }
+    }
+
+    // ---- softmax statistics by the last workgroup of this (row, kv head):
+    // one release per workgroup (after the barrier) before its ticket
+    __syncthreads();
+    if (tid == 0) {
+        __threadfence();
+        last = atomicAdd(&a.tickets[b * a.nkv + kvh], 1u) == (unsigned)nblk - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    // thread t owns 8-element blocks t, t+256, ... of every head; all loads
+    // of a 4096-token span are issued together
+    float m[G];
+    double sum[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        sum[g] = 0.0;
+    }
+    for (int pass = 0; pass < 2; ++pass) {
+        for (int base = 0; base < T; base += 4096) {
+            float e[G][2][8];
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int at = base + 8 * (tid + 256 * r) + i;
+                        e[g][r][i] = at < T ? sb[(size_t)g * a.head_stride + at] : -INFINITY;
+                    }
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    if (pass == 0) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) m[g] = fmaxf(m[g], e[g][r][i]);
+                    } else if (base + 8 * (tid + 256 * r) < T) {
+                        float x[8];
+#pragma unroll
+                        for (int i = 0; i < 8; ++i)
+                            x[i] = base + 8 * (tid + 256 * r) + i < T ? ggml_exp(e[g][r][i] - m[g]) : 0.0f;
+                        const float partial = ((x[0] + x[4]) + (x[2] + x[6])) + ((x[1] + x[5]) + (x[3] + x[7]));
+                        sum[g] += (double)partial;
+                    }
+                }
+        }
+        if (pass == 0) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float v = wave_max(m[g]);
+                if (lane == 0) wmax[wv][g] = v;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int g = 0; g < G; ++g) m[g] = fmaxf(fmaxf(wmax[0][g], wmax[1][g]), fmaxf(wmax[2][g], wmax[3][g]));
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const double v = wave_sum_xor<double>(sum[g], 64);
+        if (lane == 0) wsum[wv][g] = v;
+    }
+    __syncthreads();
+    if (tid < G) {
+        const int g = tid;
+        const double total = (wsum[0][g] + wsum[1][g]) + (wsum[2][g] + wsum[3][g]);
+        const int h = kvh * G + g;
+        a.stats[((size_t)b * a.nq + h) * 2] = m[g];
+        a.stats[((size_t)b * a.nq + h) * 2 + 1] = (float)(1.0 / total);
+        if (!(total >= 1.0) || !(total < INFINITY)) atomicOr(a.status, 8);
+    }
+    if (tid == 0) a.tickets[b * a.nkv + kvh] = 0u;
+}
+
+// Grid (256/8, kv_heads, B): the value sum of attn_pv_kernel (32 FMA chains
+// over tokens per channel, lib.rs:1276-1305) for the G query heads of one kv
+// head, per 2048-token tile: the tile's values and scores are loaded in one
+// go, p = GGML exp(score - max) * inv is staged in LDS, then the chains run;
+// the fixed tree and the sigmoid output gate (forward.rs:751) finish.
+template <typename KV, int G>
+__global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
+    constexpr int D = 256, TT = 2048, NV = TT / 32;
+    __shared__ float pt[G][TT];
+    __shared__ float red[G][8][33];
+    const int kvh = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int T = a.pos[b] + 1;
+    const float* sb = a.scores + (size_t)b * a.score_stride + (size_t)kvh * G * a.head_stride;
+    float mx[G], inv[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        mx[g] = a.stats[((size_t)b * a.nq + kvh * G + g) * 2];
+        inv[g] = a.stats[((size_t)b * a.nq + kvh * G + g) * 2 + 1];
+    }
+    const int ch = lane >> 3, acc_id = wv * 8 + (lane & 7);
+    const int j = blockIdx.x * 8 + ch;
+    const KV* vb = (const KV*)a.vcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D + j;
+    const size_t vstep = (size_t)a.nkv * D;
+    float acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+    for (int t0 = 0; t0 < T; t0 += TT) {
+        float vv[NV];
+#pragma unroll
+        for (int n = 0; n < NV; ++n) {
+            const int t = t0 + acc_id + 32 * n;
+            vv[n] = t < T ? kv_ld<KV>(vb + (size_t)t * vstep) : 0.0f;
+        }
+        float sv[G * TT / 256];
+#pragma unroll
+        for (int r = 0; r < G * TT / 256; ++r) {
+            const int i = tid + 256 * r, g = i / TT, t = t0 + i % TT;
+            sv[r] = t < T ? sb[(size_t)g * a.head_stride + t] : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < G * TT / 256; ++r) {
+            const int i = tid + 256 * r, g = i / TT, tt = i % TT;
+            pt[g][tt] = t0 + tt < T ? ggml_exp(sv[r] - mx[g]) * inv[g] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int n = 0; n < NV; ++n) {
+            const int tt = acc_id + 32 * n;
+            if (t0 + tt < T) {
+#pragma unroll
+                for (int g = 0; g < G; ++g) acc[g] = fmaf(vv[n], pt[g][tt], acc[g]);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) red[g][ch][acc_id] = acc[g];
+    __syncthreads();
+    if (tid < G * 8) {
+        const int g = tid >> 3, c = tid & 7;
+        const float* r = red[g][c];
+        float comb[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) comb[l] = (r[l] + r[16 + l]) + (r[8 + l] + r[24 + l]);
+        const float h0 = comb[0] + comb[4], h1 = comb[1] + comb[5], h2 = comb[2] + comb[6], h3 = comb[3] + comb[7];
+        float v = (h0 + h1) + (h2 + h3);
+        const int jj = blockIdx.x * 8 + c, h = kvh * G + g;
+        const float gate = a.proj[(size_t)b * a.proj_stride + (size_t)h * 2 * D + D + jj];
+        v = v * source_sigmoid(gate);
+        a.out[(size_t)b * a.out_stride + (size_t)h * D + jj] = v;
+    }
+}
+
+template <typename KV, int G>
+static void launch_attn(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
+    const unsigned nblk = (unsigned)std::min<size_t>((a.max_ctx + 31) / 32, 64);
+    hipLaunchKernelGGL((attn_decode_qk_kernel<KV, G>), dim3(nblk, a.nkv, (unsigned)B), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((attn_decode_pv_kernel<KV, G>), dim3(256 / 8, a.nkv, (unsigned)B), dim3(256), 0, s, a);
+}
+
+hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
+    if (a.nkv <= 0 || a.nq % a.nkv || B == 0 || a.max_ctx <= 0) return hipErrorInvalidValue;
+    const int G = a.nq / a.nkv;
+#define ZG_AT(KV)                                              \
+    switch (G) {                                               \
+    case 1: launch_attn<KV, 1>(a, B, s); break;                \
+    case 2: launch_attn<KV, 2>(a, B, s); break;                \
+    case 3: launch_attn<KV, 3>(a, B, s); break;                \
+    case 4: launch_attn<KV, 4>(a, B, s); break;                \
+    default: return hipErrorInvalidValue;                      \
+    }
+    if (a.kv_bf16) {
+        ZG_AT(uint16_t)
+    } else {
+        ZG_AT(float)
+    }
+#undef ZG_AT
+    return hipGetLastError();
+}
+
+// ================================================== greedy + position
+
+// Grid (kArgBlocks, B).  Each workgroup reduces its slice of the row to
+// (max, first index); the last workgroup to finish a row (one atomic
+// ticket per workgroup, no waiting) reduces the partials, writes the greedy
+// id (core/src/numerics.rs:126-140: first maximum wins, nonfinite is an
+// error -> status bit 2), resets the row's ticket for the next step and,
+// when asked, moves the row's position on.
+constexpr int kArgBlocks = 32;
+
+__global__ __launch_bounds__(256) void argmax_step_kernel(const float* __restrict__ logits, int V, size_t ld,
+                                                          uint32_t* __restrict__ greedy, int* __restrict__ status,
+                                                          float* __restrict__ pmax, int* __restrict__ pidx,
+                                                          unsigned* __restrict__ tickets, int* __restrict__ pos,
+                                                          int* __restrict__ ntok, int advance) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    __shared__ bool last;
+    const int blk = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int per = (V + kArgBlocks - 1) / kArgBlocks;
+    const int lo = blk * per, hi = min(V, lo + per);
+    const float* row = logits + (size_t)b * ld;
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    bool bad = false;
+    for (int i = lo + tid; i < hi; i += 256) {
+        const float v = row[i];
+        if (!finite_f32(v)) bad = true;
+        if (v > best) {
+            best = v;
+            bi = i;
+        }
+    }
+    if (bad) atomicOr(status, 4);
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (ov > best || (ov == best && oi < bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        sv[wv] = best;
+        si[wv] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
+                best = sv[w];
+                bi = si[w];
+            }
+        pmax[b * kArgBlocks + blk] = best;
+        pidx[b * kArgBlocks + blk] = bi;
+        __threadfence();
+        last = atomicAdd(&tickets[b], 1u) == kArgBlocks - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    if (tid < 64) {
+        float m = tid < kArgBlocks ? __hip_atomic_load(&pmax[b * kArgBlocks + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
+        int mi = tid < kArgBlocks ? __hip_atomic_load(&pidx[b * kArgBlocks + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0x7fffffff;
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(m, off, 64);
+            const int oi = __shfl_xor(mi, off, 64);
+            if (ov > m || (ov == m && oi < mi)) {
+                m = ov;
+                mi = oi;
+            }
+        }
+        if (tid == 0) {
+            greedy[b] = mi == 0x7fffffff ? 0u : (uint32_t)mi;
+            tickets[b] = 0u;
+            if (advance) {
+                const int np = pos[b] + 1;
+                pos[b] = np;
+                ntok[b] = np + 1;
+            }
+        }
+    }
+}
+
+hipError_t argmax_step(const float* logits, size_t V, size_t ld, size_t B, uint32_t* greedy, int* status, float* pmax,
+                       int* pidx, unsigned* tickets, int* pos, int* ntok, int advance, hipStream_t s) {
+    hipLaunchKernelGGL(argmax_step_kernel, dim3(kArgBlocks, (unsigned)B), dim3(256), 0, s, logits, (int)V, ld, greedy,
+                       status, pmax, pidx, tickets, pos, ntok, advance);
+    return hipGetLastError();
+}
+
+size_t argmax_partials(size_t B) { return B * kArgBlocks; }
+
+}  // namespace zg

@@ -57,14 +57,6 @@ hipError_t gdn_conv(const float* x, const float* w, float* hist, float* out, siz
 
 // ---------------------------------------------------------- coefficients
 
-__device__ __forceinline__ void gdn_coef(float alpha, float beta_p, float dt, float a, float& gain, float& beta,
-                                         float& sp, float& gate_raw) {
-    const float biased = alpha + dt;
-    sp = source_softplus(biased);
-    gate_raw = sp * a;
-    gain = cr_expf(gate_raw);
-    beta = source_sigmoid(beta_p);
-}
 
 __global__ void gdn_coef_kernel(const float* __restrict__ alpha, const float* __restrict__ beta,
                                 const float* __restrict__ dt, const float* __restrict__ a, int H,
@@ -88,33 +80,6 @@ hipError_t gdn_coefficients(const float* alpha, const float* beta, const float* 
 }
 
 // ------------------------------------------------------------- recurrence
-
-// Eight lanes own one value column j.  The reference dot (source_dot_f32,
-// model-qwen35/src/lib.rs:1394-1423) keeps 32 f32 accumulators, accumulator
-// a = 8i + l taking elements a, a+32, a+64, a+96 in that order, then reduces
-// combined[l] = (s[0][l]+s[2][l]) + (s[1][l]+s[3][l]),
-// halves[m] = combined[m] + combined[m+4], (h0+h1)+(h2+h3).
-// Lane s of the column holds accumulators 4s..4s+3, i.e. elements
-// 32c + 4s + t (c, t in 0..3): one float4 per c, coalesced across the 8
-// lanes.  XOR-4 then XOR-2 shuffles form `combined`, XOR-1 forms `halves`
-// and the last two levels are local: the dot is bit-identical to the CPU.
-__device__ __forceinline__ float column_dot(const float (&a)[4][4], const float (&b)[4][4]) {
-    float acc[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        float v = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) v = fmaf(a[c][t], b[c][t], v);
-        acc[t] = v;
-    }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        acc[t] = acc[t] + __shfl_xor(acc[t], 4, 64);
-        acc[t] = acc[t] + __shfl_xor(acc[t], 2, 64);
-        acc[t] = acc[t] + __shfl_xor(acc[t], 1, 64);
-    }
-    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
-}
 
 // Grid: x = heads * (d/8) / 4 workgroups of 4 waves, y = rows.  Wave w of
 // the grid owns columns j0..j0+7 of one head (lane = (j - j0) * 8 + s).

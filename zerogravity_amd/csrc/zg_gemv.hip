@@ -60,28 +60,6 @@ __device__ __forceinline__ void q4k_scale_min(const uint8_t* s, int g, uint32_t&
     }
 }
 
-// Q4_K header relayout.  GGUF packs 8 six-bit scales and 8 six-bit mins into
-// 12 bytes (codecs/q4.rs:58-65), which forces a lane-dependent multi-byte
-// gather per group.  The device header keeps d and dmin (bytes 0-3) and
-// stores the four values of group pair p (sc[2p], mn[2p], sc[2p+1],
-// mn[2p+1]) in byte p of dwords 1..3:
-//   dw1.byte[p] = sc[2p]   | (mn[2p+1] & 3) << 6
-//   dw2.byte[p] = mn[2p]   | ((mn[2p+1] >> 2) & 3) << 6
-//   dw3.byte[p] = sc[2p+1] | ((mn[2p+1] >> 4) & 3) << 6
-// so a lane decodes its pair with three fixed-offset byte extracts.  The
-// mapping is a bijection of the same 96 bits: no information is added or lost.
-__device__ __forceinline__ void q4k_dev_scale_min(const v4u h, int g, uint32_t& sc, uint32_t& mn) {
-    const int sh = 8 * (g >> 1);
-    const uint32_t b1 = (h.y >> sh) & 0xffu, b2 = (h.z >> sh) & 0xffu, b3 = (h.w >> sh) & 0xffu;
-    if ((g & 1) == 0) {
-        sc = b1 & 63;
-        mn = b2 & 63;
-    } else {
-        sc = b3 & 63;
-        mn = (b1 >> 6) | ((b2 >> 6) << 2) | ((b3 >> 6) << 4);
-    }
-}
-
 __global__ void repack_q4k_kernel(const v4i* __restrict__ src, v4i* __restrict__ qs, v4u* __restrict__ hdr,
                                   size_t nblocks, int* bad) {
     size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;

@@ -116,4 +116,82 @@ hipError_t convert_kv(const void* in, void* out, size_t n, bool to_f32, hipStrea
 hipError_t fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
 hipError_t advance_positions(int* pos, int* ntok, size_t B, hipStream_t s);  // B <= 64
 
+// ---------------------------------------------------- fused decode step
+// (zg_decode.hip).  A GEMV launch with an activation prologue and an output
+// epilogue:
+//   PRO_RMS       x[m][0:K] -> (x*inv)*gamma            (RMSNorm, eps)
+//   PRO_GATED     per group of `group` elements: ((x*inv)*gamma[i % group])
+//                 * silu(x2)                            (gated RMSNorm)
+//   PRO_SILU_MUL  x2 * silu(x)                          (x = gate, x2 = up)
+//   PRO_PLAIN     x
+//   EPI_STORE     y[m][n] = W a
+//   EPI_RESID     y[m][n] += W a, nonfinite -> status bit 0
+enum { PRO_RMS = 0, PRO_GATED = 1, PRO_SILU_MUL = 2, PRO_PLAIN = 3 };
+enum { EPI_STORE = 0, EPI_RESID = 1 };
+struct FusedGemvArgs {
+    const void* qs = nullptr;  // filled from the weight
+    const void* hdr = nullptr;
+    int N = 0, K = 0;
+    int M = 0;  // activation rows
+    int pro = PRO_PLAIN, epi = EPI_STORE;
+    const float* x = nullptr;
+    size_t ldx = 0;
+    const float* x2 = nullptr;
+    size_t ldx2 = 0;
+    const float* gamma = nullptr;
+    float eps = 0.0f;
+    int group = 128;
+    float* y = nullptr;
+    size_t ldy = 0;
+    int* status = nullptr;
+};
+bool fused_gemv_supported(int type, size_t K, size_t N, int pro);
+hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& a, hipStream_t s);
+
+// GDN decode: conv (4-slot ring per channel) + SiLU + q/k L2 + gates +
+// recurrence for B rows.  proj rows: [qkv (3W) | z (W) | alpha (H) | beta (H)].
+struct GdnDecodeArgs {
+    const float* proj = nullptr;
+    size_t proj_stride = 0;
+    const float* conv_w = nullptr;  // [3W][4]
+    float* ring = nullptr;          // [B][3W][4]
+    const int* pos = nullptr;       // [B] position of this step's token
+    const float *dt = nullptr, *ssm_a = nullptr;
+    float eps = 0.0f, scale = 0.0f;
+    float* state = nullptr;  // [B][H][128][128] value-major
+    float* core = nullptr;   // [B][W]
+    int H = 0;
+};
+hipError_t gdn_decode(const GdnDecodeArgs& a, size_t B, hipStream_t s);
+
+// Attention decode (d = 256): proj rows [q|gate per head (nq*2d) | k (nkv*d)
+// | v (nkv*d)]; KV cache [B][max_ctx][nkv*d]; scores at
+// b*score_stride + h*head_stride + t; out [B][nq*d] (gated).
+struct AttnDecodeArgs {
+    const float* proj = nullptr;
+    size_t proj_stride = 0;
+    const float *qnorm = nullptr, *knorm = nullptr;
+    float eps = 0.0f, theta_scale = 0.0f, scale = 0.0f;
+    const int* pos = nullptr;
+    void *kcache = nullptr, *vcache = nullptr;
+    size_t cache_row_stride = 0;
+    int kv_bf16 = 0;
+    float* scores = nullptr;
+    size_t score_stride = 0, head_stride = 0;
+    float* out = nullptr;
+    size_t out_stride = 0;
+    int* status = nullptr;      // bit 3: degenerate softmax sum
+    unsigned* tickets = nullptr;  // [B][nkv], zero between steps
+    float* stats = nullptr;       // [B][nq][2] softmax max, 1/sum
+    int nq = 0, nkv = 0, max_ctx = 0;
+};
+hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s);
+
+// Greedy ids of B logit rows (leading dimension ld) with a per-row ticket
+// (tickets[B], zero between steps) and partials [argmax_partials(B)]; when
+// `advance`, the last workgroup of a row also moves pos/ntok on.
+size_t argmax_partials(size_t B);
+hipError_t argmax_step(const float* logits, size_t V, size_t ld, size_t B, uint32_t* greedy, int* status, float* pmax,
+                       int* pidx, unsigned* tickets, int* pos, int* ntok, int advance, hipStream_t s);
+
 }  // namespace zg

@@ -50,4 +50,42 @@ __device__ __forceinline__ float source_softplus(float x) {
     return cr_logf(1.0f + cr_expf(x));
 }
 
+// GDN gates, lib.rs:339-362: sp = softplus(alpha + dt), gate_raw = sp * a,
+// gain = exp(gate_raw), beta = sigmoid(beta projection).
+__device__ __forceinline__ void gdn_coef(float alpha, float beta_p, float dt, float a, float& gain, float& beta,
+                                         float& sp, float& gate_raw) {
+    const float biased = alpha + dt;
+    sp = source_softplus(biased);
+    gate_raw = sp * a;
+    gain = cr_expf(gate_raw);
+    beta = source_sigmoid(beta_p);
+}
+
+// Eight lanes own one value column j.  The reference dot (source_dot_f32,
+// model-qwen35/src/lib.rs:1394-1423) keeps 32 f32 accumulators, accumulator
+// a = 8i + l taking elements a, a+32, a+64, a+96 in that order, then reduces
+// combined[l] = (s[0][l]+s[2][l]) + (s[1][l]+s[3][l]),
+// halves[m] = combined[m] + combined[m+4], (h0+h1)+(h2+h3).
+// Lane s of the column holds accumulators 4s..4s+3, i.e. elements
+// 32c + 4s + t (c, t in 0..3): one float4 per c, coalesced across the 8
+// lanes.  XOR-4 then XOR-2 shuffles form `combined`, XOR-1 forms `halves`
+// and the last two levels are local: the dot is bit-identical to the CPU.
+__device__ __forceinline__ float column_dot(const float (&a)[4][4], const float (&b)[4][4]) {
+    float acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        float v = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v = fmaf(a[c][t], b[c][t], v);
+        acc[t] = v;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        acc[t] = acc[t] + __shfl_xor(acc[t], 4, 64);
+        acc[t] = acc[t] + __shfl_xor(acc[t], 2, 64);
+        acc[t] = acc[t] + __shfl_xor(acc[t], 1, 64);
+    }
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+}
+
 }  // namespace zg

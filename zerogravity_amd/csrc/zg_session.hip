@@ -1,9 +1,23 @@
-// Boundary B: resident Qwen3.5 hybrid model + decode sessions, and the GDN /
-// attention boundary-A regions.  See zg_model.hip for the per-step schedule.
+// Boundary B: the resident Qwen3.5 hybrid model and its decode sessions
+// (the reference's LoadedQwenModel + QwenDenseCpu, model-qwen35/src/
+// lib.rs:386-507,1058-1254, with the per-token schedule of forward.rs:451-755).
+//
+// Weights that share an input are registered as one matrix with their rows
+// stacked (GGUF rows are independent, so the outputs are unchanged):
+//   GDN in-proj  = [attn_qkv | attn_gate | ssm_alpha | ssm_beta]
+//   attn in-proj = [attn_q | attn_k | attn_v]
+//   FFN          = [ffn_gate | ffn_up]
+// A decode step is then 5 launches per GDN layer, 6 per attention layer and
+// 3 around them (zg_decode.hip), replayed as one HIP graph per
+// (rows, token/logit/greedy buffers): every kernel reads positions from
+// device memory, so the captured step is valid at any position.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
+#include <map>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "zg_context.hpp"
@@ -14,9 +28,7 @@ namespace {
 
 struct LayerW {
     bool full = false;
-    zg_weight *qkv = nullptr, *gate = nullptr, *alpha = nullptr, *beta = nullptr, *ssm_out = nullptr;
-    zg_weight *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr;
-    zg_weight *ffn_gate = nullptr, *ffn_up = nullptr, *ffn_down = nullptr;
+    zg_weight *in_proj = nullptr, *out_proj = nullptr, *ffn_gu = nullptr, *ffn_down = nullptr;
     float *attn_norm = nullptr, *post_norm = nullptr, *conv_w = nullptr, *ssm_norm = nullptr, *ssm_a = nullptr,
           *ssm_dt = nullptr, *q_norm = nullptr, *k_norm = nullptr;
 };
@@ -41,22 +53,19 @@ struct zg_session {
     std::vector<int> pos;  // host copy of each row's next position
     bool poisoned = false;
     bool pos_dirty = true;  // device positions must be re-uploaded from pos
+    bool use_graphs = true;
     // device buffers
     std::vector<void*> allocs;
-    int *d_pos = nullptr, *d_ntok = nullptr, *d_status = nullptr;
+    int *d_pos = nullptr, *d_ntok = nullptr, *d_status = nullptr, *pidx = nullptr;
+    unsigned *tickets = nullptr, *att_tickets = nullptr;
     uint32_t *d_tokens = nullptr, *d_greedy = nullptr;
-    float *x = nullptr, *y0 = nullptr, *y1 = nullptr, *y2 = nullptr, *y3 = nullptr, *mixed = nullptr, *core = nullptr,
-          *gated = nullptr, *out = nullptr, *logits = nullptr, *qr = nullptr, *scores = nullptr, *probs = nullptr;
-    void* prep = nullptr;
-    size_t prep_bytes = 0, y0w = 0, y1w = 0, y2w = 0, gatedw = 0;
-    std::vector<float*> conv, rec;   // per GDN layer
-    std::vector<void*> kc, vc;       // per attention layer
-    std::vector<int> layer_slot;     // layer -> index into conv/rec or kc/vc
-    // prepared-activation memo for one step
-    const void* prep_src = nullptr;
-    const float* prep_gamma = nullptr;
-    int prep_type = -1;
-    size_t prep_rows = 0;
+    float *x = nullptr, *y0 = nullptr, *core = nullptr, *ao = nullptr, *logits = nullptr, *scores = nullptr,
+          *pmax = nullptr, *att_stats = nullptr;
+    size_t y0w = 0;
+    std::vector<float*> ring, rec;  // per GDN layer: conv ring [B][3W][4], state [B][H][128][128]
+    std::vector<void*> kc, vc;      // per attention layer: [B][max_ctx][kv_heads*256]
+    std::vector<int> layer_slot;    // layer -> index into ring/rec or kc/vc
+    std::map<std::tuple<size_t, const void*, const void*, const void*>, hipGraphExec_t> graphs;
 };
 
 namespace {
@@ -69,17 +78,40 @@ const zg_tensor_desc* find_tensor(const zg_tensor_desc* t, size_t n, const std::
 
 std::string lname(unsigned i, const char* suffix) { return "blk." + std::to_string(i) + "." + suffix; }
 
-int load_matrix(zg_model* m, const zg_tensor_desc* ts, size_t n, const std::string& name, uint64_t K, uint64_t N,
-                zg_weight** out) {
+// Rows of several [K, N_i] GGUF matrices stacked into one registered weight.
+int load_stacked(zg_model* m, const zg_tensor_desc* ts, size_t n, const std::vector<std::string>& names, uint64_t K,
+                 const std::vector<uint64_t>& Ns, const std::string& key, int pro, zg_weight** out) {
     zg_ctx* ctx = m->ctx;
-    const zg_tensor_desc* t = find_tensor(ts, n, name);
-    if (!t) return fail(ctx, ZG_E_MALFORMED, "missing tensor " + name);
-    if (t->shape0 != K || t->shape1 != N)
-        return fail(ctx, ZG_E_MALFORMED, "tensor " + name + " geometry differs from the model configuration");
-    int rc = check_matrix(ctx, t->ggml_type, K, N, t->data, t->nbytes);
-    if (rc == ZG_UNSUPPORTED) return fail(ctx, ZG_E_UNSUPPORTED, "tensor " + name + ": " + ctx->err);
-    if (rc) return rc;
-    return lookup_or_register(ctx, m->source, name.c_str(), t->ggml_type, K, N, t->data, t->nbytes, out);
+    int type = -1;
+    uint64_t rows = 0;
+    size_t bytes = 0;
+    std::vector<const zg_tensor_desc*> parts;
+    for (size_t i = 0; i < names.size(); ++i) {
+        const zg_tensor_desc* t = find_tensor(ts, n, names[i]);
+        if (!t) return fail(ctx, ZG_E_MALFORMED, "missing tensor " + names[i]);
+        if (t->shape0 != K || t->shape1 != Ns[i])
+            return fail(ctx, ZG_E_MALFORMED, "tensor " + names[i] + " geometry differs from the model configuration");
+        int rc = check_matrix(ctx, t->ggml_type, K, Ns[i], t->data, t->nbytes);
+        if (rc == ZG_UNSUPPORTED) return fail(ctx, ZG_E_UNSUPPORTED, "tensor " + names[i] + ": " + ctx->err);
+        if (rc) return rc;
+        if (type >= 0 && t->ggml_type != type)
+            return fail(ctx, ZG_E_UNSUPPORTED, "tensors stacked with " + names[0] + " must share its codec");
+        type = t->ggml_type;
+        rows += Ns[i];
+        bytes += t->nbytes;
+        parts.push_back(t);
+    }
+    if (!zg::fused_gemv_supported(type, K, rows, pro))
+        return fail(ctx, ZG_E_UNSUPPORTED, "resident decode needs Q8_0/Q4_K projections (" + names[0] + ")");
+    if (parts.size() == 1)
+        return lookup_or_register(ctx, m->source, key.c_str(), type, K, rows, parts[0]->data, parts[0]->nbytes, out);
+    std::vector<uint8_t> buf(bytes);
+    size_t at = 0;
+    for (const zg_tensor_desc* t : parts) {
+        memcpy(buf.data() + at, t->data, t->nbytes);
+        at += t->nbytes;
+    }
+    return lookup_or_register(ctx, m->source, key.c_str(), type, K, rows, buf.data(), bytes, out);
 }
 
 int load_vector(zg_model* m, const zg_tensor_desc* ts, size_t n, const std::string& name, uint64_t len, float** out) {
@@ -105,108 +137,130 @@ int dalloc(zg_session* s, void** p, size_t bytes) {
     return ZG_COMPLETED;
 }
 
-size_t conv_floats(const zg_geometry& g) { return (size_t)g.gdn_heads * g.gdn_dim * 3 * 3; }
+size_t conv_floats(const zg_geometry& g) { return (size_t)g.gdn_heads * g.gdn_dim * 3 * 3; }  // exported history
+size_t ring_floats(const zg_geometry& g) { return (size_t)g.gdn_heads * g.gdn_dim * 3 * 4; }  // device ring
 size_t rec_floats(const zg_geometry& g) { return (size_t)g.gdn_heads * g.gdn_dim * g.gdn_dim; }
 size_t kvw(const zg_geometry& g) { return (size_t)g.kv_heads * g.head_dim; }
 
-// Prepare the activation of `src` for weight w (RMS with gamma when given),
-// reusing the previous preparation when source, gamma, codec and rows match.
-int project(zg_session* s, zg_weight* w, const float* src, const float* gamma, float* y, size_t B, hipStream_t st) {
-    zg_ctx* ctx = s->m->ctx;
-    if (!(s->prep_src == src && s->prep_gamma == gamma && s->prep_type == w->dw.type && s->prep_rows == B)) {
-        ZG_HIP(zg::act_prepare_for(w->dw.type, src, 0, B, w->dw.K, gamma, s->m->g.eps, s->prep, st));
-        s->prep_src = src;
-        s->prep_gamma = gamma;
-        s->prep_type = w->dw.type;
-        s->prep_rows = B;
-    }
-    ZG_HIP(zg::gemv(w->dw, B, s->prep, y, st));
-    return ZG_COMPLETED;
-}
-
-void invalidate_prep(zg_session* s) { s->prep_src = nullptr; }
-
-// One decode step for rows [0, B): tokens already in s->d_tokens, positions
-// in s->d_pos / s->d_ntok.  Logits land in s->logits, greedy ids in
-// s->d_greedy.  Asynchronous on st.
+// One decode step for rows [0, B): tokens in `tokens` (device), positions in
+// d_pos / d_ntok.  Logits to `logits` (may be the session buffer), greedy
+// ids to `greedy` (nullable); positions advance on the device as the last
+// launch.  Asynchronous on st, no host synchronisation, capturable.
 int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_t* greedy, hipStream_t st) {
     zg_model* m = s->m;
     zg_ctx* ctx = m->ctx;
     const zg_geometry& g = m->g;
-    const size_t H = g.hidden, F = g.ffn, W = (size_t)g.gdn_heads * g.gdn_dim;
-    int rc;
-    invalidate_prep(s);
+    const size_t H = g.hidden, F = g.ffn, V = g.vocab, W = (size_t)g.gdn_heads * g.gdn_dim;
+    const size_t QD = (size_t)g.q_heads * g.head_dim;
+    auto gemv = [&](zg_weight* w, int pro, const float* x, size_t ldx, const float* x2, size_t ldx2,
+                    const float* gamma, int epi, float* y, size_t ldy) {
+        zg::FusedGemvArgs f;
+        f.M = (int)B;
+        f.pro = pro;
+        f.epi = epi;
+        f.x = x;
+        f.ldx = ldx;
+        f.x2 = x2;
+        f.ldx2 = ldx2;
+        f.gamma = gamma;
+        f.eps = g.eps;
+        f.group = (int)g.gdn_dim;
+        f.y = y;
+        f.ldy = ldy;
+        f.status = s->d_status;
+        return zg::fused_gemv(w->dw, f, st);
+    };
     ZG_HIP(zg::embed(m->embd->dw, tokens, s->x, B, s->d_status, st));
     for (size_t i = 0; i < m->layers.size(); ++i) {
         LayerW& L = m->layers[i];
         const int slot = s->layer_slot[i];
+        ZG_HIP(gemv(L.in_proj, zg::PRO_RMS, s->x, H, nullptr, 0, L.attn_norm, zg::EPI_STORE, s->y0, s->y0w));
         if (!L.full) {
-            if ((rc = project(s, L.qkv, s->x, L.attn_norm, s->y0, B, st))) return rc;
-            if ((rc = project(s, L.gate, s->x, L.attn_norm, s->y1, B, st))) return rc;
-            if ((rc = project(s, L.alpha, s->x, L.attn_norm, s->y2, B, st))) return rc;
-            if ((rc = project(s, L.beta, s->x, L.attn_norm, s->y3, B, st))) return rc;
-            ZG_HIP(zg::gdn_conv(s->y0, L.conv_w, s->conv[slot], s->mixed, 3 * W, B, 1, 3 * W, 3 * W * 3, 3 * W, st));
-            ZG_HIP(zg::gdn_recurrent(true, s->mixed, s->mixed + W, s->mixed + 2 * W, 3 * W, s->y2, s->y3, g.gdn_heads,
-                                     L.ssm_dt, L.ssm_a, g.eps, 1.0f / sqrtf((float)g.gdn_dim), nullptr, s->rec[slot],
-                                     s->core, W, g.gdn_heads, g.gdn_dim, B, st));
-            // grouped RMS over heads with ssm_norm, then normalized * silu(z)
-            ZG_HIP(zg::rms_groups(s->core, L.ssm_norm, g.gdn_dim, B * g.gdn_heads, g.eps, s->gated, st));
-            ZG_HIP(zg::silu(s->y1, s->gated, B * W, s->gated, st));
-            if ((rc = project(s, L.ssm_out, s->gated, nullptr, s->out, B, st))) return rc;
+            zg::GdnDecodeArgs d;
+            d.proj = s->y0;
+            d.proj_stride = s->y0w;
+            d.conv_w = L.conv_w;
+            d.ring = s->ring[slot];
+            d.pos = s->d_pos;
+            d.dt = L.ssm_dt;
+            d.ssm_a = L.ssm_a;
+            d.eps = g.eps;
+            d.scale = 1.0f / sqrtf((float)g.gdn_dim);
+            d.state = s->rec[slot];
+            d.core = s->core;
+            d.H = (int)g.gdn_heads;
+            ZG_HIP(zg::gdn_decode(d, B, st));
+            // gated RMSNorm (ssm_norm) * silu(z) -> ssm_out -> residual
+            ZG_HIP(gemv(L.out_proj, zg::PRO_GATED, s->core, W, s->y0 + 3 * W, s->y0w, L.ssm_norm, zg::EPI_RESID, s->x,
+                        H));
         } else {
-            if ((rc = project(s, L.wq, s->x, L.attn_norm, s->y0, B, st))) return rc;
-            if ((rc = project(s, L.wk, s->x, L.attn_norm, s->y1, B, st))) return rc;
-            if ((rc = project(s, L.wv, s->x, L.attn_norm, s->y2, B, st))) return rc;
-            zg::AttnArgs a;
-            a.B = (int)B;
-            a.nq = (int)g.q_heads;
-            a.nkv = (int)g.kv_heads;
-            a.d = (int)g.head_dim;
-            a.rotate = 64;
-            a.tmax = (int)s->max_ctx;
-            a.kv_bf16 = s->kv_bf16;
-            a.do_prep = 1;
-            a.qproj = s->y0;
-            a.q_stride = 2 * (size_t)g.q_heads * g.head_dim;  // compact GEMV output of attn_q
-            a.kproj = s->y1;
-            a.vproj = s->y2;
-            a.kv_stride = kvw(g);
+            zg::AttnDecodeArgs a;
+            a.proj = s->y0;
+            a.proj_stride = s->y0w;
             a.qnorm = L.q_norm;
             a.knorm = L.k_norm;
-            a.pos = s->d_pos;
-            a.ntok = s->d_ntok;
-            a.theta_scale = powf(10000000.0f, -2.0f / 64.0f);
             a.eps = g.eps;
+            a.theta_scale = powf(10000000.0f, -2.0f / 64.0f);
             a.scale = 1.0f / sqrtf((float)g.head_dim);
-            a.qr = s->qr;
-            a.qr_stride = (size_t)g.q_heads * g.head_dim;
+            a.pos = s->d_pos;
             a.kcache = s->kc[slot];
             a.vcache = s->vc[slot];
             a.cache_row_stride = s->max_ctx * kvw(g);
+            a.kv_bf16 = s->kv_bf16;
             a.scores = s->scores;
-            a.probs = s->probs;
             a.score_stride = (size_t)g.q_heads * s->max_ctx;
-            int maxpos = 0;
-            for (size_t b = 0; b < B; ++b) maxpos = std::max(maxpos, s->pos[b] + 1);
-            a.tmax = maxpos;
-            a.gate = s->y0;
-            a.gate_stride = 2 * (size_t)g.q_heads * g.head_dim;
-            a.out = s->gated;
-            a.out_stride = (size_t)g.q_heads * g.head_dim;
-            ZG_HIP(zg::attention(a, st));
-            if ((rc = project(s, L.wo, s->gated, nullptr, s->out, B, st))) return rc;
+            a.head_stride = s->max_ctx;
+            a.out = s->ao;
+            a.out_stride = QD;
+            a.status = s->d_status;
+            a.tickets = s->att_tickets;
+            a.stats = s->att_stats;
+            a.nq = (int)g.q_heads;
+            a.nkv = (int)g.kv_heads;
+            a.max_ctx = (int)s->max_ctx;
+            ZG_HIP(zg::attn_decode(a, B, st));
+            ZG_HIP(gemv(L.out_proj, zg::PRO_PLAIN, s->ao, QD, nullptr, 0, nullptr, zg::EPI_RESID, s->x, H));
         }
-        ZG_HIP(zg::residual_add(s->x, s->out, B * H, s->d_status, st));
-        if ((rc = project(s, L.ffn_gate, s->x, L.post_norm, s->y0, B, st))) return rc;
-        if ((rc = project(s, L.ffn_up, s->x, L.post_norm, s->y1, B, st))) return rc;
-        ZG_HIP(zg::silu(s->y0, s->y1, B * F, s->gated, st));
-        if ((rc = project(s, L.ffn_down, s->gated, nullptr, s->out, B, st))) return rc;
-        ZG_HIP(zg::residual_add(s->x, s->out, B * H, s->d_status, st));
+        ZG_HIP(gemv(L.ffn_gu, zg::PRO_RMS, s->x, H, nullptr, 0, L.post_norm, zg::EPI_STORE, s->y0, s->y0w));
+        ZG_HIP(gemv(L.ffn_down, zg::PRO_SILU_MUL, s->y0, s->y0w, s->y0 + F, s->y0w, nullptr, zg::EPI_RESID, s->x, H));
     }
     if (logits || greedy) {
-        if ((rc = project(s, m->embd, s->x, m->out_norm, logits ? logits : s->logits, B, st))) return rc;
-        if (greedy) ZG_HIP(zg::argmax(logits ? logits : s->logits, g.vocab, B, greedy, s->d_status, st));
+        float* lg = logits ? logits : s->logits;
+        ZG_HIP(gemv(m->embd, zg::PRO_RMS, s->x, H, nullptr, 0, m->out_norm, zg::EPI_STORE, lg, V));
+        if (greedy) {
+            ZG_HIP(zg::argmax_step(lg, V, V, B, greedy, s->d_status, s->pmax, s->pidx, s->tickets, s->d_pos, s->d_ntok, 1,
+                                   st));
+            return ZG_COMPLETED;
+        }
     }
+    ZG_HIP(zg::advance_positions(s->d_pos, s->d_ntok, B, st));
+    return ZG_COMPLETED;
+}
+
+// The step through a cached HIP graph (one per rows/buffer set), captured on
+// first use.  ZG_GRAPHS=0 in the environment launches the kernels directly.
+int run_step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_t* greedy, hipStream_t st) {
+    zg_ctx* ctx = s->m->ctx;
+    if (!s->use_graphs) return step(s, B, tokens, logits, greedy, st);
+    const auto key = std::make_tuple(B, (const void*)tokens, (const void*)logits, (const void*)greedy);
+    auto it = s->graphs.find(key);
+    if (it == s->graphs.end()) {
+        hipGraph_t graph = nullptr;
+        ZG_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
+        const int rc = step(s, B, tokens, logits, greedy, st);
+        const hipError_t e = hipStreamEndCapture(st, &graph);
+        if (rc) {
+            if (e == hipSuccess && graph) (void)hipGraphDestroy(graph);
+            return rc;
+        }
+        ZG_HIP(e);
+        hipGraphExec_t exec = nullptr;
+        const hipError_t e2 = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        ZG_HIP(e2);
+        it = s->graphs.emplace(key, exec).first;
+    }
+    ZG_HIP(hipGraphLaunch(it->second, st));
     return ZG_COMPLETED;
 }
 
@@ -221,15 +275,16 @@ int read_status(zg_session* s, hipStream_t st) {
         s->poisoned = true;
         if (status & 2) return fail(ctx, ZG_E_MALFORMED, "decode step contains an out-of-vocabulary token id");
         if (status & 1) return fail(ctx, ZG_E_STATE, "nonfinite layer computation");
+        if (status & 8) return fail(ctx, ZG_E_STATE, "degenerate attention softmax");
         return fail(ctx, ZG_E_STATE, "decoder produced nonfinite logits");
     }
     return ZG_COMPLETED;
 }
 
-// Device positions follow the host copy: steps advance both (a one-wave
-// kernel on the stream, so device-driven decode loops never wait on the
-// host); reset, import and random fill mark them dirty and the next step
-// uploads them once.
+// Device positions follow the host copy: steps advance both (the last
+// launch of a step, so device-driven decode loops never wait on the host);
+// reset, import and random fill mark them dirty and the next step uploads
+// them once.
 int sync_positions(zg_session* s, hipStream_t st) {
     if (!s->pos_dirty) return ZG_COMPLETED;
     zg_ctx* ctx = s->m->ctx;
@@ -247,13 +302,6 @@ int sync_positions(zg_session* s, hipStream_t st) {
     return ZG_COMPLETED;
 }
 
-int advance(zg_session* s, size_t rows, hipStream_t st) {
-    zg_ctx* ctx = s->m->ctx;
-    ZG_HIP(zg::advance_positions(s->d_pos, s->d_ntok, rows, st));
-    for (size_t b = 0; b < rows; ++b) s->pos[b] += 1;
-    return ZG_COMPLETED;
-}
-
 int check_rows(zg_session* s, size_t rows) {
     zg_ctx* ctx = s->m->ctx;
     if (s->poisoned) return fail(ctx, ZG_E_STATE, "session poisoned by a failed step: reset or import state");
@@ -262,6 +310,9 @@ int check_rows(zg_session* s, size_t rows) {
         if ((size_t)s->pos[b] >= s->max_ctx) return fail(ctx, ZG_E_LIMIT, "model context capacity exhausted");
     return ZG_COMPLETED;
 }
+
+// Slot of the ring holding x[pos - 3 + k] (k = 0, 1, 2) at a row's position.
+inline size_t ring_slot(int pos, int k) { return (size_t)((pos + 1 + k) & 3); }
 
 }  // namespace
 
@@ -275,7 +326,7 @@ int zg_model_load(zg_ctx* ctx, uint64_t source_id, const zg_geometry* g, const z
     *out = nullptr;
     if (source_id == 0) return fail(ctx, ZG_E_MALFORMED, "unbound source identity cannot own a resident model");
     if (g->layers == 0 || g->layers > 4096 || g->full_attention_interval == 0 || g->gdn_dim != 128 ||
-        g->head_dim != 256 || g->q_heads == 0 || g->q_heads > 8 || g->kv_heads == 0 || g->q_heads % g->kv_heads ||
+        g->head_dim != 256 || g->q_heads == 0 || g->kv_heads == 0 || g->q_heads % g->kv_heads ||
         g->q_heads / g->kv_heads > 4 || g->gdn_heads == 0 || g->gdn_heads > 64 || !(g->eps > 0.0f) ||
         g->max_context == 0 || g->hidden % 256 || g->ffn % 256)
         return fail(ctx, ZG_E_UNSUPPORTED, "model geometry outside the resident decode path (gdn_dim 128, head_dim 256)");
@@ -285,7 +336,7 @@ int zg_model_load(zg_ctx* ctx, uint64_t source_id, const zg_geometry* g, const z
     m->g = *g;
     const uint64_t H = g->hidden, F = g->ffn, V = g->vocab, W = (uint64_t)g->gdn_heads * g->gdn_dim;
     const uint64_t QD = (uint64_t)g->q_heads * g->head_dim, KD = (uint64_t)g->kv_heads * g->head_dim;
-    int rc = load_matrix(m, tensors, n, "token_embd.weight", H, V, &m->embd);
+    int rc = load_stacked(m, tensors, n, {"token_embd.weight"}, H, {V}, "token_embd.weight", zg::PRO_RMS, &m->embd);
     if (!rc) rc = load_vector(m, tensors, n, "output_norm.weight", H, &m->out_norm);
     m->layers.resize(g->layers);
     for (unsigned i = 0; i < g->layers && !rc; ++i) {
@@ -294,24 +345,31 @@ int zg_model_load(zg_ctx* ctx, uint64_t source_id, const zg_geometry* g, const z
         L.full = ((i + 1) % g->full_attention_interval) == 0;
         rc = load_vector(m, tensors, n, lname(i, "attn_norm.weight"), H, &L.attn_norm);
         if (!rc) rc = load_vector(m, tensors, n, lname(i, "post_attention_norm.weight"), H, &L.post_norm);
-        if (!rc) rc = load_matrix(m, tensors, n, lname(i, "ffn_gate.weight"), H, F, &L.ffn_gate);
-        if (!rc) rc = load_matrix(m, tensors, n, lname(i, "ffn_up.weight"), H, F, &L.ffn_up);
-        if (!rc) rc = load_matrix(m, tensors, n, lname(i, "ffn_down.weight"), F, H, &L.ffn_down);
+        if (!rc)
+            rc = load_stacked(m, tensors, n, {lname(i, "ffn_gate.weight"), lname(i, "ffn_up.weight")}, H, {F, F},
+                              lname(i, "ffn_gate_up"), zg::PRO_RMS, &L.ffn_gu);
+        if (!rc)
+            rc = load_stacked(m, tensors, n, {lname(i, "ffn_down.weight")}, F, {H}, lname(i, "ffn_down.weight"),
+                              zg::PRO_SILU_MUL, &L.ffn_down);
         if (rc) break;
         if (L.full) {
-            rc = load_matrix(m, tensors, n, lname(i, "attn_q.weight"), H, 2 * QD, &L.wq);
-            if (!rc) rc = load_matrix(m, tensors, n, lname(i, "attn_k.weight"), H, KD, &L.wk);
-            if (!rc) rc = load_matrix(m, tensors, n, lname(i, "attn_v.weight"), H, KD, &L.wv);
-            if (!rc) rc = load_matrix(m, tensors, n, lname(i, "attn_output.weight"), QD, H, &L.wo);
+            rc = load_stacked(m, tensors, n,
+                              {lname(i, "attn_q.weight"), lname(i, "attn_k.weight"), lname(i, "attn_v.weight")}, H,
+                              {2 * QD, KD, KD}, lname(i, "attn_qkv_in"), zg::PRO_RMS, &L.in_proj);
+            if (!rc)
+                rc = load_stacked(m, tensors, n, {lname(i, "attn_output.weight")}, QD, {H},
+                                  lname(i, "attn_output.weight"), zg::PRO_PLAIN, &L.out_proj);
             if (!rc) rc = load_vector(m, tensors, n, lname(i, "attn_q_norm.weight"), g->head_dim, &L.q_norm);
             if (!rc) rc = load_vector(m, tensors, n, lname(i, "attn_k_norm.weight"), g->head_dim, &L.k_norm);
             m->n_attn++;
         } else {
-            rc = load_matrix(m, tensors, n, lname(i, "attn_qkv.weight"), H, 3 * W, &L.qkv);
-            if (!rc) rc = load_matrix(m, tensors, n, lname(i, "attn_gate.weight"), H, W, &L.gate);
-            if (!rc) rc = load_matrix(m, tensors, n, lname(i, "ssm_alpha.weight"), H, g->gdn_heads, &L.alpha);
-            if (!rc) rc = load_matrix(m, tensors, n, lname(i, "ssm_beta.weight"), H, g->gdn_heads, &L.beta);
-            if (!rc) rc = load_matrix(m, tensors, n, lname(i, "ssm_out.weight"), W, H, &L.ssm_out);
+            rc = load_stacked(m, tensors, n,
+                              {lname(i, "attn_qkv.weight"), lname(i, "attn_gate.weight"), lname(i, "ssm_alpha.weight"),
+                               lname(i, "ssm_beta.weight")},
+                              H, {3 * W, W, g->gdn_heads, g->gdn_heads}, lname(i, "gdn_in"), zg::PRO_RMS, &L.in_proj);
+            if (!rc)
+                rc = load_stacked(m, tensors, n, {lname(i, "ssm_out.weight")}, W, {H}, lname(i, "ssm_out.weight"),
+                                  zg::PRO_GATED, &L.out_proj);
             if (!rc) rc = load_vector(m, tensors, n, lname(i, "ssm_conv1d.weight"), 4 * 3 * W, &L.conv_w);
             if (!rc) rc = load_vector(m, tensors, n, lname(i, "ssm_norm.weight"), g->gdn_dim, &L.ssm_norm);
             if (!rc) rc = load_vector(m, tensors, n, lname(i, "ssm_a"), g->gdn_heads, &L.ssm_a);
@@ -354,17 +412,11 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     s->max_ctx = max_context;
     s->kv_bf16 = kv_dtype == ZG_BF16;
     s->pos.assign(max_batch, 0);
+    const char* env = getenv("ZG_GRAPHS");
+    s->use_graphs = !(env && env[0] == '0');
     const size_t B = max_batch, H = g.hidden, F = g.ffn, V = g.vocab, W = (size_t)g.gdn_heads * g.gdn_dim;
     const size_t QD = (size_t)g.q_heads * g.head_dim;
-    s->y0w = std::max({3 * W, 2 * QD, F});
-    s->y1w = std::max({W, F, kvw(g)});
-    s->y2w = std::max<size_t>(g.gdn_heads, kvw(g));
-    s->gatedw = std::max({W, F, QD});
-    size_t prep = 0;
-    for (size_t K : {H, F, W, QD}) prep = std::max(prep, zg::prepared_bytes(ZG_Q4_K, B, K));
-    for (size_t K : {H, F, W, QD}) prep = std::max(prep, zg::prepared_bytes(ZG_Q8_0, B, K));
-    for (size_t K : {H, F, W, QD}) prep = std::max(prep, zg::prepared_bytes(ZG_F32, B, K));
-    s->prep_bytes = prep;
+    s->y0w = std::max({4 * W + 2 * (size_t)g.gdn_heads, 2 * QD + 2 * kvw(g), 2 * F});
     int rc = 0;
     auto A = [&](void** p, size_t bytes) {
         if (!rc) rc = dalloc(s, p, bytes);
@@ -374,20 +426,17 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     A((void**)&s->d_status, 4);
     A((void**)&s->d_tokens, B * 4);
     A((void**)&s->d_greedy, B * 4);
+    A((void**)&s->tickets, B * 4);
+    A((void**)&s->att_tickets, B * g.kv_heads * 4);
+    A((void**)&s->att_stats, B * g.q_heads * 2 * 4);
+    A((void**)&s->pmax, zg::argmax_partials(B) * 4);
+    A((void**)&s->pidx, zg::argmax_partials(B) * 4);
     A((void**)&s->x, B * H * 4);
     A((void**)&s->y0, B * s->y0w * 4);
-    A((void**)&s->y1, B * s->y1w * 4);
-    A((void**)&s->y2, B * s->y2w * 4);
-    A((void**)&s->y3, B * g.gdn_heads * 4);
-    A((void**)&s->mixed, B * 3 * W * 4);
     A((void**)&s->core, B * W * 4);
-    A((void**)&s->gated, B * s->gatedw * 4);
-    A((void**)&s->out, B * H * 4);
+    A((void**)&s->ao, B * QD * 4);
     A((void**)&s->logits, B * V * 4);
-    A((void**)&s->qr, B * QD * 4);
     A((void**)&s->scores, B * g.q_heads * max_context * 4);
-    A((void**)&s->probs, B * g.q_heads * max_context * 4);
-    A(&s->prep, prep);
     s->layer_slot.resize(g.layers);
     for (size_t i = 0; i < m->layers.size() && !rc; ++i) {
         if (m->layers[i].full) {
@@ -399,11 +448,11 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
             s->kc.push_back(k);
             s->vc.push_back(v);
         } else {
-            s->layer_slot[i] = (int)s->conv.size();
+            s->layer_slot[i] = (int)s->ring.size();
             float *c = nullptr, *r = nullptr;
-            A((void**)&c, B * conv_floats(g) * 4);
+            A((void**)&c, B * ring_floats(g) * 4);
             A((void**)&r, B * rec_floats(g) * 4);
-            s->conv.push_back(c);
+            s->ring.push_back(c);
             s->rec.push_back(r);
         }
     }
@@ -420,7 +469,8 @@ void zg_session_destroy(zg_session* s) {
     zg_ctx* ctx = s->m->ctx;
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
     (void)hipSetDevice(ctx->device);
-    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipDeviceSynchronize();
+    for (auto& kv : s->graphs) (void)hipGraphExecDestroy(kv.second);
     for (void* p : s->allocs) (void)hipFree(p);
     delete s;
 }
@@ -432,7 +482,7 @@ int zg_session_reset(zg_session* s) {
     (void)hipSetDevice(ctx->device);
     const zg_geometry& g = s->m->g;
     const size_t B = s->max_batch;
-    for (float* c : s->conv) ZG_HIP(hipMemsetAsync(c, 0, B * conv_floats(g) * 4, ctx->stream));
+    for (float* c : s->ring) ZG_HIP(hipMemsetAsync(c, 0, B * ring_floats(g) * 4, ctx->stream));
     for (float* r : s->rec) ZG_HIP(hipMemsetAsync(r, 0, B * rec_floats(g) * 4, ctx->stream));
     const size_t kvb = B * s->max_ctx * kvw(g) * (s->kv_bf16 ? 2 : 4);
     for (size_t i = 0; i < s->kc.size(); ++i) {
@@ -440,6 +490,8 @@ int zg_session_reset(zg_session* s) {
         ZG_HIP(hipMemsetAsync(s->vc[i], 0, kvb, ctx->stream));
     }
     ZG_HIP(hipMemsetAsync(s->d_status, 0, 4, ctx->stream));
+    ZG_HIP(hipMemsetAsync(s->tickets, 0, B * 4, ctx->stream));
+    ZG_HIP(hipMemsetAsync(s->att_tickets, 0, B * g.kv_heads * 4, ctx->stream));
     ZG_HIP(hipStreamSynchronize(ctx->stream));
     std::fill(s->pos.begin(), s->pos.end(), 0);
     s->pos_dirty = true;
@@ -466,11 +518,11 @@ int zg_decode_step(zg_session* s, size_t rows, const uint32_t* tokens, float* lo
     ZG_HIP(hipMemcpyAsync(s->d_tokens, tokens, rows * 4, hipMemcpyHostToDevice, st));
     ZG_HIP(hipStreamSynchronize(st));
     const bool want = logits || greedy;
-    if ((rc = step(s, rows, s->d_tokens, want ? s->logits : nullptr, want ? s->d_greedy : nullptr, st))) {
+    if ((rc = run_step(s, rows, s->d_tokens, want ? s->logits : nullptr, want ? s->d_greedy : nullptr, st))) {
         s->poisoned = true;
         return rc;
     }
-    if ((rc = advance(s, rows, st))) return rc;
+    for (size_t b = 0; b < rows; ++b) s->pos[b] += 1;
     if ((rc = read_status(s, st))) return rc;
     if (logits) ZG_HIP(hipMemcpyAsync(logits, s->logits, rows * s->m->g.vocab * 4, hipMemcpyDeviceToHost, st));
     if (greedy) ZG_HIP(hipMemcpyAsync(greedy, s->d_greedy, rows * 4, hipMemcpyDeviceToHost, st));
@@ -501,11 +553,12 @@ int zg_decode_step_device(zg_session* s, size_t rows, const uint32_t* d_tokens, 
     if (rc) return rc;
     hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
     if ((rc = sync_positions(s, st))) return rc;
-    if ((rc = step(s, rows, d_tokens, d_logits ? d_logits : (d_greedy ? s->logits : nullptr), d_greedy, st))) {
+    if ((rc = run_step(s, rows, d_tokens, d_logits ? d_logits : (d_greedy ? s->logits : nullptr), d_greedy, st))) {
         s->poisoned = true;
         return rc;
     }
-    return advance(s, rows, st);
+    for (size_t b = 0; b < rows; ++b) s->pos[b] += 1;
+    return ZG_COMPLETED;
 }
 
 int zg_session_check(zg_session* s, void* stream) {
@@ -529,16 +582,22 @@ int zg_state_export(zg_session* s, size_t row, float* out, size_t n) {
     if (row >= s->max_batch || n != zg_state_floats(s, row)) return fail(ctx, ZG_E_MALFORMED, "state length mismatch");
     const zg_geometry& g = s->m->g;
     hipStream_t st = ctx->stream;
-    const size_t T = (size_t)s->pos[row], kw = kvw(g);
+    ZG_HIP(hipDeviceSynchronize());
+    const int P = s->pos[row];
+    const size_t T = (size_t)P, kw = kvw(g), C = (size_t)g.gdn_heads * g.gdn_dim * 3;
     int rc = ensure(ctx, ctx->scratch, std::max<size_t>(T * kw * 4, 256));
     if (rc) return rc;
+    std::vector<float> ring(ring_floats(g));
     size_t at = 0;
     for (size_t i = 0; i < s->m->layers.size(); ++i) {
         const int slot = s->layer_slot[i];
         if (!s->m->layers[i].full) {
-            ZG_HIP(hipMemcpyAsync(out + at, s->conv[slot] + row * conv_floats(g), conv_floats(g) * 4, hipMemcpyDeviceToHost, st));
+            // history [channel][oldest..newest] (lib.rs:79-80) from the ring
+            ZG_HIP(hipMemcpy(ring.data(), s->ring[slot] + row * ring_floats(g), ring_floats(g) * 4, hipMemcpyDeviceToHost));
+            for (size_t c = 0; c < C; ++c)
+                for (int k = 0; k < 3; ++k) out[at + c * 3 + k] = ring[c * 4 + ring_slot(P, k)];
             at += conv_floats(g);
-            ZG_HIP(hipMemcpyAsync(out + at, s->rec[slot] + row * rec_floats(g), rec_floats(g) * 4, hipMemcpyDeviceToHost, st));
+            ZG_HIP(hipMemcpy(out + at, s->rec[slot] + row * rec_floats(g), rec_floats(g) * 4, hipMemcpyDeviceToHost));
             at += rec_floats(g);
         } else {
             for (void* cache : {s->kc[slot], s->vc[slot]}) {
@@ -548,8 +607,8 @@ int zg_state_export(zg_session* s, size_t row, float* out, size_t n) {
                         ZG_HIP(hipMemcpyAsync(out + at, ctx->scratch.ptr, T * kw * 4, hipMemcpyDeviceToHost, st));
                         ZG_HIP(hipStreamSynchronize(st));
                     } else {
-                        ZG_HIP(hipMemcpyAsync(out + at, (const float*)cache + row * s->max_ctx * kw, T * kw * 4,
-                                              hipMemcpyDeviceToHost, st));
+                        ZG_HIP(hipMemcpy(out + at, (const float*)cache + row * s->max_ctx * kw, T * kw * 4,
+                                         hipMemcpyDeviceToHost));
                     }
                 }
                 at += T * kw;
@@ -575,16 +634,21 @@ int zg_state_import(zg_session* s, size_t row, const float* in, size_t n, int po
     }
     const zg_geometry& g = s->m->g;
     hipStream_t st = ctx->stream;
-    const size_t T = (size_t)position, kw = kvw(g);
+    ZG_HIP(hipDeviceSynchronize());
+    const size_t T = (size_t)position, kw = kvw(g), C = (size_t)g.gdn_heads * g.gdn_dim * 3;
     int rc = ensure(ctx, ctx->scratch, std::max<size_t>(T * kw * 4, 256));
     if (rc) return rc;
+    std::vector<float> ring(ring_floats(g));
     size_t at = 0;
     for (size_t i = 0; i < s->m->layers.size(); ++i) {
         const int slot = s->layer_slot[i];
         if (!s->m->layers[i].full) {
-            ZG_HIP(hipMemcpyAsync(s->conv[slot] + row * conv_floats(g), in + at, conv_floats(g) * 4, hipMemcpyHostToDevice, st));
+            std::fill(ring.begin(), ring.end(), 0.0f);
+            for (size_t c = 0; c < C; ++c)
+                for (int k = 0; k < 3; ++k) ring[c * 4 + ring_slot(position, k)] = in[at + c * 3 + k];
+            ZG_HIP(hipMemcpy(s->ring[slot] + row * ring_floats(g), ring.data(), ring_floats(g) * 4, hipMemcpyHostToDevice));
             at += conv_floats(g);
-            ZG_HIP(hipMemcpyAsync(s->rec[slot] + row * rec_floats(g), in + at, rec_floats(g) * 4, hipMemcpyHostToDevice, st));
+            ZG_HIP(hipMemcpy(s->rec[slot] + row * rec_floats(g), in + at, rec_floats(g) * 4, hipMemcpyHostToDevice));
             at += rec_floats(g);
         } else {
             for (void* cache : {s->kc[slot], s->vc[slot]}) {
@@ -594,8 +658,8 @@ int zg_state_import(zg_session* s, size_t row, const float* in, size_t n, int po
                         ZG_HIP(zg::convert_kv(ctx->scratch.ptr, (uint16_t*)cache + row * s->max_ctx * kw, T * kw, false, st));
                         ZG_HIP(hipStreamSynchronize(st));
                     } else {
-                        ZG_HIP(hipMemcpyAsync((float*)cache + row * s->max_ctx * kw, in + at, T * kw * 4,
-                                              hipMemcpyHostToDevice, st));
+                        ZG_HIP(hipMemcpy((float*)cache + row * s->max_ctx * kw, in + at, T * kw * 4,
+                                         hipMemcpyHostToDevice));
                     }
                 }
                 at += T * kw;
@@ -617,10 +681,11 @@ int zg_session_fill_random(zg_session* s, size_t rows, size_t prefix, uint64_t s
         return fail(ctx, ZG_E_LIMIT, "random prefix exceeds the session");
     const zg_geometry& g = s->m->g;
     hipStream_t st = ctx->stream;
+    ZG_HIP(hipDeviceSynchronize());
     uint64_t k = seed * 0x9e3779b97f4a7c15ull;
     const size_t kw = kvw(g);
-    for (size_t i = 0; i < s->conv.size(); ++i) {
-        ZG_HIP(zg::fill_normal(s->conv[i], rows * conv_floats(g), false, ++k, 0.5f, st));
+    for (size_t i = 0; i < s->ring.size(); ++i) {
+        ZG_HIP(zg::fill_normal(s->ring[i], rows * ring_floats(g), false, ++k, 0.5f, st));
         ZG_HIP(zg::fill_normal(s->rec[i], rows * rec_floats(g), false, ++k, 0.02f, st));
     }
     for (size_t i = 0; i < s->kc.size(); ++i) {
@@ -634,281 +699,6 @@ int zg_session_fill_random(zg_session* s, size_t rows, size_t prefix, uint64_t s
     for (size_t b = 0; b < rows; ++b) s->pos[b] = (int)prefix;
     s->pos_dirty = true;
     s->poisoned = false;
-    return ZG_COMPLETED;
-}
-
-// ----------------------------------------------------- boundary-A regions
-
-int zg_gdn_conv(zg_ctx* ctx, const float* activation, const float* weights, const float* history, size_t channels,
-                float* raw_out, float* history_out) {
-    if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::recursive_mutex> g(ctx->mu);
-    (void)hipSetDevice(ctx->device);
-    if (!activation || !weights || !history || !raw_out || !history_out || channels == 0 ||
-        !all_finite(activation, channels) || !all_finite(weights, channels * 4) || !all_finite(history, channels * 3))
-        return fail(ctx, ZG_E_MALFORMED, "GDN causal convolution source geometry/nonfinite input");
-    const size_t oa = 0, ow = align256(channels * 4), oh = ow + align256(channels * 16), oo = oh + align256(channels * 12);
-    int rc = ensure(ctx, ctx->scratch, oo + align256(channels * 4));
-    if (rc) return rc;
-    char* b = (char*)ctx->scratch.ptr;
-    hipStream_t st = ctx->stream;
-    ZG_HIP(hipMemcpyAsync(b + oa, activation, channels * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(hipMemcpyAsync(b + ow, weights, channels * 16, hipMemcpyHostToDevice, st));
-    ZG_HIP(hipMemcpyAsync(b + oh, history, channels * 12, hipMemcpyHostToDevice, st));
-    ZG_HIP(zg::gdn_conv((const float*)(b + oa), (const float*)(b + ow), (float*)(b + oh), (float*)(b + oo), channels, 1,
-                        0, 0, 0, 0, st));
-    ZG_HIP(hipMemcpyAsync(raw_out, b + oo, channels * 4, hipMemcpyDeviceToHost, st));
-    ZG_HIP(hipMemcpyAsync(history_out, b + oh, channels * 12, hipMemcpyDeviceToHost, st));
-    ZG_HIP(hipStreamSynchronize(st));
-    if (!all_finite(raw_out, channels) || !all_finite(history_out, channels * 3))
-        return fail(ctx, ZG_E_STATE, "physical GDN convolution returned incomplete/nonfinite source state");
-    return ZG_COMPLETED;
-}
-
-int zg_gdn_coefficients(zg_ctx* ctx, const float* alpha, const float* beta, const float* dt, const float* a,
-                        size_t heads, float scale, float* gain_out, float* beta_out, float* softplus_out,
-                        float* gate_raw_out) {
-    if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::recursive_mutex> g(ctx->mu);
-    (void)hipSetDevice(ctx->device);
-    if (!alpha || !beta || !dt || !a || !gain_out || !beta_out || !softplus_out || !gate_raw_out || heads == 0 ||
-        !all_finite(alpha, heads) || !all_finite(beta, heads) || !all_finite(dt, heads) || !all_finite(a, heads) ||
-        !std::isfinite(scale) || scale <= 0.0f)
-        return fail(ctx, ZG_E_MALFORMED, "invalid source GDN coefficient inputs");
-    const size_t stride = align256(heads * 4);
-    int rc = ensure(ctx, ctx->scratch, 8 * stride);
-    if (rc) return rc;
-    char* b = (char*)ctx->scratch.ptr;
-    hipStream_t st = ctx->stream;
-    const float* ins[4] = {alpha, beta, dt, a};
-    for (int i = 0; i < 4; ++i) ZG_HIP(hipMemcpyAsync(b + i * stride, ins[i], heads * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(zg::gdn_coefficients((const float*)b, (const float*)(b + stride), (const float*)(b + 2 * stride),
-                                (const float*)(b + 3 * stride), heads, (float*)(b + 4 * stride), (float*)(b + 5 * stride),
-                                (float*)(b + 6 * stride), (float*)(b + 7 * stride), st));
-    float* outs[4] = {gain_out, beta_out, softplus_out, gate_raw_out};
-    for (int i = 0; i < 4; ++i)
-        ZG_HIP(hipMemcpyAsync(outs[i], b + (4 + i) * stride, heads * 4, hipMemcpyDeviceToHost, st));
-    ZG_HIP(hipStreamSynchronize(st));
-    for (int i = 0; i < 4; ++i)
-        if (!all_finite(outs[i], heads)) return fail(ctx, ZG_E_STATE, "incomplete/nonfinite source GDN coefficients");
-    return ZG_COMPLETED;
-}
-
-int zg_gdn_recurrent(zg_ctx* ctx, size_t width, size_t heads, const float* q, const float* k, const float* v,
-                     const float* coefficients, const float* state, float* output, float* state_out) {
-    if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::recursive_mutex> g(ctx->mu);
-    (void)hipSetDevice(ctx->device);
-    if (!q || !k || !v || !coefficients || !state || !output || !state_out || width == 0 || heads == 0)
-        return fail(ctx, ZG_E_MALFORMED, "invalid source GDN recurrent geometry or FP32 inputs");
-    const size_t n = heads * width, ns = n * width;
-    if (!all_finite(q, n) || !all_finite(k, n) || !all_finite(v, n) || !all_finite(state, ns) ||
-        !all_finite(coefficients, heads * 3))
-        return fail(ctx, ZG_E_MALFORMED, "invalid source GDN recurrent geometry or FP32 inputs");
-    if (width != 128) return fail(ctx, ZG_UNSUPPORTED, "GDN recurrence offered for head width 128");
-    std::vector<float> gain(heads), beta(heads), scale(heads);
-    for (size_t h = 0; h < heads; ++h) {
-        gain[h] = coefficients[3 * h];
-        beta[h] = coefficients[3 * h + 1];
-        scale[h] = coefficients[3 * h + 2];
-    }
-    const size_t oq = 0, ok = align256(n * 4), ov = ok + align256(n * 4), oc = ov + align256(n * 4),
-                 os = oc + 3 * align256(heads * 4), oo = os + align256(ns * 4);
-    int rc = ensure(ctx, ctx->scratch, oo + align256(n * 4));
-    if (rc) return rc;
-    char* b = (char*)ctx->scratch.ptr;
-    hipStream_t st = ctx->stream;
-    ZG_HIP(hipMemcpyAsync(b + oq, q, n * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(hipMemcpyAsync(b + ok, k, n * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(hipMemcpyAsync(b + ov, v, n * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(hipMemcpyAsync(b + oc, gain.data(), heads * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(hipMemcpyAsync(b + oc + align256(heads * 4), beta.data(), heads * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(hipMemcpyAsync(b + oc + 2 * align256(heads * 4), scale.data(), heads * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(hipMemcpyAsync(b + os, state, ns * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(zg::gdn_recurrent(false, (const float*)(b + oq), (const float*)(b + ok), (const float*)(b + ov), 0,
-                             (const float*)(b + oc), (const float*)(b + oc + align256(heads * 4)), 0, nullptr, nullptr,
-                             0.0f, 0.0f, (const float*)(b + oc + 2 * align256(heads * 4)), (float*)(b + os),
-                             (float*)(b + oo), 0, heads, width, 1, st));
-    ZG_HIP(hipMemcpyAsync(output, b + oo, n * 4, hipMemcpyDeviceToHost, st));
-    ZG_HIP(hipMemcpyAsync(state_out, b + os, ns * 4, hipMemcpyDeviceToHost, st));
-    ZG_HIP(hipStreamSynchronize(st));
-    if (!all_finite(output, n) || !all_finite(state_out, ns))
-        return fail(ctx, ZG_E_STATE, "incomplete/nonfinite GDN recurrent proposal");
-    return ZG_COMPLETED;
-}
-
-int zg_rope_kv(zg_ctx* ctx, const float* query, const float* key, const float* value, size_t head_width,
-               size_t query_heads, size_t kv_heads, size_t rotate, size_t position, float theta_scale, float* query_out,
-               float* key_out, float* value_out) {
-    if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::recursive_mutex> g(ctx->mu);
-    (void)hipSetDevice(ctx->device);
-    if (!query || !key || !value || !query_out || !key_out || !value_out || head_width == 0 || query_heads == 0 ||
-        kv_heads == 0 || query_heads % kv_heads || rotate == 0 || rotate > head_width || rotate % 2 ||
-        position > 2147483647u || !std::isfinite(theta_scale) || theta_scale <= 0.0f || theta_scale > 1.0f ||
-        !all_finite(query, query_heads * head_width) || !all_finite(key, kv_heads * head_width) ||
-        !all_finite(value, kv_heads * head_width))
-        return fail(ctx, ZG_E_MALFORMED, "invalid source RoPE/KV geometry or FP32 input");
-    if (head_width > 256 || rotate > 128) return fail(ctx, ZG_UNSUPPORTED, "RoPE offered for head width <= 256");
-    const size_t nq = query_heads * head_width, nk = kv_heads * head_width;
-    // The prep kernel reads q from a [q | gate] layout (stride 2*head_width);
-    // lay the query out that way.
-    std::vector<float> qpad(2 * nq, 0.0f);
-    for (size_t h = 0; h < query_heads; ++h)
-        std::memcpy(qpad.data() + h * 2 * head_width, query + h * head_width, head_width * 4);
-    const size_t oq = 0, ok = align256(2 * nq * 4), ov = ok + align256(nk * 4), op = ov + align256(nk * 4),
-                 oqr = op + 256, oko = oqr + align256(nq * 4), ovo = oko + align256(nk * 4);
-    int rc = ensure(ctx, ctx->scratch, ovo + align256(nk * 4));
-    if (rc) return rc;
-    char* b = (char*)ctx->scratch.ptr;
-    hipStream_t st = ctx->stream;
-    const int p = (int)position;
-    ZG_HIP(hipMemcpyAsync(b + oq, qpad.data(), 2 * nq * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(hipMemcpyAsync(b + ok, key, nk * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(hipMemcpyAsync(b + ov, value, nk * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(hipMemcpyAsync(b + op, &p, 4, hipMemcpyHostToDevice, st));
-    zg::AttnArgs a;
-    a.B = 1;
-    a.nq = (int)query_heads;
-    a.nkv = (int)kv_heads;
-    a.d = (int)head_width;
-    a.rotate = (int)rotate;
-    a.do_prep = 1;
-    a.prep_only = 1;
-    a.norm = 0;
-    a.qproj = (const float*)(b + oq);
-    a.q_stride = 2 * nq;
-    a.kproj = (const float*)(b + ok);
-    a.vproj = (const float*)(b + ov);
-    a.kv_stride = nk;
-    a.pos = (const int*)(b + op);
-    a.theta_scale = theta_scale;
-    a.qr = (float*)(b + oqr);
-    a.qr_stride = nq;
-    a.kout = (float*)(b + oko);
-    a.vout = (float*)(b + ovo);
-    ZG_HIP(zg::rope_prep(a, st));
-    ZG_HIP(hipMemcpyAsync(query_out, b + oqr, nq * 4, hipMemcpyDeviceToHost, st));
-    ZG_HIP(hipMemcpyAsync(key_out, b + oko, nk * 4, hipMemcpyDeviceToHost, st));
-    ZG_HIP(hipMemcpyAsync(value_out, b + ovo, nk * 4, hipMemcpyDeviceToHost, st));
-    ZG_HIP(hipStreamSynchronize(st));
-    if (!all_finite(query_out, nq) || !all_finite(key_out, nk))
-        return fail(ctx, ZG_E_STATE, "incomplete/nonfinite RoPE proposal");
-    return ZG_COMPLETED;
-}
-
-// QK + softmax + PV regions share one driver over f32 host keys/values.
-static int attention_region(zg_ctx* ctx, const float* query, const float* keys, const float* values, size_t tokens,
-                            size_t head_width, size_t query_heads, size_t kv_heads, float scale, float* dots,
-                            float* scores, float* probs, float* out) {
-    const size_t nq = query_heads * head_width, kw = kv_heads * head_width, ns = query_heads * tokens;
-    const size_t oq = 0, ok = align256(nq * 4), ov = ok + align256(tokens * kw * 4), on = ov + align256(values ? tokens * kw * 4 : 4),
-                 od = on + 256, osc = od + align256(ns * 4), opr = osc + align256(ns * 4),
-                 oo = opr + align256(ns * 4);
-    int rc = ensure(ctx, ctx->scratch, oo + align256(nq * 4));
-    if (rc) return rc;
-    char* b = (char*)ctx->scratch.ptr;
-    hipStream_t st = ctx->stream;
-    const int T = (int)tokens;
-    ZG_HIP(hipMemcpyAsync(b + oq, query, nq * 4, hipMemcpyHostToDevice, st));
-    if (keys) ZG_HIP(hipMemcpyAsync(b + ok, keys, tokens * kw * 4, hipMemcpyHostToDevice, st));
-    if (values) ZG_HIP(hipMemcpyAsync(b + ov, values, tokens * kw * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(hipMemcpyAsync(b + on, &T, 4, hipMemcpyHostToDevice, st));
-    if (probs && !keys) ZG_HIP(hipMemcpyAsync(b + opr, probs, ns * 4, hipMemcpyHostToDevice, st));
-    zg::AttnArgs a;
-    a.B = 1;
-    a.nq = (int)query_heads;
-    a.nkv = (int)kv_heads;
-    a.d = (int)head_width;
-    a.tmax = T;
-    a.kv_bf16 = 0;
-    a.qr = (float*)(b + oq);
-    a.qr_stride = nq;
-    a.kcache = b + ok;
-    a.vcache = b + ov;
-    a.cache_row_stride = tokens * kw;
-    a.ntok = (const int*)(b + on);
-    a.scale = scale;
-    a.dots = (float*)(b + od);
-    a.scores = (float*)(b + osc);
-    a.probs = (float*)(b + opr);
-    a.score_stride = ns;
-    a.out = out ? (float*)(b + oo) : nullptr;
-    a.out_stride = nq;
-    ZG_HIP(zg::attention_parts(a, keys != nullptr, keys != nullptr, out != nullptr, st));
-    if (dots) ZG_HIP(hipMemcpyAsync(dots, b + od, ns * 4, hipMemcpyDeviceToHost, st));
-    if (scores) ZG_HIP(hipMemcpyAsync(scores, b + osc, ns * 4, hipMemcpyDeviceToHost, st));
-    if (probs && keys) ZG_HIP(hipMemcpyAsync(probs, b + opr, ns * 4, hipMemcpyDeviceToHost, st));
-    if (out) ZG_HIP(hipMemcpyAsync(out, b + oo, nq * 4, hipMemcpyDeviceToHost, st));
-    ZG_HIP(hipStreamSynchronize(st));
-    return ZG_COMPLETED;
-}
-
-int zg_attention_qk(zg_ctx* ctx, const float* query, const float* keys, size_t tokens, size_t head_width,
-                    size_t query_heads, size_t kv_heads, float scale, float* dots, float* scores) {
-    if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::recursive_mutex> g(ctx->mu);
-    (void)hipSetDevice(ctx->device);
-    if (!query || !keys || !dots || !scores || head_width == 0 || query_heads == 0 || kv_heads == 0 ||
-        query_heads % kv_heads || tokens == 0 || !std::isfinite(scale) || scale <= 0.0f ||
-        !all_finite(query, query_heads * head_width) || !all_finite(keys, tokens * kv_heads * head_width))
-        return fail(ctx, ZG_E_MALFORMED, "invalid source attention QK region");
-    if (head_width != 256 || query_heads / kv_heads > 4)
-        return fail(ctx, ZG_UNSUPPORTED, "attention offered for head width 256, GQA group <= 4");
-    const size_t ns = query_heads * tokens;
-    std::vector<float> probs(ns);
-    int rc = attention_region(ctx, query, keys, nullptr, tokens, head_width, query_heads, kv_heads, scale, dots, scores,
-                              probs.data(), nullptr);
-    if (rc) return rc;
-    for (size_t i = 0; i < ns; ++i)
-        if (!std::isfinite(dots[i]) || scores[i] != dots[i] * scale)
-            return fail(ctx, ZG_E_STATE, "incomplete/nonfinite QK proposal or wrong source scale");
-    return ZG_COMPLETED;
-}
-
-int zg_attention_softmax(zg_ctx* ctx, const float* scores, size_t heads, size_t width, float* probabilities) {
-    if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::recursive_mutex> g(ctx->mu);
-    (void)hipSetDevice(ctx->device);
-    if (!scores || !probabilities || heads == 0 || width == 0 || !all_finite(scores, heads * width))
-        return fail(ctx, ZG_E_MALFORMED, "invalid source attention softmax region");
-    const size_t ns = heads * width;
-    const size_t osc = 0, on = align256(ns * 4), opr = on + 256;
-    int rc = ensure(ctx, ctx->scratch, opr + align256(ns * 4));
-    if (rc) return rc;
-    char* b = (char*)ctx->scratch.ptr;
-    hipStream_t st = ctx->stream;
-    const int T = (int)width;
-    ZG_HIP(hipMemcpyAsync(b + osc, scores, ns * 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(hipMemcpyAsync(b + on, &T, 4, hipMemcpyHostToDevice, st));
-    ZG_HIP(zg::softmax_rows((const float*)(b + osc), ns, (const int*)(b + on), (float*)(b + opr), heads, 1, st));
-    ZG_HIP(hipMemcpyAsync(probabilities, b + opr, ns * 4, hipMemcpyDeviceToHost, st));
-    ZG_HIP(hipStreamSynchronize(st));
-    for (size_t i = 0; i < ns; ++i)
-        if (!std::isfinite(probabilities[i]) || probabilities[i] < 0.0f || probabilities[i] > 1.0f)
-            return fail(ctx, ZG_E_STATE, "invalid source softmax probability");
-    return ZG_COMPLETED;
-}
-
-int zg_attention_value(zg_ctx* ctx, const float* probabilities, const float* values, size_t tokens, size_t head_width,
-                       size_t query_heads, size_t kv_heads, float* out) {
-    if (!ctx) return ZG_E_MALFORMED;
-    std::lock_guard<std::recursive_mutex> g(ctx->mu);
-    (void)hipSetDevice(ctx->device);
-    if (!probabilities || !values || !out || head_width == 0 || query_heads == 0 || kv_heads == 0 ||
-        query_heads % kv_heads || tokens == 0 || !all_finite(values, tokens * kv_heads * head_width))
-        return fail(ctx, ZG_E_MALFORMED, "invalid source attention value region");
-    for (size_t i = 0; i < query_heads * tokens; ++i)
-        if (!std::isfinite(probabilities[i]) || std::signbit(probabilities[i]) || probabilities[i] > 1.0f)
-            return fail(ctx, ZG_E_MALFORMED, "invalid source attention value region");
-    if (head_width != 256 || query_heads / kv_heads > 4)
-        return fail(ctx, ZG_UNSUPPORTED, "attention offered for head width 256, GQA group <= 4");
-    std::vector<float> dummy(query_heads * head_width);
-    int rc = attention_region(ctx, dummy.data(), nullptr, values, tokens, head_width, query_heads, kv_heads, 1.0f,
-                              nullptr, nullptr, const_cast<float*>(probabilities), out);
-    if (rc) return rc;
-    if (!all_finite(out, query_heads * head_width))
-        return fail(ctx, ZG_E_STATE, "incomplete/nonfinite source attention value proposal");
     return ZG_COMPLETED;
 }
 
