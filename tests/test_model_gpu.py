@@ -238,6 +238,29 @@ def test_batched_rows_match_independent_sessions(kern, tiny_q4k):
     m.close()
 
 
+def test_batched_mfma_rows_match_oracle(kern, tiny_q4k):
+    """More than 4 rows take the batched projections (activation rounded to
+    f16, Q4_K weights dequantized to f16 on the fly, f16 MFMA with f32
+    accumulation); every row must still track its own CPU session within
+    the end-to-end bound and pick the same greedy tokens."""
+    g, t = tiny_q4k
+    B, steps = 8, 5
+    m = qwen35.QwenModelHip(g, t, kernel=kern)
+    s = m.session(max_batch=B, max_context=64, kv_dtype=L.F32)
+    toks = _tokens(13, B * steps, g["vocab"]).reshape(steps, B)
+    got = [s.step(toks[i])[0] for i in range(steps)]
+    worst = 0.0
+    for b in range(B):
+        o = _oracle(g, t).session()
+        for i in range(steps):
+            ref = o.forward(int(toks[i, b]))
+            worst = max(worst, float(np.max(np.abs(got[i][b] - ref))))
+            assert int(np.argmax(got[i][b])) == int(np.argmax(ref)), (b, i)
+    print(f"batched B={B}: worst logit max-abs {worst:.3e}")
+    assert worst <= LOGIT_TOL
+    m.close()
+
+
 def test_state_export_import_and_reset(kern, tiny_q8):
     m = qwen35.QwenModelHip(TINY, tiny_q8, kernel=kern)
     s = m.session(max_batch=1, max_context=64, kv_dtype=L.F32)

@@ -364,6 +364,206 @@ __global__ __launch_bounds__(256) void fused_q8_kernel(FusedGemvArgs a) {
     }
 }
 
+// ============================================== batched rows: f16 MFMA
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+// One workgroup per activation row (rows M..Mpad-1 zero): the prologue
+// values of wg_prologue, rounded once to f16, into xh[Mpad][K].
+template <int PRO, int JMAX>
+__global__ __launch_bounds__(256) void act16_kernel(FusedGemvArgs a, _Float16* __restrict__ xh) {
+    __shared__ double red[4];
+    const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, K = a.K;
+    const bool valid = m < a.M;
+    v4f v[JMAX], w[JMAX];
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) {
+        const int k = 4 * tid + 1024 * j;
+        v[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        w[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (valid && k < K) {
+            v[j] = *(const v4f*)(a.x + (size_t)m * a.ldx + k);
+            if (PRO == PRO_RMS) w[j] = *(const v4f*)(a.gamma + k);
+            if (PRO == PRO_GATED || PRO == PRO_SILU_MUL) w[j] = *(const v4f*)(a.x2 + (size_t)m * a.ldx2 + k);
+        }
+    }
+    float inv = 1.0f;
+    if (PRO == PRO_RMS) {
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < JMAX; ++j) {
+            const float q0 = v[j].x * v[j].x, q1 = v[j].y * v[j].y, q2 = v[j].z * v[j].z, q3 = v[j].w * v[j].w;
+            s += (double)q0;
+            s += (double)q1;
+            s += (double)q2;
+            s += (double)q3;
+        }
+        s = wave_sum_xor<double>(s, 64);
+        if (lane == 0) red[tid >> 6] = s;
+        __syncthreads();
+        inv = rms_inv((red[0] + red[1]) + (red[2] + red[3]), K, a.eps);
+    }
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) {
+        const int k = 4 * tid + 1024 * j;
+        if (1024 * j >= K) break;
+        float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        const float o[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+        if (PRO == PRO_RMS) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) e[t] = (e[t] * inv) * o[t];
+        } else if (PRO == PRO_GATED) {
+            double s = 0.0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float q = e[t] * e[t];
+                s += (double)q;
+            }
+            s = wave_sum_xor<double>(s, 32);
+            const float gi = rms_inv(s, a.group, a.eps);
+            const v4f g = k < K ? *(const v4f*)(a.gamma + (k & (a.group - 1))) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            const float gg[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) e[t] = ((e[t] * gi) * gg[t]) * ggml_silu(o[t]);
+        } else if (PRO == PRO_SILU_MUL) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) e[t] = o[t] * ggml_silu(e[t]);
+        }
+        if (k < K) {
+            typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+            h4v hv4;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) hv4[t] = valid ? (_Float16)e[t] : (_Float16)0.0f;
+            *(h4v*)(xh + (size_t)m * K + k) = hv4;
+        }
+    }
+}
+
+// Y[m][n] = sum_k X[m][k] W[n][k] for up to 64 rows on v_mfma_f32_32x32x16_f16:
+// A = X tile (32 rows m x 16 k), B = dequantized weights (16 k x 32 rows n),
+// so D[i = m][j = n] and the lanes of a row store adjacent outputs.  Lane l
+// holds A[m = l%32][k = 8*(l/32) + e] and B[k = 8*(l/32) + e][n = l%32]
+// (e < 8); D register r is row m = (r%4) + 8*(r/4) + 4*(l/32), column
+// n = l%32.  Per 256-element Q4_K block a lane reads the 8-byte pieces
+// 32*c4 + 16*half + 8*(l/32) of its weight row: K step s (16 per block)
+// uses piece (s/4, s%2), nibble (s/2)&1, group s/2.  Weights are
+// dequantized as the reference does (f32(q)*scale - min, two roundings)
+// and rounded once to f16; activations arrive in f16.  Each wave owns 32
+// weight rows x 32 activation rows, 4 waves per workgroup.
+template <int EPI, int KS>
+__global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, const _Float16* __restrict__ xh) {
+    // KS waves share one 32 x 32 output tile and split its K blocks
+    // (wave w takes blocks w, w+KS, ...); the partial tiles are summed in a
+    // fixed order through LDS, so the result does not depend on timing.
+    __shared__ float red[KS][16][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, hsel = lane >> 5, r32 = lane & 31;
+    const int n0 = blockIdx.x * 32;
+    const int m0 = blockIdx.y * 32;
+    const int K = a.K, N = a.N, nbk = K >> 8;
+    const int n = n0 + r32;
+    const bool nv = n < N;
+    const uint8_t* qrow = (const uint8_t*)a.qs + (size_t)(nv ? n : 0) * (K >> 1) + 8 * hsel;
+    const v4u* hrow = (const v4u*)a.hdr + (size_t)(nv ? n : 0) * nbk;
+    const _Float16* xrow = xh + (size_t)(m0 + r32) * K + 8 * hsel;
+    f16v acc = {};
+    for (int kb = wv; kb < nbk; kb += KS) {
+        uint2 pc[4][2];
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) pc[c4][hf] = *(const uint2*)(qrow + (size_t)kb * 128 + 32 * c4 + 16 * hf);
+        const v4u hd = hrow[kb];
+        h8v xa[16];
+#pragma unroll
+        for (int s = 0; s < 16; ++s) xa[s] = *(const h8v*)(xrow + (size_t)kb * 256 + 16 * s);
+        const float d = f16_to_f32((uint16_t)(hd.x & 0xffffu));
+        const float dmin = f16_to_f32((uint16_t)(hd.x >> 16));
+        float scale[8], mnv[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            uint32_t sc, mn;
+            q4k_dev_scale_min(hd, g, sc, mn);
+            scale[g] = d * (float)sc;
+            mnv[g] = dmin * (float)mn;
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int g = s >> 1, nib = (s >> 1) & 1;
+            const uint2 pw = pc[s >> 2][s & 1];
+            const uint32_t w0 = (nib ? (pw.x >> 4) : pw.x) & 0x0f0f0f0fu;
+            const uint32_t w1 = (nib ? (pw.y >> 4) : pw.y) & 0x0f0f0f0fu;
+            h8v wb;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float q0 = (float)((w0 >> (8 * e)) & 0xffu);
+                const float q1 = (float)((w1 >> (8 * e)) & 0xffu);
+                const float t0 = q0 * scale[g];
+                const float t1 = q1 * scale[g];
+                wb[e] = nv ? (_Float16)(t0 - mnv[g]) : (_Float16)0.0f;
+                wb[4 + e] = nv ? (_Float16)(t1 - mnv[g]) : (_Float16)0.0f;
+            }
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[s], wb, acc, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[wv][r][lane] = acc[r];
+    __syncthreads();
+    // wave w finishes registers r = w, w+KS, ... of every lane
+    for (int r = wv; r < 16; r += KS) {
+        float v;
+        if (KS == 4) {
+            v = (red[0][r][lane] + red[1][r][lane]) + (red[2][r][lane] + red[3][r][lane]);
+        } else {
+            v = ((red[0][r][lane] + red[1][r][lane]) + (red[2][r][lane] + red[3][r][lane])) +
+                ((red[4][r][lane] + red[5][r][lane]) + (red[6][r][lane] + red[7][r][lane]));
+        }
+        const int m = m0 + (r & 3) + 8 * (r >> 2) + 4 * hsel;
+        if (nv && m < a.M) epilogue(a, m, n, v, EPI);
+    }
+}
+
+size_t batched_scratch_bytes(size_t M, size_t K) { return ((M + 31) / 32) * 32 * K * 2; }
+
+template <int PRO>
+static void launch_act16(const FusedGemvArgs& a, int mpad, _Float16* xh, hipStream_t s) {
+    if (a.K <= 1024) hipLaunchKernelGGL((act16_kernel<PRO, 1>), dim3(mpad), dim3(256), 0, s, a, xh);
+    else if (a.K <= 2048) hipLaunchKernelGGL((act16_kernel<PRO, 2>), dim3(mpad), dim3(256), 0, s, a, xh);
+    else if (a.K <= 4096) hipLaunchKernelGGL((act16_kernel<PRO, 4>), dim3(mpad), dim3(256), 0, s, a, xh);
+    else hipLaunchKernelGGL((act16_kernel<PRO, 8>), dim3(mpad), dim3(256), 0, s, a, xh);
+}
+
+hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* scratch, hipStream_t s) {
+    if (w.type != kQ4_K || w.K % 256 || w.K > 8192 || args.M <= 0 || args.M > 64) return hipErrorInvalidValue;
+    if (args.pro == PRO_GATED && args.group != 128) return hipErrorInvalidValue;
+    FusedGemvArgs a = args;
+    a.qs = w.qs;
+    a.hdr = w.hdr;
+    a.K = (int)w.K;
+    a.N = (int)w.N;
+    const int mpad = (a.M + 31) / 32 * 32;
+    _Float16* xh = (_Float16*)scratch;
+    switch (a.pro) {
+    case PRO_RMS: launch_act16<PRO_RMS>(a, mpad, xh, s); break;
+    case PRO_GATED: launch_act16<PRO_GATED>(a, mpad, xh, s); break;
+    case PRO_SILU_MUL: launch_act16<PRO_SILU_MUL>(a, mpad, xh, s); break;
+    case PRO_PLAIN: launch_act16<PRO_PLAIN>(a, mpad, xh, s); break;
+    default: return hipErrorInvalidValue;
+    }
+    // one 32-row weight tile per workgroup, K split over 8 waves when the
+    // matrix has few tiles, else over 4
+    dim3 g((unsigned)((a.N + 31) / 32), (unsigned)(mpad / 32));
+    const bool wide = (a.N + 31) / 32 >= 512;
+    if (a.epi == EPI_RESID) {
+        if (wide) hipLaunchKernelGGL((mfma_q4k_kernel<EPI_RESID, 4>), g, dim3(256), 0, s, a, (const _Float16*)xh);
+        else hipLaunchKernelGGL((mfma_q4k_kernel<EPI_RESID, 8>), g, dim3(512), 0, s, a, (const _Float16*)xh);
+    } else {
+        if (wide) hipLaunchKernelGGL((mfma_q4k_kernel<EPI_STORE, 4>), g, dim3(256), 0, s, a, (const _Float16*)xh);
+        else hipLaunchKernelGGL((mfma_q4k_kernel<EPI_STORE, 8>), g, dim3(512), 0, s, a, (const _Float16*)xh);
+    }
+    return hipGetLastError();
+}
+
 // ============================================================ dispatch
 
 template <int PRO, int EPI>
@@ -626,6 +826,29 @@ __device__ __forceinline__ void kv_ld4<uint16_t>(const uint16_t* p, float (&o)[4
     o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xffff0000u);
 }
 
+// Four consecutive cache elements kept in their storage form until used.
+template <typename KV>
+struct KVPack;
+template <>
+struct KVPack<float> {
+    v4f v;
+    __device__ __forceinline__ void load(const float* p) { v = *(const v4f*)p; }
+    __device__ __forceinline__ void zero() { v = v4f{0.0f, 0.0f, 0.0f, 0.0f}; }
+    __device__ __forceinline__ void unpack(float (&o)[4]) const {
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    }
+};
+template <>
+struct KVPack<uint16_t> {
+    uint2 v;
+    __device__ __forceinline__ void load(const uint16_t* p) { v = *(const uint2*)p; }
+    __device__ __forceinline__ void zero() { v = make_uint2(0u, 0u); }
+    __device__ __forceinline__ void unpack(float (&o)[4]) const {
+        o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xffff0000u);
+        o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xffff0000u);
+    }
+};
+
 // RoPE of one 256-wide head held in LDS, lanes < 32 of a wave
 // (lib.rs:1552-1577: pairs (i, i+32), angle starts at the position and is
 // multiplied by theta_scale per pair, FMA form).
@@ -644,18 +867,12 @@ __device__ __forceinline__ void head_rope(float* hv, const float* sn, const floa
 // K/V at the row's position if it owns that token block, (4) scores its token
 // blocks blockIdx.x, +nblk, ... in the reference's 32-accumulator dot order
 // (see attn_qk_kernel), the position's own token from its copy of the stored
-// key.  The last workgroup of a (row, kv head) to finish (one atomic ticket
-// each, no waiting) reduces the softmax statistics of the G heads
-// (lib.rs:1352-1387: max, GGML exp, 8-wide f32 partials summed in f64,
-// inv = (float)(1/sum)) and resets the ticket.
+// key.
 template <typename KV, int G>
 __global__ __launch_bounds__(256) void attn_decode_qk_kernel(AttnDecodeArgs a) {
     constexpr int D = 256;
     __shared__ float hv[G + 1][D];
     __shared__ float rsin[32], rcos[32];
-    __shared__ float wmax[4][G];
-    __shared__ double wsum[4][G];
-    __shared__ bool last;
     const int kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int p = a.pos[b], T = p + 1;
@@ -667,17 +884,13 @@ __global__ __launch_bounds__(256) void attn_decode_qk_kernel(AttnDecodeArgs a) {
     KV* vc = (KV*)a.vcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D;
     const size_t tstep = (size_t)a.nkv * D;
 
-    float kk[8][4];
+    KVPack<KV> kn[8];  // keys of the next token block, loaded ahead
     auto load_keys = [&](int tb) {
         const int t = tb * 32 + (tid >> 3);
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            if (t < T && t != p) {
-                kv_ld4<KV>(kc + (size_t)t * tstep + 32 * c + 4 * s, kk[c]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) kk[c][e] = 0.0f;
-            }
+            if (t < T && t != p) kn[c].load(kc + (size_t)t * tstep + 32 * c + 4 * s);
+            else kn[c].zero();
         }
     };
     if (blockIdx.x * 32 < T) load_keys(blockIdx.x);
@@ -743,16 +956,21 @@ __global__ __launch_bounds__(256) void attn_decode_qk_kernel(AttnDecodeArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) qv[g][c][e] = hv[g][32 * c + 4 * s + e];
     float* sb = a.scores + (size_t)b * a.score_stride + (size_t)kvh * G * a.head_stride;
-    bool first = true;
     for (int tb = blockIdx.x; tb * 32 < T; tb += nblk) {
-        if (!first) load_keys(tb);
-        first = false;
-        const int t = tb * 32 + (tid >> 3);
-        if (t == p) {
+        KVPack<KV> cur[8];
 #pragma unroll
-            for (int c = 0; c < 8; ++c)
+        for (int c = 0; c < 8; ++c) cur[c] = kn[c];
+        if ((tb + nblk) * 32 < T) load_keys(tb + nblk);
+        const int t = tb * 32 + (tid >> 3);
+        float kk[8][4];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            if (t == p) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) kk[c][e] = hv[G][32 * c + 4 * s + e];
+            } else {
+                cur[c].unpack(kk[c]);
+            }
         }
         float acc[G][4];
 #pragma unroll
@@ -784,92 +1002,75 @@ __global__ __launch_bounds__(256) void attn_decode_qk_kernel(AttnDecodeArgs a) {
         }
     }
 
-    // ---- softmax statistics by the last workgroup of this (row, kv head):
-    // one release per workgroup (after the barrier) before its ticket
-    __syncthreads();
-    if (tid == 0) {
-        __threadfence();
-        last = atomicAdd(&a.tickets[b * a.nkv + kvh], 1u) == (unsigned)nblk - 1;
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    // thread t owns 8-element blocks t, t+256, ... of every head; all loads
-    // of a 4096-token span are issued together
-    float m[G];
-    double sum[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = -INFINITY;
-        sum[g] = 0.0;
-    }
+}
+
+// Grid (q_heads, B): softmax statistics of one head (lib.rs:1352-1387): max,
+// GGML exp, 8-wide f32 partials summed in f64, inv = (float)(1/sum), stored
+// as {max, inv} for the value kernel.  Thread t owns 8-element blocks t,
+// t+256, ...; each pass over a 4096-token span issues its loads together.
+__global__ __launch_bounds__(256) void attn_decode_stats_kernel(AttnDecodeArgs a) {
+    __shared__ float wmax[4];
+    __shared__ double wsum[4];
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int T = a.pos[b] + 1;
+    const float* row = a.scores + (size_t)b * a.score_stride + (size_t)h * a.head_stride;
+    float m = -INFINITY;
+    double sum = 0.0;
     for (int pass = 0; pass < 2; ++pass) {
         for (int base = 0; base < T; base += 4096) {
-            float e[G][2][8];
+            float e[2][8];
 #pragma unroll
-            for (int g = 0; g < G; ++g)
+            for (int r = 0; r < 2; ++r)
 #pragma unroll
-                for (int r = 0; r < 2; ++r)
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const int at = base + 8 * (tid + 256 * r) + i;
-                        e[g][r][i] = at < T ? sb[(size_t)g * a.head_stride + at] : -INFINITY;
-                    }
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int r = 0; r < 2; ++r) {
-                    if (pass == 0) {
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) m[g] = fmaxf(m[g], e[g][r][i]);
-                    } else if (base + 8 * (tid + 256 * r) < T) {
-                        float x[8];
-#pragma unroll
-                        for (int i = 0; i < 8; ++i)
-                            x[i] = base + 8 * (tid + 256 * r) + i < T ? ggml_exp(e[g][r][i] - m[g]) : 0.0f;
-                        const float partial = ((x[0] + x[4]) + (x[2] + x[6])) + ((x[1] + x[5]) + (x[3] + x[7]));
-                        sum[g] += (double)partial;
-                    }
+                for (int i = 0; i < 8; ++i) {
+                    const int at = base + 8 * (tid + 256 * r) + i;
+                    e[r][i] = at < T ? row[at] : -INFINITY;
                 }
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                if (pass == 0) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) m = fmaxf(m, e[r][i]);
+                } else if (base + 8 * (tid + 256 * r) < T) {
+                    float x[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) x[i] = base + 8 * (tid + 256 * r) + i < T ? ggml_exp(e[r][i] - m) : 0.0f;
+                    const float partial = ((x[0] + x[4]) + (x[2] + x[6])) + ((x[1] + x[5]) + (x[3] + x[7]));
+                    sum += (double)partial;
+                }
+            }
         }
         if (pass == 0) {
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float v = wave_max(m[g]);
-                if (lane == 0) wmax[wv][g] = v;
-            }
+            m = wave_max(m);
+            if (lane == 0) wmax[wv] = m;
             __syncthreads();
-#pragma unroll
-            for (int g = 0; g < G; ++g) m[g] = fmaxf(fmaxf(wmax[0][g], wmax[1][g]), fmaxf(wmax[2][g], wmax[3][g]));
+            m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
         }
     }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const double v = wave_sum_xor<double>(sum[g], 64);
-        if (lane == 0) wsum[wv][g] = v;
-    }
+    sum = wave_sum_xor<double>(sum, 64);
+    if (lane == 0) wsum[wv] = sum;
     __syncthreads();
-    if (tid < G) {
-        const int g = tid;
-        const double total = (wsum[0][g] + wsum[1][g]) + (wsum[2][g] + wsum[3][g]);
-        const int h = kvh * G + g;
-        a.stats[((size_t)b * a.nq + h) * 2] = m[g];
+    if (tid == 0) {
+        const double total = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+        a.stats[((size_t)b * a.nq + h) * 2] = m;
         a.stats[((size_t)b * a.nq + h) * 2 + 1] = (float)(1.0 / total);
         if (!(total >= 1.0) || !(total < INFINITY)) atomicOr(a.status, 8);
     }
-    if (tid == 0) a.tickets[b * a.nkv + kvh] = 0u;
 }
 
-// Grid (256/8, kv_heads, B): the value sum of attn_pv_kernel (32 FMA chains
+// Grid (256/32, kv_heads, B): the value sum of attn_pv_kernel (32 FMA chains
 // over tokens per channel, lib.rs:1276-1305) for the G query heads of one kv
-// head, per 2048-token tile: the tile's values and scores are loaded in one
-// go, p = GGML exp(score - max) * inv is staged in LDS, then the chains run;
-// the fixed tree and the sigmoid output gate (forward.rs:751) finish.
+// head.  Lane = channel-quad * 8 + chain % 8, wave = chain / 8: a thread runs
+// chain `a` for 4 adjacent channels (8-byte value loads).  Per 512-token
+// tile the values and scores are loaded in one go, p = GGML exp(score - max)
+// * inv is staged in LDS, the chains advance in token order; the fixed tree
+// and the sigmoid output gate (forward.rs:751) finish.
 template <typename KV, int G>
 __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
-    constexpr int D = 256, TT = 2048, NV = TT / 32;
+    constexpr int D = 256, TT = 512, NV = TT / 32;
     __shared__ float pt[G][TT];
-    __shared__ float red[G][8][33];
+    __shared__ float red[G][32][33];
     const int kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int T = a.pos[b] + 1;
@@ -880,19 +1081,26 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
         mx[g] = a.stats[((size_t)b * a.nq + kvh * G + g) * 2];
         inv[g] = a.stats[((size_t)b * a.nq + kvh * G + g) * 2 + 1];
     }
-    const int ch = lane >> 3, acc_id = wv * 8 + (lane & 7);
-    const int j = blockIdx.x * 8 + ch;
-    const KV* vb = (const KV*)a.vcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D + j;
+    const int cq = lane >> 3, ai = wv * 8 + (lane & 7);
+    const int j0 = blockIdx.x * 32 + cq * 4;
+    const KV* vb = (const KV*)a.vcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D + j0;
     const size_t vstep = (size_t)a.nkv * D;
-    float acc[G];
+    float acc[G][4];
 #pragma unroll
-    for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[g][c] = 0.0f;
     for (int t0 = 0; t0 < T; t0 += TT) {
-        float vv[NV];
+        float vv[NV][4];
 #pragma unroll
         for (int n = 0; n < NV; ++n) {
-            const int t = t0 + acc_id + 32 * n;
-            vv[n] = t < T ? kv_ld<KV>(vb + (size_t)t * vstep) : 0.0f;
+            const int t = t0 + ai + 32 * n;
+            if (t < T) {
+                kv_ld4<KV>(vb + (size_t)t * vstep, vv[n]);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) vv[n][c] = 0.0f;
+            }
         }
         float sv[G * TT / 256];
 #pragma unroll
@@ -908,26 +1116,32 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
         __syncthreads();
 #pragma unroll
         for (int n = 0; n < NV; ++n) {
-            const int tt = acc_id + 32 * n;
+            const int tt = ai + 32 * n;
             if (t0 + tt < T) {
 #pragma unroll
-                for (int g = 0; g < G; ++g) acc[g] = fmaf(vv[n], pt[g][tt], acc[g]);
+                for (int g = 0; g < G; ++g) {
+                    const float pv = pt[g][tt];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[g][c] = fmaf(vv[n][c], pv, acc[g][c]);
+                }
             }
         }
         __syncthreads();
     }
 #pragma unroll
-    for (int g = 0; g < G; ++g) red[g][ch][acc_id] = acc[g];
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) red[g][cq * 4 + c][ai] = acc[g][c];
     __syncthreads();
-    if (tid < G * 8) {
-        const int g = tid >> 3, c = tid & 7;
+    if (tid < G * 32) {
+        const int g = tid >> 5, c = tid & 31;
         const float* r = red[g][c];
         float comb[8];
 #pragma unroll
         for (int l = 0; l < 8; ++l) comb[l] = (r[l] + r[16 + l]) + (r[8 + l] + r[24 + l]);
         const float h0 = comb[0] + comb[4], h1 = comb[1] + comb[5], h2 = comb[2] + comb[6], h3 = comb[3] + comb[7];
         float v = (h0 + h1) + (h2 + h3);
-        const int jj = blockIdx.x * 8 + c, h = kvh * G + g;
+        const int jj = blockIdx.x * 32 + c, h = kvh * G + g;
         const float gate = a.proj[(size_t)b * a.proj_stride + (size_t)h * 2 * D + D + jj];
         v = v * source_sigmoid(gate);
         a.out[(size_t)b * a.out_stride + (size_t)h * D + jj] = v;
@@ -936,9 +1150,13 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
 
 template <typename KV, int G>
 static void launch_attn(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
-    const unsigned nblk = (unsigned)std::min<size_t>((a.max_ctx + 31) / 32, 64);
+    // token blocks per (row, kv head): 64 at batch 1, fewer as rows add
+    // parallelism (each workgroup then pipelines several blocks)
+    const size_t want = B >= 8 ? 8 : 64 / B;
+    const unsigned nblk = (unsigned)std::min<size_t>((a.max_ctx + 31) / 32, want);
     hipLaunchKernelGGL((attn_decode_qk_kernel<KV, G>), dim3(nblk, a.nkv, (unsigned)B), dim3(256), 0, s, a);
-    hipLaunchKernelGGL((attn_decode_pv_kernel<KV, G>), dim3(256 / 8, a.nkv, (unsigned)B), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(attn_decode_stats_kernel, dim3(a.nq, (unsigned)B), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((attn_decode_pv_kernel<KV, G>), dim3(256 / 32, a.nkv, (unsigned)B), dim3(256), 0, s, a);
 }
 
 hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
@@ -963,92 +1181,84 @@ hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
 
 // ================================================== greedy + position
 
-// Grid (kArgBlocks, B).  Each workgroup reduces its slice of the row to
-// (max, first index); the last workgroup to finish a row (one atomic
-// ticket per workgroup, no waiting) reduces the partials, writes the greedy
-// id (core/src/numerics.rs:126-140: first maximum wins, nonfinite is an
-// error -> status bit 2), resets the row's ticket for the next step and,
-// when asked, moves the row's position on.
-constexpr int kArgBlocks = 32;
+// Greedy id per row (core/src/numerics.rs:126-140: first maximum wins,
+// nonfinite is an error -> status bit 2) in two launches: kArgBlocks
+// partial (max, first index) pairs per row, then one wave per row reduces
+// them, writes the id and, when asked, moves the row's position on.
+constexpr int kArgBlocks = 64;
 
-__global__ __launch_bounds__(256) void argmax_step_kernel(const float* __restrict__ logits, int V, size_t ld,
-                                                          uint32_t* __restrict__ greedy, int* __restrict__ status,
-                                                          float* __restrict__ pmax, int* __restrict__ pidx,
-                                                          unsigned* __restrict__ tickets, int* __restrict__ pos,
-                                                          int* __restrict__ ntok, int advance) {
+__device__ __forceinline__ void argmax_merge(float& best, int& bi, float ov, int oi) {
+    if (ov > best || (ov == best && oi < bi)) {
+        best = ov;
+        bi = oi;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ logits, int V, size_t ld,
+                                                             int* __restrict__ status, float* __restrict__ pmax,
+                                                             int* __restrict__ pidx) {
     __shared__ float sv[4];
     __shared__ int si[4];
-    __shared__ bool last;
     const int blk = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int per = (V + kArgBlocks - 1) / kArgBlocks;
+    const int per = ((V + kArgBlocks - 1) / kArgBlocks + 3) & ~3;
     const int lo = blk * per, hi = min(V, lo + per);
     const float* row = logits + (size_t)b * ld;
     float best = -INFINITY;
     int bi = 0x7fffffff;
     bool bad = false;
-    for (int i = lo + tid; i < hi; i += 256) {
-        const float v = row[i];
-        if (!finite_f32(v)) bad = true;
-        if (v > best) {
-            best = v;
-            bi = i;
+    for (int i0 = lo; i0 < hi; i0 += 256 * 4) {
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = i0 + tid + 256 * r;
+            v[r] = i < hi ? row[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = i0 + tid + 256 * r;
+            if (i < hi) {
+                if (!finite_f32(v[r])) bad = true;
+                argmax_merge(best, bi, v[r], i);
+            }
         }
     }
     if (bad) atomicOr(status, 4);
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(best, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        if (ov > best || (ov == best && oi < bi)) {
-            best = ov;
-            bi = oi;
-        }
-    }
+    for (int off = 32; off > 0; off >>= 1) argmax_merge(best, bi, __shfl_xor(best, off, 64), __shfl_xor(bi, off, 64));
     if (lane == 0) {
         sv[wv] = best;
         si[wv] = bi;
     }
     __syncthreads();
     if (tid == 0) {
-        for (int w = 1; w < 4; ++w)
-            if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
-                best = sv[w];
-                bi = si[w];
-            }
+        for (int w = 1; w < 4; ++w) argmax_merge(best, bi, sv[w], si[w]);
         pmax[b * kArgBlocks + blk] = best;
         pidx[b * kArgBlocks + blk] = bi;
-        __threadfence();
-        last = atomicAdd(&tickets[b], 1u) == kArgBlocks - 1;
     }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    if (tid < 64) {
-        float m = tid < kArgBlocks ? __hip_atomic_load(&pmax[b * kArgBlocks + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
-        int mi = tid < kArgBlocks ? __hip_atomic_load(&pidx[b * kArgBlocks + tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0x7fffffff;
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(m, off, 64);
-            const int oi = __shfl_xor(mi, off, 64);
-            if (ov > m || (ov == m && oi < mi)) {
-                m = ov;
-                mi = oi;
-            }
-        }
-        if (tid == 0) {
-            greedy[b] = mi == 0x7fffffff ? 0u : (uint32_t)mi;
-            tickets[b] = 0u;
-            if (advance) {
-                const int np = pos[b] + 1;
-                pos[b] = np;
-                ntok[b] = np + 1;
-            }
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ pmax, const int* __restrict__ pidx,
+                                                          uint32_t* __restrict__ greedy, int* __restrict__ pos,
+                                                          int* __restrict__ ntok, int advance) {
+    const int b = blockIdx.x, lane = threadIdx.x;
+    float m = lane < kArgBlocks ? pmax[b * kArgBlocks + lane] : -INFINITY;
+    int mi = lane < kArgBlocks ? pidx[b * kArgBlocks + lane] : 0x7fffffff;
+    for (int off = 32; off > 0; off >>= 1) argmax_merge(m, mi, __shfl_xor(m, off, 64), __shfl_xor(mi, off, 64));
+    if (lane == 0) {
+        greedy[b] = mi == 0x7fffffff ? 0u : (uint32_t)mi;
+        if (advance) {
+            const int np = pos[b] + 1;
+            pos[b] = np;
+            ntok[b] = np + 1;
         }
     }
 }
 
 hipError_t argmax_step(const float* logits, size_t V, size_t ld, size_t B, uint32_t* greedy, int* status, float* pmax,
                        int* pidx, unsigned* tickets, int* pos, int* ntok, int advance, hipStream_t s) {
-    hipLaunchKernelGGL(argmax_step_kernel, dim3(kArgBlocks, (unsigned)B), dim3(256), 0, s, logits, (int)V, ld, greedy,
-                       status, pmax, pidx, tickets, pos, ntok, advance);
+    (void)tickets;
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgBlocks, (unsigned)B), dim3(256), 0, s, logits, (int)V, ld, status,
+                       pmax, pidx);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)B), dim3(64), 0, s, pmax, pidx, greedy, pos, ntok, advance);
     return hipGetLastError();
 }
 

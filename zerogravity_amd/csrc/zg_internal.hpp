@@ -147,6 +147,10 @@ struct FusedGemvArgs {
 };
 bool fused_gemv_supported(int type, size_t K, size_t N, int pro);
 hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& a, hipStream_t s);
+// Batched rows (M <= 64, Q4_K): the prologue values rounded to f16 into
+// `scratch` (batched_scratch_bytes), then an f16 MFMA GEMM with the epilogue.
+size_t batched_scratch_bytes(size_t M, size_t K);
+hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& a, void* scratch, hipStream_t s);
 
 // GDN decode: conv (4-slot ring per channel) + SiLU + q/k L2 + gates +
 // recurrence for B rows.  proj rows: [qkv (3W) | z (W) | alpha (H) | beta (H)].
@@ -180,16 +184,14 @@ struct AttnDecodeArgs {
     size_t score_stride = 0, head_stride = 0;
     float* out = nullptr;
     size_t out_stride = 0;
-    int* status = nullptr;      // bit 3: degenerate softmax sum
-    unsigned* tickets = nullptr;  // [B][nkv], zero between steps
-    float* stats = nullptr;       // [B][nq][2] softmax max, 1/sum
+    int* status = nullptr;  // bit 3: degenerate softmax sum
+    float* stats = nullptr;  // [B][nq][2] softmax {max, 1/sum}
     int nq = 0, nkv = 0, max_ctx = 0;
 };
 hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s);
 
-// Greedy ids of B logit rows (leading dimension ld) with a per-row ticket
-// (tickets[B], zero between steps) and partials [argmax_partials(B)]; when
-// `advance`, the last workgroup of a row also moves pos/ntok on.
+// Greedy ids of B logit rows (leading dimension ld) through partials
+// [argmax_partials(B)]; when `advance`, pos/ntok move on (tickets unused).
 size_t argmax_partials(size_t B);
 hipError_t argmax_step(const float* logits, size_t V, size_t ld, size_t B, uint32_t* greedy, int* status, float* pmax,
                        int* pidx, unsigned* tickets, int* pos, int* ntok, int advance, hipStream_t s);

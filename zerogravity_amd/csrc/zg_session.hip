@@ -57,10 +57,11 @@ struct zg_session {
     // device buffers
     std::vector<void*> allocs;
     int *d_pos = nullptr, *d_ntok = nullptr, *d_status = nullptr, *pidx = nullptr;
-    unsigned *tickets = nullptr, *att_tickets = nullptr;
+    unsigned* tickets = nullptr;
     uint32_t *d_tokens = nullptr, *d_greedy = nullptr;
     float *x = nullptr, *y0 = nullptr, *core = nullptr, *ao = nullptr, *logits = nullptr, *scores = nullptr,
           *pmax = nullptr, *att_stats = nullptr;
+    void* xh = nullptr;  // f16 activations of the batched (B > 4) projections
     size_t y0w = 0;
     std::vector<float*> ring, rec;  // per GDN layer: conv ring [B][3W][4], state [B][H][128][128]
     std::vector<void*> kc, vc;      // per attention layer: [B][max_ctx][kv_heads*256]
@@ -168,6 +169,9 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
         f.y = y;
         f.ldy = ldy;
         f.status = s->d_status;
+        // one launch with the prologue in-kernel up to 4 rows; beyond, the
+        // activation in f16 and the MFMA GEMM (weights read once)
+        if (B > 4 && w->dw.type == zg::kQ4_K) return zg::batched_gemv(w->dw, f, s->xh, st);
         return zg::fused_gemv(w->dw, f, st);
     };
     ZG_HIP(zg::embed(m->embd->dw, tokens, s->x, B, s->d_status, st));
@@ -213,7 +217,6 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             a.out = s->ao;
             a.out_stride = QD;
             a.status = s->d_status;
-            a.tickets = s->att_tickets;
             a.stats = s->att_stats;
             a.nq = (int)g.q_heads;
             a.nkv = (int)g.kv_heads;
@@ -427,9 +430,9 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     A((void**)&s->d_tokens, B * 4);
     A((void**)&s->d_greedy, B * 4);
     A((void**)&s->tickets, B * 4);
-    A((void**)&s->att_tickets, B * g.kv_heads * 4);
-    A((void**)&s->att_stats, B * g.q_heads * 2 * 4);
     A((void**)&s->pmax, zg::argmax_partials(B) * 4);
+    A((void**)&s->att_stats, B * g.q_heads * 2 * 4);
+    A(&s->xh, zg::batched_scratch_bytes(B, std::max({H, F, W, QD})));
     A((void**)&s->pidx, zg::argmax_partials(B) * 4);
     A((void**)&s->x, B * H * 4);
     A((void**)&s->y0, B * s->y0w * 4);
@@ -491,7 +494,6 @@ int zg_session_reset(zg_session* s) {
     }
     ZG_HIP(hipMemsetAsync(s->d_status, 0, 4, ctx->stream));
     ZG_HIP(hipMemsetAsync(s->tickets, 0, B * 4, ctx->stream));
-    ZG_HIP(hipMemsetAsync(s->att_tickets, 0, B * g.kv_heads * 4, ctx->stream));
     ZG_HIP(hipStreamSynchronize(ctx->stream));
     std::fill(s->pos.begin(), s->pos.end(), 0);
     s->pos_dirty = true;
