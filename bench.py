@@ -52,8 +52,10 @@ def gemv_bytes(kind, N, K, M):
 # ------------------------------------------------------------------ decode
 
 def decode_matrices(g):
-    """(name, K, N) of every quantized matrix one decode step streams, in
-    launch order (model-qwen35/src/forward.rs layer schedule + tied LM head)."""
+    """The projections one decode step streams, in launch order, as the
+    resident model registers them: (label, [tensor names stacked by rows], K,
+    N).  Inputs shared by several GGUF matrices are one stacked launch
+    (model-qwen35/src/forward.rs layer schedule + tied LM head)."""
     H, F, V = g["hidden"], g["ffn"], g["vocab"]
     W = g["gdn_heads"] * g["gdn_dim"]
     QD, KD = g["q_heads"] * g["head_dim"], g["kv_heads"] * g["head_dim"]
@@ -61,14 +63,16 @@ def decode_matrices(g):
     for i in range(g["layers"]):
         p = f"blk.{i}."
         if (i + 1) % g["full_attention_interval"] == 0:
-            out += [(p + "attn_q.weight", H, 2 * QD), (p + "attn_k.weight", H, KD), (p + "attn_v.weight", H, KD),
-                    (p + "attn_output.weight", QD, H)]
+            out.append((p + "attn_in", [p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"], H,
+                        2 * QD + 2 * KD))
+            out.append((p + "attn_output", [p + "attn_output.weight"], QD, H))
         else:
-            out += [(p + "attn_qkv.weight", H, 3 * W), (p + "attn_gate.weight", H, W),
-                    (p + "ssm_alpha.weight", H, g["gdn_heads"]), (p + "ssm_beta.weight", H, g["gdn_heads"]),
-                    (p + "ssm_out.weight", W, H)]
-        out += [(p + "ffn_gate.weight", H, F), (p + "ffn_up.weight", H, F), (p + "ffn_down.weight", F, H)]
-    out.append(("token_embd.weight", H, V))
+            out.append((p + "gdn_in", [p + "attn_qkv.weight", p + "attn_gate.weight", p + "ssm_alpha.weight",
+                                       p + "ssm_beta.weight"], H, 4 * W + 2 * g["gdn_heads"]))
+            out.append((p + "ssm_out", [p + "ssm_out.weight"], W, H))
+        out.append((p + "ffn_gate_up", [p + "ffn_gate.weight", p + "ffn_up.weight"], H, 2 * F))
+        out.append((p + "ffn_down", [p + "ffn_down.weight"], F, H))
+    out.append(("token_embd", ["token_embd.weight"], H, V))
     return out
 
 
@@ -76,7 +80,7 @@ def step_bytes(g, kind, B, T):
     """Algorithmic HBM bytes of one decode step at B rows, T cached tokens:
     every weight once, GDN state read+write and conv history per row, K and
     V of T tokens (bf16) per attention layer and row, activations ignored."""
-    w = sum(N * K * BPE[kind] for _, K, N in decode_matrices(g))
+    w = sum(N * K * BPE[kind] for _, _, K, N in decode_matrices(g))
     W = g["gdn_heads"] * g["gdn_dim"]
     n_attn = g["layers"] // g["full_attention_interval"]
     n_gdn = g["layers"] - n_attn
@@ -120,36 +124,32 @@ def run_decode(model, torch, B, prefix, steps, warmup, seed):
 
 def gemv_leg(kern, torch, g, tensors, kind, reps):
     """The dominant kernel: the Q4_K dequant-GEMV launches of one B=1 decode
-    step (every quantized matrix of the model in launch order, ~0.95 GB, so
-    nothing is served from the 256 MB Infinity Cache), replayed `reps` times
-    with HIP events around each replay."""
+    step -- the same stacked matrices and the same fused kernel (activation
+    prologue in-kernel, f32 activation, RMSNorm) -- replayed `reps` times
+    with HIP events around each replay.  ~0.95 GB per replay, so nothing is
+    served from the 256 MB Infinity Cache."""
     from zerogravity_amd import _lib as L
     lib, ctx = L.lib(), kern.ctx
-    mats = decode_matrices(g)
     handles = []
-    for name, K, N in mats:
-        ty, s0, s1, data = tensors[name]
-        assert ty == kind and s0 == K and s1 == N, name
-        handles.append((kern.register(4243, "leg." + name, kind, K, N, data), K, N))
+    for label, names, K, N in decode_matrices(g):
+        parts = [tensors[n] for n in names]
+        assert all(p[0] == kind and p[1] == K for p in parts), label
+        data = np.concatenate([p[3] for p in parts])
+        handles.append((kern.register(4243, "leg." + label, kind, K, N, data), K, N))
     s = torch.cuda.current_stream()
     rng = np.random.default_rng(7)
-    preps = {}
-    for h, K, N in handles:
-        if K not in preps:
-            from zerogravity_amd import synth
-            _, xb = synth.bf16_round(rng.standard_normal((1, K)).astype(np.float32))
-            x_d = torch.from_numpy(xb.view(np.int16)).cuda()
-            g_d = torch.ones(K, dtype=torch.float32, device="cuda")
-            nb = lib.zg_act_prepared_bytes(h.h, 1)
-            prep = torch.empty(nb, dtype=torch.uint8, device="cuda")
-            ctx.check(lib.zg_act_prepare_device(ctx.h, h.h, x_d.data_ptr(), L.BF16, 1, g_d.data_ptr(), 1e-6,
-                                                prep.data_ptr(), nb, s.cuda_stream))
-            preps[K] = (prep, x_d, g_d)
+    xs = {}
+    for _, K, _ in handles:
+        if K not in xs:
+            xs[K] = (torch.from_numpy(rng.standard_normal(K).astype(np.float32)).cuda(),
+                     torch.from_numpy((1 + 0.1 * rng.standard_normal(K)).astype(np.float32)).cuda())
     y = torch.empty(max(N for _, _, N in handles), dtype=torch.float32, device="cuda")
 
     def replay():
         for h, K, N in handles:
-            ctx.check(lib.zg_gemv_prepared_device(ctx.h, h.h, 1, preps[K][0].data_ptr(), y.data_ptr(), s.cuda_stream))
+            x_d, g_d = xs[K]
+            ctx.check(lib.zg_gemv_device(ctx.h, h.h, x_d.data_ptr(), L.F32, 1, g_d.data_ptr(), 1e-6, y.data_ptr(),
+                                         s.cuda_stream))
 
     replay()
     torch.cuda.synchronize()
@@ -235,7 +235,7 @@ def bench_decode(args):
                    "b32_tok_s": round(res[32]["tok_s"], 1)},
         "roofline": {"bound": "hbm", "achieved": round(leg["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(leg["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_q4k_kernel (decode-step launches, B=1)",
+                     "kernel": "fused_q4k_kernel (the B=1 decode step's stacked projections, one launch each)",
                      "bytes_per_launch": round(leg["bytes_per_launch"]), "us_per_launch": round(leg["us_per_launch"], 3)},
     }
     if not args.no_cpu:

@@ -246,6 +246,10 @@ int zg_session_fill_random(zg_session* s, size_t rows, size_t prefix, uint64_t s
  * or f32 (ZG_F32), row-major [M][columns]; gamma (device, [columns]) applies
  * the RMSNorm prologue of lib.rs:263-284 when non-NULL; y is f32.  Runs on
  * `stream` (hipStream_t) or the ctx stream when NULL; asynchronous.  M <= 64.
+ * f32 activations run the decode step's own kernels: one launch with the
+ * prologue inside for M <= 4 (Q8_0 bit-identical to the CPU), and for Q4_K
+ * with M > 4 the activation rounded to f16 and an f16 MFMA GEMM (f32
+ * accumulate; within 1e-3 relative of the CPU).
  * No counterpart in the reference beyond MatVecKernel::try_execute; this is
  * the resident form the whole-program provider uses. */
 int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows,

@@ -124,6 +124,36 @@ def test_gemv_device_rms_prologue_bf16(kern, torch_cuda, kind, N, K, M):
     assert worst <= REL_TOL, worst
 
 
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("N,K", [(3584, 1024), (2048, 6144), (151936, 2048)])
+@pytest.mark.parametrize("M", [1, 3, 16, 32])
+def test_gemv_device_f32_decode_kernels(kern, torch_cuda, kind, N, K, M):
+    """f32 activations take the decode-step kernels (in-kernel RMS prologue;
+    Q4_K beyond 4 rows on the f16 MFMA path)."""
+    torch = torch_cuda
+    w, h = weight(kern, kind, N, K)
+    rng = np.random.default_rng(M * 11 + N)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    x_d = torch.from_numpy(x).cuda()
+    g_d = torch.from_numpy(gamma).cuda()
+    y_d = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    stream = _stream(torch)
+    kern.ctx.check(L.lib().zg_gemv_device(kern.ctx.h, h.h, x_d.data_ptr(), L.F32, M, g_d.data_ptr(), 1e-6,
+                                          y_d.data_ptr(), stream))
+    torch.cuda.synchronize()
+    y = y_d.cpu().numpy()
+    worst = 0.0
+    for m in range(M):
+        xn = O.rms_norm(x[m], gamma, 1e-6)
+        for rows in row_subset(N):
+            ref = O.matvec(kind, w[rows].reshape(-1), rows.size, K, xn)
+            if kind == synth.Q8_0:
+                assert np.array_equal(y[m, rows].view(np.uint32), ref.view(np.uint32)), m
+            worst = max(worst, rel_err(y[m, rows], ref))
+    assert worst <= REL_TOL, worst
+
+
 def test_q8_activation_codes_bit_exact(kern, torch_cuda):
     # The prepared Q8_0 activation (RMSNorm + dynamic coding) must equal the
     # oracle's codes and f16-rounded scales bit for bit.

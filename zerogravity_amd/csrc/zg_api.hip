@@ -410,8 +410,34 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
     (void)hipSetDevice(ctx->device);
     if (!w || !x || !y || (x_dtype != ZG_BF16 && x_dtype != ZG_F32)) return fail(ctx, ZG_E_MALFORMED, "invalid gemv arguments");
     if (!zg::gemv_supported(w->dw.type, w->dw.K, m_rows)) return fail(ctx, ZG_UNSUPPORTED, "geometry not offered");
-    const size_t need = zg::prepared_bytes(w->dw.type, m_rows, w->dw.K);
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    const int pro = gamma ? zg::PRO_RMS : zg::PRO_PLAIN;
+    if (x_dtype == ZG_F32 && zg::fused_gemv_supported(w->dw.type, w->dw.K, w->dw.N, pro)) {
+        // f32 activations: the decode-step kernels themselves (activation
+        // prologue in-kernel up to 4 rows, f16 MFMA beyond for Q4_K)
+        zg::FusedGemvArgs f;
+        f.M = (int)m_rows;
+        f.pro = pro;
+        f.epi = zg::EPI_STORE;
+        f.x = (const float*)x;
+        f.ldx = w->dw.K;
+        f.gamma = gamma;
+        f.eps = eps;
+        f.y = y;
+        f.ldy = w->dw.N;
+        f.status = ctx->d_flag;
+        if (m_rows > 4 && w->dw.type == zg::kQ4_K) {
+            const size_t need = zg::batched_scratch_bytes(m_rows, w->dw.K);
+            if (ctx->actbuf.bytes < need) ZG_HIP(hipStreamSynchronize(s));
+            int rc = ensure(ctx, ctx->actbuf, need);
+            if (rc) return rc;
+            ZG_HIP(zg::batched_gemv(w->dw, f, ctx->actbuf.ptr, s));
+        } else {
+            ZG_HIP(zg::fused_gemv(w->dw, f, s));
+        }
+        return ZG_COMPLETED;
+    }
+    const size_t need = zg::prepared_bytes(w->dw.type, m_rows, w->dw.K);
     if (ctx->actbuf.bytes < need) {
         // Growing the buffer must not race work still queued on the caller stream.
         ZG_HIP(hipStreamSynchronize(s));
