@@ -146,6 +146,31 @@ int zg_gdn_coefficients(zg_ctx* ctx, const float* alpha, const float* beta, cons
 int zg_gdn_recurrent(zg_ctx* ctx, size_t width, size_t heads, const float* q, const float* k, const float* v,
                      const float* coefficients, const float* state, float* output, float* state_out);
 
+/* Chunked (WY/UT) GDN prefill over one chunk: replaces
+ * numerics/torch_cpu/gdn/chunk/core.rs:69-274 (`core(ChunkInputs)`), with
+ * its checks (:86-116).  rows 1..64; heads a multiple of 16, at most 48;
+ * query/key/value [rows][heads][128] and beta [rows][heads] bf16-exact f32;
+ * beta in [0, 1]; log_decay [rows][heads] finite and <= 0; previous_state
+ * key-major [heads][128 key][128 value] or NULL for zero.  output_bf16
+ * [rows][heads][128] is the core output rounded to bf16 (gdn.rs:69-76);
+ * state_out key-major.  ZG_E_MALFORMED on a failed check. */
+int zg_gdn_chunk(zg_ctx* ctx, size_t rows, size_t heads, const float* query, const float* key, const float* value,
+                 const float* beta, const float* log_decay, const float* previous_state, float* output_bf16,
+                 float* state_out);
+
+/* Multi-chunk prefill on device buffers and the caller's stream (the same
+ * kernels as zg_gdn_chunk; no reference counterpart takes more than one
+ * chunk per call, core.rs:89).  Chunks of 64 tokens in order; query, key,
+ * value, output [tokens][heads][128] f32; beta, log_decay [tokens][heads];
+ * state value-major [heads][128 value][128 key] (the decode recurrence's
+ * layout, lib.rs:81-83), updated in place; output f32 before rounding.
+ * Inputs are not inspected on the host.  zg_gdn_chunk_scratch_bytes is the
+ * size of the context-owned record buffer a call of this size uses. */
+size_t zg_gdn_chunk_scratch_bytes(size_t tokens, size_t heads);
+int zg_gdn_chunk_prefill_device(zg_ctx* ctx, size_t tokens, size_t heads, const float* query, const float* key,
+                                const float* value, const float* beta, const float* log_decay, float* state,
+                                float* output, void* stream);
+
 /* RopeKvRegion (accelerator.rs:205-296) -> try_rope_kv; source_rope_kv
  * (lib.rs:1552-1577).  Returns the rotated query and key and the unchanged
  * value slab. */

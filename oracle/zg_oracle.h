@@ -97,7 +97,9 @@ int zgo_attention_value(const float* probs, const float* values, size_t tokens,
 int zgo_greedy(const float* logits, size_t n, uint32_t* out);
 
 /* Chunked (WY/UT) GDN prefill restated from the Torch-profile chunk reference,
- * numerics/torch_cpu/gdn/chunk/core.rs:152-363.  Key-major state [h][k][v]. */
+ * numerics/torch_cpu/gdn/chunk/core.rs:152-363.  q, k, v: [tokens][heads][d];
+ * beta, log_decay: [tokens][heads]; state in/out value-major [h][v][k] (the
+ * decode recurrence's layout, lib.rs:81-83), key-major [k][v] inside. */
 int zgo_gdn_chunk_prefill(const float* q, const float* k, const float* v, const float* beta,
                           const float* log_decay, size_t tokens, size_t heads, size_t d,
                           size_t chunk, float* state, float* out);

@@ -156,6 +156,7 @@ void zg_ctx_destroy(zg_ctx* ctx) {
         ctx->weights.clear();
         if (ctx->scratch.ptr) (void)hipFree(ctx->scratch.ptr);
         if (ctx->actbuf.ptr) (void)hipFree(ctx->actbuf.ptr);
+        if (ctx->chunkbuf.ptr) (void)hipFree(ctx->chunkbuf.ptr);
         if (ctx->d_flag) (void)hipFree(ctx->d_flag);
         (void)hipStreamDestroy(ctx->stream);
     }

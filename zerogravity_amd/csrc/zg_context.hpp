@@ -28,6 +28,7 @@ struct zg_ctx {
     std::map<std::tuple<uint64_t, std::string, int, size_t, size_t>, std::unique_ptr<zg_weight>> weights;
     DeviceBuffer scratch;    // region calls: inputs/outputs staged here
     DeviceBuffer actbuf;     // zg_gemv_device: prepared activations
+    DeviceBuffer chunkbuf;   // zg_gdn_chunk_prefill_device: per-(chunk, head) records
     int* d_flag = nullptr;
 };
 

@@ -190,6 +190,16 @@ struct AttnDecodeArgs {
 };
 hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s);
 
+// Chunked GDN prefill (zg_prefill.hip), d = 128, chunk 64: q, k, v
+// [T][H][128], beta and log decay [T][H], state [H][128][128] updated in
+// place (value-major [h][v][k], or [h][k][v] with key_major), out
+// [T][H][128] (before the gated norm; bf16-rounded with round_bf16); scratch
+// of gdn_chunk_scratch_bytes(T, H).
+size_t gdn_chunk_scratch_bytes(size_t T, size_t H);
+hipError_t gdn_chunk_prefill(const float* q, const float* k, const float* v, const float* beta, const float* logd,
+                             size_t T, size_t H, float* state, float* out, float* scratch, bool key_major,
+                             bool round_bf16, hipStream_t s);
+
 // Greedy ids of B logit rows (leading dimension ld) through partials
 // [argmax_partials(B)]; when `advance`, pos/ntok move on (tickets unused).
 size_t argmax_partials(size_t B);

@@ -112,6 +112,96 @@ int zg_gdn_recurrent(zg_ctx* ctx, size_t width, size_t heads, const float* q, co
     return ZG_COMPLETED;
 }
 
+// The chunk (WY/UT) GDN step of numerics/torch_cpu/gdn/chunk/core.rs:69-274
+// over one chunk of rows <= 64, with core()'s input checks (:86-116):
+// heads a multiple of 16 and at most 48, q/k/v bf16-exact and finite, beta in
+// [0, 1], log decay finite and <= 0, prior state finite.  State key-major
+// [heads][128][128]; outputs rounded to bf16 (gdn.rs:69-76).
+int zg_gdn_chunk(zg_ctx* ctx, size_t rows, size_t heads, const float* query, const float* key, const float* value,
+                 const float* beta, const float* log_decay, const float* previous_state, float* output_bf16,
+                 float* state_out) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    const size_t W = 128;
+    if (!query || !key || !value || !beta || !log_decay || !output_bf16 || !state_out || rows < 1 || rows > 64 ||
+        heads == 0 || heads > 48 || heads % 16 != 0)
+        return fail(ctx, ZG_E_MALFORMED, "source chunk grouped input/state geometry");
+    const size_t n = rows * heads * W, nb = rows * heads, ns = heads * W * W;
+    auto bf16_exact = [](const float* x, size_t m) {
+        for (size_t i = 0; i < m; ++i) {
+            uint32_t b;
+            std::memcpy(&b, &x[i], 4);
+            if (!std::isfinite(x[i]) || (b & 0xffffu) != 0) return false;
+        }
+        return true;
+    };
+    bool ok = bf16_exact(query, n) && bf16_exact(key, n) && bf16_exact(value, n) && bf16_exact(beta, nb);
+    for (size_t i = 0; ok && i < nb; ++i) ok = beta[i] >= 0.0f && beta[i] <= 1.0f;
+    for (size_t i = 0; ok && i < nb; ++i) ok = std::isfinite(log_decay[i]) && log_decay[i] <= 0.0f;
+    if (ok && previous_state) ok = all_finite(previous_state, ns);
+    // the f64 cumulative decay must stay finite once rounded to f32 (finite
+    // inputs cannot publish an overflowing cumsum)
+    for (size_t h = 0; ok && h < heads; ++h) {
+        double running = 0.0;
+        for (size_t t = 0; ok && t < rows; ++t) {
+            running += (double)log_decay[t * heads + h];
+            ok = std::isfinite((float)running);
+        }
+    }
+    if (!ok) return fail(ctx, ZG_E_MALFORMED, "source chunk BF16/decay/state operands");
+    const size_t oq = 0, ok_ = align256(n * 4), ov = ok_ + align256(n * 4), ob = ov + align256(n * 4),
+                 ol = ob + align256(nb * 4), os = ol + align256(nb * 4), oo = os + align256(ns * 4),
+                 osc = oo + align256(n * 4);
+    int rc = ensure(ctx, ctx->scratch, osc + zg::gdn_chunk_scratch_bytes(rows, heads));
+    if (rc) return rc;
+    char* b = (char*)ctx->scratch.ptr;
+    hipStream_t st = ctx->stream;
+    ZG_HIP(hipMemcpyAsync(b + oq, query, n * 4, hipMemcpyHostToDevice, st));
+    ZG_HIP(hipMemcpyAsync(b + ok_, key, n * 4, hipMemcpyHostToDevice, st));
+    ZG_HIP(hipMemcpyAsync(b + ov, value, n * 4, hipMemcpyHostToDevice, st));
+    ZG_HIP(hipMemcpyAsync(b + ob, beta, nb * 4, hipMemcpyHostToDevice, st));
+    ZG_HIP(hipMemcpyAsync(b + ol, log_decay, nb * 4, hipMemcpyHostToDevice, st));
+    if (previous_state)
+        ZG_HIP(hipMemcpyAsync(b + os, previous_state, ns * 4, hipMemcpyHostToDevice, st));
+    else
+        ZG_HIP(hipMemsetAsync(b + os, 0, ns * 4, st));
+    ZG_HIP(zg::gdn_chunk_prefill((const float*)(b + oq), (const float*)(b + ok_), (const float*)(b + ov),
+                                 (const float*)(b + ob), (const float*)(b + ol), rows, heads, (float*)(b + os),
+                                 (float*)(b + oo), (float*)(b + osc), true, true, st));
+    ZG_HIP(hipMemcpyAsync(output_bf16, b + oo, n * 4, hipMemcpyDeviceToHost, st));
+    ZG_HIP(hipMemcpyAsync(state_out, b + os, ns * 4, hipMemcpyDeviceToHost, st));
+    ZG_HIP(hipStreamSynchronize(st));
+    if (!all_finite(output_bf16, n) || !all_finite(state_out, ns))
+        return fail(ctx, ZG_E_MALFORMED, "diagnostic GDN BF16 overflow");
+    return ZG_COMPLETED;
+}
+
+size_t zg_gdn_chunk_scratch_bytes(size_t tokens, size_t heads) { return zg::gdn_chunk_scratch_bytes(tokens, heads); }
+
+// Multi-chunk prefill over device buffers on the caller's stream: chunks of
+// 64 tokens in order, state value-major [heads][128][128] in place, f32
+// outputs.  The per-(chunk, head) records live in the context's buffer,
+// grown (after a stream synchronisation) when a longer prompt arrives.
+int zg_gdn_chunk_prefill_device(zg_ctx* ctx, size_t tokens, size_t heads, const float* query, const float* key,
+                                const float* value, const float* beta, const float* log_decay, float* state,
+                                float* output, void* stream) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!query || !key || !value || !beta || !log_decay || !state || !output || tokens == 0 || heads == 0 ||
+        tokens > (1u << 24) || heads > 4096)
+        return fail(ctx, ZG_E_MALFORMED, "chunk prefill geometry");
+    hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
+    const size_t need = zg::gdn_chunk_scratch_bytes(tokens, heads);
+    if (ctx->chunkbuf.bytes < need) ZG_HIP(hipStreamSynchronize(st));
+    int rc = ensure(ctx, ctx->chunkbuf, need);
+    if (rc) return rc;
+    ZG_HIP(zg::gdn_chunk_prefill(query, key, value, beta, log_decay, tokens, heads, state, output,
+                                 (float*)ctx->chunkbuf.ptr, false, false, st));
+    return ZG_COMPLETED;
+}
+
 int zg_rope_kv(zg_ctx* ctx, const float* query, const float* key, const float* value, size_t head_width,
                size_t query_heads, size_t kv_heads, size_t rotate, size_t position, float theta_scale, float* query_out,
                float* key_out, float* value_out) {
