@@ -10,6 +10,9 @@ Workloads (synthetic, seeded random-init weights in the named GGUF codec):
   gemv   dequant-GEMV sweep (Q8_0/Q4_K, M in {1,4,16,32}) with the RMSNorm
          prologue; weights rotate across distinct buffers totalling > 2x the
          256 MB Infinity Cache.
+  prefill chunked GDN prefill of one layer's core (H=16, d=128, chunks of
+         64) at L=2048 and L=8192 from a zero state; value = L=8192 tokens/s,
+         roofline against the f32 MFMA peak the kernels compute on.
 
 Every timed region uses HIP events recorded on the stream the kernels are
 launched on (a non-null torch stream at default priority).
@@ -348,12 +351,117 @@ def bench_gemv(args):
     return line
 
 
+# ----------------------------------------------------------------- prefill
+
+F32_MFMA_PEAK_TFLOPS = 157.3
+PREFILL_C, PREFILL_D = 64, 128
+
+
+def prefill_flops_per_chunk_head():
+    """Algorithmic multiply-adds of one 64-token chunk of one head (C = 64,
+    d = 128), counted as the chunk reference computes them
+    (numerics/torch_cpu/gdn/chunk/core.rs:152-274): A and intra (C x C x d
+    each, full squares), the two unit-lower solves (C(C-1)/2 x d each), W S
+    and dq S (C x d x d each), intra corr (C x d x C) and the state update
+    dk^T corr (d x d x C).  Two flops per multiply-add."""
+    C, d = PREFILL_C, PREFILL_D
+    macs = 2 * C * C * d + 2 * (C * (C - 1) // 2) * d + 2 * C * d * d + C * d * C + d * d * C
+    return 2 * macs
+
+
+def prefill_inputs(torch, T, H, seed):
+    """Config 4's synthetic distribution on the device: bf16-exact q, k, v,
+    beta = sigmoid(N(0,1)) (bf16-exact), log decay = -softplus(N(0,1)) *
+    exp(N(0,0.5)), zero initial state."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    n = T * H * PREFILL_D
+    q, k, v = (torch.randn(n, device="cuda", generator=g).bfloat16().float() for _ in range(3))
+    beta = torch.sigmoid(torch.randn(T * H, device="cuda", generator=g)).bfloat16().float()
+    a, b = torch.randn(T * H, device="cuda", generator=g), torch.randn(T * H, device="cuda", generator=g)
+    logd = (-torch.nn.functional.softplus(a) * torch.exp(0.5 * b)).clamp(max=0.0)
+    return q, k, v, beta, logd
+
+
+def cpu_prefill_baseline(T, H, seconds):
+    """The oracle's chunk prefill (one host thread) on L = T tokens of H heads."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import zg_oracle as O
+    rng = np.random.default_rng(3)
+    n = T * H * PREFILL_D
+    q, k, v = (rng.standard_normal(n).astype(np.float32) for _ in range(3))
+    beta = (1 / (1 + np.exp(-rng.standard_normal(T * H)))).astype(np.float32)
+    logd = (-np.log1p(np.exp(rng.standard_normal(T * H)))).astype(np.float32)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        O.gdn_chunk_prefill(q, k, v, beta, logd, H, PREFILL_D, PREFILL_C)
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    return T / dt, 1, f"L={T} tokens x {H} heads, {reps} pass(es) of the oracle chunk prefill"
+
+
+def bench_prefill(args):
+    import torch
+    from zerogravity_amd import _lib as L
+    from zerogravity_amd import chunk as CH
+    ctx = L.Context(0)
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    H = 16
+    results = []
+    for T in (2048, 8192):
+        q, k, v, beta, logd = prefill_inputs(torch, T, H, 4 + T)
+        state = torch.zeros(H * PREFILL_D * PREFILL_D, device="cuda")
+        out = torch.empty(T * H * PREFILL_D, device="cuda")
+        torch.cuda.synchronize()
+
+        def launch():
+            state.zero_()
+            CH.prefill_device(ctx, T, H, q, k, v, beta, logd, state, out, stream.cuda_stream)
+
+        for _ in range(args.warmup):
+            launch()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            launch()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        chunks = (T + PREFILL_C - 1) // PREFILL_C
+        tflops = chunks * H * prefill_flops_per_chunk_head() / (ms * 1e-3) / 1e12
+        log(f"prefill L={T} H={H}: {ms * 1e3:9.1f} us/call  {T / ms * 1e3:12.0f} tok/s  {tflops:7.2f} TFLOP/s "
+            f"({tflops / F32_MFMA_PEAK_TFLOPS:.1%} of f32 MFMA peak)")
+        results.append(dict(L=T, H=H, us=round(ms * 1e3, 2), tok_s=round(T / ms * 1e3, 1),
+                            tflops=round(tflops, 3)))
+    head = results[-1]
+    line = {
+        "metric": "chunked GDN prefill tokens/s (one GDN layer's core, L=8192, H=16, d=128, C=64)",
+        "value": head["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": head["us"] / 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded bf16-exact q/k/v, sigmoid beta, softplus decay)",
+        "config": {"workload": "chunked GDN prefill", "sweep": results},
+        "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(head["tflops"] / F32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
+    }
+    if not args.no_cpu:
+        v, cores, sample = cpu_prefill_baseline(2048, H, args.cpu_seconds)
+        line["cpu_baseline"] = {"value": round(v, 2), "unit": "tok/s", "cores": cores, "kind": "port",
+                                "sample": sample}
+    ctx.close()
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="decode", choices=["decode", "gemv"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "prefill"])
     ap.add_argument("--prefix", type=int, default=2048)
     ap.add_argument("--leg-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -363,7 +471,8 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU would run its own "
               "sessions; see the sharding notes in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
-    line = bench_decode(args) if args.workload == "decode" else bench_gemv(args)
+    bench = {"decode": bench_decode, "gemv": bench_gemv, "prefill": bench_prefill}[args.workload]
+    line = bench(args)
     print(json.dumps(line), flush=True)
 
 

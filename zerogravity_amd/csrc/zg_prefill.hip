@@ -14,13 +14,21 @@
 //   o     =  intra corr + (q .* exp(g)) S
 //   S     <- (k .* exp(g_last - g))^T corr + exp(g_last) S
 //
-// Two launches.  gdn_chunk_prep_kernel runs every (chunk, head) in parallel:
-// normalisation, gates, A and intra on f32 MFMA (16x16x4), and the unit-lower
-// solves, one column per thread in the reference's summation order.  It
-// writes U, W, dq, dk, intra and exp(g_last) to a scratch record per
-// (chunk, head).  gdn_chunk_scan_kernel carries the state: workgroup
-// (value slab of 32 columns, head) walks the chunks in order (the value
-// columns of S evolve independently) with every product on f32 MFMA.
+// Four launches.  gdn_chunk_prep_kernel runs every (chunk, head) in
+// parallel: normalisation, gates, A and intra on f32 MFMA (16x16x4), dq, dk
+// and exp(g_last), into a record per (chunk, head); gdn_chunk_solve_kernel
+// solves for U and W, one column per thread in the reference's summation
+// order.  gdn_chunk_scan_kernel carries the state through the chunks
+// in order, one workgroup per (head, 16-column value slab) since the value
+// columns of S evolve independently: per chunk only W S, corr = U - W S and
+// the state update, storing corr and the state entering the chunk.
+// gdn_chunk_out_kernel then forms o = intra corr + dq S for every (chunk,
+// head) in parallel.
+//
+// Every product is a single v_mfma_f32_16x16x4f32 accumulator chain over k
+// in increasing order; the instruction accumulates its four products as a
+// chain of fused multiply-adds, so each output equals the reference's FMA
+// chain (chunk/core.rs:277-310) bit for bit.
 #include <algorithm>
 
 #include "zg_device.hpp"
@@ -31,42 +39,83 @@ namespace zg {
 
 namespace {
 
-constexpr int kC = 64, kD = 128, kSlab = 32;
-constexpr int kPad = 132;  // LDS row pitch (floats) for [64][128] tiles
+constexpr int kC = 64, kD = 128, kSW = 16;  // chunk rows, head width, scan slab width
+constexpr int kPad = 132;                   // LDS row pitch (floats) of [rows][128] tiles
+constexpr int kApad = 68;                   // LDS row pitch of [64][64] tiles
 typedef float f4m __attribute__((ext_vector_type(4)));
 
-// Scratch record per (chunk, head), floats.
+// Record per (chunk, head), floats.  W first holds the solve's right-hand
+// side (beta k) exp(g); U is overwritten in place by corr in the scan; A is
+// the decayed (beta k) k^T (strictly lower part used); S holds the state
+// entering the chunk, key-major [k][v].
 constexpr size_t kOffU = 0, kOffW = kOffU + kC * kD, kOffDq = kOffW + kC * kD, kOffDk = kOffDq + kC * kD,
-                 kOffIntra = kOffDk + kC * kD, kOffDecay = kOffIntra + kC * kC, kRec = kOffDecay + 64;
+                 kOffIntra = kOffDk + kC * kD, kOffA = kOffIntra + kC * kC, kOffDecay = kOffA + kC * kC,
+                 kOffS = kOffDecay + 64, kRec = kOffS + kD * kD;
 
-// 16x16 output tile of X Y^T over K = kD (X, Y: rows of 128 in LDS with
-// pitch kPad) on v_mfma_f32_16x16x4f32.  Lane l supplies X[i0 + l%16][4s + l/16]
-// and Y[j0 + l%16][4s + l/16]; result register r is (i0 + 4(l/16) + r, j0 + l%16).
+__device__ __forceinline__ f4m mfma4(float a, float b, f4m c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS
+// operations, not for its outstanding global loads (which carry the next
+// chunk's operands across the barrier).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// 16x16 output tiles of X Y^T over K = kD (X, Y: rows of 128 in LDS with
+// pitch kPad), one MFMA chain each.  Lane l supplies X[i0 + l%16][4s + l/16]
+// and Y[j0 + l%16][4s + l/16]; result register r is
+// (i0 + 4(l/16) + r, j0 + l%16).  Operands are read into registers first so
+// that the chain does not wait on LDS between steps.
 __device__ __forceinline__ f4m tile_xyT(const float* X, const float* Y, int i0, int j0, int lane, float xscale_row) {
-    f4m acc = {0.0f, 0.0f, 0.0f, 0.0f};
     const float* xr = X + (i0 + (lane & 15)) * kPad + (lane >> 4);
     const float* yr = Y + (j0 + (lane & 15)) * kPad + (lane >> 4);
-#pragma unroll 8
+    float xa[kD / 4], yb[kD / 4];
+#pragma unroll
     for (int s = 0; s < kD / 4; ++s) {
-        const float xa = xr[4 * s] * xscale_row;
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, yr[4 * s], acc, 0, 0, 0);
+        xa[s] = xr[4 * s] * xscale_row;
+        yb[s] = yr[4 * s];
     }
+    __builtin_amdgcn_sched_barrier(0);
+    f4m acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < kD / 4; ++s) acc = mfma4(xa[s], yb[s], acc);
     return acc;
+}
+
+// Both products of a lower tile: (beta k) k^T and q k^T, interleaved.
+__device__ __forceinline__ void tile_pair(const float* Q, const float* K, int i0, int j0, int lane, float brow,
+                                          f4m& a4, f4m& q4) {
+    const float* kr = K + (i0 + (lane & 15)) * kPad + (lane >> 4);
+    const float* qr = Q + (i0 + (lane & 15)) * kPad + (lane >> 4);
+    const float* yr = K + (j0 + (lane & 15)) * kPad + (lane >> 4);
+    float ka[kD / 4], qa[kD / 4], yb[kD / 4];
+#pragma unroll
+    for (int s = 0; s < kD / 4; ++s) {
+        ka[s] = kr[4 * s] * brow;
+        qa[s] = qr[4 * s];
+        yb[s] = yr[4 * s];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    a4 = f4m{0.0f, 0.0f, 0.0f, 0.0f};
+    q4 = a4;
+#pragma unroll
+    for (int s = 0; s < kD / 4; ++s) {
+        a4 = mfma4(ka[s], yb[s], a4);
+        q4 = mfma4(qa[s], yb[s], q4);
+    }
 }
 
 }  // namespace
 
-// Grid (chunks, H), 256 threads.
+// Grid (chunks, H), 256 threads: everything of a (chunk, head) but the
+// solves.  LDS: q and k rows, 68 KB.
 __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                             const float* __restrict__ v,
                                                              const float* __restrict__ beta,
                                                              const float* __restrict__ logd, int T, int H,
                                                              float* __restrict__ scratch) {
     __shared__ float qs[kC * kPad];
     __shared__ float ks[kC * kPad];
-    __shared__ float as[kC][kC + 1];
-    __shared__ float is_[kC][kC + 1];
-    __shared__ float gs[kC], bs[kC], eg[kC], el[kC];
+    __shared__ float gs[kC], bs[kC], eg[kC], el[kC], lg[kC];
     const int c = blockIdx.x, h = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int t0 = c * kC, rows = min(kC, T - t0);
@@ -74,267 +123,403 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const float* __rest
     const float inv_sqrt = 1.0f / sqrtf((float)kD);
     const float eps = 1e-6f / (float)kD;
 
-    // q, k rows: two-stage L2 (zgo restatement of forward.rs:564-576), one row
-    // per wave at a time, two elements per lane
-    for (int t = wv; t < kC; t += 4) {
-        float xq[2] = {0.0f, 0.0f}, xk[2] = {0.0f, 0.0f};
-        if (t < rows) {
-            const size_t src = ((size_t)(t0 + t) * H + h) * kD;
+    // Two-stage L2 of q and k rows (forward.rs:564-576): sum of f32 squares
+    // in f64, mean rounded to f32, f32 sqrt and reciprocal; q also carries
+    // the output scale.  Thread (row tid/4, quarter tid%4) holds 32 elements
+    // of the row of q and of k; zero rows past the last token.
+    {
+        const int t = tid >> 2, d0 = 32 * (tid & 3);
+        v4f xq[8], xk[8];
+        const size_t src = ((size_t)(t0 + t) * H + h) * kD + d0;
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                xq[e] = q[src + lane + 64 * e];
-                xk[e] = k[src + lane + 64 * e];
+        for (int i = 0; i < 8; ++i) {
+            xq[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            xk[i] = xq[i];
+            if (t < rows) {
+                xq[i] = *(const v4f*)(q + src + 4 * i);
+                xk[i] = *(const v4f*)(k + src + 4 * i);
             }
+        }
+        if (tid < kC) {
+            const bool in = tid < rows;
+            bs[tid] = in ? beta[(size_t)(t0 + tid) * H + h] : 0.0f;
+            lg[tid] = in ? logd[(size_t)(t0 + tid) * H + h] : 0.0f;
         }
         double sq = 0.0, sk = 0.0;
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const float a2 = xq[e] * xq[e], b2 = xk[e] * xk[e];
-            sq += (double)a2;
-            sk += (double)b2;
-        }
-        sq = wave_sum_xor<double>(sq, 64);
-        sk = wave_sum_xor<double>(sk, 64);
-        const float iq = 1.0f / sqrtf((float)(sq / (double)kD) + eps);
-        const float ik = 1.0f / sqrtf((float)(sk / (double)kD) + eps);
+        for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            float a = 0.0f, b = 0.0f;
-            if (t < rows) {
-                const float tq = xq[e] * iq;
-                const float nq = tq * inv_sqrt;
-                a = nq * inv_sqrt;
-                const float tk = xk[e] * ik;
-                b = tk * inv_sqrt;
+            for (int e = 0; e < 4; ++e) {
+                const float a2 = xq[i][e] * xq[i][e], b2 = xk[i][e] * xk[i][e];
+                sq += (double)a2;
+                sk += (double)b2;
             }
-            qs[t * kPad + lane + 64 * e] = a;
-            ks[t * kPad + lane + 64 * e] = b;
+        sq = wave_sum_xor<double>(sq, 4);
+        sk = wave_sum_xor<double>(sk, 4);
+        const float iq = 1.0f / sqrtf((float)(sq * (1.0 / kD)) + eps);
+        const float ik = 1.0f / sqrtf((float)(sk * (1.0 / kD)) + eps);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v4f a, b;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float tq = xq[i][e] * iq;
+                const float nq = tq * inv_sqrt;
+                a[e] = nq * inv_sqrt;
+                const float tk = xk[i][e] * ik;
+                b[e] = tk * inv_sqrt;
+            }
+            *(v4f*)&qs[t * kPad + d0 + 4 * i] = a;
+            *(v4f*)&ks[t * kPad + d0 + 4 * i] = b;
         }
     }
-    if (tid < kC) bs[tid] = tid < rows ? beta[(size_t)(t0 + tid) * H + h] : 0.0f;
+    __syncthreads();
+    // g = cumsum(log decay) in f64 (chunk/core.rs:135-150; padded rows add 0)
     if (tid == 0) {
+        float l[kC];
+#pragma unroll
+        for (int t = 0; t < kC; ++t) l[t] = lg[t];
         double running = 0.0;
+#pragma unroll
         for (int t = 0; t < kC; ++t) {
-            if (t < rows) running += (double)logd[(size_t)(t0 + t) * H + h];
+            running += (double)l[t];
             gs[t] = (float)running;
         }
     }
     __syncthreads();
 
-    // A = (beta k) k^T and intra = q k^T, decayed; 16 tiles each, 4 per wave
-    for (int tile = wv; tile < 16; tile += 4) {
-        const int i0 = (tile >> 2) * 16, j0 = (tile & 3) * 16;
-        const float brow = bs[i0 + (lane & 15)];
-        const f4m a4 = tile_xyT(ks, ks, i0, j0, lane, brow);
-        const f4m q4 = tile_xyT(qs, ks, i0, j0, lane, 1.0f);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = i0 + 4 * (lane >> 4) + r, s = j0 + (lane & 15);
-            const float decay = s <= t ? cr_expf(gs[t] - gs[s]) : 0.0f;
-            as[t][s] = a4[r] * decay;
-            is_[t][s] = q4[r] * decay;
-        }
-    }
-    // dq = q exp(g), dk = k exp(g_last - g); intra and exp(g_last) to scratch
-    const float last = gs[kC - 1];
+    // A = (beta k) k^T and intra = q k^T, decayed by exp(g_t - g_s) on and
+    // below the diagonal (0 * the product above it, as the reference's
+    // exp(-inf) factor gives).  A is read only strictly below the diagonal,
+    // so its tiles above are skipped.  Lower tile pairs go round-robin over
+    // the waves, the six upper intra tiles to waves 2 and 3.
     if (tid < kC) {
+        const float last = gs[kC - 1];
         eg[tid] = cr_expf(gs[tid]);
         el[tid] = cr_expf(last - gs[tid]);
     }
-    __syncthreads();
-    for (int i = tid; i < kC * kD / 4; i += 256) {
-        const int t = (4 * i) / kD, d = (4 * i) % kD;
-        const v4f qv = *(const v4f*)&qs[t * kPad + d], kv = *(const v4f*)&ks[t * kPad + d];
-        *(v4f*)(rec + kOffDq + 4 * i) = qv * eg[t];
-        *(v4f*)(rec + kOffDk + 4 * i) = kv * el[t];
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+        const int n = wv + 4 * m;
+        if (n >= 10) break;
+        const int ti = n < 1 ? 0 : n < 3 ? 1 : n < 6 ? 2 : 3;
+        const int tj = n - ti * (ti + 1) / 2;
+        const int i0 = 16 * ti, j0 = 16 * tj;
+        const float brow = bs[i0 + (lane & 15)];
+        f4m a4, q4;
+        tile_pair(qs, ks, i0, j0, lane, brow, a4, q4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = i0 + 4 * (lane >> 4) + r, s2 = j0 + (lane & 15);
+            const float decay = s2 <= t ? cr_expf(gs[t] - gs[s2]) : 0.0f;
+            rec[kOffA + t * kC + s2] = a4[r] * decay;
+            rec[kOffIntra + t * kC + s2] = q4[r] * decay;
+        }
     }
-    for (int i = tid; i < kC * kC; i += 256) rec[kOffIntra + i] = is_[i / kC][i % kC];
-    if (tid == 0) rec[kOffDecay] = cr_expf(last);
+    if (wv >= 2) {
+        for (int n = 3 * (wv - 2); n < 3 * (wv - 1); ++n) {
+            const int ti = n < 3 ? 0 : n < 5 ? 1 : 2;  // upper tiles (ti, tj), tj > ti
+            const int tj = ti + 1 + (n - (ti == 0 ? 0 : ti == 1 ? 3 : 5));
+            const int i0 = 16 * ti, j0 = 16 * tj;
+            const f4m q4 = tile_xyT(qs, ks, i0, j0, lane, 1.0f);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                rec[kOffIntra + (i0 + 4 * (lane >> 4) + r) * kC + j0 + (lane & 15)] = q4[r] * 0.0f;
+        }
+    }
+    __syncthreads();
+    // dq = q exp(g), dk = k exp(g_last - g), and the W right-hand side
+    // (beta k) exp(g)
+#pragma unroll
+    for (int i = 0; i < kC * kD / 4 / 256; ++i) {
+        const int f = tid + 256 * i, t = f >> 5, d = 4 * (f & 31);
+        const v4f qv = *(const v4f*)&qs[t * kPad + d], kv = *(const v4f*)&ks[t * kPad + d];
+        *(v4f*)(rec + kOffDq + t * kD + d) = qv * eg[t];
+        *(v4f*)(rec + kOffDk + t * kD + d) = kv * el[t];
+        *(v4f*)(rec + kOffW + t * kD + d) = (kv * bs[t]) * eg[t];
+    }
+    if (tid < 64) rec[kOffDecay + tid] = cr_expf(gs[kC - 1]);  // replicated for vector loads
+}
 
-    // unit-lower solves (gdn/chunk.rs:16-76: separate products, four
-    // interleaved partial sums, (s0+s2)+(s1+s3), scalar tail, one subtraction):
-    // thread j < 128 solves column j of U (rhs beta v), thread 128 + j column j
-    // of W (rhs (beta k) exp(g)), the column in registers
-    {
-        const int col = tid & (kD - 1);
-        float xr[kC];
+// Grid (chunks, H, 2), 128 threads: the unit-lower solves of gdn/chunk.rs:16-76
+// (separate products, four interleaved partial sums, (s0+s2)+(s1+s3), scalar
+// tail, one subtraction) for the 128 columns of U (z = 0, rhs beta v) or of
+// W (z = 1, rhs in place), one column per thread, held in registers.  The
+// coefficients are uniform across the wave and are read as scalar loads
+// through `amat` (the same records, never written here).
+__global__ __launch_bounds__(128) void gdn_chunk_solve_kernel(const float* __restrict__ v,
+                                                              const float* __restrict__ beta,
+                                                              const float* __restrict__ amat, int T, int H,
+                                                              float* __restrict__ scratch) {
+    const int c = blockIdx.x, h = blockIdx.y, z = blockIdx.z;
+    const int col = threadIdx.x;
+    const int t0 = c * kC, rows = min(kC, T - t0);
+    float* rec = scratch + ((size_t)c * H + h) * kRec;
+    const float* A = amat + ((size_t)c * H + h) * kRec + kOffA;
+    float xr[kC];
+    if (z == 0) {
 #pragma unroll
         for (int t = 0; t < kC; ++t) {
             float r = 0.0f;
             if (t < rows) {
-                if (tid < kD) {
-                    const float vv = v[((size_t)(t0 + t) * H + h) * kD + col];
-                    r = vv * bs[t];
-                } else {
-                    const float kb = ks[t * kPad + col] * bs[t];
-                    r = kb * eg[t];
-                }
+                const float vv = v[((size_t)(t0 + t) * H + h) * kD + col];
+                r = vv * beta[(size_t)(t0 + t) * H + h];
             }
             xr[t] = r;
         }
+    } else {
 #pragma unroll
-        for (int row = 0; row < kC; ++row) {
-            const int vend = row / 4 * 4;
-            float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int t = 0; t < kC; ++t) xr[t] = rec[kOffW + t * kD + col];
+    }
 #pragma unroll
-            for (int st = 0; st < vend; st += 4) {
+    for (int row = 0; row < kC; ++row) {
+        const int vend = row / 4 * 4;
+        const float* arow = A + row * kC;
+        float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int l = 0; l < 4; ++l) {
-                    const float p = as[row][st + l] * xr[st + l];
-                    s4[l] = s4[l] + p;
-                }
+        for (int st = 0; st < vend; st += 4) {
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const float p = arow[st + l] * xr[st + l];
+                s4[l] = s4[l] + p;
             }
-            float sum = (s4[0] + s4[2]) + (s4[1] + s4[3]);
-#pragma unroll
-            for (int kk = vend; kk < row; ++kk) {
-                const float p = as[row][kk] * xr[kk];
-                sum = sum + p;
-            }
-            xr[row] = xr[row] - sum;
         }
-        float* dst = rec + (tid < kD ? kOffU : kOffW);
+        float sum = (s4[0] + s4[2]) + (s4[1] + s4[3]);
 #pragma unroll
-        for (int t = 0; t < kC; ++t) dst[t * kD + col] = xr[t];
+        for (int kk = vend; kk < row; ++kk) {
+            const float p = arow[kk] * xr[kk];
+            sum = sum + p;
+        }
+        xr[row] = xr[row] - sum;
+    }
+    float* dst = rec + (z == 0 ? kOffU : kOffW);
+#pragma unroll
+    for (int t = 0; t < kC; ++t) dst[t * kD + col] = xr[t];
+}
+
+// Grid (H, kD / kSW), 256 threads: value columns [16 slab, 16 slab + 16) of
+// head h through all chunks in order (every slab of a head on one XCD, whose
+// L2 then serves the shared W and dk).  The state is held key-major S[k][j]
+// in LDS; in memory it is value-major [h][v][k] (the decode layout) or, with
+// key_major, [h][k][v] (the chunk reference's layout).  Per chunk: store the
+// entering state, pred = W S, corr = U - pred (written over U), then
+// S <- dk^T corr + exp(g_last) S.  The next chunk's operands are loaded into
+// registers one chunk ahead.
+__global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(float* __restrict__ scratch, int T, int H,
+                                                             float* __restrict__ state, int key_major) {
+    __shared__ float S[kD][kSW + 1];
+    __shared__ float Wl[kC * kPad];  // wave w stages rows 16w..16w+15
+    __shared__ float Dk[kC * kPad];
+    __shared__ float Cr[kC][kSW + 1];
+    const int h = blockIdx.x, slab = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int j0 = slab * kSW, i0 = 16 * wv, jl = lane & 15, kq = lane >> 4;
+    float* sh = state + (size_t)h * kD * kD;
+    for (int i = tid; i < kD * kSW; i += 256) {
+        const int kk = key_major ? i / kSW : i % kD, j = key_major ? i % kSW : i / kD;
+        S[kk][j] = key_major ? sh[(size_t)kk * kD + j0 + j] : sh[(size_t)(j0 + j) * kD + kk];
+    }
+    const int nch = (T + kC - 1) / kC;
+    // operands of the next chunk, in flight while this one computes
+    struct Ops {
+        v4f w[8], dk[8];
+        float u[4], decay;
+    };
+    auto fetch = [&](int c, Ops& o) {
+        const float* rec = scratch + ((size_t)c * H + h) * kRec;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int f = lane + 64 * i;  // own 16 rows of W: row i0 + f/32, float4 f%32
+            o.w[i] = *(const v4f*)(rec + kOffW + (i0 + (f >> 5)) * kD + 4 * (f & 31));
+            const int g = tid + 256 * i;  // all of dk
+            o.dk[i] = *(const v4f*)(rec + kOffDk + (g >> 5) * kD + 4 * (g & 31));
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o.u[r] = rec[kOffU + (i0 + 4 * kq + r) * kD + j0 + jl];
+        o.decay = rec[kOffDecay + lane];  // replicated: a vector load, not a scalar one
+    };
+    auto step = [&](int c, Ops& o) {
+        float* rec = scratch + ((size_t)c * H + h) * kRec;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int f = lane + 64 * i, g = tid + 256 * i;
+            *(v4f*)&Wl[(i0 + (f >> 5)) * kPad + 4 * (f & 31)] = o.w[i];
+            *(v4f*)&Dk[(g >> 5) * kPad + 4 * (g & 31)] = o.dk[i];
+        }
+        const float decay = o.decay;
+        float u[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) u[r] = o.u[r];
+        if (c + 1 < nch) fetch(c + 1, o);
+        // the state entering this chunk, for the output kernel
+        {
+            float sv[kD * kSW / 256];
+#pragma unroll
+            for (int i = 0; i < kD * kSW / 256; ++i) {
+                const int f = tid + 256 * i;
+                sv[i] = S[f / kSW][f % kSW];
+            }
+#pragma unroll
+            for (int i = 0; i < kD * kSW / 256; ++i) {
+                const int f = tid + 256 * i;
+                rec[kOffS + (f / kSW) * kD + j0 + f % kSW] = sv[i];
+            }
+        }
+        lds_barrier();
+        // pred = W S: wave w owns rows 16w..16w+15
+        f4m acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        {
+            float wa[kD / 4], sb[kD / 4];
+#pragma unroll
+            for (int s = 0; s < kD / 4; ++s) {
+                wa[s] = Wl[(i0 + jl) * kPad + 4 * s + kq];
+                sb[s] = S[4 * s + kq][jl];
+            }
+            __builtin_amdgcn_sched_barrier(0);  // issue every operand read before the chain
+#pragma unroll
+            for (int s = 0; s < kD / 4; ++s) acc = mfma4(wa[s], sb[s], acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = i0 + 4 * kq + r;
+            const float cr = u[r] - acc[r];
+            Cr[t][jl] = cr;
+            rec[kOffU + t * kD + j0 + jl] = cr;
+        }
+        lds_barrier();
+        // S <- dk^T corr + decay S: wave w owns key rows 32w..32w+31
+        f4m sn[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+        float sold[2][4];
+        {
+            float cb[kC / 4], da[2][kC / 4];
+#pragma unroll
+            for (int s = 0; s < kC / 4; ++s) {
+                const int tt = 4 * s + kq;
+                cb[s] = Cr[tt][jl];
+#pragma unroll
+                for (int it2 = 0; it2 < 2; ++it2) da[it2][s] = Dk[tt * kPad + 32 * wv + 16 * it2 + jl];
+            }
+#pragma unroll
+            for (int it2 = 0; it2 < 2; ++it2)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sold[it2][r] = S[32 * wv + 16 * it2 + 4 * kq + r][jl];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < kC / 4; ++s)
+#pragma unroll
+                for (int it2 = 0; it2 < 2; ++it2) sn[it2] = mfma4(da[it2][s], cb[s], sn[it2]);
+        }
+#pragma unroll
+        for (int it2 = 0; it2 < 2; ++it2)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float sd = sold[it2][r] * decay;
+                S[32 * wv + 16 * it2 + 4 * kq + r][jl] = sn[it2][r] + sd;
+            }
+        lds_barrier();
+    };
+    Ops ops;
+    fetch(0, ops);
+    for (int c = 0; c < nch; ++c) step(c, ops);
+    for (int i = tid; i < kD * kSW; i += 256) {
+        const int kk = key_major ? i / kSW : i % kD, j = key_major ? i % kSW : i / kD;
+        if (key_major)
+            sh[(size_t)kk * kD + j0 + j] = S[kk][j];
+        else
+            sh[(size_t)(j0 + j) * kD + kk] = S[kk][j];
     }
 }
 
-// Grid (kD / kSlab, H), 256 threads: value columns [32 slab, 32 slab + 32) of
-// head h across all chunks in order.  The state is held key-major S[k][j] in
-// LDS; in memory it is value-major [h][v][k] (the decode layout) or, with
-// key_major, [h][k][v] (the chunk reference's layout).  round_bf16 rounds
-// each output to the nearest bf16 (ties to even), as the reference's
-// output_bf16 does (gdn.rs:69-76).
-__global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(const float* __restrict__ scratch, int T, int H,
-                                                             float* __restrict__ state, float* __restrict__ out,
-                                                             int key_major, int round_bf16) {
-    __shared__ float Ws[kC * kPad];  // W, later dk
+// Grid (chunks, H), 512 threads: o = intra corr + dq S for one (chunk,
+// head), S the state entering the chunk (chunk/core.rs:236-252: the intra
+// product, then the inter product added).  Wave w computes rows
+// 16 (w % 4) .. +15 of columns 64 (w / 4) .. +63.  round_bf16 rounds each
+// output to the nearest bf16, ties to even, as the reference's output_bf16
+// does (gdn.rs:69-76).
+__global__ __launch_bounds__(512) void gdn_chunk_out_kernel(const float* __restrict__ scratch, int T, int H,
+                                                            float* __restrict__ out, int round_bf16) {
+    __shared__ float Sc[kD * kPad];
+    __shared__ float Cr[kC * kPad];
     __shared__ float Dq[kC * kPad];
-    __shared__ float S[kD][kSlab + 1];
-    __shared__ float corr[kC][kSlab + 1];
-    __shared__ float In[kC][kC + 1];
-    const int slab = blockIdx.x, h = blockIdx.y;
+    __shared__ float In[kC * kApad];
+    const int c = blockIdx.x, h = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int j0 = slab * kSlab;
-    float* sh = state + (size_t)h * kD * kD;
-    if (key_major) {
-        for (int i = tid; i < kD * kSlab; i += 256) S[i / kSlab][i % kSlab] = sh[(size_t)(i / kSlab) * kD + j0 + i % kSlab];
-    } else {
-        for (int i = tid; i < kD * kSlab; i += 256) S[i % kD][i / kD] = sh[(size_t)(j0 + i / kD) * kD + i % kD];
+    const int t0 = c * kC, rows = min(kC, T - t0);
+    const int i0 = 16 * (wv & 3), c0 = 64 * (wv >> 2), jl = lane & 15, kq = lane >> 4;
+    const float* rec = scratch + ((size_t)c * H + h) * kRec;
+#pragma unroll
+    for (int i = 0; i < kD * kD / 4 / 512; ++i) {
+        const int f = tid + 512 * i;
+        *(v4f*)&Sc[(f >> 5) * kPad + 4 * (f & 31)] = *(const v4f*)(rec + kOffS + 4 * f);
     }
-    const int nch = (T + kC - 1) / kC;
-    for (int c = 0; c < nch; ++c) {
-        const int t0 = c * kC, rows = min(kC, T - t0);
-        const float* rec = scratch + ((size_t)c * H + h) * kRec;
-        for (int i = tid; i < kC * kD / 4; i += 256) {
-            const int t = (4 * i) / kD, d = (4 * i) % kD;
-            *(v4f*)&Ws[t * kPad + d] = *(const v4f*)(rec + kOffW + 4 * i);
-            *(v4f*)&Dq[t * kPad + d] = *(const v4f*)(rec + kOffDq + 4 * i);
+#pragma unroll
+    for (int i = 0; i < kC * kD / 4 / 512; ++i) {
+        const int f = tid + 512 * i;
+        *(v4f*)&Cr[(f >> 5) * kPad + 4 * (f & 31)] = *(const v4f*)(rec + kOffU + 4 * f);
+        *(v4f*)&Dq[(f >> 5) * kPad + 4 * (f & 31)] = *(const v4f*)(rec + kOffDq + 4 * f);
+    }
+#pragma unroll
+    for (int i = 0; i < kC * kC / 4 / 512; ++i) {
+        const int f = tid + 512 * i;
+        *(v4f*)&In[(f >> 4) * kApad + 4 * (f & 15)] = *(const v4f*)(rec + kOffIntra + 4 * f);
+    }
+    __syncthreads();
+    f4m oo[4], it[4];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+        oo[jt] = f4m{0.0f, 0.0f, 0.0f, 0.0f};
+        it[jt] = oo[jt];
+    }
+    {
+        float ia[kC / 4];
+#pragma unroll
+        for (int s = 0; s < kC / 4; ++s) ia[s] = In[(i0 + jl) * kApad + 4 * s + kq];
+#pragma unroll
+        for (int s0 = 0; s0 < kC / 4; s0 += 8) {
+            float cb[8][4];
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+#pragma unroll
+                for (int jt = 0; jt < 4; ++jt) cb[s][jt] = Cr[(4 * (s0 + s) + kq) * kPad + c0 + 16 * jt + jl];
+            __builtin_amdgcn_sched_barrier(0);  // a block of operand reads, then its MFMAs
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+#pragma unroll
+                for (int jt = 0; jt < 4; ++jt) oo[jt] = mfma4(ia[s0 + s], cb[s][jt], oo[jt]);
         }
-        for (int i = tid; i < kC * kC; i += 256) In[i / kC][i % kC] = rec[kOffIntra + i];
-        const float decay = rec[kOffDecay];
-        __syncthreads();
-        // pred = W S and inter = dq S: wave w owns rows 16w..16w+15, both 16-column tiles
-        const int i0 = 16 * wv;
-        f4m pr[2], it[2];
+    }
+    {
+        float da[kD / 4];
 #pragma unroll
-        for (int jt = 0; jt < 2; ++jt) {
-            pr[jt] = f4m{0.0f, 0.0f, 0.0f, 0.0f};
-            it[jt] = f4m{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s = 0; s < kD / 4; ++s) da[s] = Dq[(i0 + jl) * kPad + 4 * s + kq];
+#pragma unroll
+        for (int s0 = 0; s0 < kD / 4; s0 += 8) {
+            float sb[8][4];
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+#pragma unroll
+                for (int jt = 0; jt < 4; ++jt) sb[s][jt] = Sc[(4 * (s0 + s) + kq) * kPad + c0 + 16 * jt + jl];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+#pragma unroll
+                for (int jt = 0; jt < 4; ++jt) it[jt] = mfma4(da[s0 + s], sb[s][jt], it[jt]);
         }
-        for (int s = 0; s < kD / 4; ++s) {
-            const int kk = 4 * s + (lane >> 4);
-            const float wa = Ws[(i0 + (lane & 15)) * kPad + kk];
-            const float da = Dq[(i0 + (lane & 15)) * kPad + kk];
+    }
 #pragma unroll
-            for (int jt = 0; jt < 2; ++jt) {
-                const float sb = S[kk][16 * jt + (lane & 15)];
-                pr[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa, sb, pr[jt], 0, 0, 0);
-                it[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(da, sb, it[jt], 0, 0, 0);
-            }
-        }
-        // corr = U - pred
+    for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-        for (int jt = 0; jt < 2; ++jt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = i0 + 4 * (lane >> 4) + r, j = 16 * jt + (lane & 15);
-                corr[t][j] = rec[kOffU + t * kD + j0 + j] - pr[jt][r];
-            }
-        __syncthreads();
-        // o = intra corr + inter
-        f4m oo[2];
-#pragma unroll
-        for (int jt = 0; jt < 2; ++jt) oo[jt] = f4m{0.0f, 0.0f, 0.0f, 0.0f};
-        for (int s = 0; s < kC / 4; ++s) {
-            const int kk = 4 * s + (lane >> 4);
-            const float ia = In[i0 + (lane & 15)][kk];
-#pragma unroll
-            for (int jt = 0; jt < 2; ++jt)
-                oo[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(ia, corr[kk][16 * jt + (lane & 15)], oo[jt], 0, 0, 0);
-        }
-#pragma unroll
-        for (int jt = 0; jt < 2; ++jt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = i0 + 4 * (lane >> 4) + r, j = 16 * jt + (lane & 15);
-                if (t < rows) {
-                    float o = oo[jt][r] + it[jt][r];
-                    if (round_bf16) {
-                        const unsigned b = __float_as_uint(o);
-                        o = __uint_as_float((b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u);
-                    }
-                    out[((size_t)(t0 + t) * H + h) * kD + j0 + j] = o;
+        for (int r = 0; r < 4; ++r) {
+            const int t = i0 + 4 * kq + r;
+            if (t < rows) {
+                float o = oo[jt][r] + it[jt][r];
+                if (round_bf16) {
+                    const unsigned b = __float_as_uint(o);
+                    o = __uint_as_float((b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u);
                 }
-            }
-        // dk into the W buffer (W no longer needed after the barrier)
-        __syncthreads();
-        for (int i = tid; i < kC * kD / 4; i += 256) {
-            const int t = (4 * i) / kD, d = (4 * i) % kD;
-            *(v4f*)&Ws[t * kPad + d] = *(const v4f*)(rec + kOffDk + 4 * i);
-        }
-        __syncthreads();
-        // S <- dk^T corr + decay S: wave w owns key rows 32w..32w+31 (two tiles) x 2 column tiles
-        f4m sn[2][2];
-#pragma unroll
-        for (int it2 = 0; it2 < 2; ++it2)
-#pragma unroll
-            for (int jt = 0; jt < 2; ++jt) sn[it2][jt] = f4m{0.0f, 0.0f, 0.0f, 0.0f};
-        for (int s = 0; s < kC / 4; ++s) {
-            const int tt = 4 * s + (lane >> 4);
-#pragma unroll
-            for (int it2 = 0; it2 < 2; ++it2) {
-                const float ka = Ws[tt * kPad + 32 * wv + 16 * it2 + (lane & 15)];
-#pragma unroll
-                for (int jt = 0; jt < 2; ++jt)
-                    sn[it2][jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka, corr[tt][16 * jt + (lane & 15)], sn[it2][jt], 0, 0, 0);
+                out[((size_t)(t0 + t) * H + h) * kD + c0 + 16 * jt + jl] = o;
             }
         }
-        float snew[2][2][4];
-#pragma unroll
-        for (int it2 = 0; it2 < 2; ++it2)
-#pragma unroll
-            for (int jt = 0; jt < 2; ++jt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int kr = 32 * wv + 16 * it2 + 4 * (lane >> 4) + r, j = 16 * jt + (lane & 15);
-                    const float sd = S[kr][j] * decay;
-                    snew[it2][jt][r] = sn[it2][jt][r] + sd;
-                }
-        __syncthreads();
-#pragma unroll
-        for (int it2 = 0; it2 < 2; ++it2)
-#pragma unroll
-            for (int jt = 0; jt < 2; ++jt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    S[32 * wv + 16 * it2 + 4 * (lane >> 4) + r][16 * jt + (lane & 15)] = snew[it2][jt][r];
-        __syncthreads();
-    }
-    if (key_major) {
-        for (int i = tid; i < kD * kSlab; i += 256) sh[(size_t)(i / kSlab) * kD + j0 + i % kSlab] = S[i / kSlab][i % kSlab];
-    } else {
-        for (int i = tid; i < kD * kSlab; i += 256) sh[(size_t)(j0 + i / kD) * kD + i % kD] = S[i % kD][i / kD];
-    }
 }
 
 size_t gdn_chunk_scratch_bytes(size_t T, size_t H) { return ((T + kC - 1) / kC) * H * kRec * sizeof(float); }
@@ -344,10 +529,14 @@ hipError_t gdn_chunk_prefill(const float* q, const float* k, const float* v, con
                              bool round_bf16, hipStream_t s) {
     if (T == 0 || H == 0) return hipErrorInvalidValue;
     const unsigned nch = (unsigned)((T + kC - 1) / kC);
-    hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(nch, (unsigned)H), dim3(256), 0, s, q, k, v, beta, logd, (int)T,
+    hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(nch, (unsigned)H), dim3(256), 0, s, q, k, beta, logd, (int)T,
                        (int)H, scratch);
-    hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kD / kSlab, (unsigned)H), dim3(256), 0, s, scratch, (int)T, (int)H,
-                       state, out, key_major ? 1 : 0, round_bf16 ? 1 : 0);
+    hipLaunchKernelGGL(gdn_chunk_solve_kernel, dim3(nch, (unsigned)H, 2), dim3(128), 0, s, v, beta,
+                       (const float*)scratch, (int)T, (int)H, scratch);
+    hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3((unsigned)H, kD / kSW), dim3(256), 0, s, scratch, (int)T, (int)H,
+                       state, key_major ? 1 : 0);
+    hipLaunchKernelGGL(gdn_chunk_out_kernel, dim3(nch, (unsigned)H), dim3(512), 0, s, scratch, (int)T, (int)H, out,
+                       round_bf16 ? 1 : 0);
     return hipGetLastError();
 }
 
