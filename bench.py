@@ -10,6 +10,9 @@ Workloads (synthetic, seeded random-init weights in the named GGUF codec):
   gemv   dequant-GEMV sweep (Q8_0/Q4_K, M in {1,4,16,32}) with the RMSNorm
          prologue; weights rotate across distinct buffers totalling > 2x the
          256 MB Infinity Cache.
+  gdn    GDN decode kernel alone (conv, L2, gates, recurrence) at B in
+         {1, 8, 32, 64}, 16 heads; value = B=64 GB/s.  The decode line carries
+         the same sweep as config.gdn_decode_leg.
   prefill chunked GDN prefill of one layer's core (H=16, d=128, chunks of
          64) at L=2048 and L=8192 from a zero state; value = L=8192 tokens/s,
          roofline against the f32 MFMA peak the kernels compute on.
@@ -169,6 +172,59 @@ def gemv_leg(kern, torch, g, tensors, kind, reps):
                 bytes_per_launch=byts / len(handles), gbs=byts / us / 1e3)
 
 
+def gdn_bytes(B, H=16, dk=128, dv=128):
+    """Algorithmic bytes of one GDN decode step: the fp32 state read and
+    written once, q/k/v in bf16, z in bf16 and o in f32 (per row and head)."""
+    return B * H * (dk * dv * 4 * 2 + (dk + dk + dv) * 2 + dv * (2 + 4))
+
+
+def gdn_leg(ctx, torch, rows=(1, 8, 32, 64), reps=20, H=16):
+    """GDN decode kernel alone (conv + L2 + gates + recurrence, state
+    read-modify-write) at B rows, config 3's distributions; the states rotate
+    over distinct buffers totalling > 2.2x the Infinity Cache."""
+    from zerogravity_amd import _lib as L
+    lib = L.lib()
+    s = torch.cuda.current_stream()
+    out = {}
+    for B in rows:
+        W = H * 128
+        stride = 4 * W + 2 * H
+        g = torch.Generator(device="cuda")
+        g.manual_seed(B)
+        proj = torch.randn(B, stride, device="cuda", generator=g)
+        conv_w = 0.5 * torch.randn(3 * W * 4, device="cuda", generator=g)
+        dt = 0.1 * torch.randn(H, device="cuda", generator=g)
+        ssm_a = -torch.exp(torch.randn(H, device="cuda", generator=g))
+        ring = torch.zeros(B * 3 * W * 4, device="cuda")
+        pos = torch.zeros(B, dtype=torch.int32, device="cuda")
+        core = torch.empty(B * W, device="cuda")
+        sbytes = B * H * 128 * 128 * 4
+        copies = int(min(256, max(2, np.ceil(2.2 * MALL_BYTES / sbytes))))
+        states = [0.02 * torch.randn(B * H * 128 * 128, device="cuda", generator=g) for _ in range(copies)]
+
+        def launch(i):
+            ctx.check(lib.zg_gdn_decode_device(ctx.h, B, H, proj.data_ptr(), stride, conv_w.data_ptr(),
+                                               ring.data_ptr(), pos.data_ptr(), dt.data_ptr(), ssm_a.data_ptr(),
+                                               1e-6, states[i % copies].data_ptr(), core.data_ptr(), s.cuda_stream))
+
+        for i in range(copies):
+            launch(i)
+        torch.cuda.synchronize()
+        n = max(reps, copies)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for i in range(n):
+            launch(i)
+        e1.record(s)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / n
+        gbs = gdn_bytes(B, H) / us / 1e3
+        out[B] = dict(us=round(us, 3), gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
+        log(f"GDN decode B={B:2d}: {us:8.2f} us  {gbs:8.1f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+        del states
+    return out
+
+
 def cpu_decode_baseline(g, tensors, prefix, seconds):
     """The oracle (C restatement of the reference CPU path, OpenMP over GEMV
     rows on every host core) decoding greedily at B=1 after importing a random
@@ -227,6 +283,7 @@ def bench_decode(args):
     leg = gemv_leg(kern, torch, g, tensors, gguf.Q4_K, args.leg_reps)
     log(f"Q4_K GEMV leg: {leg['launches']} launches {leg['us_per_step']:.1f} us/step, "
         f"{leg['us_per_launch']:.2f} us/launch, {leg['gbs']:.0f} GB/s")
+    gdn = gdn_leg(kern.ctx, torch)
     line = {
         "metric": "decode tok/s @B=1 (2B-shaped Q4_K, 2048-token prefix, bf16 KV)",
         "value": round(res[1]["tok_s"], 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
@@ -235,7 +292,7 @@ def bench_decode(args):
         "data": "synthetic (seeded random-init Q4_K GGUF weights, random prefix state)",
         "config": {"workload": "2B-shaped Q4_K continuous-batch greedy decode", "prefix": prefix,
                    "kv_cache": "bf16", "b1": res[1], "b32": res[32],
-                   "b32_tok_s": round(res[32]["tok_s"], 1)},
+                   "b32_tok_s": round(res[32]["tok_s"], 1), "gdn_decode_leg": gdn},
         "roofline": {"bound": "hbm", "achieved": round(leg["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(leg["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "fused_q4k_kernel (the B=1 decode step's stacked projections, one launch each)",
@@ -456,12 +513,32 @@ def bench_prefill(args):
     return line
 
 
+def bench_gdn(args):
+    import torch
+    from zerogravity_amd import _lib as L
+    ctx = L.Context(0)
+    torch.cuda.set_stream(torch.cuda.Stream())
+    res = gdn_leg(ctx, torch, reps=max(args.steps, 20))
+    head = res[64]
+    line = {
+        "metric": "GDN decode achieved HBM GB/s (B=64, 16 heads, dk=dv=128, fp32 state read-modify-write)",
+        "value": head["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": max(args.steps, 20), "warmup": 1,
+        "ms_per_step": head["us"] / 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded projections, N(0,0.02) states)",
+        "config": {"workload": "GDN decode step (conv + L2 + gates + recurrence)", "sweep": res},
+        "roofline": {"bound": "hbm", "achieved": head["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": head["frac"], "traffic": None},
+    }
+    ctx.close()
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "prefill"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "prefill", "gdn"])
     ap.add_argument("--prefix", type=int, default=2048)
     ap.add_argument("--leg-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -471,7 +548,7 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU would run its own "
               "sessions; see the sharding notes in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
-    bench = {"decode": bench_decode, "gemv": bench_gemv, "prefill": bench_prefill}[args.workload]
+    bench = {"decode": bench_decode, "gemv": bench_gemv, "prefill": bench_prefill, "gdn": bench_gdn}[args.workload]
     line = bench(args)
     print(json.dumps(line), flush=True)
 

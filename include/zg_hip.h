@@ -158,6 +158,21 @@ int zg_gdn_chunk(zg_ctx* ctx, size_t rows, size_t heads, const float* query, con
                  const float* beta, const float* log_decay, const float* previous_state, float* output_bf16,
                  float* state_out);
 
+/* One GDN layer's decode step for `rows` sequences on device buffers and the
+ * caller's stream: the causal conv (cpu/src/ops/gdn.rs:7-44) over a 4-slot
+ * ring per channel, SiLU, two-stage q/k L2 (forward.rs:564-576), gates
+ * (lib.rs:339-362) and the recurrence (lib.rs:1446-1499), i.e. gdn_layer
+ * (forward.rs:518-632) up to the gated norm.  Replaces the per-token
+ * GdnConvRegion + GdnRecurrentRegion pair (accelerator.rs:592-633) for a
+ * resident state.  proj [rows][proj_stride]: [qkv (3W) | z (W) | alpha (H) |
+ * beta (H)], W = 128 heads; conv_w [3W][4] (the GGUF ssm_conv1d layout);
+ * ring [rows][3W][4]: the token at position p lives in slot p % 4;
+ * positions [rows]; dt, ssm_a [heads]; state [rows][heads][128 v][128 k];
+ * core [rows][W] = o / sqrt(128). */
+int zg_gdn_decode_device(zg_ctx* ctx, size_t rows, size_t heads, const float* proj, size_t proj_stride,
+                         const float* conv_w, float* ring, const int32_t* positions, const float* dt,
+                         const float* ssm_a, float eps, float* state, float* core, void* stream);
+
 /* Multi-chunk prefill on device buffers and the caller's stream (the same
  * kernels as zg_gdn_chunk; no reference counterpart takes more than one
  * chunk per call, core.rs:89).  Chunks of 64 tokens in order; query, key,

@@ -42,6 +42,7 @@ _SIGS = {
     "zg_gdn_chunk": (C.c_int, [P, SZ, SZ, P, P, P, P, P, P, P, P]),
     "zg_gdn_chunk_scratch_bytes": (SZ, [SZ, SZ]),
     "zg_gdn_chunk_prefill_device": (C.c_int, [P, SZ, SZ, P, P, P, P, P, P, P, P]),
+    "zg_gdn_decode_device": (C.c_int, [P, SZ, SZ, P, SZ, P, P, P, P, P, C.c_float, P, P, P]),
     "zg_rope_kv": (C.c_int, [P, P, P, P, SZ, SZ, SZ, SZ, SZ, C.c_float, P, P, P]),
     "zg_attention_qk": (C.c_int, [P, P, P, SZ, SZ, SZ, SZ, C.c_float, P, P]),
     "zg_attention_softmax": (C.c_int, [P, P, SZ, SZ, P]),

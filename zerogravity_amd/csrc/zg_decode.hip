@@ -698,6 +698,16 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3, b = blockIdx.y;
     const int tid = threadIdx.x;
     const int W = a.H * D;
+    // this thread's 16 state values (the bulk of the traffic) are requested
+    // first, so that their latency overlaps the conv, norms and gates
+    const int lane = tid & 63, wv = tid >> 6;
+    const int jl = wv * 8 + (lane >> 3);  // column within the quarter
+    const int j = quarter * 32 + jl;
+    const int s = lane & 7;
+    float* col = a.state + (((size_t)b * a.H + h) * D + j) * D + 4 * s;
+    v4f sv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) sv[c] = *(const v4f*)(col + 32 * c);
     const int p = a.pos[b];
     const int s0 = (p + 1) & 3, s1 = (p + 2) & 3, s2 = (p + 3) & 3, sw = p & 3;
     const float* xin = a.proj + (size_t)b * a.proj_stride;
@@ -726,12 +736,8 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
         vv[tid] = ggml_silu(conv(ch));
         ring[(size_t)ch * 4 + sw] = xin[ch];
     }
-    __syncthreads();
+    lds_barrier();  // the state loads stay in flight
 
-    const int lane = tid & 63, wv = tid >> 6;
-    const int jl = wv * 8 + (lane >> 3);  // column within the quarter
-    const int j = quarter * 32 + jl;
-    const int s = lane & 7;
     float q[4][4], k[4][4];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
@@ -769,11 +775,10 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     float gain, beta, sp, gr;
     gdn_coef(xin[4 * W + h], xin[4 * W + a.H + h], a.dt[h], a.ssm_a[h], gain, beta, sp, gr);
     const float vj = vv[jl];
-    float* col = a.state + (((size_t)b * a.H + h) * D + j) * D + 4 * s;
     float cv[4][4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-        const v4f v = *(const v4f*)(col + 32 * c);
+        const v4f v = sv[c];
         cv[c][0] = v.x * gain; cv[c][1] = v.y * gain; cv[c][2] = v.z * gain; cv[c][3] = v.w * gain;
     }
     const float prev = column_dot(cv, k);
@@ -1059,18 +1064,38 @@ __global__ __launch_bounds__(256) void attn_decode_stats_kernel(AttnDecodeArgs a
     }
 }
 
-// Grid (256/32, kv_heads, B): the value sum of attn_pv_kernel (32 FMA chains
-// over tokens per channel, lib.rs:1276-1305) for the G query heads of one kv
-// head.  Lane = channel-quad * 8 + chain % 8, wave = chain / 8: a thread runs
-// chain `a` for 4 adjacent channels (8-byte value loads).  Per 512-token
-// tile the values and scores are loaded in one go, p = GGML exp(score - max)
-// * inv is staged in LDS, the chains advance in token order; the fixed tree
-// and the sigmoid output gate (forward.rs:751) finish.
-template <typename KV, int G>
+// CPT consecutive cache elements as f32 (CPT = 1, 2 or 4).
+template <typename KV, int CPT>
+__device__ __forceinline__ void kv_ldn(const KV* p, float (&o)[CPT]) {
+    if constexpr (CPT == 4) {
+        kv_ld4<KV>(p, o);
+    } else if constexpr (sizeof(KV) == 4) {
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) o[c] = ((const float*)p)[c];
+    } else if constexpr (CPT == 2) {
+        const uint32_t v = *(const uint32_t*)p;
+        o[0] = __uint_as_float(v << 16);
+        o[1] = __uint_as_float(v & 0xffff0000u);
+    } else {
+        o[0] = __uint_as_float((uint32_t)*(const uint16_t*)p << 16);
+    }
+}
+
+// Grid (256 / (8 CPT), kv_heads, B): the value sum of attn_pv_kernel (32
+// FMA chains over tokens per channel, lib.rs:1276-1305) for the G query
+// heads of one kv head, over 8 CPT channels per workgroup.  Lane =
+// channel-group * 8 + chain % 8, wave = chain / 8: a thread runs chain `a`
+// for CPT adjacent channels.  Per tile of 32 NV tokens every value and score
+// load is issued at once, p = GGML exp(score - max) * inv is staged in LDS
+// as [token][4 heads] (every workgroup of a kv head forms the same p), and
+// the chains advance in token order; the fixed tree and the sigmoid output
+// gate (forward.rs:751) finish.  The LDS barriers do not wait for the value
+// loads, which are consumed only by the chains.
+template <typename KV, int G, int CPT, int NV>
 __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
-    constexpr int D = 256, TT = 512, NV = TT / 32;
-    __shared__ float pt[G][TT];
-    __shared__ float red[G][32][33];
+    constexpr int D = 256, TT = 32 * NV, CB = 8 * CPT, NS = G * TT / 256;
+    __shared__ v4f pt[TT];
+    __shared__ float red[G][CB][33];
     const int kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int T = a.pos[b] + 1;
@@ -1081,70 +1106,72 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
         mx[g] = a.stats[((size_t)b * a.nq + kvh * G + g) * 2];
         inv[g] = a.stats[((size_t)b * a.nq + kvh * G + g) * 2 + 1];
     }
+    float gate = 0.0f;
+    if (tid < G * CB) {
+        const int g = tid / CB, c = tid % CB;
+        gate = a.proj[(size_t)b * a.proj_stride + (size_t)(kvh * G + g) * 2 * D + D + blockIdx.x * CB + c];
+    }
     const int cq = lane >> 3, ai = wv * 8 + (lane & 7);
-    const int j0 = blockIdx.x * 32 + cq * 4;
+    const int j0 = blockIdx.x * CB + cq * CPT;
     const KV* vb = (const KV*)a.vcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D + j0;
     const size_t vstep = (size_t)a.nkv * D;
-    float acc[G][4];
+    float acc[G][CPT];
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[g][c] = 0.0f;
+        for (int c = 0; c < CPT; ++c) acc[g][c] = 0.0f;
     for (int t0 = 0; t0 < T; t0 += TT) {
-        float vv[NV][4];
+        float vv[NV][CPT];
 #pragma unroll
         for (int n = 0; n < NV; ++n) {
             const int t = t0 + ai + 32 * n;
             if (t < T) {
-                kv_ld4<KV>(vb + (size_t)t * vstep, vv[n]);
+                kv_ldn<KV, CPT>(vb + (size_t)t * vstep, vv[n]);
             } else {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) vv[n][c] = 0.0f;
+                for (int c = 0; c < CPT; ++c) vv[n][c] = 0.0f;
             }
         }
-        float sv[G * TT / 256];
+        float sv[NS];
 #pragma unroll
-        for (int r = 0; r < G * TT / 256; ++r) {
+        for (int r = 0; r < NS; ++r) {
             const int i = tid + 256 * r, g = i / TT, t = t0 + i % TT;
             sv[r] = t < T ? sb[(size_t)g * a.head_stride + t] : 0.0f;
         }
 #pragma unroll
-        for (int r = 0; r < G * TT / 256; ++r) {
+        for (int r = 0; r < NS; ++r) {
             const int i = tid + 256 * r, g = i / TT, tt = i % TT;
-            pt[g][tt] = t0 + tt < T ? ggml_exp(sv[r] - mx[g]) * inv[g] : 0.0f;
+            ((float*)&pt[tt])[g] = t0 + tt < T ? ggml_exp(sv[r] - mx[g]) * inv[g] : 0.0f;
         }
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int n = 0; n < NV; ++n) {
             const int tt = ai + 32 * n;
             if (t0 + tt < T) {
+                const v4f p4 = pt[tt];
 #pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const float pv = pt[g][tt];
+                for (int g = 0; g < G; ++g)
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) acc[g][c] = fmaf(vv[n][c], pv, acc[g][c]);
-                }
+                    for (int c = 0; c < CPT; ++c) acc[g][c] = fmaf(vv[n][c], p4[g], acc[g][c]);
             }
         }
-        __syncthreads();
+        lds_barrier();
     }
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) red[g][cq * 4 + c][ai] = acc[g][c];
+        for (int c = 0; c < CPT; ++c) red[g][cq * CPT + c][ai] = acc[g][c];
     __syncthreads();
-    if (tid < G * 32) {
-        const int g = tid >> 5, c = tid & 31;
+    if (tid < G * CB) {
+        const int g = tid / CB, c = tid % CB;
         const float* r = red[g][c];
         float comb[8];
 #pragma unroll
         for (int l = 0; l < 8; ++l) comb[l] = (r[l] + r[16 + l]) + (r[8 + l] + r[24 + l]);
         const float h0 = comb[0] + comb[4], h1 = comb[1] + comb[5], h2 = comb[2] + comb[6], h3 = comb[3] + comb[7];
         float v = (h0 + h1) + (h2 + h3);
-        const int jj = blockIdx.x * 32 + c, h = kvh * G + g;
-        const float gate = a.proj[(size_t)b * a.proj_stride + (size_t)h * 2 * D + D + jj];
         v = v * source_sigmoid(gate);
-        a.out[(size_t)b * a.out_stride + (size_t)h * D + jj] = v;
+        a.out[(size_t)b * a.out_stride + (size_t)(kvh * G + g) * D + blockIdx.x * CB + c] = v;
     }
 }
 
@@ -1156,7 +1183,14 @@ static void launch_attn(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
     const unsigned nblk = (unsigned)std::min<size_t>((a.max_ctx + 31) / 32, want);
     hipLaunchKernelGGL((attn_decode_qk_kernel<KV, G>), dim3(nblk, a.nkv, (unsigned)B), dim3(256), 0, s, a);
     hipLaunchKernelGGL(attn_decode_stats_kernel, dim3(a.nq, (unsigned)B), dim3(256), 0, s, a);
-    hipLaunchKernelGGL((attn_decode_pv_kernel<KV, G>), dim3(256 / 32, a.nkv, (unsigned)B), dim3(256), 0, s, a);
+    // channels per thread: 1 while rows are few (more workgroups, a whole
+    // 3072-token context per load burst), 4 once rows supply the parallelism
+    if (B >= 8)
+        hipLaunchKernelGGL((attn_decode_pv_kernel<KV, G, 4, 16>), dim3(256 / 32, a.nkv, (unsigned)B), dim3(256), 0, s,
+                           a);
+    else
+        hipLaunchKernelGGL((attn_decode_pv_kernel<KV, G, 1, 96>), dim3(256 / 8, a.nkv, (unsigned)B), dim3(256), 0, s,
+                           a);
 }
 
 hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s) {

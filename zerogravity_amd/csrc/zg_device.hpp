@@ -58,6 +58,11 @@ __device__ __forceinline__ T wave_sum_xor(T v, int width) {
     return v;
 }
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS
+// operations, not for its outstanding global loads, which stay in flight
+// across it (__syncthreads waits for those too).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
     return v;

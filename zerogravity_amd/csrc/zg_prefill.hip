@@ -56,11 +56,6 @@ __device__ __forceinline__ f4m mfma4(float a, float b, f4m c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Workgroup barrier for LDS traffic only: waits for this wave's LDS
-// operations, not for its outstanding global loads (which carry the next
-// chunk's operands across the barrier).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 // 16x16 output tiles of X Y^T over K = kD (X, Y: rows of 128 in LDS with
 // pitch kPad), one MFMA chain each.  Lane l supplies X[i0 + l%16][4s + l/16]
 // and Y[j0 + l%16][4s + l/16]; result register r is

@@ -202,6 +202,34 @@ int zg_gdn_chunk_prefill_device(zg_ctx* ctx, size_t tokens, size_t heads, const 
     return ZG_COMPLETED;
 }
 
+// One GDN layer's token step for `rows` sequences on device buffers (the
+// resident decode step's kernel; forward.rs:518-632 up to the gated norm).
+int zg_gdn_decode_device(zg_ctx* ctx, size_t rows, size_t heads, const float* proj, size_t proj_stride,
+                         const float* conv_w, float* ring, const int32_t* positions, const float* dt,
+                         const float* ssm_a, float eps, float* state, float* core, void* stream) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!proj || !conv_w || !ring || !positions || !dt || !ssm_a || !state || !core || rows == 0 || heads == 0 ||
+        rows > 65535 || heads > 1024 || proj_stride < heads * 128 * 4 + 2 * heads || !(eps > 0.0f))
+        return fail(ctx, ZG_E_MALFORMED, "GDN decode geometry");
+    zg::GdnDecodeArgs d;
+    d.proj = proj;
+    d.proj_stride = proj_stride;
+    d.conv_w = conv_w;
+    d.ring = ring;
+    d.pos = positions;
+    d.dt = dt;
+    d.ssm_a = ssm_a;
+    d.eps = eps;
+    d.scale = 1.0f / sqrtf(128.0f);
+    d.state = state;
+    d.core = core;
+    d.H = (int)heads;
+    ZG_HIP(zg::gdn_decode(d, rows, stream ? (hipStream_t)stream : ctx->stream));
+    return ZG_COMPLETED;
+}
+
 int zg_rope_kv(zg_ctx* ctx, const float* query, const float* key, const float* value, size_t head_width,
                size_t query_heads, size_t kv_heads, size_t rotate, size_t position, float theta_scale, float* query_out,
                float* key_out, float* value_out) {
