@@ -118,9 +118,7 @@ __device__ void wg_prologue(const FusedGemvArgs& a, int m, bool valid, uint32_t*
         }
         if (!(valid && k < K)) e[0] = e[1] = e[2] = e[3] = 0.0f;
         float amax = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = group8_max_all(amax);
         const int l = tid & 7;
         if (k < K) {
             if (CODEC == kCodecQ8) {
@@ -139,9 +137,7 @@ __device__ void wg_prologue(const FusedGemvArgs& a, int m, bool valid, uint32_t*
         }
         if (CODEC == kCodecQ4K) {
             float sum = ((e[0] + e[1]) + e[2]) + e[3];
-            sum += __shfl_xor(sum, 4, 64);
-            sum += __shfl_xor(sum, 2, 64);
-            sum += __shfl_xor(sum, 1, 64);
+            sum = group8_sum_all(sum);
             if (k < K) {
                 const float qi = amax == 0.0f ? 0.0f : 32767.0f / amax;
                 const int q0 = (int)rintf(e[0] * qi), q1 = (int)rintf(e[1] * qi);
@@ -293,8 +289,8 @@ __global__ __launch_bounds__(256) void fused_q4k_kernel(FusedGemvArgs a, int lpr
                 }
             }
 #pragma unroll
-            for (int m = 0; m < MT; ++m) acc[m] = wave_sum_xor(acc[m], lpr);
-            if (row < N && sub == 0) {
+            for (int m = 0; m < MT; ++m) acc[m] = group_sum_last(acc[m], lpr_log2);
+            if (row < N && sub == lpr - 1) {
 #pragma unroll
                 for (int m = 0; m < MT; ++m)
                     if (m0 + m < a.M) epilogue(a, m0 + m, row, acc[m], EPI);
@@ -695,6 +691,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
     constexpr int D = 128;
     __shared__ float qk[2 * D];
     __shared__ float vv[32];
+    __shared__ float gates[2];
     const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3, b = blockIdx.y;
     const int tid = threadIdx.x;
     const int W = a.H * D;
@@ -736,6 +733,14 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
         vv[tid] = ggml_silu(conv(ch));
         ring[(size_t)ch * 4 + sw] = xin[ch];
     }
+    // the head's gates (f64-evaluated transcendentals) once per workgroup,
+    // by the wave without value channels
+    if (tid == 192) {
+        float gn, bt, sp, gr;
+        gdn_coef(xin[4 * W + h], xin[4 * W + a.H + h], a.dt[h], a.ssm_a[h], gn, bt, sp, gr);
+        gates[0] = gn;
+        gates[1] = bt;
+    }
     lds_barrier();  // the state loads stay in flight
 
     float q[4][4], k[4][4];
@@ -772,8 +777,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
             const float tk = k[c][t] * ik;
             k[c][t] = tk * dsq;
         }
-    float gain, beta, sp, gr;
-    gdn_coef(xin[4 * W + h], xin[4 * W + a.H + h], a.dt[h], a.ssm_a[h], gain, beta, sp, gr);
+    const float gain = gates[0], beta = gates[1];
     const float vj = vv[jl];
     float cv[4][4];
 #pragma unroll

@@ -58,6 +58,51 @@ __device__ __forceinline__ T wave_sum_xor(T v, int width) {
     return v;
 }
 
+// DPP lane moves (VALU, no LDS round trip).  dpp_f<CTRL> returns, in each
+// lane, the value of the lane CTRL selects (0 where the source lies outside
+// the row and bound_ctrl applies).
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWMASK, 0xf, true));
+}
+constexpr int kDppXor1 = 0xb1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4e;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within 8
+
+// Sum over groups of W consecutive lanes (W = 2..64), complete in the LAST
+// lane of each group (row shifts toward higher lanes, then row broadcasts).
+template <int W>
+__device__ __forceinline__ float group_sum_last(float v) {
+    if (W >= 2) v += dpp_f<0x111>(v);       // row_shr:1
+    if (W >= 4) v += dpp_f<0x112>(v);       // row_shr:2
+    if (W >= 8) v += dpp_f<0x114>(v);       // row_shr:4
+    if (W >= 16) v += dpp_f<0x118>(v);      // row_shr:8
+    if (W >= 32) v += dpp_f<0x142, 0xa>(v); // row_bcast:15 into rows 1 and 3
+    if (W >= 64) v += dpp_f<0x143, 0xc>(v); // row_bcast:31 into rows 2 and 3
+    return v;
+}
+__device__ __forceinline__ float group_sum_last(float v, int log2w) {
+    switch (log2w) {
+    case 1: return group_sum_last<2>(v);
+    case 2: return group_sum_last<4>(v);
+    case 3: return group_sum_last<8>(v);
+    case 4: return group_sum_last<16>(v);
+    case 5: return group_sum_last<32>(v);
+    default: return group_sum_last<64>(v);
+    }
+}
+// Max / sum over aligned groups of 8 lanes, the result in every lane.
+__device__ __forceinline__ float group8_max_all(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    return fmaxf(v, dpp_f<kDppHalfMirror>(v));
+}
+__device__ __forceinline__ float group8_sum_all(float v) {
+    v += dpp_f<kDppXor1>(v);
+    v += dpp_f<kDppXor2>(v);
+    return v + dpp_f<kDppHalfMirror>(v);
+}
+
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS
 // operations, not for its outstanding global loads, which stay in flight
 // across it (__syncthreads waits for those too).
