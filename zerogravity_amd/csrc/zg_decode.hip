@@ -84,8 +84,8 @@ __device__ void wg_prologue(const FusedGemvArgs& a, int m, bool valid, uint32_t*
             s += (double)q2;
             s += (double)q3;
         }
-        s = wave_sum_xor<double>(s, 64);
-        if (lane == 0) red[tid >> 6] = s;
+        s = group_sum_last<64>(s);
+        if (lane == 63) red[tid >> 6] = s;
         __syncthreads();
         inv = rms_inv((red[0] + red[1]) + (red[2] + red[3]), K, a.eps);
     }
@@ -106,7 +106,8 @@ __device__ void wg_prologue(const FusedGemvArgs& a, int m, bool valid, uint32_t*
                 const float q = e[t] * e[t];
                 s += (double)q;
             }
-            s = wave_sum_xor<double>(s, 32);
+            s = group_sum_last<32>(s);
+            s = __shfl(s, (lane & 32) | 31, 64);
             const float gi = rms_inv(s, a.group, a.eps);
             const v4f g = k < K ? *(const v4f*)(a.gamma + (k & (a.group - 1))) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
             const float gg[4] = {g.x, g.y, g.z, g.w};
@@ -395,8 +396,8 @@ __global__ __launch_bounds__(256) void act16_kernel(FusedGemvArgs a, _Float16* _
             s += (double)q2;
             s += (double)q3;
         }
-        s = wave_sum_xor<double>(s, 64);
-        if (lane == 0) red[tid >> 6] = s;
+        s = group_sum_last<64>(s);
+        if (lane == 63) red[tid >> 6] = s;
         __syncthreads();
         inv = rms_inv((red[0] + red[1]) + (red[2] + red[3]), K, a.eps);
     }
@@ -416,7 +417,8 @@ __global__ __launch_bounds__(256) void act16_kernel(FusedGemvArgs a, _Float16* _
                 const float q = e[t] * e[t];
                 s += (double)q;
             }
-            s = wave_sum_xor<double>(s, 32);
+            s = group_sum_last<32>(s);
+            s = __shfl(s, (lane & 32) | 31, 64);
             const float gi = rms_inv(s, a.group, a.eps);
             const v4f g = k < K ? *(const v4f*)(a.gamma + (k & (a.group - 1))) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
             const float gg[4] = {g.x, g.y, g.z, g.w};
@@ -444,78 +446,106 @@ __global__ __launch_bounds__(256) void act16_kernel(FusedGemvArgs a, _Float16* _
 // n = l%32.  Per 256-element Q4_K block a lane reads the 8-byte pieces
 // 32*c4 + 16*half + 8*(l/32) of its weight row: K step s (16 per block)
 // uses piece (s/4, s%2), nibble (s/2)&1, group s/2.  Weights are
-// dequantized as the reference does (f32(q)*scale - min, two roundings)
-// and rounded once to f16; activations arrive in f16.  Each wave owns 32
-// weight rows x 32 activation rows, 4 waves per workgroup.
-template <int EPI, int KS>
+// dequantized on packed f16: the nibble q becomes the f16 1024 + q by a
+// byte permute, 1024 is subtracted exactly, and w = fma(q, scale, -min)
+// with the group's scale and min rounded once to f16 (one rounding of the
+// weight, against the reference's f32 q*scale - min then rounded to f16:
+// they differ by the f16 rounding of scale and min).  Activations arrive in
+// f16.  A wave owns NT tiles of 32 weight rows for 32 activation rows, so
+// every activation load feeds NT MFMAs.
+template <int EPI, int KS, int NT>
 __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, const _Float16* __restrict__ xh) {
-    // KS waves share one 32 x 32 output tile and split its K blocks
-    // (wave w takes blocks w, w+KS, ...); the partial tiles are summed in a
-    // fixed order through LDS, so the result does not depend on timing.
+    // KS waves share the NT output tiles and split their K blocks (wave w
+    // takes blocks w, w+KS, ...); the partial tiles are summed in a fixed
+    // order through LDS, so the result does not depend on timing.
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
     __shared__ float red[KS][16][64];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, hsel = lane >> 5, r32 = lane & 31;
-    const int n0 = blockIdx.x * 32;
+    const int nb0 = blockIdx.x * 32 * NT;
     const int m0 = blockIdx.y * 32;
     const int K = a.K, N = a.N, nbk = K >> 8;
-    const int n = n0 + r32;
-    const bool nv = n < N;
-    const uint8_t* qrow = (const uint8_t*)a.qs + (size_t)(nv ? n : 0) * (K >> 1) + 8 * hsel;
-    const v4u* hrow = (const v4u*)a.hdr + (size_t)(nv ? n : 0) * nbk;
+    bool nv[NT];
+    const uint8_t* qrow[NT];
+    const v4u* hrow[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int n = nb0 + 32 * t + r32;
+        nv[t] = n < N;
+        qrow[t] = (const uint8_t*)a.qs + (size_t)(nv[t] ? n : 0) * (K >> 1) + 8 * hsel;
+        hrow[t] = (const v4u*)a.hdr + (size_t)(nv[t] ? n : 0) * nbk;
+    }
     const _Float16* xrow = xh + (size_t)(m0 + r32) * K + 8 * hsel;
-    f16v acc = {};
+    f16v acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = f16v{};
     for (int kb = wv; kb < nbk; kb += KS) {
-        uint2 pc[4][2];
+        uint2 pc[NT][4][2];
+        v4u hd[NT];
 #pragma unroll
-        for (int c4 = 0; c4 < 4; ++c4)
+        for (int t = 0; t < NT; ++t) {
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf) pc[c4][hf] = *(const uint2*)(qrow + (size_t)kb * 128 + 32 * c4 + 16 * hf);
-        const v4u hd = hrow[kb];
+            for (int c4 = 0; c4 < 4; ++c4)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+                    pc[t][c4][hf] = *(const uint2*)(qrow[t] + (size_t)kb * 128 + 32 * c4 + 16 * hf);
+            hd[t] = hrow[t][kb];
+        }
         h8v xa[16];
 #pragma unroll
         for (int s = 0; s < 16; ++s) xa[s] = *(const h8v*)(xrow + (size_t)kb * 256 + 16 * s);
-        const float d = f16_to_f32((uint16_t)(hd.x & 0xffffu));
-        const float dmin = f16_to_f32((uint16_t)(hd.x >> 16));
-        float scale[8], mnv[8];
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            uint32_t sc, mn;
-            q4k_dev_scale_min(hd, g, sc, mn);
-            scale[g] = d * (float)sc;
-            mnv[g] = dmin * (float)mn;
-        }
+        for (int t = 0; t < NT; ++t) {
+            const float d = f16_to_f32((uint16_t)(hd[t].x & 0xffffu));
+            const float dmin = f16_to_f32((uint16_t)(hd[t].x >> 16));
+            h2v sc2[8], nm2[8];
 #pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            const int g = s >> 1, nib = (s >> 1) & 1;
-            const uint2 pw = pc[s >> 2][s & 1];
-            const uint32_t w0 = (nib ? (pw.x >> 4) : pw.x) & 0x0f0f0f0fu;
-            const uint32_t w1 = (nib ? (pw.y >> 4) : pw.y) & 0x0f0f0f0fu;
-            h8v wb;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float q0 = (float)((w0 >> (8 * e)) & 0xffu);
-                const float q1 = (float)((w1 >> (8 * e)) & 0xffu);
-                const float t0 = q0 * scale[g];
-                const float t1 = q1 * scale[g];
-                wb[e] = nv ? (_Float16)(t0 - mnv[g]) : (_Float16)0.0f;
-                wb[4 + e] = nv ? (_Float16)(t1 - mnv[g]) : (_Float16)0.0f;
+            for (int g = 0; g < 8; ++g) {
+                uint32_t sc, mn;
+                q4k_dev_scale_min(hd[t], g, sc, mn);
+                const _Float16 sh = (_Float16)(d * (float)sc), mh = (_Float16)(dmin * (float)mn);
+                sc2[g] = h2v{sh, sh};
+                nm2[g] = h2v{-mh, -mh};
             }
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[s], wb, acc, 0, 0, 0);
+            const h2v bias = h2v{(_Float16)1024.0f, (_Float16)1024.0f};
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const int g = s >> 1, nib = (s >> 1) & 1;
+                const uint2 pw = pc[t][s >> 2][s & 1];
+                const uint32_t w0 = (nib ? (pw.x >> 4) : pw.x) & 0x0f0f0f0fu;
+                const uint32_t w1 = (nib ? (pw.y >> 4) : pw.y) & 0x0f0f0f0fu;
+                // bytes (q, 0x64) pairs: the f16 bit patterns of 1024 + q
+                const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u);
+                const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u);
+                const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u);
+                const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u);
+                const h2v e0 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p0) - bias, sc2[g], nm2[g]);
+                const h2v e1 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p1) - bias, sc2[g], nm2[g]);
+                const h2v e2 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p2) - bias, sc2[g], nm2[g]);
+                const h2v e3 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p3) - bias, sc2[g], nm2[g]);
+                h8v wb = h8v{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
+                if (!nv[t]) wb = h8v{};
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[s], wb, acc[t], 0, 0, 0);
+            }
         }
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[wv][r][lane] = acc[r];
-    __syncthreads();
-    // wave w finishes registers r = w, w+KS, ... of every lane
-    for (int r = wv; r < 16; r += KS) {
-        float v;
-        if (KS == 4) {
-            v = (red[0][r][lane] + red[1][r][lane]) + (red[2][r][lane] + red[3][r][lane]);
-        } else {
-            v = ((red[0][r][lane] + red[1][r][lane]) + (red[2][r][lane] + red[3][r][lane])) +
-                ((red[4][r][lane] + red[5][r][lane]) + (red[6][r][lane] + red[7][r][lane]));
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[wv][r][lane] = acc[t][r];
+        __syncthreads();
+        // wave w finishes registers r = w, w+KS, ... of every lane
+        for (int r = wv; r < 16; r += KS) {
+            float v;
+            if (KS == 4) {
+                v = (red[0][r][lane] + red[1][r][lane]) + (red[2][r][lane] + red[3][r][lane]);
+            } else {
+                v = ((red[0][r][lane] + red[1][r][lane]) + (red[2][r][lane] + red[3][r][lane])) +
+                    ((red[4][r][lane] + red[5][r][lane]) + (red[6][r][lane] + red[7][r][lane]));
+            }
+            const int m = m0 + (r & 3) + 8 * (r >> 2) + 4 * hsel;
+            if (nv[t] && m < a.M) epilogue(a, m, nb0 + 32 * t + r32, v, EPI);
         }
-        const int m = m0 + (r & 3) + 8 * (r >> 2) + 4 * hsel;
-        if (nv && m < a.M) epilogue(a, m, n, v, EPI);
+        __syncthreads();
     }
 }
 
@@ -546,17 +576,33 @@ hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* 
     case PRO_PLAIN: launch_act16<PRO_PLAIN>(a, mpad, xh, s); break;
     default: return hipErrorInvalidValue;
     }
-    // one 32-row weight tile per workgroup, K split over 8 waves when the
-    // matrix has few tiles, else over 4
-    dim3 g((unsigned)((a.N + 31) / 32), (unsigned)(mpad / 32));
-    const bool wide = (a.N + 31) / 32 >= 512;
+    // NT tiles of 32 weight rows per workgroup (each activation load feeds
+    // NT MFMAs) while that still leaves >= 192 workgroups; K split over 8
+    // waves when the workgroups are few, else over 4
+    const int tiles = (a.N + 31) / 32;
+    const int nt = tiles / 4 >= 192 ? 4 : (tiles / 2 >= 192 ? 2 : 1);
+    dim3 g((unsigned)((tiles + nt - 1) / nt), (unsigned)(mpad / 32));
+    const bool wide = (tiles + nt - 1) / nt >= 512;
+#define ZG_MQ(E, KSV, NTV) hipLaunchKernelGGL((mfma_q4k_kernel<E, KSV, NTV>), g, dim3(64 * KSV), 0, s, a, (const _Float16*)xh)
+#define ZG_MQN(E, KSV)            \
+    if (nt == 4) ZG_MQ(E, KSV, 4);      \
+    else if (nt == 2) ZG_MQ(E, KSV, 2); \
+    else ZG_MQ(E, KSV, 1);
     if (a.epi == EPI_RESID) {
-        if (wide) hipLaunchKernelGGL((mfma_q4k_kernel<EPI_RESID, 4>), g, dim3(256), 0, s, a, (const _Float16*)xh);
-        else hipLaunchKernelGGL((mfma_q4k_kernel<EPI_RESID, 8>), g, dim3(512), 0, s, a, (const _Float16*)xh);
+        if (wide) {
+            ZG_MQN(EPI_RESID, 4)
+        } else {
+            ZG_MQN(EPI_RESID, 8)
+        }
     } else {
-        if (wide) hipLaunchKernelGGL((mfma_q4k_kernel<EPI_STORE, 4>), g, dim3(256), 0, s, a, (const _Float16*)xh);
-        else hipLaunchKernelGGL((mfma_q4k_kernel<EPI_STORE, 8>), g, dim3(512), 0, s, a, (const _Float16*)xh);
+        if (wide) {
+            ZG_MQN(EPI_STORE, 4)
+        } else {
+            ZG_MQN(EPI_STORE, 8)
+        }
     }
+#undef ZG_MQN
+#undef ZG_MQ
     return hipGetLastError();
 }
 
@@ -762,8 +808,8 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
             sq += (double)a2;
             sk += (double)b2;
         }
-    sq = wave_sum_xor<double>(sq, 8);
-    sk = wave_sum_xor<double>(sk, 8);
+    sq = group8_sum_all(sq);
+    sk = group8_sum_all(sk);
     const float dsq = 1.0f / sqrtf((float)D);
     const float eps_d = a.eps / (float)D;
     const float iq = 1.0f / sqrtf((float)(sq / (double)D) + eps_d);

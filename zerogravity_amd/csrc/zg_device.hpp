@@ -91,6 +91,29 @@ __device__ __forceinline__ float group_sum_last(float v, int log2w) {
     default: return group_sum_last<64>(v);
     }
 }
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ double dpp_d(double v) {
+    const unsigned long long u = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(u & 0xffffffffu), CTRL, ROWMASK, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(u >> 32), CTRL, ROWMASK, 0xf, true);
+    return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+template <int W>
+__device__ __forceinline__ double group_sum_last(double v) {
+    if (W >= 2) v += dpp_d<0x111>(v);
+    if (W >= 4) v += dpp_d<0x112>(v);
+    if (W >= 8) v += dpp_d<0x114>(v);
+    if (W >= 16) v += dpp_d<0x118>(v);
+    if (W >= 32) v += dpp_d<0x142, 0xa>(v);
+    if (W >= 64) v += dpp_d<0x143, 0xc>(v);
+    return v;
+}
+__device__ __forceinline__ double group8_sum_all(double v) {
+    v += dpp_d<0xb1>(v);
+    v += dpp_d<0x4e>(v);
+    return v + dpp_d<0x141>(v);
+}
+
 // Max / sum over aligned groups of 8 lanes, the result in every lane.
 __device__ __forceinline__ float group8_max_all(float v) {
     v = fmaxf(v, dpp_f<kDppXor1>(v));
