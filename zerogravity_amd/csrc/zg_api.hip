@@ -46,7 +46,9 @@ void free_weight(zg_weight* w) {
     if (!w) return;
     if (w->dw.qs) (void)hipFree(w->dw.qs);
     if (w->dw.hdr) (void)hipFree(w->dw.hdr);
-    w->dw.qs = w->dw.hdr = nullptr;
+    if (w->dw.qs_t) (void)hipFree(w->dw.qs_t);
+    if (w->dw.hdr_t) (void)hipFree(w->dw.hdr_t);
+    w->dw.qs = w->dw.hdr = w->dw.qs_t = w->dw.hdr_t = nullptr;
 }
 
 bool supported_type(int t) { return t == ZG_Q8_0 || t == ZG_Q4_K || t == ZG_F32; }
@@ -428,6 +430,10 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
         f.ldy = w->dw.N;
         f.status = ctx->d_flag;
         if (m_rows > 4 && w->dw.type == zg::kQ4_K) {
+            if (!w->dw.qs_t) {
+                ZG_HIP(hipStreamSynchronize(s));
+                ZG_HIP(zg::ensure_mfma_tiles(const_cast<zg_weight*>(w)->dw, s));
+            }
             const size_t need = zg::batched_scratch_bytes(m_rows, w->dw.K);
             if (ctx->actbuf.bytes < need) ZG_HIP(hipStreamSynchronize(s));
             int rc = ensure(ctx, ctx->actbuf, need);

@@ -367,7 +367,11 @@ typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
 // One workgroup per activation row (rows M..Mpad-1 zero): the prologue
-// values of wg_prologue, rounded once to f16, into xh[Mpad][K].
+// values of wg_prologue, rounded once to f16, into xh in the MFMA A-operand
+// order of 32-row tiles: element (m, k) of tile mt = m/32 sits at
+// ((mt*(K/256) + k/256)*16 + (k%256)/16)*64 + (k%16)/8*32 + m%32, times 8,
+// plus k%8, so that lane l of the MFMA kernel loads step s of its K block
+// as 16 contiguous bytes and a wave-instruction reads 1 KB contiguous.
 template <int PRO, int JMAX>
 __global__ __launch_bounds__(256) void act16_kernel(FusedGemvArgs a, _Float16* __restrict__ xh) {
     __shared__ double red[4];
@@ -433,7 +437,9 @@ __global__ __launch_bounds__(256) void act16_kernel(FusedGemvArgs a, _Float16* _
             h4v hv4;
 #pragma unroll
             for (int t = 0; t < 4; ++t) hv4[t] = valid ? (_Float16)e[t] : (_Float16)0.0f;
-            *(h4v*)(xh + (size_t)m * K + k) = hv4;
+            const size_t lane_t = (size_t)((k & 15) >> 3) * 32 + (m & 31);
+            const size_t at = ((((size_t)(m >> 5) * (K >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + lane_t) * 8 + (k & 7);
+            *(h4v*)(xh + at) = hv4;
         }
     }
 }
@@ -443,9 +449,11 @@ __global__ __launch_bounds__(256) void act16_kernel(FusedGemvArgs a, _Float16* _
 // so D[i = m][j = n] and the lanes of a row store adjacent outputs.  Lane l
 // holds A[m = l%32][k = 8*(l/32) + e] and B[k = 8*(l/32) + e][n = l%32]
 // (e < 8); D register r is row m = (r%4) + 8*(r/4) + 4*(l/32), column
-// n = l%32.  Per 256-element Q4_K block a lane reads the 8-byte pieces
+// n = l%32.  Per 256-element Q4_K block a lane uses the 8-byte pieces
 // 32*c4 + 16*half + 8*(l/32) of its weight row: K step s (16 per block)
-// uses piece (s/4, s%2), nibble (s/2)&1, group s/2.  Weights are
+// uses piece (s/4, s%2), nibble (s/2)&1, group s/2.  Weights, headers and
+// activations come in tile order (ensure_mfma_tiles, act16_kernel): each
+// wave-instruction reads one contiguous run.  Weights are
 // dequantized on packed f16: the nibble q becomes the f16 1024 + q by a
 // byte permute, 1024 is subtracted exactly, and w = fma(q, scale, -min)
 // with the group's scale and min rounded once to f16 (one rounding of the
@@ -465,16 +473,17 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
     const int m0 = blockIdx.y * 32;
     const int K = a.K, N = a.N, nbk = K >> 8;
     bool nv[NT];
-    const uint8_t* qrow[NT];
-    const v4u* hrow[NT];
+    const v4u* qtile[NT];
+    const v4u* htile[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        const int n = nb0 + 32 * t + r32;
-        nv[t] = n < N;
-        qrow[t] = (const uint8_t*)a.qs + (size_t)(nv[t] ? n : 0) * (K >> 1) + 8 * hsel;
-        hrow[t] = (const v4u*)a.hdr + (size_t)(nv[t] ? n : 0) * nbk;
+        const int tile = blockIdx.x * NT + t;
+        nv[t] = nb0 + 32 * t + r32 < N;
+        const int tt = min(tile, (N - 1) >> 5);  // tiles past the end read the last one (results dropped)
+        qtile[t] = (const v4u*)a.qs + (size_t)tt * nbk * 256 + lane;
+        htile[t] = (const v4u*)a.hdr + (size_t)tt * nbk * 32 + r32;
     }
-    const _Float16* xrow = xh + (size_t)(m0 + r32) * K + 8 * hsel;
+    const h8v* xtile = (const h8v*)xh + (size_t)blockIdx.y * nbk * 1024 + lane;
     f16v acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = f16v{};
@@ -484,15 +493,16 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
 #pragma unroll
-            for (int c4 = 0; c4 < 4; ++c4)
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf)
-                    pc[t][c4][hf] = *(const uint2*)(qrow[t] + (size_t)kb * 128 + 32 * c4 + 16 * hf);
-            hd[t] = hrow[t][kb];
+            for (int c4 = 0; c4 < 4; ++c4) {
+                const v4u q = qtile[t][((size_t)kb * 4 + c4) * 64];
+                pc[t][c4][0] = make_uint2(q.x, q.y);
+                pc[t][c4][1] = make_uint2(q.z, q.w);
+            }
+            hd[t] = htile[t][(size_t)kb * 32];
         }
         h8v xa[16];
 #pragma unroll
-        for (int s = 0; s < 16; ++s) xa[s] = *(const h8v*)(xrow + (size_t)kb * 256 + 16 * s);
+        for (int s = 0; s < 16; ++s) xa[s] = xtile[((size_t)kb * 16 + s) * 64];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const float d = f16_to_f32((uint16_t)(hd[t].x & 0xffffu));
@@ -551,6 +561,54 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
 
 size_t batched_scratch_bytes(size_t M, size_t K) { return ((M + 31) / 32) * 32 * K * 2; }
 
+// Grid (tiles, K/256), 256 threads: Q4_K payload and headers of 32-row tile
+// `tile`, block kb, into the MFMA operand order: thread (c4, lane) writes
+// the 16 bytes lane l uses for pieces (c4, 0) and (c4, 1), the 8 bytes at
+// 32*c4 + 8*(l/32) and 32*c4 + 16 + 8*(l/32) of row 32*tile + l%32; rows
+// past N are zero (d = dmin = 0, so they dequantize to 0).
+__global__ __launch_bounds__(256) void mfma_tile_q4k_kernel(const uint8_t* __restrict__ qs, const v4u* __restrict__ hdr,
+                                                            int N, int K, v4u* __restrict__ qs_t,
+                                                            v4u* __restrict__ hdr_t) {
+    const int tile = blockIdx.x, kb = blockIdx.y, nbk = K >> 8;
+    const int tid = threadIdx.x, c4 = tid >> 6, lane = tid & 63;
+    const int row = tile * 32 + (lane & 31), hsel = lane >> 5;
+    v4u out = v4u{0u, 0u, 0u, 0u};
+    if (row < N) {
+        const uint8_t* b = qs + (size_t)row * (K >> 1) + (size_t)kb * 128 + 32 * c4 + 8 * hsel;
+        const uint2 p0 = *(const uint2*)b, p1 = *(const uint2*)(b + 16);
+        out = v4u{p0.x, p0.y, p1.x, p1.y};
+    }
+    qs_t[(((size_t)tile * nbk + kb) * 4 + c4) * 64 + lane] = out;
+    if (tid < 32) {
+        const int r = tile * 32 + tid;
+        hdr_t[((size_t)tile * nbk + kb) * 32 + tid] = r < N ? hdr[(size_t)r * nbk + kb] : v4u{0u, 0u, 0u, 0u};
+    }
+}
+
+hipError_t ensure_mfma_tiles(DeviceWeight& w, hipStream_t s) {
+    if (w.type != kQ4_K || w.K % 256 || w.N == 0) return hipErrorInvalidValue;
+    if (w.qs_t) return hipSuccess;
+    const size_t tiles = (w.N + 31) / 32, nbk = w.K / 256;
+    void *q = nullptr, *h = nullptr;
+    hipError_t e = hipMalloc(&q, tiles * nbk * 4096);
+    if (e == hipSuccess) e = hipMalloc(&h, tiles * nbk * 512);
+    if (e != hipSuccess) {
+        if (q) (void)hipFree(q);
+        return e;
+    }
+    hipLaunchKernelGGL(mfma_tile_q4k_kernel, dim3((unsigned)tiles, (unsigned)nbk), dim3(256), 0, s,
+                       (const uint8_t*)w.qs, (const v4u*)w.hdr, (int)w.N, (int)w.K, (v4u*)q, (v4u*)h);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+        (void)hipFree(q);
+        (void)hipFree(h);
+        return e;
+    }
+    w.qs_t = q;
+    w.hdr_t = h;
+    return hipSuccess;
+}
+
 template <int PRO>
 static void launch_act16(const FusedGemvArgs& a, int mpad, _Float16* xh, hipStream_t s) {
     if (a.K <= 1024) hipLaunchKernelGGL((act16_kernel<PRO, 1>), dim3(mpad), dim3(256), 0, s, a, xh);
@@ -562,9 +620,10 @@ static void launch_act16(const FusedGemvArgs& a, int mpad, _Float16* xh, hipStre
 hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* scratch, hipStream_t s) {
     if (w.type != kQ4_K || w.K % 256 || w.K > 8192 || args.M <= 0 || args.M > 64) return hipErrorInvalidValue;
     if (args.pro == PRO_GATED && args.group != 128) return hipErrorInvalidValue;
+    if (!w.qs_t || !w.hdr_t) return hipErrorNotReady;  // ensure_mfma_tiles first
     FusedGemvArgs a = args;
-    a.qs = w.qs;
-    a.hdr = w.hdr;
+    a.qs = w.qs_t;
+    a.hdr = w.hdr_t;
     a.K = (int)w.K;
     a.N = (int)w.N;
     const int mpad = (a.M + 31) / 32 * 32;

@@ -22,6 +22,10 @@ struct DeviceWeight {
     void* qs = nullptr;
     void* hdr = nullptr;
     size_t qs_bytes = 0, hdr_bytes = 0;
+    // Q4_K only, built on demand for the batched-row MFMA path: payload and
+    // headers in the MFMA operand order of 32-row tiles (ensure_mfma_tiles).
+    void* qs_t = nullptr;
+    void* hdr_t = nullptr;
 };
 
 size_t gguf_row_bytes(int type, size_t K);
@@ -150,6 +154,9 @@ hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& a, hipStream_t
 // Batched rows (M <= 64, Q4_K): the prologue values rounded to f16 into
 // `scratch` (batched_scratch_bytes), then an f16 MFMA GEMM with the epilogue.
 size_t batched_scratch_bytes(size_t M, size_t K);
+// Builds w.qs_t / w.hdr_t (Q4_K) if absent: allocates, so call it outside
+// graph capture.  batched_gemv refuses a Q4_K weight without them.
+hipError_t ensure_mfma_tiles(DeviceWeight& w, hipStream_t s);
 hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& a, void* scratch, hipStream_t s);
 
 // GDN decode: conv (4-slot ring per channel) + SiLU + q/k L2 + gates +

@@ -409,6 +409,17 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     if (max_batch == 0 || max_batch > 64 || max_context == 0 || max_context > g.max_context)
         return fail(ctx, ZG_E_LIMIT, "session batch must be 1..64 and context within the model's");
     if (kv_dtype != ZG_BF16 && kv_dtype != ZG_F32) return fail(ctx, ZG_E_MALFORMED, "KV cache dtype must be BF16 or F32");
+    if (max_batch > 4) {
+        // the batched-row path reads Q4_K weights in MFMA tile order
+        std::vector<zg_weight*> ws = {m->embd};
+        for (auto& L : m->layers) ws.insert(ws.end(), {L.in_proj, L.out_proj, L.ffn_gu, L.ffn_down});
+        for (zg_weight* w : ws)
+            if (w && w->dw.type == zg::kQ4_K && !w->dw.qs_t) {
+                const hipError_t e = zg::ensure_mfma_tiles(w->dw, ctx->stream);
+                if (e != hipSuccess) return fail(ctx, ZG_E_RESOURCE, "MFMA tile layout of a Q4_K weight");
+            }
+        if (hipStreamSynchronize(ctx->stream) != hipSuccess) return fail(ctx, ZG_E_DEVICE, "tile layout build");
+    }
     auto s = new zg_session();
     s->m = m;
     s->max_batch = max_batch;
