@@ -318,3 +318,31 @@ def test_qwen35_08b_q8_0_prompt32_greedy32(kern, model_08b, kv):
     assert worst <= LOGIT_TOL
     assert seq_gpu == seq_ref
     m.close()
+
+
+WIDE = dict(hidden=2048, layers=4, ffn=6144, vocab=1000, gdn_heads=16, gdn_dim=128, q_heads=8, kv_heads=2,
+            head_dim=256, full_attention_interval=4, max_context=4096, eps=1e-6)
+
+
+def test_batched_split_k_rows_match_oracle(kern):
+    """The 2B layer shapes at B=32: the 2048-row residual projections split
+    K over workgroups (ssm_out and o-proj 2 ways, the FFN down projection 6
+    ways) and the next RMS activation kernel adds the partial tiles into the
+    residual stream; every row must track its CPU session within the
+    end-to-end bound with the same greedy tokens."""
+    t = qwen35.synthetic_tensors(WIDE, gguf.Q4_K, seed=21)
+    B, steps = 32, 3
+    m = qwen35.QwenModelHip(WIDE, t, kernel=kern)
+    s = m.session(max_batch=B, max_context=64, kv_dtype=L.F32)
+    toks = _tokens(17, B * steps, WIDE["vocab"]).reshape(steps, B)
+    got = [s.step(toks[i])[0] for i in range(steps)]
+    worst = 0.0
+    for b in range(0, B, 5):
+        o = _oracle(WIDE, t).session()
+        for i in range(steps):
+            ref = o.forward(int(toks[i, b]))
+            worst = max(worst, float(np.max(np.abs(got[i][b] - ref))))
+            assert int(np.argmax(got[i][b])) == int(np.argmax(ref)), (b, i)
+    print(f"batched split-K B={B}: worst logit max-abs {worst:.3e}")
+    assert worst <= LOGIT_TOL
+    m.close()

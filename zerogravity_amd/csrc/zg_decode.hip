@@ -389,6 +389,23 @@ __global__ __launch_bounds__(256) void act16_kernel(FusedGemvArgs a, _Float16* _
             if (PRO == PRO_GATED || PRO == PRO_SILU_MUL) w[j] = *(const v4f*)(a.x2 + (size_t)m * a.ldx2 + k);
         }
     }
+    if (PRO == PRO_RMS && a.rsplits > 0) {
+        // the residual the previous (split-K) GEMM left pending: x += sum of
+        // its partial tiles, split 0 first, written back as the new x
+        const size_t mpad = (size_t)gridDim.x;
+#pragma unroll
+        for (int j = 0; j < JMAX; ++j) {
+            const int k = 4 * tid + 1024 * j;
+            if (valid && k < K) {
+                v4f acc = *(const v4f*)(a.rparts + (size_t)m * K + k);
+                for (int z = 1; z < a.rsplits; ++z) acc = acc + *(const v4f*)(a.rparts + ((size_t)z * mpad + m) * K + k);
+                v[j] = v[j] + acc;
+                *(v4f*)(a.xw + (size_t)m * a.ldx + k) = v[j];
+                if (!finite_f32(v[j].x) || !finite_f32(v[j].y) || !finite_f32(v[j].z) || !finite_f32(v[j].w))
+                    atomicOr(a.status, 1);
+            }
+        }
+    }
     float inv = 1.0f;
     if (PRO == PRO_RMS) {
         double s = 0.0;
@@ -487,7 +504,10 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
     f16v acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = f16v{};
-    for (int kb = wv; kb < nbk; kb += KS) {
+    // K blocks of this workgroup: all, or its 1/gridDim.z share (split-K)
+    const int per = (nbk + gridDim.z - 1) / gridDim.z;
+    const int kb0 = blockIdx.z * per, kb1 = min(nbk, kb0 + per);
+    for (int kb = kb0 + wv; kb < kb1; kb += KS) {
         uint2 pc[NT][4][2];
         v4u hd[NT];
 #pragma unroll
@@ -553,13 +573,25 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
                     ((red[4][r][lane] + red[5][r][lane]) + (red[6][r][lane] + red[7][r][lane]));
             }
             const int m = m0 + (r & 3) + 8 * (r >> 2) + 4 * hsel;
-            if (nv[t] && m < a.M) epilogue(a, m, nb0 + 32 * t + r32, v, EPI);
+            if (gridDim.z > 1) {
+                if (nv[t]) a.parts[((size_t)blockIdx.z * 32 * gridDim.y + m) * N + nb0 + 32 * t + r32] = v;
+            } else if (nv[t] && m < a.M) {
+                epilogue(a, m, nb0 + 32 * t + r32, v, EPI);
+            }
         }
         __syncthreads();
     }
 }
 
 size_t batched_scratch_bytes(size_t M, size_t K) { return ((M + 31) / 32) * 32 * K * 2; }
+
+int batched_splits(size_t N, size_t K) {
+    // few 32-row tiles leave most CUs idle: split K over workgroups of 4
+    // waves, one block per wave
+    const size_t tiles = (N + 31) / 32, nbk = K / 256;
+    if (tiles >= 128 || nbk < 8) return 1;
+    return (int)std::min<size_t>(8, nbk / 4);
+}
 
 // Grid (tiles, K/256), 256 threads: Q4_K payload and headers of 32-row tile
 // `tile`, block kb, into the MFMA operand order: thread (c4, lane) writes
@@ -640,8 +672,9 @@ hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* 
     // waves when the workgroups are few, else over 4
     const int tiles = (a.N + 31) / 32;
     const int nt = tiles / 4 >= 192 ? 4 : (tiles / 2 >= 192 ? 2 : 1);
-    dim3 g((unsigned)((tiles + nt - 1) / nt), (unsigned)(mpad / 32));
-    const bool wide = (tiles + nt - 1) / nt >= 512;
+    const int splits = a.epi == EPI_RESID && a.splits > 1 && a.parts ? a.splits : 1;
+    dim3 g((unsigned)((tiles + nt - 1) / nt), (unsigned)(mpad / 32), (unsigned)splits);
+    const bool wide = (tiles + nt - 1) / nt >= 512 || splits > 1;
 #define ZG_MQ(E, KSV, NTV) hipLaunchKernelGGL((mfma_q4k_kernel<E, KSV, NTV>), g, dim3(64 * KSV), 0, s, a, (const _Float16*)xh)
 #define ZG_MQN(E, KSV)            \
     if (nt == 4) ZG_MQ(E, KSV, 4);      \

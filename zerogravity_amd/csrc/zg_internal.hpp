@@ -148,7 +148,19 @@ struct FusedGemvArgs {
     float* y = nullptr;
     size_t ldy = 0;
     int* status = nullptr;
+    // batched rows only.  splits > 1 (EPI_RESID): the GEMM writes partial
+    // tiles parts[split][Mpad][N] instead of adding into y; the following
+    // PRO_RMS call over y passes them as rparts/rsplits and its activation
+    // kernel first adds their fixed-order sum into its input rows (x, which
+    // must then be writable: xw).
+    float* parts = nullptr;
+    int splits = 0;
+    const float* rparts = nullptr;
+    int rsplits = 0;
+    float* xw = nullptr;
 };
+// K splits for a residual batched GEMM of this shape (1: none).
+int batched_splits(size_t N, size_t K);
 bool fused_gemv_supported(int type, size_t K, size_t N, int pro);
 hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& a, hipStream_t s);
 // Batched rows (M <= 64, Q4_K): the prologue values rounded to f16 into

@@ -62,6 +62,7 @@ struct zg_session {
     float *x = nullptr, *y0 = nullptr, *core = nullptr, *ao = nullptr, *logits = nullptr, *scores = nullptr,
           *pmax = nullptr, *att_stats = nullptr;
     void* xh = nullptr;  // f16 activations of the batched (B > 4) projections
+    float* parts = nullptr;  // split-K partial tiles of residual projections (B > 4)
     size_t y0w = 0;
     std::vector<float*> ring, rec;  // per GDN layer: conv ring [B][3W][4], state [B][H][128][128]
     std::vector<void*> kc, vc;      // per attention layer: [B][max_ctx][kv_heads*256]
@@ -153,6 +154,7 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
     const zg_geometry& g = m->g;
     const size_t H = g.hidden, F = g.ffn, V = g.vocab, W = (size_t)g.gdn_heads * g.gdn_dim;
     const size_t QD = (size_t)g.q_heads * g.head_dim;
+    int pending = 0;  // splits of a residual GEMM whose partial tiles the next RMS activation adds
     auto gemv = [&](zg_weight* w, int pro, const float* x, size_t ldx, const float* x2, size_t ldx2,
                     const float* gamma, int epi, float* y, size_t ldy) {
         zg::FusedGemvArgs f;
@@ -171,7 +173,25 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
         f.status = s->d_status;
         // one launch with the prologue in-kernel up to 4 rows; beyond, the
         // activation in f16 and the MFMA GEMM (weights read once)
-        if (B > 4 && w->dw.type == zg::kQ4_K) return zg::batched_gemv(w->dw, f, s->xh, st);
+        if (pending && !(B > 4 && w->dw.type == zg::kQ4_K && pro == zg::PRO_RMS && x == s->x))
+            return hipErrorInvalidValue;  // a pending split-K residual must be consumed by the next RMS projection
+        if (B > 4 && w->dw.type == zg::kQ4_K) {
+            if (pending && pro == zg::PRO_RMS && x == s->x) {
+                f.rparts = s->parts;
+                f.rsplits = pending;
+                f.xw = s->x;
+                pending = 0;
+            }
+            if (epi == zg::EPI_RESID && y == s->x) {
+                const int sp = zg::batched_splits(w->dw.N, w->dw.K);
+                if (sp > 1) {
+                    f.parts = s->parts;
+                    f.splits = sp;
+                    pending = sp;
+                }
+            }
+            return zg::batched_gemv(w->dw, f, s->xh, st);
+        }
         return zg::fused_gemv(w->dw, f, st);
     };
     ZG_HIP(zg::embed(m->embd->dw, tokens, s->x, B, s->d_status, st));
@@ -444,6 +464,7 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     A((void**)&s->pmax, zg::argmax_partials(B) * 4);
     A((void**)&s->att_stats, B * g.q_heads * 2 * 4);
     A(&s->xh, zg::batched_scratch_bytes(B, std::max({H, F, W, QD})));
+    if (B > 4) A((void**)&s->parts, 8 * ((B + 31) / 32 * 32) * H * sizeof(float));
     A((void**)&s->pidx, zg::argmax_partials(B) * 4);
     A((void**)&s->x, B * H * 4);
     A((void**)&s->y0, B * s->y0w * 4);
