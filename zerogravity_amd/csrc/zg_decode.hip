@@ -182,17 +182,32 @@ __global__ __launch_bounds__(256) void fused_q4k_kernel(FusedGemvArgs a, int lpr
     const uint8_t* qs = (const uint8_t*)a.qs;
     const v4u* hdr = (const v4u*)a.hdr;
 
+    // row of lane group rsub in row group rg; with EPI_GLU a row group holds
+    // rpw/2 (gate j, up j) pairs: even groups gate row j, odd groups up row
+    // N/2 + j
+    auto row_of = [&](int rg) {
+        if (EPI == EPI_GLU) {
+            const int j = rg * (rpw >> 1) + (rsub >> 1);
+            return (rsub & 1) ? (N >> 1) + j : j;
+        }
+        return rg * rpw + rsub;
+    };
+    auto row_ok = [&](int rg) {
+        if (EPI == EPI_GLU) return rg * (rpw >> 1) + (rsub >> 1) < (N >> 1);
+        return rg * rpw + rsub < N;
+    };
     // RG consecutive row groups per wave, all their loads issued together
     v4i w0[RG][CH], w1[RG][CH];
     v4u h[RG][CH];
     auto load_rows = [&](int rg0) {
 #pragma unroll
         for (int r = 0; r < RG; ++r) {
-            const int row = (rg0 + r) * rpw + rsub;
+            const int row = row_of(rg0 + r);
+            const bool rok = row_ok(rg0 + r);
 #pragma unroll
             for (int i = 0; i < CH; ++i) {
                 const int c = sub + i * lpr;
-                if (row < N && c < nchunk) {
+                if (rok && c < nchunk) {
                     const uint8_t* base = qs + (size_t)row * (K >> 1) + (size_t)c * 32;
                     w0[r][i] = load_nt(base);
                     w1[r][i] = load_nt(base + 16);
@@ -242,12 +257,13 @@ __global__ __launch_bounds__(256) void fused_q4k_kernel(FusedGemvArgs a, int lpr
         }
 
     bool first = true;
-    for (int rg0 = wave * RG; rg0 * rpw < N; rg0 += nwaves * RG) {
+    for (int rg0 = wave * RG; rg0 * rpw < N; rg0 += nwaves * RG) {  // (GLU: rg0 * rpw/2 < N/2, the same)
         if (!first) load_rows(rg0);
         first = false;
 #pragma unroll
         for (int r = 0; r < RG; ++r) {
-            const int row = (rg0 + r) * rpw + rsub;
+            const int row = row_of(rg0 + r);
+            const bool rok = row_ok(rg0 + r);
             float acc[MT];
 #pragma unroll
             for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
@@ -291,7 +307,18 @@ __global__ __launch_bounds__(256) void fused_q4k_kernel(FusedGemvArgs a, int lpr
             }
 #pragma unroll
             for (int m = 0; m < MT; ++m) acc[m] = group_sum_last(acc[m], lpr_log2);
-            if (row < N && sub == lpr - 1) {
+            if (EPI == EPI_GLU) {
+                // the gate sum sits in the last lane of the group before
+                float gv[MT];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) gv[m] = __shfl(acc[m], lane >= lpr ? lane - lpr : lane, 64);
+                if (rok && (rsub & 1) && sub == lpr - 1) {
+                    const int j = row - (N >> 1);
+#pragma unroll
+                    for (int m = 0; m < MT; ++m)
+                        if (m0 + m < a.M) a.y[(size_t)(m0 + m) * a.ldy + j] = acc[m] * ggml_silu(gv[m]);
+                }
+            } else if (rok && sub == lpr - 1) {
 #pragma unroll
                 for (int m = 0; m < MT; ++m)
                     if (m0 + m < a.M) epilogue(a, m0 + m, row, acc[m], EPI);
@@ -486,16 +513,18 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
     typedef _Float16 h2v __attribute__((ext_vector_type(2)));
     __shared__ float red[KS][16][64];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, hsel = lane >> 5, r32 = lane & 31;
-    const int nb0 = blockIdx.x * 32 * NT;
     const int m0 = blockIdx.y * 32;
     const int K = a.K, N = a.N, nbk = K >> 8;
     bool nv[NT];
+    int nbase[NT];
     const v4u* qtile[NT];
     const v4u* htile[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        const int tile = blockIdx.x * NT + t;
-        nv[t] = nb0 + 32 * t + r32 < N;
+        // EPI_GLU (NT = 2): gate tile x and the up tile N/64 tiles later
+        const int tile = EPI == EPI_GLU ? blockIdx.x + t * (N >> 6) : blockIdx.x * NT + t;
+        nbase[t] = tile * 32;
+        nv[t] = nbase[t] + r32 < N;
         const int tt = min(tile, (N - 1) >> 5);  // tiles past the end read the last one (results dropped)
         qtile[t] = (const v4u*)a.qs + (size_t)tt * nbk * 256 + lane;
         htile[t] = (const v4u*)a.hdr + (size_t)tt * nbk * 32 + r32;
@@ -558,13 +587,16 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
             }
         }
     }
+    float vg[16 / KS];  // EPI_GLU: the gate tile's sums
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) red[wv][r][lane] = acc[t][r];
         __syncthreads();
         // wave w finishes registers r = w, w+KS, ... of every lane
-        for (int r = wv; r < 16; r += KS) {
+#pragma unroll
+        for (int i = 0; i < 16 / KS; ++i) {
+            const int r = wv + KS * i;
             float v;
             if (KS == 4) {
                 v = (red[0][r][lane] + red[1][r][lane]) + (red[2][r][lane] + red[3][r][lane]);
@@ -573,10 +605,21 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
                     ((red[4][r][lane] + red[5][r][lane]) + (red[6][r][lane] + red[7][r][lane]));
             }
             const int m = m0 + (r & 3) + 8 * (r >> 2) + 4 * hsel;
-            if (gridDim.z > 1) {
-                if (nv[t]) a.parts[((size_t)blockIdx.z * 32 * gridDim.y + m) * N + nb0 + 32 * t + r32] = v;
+            if (EPI == EPI_GLU) {
+                if (t == 0) {
+                    vg[i] = v;
+                } else if (nv[t]) {
+                    // up * silu(gate), rounded to f16 into the down
+                    // projection's activation tiles (K2 = N/2 columns)
+                    const int j = nbase[0] + r32, nbk2 = (N >> 1) >> 8;
+                    const size_t at = ((((size_t)(m >> 5) * nbk2 + (j >> 8)) * 16 + ((j & 255) >> 4)) * 64 +
+                                       ((j & 15) >> 3) * 32 + (m & 31)) * 8 + (j & 7);
+                    ((_Float16*)a.xh_out)[at] = (_Float16)(m < a.M ? v * ggml_silu(vg[i]) : 0.0f);
+                }
+            } else if (gridDim.z > 1) {
+                if (nv[t]) a.parts[((size_t)blockIdx.z * 32 * gridDim.y + m) * N + nbase[t] + r32] = v;
             } else if (nv[t] && m < a.M) {
-                epilogue(a, m, nb0 + 32 * t + r32, v, EPI);
+                epilogue(a, m, nbase[t] + r32, v, EPI);
             }
         }
         __syncthreads();
@@ -660,12 +703,23 @@ hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* 
     a.N = (int)w.N;
     const int mpad = (a.M + 31) / 32 * 32;
     _Float16* xh = (_Float16*)scratch;
-    switch (a.pro) {
-    case PRO_RMS: launch_act16<PRO_RMS>(a, mpad, xh, s); break;
-    case PRO_GATED: launch_act16<PRO_GATED>(a, mpad, xh, s); break;
-    case PRO_SILU_MUL: launch_act16<PRO_SILU_MUL>(a, mpad, xh, s); break;
-    case PRO_PLAIN: launch_act16<PRO_PLAIN>(a, mpad, xh, s); break;
-    default: return hipErrorInvalidValue;
+    if (a.xh_in) {
+        xh = (_Float16*)a.xh_in;  // prepared by the previous GEMM's EPI_GLU
+    } else {
+        switch (a.pro) {
+        case PRO_RMS: launch_act16<PRO_RMS>(a, mpad, xh, s); break;
+        case PRO_GATED: launch_act16<PRO_GATED>(a, mpad, xh, s); break;
+        case PRO_SILU_MUL: launch_act16<PRO_SILU_MUL>(a, mpad, xh, s); break;
+        case PRO_PLAIN: launch_act16<PRO_PLAIN>(a, mpad, xh, s); break;
+        default: return hipErrorInvalidValue;
+        }
+    }
+    if (a.epi == EPI_GLU) {
+        if (!batched_glu_supported(w.type, w.K, w.N) || !a.xh_out) return hipErrorInvalidValue;
+        dim3 g((unsigned)(a.N / 64), (unsigned)(mpad / 32), 1u);
+        if (a.N / 64 >= 512) hipLaunchKernelGGL((mfma_q4k_kernel<EPI_GLU, 4, 2>), g, dim3(256), 0, s, a, (const _Float16*)xh);
+        else hipLaunchKernelGGL((mfma_q4k_kernel<EPI_GLU, 8, 2>), g, dim3(512), 0, s, a, (const _Float16*)xh);
+        return hipGetLastError();
     }
     // NT tiles of 32 weight rows per workgroup (each activation load feeds
     // NT MFMAs) while that still leaves >= 192 workgroups; K split over 8
@@ -784,9 +838,25 @@ static hipError_t launch_q8(const FusedGemvArgs& a, hipStream_t s) {
 
 template <int PRO>
 static hipError_t launch_pro(const FusedGemvArgs& a, int type, hipStream_t s) {
+    if (a.epi == EPI_GLU) {
+        if constexpr (PRO == PRO_RMS) {
+            if (type == kQ4_K) return launch_q4k<PRO_RMS, EPI_GLU>(a, s);
+        }
+        return hipErrorInvalidValue;
+    }
     if (type == kQ4_K) return a.epi == EPI_RESID ? launch_q4k<PRO, EPI_RESID>(a, s) : launch_q4k<PRO, EPI_STORE>(a, s);
     if (type == kQ8_0) return a.epi == EPI_RESID ? launch_q8<PRO, EPI_RESID>(a, s) : launch_q8<PRO, EPI_STORE>(a, s);
     return hipErrorInvalidValue;
+}
+
+bool fused_glu_supported(int type, size_t K, size_t N) {
+    // a row group must hold whole (gate, up) pairs: 64 lanes over <= 32
+    // lanes per row (K <= 2048), rpw even
+    return type == kQ4_K && K % 256 == 0 && K <= 2048 && N % 2 == 0 && N > 0;
+}
+
+bool batched_glu_supported(int type, size_t K, size_t N) {
+    return type == kQ4_K && K % 256 == 0 && K <= 8192 && N % 64 == 0 && (N / 2) % 256 == 0;
 }
 
 bool fused_gemv_supported(int type, size_t K, size_t N, int pro) {
@@ -801,6 +871,7 @@ bool fused_gemv_supported(int type, size_t K, size_t N, int pro) {
 hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& args, hipStream_t s) {
     if (!fused_gemv_supported(w.type, w.K, w.N, args.pro) || args.M <= 0) return hipErrorInvalidValue;
     if (args.pro == PRO_GATED && args.group != 128) return hipErrorInvalidValue;  // 32 lanes x 4 per group
+    if (args.epi == EPI_GLU && !fused_glu_supported(w.type, w.K, w.N)) return hipErrorInvalidValue;
     FusedGemvArgs a = args;
     a.qs = w.qs;
     a.hdr = w.hdr;

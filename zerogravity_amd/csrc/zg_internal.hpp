@@ -130,8 +130,12 @@ hipError_t advance_positions(int* pos, int* ntok, size_t B, hipStream_t s);  // 
 //   PRO_PLAIN     x
 //   EPI_STORE     y[m][n] = W a
 //   EPI_RESID     y[m][n] += W a, nonfinite -> status bit 0
+//   EPI_GLU       stacked [gate (N/2 rows) | up (N/2 rows)]:
+//                 y[m][j] = up_j * silu(gate_j) for j < N/2 (the SwiGLU
+//                 product the down projection takes, forward.rs ffn);
+//                 batched rows write it in f16 MFMA tile order to xh_out
 enum { PRO_RMS = 0, PRO_GATED = 1, PRO_SILU_MUL = 2, PRO_PLAIN = 3 };
-enum { EPI_STORE = 0, EPI_RESID = 1 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_GLU = 2 };
 struct FusedGemvArgs {
     const void* qs = nullptr;  // filled from the weight
     const void* hdr = nullptr;
@@ -158,7 +162,13 @@ struct FusedGemvArgs {
     const float* rparts = nullptr;
     int rsplits = 0;
     float* xw = nullptr;
+    void* xh_out = nullptr;      // EPI_GLU, batched: f16 tiled product
+    const void* xh_in = nullptr;  // batched: f16 tiled activation ready (no activation kernel)
 };
+// EPI_GLU offered for these shapes (fused path: K <= 2048 so a row group
+// holds a gate and an up row; batched path: N/2 a multiple of 32).
+bool fused_glu_supported(int type, size_t K, size_t N);
+bool batched_glu_supported(int type, size_t K, size_t N);
 // K splits for a residual batched GEMM of this shape (1: none).
 int batched_splits(size_t N, size_t K);
 bool fused_gemv_supported(int type, size_t K, size_t N, int pro);

@@ -63,6 +63,7 @@ struct zg_session {
           *pmax = nullptr, *att_stats = nullptr;
     void* xh = nullptr;  // f16 activations of the batched (B > 4) projections
     float* parts = nullptr;  // split-K partial tiles of residual projections (B > 4)
+    void* xh2 = nullptr;     // the SwiGLU product in f16 tiles, down projection input (B > 4)
     size_t y0w = 0;
     std::vector<float*> ring, rec;  // per GDN layer: conv ring [B][3W][4], state [B][H][128][128]
     std::vector<void*> kc, vc;      // per attention layer: [B][max_ctx][kv_heads*256]
@@ -156,7 +157,8 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
     const size_t QD = (size_t)g.q_heads * g.head_dim;
     int pending = 0;  // splits of a residual GEMM whose partial tiles the next RMS activation adds
     auto gemv = [&](zg_weight* w, int pro, const float* x, size_t ldx, const float* x2, size_t ldx2,
-                    const float* gamma, int epi, float* y, size_t ldy) {
+                    const float* gamma, int epi, float* y, size_t ldy, void* xh_out = nullptr,
+                    const void* xh_in = nullptr) {
         zg::FusedGemvArgs f;
         f.M = (int)B;
         f.pro = pro;
@@ -171,6 +173,8 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
         f.y = y;
         f.ldy = ldy;
         f.status = s->d_status;
+        f.xh_out = xh_out;
+        f.xh_in = xh_in;
         // one launch with the prologue in-kernel up to 4 rows; beyond, the
         // activation in f16 and the MFMA GEMM (weights read once)
         if (pending && !(B > 4 && w->dw.type == zg::kQ4_K && pro == zg::PRO_RMS && x == s->x))
@@ -244,8 +248,21 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             ZG_HIP(zg::attn_decode(a, B, st));
             ZG_HIP(gemv(L.out_proj, zg::PRO_PLAIN, s->ao, QD, nullptr, 0, nullptr, zg::EPI_RESID, s->x, H));
         }
-        ZG_HIP(gemv(L.ffn_gu, zg::PRO_RMS, s->x, H, nullptr, 0, L.post_norm, zg::EPI_STORE, s->y0, s->y0w));
-        ZG_HIP(gemv(L.ffn_down, zg::PRO_SILU_MUL, s->y0, s->y0w, s->y0 + F, s->y0w, nullptr, zg::EPI_RESID, s->x, H));
+        const zg::DeviceWeight& gu = L.ffn_gu->dw;
+        const bool glu = L.ffn_down->dw.type == zg::kQ4_K &&
+                         (B > 4 ? zg::batched_glu_supported(gu.type, gu.K, gu.N) : zg::fused_glu_supported(gu.type, gu.K, gu.N));
+        if (glu) {
+            // SwiGLU in the gate/up epilogue: the down projection takes the
+            // product as a plain activation (f16 tiles when batched)
+            ZG_HIP(gemv(L.ffn_gu, zg::PRO_RMS, s->x, H, nullptr, 0, L.post_norm, zg::EPI_GLU, s->y0, s->y0w,
+                        B > 4 ? s->xh2 : nullptr));
+            ZG_HIP(gemv(L.ffn_down, zg::PRO_PLAIN, s->y0, s->y0w, nullptr, 0, nullptr, zg::EPI_RESID, s->x, H, nullptr,
+                        B > 4 ? s->xh2 : nullptr));
+        } else {
+            ZG_HIP(gemv(L.ffn_gu, zg::PRO_RMS, s->x, H, nullptr, 0, L.post_norm, zg::EPI_STORE, s->y0, s->y0w));
+            ZG_HIP(gemv(L.ffn_down, zg::PRO_SILU_MUL, s->y0, s->y0w, s->y0 + F, s->y0w, nullptr, zg::EPI_RESID, s->x,
+                        H));
+        }
     }
     if (logits || greedy) {
         float* lg = logits ? logits : s->logits;
@@ -465,6 +482,7 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     A((void**)&s->att_stats, B * g.q_heads * 2 * 4);
     A(&s->xh, zg::batched_scratch_bytes(B, std::max({H, F, W, QD})));
     if (B > 4) A((void**)&s->parts, 8 * ((B + 31) / 32 * 32) * H * sizeof(float));
+    if (B > 4) A(&s->xh2, zg::batched_scratch_bytes(B, F));
     A((void**)&s->pidx, zg::argmax_partials(B) * 4);
     A((void**)&s->x, B * H * 4);
     A((void**)&s->y0, B * s->y0w * 4);
