@@ -375,12 +375,8 @@ __global__ __launch_bounds__(256) void fused_q8_kernel(FusedGemvArgs a) {
             }
         }
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            acc[m] = acc[m] + __shfl_xor(acc[m], 4, 64);
-            acc[m] = acc[m] + __shfl_xor(acc[m], 2, 64);
-            acc[m] = acc[m] + __shfl_xor(acc[m], 1, 64);
-        }
-        if (row < N && l == 0) {
+        for (int m = 0; m < MT; ++m) acc[m] = group8_tree_last(acc[m]);  // the reference's lane tree, in lane 7
+        if (row < N && l == 7) {
 #pragma unroll
             for (int m = 0; m < MT; ++m)
                 if (m0 + m < a.M) epilogue(a, m0 + m, row, acc[m], EPI);
@@ -1103,15 +1099,18 @@ __global__ __launch_bounds__(256) void attn_decode_qk_kernel(AttnDecodeArgs a) {
     const size_t tstep = (size_t)a.nkv * D;
 
     KVPack<KV> kn[8];  // keys of the next token block, loaded ahead
+    // bounded by the cache size, not by the position, so the first loads do
+    // not wait for it; tokens at or past the position are replaced or
+    // dropped where they are used
     auto load_keys = [&](int tb) {
         const int t = tb * 32 + (tid >> 3);
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            if (t < T && t != p) kn[c].load(kc + (size_t)t * tstep + 32 * c + 4 * s);
+            if (t < a.max_ctx) kn[c].load(kc + (size_t)t * tstep + 32 * c + 4 * s);
             else kn[c].zero();
         }
     };
-    if (blockIdx.x * 32 < T) load_keys(blockIdx.x);
+    load_keys(blockIdx.x);
 
     // rotation angles of this position, shared by every head
     if (tid < 32) {
@@ -1204,14 +1203,8 @@ __global__ __launch_bounds__(256) void attn_decode_qk_kernel(AttnDecodeArgs a) {
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float v = acc[g][e];
-                v = v + __shfl_xor(v, 4, 64);
-                v = v + __shfl_xor(v, 2, 64);
-                v = v + __shfl_xor(v, 1, 64);
-                acc[g][e] = v;
-            }
-        if (t < T && s == 0) {
+            for (int e = 0; e < 4; ++e) acc[g][e] = group8_tree_last(acc[g][e]);
+        if (t < T && s == 7) {
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 const float dot = (acc[g][0] + acc[g][1]) + (acc[g][2] + acc[g][3]);
@@ -1243,7 +1236,8 @@ __global__ __launch_bounds__(256) void attn_decode_stats_kernel(AttnDecodeArgs a
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const int at = base + 8 * (tid + 256 * r) + i;
-                    e[r][i] = at < T ? row[at] : -INFINITY;
+                    const float sv = at < a.max_ctx ? row[at] : -INFINITY;  // issued before T is known
+                    e[r][i] = at < T ? sv : -INFINITY;
                 }
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
@@ -1338,7 +1332,7 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
 #pragma unroll
         for (int n = 0; n < NV; ++n) {
             const int t = t0 + ai + 32 * n;
-            if (t < T) {
+            if (t < a.max_ctx) {  // bounded by the cache, not the position: tokens >= T are masked below
                 kv_ldn<KV, CPT>(vb + (size_t)t * vstep, vv[n]);
             } else {
 #pragma unroll
@@ -1349,7 +1343,7 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
 #pragma unroll
         for (int r = 0; r < NS; ++r) {
             const int i = tid + 256 * r, g = i / TT, t = t0 + i % TT;
-            sv[r] = t < T ? sb[(size_t)g * a.head_stride + t] : 0.0f;
+            sv[r] = t < a.max_ctx ? sb[(size_t)g * a.head_stride + t] : 0.0f;
         }
 #pragma unroll
         for (int r = 0; r < NS; ++r) {

@@ -114,6 +114,15 @@ __device__ __forceinline__ double group8_sum_all(double v) {
     return v + dpp_d<0x141>(v);
 }
 
+// The XOR-4/2/1 tree of 8 lanes, ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)),
+// complete in the LAST lane of each group of 8 (row shifts by 4, 2, 1;
+// f32 addition is commutative, so the operand swaps change no bit).
+__device__ __forceinline__ float group8_tree_last(float v) {
+    v += dpp_f<0x114>(v);  // row_shr:4
+    v += dpp_f<0x112>(v);  // row_shr:2
+    return v + dpp_f<0x111>(v);  // row_shr:1
+}
+
 // Max / sum over aligned groups of 8 lanes, the result in every lane.
 __device__ __forceinline__ float group8_max_all(float v) {
     v = fmaxf(v, dpp_f<kDppXor1>(v));
