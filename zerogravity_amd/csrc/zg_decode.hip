@@ -1103,12 +1103,9 @@ __global__ __launch_bounds__(256) void attn_decode_qk_kernel(AttnDecodeArgs a) {
     // not wait for it; tokens at or past the position are replaced or
     // dropped where they are used
     auto load_keys = [&](int tb) {
-        const int t = tb * 32 + (tid >> 3);
+        const int t = min(tb * 32 + (tid >> 3), a.max_ctx - 1);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            if (t < a.max_ctx) kn[c].load(kc + (size_t)t * tstep + 32 * c + 4 * s);
-            else kn[c].zero();
-        }
+        for (int c = 0; c < 8; ++c) kn[c].load(kc + (size_t)t * tstep + 32 * c + 4 * s);
     };
     load_keys(blockIdx.x);
 
@@ -1236,7 +1233,7 @@ __global__ __launch_bounds__(256) void attn_decode_stats_kernel(AttnDecodeArgs a
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const int at = base + 8 * (tid + 256 * r) + i;
-                    const float sv = at < a.max_ctx ? row[at] : -INFINITY;  // issued before T is known
+                    const float sv = row[min(at, a.max_ctx - 1)];  // issued before T is known, no branch
                     e[r][i] = at < T ? sv : -INFINITY;
                 }
 #pragma unroll
@@ -1288,97 +1285,109 @@ __device__ __forceinline__ void kv_ldn(const KV* p, float (&o)[CPT]) {
     }
 }
 
-// Grid (256 / (8 CPT), kv_heads, B): the value sum of attn_pv_kernel (32
-// FMA chains over tokens per channel, lib.rs:1276-1305) for the G query
-// heads of one kv head, over 8 CPT channels per workgroup.  Lane =
+// Grid (256 / (8 CPT), q_heads / HG, B): the value sum of attn_pv_kernel
+// (32 FMA chains over tokens per channel, lib.rs:1276-1305) for HG query
+// heads (sharing one kv head) over 8 CPT channels per workgroup.  Lane =
 // channel-group * 8 + chain % 8, wave = chain / 8: a thread runs chain `a`
 // for CPT adjacent channels.  Per tile of 32 NV tokens every value and score
-// load is issued at once, p = GGML exp(score - max) * inv is staged in LDS
-// as [token][4 heads] (every workgroup of a kv head forms the same p), and
-// the chains advance in token order; the fixed tree and the sigmoid output
-// gate (forward.rs:751) finish.  The LDS barriers do not wait for the value
-// loads, which are consumed only by the chains.
-template <typename KV, int G, int CPT, int NV>
+// load is issued at once (bounded by the cache, not the position, so they
+// do not wait for it), p = GGML exp(score - max) * inv is staged in LDS as
+// [token][heads], and the chains advance in token order; the fixed tree and
+// the sigmoid output gate (forward.rs:751) finish.  The LDS barriers do not
+// wait for the value loads, which only the chains consume.  Few heads and
+// channels per workgroup spread a single row over many workgroups.
+template <typename KV, int HG, int CPT, int NV>
 __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
-    constexpr int D = 256, TT = 32 * NV, CB = 8 * CPT, NS = G * TT / 256;
-    __shared__ v4f pt[TT];
-    __shared__ float red[G][CB][33];
-    const int kvh = blockIdx.y, b = blockIdx.z;
+    constexpr int D = 256, TT = 32 * NV, CB = 8 * CPT, NS = HG * TT / 256, HP = HG == 3 ? 4 : HG;
+    __shared__ float pt[TT * HP];
+    __shared__ float red[HG][CB][33];
+    const int h0 = blockIdx.y * HG, b = blockIdx.z;
+    const int kvh = h0 / (a.nq / a.nkv);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int T = a.pos[b] + 1;
-    const float* sb = a.scores + (size_t)b * a.score_stride + (size_t)kvh * G * a.head_stride;
-    float mx[G], inv[G];
+    const float* sb = a.scores + (size_t)b * a.score_stride + (size_t)h0 * a.head_stride;
+    float mx[HG], inv[HG];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        mx[g] = a.stats[((size_t)b * a.nq + kvh * G + g) * 2];
-        inv[g] = a.stats[((size_t)b * a.nq + kvh * G + g) * 2 + 1];
+    for (int g = 0; g < HG; ++g) {
+        mx[g] = a.stats[((size_t)b * a.nq + h0 + g) * 2];
+        inv[g] = a.stats[((size_t)b * a.nq + h0 + g) * 2 + 1];
     }
     float gate = 0.0f;
-    if (tid < G * CB) {
+    if (tid < HG * CB) {
         const int g = tid / CB, c = tid % CB;
-        gate = a.proj[(size_t)b * a.proj_stride + (size_t)(kvh * G + g) * 2 * D + D + blockIdx.x * CB + c];
+        gate = a.proj[(size_t)b * a.proj_stride + (size_t)(h0 + g) * 2 * D + D + blockIdx.x * CB + c];
     }
     const int cq = lane >> 3, ai = wv * 8 + (lane & 7);
     const int j0 = blockIdx.x * CB + cq * CPT;
     const KV* vb = (const KV*)a.vcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D + j0;
     const size_t vstep = (size_t)a.nkv * D;
-    float acc[G][CPT];
+    float acc[HG][CPT];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < HG; ++g)
 #pragma unroll
         for (int c = 0; c < CPT; ++c) acc[g][c] = 0.0f;
     for (int t0 = 0; t0 < T; t0 += TT) {
+        // unconditional loads (no per-lane branches): token indices clamped
+        // to the cache, values past the position masked where they are used
+        const int tmax = a.max_ctx - 1;
         float vv[NV][CPT];
+        const KV* vt = vb + (size_t)(t0 + ai) * vstep;
+        if (t0 + TT <= a.max_ctx) {
 #pragma unroll
-        for (int n = 0; n < NV; ++n) {
-            const int t = t0 + ai + 32 * n;
-            if (t < a.max_ctx) {  // bounded by the cache, not the position: tokens >= T are masked below
-                kv_ldn<KV, CPT>(vb + (size_t)t * vstep, vv[n]);
-            } else {
+            for (int n = 0; n < NV; ++n) kv_ldn<KV, CPT>(vt + (size_t)(32 * n) * vstep, vv[n]);
+        } else {
 #pragma unroll
-                for (int c = 0; c < CPT; ++c) vv[n][c] = 0.0f;
-            }
+            for (int n = 0; n < NV; ++n) kv_ldn<KV, CPT>(vb + (size_t)min(t0 + ai + 32 * n, tmax) * vstep, vv[n]);
         }
         float sv[NS];
 #pragma unroll
         for (int r = 0; r < NS; ++r) {
             const int i = tid + 256 * r, g = i / TT, t = t0 + i % TT;
-            sv[r] = t < a.max_ctx ? sb[(size_t)g * a.head_stride + t] : 0.0f;
+            sv[r] = sb[(size_t)g * a.head_stride + min(t, tmax)];
         }
 #pragma unroll
         for (int r = 0; r < NS; ++r) {
             const int i = tid + 256 * r, g = i / TT, tt = i % TT;
-            ((float*)&pt[tt])[g] = t0 + tt < T ? ggml_exp(sv[r] - mx[g]) * inv[g] : 0.0f;
+            pt[tt * HP + g] = t0 + tt < T ? ggml_exp(sv[r] - mx[g]) * inv[g] : 0.0f;
         }
         lds_barrier();
 #pragma unroll
         for (int n = 0; n < NV; ++n) {
             const int tt = ai + 32 * n;
-            if (t0 + tt < T) {
-                const v4f p4 = pt[tt];
+            const bool live = t0 + tt < T;  // a select, not a branch: past T the chain is unchanged
+            float p4[HP];
+            if constexpr (HP == 4) {
+                const v4f q = *(const v4f*)&pt[tt * 4];
+                p4[0] = q.x; p4[1] = q.y; p4[2] = q.z; p4[3] = q.w;
+            } else {
 #pragma unroll
-                for (int g = 0; g < G; ++g)
-#pragma unroll
-                    for (int c = 0; c < CPT; ++c) acc[g][c] = fmaf(vv[n][c], p4[g], acc[g][c]);
+                for (int g = 0; g < HP; ++g) p4[g] = pt[tt * HP + g];
             }
+#pragma unroll
+            for (int g = 0; g < HG; ++g)
+#pragma unroll
+                for (int c = 0; c < CPT; ++c) {
+                    const float f = fmaf(vv[n][c], p4[g], acc[g][c]);
+                    acc[g][c] = live ? f : acc[g][c];
+                }
         }
         lds_barrier();
     }
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < HG; ++g)
 #pragma unroll
         for (int c = 0; c < CPT; ++c) red[g][cq * CPT + c][ai] = acc[g][c];
     __syncthreads();
-    if (tid < G * CB) {
+    if (tid < HG * CB) {
         const int g = tid / CB, c = tid % CB;
         const float* r = red[g][c];
         float comb[8];
 #pragma unroll
         for (int l = 0; l < 8; ++l) comb[l] = (r[l] + r[16 + l]) + (r[8 + l] + r[24 + l]);
-        const float h0 = comb[0] + comb[4], h1 = comb[1] + comb[5], h2 = comb[2] + comb[6], h3 = comb[3] + comb[7];
-        float v = (h0 + h1) + (h2 + h3);
+        const float h0s = comb[0] + comb[4], h1 = comb[1] + comb[5], h2 = comb[2] + comb[6], h3 = comb[3] + comb[7];
+        float v = (h0s + h1) + (h2 + h3);
         v = v * source_sigmoid(gate);
-        a.out[(size_t)b * a.out_stride + (size_t)(kvh * G + g) * D + blockIdx.x * CB + c] = v;
+        a.out[(size_t)b * a.out_stride + (size_t)(h0 + g) * D + blockIdx.x * CB + c] = v;
     }
 }
 
@@ -1390,14 +1399,14 @@ static void launch_attn(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
     const unsigned nblk = (unsigned)std::min<size_t>((a.max_ctx + 31) / 32, want);
     hipLaunchKernelGGL((attn_decode_qk_kernel<KV, G>), dim3(nblk, a.nkv, (unsigned)B), dim3(256), 0, s, a);
     hipLaunchKernelGGL(attn_decode_stats_kernel, dim3(a.nq, (unsigned)B), dim3(256), 0, s, a);
-    // channels per thread: 1 while rows are few (more workgroups, a whole
-    // 3072-token context per load burst), 4 once rows supply the parallelism
+    // batch 1: one head and 8 channels per workgroup (a row over 32 x nq
+    // workgroups, each token tile in one burst); rows in numbers: the kv
+    // head's G heads and 32 channels per workgroup
     if (B >= 8)
-        hipLaunchKernelGGL((attn_decode_pv_kernel<KV, G, 4, 16>), dim3(256 / 32, a.nkv, (unsigned)B), dim3(256), 0, s,
+        hipLaunchKernelGGL((attn_decode_pv_kernel<KV, G, 4, 16>), dim3(256 / 32, a.nq / G, (unsigned)B), dim3(256), 0, s,
                            a);
     else
-        hipLaunchKernelGGL((attn_decode_pv_kernel<KV, G, 1, 96>), dim3(256 / 8, a.nkv, (unsigned)B), dim3(256), 0, s,
-                           a);
+        hipLaunchKernelGGL((attn_decode_pv_kernel<KV, 1, 1, 96>), dim3(256 / 8, a.nq, (unsigned)B), dim3(256), 0, s, a);
 }
 
 hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
