@@ -262,6 +262,13 @@ int zg_decode_step(zg_session* s, size_t rows, const uint32_t* tokens, float* lo
 /* n tokens per row (tokens[row*n + t]), logits of the last only
  * (QwenDenseCpu::prefill_transaction, lib.rs:1119-1187). */
 int zg_prefill(zg_session* s, size_t rows, size_t n, const uint32_t* tokens, float* logits);
+/* n tokens of one row at once (QwenDenseCpu::prefill_transaction,
+ * lib.rs:1119-1187, computed layer by layer over the whole prompt: batched
+ * MFMA projections, the chunked GDN prefill (gdn/chunk.rs), causal attention
+ * appending to the KV cache).  Logits of the last token to host when
+ * non-NULL.  Same functions as zg_prefill in another order of summation;
+ * needs Q4_K projections (ZG_E_UNSUPPORTED otherwise). */
+int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* tokens, float* logits);
 /* Device-side step: d_tokens/d_logits/d_greedy are device pointers, no host
  * synchronisation (zg_session_check reads the device status word). */
 int zg_decode_step_device(zg_session* s, size_t rows, const uint32_t* d_tokens, float* d_logits, uint32_t* d_greedy,

@@ -55,6 +55,7 @@ _SIGS = {
     "zg_session_position": (C.c_int, [P, SZ]),
     "zg_decode_step": (C.c_int, [P, SZ, P, P, P]),
     "zg_prefill": (C.c_int, [P, SZ, SZ, P, P]),
+    "zg_prefill_batched": (C.c_int, [P, SZ, SZ, P, P]),
     "zg_decode_step_device": (C.c_int, [P, SZ, P, P, P, P]),
     "zg_session_check": (C.c_int, [P, P]),
     "zg_state_floats": (SZ, [P, SZ]),
@@ -137,4 +138,6 @@ class Context:
             self.h = None
 
     def __del__(self):
-        self.close()
+        import sys
+        if not sys.is_finalizing():  # at interpreter exit the process releases the device itself
+            self.close()

@@ -689,7 +689,7 @@ static void launch_act16(const FusedGemvArgs& a, int mpad, _Float16* xh, hipStre
 }
 
 hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* scratch, hipStream_t s) {
-    if (w.type != kQ4_K || w.K % 256 || w.K > 8192 || args.M <= 0 || args.M > 64) return hipErrorInvalidValue;
+    if (w.type != kQ4_K || w.K % 256 || w.K > 8192 || args.M <= 0 || args.M > 65535 * 32) return hipErrorInvalidValue;
     if (args.pro == PRO_GATED && args.group != 128) return hipErrorInvalidValue;
     if (!w.qs_t || !w.hdr_t) return hipErrorNotReady;  // ensure_mfma_tiles first
     FusedGemvArgs a = args;

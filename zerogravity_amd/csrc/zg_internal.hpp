@@ -229,6 +229,27 @@ hipError_t gdn_chunk_prefill(const float* q, const float* k, const float* v, con
                              size_t T, size_t H, float* state, float* out, float* scratch, bool key_major,
                              bool round_bf16, hipStream_t s);
 
+// Batched prefill of one sequence (zg_prefill_model.hip).
+// gdn_prefill_conv: conv inputs P[t][0:3W] (row stride ldp, then z, alpha,
+// beta as in the decode projection) -> SiLU(conv) split into q, k, v [n][W],
+// gates beta / log decay [n][H]; the row's ring [3W][4] then holds the last
+// four prompt tokens.
+hipError_t gdn_prefill_conv(const float* P, size_t ldp, size_t n, size_t W, size_t H, const float* conv_w,
+                            float* ring, int pos0, const float* dt, const float* ssm_a, float* q, float* k, float* v,
+                            float* beta, float* logd, hipStream_t s);
+struct AttnPrefillArgs {
+    const float* P = nullptr;  // [n][ldp]: q|gate per head, k, v (the decode projection layout)
+    size_t ldp = 0, n = 0;
+    int nq = 0, nkv = 0, pos0 = 0, kv_bf16 = 0;
+    const float *qnorm = nullptr, *knorm = nullptr;
+    float eps = 0.0f, theta_scale = 0.0f, scale = 0.0f;
+    void *kcache = nullptr, *vcache = nullptr;  // this row's [max_ctx][nkv*256]
+    float* Q = nullptr;                         // scratch [n][nq][256]
+    float* out = nullptr;                       // [n][nq*256], gated
+};
+// q/k norm + RoPE + KV append for the n tokens, then causal attention.
+hipError_t attn_prefill(const AttnPrefillArgs& a, hipStream_t s);
+
 // Greedy ids of B logit rows (leading dimension ld) through partials
 // [argmax_partials(B)]; when `advance`, pos/ntok move on (tickets unused).
 size_t argmax_partials(size_t B);

@@ -1,0 +1,265 @@
+// Batched prefill of one sequence: the per-token kernels of the decode step
+// restated over n prompt tokens at once (the GDN layers through the chunked
+// prefill of zg_prefill.hip, the projections through the batched MFMA
+// GEMMs).  Reference semantics: QwenDenseCpu::prefill_transaction
+// (model-qwen35/src/lib.rs:1119-1187) runs forward_token (forward.rs:451-516)
+// once per token; this path computes the same functions of the prompt, in
+// another order of summation (chunked GDN, blocked softmax), so it is held
+// to the end-to-end tolerance, not to the bits.
+#include <algorithm>
+
+#include "zg_device.hpp"
+#include "zg_internal.hpp"
+#include "zg_pointwise.hpp"
+
+namespace zg {
+
+namespace {
+
+template <typename KV>
+__device__ __forceinline__ void kv_load4(const KV* p, float (&o)[4]) {
+    if constexpr (sizeof(KV) == 2) {
+        const uint2 v = *(const uint2*)p;
+        o[0] = __uint_as_float(v.x << 16);
+        o[1] = __uint_as_float(v.x & 0xffff0000u);
+        o[2] = __uint_as_float(v.y << 16);
+        o[3] = __uint_as_float(v.y & 0xffff0000u);
+    } else {
+        const v4f v = *(const v4f*)p;
+        o[0] = v.x;
+        o[1] = v.y;
+        o[2] = v.z;
+        o[3] = v.w;
+    }
+}
+
+__device__ __forceinline__ float prefill_rms_inv(double total, int n, float eps) {
+    const float mean = (float)(total / (double)n);
+    return 1.0f / sqrtf(mean + eps);
+}
+
+}  // namespace
+
+// Grid ((3W + 255) / 256, n), 256 threads.  Token t, channel ch of the conv
+// input rows P[t][0:3W]: the causal 4-tap conv of cpu/src/ops/gdn.rs:7-44
+// (taps older than the prompt come from the row's ring: the token at
+// position p sits in slot p % 4), SiLU (forward.rs:548), split into q, k, v
+// [n][W].  Workgroups x = 0 also form the gates of lib.rs:339-362: beta =
+// sigmoid(beta projection) and the log decay softplus(alpha + dt) * a.
+__global__ __launch_bounds__(256) void gdn_prefill_conv_kernel(const float* __restrict__ P, size_t ldp, int n, int W,
+                                                               int H, const float* __restrict__ conv_w,
+                                                               const float* __restrict__ ring, int pos0,
+                                                               const float* __restrict__ dt,
+                                                               const float* __restrict__ ssm_a, float* __restrict__ q,
+                                                               float* __restrict__ k, float* __restrict__ v,
+                                                               float* __restrict__ beta, float* __restrict__ logd) {
+    const int t = blockIdx.y, ch = blockIdx.x * 256 + threadIdx.x;
+    const float* row = P + (size_t)t * ldp;
+    if (ch < 3 * W) {
+        float tap[3];
+#pragma unroll
+        for (int j = 1; j <= 3; ++j)
+            tap[3 - j] = t - j >= 0 ? P[(size_t)(t - j) * ldp + ch] : ring[(size_t)ch * 4 + ((pos0 + t - j) & 3)];
+        const v4f w = *(const v4f*)(conv_w + (size_t)ch * 4);
+        const float t0 = tap[0] * w.x;
+        const float t1 = tap[1] * w.y;
+        const float t2 = tap[2] * w.z;
+        const float t3 = row[ch] * w.w;
+        float acc = t0 + t1;
+        acc = acc + t2;
+        acc = acc + t3;
+        const float o = ggml_silu(acc);
+        if (ch < W) q[(size_t)t * W + ch] = o;
+        else if (ch < 2 * W) k[(size_t)t * W + ch - W] = o;
+        else v[(size_t)t * W + ch - 2 * W] = o;
+    }
+    if (blockIdx.x == 0 && (int)threadIdx.x < H) {
+        const int h = threadIdx.x;
+        float gain, bt, sp, gr;
+        gdn_coef(row[4 * W + h], row[4 * W + H + h], dt[h], ssm_a[h], gain, bt, sp, gr);
+        beta[(size_t)t * H + h] = bt;
+        logd[(size_t)t * H + h] = gr;
+    }
+}
+
+// Grid ((3W + 255) / 256), 256 threads: the conv inputs of the last four
+// prompt tokens into the row's ring (after every conv of the prompt read it).
+__global__ __launch_bounds__(256) void gdn_prefill_ring_kernel(const float* __restrict__ P, size_t ldp, int n, int W,
+                                                               float* __restrict__ ring, int pos0) {
+    const int ch = blockIdx.x * 256 + threadIdx.x;
+    if (ch >= 3 * W) return;
+    for (int t = max(0, n - 4); t < n; ++t) ring[(size_t)ch * 4 + ((pos0 + t) & 3)] = P[(size_t)t * ldp + ch];
+}
+
+// Grid (n, nq + nkv), 256 threads: head `task` of token t (forward.rs:680-
+// 695 grouped RMS with q_norm / k_norm; source_rope_kv lib.rs:1552-1577 on
+// the first 64 dimensions at position pos0 + t).  q heads go to Q [n][nq][256];
+// the key (rounded to the cache type) and the value are appended to the cache.
+template <typename KV>
+__global__ __launch_bounds__(256) void attn_prefill_prep_kernel(const float* __restrict__ P, size_t ldp, int nq,
+                                                                int nkv, const float* __restrict__ qnorm,
+                                                                const float* __restrict__ knorm, float eps,
+                                                                float theta_scale, int pos0, KV* __restrict__ kc,
+                                                                KV* __restrict__ vc, float* __restrict__ Q) {
+    constexpr int D = 256;
+    __shared__ double red[4];
+    __shared__ float hv[D];
+    __shared__ float rs[32], rc[32];
+    const int t = blockIdx.x, task = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int p = pos0 + t;
+    const float* row = P + (size_t)t * ldp;
+    const bool isq = task < nq;
+    const float x = isq ? row[(size_t)task * 2 * D + tid] : row[(size_t)nq * 2 * D + (size_t)(task - nq) * D + tid];
+    const float gm = isq ? qnorm[tid] : knorm[tid];
+    if (tid < 32) {
+        float angle = (float)p;
+        for (int i = 0; i < tid; ++i) angle *= theta_scale;
+        rs[tid] = cr_sinf(angle);
+        rc[tid] = cr_cosf(angle);
+    }
+    const float sq = x * x;
+    double s = wave_sum_xor<double>((double)sq, 64);
+    if (lane == 0) red[tid >> 6] = s;
+    __syncthreads();
+    const float inv = prefill_rms_inv((red[0] + red[1]) + (red[2] + red[3]), D, eps);
+    const float tv = x * inv;
+    hv[tid] = tv * gm;
+    __syncthreads();
+    float y = hv[tid];
+    if (tid < 32) {
+        const float a = hv[tid], b = hv[tid + 32];
+        y = fmaf(a, rc[tid], -(b * rs[tid]));
+    } else if (tid < 64) {
+        const float a = hv[tid - 32], b = hv[tid];
+        y = fmaf(a, rs[tid - 32], b * rc[tid - 32]);
+    }
+    if (isq) {
+        Q[((size_t)t * nq + task) * D + tid] = y;
+    } else {
+        const int kh = task - nq;
+        const size_t at = ((size_t)p * nkv + kh) * D + tid;
+        if constexpr (sizeof(KV) == 2) {
+            uint32_t b = __float_as_uint(y);
+            b += 0x7fffu + ((b >> 16) & 1u);
+            kc[at] = (KV)(b >> 16);
+            uint32_t c = __float_as_uint(row[(size_t)nq * 2 * D + (size_t)nkv * D + (size_t)kh * D + tid]);
+            c += 0x7fffu + ((c >> 16) & 1u);
+            vc[at] = (KV)(c >> 16);
+        } else {
+            kc[at] = y;
+            vc[at] = row[(size_t)nq * 2 * D + (size_t)nkv * D + (size_t)kh * D + tid];
+        }
+    }
+}
+
+// Grid (n, nkv), 64 * G threads: wave g is query head kvh*G + g of token t
+// over the keys 0 .. pos0 + t (causal).  Lane l holds dimensions 4l..4l+3;
+// keys and values stream in blocks of 16 with an online softmax (block max,
+// rescale), then o / l * sigmoid(gate) (forward.rs:751).
+template <typename KV, int G>
+__global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __restrict__ Q, const KV* __restrict__ kc,
+                                                              const KV* __restrict__ vc, int nq, int nkv, int pos0,
+                                                              float scale, const float* __restrict__ P, size_t ldp,
+                                                              float* __restrict__ out) {
+    constexpr int D = 256, KB = 16;
+    const int t = blockIdx.x, kvh = blockIdx.y, g = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int h = kvh * G + g;
+    const int T = pos0 + t + 1;
+    const v4f qv = *(const v4f*)(Q + ((size_t)t * nq + h) * D + 4 * lane);
+    const size_t kstep = (size_t)nkv * D;
+    const KV* kb = kc + (size_t)kvh * D + 4 * lane;
+    const KV* vb = vc + (size_t)kvh * D + 4 * lane;
+    float m = -INFINITY, l = 0.0f;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j0 = 0; j0 < T; j0 += KB) {
+        float kk[KB][4], vv[KB][4];
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            const int jj = min(j0 + j, T - 1);
+            kv_load4(kb + (size_t)jj * kstep, kk[j]);
+            kv_load4(vb + (size_t)jj * kstep, vv[j]);
+        }
+        float sc[KB];
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            float d = qv.x * kk[j][0];
+            d = fmaf(qv.y, kk[j][1], d);
+            d = fmaf(qv.z, kk[j][2], d);
+            d = fmaf(qv.w, kk[j][3], d);
+            sc[j] = d;
+        }
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            const float tot = group_sum_last<64>(sc[j]);
+            sc[j] = __shfl(tot, 63, 64) * scale;
+            if (j0 + j >= T) sc[j] = -INFINITY;
+        }
+        float bm = m;
+#pragma unroll
+        for (int j = 0; j < KB; ++j) bm = fmaxf(bm, sc[j]);
+        const float corr = __expf(m - bm);
+        l *= corr;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] *= corr;
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            const float pj = __expf(sc[j] - bm);
+            l += pj;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(pj, vv[j][e], acc[e]);
+        }
+        m = bm;
+    }
+    const float inv = 1.0f / l;
+    const float* gate = P + (size_t)t * ldp + (size_t)h * 2 * D + D + 4 * lane;
+    v4f o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = acc[e] * inv * source_sigmoid(gate[e]);
+    *(v4f*)(out + ((size_t)t * nq + h) * D + 4 * lane) = o;
+}
+
+hipError_t gdn_prefill_conv(const float* P, size_t ldp, size_t n, size_t W, size_t H, const float* conv_w,
+                            float* ring, int pos0, const float* dt, const float* ssm_a, float* q, float* k, float* v,
+                            float* beta, float* logd, hipStream_t s) {
+    if (n == 0 || W == 0 || H == 0 || H > 256) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gdn_prefill_conv_kernel, dim3((unsigned)((3 * W + 255) / 256), (unsigned)n), dim3(256), 0, s, P,
+                       ldp, (int)n, (int)W, (int)H, conv_w, (const float*)ring, pos0, dt, ssm_a, q, k, v, beta, logd);
+    hipLaunchKernelGGL(gdn_prefill_ring_kernel, dim3((unsigned)((3 * W + 255) / 256)), dim3(256), 0, s, P, ldp,
+                       (int)n, (int)W, ring, pos0);
+    return hipGetLastError();
+}
+
+hipError_t attn_prefill(const AttnPrefillArgs& a, hipStream_t s) {
+    const int G = a.nq / a.nkv;
+    if (a.n == 0 || a.nkv <= 0 || a.nq % a.nkv || G < 1 || G > 4) return hipErrorInvalidValue;
+    if (a.kv_bf16) {
+        hipLaunchKernelGGL(attn_prefill_prep_kernel<uint16_t>, dim3((unsigned)a.n, (unsigned)(a.nq + a.nkv)),
+                           dim3(256), 0, s, a.P, a.ldp, a.nq, a.nkv, a.qnorm, a.knorm, a.eps, a.theta_scale, a.pos0,
+                           (uint16_t*)a.kcache, (uint16_t*)a.vcache, a.Q);
+    } else {
+        hipLaunchKernelGGL(attn_prefill_prep_kernel<float>, dim3((unsigned)a.n, (unsigned)(a.nq + a.nkv)), dim3(256),
+                           0, s, a.P, a.ldp, a.nq, a.nkv, a.qnorm, a.knorm, a.eps, a.theta_scale, a.pos0,
+                           (float*)a.kcache, (float*)a.vcache, a.Q);
+    }
+    const dim3 grid((unsigned)a.n, (unsigned)a.nkv);
+#define ZG_AP(KV, GG)                                                                                              \
+    hipLaunchKernelGGL((attn_prefill_kernel<KV, GG>), grid, dim3(64 * GG), 0, s, a.Q, (const KV*)a.kcache,        \
+                       (const KV*)a.vcache, a.nq, a.nkv, a.pos0, a.scale, a.P, a.ldp, a.out)
+#define ZG_APG(KV)                  \
+    switch (G) {                    \
+    case 1: ZG_AP(KV, 1); break;    \
+    case 2: ZG_AP(KV, 2); break;    \
+    case 3: ZG_AP(KV, 3); break;    \
+    default: ZG_AP(KV, 4); break;   \
+    }
+    if (a.kv_bf16) {
+        ZG_APG(uint16_t)
+    } else {
+        ZG_APG(float)
+    }
+#undef ZG_APG
+#undef ZG_AP
+    return hipGetLastError();
+}
+
+}  // namespace zg

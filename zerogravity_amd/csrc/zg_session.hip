@@ -69,6 +69,9 @@ struct zg_session {
     std::vector<void*> kc, vc;      // per attention layer: [B][max_ctx][kv_heads*256]
     std::vector<int> layer_slot;    // layer -> index into ring/rec or kc/vc
     std::map<std::tuple<size_t, const void*, const void*, const void*>, hipGraphExec_t> graphs;
+    // batched prefill buffers, sized for pf_cap prompt tokens
+    size_t pf_cap = 0;
+    std::vector<void*> pf;
 };
 
 namespace {
@@ -135,7 +138,11 @@ int load_vector(zg_model* m, const zg_tensor_desc* ts, size_t n, const std::stri
 int dalloc(zg_session* s, void** p, size_t bytes) {
     zg_ctx* ctx = s->m->ctx;
     ZG_HIP(hipMalloc(p, bytes < 256 ? 256 : bytes));
-    ZG_HIP(hipMemset(*p, 0, bytes < 256 ? 256 : bytes));
+    // on the context's stream, finished before return: the stream is
+    // non-blocking, so a null-stream hipMemset could still be clearing the
+    // buffer when kernels on it start
+    ZG_HIP(hipMemsetAsync(*p, 0, bytes < 256 ? 256 : bytes, ctx->stream));
+    ZG_HIP(hipStreamSynchronize(ctx->stream));
     s->allocs.push_back(*p);
     return ZG_COMPLETED;
 }
@@ -525,6 +532,7 @@ void zg_session_destroy(zg_session* s) {
     (void)hipDeviceSynchronize();
     for (auto& kv : s->graphs) (void)hipGraphExecDestroy(kv.second);
     for (void* p : s->allocs) (void)hipFree(p);
+    for (void* p : s->pf) (void)hipFree(p);
     delete s;
 }
 
@@ -592,6 +600,162 @@ int zg_prefill(zg_session* s, size_t rows, size_t n, const uint32_t* tokens, flo
         int rc = zg_decode_step(s, rows, col.data(), t + 1 == n ? logits : nullptr, nullptr);
         if (rc) return rc;
     }
+    return ZG_COMPLETED;
+}
+
+// Batched prefill of one row: embed the n tokens, run every layer over all of
+// them (batched MFMA projections, chunked GDN prefill, causal attention with
+// the KV append), and the LM head on the last.  Same result as n decode
+// steps of that row up to the order of summation (end-to-end tolerance).
+int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* tokens, float* logits) {
+    if (!s || !tokens || n == 0) return ZG_E_MALFORMED;
+    zg_model* m = s->m;
+    zg_ctx* ctx = m->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (s->poisoned) return fail(ctx, ZG_E_STATE, "session poisoned by a failed step: reset or import state");
+    if (row >= s->max_batch) return fail(ctx, ZG_E_LIMIT, "row outside the session batch");
+    const zg_geometry& g = m->g;
+    if ((size_t)s->pos[row] + n > s->max_ctx) return fail(ctx, ZG_E_LIMIT, "prompt exceeds the session context");
+    for (size_t i = 0; i < n; ++i)
+        if (tokens[i] >= g.vocab) return fail(ctx, ZG_E_MALFORMED, "prompt contains an out-of-vocabulary token id");
+    // the chunked GDN prefill is built for 128-wide heads with the model's
+    // 1e-6 norm epsilon; the attention kernels for 256-wide heads, <= 4
+    // query heads per KV head
+    if (g.gdn_dim != 128 || g.head_dim != 256 || g.eps != 1e-6f || g.kv_heads == 0 || g.q_heads % g.kv_heads ||
+        g.q_heads / g.kv_heads > 4)
+        return fail(ctx, ZG_E_UNSUPPORTED, "batched prefill geometry not supported: use zg_prefill");
+    std::vector<zg_weight*> ws;
+    for (auto& L : m->layers) ws.insert(ws.end(), {L.in_proj, L.out_proj, L.ffn_gu, L.ffn_down});
+    for (zg_weight* w : ws)
+        if (!w || w->dw.type != zg::kQ4_K)
+            return fail(ctx, ZG_E_UNSUPPORTED, "batched prefill needs Q4_K projections: use zg_prefill");
+    hipStream_t st = ctx->stream;
+    for (zg_weight* w : ws)
+        if (!w->dw.qs_t) ZG_HIP(zg::ensure_mfma_tiles(w->dw, st));
+    const size_t H = g.hidden, F = g.ffn, W = (size_t)g.gdn_heads * g.gdn_dim, GH = g.gdn_heads;
+    const size_t QD = (size_t)g.q_heads * g.head_dim;
+    const size_t mpad = (n + 31) / 32 * 32;
+    const size_t ldp = s->y0w;
+    enum { X, P, Q, K, V, BETA, LOGD, CORE, QB, OB, XH, XH2, CHUNK, TOK, NBUF };
+    if (n > s->pf_cap) {
+        ZG_HIP(hipStreamSynchronize(st));
+        for (void* p : s->pf) (void)hipFree(p);
+        s->pf.assign(NBUF, nullptr);
+        s->pf_cap = 0;
+        const size_t bytes[NBUF] = {mpad * H * 4, mpad * ldp * 4, n * W * 4, n * W * 4, n * W * 4, n * GH * 4,
+                                    n * GH * 4, mpad * W * 4, n * QD * 4, mpad * QD * 4,
+                                    zg::batched_scratch_bytes(n, std::max({H, F, W, QD})),
+                                    zg::batched_scratch_bytes(n, F), zg::gdn_chunk_scratch_bytes(n, GH), n * 4};
+        for (int i = 0; i < NBUF; ++i) {
+            ZG_HIP(hipMalloc(&s->pf[i], std::max<size_t>(bytes[i], 256)));
+            ZG_HIP(hipMemsetAsync(s->pf[i], 0, std::max<size_t>(bytes[i], 256), st));  // stream-ordered
+        }
+        s->pf_cap = n;
+    }
+    float* x = (float*)s->pf[X];
+    float* pj = (float*)s->pf[P];
+    uint32_t* dtok = (uint32_t*)s->pf[TOK];
+    const int pos0 = s->pos[row];
+    ZG_HIP(hipMemcpyAsync(dtok, tokens, n * 4, hipMemcpyHostToDevice, st));
+    ZG_HIP(hipStreamSynchronize(st));
+    ZG_HIP(zg::embed(m->embd->dw, dtok, x, n, s->d_status, st));
+    auto gemm = [&](zg_weight* w, int pro, const float* xin, size_t ldx, const float* x2, size_t ldx2,
+                    const float* gamma, int epi, float* y, size_t ldy, void* xh_out = nullptr,
+                    const void* xh_in = nullptr) {
+        zg::FusedGemvArgs f;
+        f.M = (int)n;
+        f.pro = pro;
+        f.epi = epi;
+        f.x = xin;
+        f.ldx = ldx;
+        f.x2 = x2;
+        f.ldx2 = ldx2;
+        f.gamma = gamma;
+        f.eps = g.eps;
+        f.group = (int)g.gdn_dim;
+        f.y = y;
+        f.ldy = ldy;
+        f.status = s->d_status;
+        f.xh_out = xh_out;
+        f.xh_in = xh_in;
+        return zg::batched_gemv(w->dw, f, s->pf[XH], st);
+    };
+    for (size_t i = 0; i < m->layers.size(); ++i) {
+        LayerW& L = m->layers[i];
+        const int slot = s->layer_slot[i];
+        if (!L.full) {
+            ZG_HIP(gemm(L.in_proj, zg::PRO_RMS, x, H, nullptr, 0, L.attn_norm, zg::EPI_STORE, pj, ldp));
+            float* ring = s->ring[slot] + row * 3 * W * 4;
+            float* state = s->rec[slot] + row * GH * g.gdn_dim * g.gdn_dim;
+            ZG_HIP(zg::gdn_prefill_conv(pj, ldp, n, W, GH, L.conv_w, ring, pos0, L.ssm_dt, L.ssm_a, (float*)s->pf[Q],
+                                        (float*)s->pf[K], (float*)s->pf[V], (float*)s->pf[BETA],
+                                        (float*)s->pf[LOGD], st));
+            ZG_HIP(zg::gdn_chunk_prefill((const float*)s->pf[Q], (const float*)s->pf[K], (const float*)s->pf[V],
+                                         (const float*)s->pf[BETA], (const float*)s->pf[LOGD], n, GH, state,
+                                         (float*)s->pf[CORE], (float*)s->pf[CHUNK], false, false, st));
+            ZG_HIP(gemm(L.out_proj, zg::PRO_GATED, (const float*)s->pf[CORE], W, pj + 3 * W, ldp, L.ssm_norm,
+                        zg::EPI_RESID, x, H));
+        } else {
+            ZG_HIP(gemm(L.in_proj, zg::PRO_RMS, x, H, nullptr, 0, L.attn_norm, zg::EPI_STORE, pj, ldp));
+            zg::AttnPrefillArgs a;
+            a.P = pj;
+            a.ldp = ldp;
+            a.n = n;
+            a.nq = (int)g.q_heads;
+            a.nkv = (int)g.kv_heads;
+            a.pos0 = pos0;
+            a.kv_bf16 = s->kv_bf16;
+            a.qnorm = L.q_norm;
+            a.knorm = L.k_norm;
+            a.eps = g.eps;
+            a.theta_scale = powf(10000000.0f, -2.0f / 64.0f);
+            a.scale = 1.0f / sqrtf((float)g.head_dim);
+            const size_t esz = s->kv_bf16 ? 2 : 4;
+            a.kcache = (char*)s->kc[slot] + row * s->max_ctx * kvw(g) * esz;
+            a.vcache = (char*)s->vc[slot] + row * s->max_ctx * kvw(g) * esz;
+            a.Q = (float*)s->pf[QB];
+            a.out = (float*)s->pf[OB];
+            ZG_HIP(zg::attn_prefill(a, st));
+            ZG_HIP(gemm(L.out_proj, zg::PRO_PLAIN, (const float*)s->pf[OB], QD, nullptr, 0, nullptr, zg::EPI_RESID, x,
+                        H));
+        }
+        const zg::DeviceWeight& gu = L.ffn_gu->dw;
+        if (zg::batched_glu_supported(gu.type, gu.K, gu.N)) {
+            ZG_HIP(gemm(L.ffn_gu, zg::PRO_RMS, x, H, nullptr, 0, L.post_norm, zg::EPI_GLU, pj, ldp, s->pf[XH2]));
+            ZG_HIP(gemm(L.ffn_down, zg::PRO_PLAIN, pj, ldp, nullptr, 0, nullptr, zg::EPI_RESID, x, H, nullptr,
+                        s->pf[XH2]));
+        } else {
+            ZG_HIP(gemm(L.ffn_gu, zg::PRO_RMS, x, H, nullptr, 0, L.post_norm, zg::EPI_STORE, pj, ldp));
+            ZG_HIP(gemm(L.ffn_down, zg::PRO_SILU_MUL, pj, ldp, pj + F, ldp, nullptr, zg::EPI_RESID, x, H));
+        }
+    }
+    if (!logits) {
+        int rc = read_status(s, st);
+        if (rc) return rc;
+        s->pos[row] += (int)n;
+        s->pos_dirty = true;
+        return ZG_COMPLETED;
+    }
+    // LM head on the last prompt token (tied embedding, output norm)
+    zg::FusedGemvArgs f;
+    f.M = 1;
+    f.pro = zg::PRO_RMS;
+    f.epi = zg::EPI_STORE;
+    f.x = x + (n - 1) * H;
+    f.ldx = H;
+    f.gamma = m->out_norm;
+    f.eps = g.eps;
+    f.y = s->logits;
+    f.ldy = g.vocab;
+    f.status = s->d_status;
+    ZG_HIP(zg::fused_gemv(m->embd->dw, f, st));
+    int rc = read_status(s, st);
+    if (rc) return rc;
+    ZG_HIP(hipMemcpyAsync(logits, s->logits, g.vocab * 4, hipMemcpyDeviceToHost, st));
+    ZG_HIP(hipStreamSynchronize(st));
+    s->pos[row] += (int)n;
+    s->pos_dirty = true;
     return ZG_COMPLETED;
 }
 

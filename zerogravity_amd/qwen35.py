@@ -240,6 +240,17 @@ class QwenDenseHip:
         self.model.ctx.check(L.lib().zg_prefill(self.h, 1, toks.size, toks.ctypes.data, lg.ctypes.data))
         return lg
 
+    def prefill_batched(self, tokens, row=0, logits=True):
+        """The whole prompt of one row layer by layer (batched projections,
+        chunked GDN prefill, causal attention); logits of the last token."""
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        if toks.size == 0:
+            raise L.ZgError(L.E_MALFORMED, "prefill must contain at least one token")
+        lg = np.empty(self.vocab, np.float32) if logits else None
+        self.model.ctx.check(L.lib().zg_prefill_batched(self.h, row, toks.size, toks.ctypes.data,
+                                                          None if lg is None else lg.ctypes.data))
+        return lg
+
     def prefill_chunk_without_logits(self, tokens):
         toks = np.ascontiguousarray(tokens, np.uint32)
         self.model.ctx.check(L.lib().zg_prefill(self.h, 1, toks.size, toks.ctypes.data, None))
