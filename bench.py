@@ -411,6 +411,7 @@ def bench_gemv(args):
 # ----------------------------------------------------------------- prefill
 
 F32_MFMA_PEAK_TFLOPS = 157.3
+F16_MFMA_PEAK_TFLOPS = 2500.0  # dense f16 MFMA (no sparsity)
 PREFILL_C, PREFILL_D = 64, 128
 
 
@@ -513,6 +514,91 @@ def bench_prefill(args):
     return line
 
 
+def model_prefill_flops(g, L):
+    """Algorithmic flops of one batched prefill of L tokens: every projection
+    once per token (2 N K), the GDN chunk cores (prefill_flops_per_chunk_head
+    per 64-token chunk and head), causal attention (QK and PV over t + 1 keys
+    for token t, every query head) and the LM head of the last token."""
+    proj = sum(N * K for _, _, K, N in decode_matrices(g)[:-1])
+    n_attn = g["layers"] // g["full_attention_interval"]
+    n_gdn = g["layers"] - n_attn
+    chunks = (L + PREFILL_C - 1) // PREFILL_C
+    gdn = n_gdn * chunks * g["gdn_heads"] * prefill_flops_per_chunk_head()
+    attn = n_attn * g["q_heads"] * 2 * 2 * g["head_dim"] * (L * (L + 1) // 2)
+    return 2 * proj * L + gdn + attn + 2 * g["vocab"] * g["hidden"]
+
+
+def cpu_model_prefill_baseline(g, tensors, seconds):
+    """The oracle's per-token prefill (QwenDenseCpu::prefill_transaction,
+    OpenMP over GEMV rows on every host core) on a bounded prompt."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import zg_oracle as O
+    threads = host_threads()
+    model = O.Model(dict(g, max_context=1024), tensors, threads)
+    sess = model.session()
+    toks = np.random.default_rng(5).integers(0, g["vocab"], 1000)
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0 < seconds or n < 2) and n < len(toks):
+        sess.forward(int(toks[n]), need_logits=n == len(toks) - 1)
+        n += 1
+    dt = time.perf_counter() - t0
+    return n / dt, threads, f"{n} prompt tokens through the per-token prefill"
+
+
+def bench_model_prefill(args):
+    """Batched prefill of one prompt on the 2B-shaped Q4_K model
+    (zg_prefill_batched), L = 512, 2048 and 8192; each timed call starts from
+    a reset session (the reset is outside the timed region)."""
+    from zerogravity_amd import _lib as L
+    from zerogravity_amd import gguf, qwen35
+    from zerogravity_amd import regions as R
+    kern = R.HipMatVecKernel(0)
+    g = dict(qwen35.QWEN35_2B)
+    tensors = qwen35.synthetic_tensors(g, gguf.Q4_K, seed=2026)
+    model = qwen35.QwenModelHip(g, tensors, kernel=kern)
+    rng = np.random.default_rng(7)
+    steps = max(1, min(args.steps, 16))
+    results = []
+    for T in (512, 2048, 8192):
+        sess = model.session(max_batch=1, max_context=T, kv_dtype=L.BF16)
+        toks = rng.integers(0, g["vocab"], T).astype(np.uint32)
+        for _ in range(max(1, min(args.warmup, 2))):
+            sess.reset()
+            sess.prefill_batched(toks)
+        total = 0.0
+        for _ in range(steps):
+            sess.reset()
+            t0 = time.perf_counter()
+            sess.prefill_batched(toks)  # returns after the logits reach the host
+            total += time.perf_counter() - t0
+        sess.close()
+        ms = total / steps * 1e3
+        tflops = model_prefill_flops(g, T) / (ms * 1e-3) / 1e12
+        log(f"model prefill L={T}: {ms:8.2f} ms  {T / ms * 1e3:10.0f} tok/s  {tflops:7.1f} TFLOP/s "
+            f"({tflops / F16_MFMA_PEAK_TFLOPS:.1%} of f16 MFMA peak)")
+        results.append(dict(L=T, ms=round(ms, 3), tok_s=round(T / ms * 1e3, 1), tflops=round(tflops, 2)))
+    model.close()
+    head = results[1]
+    line = {
+        "metric": "batched prefill tok/s (2B-shaped Q4_K, 2048-token prompt, bf16 KV)",
+        "value": head["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": head["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_k weights, f16 MFMA, f32 accumulate",
+        "data": "synthetic (seeded random-init Q4_K GGUF weights, random prompt ids)",
+        "config": {"workload": "2B-shaped Q4_K batched prefill of one row", "sweep": results},
+        "roofline": {"bound": "mfma", "achieved": head["tflops"], "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(head["tflops"] / F16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "whole prefill (all kernels; algorithmic flops / wall time)"},
+    }
+    if not args.no_cpu:
+        v, cores, sample = cpu_model_prefill_baseline(g, tensors, args.cpu_seconds)
+        line["cpu_baseline"] = {"value": round(v, 2), "unit": "tok/s", "cores": cores, "kind": "port",
+                                "sample": sample}
+    kern.ctx.close()
+    return line
+
+
 def bench_gdn(args):
     import torch
     from zerogravity_amd import _lib as L
@@ -538,7 +624,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "prefill", "gdn"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "prefill", "gdn", "model_prefill"])
     ap.add_argument("--prefix", type=int, default=2048)
     ap.add_argument("--leg-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -548,7 +634,8 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU would run its own "
               "sessions; see the sharding notes in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
-    bench = {"decode": bench_decode, "gemv": bench_gemv, "prefill": bench_prefill, "gdn": bench_gdn}[args.workload]
+    bench = {"decode": bench_decode, "gemv": bench_gemv, "prefill": bench_prefill, "gdn": bench_gdn,
+             "model_prefill": bench_model_prefill}[args.workload]
     line = bench(args)
     print(json.dumps(line), flush=True)
 

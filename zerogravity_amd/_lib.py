@@ -138,6 +138,7 @@ class Context:
             self.h = None
 
     def __del__(self):
-        import sys
-        if not sys.is_finalizing():  # at interpreter exit the process releases the device itself
+        try:
             self.close()
+        except Exception:  # interpreter teardown: the library may be gone; the process releases the device
+            pass
