@@ -252,6 +252,17 @@ void zg_session_destroy(zg_session* s);
 /* All rows back to position 0 with zero state (QwenDenseCpu::reset). */
 int zg_session_reset(zg_session* s);
 int zg_session_position(const zg_session* s, size_t row);
+/* Continuous-batch row management over the session's contiguous per-row
+ * slots (the reference keeps private per-row state in cohorts,
+ * resident_inference.rs:1101-1111, and shares prompt prefixes through
+ * paged block tables, core/src/paged_state.rs:239-330).  reset_row retires
+ * one row (state and KV zeroed, position 0).  copy_row gives row dst a copy
+ * of row src's state, KV prefix and position: retiring row r of a batch of
+ * n active rows is copy_row(r, n-1) + reset_row(n-1), which keeps the active
+ * rows dense for zg_decode_step; copying a prefilled row forks its prompt.
+ * ZG_E_LIMIT for a row outside the batch. */
+int zg_session_reset_row(zg_session* s, size_t row);
+int zg_session_copy_row(zg_session* s, size_t dst, size_t src);
 
 /* One forward_token for rows [0, rows): tokens[rows] host ids, logits
  * [rows][vocab] and/or greedy [rows] (first maximum, numerics.rs:126-140)

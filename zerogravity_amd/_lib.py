@@ -56,6 +56,8 @@ _SIGS = {
     "zg_decode_step": (C.c_int, [P, SZ, P, P, P]),
     "zg_prefill": (C.c_int, [P, SZ, SZ, P, P]),
     "zg_prefill_batched": (C.c_int, [P, SZ, SZ, P, P]),
+    "zg_session_reset_row": (C.c_int, [P, SZ]),
+    "zg_session_copy_row": (C.c_int, [P, SZ, SZ]),
     "zg_decode_step_device": (C.c_int, [P, SZ, P, P, P, P]),
     "zg_session_check": (C.c_int, [P, P]),
     "zg_state_floats": (SZ, [P, SZ]),

@@ -559,6 +559,68 @@ int zg_session_reset(zg_session* s) {
     return ZG_COMPLETED;
 }
 
+// Row retirement: the row's conv history, GDN state and KV cache back to
+// zero and its position to 0; the other rows are untouched.
+int zg_session_reset_row(zg_session* s, size_t row) {
+    if (!s) return ZG_E_MALFORMED;
+    zg_ctx* ctx = s->m->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (row >= s->max_batch) return fail(ctx, ZG_E_LIMIT, "row outside the session batch");
+    const zg_geometry& g = s->m->g;
+    hipStream_t st = ctx->stream;
+    ZG_HIP(hipDeviceSynchronize());  // work queued on a caller's stream (device entry points) lands first
+    for (float* c : s->ring) ZG_HIP(hipMemsetAsync(c + row * ring_floats(g), 0, ring_floats(g) * 4, st));
+    for (float* r : s->rec) ZG_HIP(hipMemsetAsync(r + row * rec_floats(g), 0, rec_floats(g) * 4, st));
+    const size_t rowb = s->max_ctx * kvw(g) * (s->kv_bf16 ? 2 : 4);
+    for (size_t i = 0; i < s->kc.size(); ++i) {
+        ZG_HIP(hipMemsetAsync((char*)s->kc[i] + row * rowb, 0, rowb, st));
+        ZG_HIP(hipMemsetAsync((char*)s->vc[i] + row * rowb, 0, rowb, st));
+    }
+    ZG_HIP(hipStreamSynchronize(st));
+    s->pos[row] = 0;
+    s->pos_dirty = true;
+    return ZG_COMPLETED;
+}
+
+// Row admission by copy: row dst takes row src's whole state (conv history,
+// GDN state, the KV cache up to src's position) and position.  With
+// zg_session_reset_row this keeps the active rows of a continuous batch
+// dense (retire row r: copy the last active row into r, reset the last),
+// and it forks a prefilled prompt into several rows.
+int zg_session_copy_row(zg_session* s, size_t dst, size_t src) {
+    if (!s) return ZG_E_MALFORMED;
+    zg_ctx* ctx = s->m->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (dst >= s->max_batch || src >= s->max_batch) return fail(ctx, ZG_E_LIMIT, "row outside the session batch");
+    if (dst == src) return ZG_COMPLETED;
+    const zg_geometry& g = s->m->g;
+    hipStream_t st = ctx->stream;
+    ZG_HIP(hipDeviceSynchronize());
+    for (float* c : s->ring)
+        ZG_HIP(hipMemcpyAsync(c + dst * ring_floats(g), c + src * ring_floats(g), ring_floats(g) * 4,
+                              hipMemcpyDeviceToDevice, st));
+    for (float* r : s->rec)
+        ZG_HIP(hipMemcpyAsync(r + dst * rec_floats(g), r + src * rec_floats(g), rec_floats(g) * 4,
+                              hipMemcpyDeviceToDevice, st));
+    const size_t esz = s->kv_bf16 ? 2 : 4;
+    const size_t rowb = s->max_ctx * kvw(g) * esz;
+    const size_t used = (size_t)s->pos[src] * kvw(g) * esz;
+    const size_t stale = (size_t)s->pos[dst] * kvw(g) * esz;
+    for (size_t i = 0; i < s->kc.size(); ++i) {
+        for (void* cache : {s->kc[i], s->vc[i]}) {
+            char* base = (char*)cache;
+            if (used) ZG_HIP(hipMemcpyAsync(base + dst * rowb, base + src * rowb, used, hipMemcpyDeviceToDevice, st));
+            if (stale > used) ZG_HIP(hipMemsetAsync(base + dst * rowb + used, 0, stale - used, st));
+        }
+    }
+    ZG_HIP(hipStreamSynchronize(st));
+    s->pos[dst] = s->pos[src];
+    s->pos_dirty = true;
+    return ZG_COMPLETED;
+}
+
 int zg_session_position(const zg_session* s, size_t row) {
     if (!s || row >= s->max_batch) return -1;
     return s->pos[row];

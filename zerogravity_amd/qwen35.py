@@ -258,6 +258,26 @@ class QwenDenseHip:
     def reset(self):
         self.model.ctx.check(L.lib().zg_session_reset(self.h))
 
+    def reset_row(self, row):
+        """Retire one row: its state and KV cache zeroed, position 0."""
+        self.model.ctx.check(L.lib().zg_session_reset_row(self.h, row))
+
+    def copy_row(self, dst, src):
+        """Row dst takes a copy of row src's state, KV prefix and position."""
+        self.model.ctx.check(L.lib().zg_session_copy_row(self.h, dst, src))
+
+    def retire(self, row, active):
+        """Retire `row` of a batch whose active rows are [0, active): the last
+        active row moves into its slot, so [0, active - 1) stays dense.
+        Returns the new active count."""
+        if not 0 <= row < active <= self.rows:
+            raise L.ZgError(L.E_LIMIT, "row outside the active batch")
+        last = active - 1
+        if row != last:
+            self.copy_row(row, last)
+        self.reset_row(last)
+        return last
+
     def state(self, row=0):
         n = L.lib().zg_state_floats(self.h, row)
         out = np.empty(n, np.float32)
