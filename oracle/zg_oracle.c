@@ -236,6 +236,155 @@ float zgo_dot_q8_0_row(const uint8_t* row, const int8_t* qs, const float* d, siz
     return (r0 + r2) + (r1 + r3);
 }
 
+/* quantization.rs:66-92 (GgmlQ8K, Q6_K/Q4_K pairing): per 256-block the
+ * FIRST element of largest magnitude (strict > while scanning in order)
+ * gives the signed max; inv = -127/max_signed, d = 1/inv (0 for an all-zero
+ * block), q = clamp(round_ties_even(x*inv)).  bsums (sums of 16 codes, used
+ * by the Q6_K offset correction) are optional. */
+int zgo_q8k_activation(const float* x, size_t n, int8_t* qs, float* d, int32_t* bsums) {
+    if (!finite_all(x, n)) return ZGO_E_MALFORMED;
+    if (n % 256 != 0) return ZGO_E_MALFORMED;
+    for (size_t b = 0; b < n / 256; ++b) {
+        const float* blk = x + b * 256;
+        float max_signed = 0.0f, amax = 0.0f;
+        for (int i = 0; i < 256; ++i)
+            if (fabsf(blk[i]) > amax) {
+                amax = fabsf(blk[i]);
+                max_signed = blk[i];
+            }
+        float inv = amax == 0.0f ? 0.0f : -127.0f / max_signed;
+        d[b] = amax == 0.0f ? 0.0f : 1.0f / inv;
+        for (int i = 0; i < 256; ++i) {
+            float r = rintf(blk[i] * inv);
+            if (r < -128.0f) r = -128.0f;
+            if (r > 127.0f) r = 127.0f;
+            qs[b * 256 + i] = (int8_t)r;
+        }
+        if (bsums)
+            for (int g = 0; g < 16; ++g) {
+                int32_t t = 0;
+                for (int i = 0; i < 16; ++i) t += qs[b * 256 + g * 16 + i];
+                bsums[b * 16 + g] = t;
+            }
+    }
+    return ZGO_OK;
+}
+
+/* quantization.rs:133-170 (Q4_0 x Q8_0, rows not a multiple of 8): eight f32
+ * lanes, lane l takes elements 4l..4l+3 of each block (weights below 16 are
+ * low nibbles of bytes i, the rest high nibbles of bytes i-16, minus 8),
+ * lane = fma(d_w*d_a, int dot, lane); the same final tree as Q8_0. */
+float zgo_dot_q4_0_row(const uint8_t* row, const int8_t* qs, const float* d, size_t nblocks) {
+    float lanes[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (size_t b = 0; b < nblocks; ++b) {
+        const uint8_t* w = row + b * 18;
+        float dd = zgo_f16_to_f32(rd16(w)) * d[b];
+        const uint8_t* packed = w + 2;
+        for (int lane = 0; lane < 8; ++lane) {
+            int32_t dot = 0;
+            for (int j = lane * 4; j < lane * 4 + 4; ++j) {
+                int32_t q = j < 16 ? (int32_t)(packed[j] & 15) - 8 : (int32_t)(packed[j - 16] >> 4) - 8;
+                dot += q * (int32_t)qs[b * 32 + j];
+            }
+            lanes[lane] = fmaf(dd, (float)dot, lanes[lane]);
+        }
+    }
+    float r0 = lanes[0] + lanes[4], r1 = lanes[1] + lanes[5];
+    float r2 = lanes[2] + lanes[6], r3 = lanes[3] + lanes[7];
+    return (r0 + r2) + (r1 + r3);
+}
+
+/* quantization.rs:105-124 (Q4_0 x Q8_0, rows a multiple of 8, the GGML
+ * 8x8-repacked schedule): one int32 sum per block, one fma per block. */
+float zgo_dot_q4_0_repacked_row(const uint8_t* row, const int8_t* qs, const float* d, size_t nblocks) {
+    float acc = 0.0f;
+    for (size_t b = 0; b < nblocks; ++b) {
+        const uint8_t* w = row + b * 18;
+        const uint8_t* packed = w + 2;
+        int32_t sum = 0;
+        for (int i = 0; i < 16; ++i) {
+            sum += ((int32_t)(packed[i] & 15) - 8) * (int32_t)qs[b * 32 + i];
+            sum += ((int32_t)(packed[i] >> 4) - 8) * (int32_t)qs[b * 32 + i + 16];
+        }
+        float scale = zgo_f16_to_f32(rd16(w)) * d[b];
+        acc = fmaf((float)sum, scale, acc);
+    }
+    return acc;
+}
+
+/* quantization.rs:198-227 (Q4_1 x Q8_1): eight f32 lanes as Q8_0 over the
+ * unsigned nibbles, scale = d_w * d_a; the zero points accumulate apart,
+ * summs = summs + m_w * s_a (product, then sum), added after the tree. */
+float zgo_dot_q4_1_row(const uint8_t* row, const int8_t* qs, const float* d, const float* s, size_t nblocks) {
+    float lanes[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float summs = 0.0f;
+    for (size_t b = 0; b < nblocks; ++b) {
+        const uint8_t* w = row + b * 20;
+        float d0 = zgo_f16_to_f32(rd16(w));
+        float m = zgo_f16_to_f32(rd16(w + 2));
+        float ms = m * s[b];
+        summs = summs + ms;
+        float scale = d0 * d[b];
+        const uint8_t* packed = w + 4;
+        for (int lane = 0; lane < 8; ++lane) {
+            int32_t partial = 0;
+            for (int i = lane * 4; i < lane * 4 + 4; ++i) {
+                int32_t q = i < 16 ? (int32_t)(packed[i] & 15) : (int32_t)(packed[i - 16] >> 4);
+                partial += q * (int32_t)qs[b * 32 + i];
+            }
+            lanes[lane] = fmaf((float)partial, scale, lanes[lane]);
+        }
+    }
+    float r0 = lanes[0] + lanes[4], r1 = lanes[1] + lanes[5];
+    float r2 = lanes[2] + lanes[6], r3 = lanes[3] + lanes[7];
+    return ((r0 + r2) + (r1 + r3)) + summs;
+}
+
+/* quantization.rs:228-285 (Q6_K x Q8_K): per 256-superblock eight int32
+ * lanes; element at = 128*half + 32*group + lane32 (code = 6-bit value
+ * before the -32 shift, local scale int8 scales[8*half + 2*group +
+ * lane32/16]) adds code*scale*q8 to lane (at % 32) / 4.  Lane L then
+ * subtracts 32 * sum over the contiguous 16-groups 2L, 2L+1 of
+ * (bsum * scales[group16]); lane = fma((float)int, d_a * d_w, lane); the
+ * Q8_0 final tree. */
+float zgo_dot_q6k_row(const uint8_t* row, const int8_t* qs, const float* d, const int32_t* bsums, size_t nblocks) {
+    float lanes[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (size_t b = 0; b < nblocks; ++b) {
+        const uint8_t* w = row + b * 210;
+        const int8_t* q8 = qs + b * 256;
+        float scale = d[b] * zgo_f16_to_f32(rd16(w + 208));
+        int32_t acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int half = 0; half < 2; ++half) {
+            const uint8_t* low = w + half * 64;
+            const uint8_t* high = w + 128 + half * 32;
+            const uint8_t* sc = w + 192 + half * 8;
+            for (int lane = 0; lane < 32; ++lane) {
+                uint8_t hi = high[lane];
+                for (int group = 0; group < 4; ++group) {
+                    uint8_t nib = group < 2 ? (low[lane + group * 32] & 15) : (low[lane + (group - 2) * 32] >> 4);
+                    int32_t code = (int32_t)(nib | (((hi >> (2 * group)) & 3) << 4));
+                    int32_t sub = (int32_t)(int8_t)sc[group * 2 + lane / 16];
+                    int at = half * 128 + group * 32 + lane;
+                    acc[(at % 32) / 4] += code * sub * (int32_t)q8[at];
+                }
+            }
+        }
+        const uint8_t* scales = w + 192;
+        for (int L = 0; L < 8; ++L) {
+            int32_t offset = 0;
+            for (int sub = 0; sub < 2; ++sub) {
+                int g16 = L * 2 + sub;
+                offset += bsums[b * 16 + g16] * (int32_t)(int8_t)scales[g16];
+            }
+            acc[L] -= 32 * offset;
+            lanes[L] = fmaf((float)acc[L], scale, lanes[L]);
+        }
+    }
+    float r0 = lanes[0] + lanes[4], r1 = lanes[1] + lanes[5];
+    float r2 = lanes[2] + lanes[6], r3 = lanes[3] + lanes[7];
+    return (r0 + r2) + (r1 + r3);
+}
+
 /* cpu/src/source.rs:431-459: serial f32, sum += (q*scale - min) * x, no FMA. */
 float zgo_dot_q4k_row(const uint8_t* row, const float* x, size_t nblocks) {
     float sum = 0.0f;
@@ -291,10 +440,13 @@ float zgo_dot_f32_row(const uint8_t* row, const float* x, size_t n) {
     return result;
 }
 
-/* cpu/src/source.rs:234-313 (Source profile).  Q8_0 pairs with the dynamic
- * Q8_0 activation; Q4_K uses dot_row (source.rs:431-459) because the
- * reference refuses a source-exact Q4_K projection (source.rs:265-270);
- * F32 uses the 4x8 FMA reduction.  Rows run in parallel (Rayon, :285-305). */
+/* cpu/src/source.rs:234-313 (Source profile) with the pairing of
+ * core/src/numerics.rs:96-122.  Q8_0 and Q4_0 pair with the dynamic Q8_0
+ * activation (Q4_0 in the repacked schedule when rows % 8 == 0,
+ * source.rs:286-296), Q4_1 with Q8_1, Q6_K with Q8_K; Q4_K uses dot_row
+ * (source.rs:431-459) because the reference refuses a source-exact Q4_K
+ * projection (source.rs:265-270); F32 uses the 4x8 FMA reduction.  Rows run
+ * in parallel (Rayon, :285-305). */
 int zgo_matvec(int t, const uint8_t* w, size_t wbytes, size_t rows, size_t cols,
                const float* x, float* y, int threads) {
     if (rows == 0 || rows > 1000000 || cols == 0 || !finite_all(x, cols)) return ZGO_E_MALFORMED;
@@ -303,14 +455,24 @@ int zgo_matvec(int t, const uint8_t* w, size_t wbytes, size_t rows, size_t cols,
     if (cols % be) return ZGO_E_MALFORMED;
     size_t row_bytes = (size_t)(cols / be * bb);
     if (row_bytes * rows != wbytes) return ZGO_E_MALFORMED;
-    if (t != ZGO_Q8_0 && t != ZGO_Q4_K && t != ZGO_F32) return ZGO_E_UNSUPPORTED;
+    if (t != ZGO_Q8_0 && t != ZGO_Q4_K && t != ZGO_F32 && t != ZGO_Q4_0 && t != ZGO_Q4_1 && t != ZGO_Q6_K)
+        return ZGO_E_UNSUPPORTED;
     int8_t* qs = NULL;
     float* dd = NULL;
-    if (t == ZGO_Q8_0) {
+    float* ss = NULL;
+    int32_t* bs = NULL;
+    if (t == ZGO_Q8_0 || t == ZGO_Q4_0 || t == ZGO_Q4_1) {
         qs = (int8_t*)malloc(cols);
         dd = (float*)malloc(sizeof(float) * (cols / 32));
-        int rc = zgo_q8_activation(x, cols, qs, dd, NULL);
-        if (rc) { free(qs); free(dd); return rc; }
+        ss = (float*)malloc(sizeof(float) * (cols / 32));
+        int rc = zgo_q8_activation(x, cols, qs, dd, ss);
+        if (rc) { free(qs); free(dd); free(ss); return rc; }
+    } else if (t == ZGO_Q6_K) {
+        qs = (int8_t*)malloc(cols);
+        dd = (float*)malloc(sizeof(float) * (cols / 256));
+        bs = (int32_t*)malloc(sizeof(int32_t) * (cols / 16));
+        int rc = zgo_q8k_activation(x, cols, qs, dd, bs);
+        if (rc) { free(qs); free(dd); free(bs); return rc; }
     }
     long long nrows = (long long)rows;
 #ifdef _OPENMP
@@ -321,11 +483,17 @@ int zgo_matvec(int t, const uint8_t* w, size_t wbytes, size_t rows, size_t cols,
         const uint8_t* row = w + (size_t)r * row_bytes;
         if (t == ZGO_Q8_0) y[r] = zgo_dot_q8_0_row(row, qs, dd, cols / 32);
         else if (t == ZGO_Q4_K) y[r] = zgo_dot_q4k_row(row, x, cols / 256);
+        else if (t == ZGO_Q4_0 && rows % 8 == 0) y[r] = zgo_dot_q4_0_repacked_row(row, qs, dd, cols / 32);
+        else if (t == ZGO_Q4_0) y[r] = zgo_dot_q4_0_row(row, qs, dd, cols / 32);
+        else if (t == ZGO_Q4_1) y[r] = zgo_dot_q4_1_row(row, qs, dd, ss, cols / 32);
+        else if (t == ZGO_Q6_K) y[r] = zgo_dot_q6k_row(row, qs, dd, bs, cols / 256);
         else y[r] = zgo_dot_f32_row(row, x, cols);
     }
     (void)threads;
     free(qs);
     free(dd);
+    free(ss);
+    free(bs);
     return finite_all(y, rows) ? ZGO_OK : ZGO_E_MALFORMED;
 }
 

@@ -62,6 +62,11 @@ int   zgo_q8_activation(const float* x, size_t n, int8_t* qs, float* d, float* s
 float zgo_dot_q8_0_row(const uint8_t* row, const int8_t* qs, const float* d, size_t nblocks);
 float zgo_dot_q4k_row(const uint8_t* row, const float* x, size_t nblocks);
 float zgo_dot_f32_row(const uint8_t* row, const float* x, size_t n);
+int   zgo_q8k_activation(const float* x, size_t n, int8_t* qs, float* d, int32_t* bsums);
+float zgo_dot_q4_0_row(const uint8_t* row, const int8_t* qs, const float* d, size_t nblocks);
+float zgo_dot_q4_0_repacked_row(const uint8_t* row, const int8_t* qs, const float* d, size_t nblocks);
+float zgo_dot_q4_1_row(const uint8_t* row, const int8_t* qs, const float* d, const float* s, size_t nblocks);
+float zgo_dot_q6k_row(const uint8_t* row, const int8_t* qs, const float* d, const int32_t* bsums, size_t nblocks);
 int   zgo_matvec(int ggml_type, const uint8_t* w, size_t wbytes, size_t rows, size_t cols,
                  const float* x, float* y, int threads);
 

@@ -60,6 +60,11 @@ def _declare(L):
         "zgo_dot_q8_0_row": (C.c_float, [P, P, P, SZ]),
         "zgo_dot_q4k_row": (C.c_float, [P, P, SZ]),
         "zgo_dot_f32_row": (C.c_float, [P, P, SZ]),
+        "zgo_q8k_activation": (C.c_int, [P, SZ, P, P, P]),
+        "zgo_dot_q4_0_row": (C.c_float, [P, P, P, SZ]),
+        "zgo_dot_q4_0_repacked_row": (C.c_float, [P, P, P, SZ]),
+        "zgo_dot_q4_1_row": (C.c_float, [P, P, P, P, SZ]),
+        "zgo_dot_q6k_row": (C.c_float, [P, P, P, P, SZ]),
         "zgo_matvec": (C.c_int, [C.c_int, P, SZ, SZ, SZ, P, P, C.c_int]),
         "zgo_rms_norm": (C.c_int, [P, P, SZ, C.c_float, P]),
         "zgo_grouped_rms_norm": (C.c_int, [P, P, SZ, SZ, C.c_float, P]),
@@ -146,6 +151,40 @@ def dot_q8_0_row(row, x):
     qs, d, _ = q8_activation(x)
     row = np.ascontiguousarray(row, np.uint8)
     return lib().zgo_dot_q8_0_row(ptr(row), ptr(qs), ptr(d), x.size // 32)
+
+
+def q8k_activation(x):
+    x = f32(x)
+    qs = np.empty(x.size, np.int8)
+    d = np.empty(x.size // 256, np.float32)
+    bs = np.empty(x.size // 16, np.int32)
+    _chk(lib().zgo_q8k_activation(ptr(x), x.size, ptr(qs), ptr(d), ptr(bs)), "q8k_activation")
+    return qs, d, bs
+
+
+def dot_q4_0_row(row, x, repacked=False):
+    qs, d, _ = q8_activation(x)
+    row = np.ascontiguousarray(row, np.uint8)
+    fn = lib().zgo_dot_q4_0_repacked_row if repacked else lib().zgo_dot_q4_0_row
+    return fn(ptr(row), ptr(qs), ptr(d), x.size // 32)
+
+
+def dot_q4_1_row(row, x):
+    qs, d, s = q8_activation(x)
+    row = np.ascontiguousarray(row, np.uint8)
+    return lib().zgo_dot_q4_1_row(ptr(row), ptr(qs), ptr(d), ptr(s), x.size // 32)
+
+
+def dot_q6k_row(row, x):
+    qs, d, bs = q8k_activation(x)
+    row = np.ascontiguousarray(row, np.uint8)
+    return lib().zgo_dot_q6k_row(ptr(row), ptr(qs), ptr(d), ptr(bs), x.size // 256)
+
+
+def dot_f32_row(row, x):
+    row = np.ascontiguousarray(row, np.uint8)
+    x = f32(x)
+    return lib().zgo_dot_f32_row(ptr(row), ptr(x), x.size)
 
 
 def dot_q4k_row(row, x):

@@ -261,6 +261,151 @@ def test_q4_k_row_dot_within_reference_bound_and_f64_closed_form():
     np.testing.assert_allclose(y, ref, rtol=0, atol=2e-5 * np.abs(ref).max())
 
 
+def test_q8_k_keeps_first_signed_maximum_and_zero():
+    # quantization.rs:367-400: the first element of largest magnitude sets
+    # the signed scale; an all-zero block gives d = 0 and zero codes
+    for first, scale, code in ((127.0, -1.0, -2), (-127.0, 1.0, 2)):
+        x = np.zeros(256, np.float32)
+        x[:4] = [first, -first, 0.5, 1.5]
+        qs, d, bs = O.q8k_activation(x)
+        assert bits(d[0]) == bits(scale)
+        assert list(qs[:4]) == [-127, 127, 0, code] and not qs[4:].any()
+        assert bs[0] == code and not bs[1:].any()
+    for zero in (0.0, -0.0):
+        qs, d, _ = O.q8k_activation(np.full(256, zero, np.float32))
+        assert bits(d[0]) == 0 and not qs.any()
+    with pytest.raises(O.OracleError):
+        O.q8k_activation(np.zeros(255, np.float32))
+    for v in (np.nan, np.inf):
+        with pytest.raises(O.OracleError):
+            O.q8k_activation(np.full(256, v, np.float32))
+
+
+def test_source_exact_blocks_match_hand_computed_integer_fixtures():
+    # quantization.rs:436-494: x = 127 everywhere, one block per codec
+    x32 = np.full(32, 127.0, np.float32)
+    q4_0 = np.array(le16(0x3C00) + [0xA9] * 16, np.uint8)  # 16 ones + 16 twos
+    assert bits(O.dot_q4_0_row(q4_0, x32)) == bits(6096.0)
+    assert bits(O.dot_q4_0_row(q4_0, x32, repacked=True)) == bits(6096.0)
+    q4_1 = np.array(le16(0x3800) + le16(0xBC00) + [0x32] * 16, np.uint8)  # d=1/2, m=-1
+    assert bits(O.dot_q4_1_row(q4_1, x32)) == bits(1016.0)
+    q6 = np.zeros(210, np.uint8)
+    q6[:128] = 0x21
+    q6[128:192] = 0xAA  # codes 33/34 before the -32 shift
+    q6[192:208] = 255  # local scales -1
+    q6[208:] = le16(0x3800)
+    assert bits(O.dot_q6k_row(q6, np.full(256, 127.0, np.float32))) == bits(-24384.0)
+
+
+def test_q4_0_repacked_block_order_stays_distinct_from_eight_lane_reduction():
+    # quantization.rs:497-531: block sums 2^24, 1, -2^24; the repacked
+    # schedule loses the 1, the eight-lane one keeps it
+    x = np.zeros(96, np.float32)
+    x[31::32] = 127.0
+    x[0], x[36], x[64] = -64.0, 1.0, 64.0
+    row = np.full(54, 0x88, np.uint8)
+    for b in range(3):
+        row[18 * b:18 * b + 2] = le16(0x7800)
+        row[18 * b + 2] = 0x80
+    row[18:20] = le16(0x3C00)
+    row[20] = 0x88
+    row[24] = 0x89
+    assert bits(O.dot_q4_0_row(row, x, repacked=True)) == 0
+    assert bits(O.dot_q4_0_row(row, x)) == bits(1.0)
+
+
+def test_q6_k_lane_of_an_element_is_its_position_mod_32_over_4():
+    # Three superblocks whose lane-0 sums are 2^25, -32 (offset) and -2^25,
+    # with a +1 that the reference puts in lane 1 (element 4: (4 % 32) / 4).
+    # Lane 0 at 2^25 has spacing 2, so a layout that put element 4 in lane 0
+    # (contiguous 32-groups) would lose it: -31 against -32.
+    x = np.zeros(768, np.float32)
+    row = np.zeros(3 * 210, np.uint8)
+    for b, (probe_at, probe_x, dw, s0) in enumerate(((1, -1.0, 0xF000, 0x80), (4, -1.0, 0xBC00, 1),
+                                                     (1, 1.0, 0xF000, 0x80))):
+        blk = row[210 * b:210 * (b + 1)]
+        x[256 * b] = 127.0  # the block maximum: d_a = -1, code 32, no net term
+        x[256 * b + probe_at] = probe_x
+        blk[:128] = 0x00
+        blk[128:192] = 0xAA  # high bits 2 for every group: code 32 where the nibble is 0
+        blk[192:208] = 1
+        blk[192] = s0
+        blk[208:210] = le16(dw)
+        # element `probe_at` (< 32: half 0, group 0, low nibble of ql[probe_at], high bits qh[probe_at] & 3)
+        code = 0 if b != 1 else 1
+        blk[probe_at] = code & 15
+        blk[128 + probe_at] = (0xAA & ~3) | (code >> 4)
+    got = O.dot_q6k_row(row, x)
+    assert bits(got) == bits(-31.0), got
+    # the same rows through the matrix-vector entry
+    assert bits(O.matvec(O.Q6_K, row, 1, 768, x)[0]) == bits(-31.0)
+
+
+def test_q4_1_zero_points_accumulate_apart_from_the_lanes():
+    # Lane 0 carries 2^24 then -2^24 while the zero points add m*s = 1 in
+    # between: the reference adds the separate sum after the tree (result 1);
+    # folding it into lane 0 would lose it at 2^24.
+    x = np.zeros(96, np.float32)
+    x[0:3] = [127.0, 127.0, 26.0]
+    x[32:34] = [127.0, -126.0]
+    x[64:67] = [-127.0, -127.0, -26.0]
+    row = np.zeros(60, np.uint8)
+    for b, (dw, m) in enumerate(((0x6C00, 0), (0x3C00, 0x3C00), (0x6C00, 0))):
+        blk = row[20 * b:20 * (b + 1)]
+        blk[0:2] = le16(dw)
+        blk[2:4] = le16(m)
+        if b != 1:
+            blk[4:8] = [15, 15, 11, 0]
+    assert bits(O.dot_q4_1_row(row, x)) == bits(1.0)
+
+
+def test_f32_dot_four_by_eight_accumulators_and_tree():
+    # source.rs:325-366: element 8 lands in accumulator (1, 0) and meets
+    # elements 0 and 16 (accumulators (0, 0), (2, 0)) only in the tree:
+    # (2^24 + -2^24) + 1 = 1, where a serial sum gives 0
+    x = np.zeros(40, np.float32)
+    x[0], x[8], x[16] = 2.0 ** 24, 1.0, -(2.0 ** 24)
+    x[33] = 3.0  # tail element past the last full 32-step, added serially
+    w = np.ones(40, np.float32)
+    w[33] = 0.5
+    row = np.frombuffer(w.tobytes(), np.uint8)
+    assert bits(O.dot_f32_row(row, x)) == bits(2.5)
+    assert bits(O.matvec(O.F32, row, 1, 40, x)[0]) == bits(2.5)
+
+
+@pytest.mark.parametrize("kind,K", [("Q4_0", 512), ("Q4_1", 512), ("Q6_K", 1024)])
+def test_integer_block_dots_match_exact_integer_closed_form(kind, K):
+    # f64 closed form over the decoded weights and the coded activation:
+    # sum_b scale_b * sum_i w_i q_i (+ zero points).  A wrong nibble, high
+    # bit, local scale or offset breaks the 1e-6 bound.
+    rng = np.random.default_rng(hash(kind) % 1000)
+    rows = 16
+    t = getattr(O, kind)
+    bb = {"Q4_0": 18, "Q4_1": 20, "Q6_K": 210}[kind]
+    be = 256 if kind == "Q6_K" else 32
+    w = rng.integers(0, 256, size=(rows, K // be, bb), dtype=np.uint8)
+    hdr = {"Q4_0": [0], "Q4_1": [0, 2], "Q6_K": [208]}[kind]
+    for o in hdr:
+        w[:, :, o:o + 2] = np.frombuffer(np.float16(rng.uniform(-0.01, 0.01, rows * K // be)).tobytes(),
+                                         np.uint8).reshape(rows, -1, 2)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = O.matvec(t, w.reshape(-1), rows, K, x)
+    dec = O.dequantize(t, w.reshape(-1), rows * K).reshape(rows, K).astype(np.float64)
+    if kind == "Q6_K":
+        qs, d, _ = O.q8k_activation(x)
+        xa = (qs.reshape(-1, 256).astype(np.float64) * d[:, None]).reshape(-1)
+    else:
+        qs, d, s = O.q8_activation(x)
+        xa = (qs.reshape(-1, 32).astype(np.float64) * d[:, None]).reshape(-1)
+    ref = dec @ xa
+    if kind == "Q4_1":
+        # the zero point pairs with the f16-rounded s, not with sum(q) * f16(d)
+        m = w[:, :, 2:4].copy().view(np.float16).astype(np.float64).reshape(rows, -1)
+        qsum = qs.reshape(-1, 32).astype(np.float64).sum(-1)
+        ref = ref - (m * (qsum * d)[None, :]).sum(-1) + (m * s[None, :]).sum(-1)
+    np.testing.assert_allclose(y, ref, rtol=0, atol=1e-5 * np.abs(ref).max())
+
+
 def test_q8_0_row_dot_within_reference_bound():
     # cpu/src/source.rs:641-679 for the Q8_0 codec (scale 1.0, zero codes)
     row = np.zeros(34, np.uint8)
