@@ -48,7 +48,7 @@ enum {
 };
 
 /* ggml tensor type codes, core/src/encoding.rs:77-91 */
-enum { ZG_F32 = 0, ZG_F16 = 1, ZG_Q8_0 = 8, ZG_Q4_K = 12, ZG_BF16 = 30 };
+enum { ZG_F32 = 0, ZG_F16 = 1, ZG_Q4_1 = 3, ZG_Q8_0 = 8, ZG_Q4_K = 12, ZG_Q6_K = 14, ZG_BF16 = 30 };
 
 typedef struct zg_ctx zg_ctx;
 typedef struct zg_weight zg_weight;
@@ -223,7 +223,7 @@ typedef struct zg_session zg_session;
 
 typedef struct zg_tensor_desc {
     const char* name;  /* GGUF tensor name, e.g. "blk.0.attn_qkv.weight" */
-    int ggml_type;     /* ZG_F32, ZG_Q8_0 or ZG_Q4_K */
+    int ggml_type;     /* ZG_F32, ZG_Q8_0, ZG_Q4_K, ZG_Q4_1 or ZG_Q6_K */
     uint64_t shape0;   /* GGML ne0: inner (columns / vector length) */
     uint64_t shape1;   /* GGML ne1: rows (1 for vectors) */
     const void* data;  /* host bytes, only read during zg_model_load */

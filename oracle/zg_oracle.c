@@ -987,6 +987,7 @@ struct zgo_model {
 
 struct zgo_session {
     zgo_model* m;
+    unsigned layers;  /* kept here: destroying a session must not read its model */
     int position;
     float** conv;     /* per layer [3*6144] or NULL */
     float** rec;      /* per layer [H][d][d] value-major or NULL */
@@ -1078,6 +1079,7 @@ zgo_session* zgo_session_create(zgo_model* m) {
     zgo_session* s = (zgo_session*)calloc(1, sizeof(zgo_session));
     s->m = m;
     unsigned nl = m->g.layers;
+    s->layers = nl;
     s->conv = (float**)calloc(nl, sizeof(float*));
     s->rec = (float**)calloc(nl, sizeof(float*));
     s->keys = (float**)calloc(nl, sizeof(float*));
@@ -1097,7 +1099,7 @@ zgo_session* zgo_session_create(zgo_model* m) {
 
 void zgo_session_destroy(zgo_session* s) {
     if (!s) return;
-    for (unsigned i = 0; i < s->m->g.layers; ++i) {
+    for (unsigned i = 0; i < s->layers; ++i) {
         free(s->conv[i]); free(s->rec[i]); free(s->keys[i]); free(s->values[i]);
     }
     free(s->conv); free(s->rec); free(s->keys); free(s->values);

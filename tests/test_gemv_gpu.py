@@ -186,7 +186,7 @@ def test_region_refusals(kern):
     x = np.ones(32, np.float32)
     w = np.zeros(34, np.uint8)
     # unsupported codec -> Unsupported (caller may use its CPU path)
-    r = R.MatVecRegion(R.SourceIdentity(5), "t.q6k", 14, 256, 1, np.zeros(210, np.uint8), np.ones(256, np.float32))
+    r = R.MatVecRegion(R.SourceIdentity(5), "t.q4_0", 2, 32, 1, np.zeros(18, np.uint8), np.ones(32, np.float32))
     assert kern.try_execute(r) is R.UNSUPPORTED
     # nonfinite activation -> error
     bad = R.MatVecRegion(R.SourceIdentity(5), "t.q8", synth.Q8_0, 32, 1, w, np.full(32, np.nan, np.float32))

@@ -51,9 +51,9 @@ void free_weight(zg_weight* w) {
     w->dw.qs = w->dw.hdr = w->dw.qs_t = w->dw.hdr_t = nullptr;
 }
 
-bool supported_type(int t) { return t == ZG_Q8_0 || t == ZG_Q4_K || t == ZG_F32; }
+bool supported_type(int t) { return t == ZG_Q8_0 || t == ZG_Q4_K || t == ZG_F32 || t == ZG_Q4_1 || t == ZG_Q6_K; }
 
-size_t block_elems(int t) { return t == ZG_Q8_0 ? 32 : t == ZG_Q4_K ? 256 : 1; }
+size_t block_elems(int t) { return (t == ZG_Q8_0 || t == ZG_Q4_1) ? 32 : (t == ZG_Q4_K || t == ZG_Q6_K) ? 256 : 1; }
 
 // Upload and split one GGUF matrix.  Caller holds the ctx lock.
 int build_weight(zg_ctx* ctx, int type, size_t cols, size_t rows, const void* bytes, size_t len,
@@ -69,6 +69,13 @@ int build_weight(zg_ctx* ctx, int type, size_t cols, size_t rows, const void* by
     } else if (type == ZG_Q4_K) {
         w->dw.qs_bytes = rows * (cols / 2);
         w->dw.hdr_bytes = rows * (cols / 256) * 16;
+    } else if (type == ZG_Q4_1) {
+        const size_t nbc8 = (cols / 32 + 7) / 8;
+        w->dw.qs_bytes = (rows + 7) / 8 * nbc8 * 1024;
+        w->dw.hdr_bytes = rows * nbc8 * 8 * 4;
+    } else if (type == ZG_Q6_K) {
+        w->dw.qs_bytes = (rows + 7) / 8 * (cols / 256) * 64 * 24;
+        w->dw.hdr_bytes = rows * (cols / 256) * 20;
     } else {
         w->dw.qs_bytes = rows * cols * 4;
         w->dw.hdr_bytes = 0;

@@ -42,7 +42,7 @@ __device__ __forceinline__ void epilogue(const FusedGemvArgs& a, int m, int row,
 
 // ================================================ workgroup prologue
 
-constexpr int kCodecQ4K = 0, kCodecQ8 = 1;
+constexpr int kCodecQ4K = 0, kCodecQ8 = 1, kCodecQ81 = 2, kCodecQ8K = 3, kCodecF32 = 4;
 constexpr int kRecWords = 36;  // Q4_K record: 32 dwords of int16 pairs + {xs_lo, xs_hi, sum_lo, sum_hi}
 
 // Activation row m prepared once per workgroup.  Thread t holds the float4
@@ -52,13 +52,21 @@ constexpr int kRecWords = 36;  // Q4_K record: 32 dwords of int16 pairs + {xs_lo
 //   Q8_0 (cpu/src/source/quantization.rs:37-61): per 32-block amax,
 //     d = amax/127, code = clamp(rint(v*127/amax)), d rounded to f16;
 //     codes [K/4] words, scales [K/32].
+//   Q8_1 (quantization.rs:37-61, Q4_1 pairing): as Q8_0, plus per block
+//     s = f16(sum of codes * unrounded d) in `extra`.
+//   Q8_K (quantization.rs:66-92, Q6_K pairing): per 256-block (one
+//     wavefront) the first element of largest magnitude gives the signed
+//     max, inv = -127/max, d = 1/inv in `extra` [K/256], codes as Q8_0, and
+//     the sums of 16 codes in `bsums` [K/16].
+//   F32: the values themselves, floats [K] at `codes`.
 //   Q4_K: per 32-group int16 fixed point, xq = rint(v*32767/amax), with the
 //     group's scale amax/32767 and its f32 sum; records [K/64][36] dwords in
 //     the pairing gemv_q4k_kernel expects (element e of a group goes to
 //     dword (e&1 ? 8 : 0) + e/4, half (e>>1)&1; high group +16).
-// Ends with a barrier.  K <= 1024 * JMAX, K % 32 == 0.
+// Ends with a barrier.  K <= 1024 * JMAX, K % 32 == 0 (K % 256 for Q8_K).
 template <int PRO, int CODEC, int JMAX>
-__device__ void wg_prologue(const FusedGemvArgs& a, int m, bool valid, uint32_t* rec, int* codes, float* scales) {
+__device__ void wg_prologue(const FusedGemvArgs& a, int m, bool valid, uint32_t* rec, int* codes, float* scales,
+                            float* extra = nullptr, int* bsums = nullptr) {
     __shared__ double red[4];
     const int tid = threadIdx.x, lane = tid & 63, K = a.K;
     v4f v[JMAX], w[JMAX];
@@ -118,9 +126,76 @@ __device__ void wg_prologue(const FusedGemvArgs& a, int m, bool valid, uint32_t*
             for (int t = 0; t < 4; ++t) e[t] = o[t] * ggml_silu(e[t]);
         }
         if (!(valid && k < K)) e[0] = e[1] = e[2] = e[3] = 0.0f;
+        if (CODEC == kCodecF32) {
+            if (k < K) *(v4f*)((float*)codes + k) = v4f{e[0], e[1], e[2], e[3]};
+            continue;
+        }
+        if (CODEC == kCodecQ8K) {
+            // first element of largest magnitude in the 256-block of this
+            // wavefront: (|v| bits, 63 - lane) maximised, ties to the lower lane
+            float lam = 0.0f, lsg = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                if (fabsf(e[t]) > lam) {
+                    lam = fabsf(e[t]);
+                    lsg = e[t];
+                }
+            uint32_t key_hi = __float_as_uint(lam), key_lo = 63u - (uint32_t)lane;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const uint32_t oh = __shfl_xor(key_hi, off, 64), ol = __shfl_xor(key_lo, off, 64);
+                if (oh > key_hi || (oh == key_hi && ol > key_lo)) {
+                    key_hi = oh;
+                    key_lo = ol;
+                }
+            }
+            const float amax = __uint_as_float(key_hi);
+            const float msg = __shfl(lsg, 63 - (int)key_lo, 64);
+            const float qi = amax == 0.0f ? 0.0f : -127.0f / msg;
+            const float d = amax == 0.0f ? 0.0f : 1.0f / qi;
+            uint32_t word = 0;
+            int csum = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                float r = rintf(e[t] * qi);
+                r = fminf(fmaxf(r, -128.0f), 127.0f);
+                word |= ((uint32_t)(int)r & 0xffu) << (8 * t);
+                csum += (int)r;
+            }
+            csum += __shfl_xor(csum, 1, 64);
+            csum += __shfl_xor(csum, 2, 64);
+            if (k < K) {
+                codes[k >> 2] = (int)word;
+                if ((lane & 3) == 0) bsums[k >> 4] = csum;
+                if (lane == 0) extra[k >> 8] = d;
+            }
+            continue;
+        }
         float amax = fmaxf(fmaxf(fabsf(e[0]), fabsf(e[1])), fmaxf(fabsf(e[2]), fabsf(e[3])));
         amax = group8_max_all(amax);
         const int l = tid & 7;
+        if (CODEC == kCodecQ81) {
+            const float d = amax / 127.0f;
+            const float qi = amax == 0.0f ? 0.0f : 127.0f / amax;
+            uint32_t word = 0;
+            float csum = 0.0f;  // integer-valued, |sum| <= 4096: exact in f32
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                float r = rintf(e[t] * qi);
+                r = fminf(fmaxf(r, -128.0f), 127.0f);
+                word |= ((uint32_t)(int)r & 0xffu) << (8 * t);
+                csum += r;
+            }
+            csum = group8_sum_all(csum);
+            if (k < K) {
+                codes[k >> 2] = (int)word;
+                if (l == 0) {
+                    scales[k >> 5] = f16_roundtrip(d);
+                    extra[k >> 5] = f16_roundtrip(csum * d);
+                }
+            }
+            continue;
+        }
         if (k < K) {
             if (CODEC == kCodecQ8) {
                 const float d = amax / 127.0f;
@@ -750,6 +825,249 @@ hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* 
 
 // ============================================================ dispatch
 
+// ====================================================== Q4_1, Q6_K, F32
+
+// Q4_1 x Q8_1 (cpu/src/source/quantization.rs:198-227): lane l of a row's 8
+// lanes takes elements 4l..4l+3 of every block, lane = fma(int dot,
+// d_w * d_a, lane); the zero points accumulate apart (summs = summs +
+// m_w * s_a) and join after the reference's lane tree.
+template <int MT, int J, int PRO, int EPI>
+__global__ __launch_bounds__(256) void fused_q41_kernel(FusedGemvArgs a) {
+    extern __shared__ int lds_f41[];
+    const int K = a.K, N = a.N;
+    const int nb = K >> 5, nbc8 = (nb + 7) >> 3;
+    int* codes = lds_f41;                               // [MT][K/4] words
+    float* scales = (float*)(lds_f41 + MT * (K >> 2));  // [MT][nb]
+    float* sums = scales + MT * nb;                     // [MT][nb]
+    const int m0 = blockIdx.y * MT;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+        wg_prologue<PRO, kCodecQ81, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * (K >> 2), scales + m * nb,
+                                       sums + m * nb);
+    const v4i* qs = (const v4i*)a.qs;
+    const uint32_t* hdr = (const uint32_t*)a.hdr;
+    const int lane = threadIdx.x & 63;
+    const int rl = lane >> 3, l = lane & 7;
+    const int groups = (N + 7) >> 3;
+    const int nwaves = gridDim.x * 4;
+    for (int R = blockIdx.x * 4 + (threadIdx.x >> 6); R < groups; R += nwaves) {
+        const int row = R * 8 + rl;
+        const uint32_t* hrow = hdr + (size_t)(row < N ? row : N - 1) * nbc8 * 8;
+        const v4i* tile = qs + (size_t)R * nbc8 * 64 + lane;
+        float acc[MT], summs[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = summs[m] = 0.0f;
+        for (int c = 0; c < nbc8; ++c) {
+            const v4i w4 = load_nt(tile + (size_t)c * 64);
+            const v4u h0 = *(const v4u*)(hrow + 8 * c), h1 = *(const v4u*)(hrow + 8 * c + 4);
+            const uint32_t ww[4] = {(uint32_t)w4.x, (uint32_t)w4.y, (uint32_t)w4.z, (uint32_t)w4.w};
+            const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+            for (int bi = 0; bi < 8; ++bi) {
+                const int b = 8 * c + bi;
+                if (b < nb) {
+                    const uint32_t q = (ww[bi >> 1] >> (16 * (bi & 1))) & 0xffffu;
+                    const int w8 = (int)((q & 0xfu) | ((q & 0xf0u) << 4) | ((q & 0xf00u) << 8) | ((q & 0xf000u) << 12));
+                    const float d0 = f16_to_f32((uint16_t)(hw[bi] & 0xffffu));
+                    const float mw = f16_to_f32((uint16_t)(hw[bi] >> 16));
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        const int partial = __builtin_amdgcn_sdot4(w8, codes[m * (K >> 2) + b * 8 + l], 0, false);
+                        const float ms = mw * sums[m * nb + b];
+                        summs[m] = summs[m] + ms;
+                        const float scale = d0 * scales[m * nb + b];
+                        acc[m] = fmaf((float)partial, scale, acc[m]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = group8_tree_last(acc[m]);
+        if (row < N && l == 7) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                if (m0 + m < a.M) epilogue(a, m0 + m, row, acc[m] + summs[m], EPI);
+        }
+    }
+}
+
+__device__ __forceinline__ int sbyte(const v4u& v, int idx) {
+    const int q = idx >> 2;
+    const uint32_t d = q == 0 ? v.x : (q == 1 ? v.y : (q == 2 ? v.z : v.w));
+    return (int)(int8_t)(d >> (8 * (idx & 3)));
+}
+
+// Q6_K x Q8_K (quantization.rs:228-285): lane L of a row's 8 lanes holds
+// every element at position 4L..4L+3 of its 32-group.  Per superblock its
+// int32 sum is sum(code * local scale * q8) (4-element dot products, one
+// local scale each) minus 32 * (bsum * scale) over the contiguous 16-groups
+// 2L and 2L+1; lane = fma((float)int, d_a * d_w, lane); the Q8_0 lane tree.
+template <int MT, int J, int PRO, int EPI>
+__global__ __launch_bounds__(256) void fused_q6k_kernel(FusedGemvArgs a) {
+    extern __shared__ int lds_f6[];
+    const int K = a.K, N = a.N, nsb = K >> 8;
+    int* codes = lds_f6;                                 // [MT][K/4] words
+    float* dk = (float*)(lds_f6 + MT * (K >> 2));        // [MT][nsb]
+    int* bs = (int*)(dk + MT * nsb);                     // [MT][K/16]
+    const int m0 = blockIdx.y * MT;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+        wg_prologue<PRO, kCodecQ8K, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * (K >> 2), nullptr,
+                                       dk + m * nsb, bs + m * (K >> 4));
+    const uint32_t* qa = (const uint32_t*)a.qs;
+    const uint32_t* qb = qa + q6k_b_offset((size_t)N, (size_t)K);
+    const uint8_t* scl = (const uint8_t*)a.hdr;
+    const float* dw = (const float*)(scl + (size_t)N * nsb * 16);
+    const int lane = threadIdx.x & 63;
+    const int rl = lane >> 3, l = lane & 7;
+    const int groups = (N + 7) >> 3;
+    const int nwaves = gridDim.x * 4;
+    for (int R = blockIdx.x * 4 + (threadIdx.x >> 6); R < groups; R += nwaves) {
+        const int row = R * 8 + rl;
+        const size_t rr = (size_t)(row < N ? row : N - 1);
+        float acc[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+        for (int sb = 0; sb < nsb; ++sb) {
+            const v4u A = *(const v4u*)(qa + q6k_a_index((size_t)row, (size_t)sb, l, (size_t)nsb));
+            const uint2 B = *(const uint2*)(qb + q6k_b_index((size_t)row, (size_t)sb, l, (size_t)nsb));
+            const v4u S = *(const v4u*)(scl + (rr * nsb + sb) * 16);
+            const float wd = dw[rr * nsb + sb];
+            const uint32_t av[4] = {A.x, A.y, A.z, A.w};
+            const uint32_t bv[2] = {B.x, B.y};
+            int code4[2][4], sub[2][4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const uint32_t nib = (av[h * 2 + (g & 1)] >> (g >= 2 ? 4 : 0)) & 0x0f0f0f0fu;
+                    const uint32_t hi = ((bv[h] >> (2 * g)) & 0x03030303u) << 4;
+                    code4[h][g] = (int)(nib | hi);
+                    sub[h][g] = sbyte(S, h * 8 + g * 2 + (l >> 2));
+                }
+            const int so0 = sbyte(S, 2 * l), so1 = sbyte(S, 2 * l + 1);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const int* cw = codes + m * (K >> 2) + sb * 64 + l;
+                int iacc = 0;
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+                        iacc += sub[h][g] * __builtin_amdgcn_sdot4(code4[h][g], cw[h * 32 + g * 8], 0, false);
+                const int* bm = bs + m * (K >> 4) + sb * 16;
+                iacc -= 32 * (bm[2 * l] * so0 + bm[2 * l + 1] * so1);
+                const float scale = dk[m * nsb + sb] * wd;
+                acc[m] = fmaf((float)iacc, scale, acc[m]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = group8_tree_last(acc[m]);
+        if (row < N && l == 7) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                if (m0 + m < a.M) epilogue(a, m0 + m, row, acc[m], EPI);
+        }
+    }
+}
+
+// F32 rows (cpu/src/source.rs:325-366): 32 lanes per row, lane t holds the
+// accumulator of positions t mod 32 (the reference's accum[t / 8][t % 8]),
+// fma over the 32-element steps in order; the tree (a[t] + a[t+16]) +
+// (a[t+8] + a[t+24]), then lanes t, t+4, then (h0 + h1) + (h2 + h3) is the
+// XOR tree 16, 8, 4, 1, 2; the tail past the last full step is added
+// serially (product, then sum).
+template <int MT, int J, int PRO, int EPI>
+__global__ __launch_bounds__(256) void fused_f32_kernel(FusedGemvArgs a) {
+    extern __shared__ int lds_ff[];
+    const int K = a.K, N = a.N;
+    float* xs = (float*)lds_ff;  // [MT][K]
+    const int m0 = blockIdx.y * MT;
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+        wg_prologue<PRO, kCodecF32, J>(a, m0 + m, m0 + m < a.M, nullptr, (int*)(xs + (size_t)m * K), nullptr);
+    const float* W = (const float*)a.qs;
+    const int lane = threadIdx.x & 63, t = lane & 31;
+    const int np = K & ~31;
+    const int pairs = (N + 1) >> 1;
+    const int nwaves = gridDim.x * 4;
+    for (int P = blockIdx.x * 4 + (threadIdx.x >> 6); P < pairs; P += nwaves) {
+        const int row = P * 2 + (lane >> 5);
+        const size_t rr = (size_t)(row < N ? row : N - 1);
+        const float* wr = W + rr * K;
+        float acc[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+        for (int base = 0; base < np; base += 32) {
+            const float w = wr[base + t];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) acc[m] = fmaf(w, xs[(size_t)m * K + base + t], acc[m]);
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float v = acc[m];
+            v = v + __shfl_xor(v, 16, 64);
+            v = v + __shfl_xor(v, 8, 64);
+            v = v + __shfl_xor(v, 4, 64);
+            v = v + __shfl_xor(v, 1, 64);
+            v = v + __shfl_xor(v, 2, 64);
+            acc[m] = v;
+        }
+        if (row < N && t == 0) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (m0 + m >= a.M) continue;
+                float r = acc[m];
+                for (int i = np; i < K; ++i) {
+                    const float p = wr[i] * xs[(size_t)m * K + i];
+                    r = r + p;
+                }
+                epilogue(a, m0 + m, row, r, EPI);
+            }
+        }
+    }
+}
+
+template <int PRO, int EPI>
+static hipError_t launch_codec(const FusedGemvArgs& a, int type, hipStream_t s) {
+    const int K = a.K;
+    const int mt = type == kF32 ? 1 : (a.M == 1 ? 1 : (a.M == 2 ? 2 : 4));
+    size_t per;
+    if (type == kQ4_1) per = (size_t)K + (size_t)(K / 32) * 8;
+    else if (type == kQ6_K) per = (size_t)K + (size_t)(K / 256) * 4 + (size_t)(K / 16) * 4;
+    else per = (size_t)K * 4;
+    const size_t lds = per * mt;
+    const size_t units = type == kF32 ? ((size_t)a.N + 1) / 2 : ((size_t)a.N + 7) / 8;
+    const unsigned wgs = (unsigned)std::min<size_t>((units + 3) / 4, 256 * 8);
+    dim3 g(wgs, (unsigned)((a.M + mt - 1) / mt));
+#define ZG_FC(KER, T, JJ) hipLaunchKernelGGL((KER<T, JJ, PRO, EPI>), g, dim3(256), lds, s, a)
+#define ZG_FCJ(KER, JJ)                 \
+    if (mt == 1) ZG_FC(KER, 1, JJ);      \
+    else if (mt == 2) ZG_FC(KER, 2, JJ); \
+    else ZG_FC(KER, 4, JJ);
+#define ZG_FCK(KER)          \
+    if (K <= 1024) {         \
+        ZG_FCJ(KER, 1)       \
+    } else if (K <= 2048) {  \
+        ZG_FCJ(KER, 2)       \
+    } else if (K <= 4096) {  \
+        ZG_FCJ(KER, 4)       \
+    } else {                 \
+        ZG_FCJ(KER, 8)       \
+    }
+    if (type == kQ4_1) {
+        ZG_FCK(fused_q41_kernel)
+    } else if (type == kQ6_K) {
+        ZG_FCK(fused_q6k_kernel)
+    } else {
+        ZG_FCK(fused_f32_kernel)
+    }
+#undef ZG_FCK
+#undef ZG_FCJ
+#undef ZG_FC
+    return hipGetLastError();
+}
+
 template <int PRO, int EPI>
 static hipError_t launch_q4k(const FusedGemvArgs& a, hipStream_t s) {
     // one 64-element chunk per lane while the row fits 64 lanes (K <= 4096),
@@ -842,6 +1160,8 @@ static hipError_t launch_pro(const FusedGemvArgs& a, int type, hipStream_t s) {
     }
     if (type == kQ4_K) return a.epi == EPI_RESID ? launch_q4k<PRO, EPI_RESID>(a, s) : launch_q4k<PRO, EPI_STORE>(a, s);
     if (type == kQ8_0) return a.epi == EPI_RESID ? launch_q8<PRO, EPI_RESID>(a, s) : launch_q8<PRO, EPI_STORE>(a, s);
+    if (type == kQ4_1 || type == kQ6_K || type == kF32)
+        return a.epi == EPI_RESID ? launch_codec<PRO, EPI_RESID>(a, type, s) : launch_codec<PRO, EPI_STORE>(a, type, s);
     return hipErrorInvalidValue;
 }
 
@@ -859,8 +1179,9 @@ bool fused_gemv_supported(int type, size_t K, size_t N, int pro) {
     if (N == 0 || K == 0 || N > (1u << 30)) return false;
     if (pro == PRO_GATED && (K % 128 || K / 128 > 256 || 256 % (K / 128))) return false;
     if (K > 8192) return false;  // prologue slabs
-    if (type == kQ4_K) return K % 256 == 0;
-    if (type == kQ8_0) return K % 32 == 0;
+    if (type == kQ4_K || type == kQ6_K) return K % 256 == 0;
+    if (type == kQ8_0 || type == kQ4_1) return K % 32 == 0;
+    if (type == kF32) return K % 4 == 0;
     return false;
 }
 

@@ -159,6 +159,60 @@ __device__ __forceinline__ size_t q8_tile_offset(size_t row, size_t b, int l, si
     return (((row >> 3) * nbc + (b >> 2)) * 64 + (row & 7) * 8 + l) * 16 + (b & 3) * 4;
 }
 
+// Q4_1 device layout.  Rows in tiles of 8, blocks in chunks of 8: lane
+// (row % 8) * 8 + l of a tile holds, per chunk, 16 bytes = eight 16-bit
+// words, word bi = the four nibbles of elements 4l..4l+3 of block 8c+bi
+// (element e of a GGUF block is the low nibble of byte e for e < 16, else
+// the high nibble of byte e-16), nibble j in bits 4j..4j+3.  A wavefront
+// reads one contiguous 1 KB run per chunk.  Headers: uint32 d | m << 16 per
+// (row, block), rows padded to 8 blocks.  nbc8 = ceil(K/32 / 8).
+__host__ __device__ __forceinline__ size_t q41_word_index(size_t row, size_t b, int l, size_t nbc8) {
+    return (((row >> 3) * nbc8 + (b >> 3)) * 64 + (row & 7) * 8 + l) * 8 + (b & 7);
+}
+
+// Q6_K device layout.  Rows in tiles of 8; per superblock lane (row % 8) * 8
+// + L holds the bits of the 32 elements whose position in their 32-group is
+// 4L..4L+3 (the reference's Q6_K x Q8_K lane):
+//   plane A, 4 dwords: ql bytes 4L.., 32+4L.. (first half), 64+4L..,
+//     96+4L.. (second half) -- low nibble = group 0/1, high = group 2/3;
+//   plane B, 2 dwords: qh bytes 4L.. (first half), 32+4L.. (second half),
+//     2 bits per group.
+// Headers: the 16 int8 local scales per (row, superblock), then f32 d.
+__host__ __device__ __forceinline__ size_t q6k_a_index(size_t row, size_t sb, int L, size_t nsb) {
+    return (((row >> 3) * nsb + sb) * 64 + (row & 7) * 8 + L) * 4;  // in dwords
+}
+__host__ __device__ __forceinline__ size_t q6k_b_index(size_t row, size_t sb, int L, size_t nsb) {
+    return (((row >> 3) * nsb + sb) * 64 + (row & 7) * 8 + L) * 2;  // in dwords
+}
+__host__ __device__ __forceinline__ size_t q6k_b_offset(size_t N, size_t K) {  // plane B after plane A, in dwords
+    return (N + 7) / 8 * (K / 256) * 64 * 4;
+}
+
+// Exact element decoders over the layouts above (codecs/q4.rs:22-36 Q4_1:
+// fma(q, d, m); codecs/q6.rs:6-34 Q6_K: (d * scale) * (code - 32)).
+__device__ __forceinline__ float q41_element(const uint16_t* qs, const uint32_t* hdr, size_t row, size_t e, size_t K) {
+    const size_t nb = K / 32, nbc8 = (nb + 7) / 8, b = e / 32;
+    const int i = (int)(e % 32);
+    const uint32_t word = qs[q41_word_index(row, b, i >> 2, nbc8)];
+    const float q = (float)((word >> (4 * (i & 3))) & 15u);
+    const uint32_t h = hdr[row * nbc8 * 8 + b];
+    return fmaf(q, f16_to_f32((uint16_t)(h & 0xffffu)), f16_to_f32((uint16_t)(h >> 16)));
+}
+
+__device__ __forceinline__ float q6k_element(const uint32_t* qs, const uint8_t* scales, const float* d, size_t row,
+                                             size_t e, size_t N, size_t K) {
+    const size_t nsb = K / 256, sb = e / 256;
+    const int at = (int)(e % 256), half = at >> 7, group = (at >> 5) & 3, l32 = at & 31;
+    const int L = l32 >> 2, j = l32 & 3;
+    const uint32_t a = qs[q6k_a_index(row, sb, L, nsb) + half * 2 + (group & 1)];
+    const uint32_t hb = qs[q6k_b_offset(N, K) + q6k_b_index(row, sb, L, nsb) + half];
+    const uint32_t lo = (a >> (8 * j + (group >= 2 ? 4 : 0))) & 15u;
+    const uint32_t hi = (hb >> (8 * j + 2 * group)) & 3u;
+    const int code = (int)(lo | (hi << 4)) - 32;
+    const float sc = (float)(int8_t)scales[(row * nsb + sb) * 16 + half * 8 + group * 2 + l32 / 16];
+    return (d[row * nsb + sb] * sc) * (float)code;
+}
+
 // Q4_K header relayout.  GGUF packs 8 six-bit scales and 8 six-bit mins into
 // 12 bytes (codecs/q4.rs:58-65), which forces a lane-dependent multi-byte
 // gather per group.  The device header keeps d and dmin (bytes 0-3) and

@@ -25,6 +25,8 @@ size_t gguf_row_bytes(int type, size_t K) {
     case kQ8_0: return K / 32 * 34;
     case kQ4_K: return K / 256 * 144;
     case kF32: return K * 4;
+    case kQ4_1: return K / 32 * 20;
+    case kQ6_K: return K / 256 * 210;
     default: return 0;
     }
 }
@@ -87,6 +89,60 @@ __global__ void repack_q4k_kernel(const v4i* __restrict__ src, v4i* __restrict__
     for (int i = 0; i < 8; ++i) qs[b * 8 + i] = blk[1 + i];
 }
 
+// GGUF Q4_1 block (codecs/q4.rs:22-36): d f16, m f16, 16 nibble bytes.
+__global__ void repack_q41_kernel(const uint8_t* __restrict__ src, uint16_t* __restrict__ qs,
+                                  uint32_t* __restrict__ hdr, size_t N, size_t nb, int* bad) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N * nb) return;
+    const size_t row = i / nb, b = i % nb, nbc8 = (nb + 7) / 8;
+    const uint8_t* blk = src + i * 20;
+    const uint32_t d = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8);
+    const uint32_t m = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8);
+    if ((d & 0x7c00u) == 0x7c00u || (m & 0x7c00u) == 0x7c00u) atomicOr(bad, 1);
+    hdr[row * nbc8 * 8 + b] = d | (m << 16);
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = 4 * l + j;
+            const uint32_t nib = e < 16 ? (blk[4 + e] & 15u) : (uint32_t)(blk[4 + e - 16] >> 4);
+            word |= nib << (4 * j);
+        }
+        qs[q41_word_index(row, b, l, nbc8)] = (uint16_t)word;
+    }
+}
+
+// GGUF Q6_K superblock (codecs/q6.rs): ql[128], qh[64], int8 scales[16], d f16.
+__global__ void repack_q6k_kernel(const uint8_t* __restrict__ src, uint32_t* __restrict__ qs,
+                                  uint8_t* __restrict__ scales, float* __restrict__ dplane, size_t N, size_t K,
+                                  int* bad) {
+    const size_t nsb = K / 256;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N * nsb) return;
+    const size_t row = i / nsb, sb = i % nsb;
+    const uint8_t* blk = src + i * 210;
+    const uint16_t d = (uint16_t)(blk[208] | (blk[209] << 8));
+    if ((d & 0x7c00u) == 0x7c00u) atomicOr(bad, 1);
+    dplane[i] = f16_to_f32(d);
+    for (int t = 0; t < 16; ++t) scales[i * 16 + t] = blk[192 + t];
+    auto dw = [&](int at) {
+        return (uint32_t)blk[at] | ((uint32_t)blk[at + 1] << 8) | ((uint32_t)blk[at + 2] << 16) |
+               ((uint32_t)blk[at + 3] << 24);
+    };
+    uint32_t* pb = qs + q6k_b_offset(N, K);
+    for (int L = 0; L < 8; ++L) {
+        uint32_t* a = qs + q6k_a_index(row, sb, L, nsb);
+        a[0] = dw(4 * L);
+        a[1] = dw(32 + 4 * L);
+        a[2] = dw(64 + 4 * L);
+        a[3] = dw(96 + 4 * L);
+        uint32_t* h = pb + q6k_b_index(row, sb, L, nsb);
+        h[0] = dw(128 + 4 * L);
+        h[1] = dw(128 + 32 + 4 * L);
+    }
+}
+
 hipError_t repack_weight(const uint8_t* d_gguf, DeviceWeight& w, int* d_bad, hipStream_t s) {
     if (w.type == kQ8_0) {
         const size_t nb = w.K / 32, n = w.N * nb;
@@ -102,6 +158,21 @@ hipError_t repack_weight(const uint8_t* d_gguf, DeviceWeight& w, int* d_bad, hip
                            (v4u*)w.hdr, nb, d_bad);
     } else if (w.type == kF32) {
         return hipMemcpyAsync(w.qs, d_gguf, w.qs_bytes, hipMemcpyDeviceToDevice, s);
+    } else if (w.type == kQ4_1) {
+        const size_t nb = w.K / 32, n = w.N * nb;
+        hipError_t e = hipMemsetAsync(w.qs, 0, w.qs_bytes, s);
+        if (e == hipSuccess) e = hipMemsetAsync(w.hdr, 0, w.hdr_bytes, s);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(repack_q41_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, d_gguf,
+                           (uint16_t*)w.qs, (uint32_t*)w.hdr, w.N, nb, d_bad);
+    } else if (w.type == kQ6_K) {
+        const size_t n = w.N * (w.K / 256);
+        hipError_t e = hipMemsetAsync(w.qs, 0, w.qs_bytes, s);
+        if (e != hipSuccess) return e;
+        uint8_t* sc = (uint8_t*)w.hdr;
+        float* dp = (float*)(sc + w.N * (w.K / 256) * 16);
+        hipLaunchKernelGGL(repack_q6k_kernel, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, s, d_gguf,
+                           (uint32_t*)w.qs, sc, dp, w.N, w.K, d_bad);
     } else {
         return hipErrorInvalidValue;
     }
@@ -109,6 +180,20 @@ hipError_t repack_weight(const uint8_t* d_gguf, DeviceWeight& w, int* d_bad, hip
 }
 
 // ------------------------------------------------------------- dequantize
+
+__global__ void dequant_codec_kernel(int type, const void* __restrict__ qs, const void* __restrict__ hdr,
+                                     float* __restrict__ out, size_t row0, size_t rows, size_t N, size_t K) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * K) return;
+    const size_t row = row0 + i / K, e = i % K;
+    if (type == kQ4_1) {
+        out[i] = q41_element((const uint16_t*)qs, (const uint32_t*)hdr, row, e, K);
+    } else {
+        const uint8_t* sc = (const uint8_t*)hdr;
+        const float* d = (const float*)(sc + N * (K / 256) * 16);
+        out[i] = q6k_element((const uint32_t*)qs, sc, d, row, e, N, K);
+    }
+}
 
 __global__ void dequant_q8_0_kernel(const int8_t* __restrict__ qs, const uint16_t* __restrict__ hdr,
                                     float* __restrict__ out, size_t row0, size_t rows, size_t nb) {
@@ -154,6 +239,10 @@ hipError_t dequantize_rows(const DeviceWeight& w, size_t row0, size_t rows, floa
                            (const uint8_t*)w.qs + row0 * (w.K / 2), (const v4u*)w.hdr + row0 * bpr, out, nb);
     } else if (w.type == kF32) {
         return hipMemcpyAsync(out, (const float*)w.qs + row0 * w.K, rows * w.K * 4, hipMemcpyDeviceToDevice, s);
+    } else if (w.type == kQ4_1 || w.type == kQ6_K) {
+        const size_t n = rows * w.K;
+        hipLaunchKernelGGL(dequant_codec_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, w.type, w.qs,
+                           w.hdr, out, row0, rows, w.N, w.K);
     } else {
         return hipErrorInvalidValue;
     }
@@ -489,20 +578,6 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(const uint8_t* __restrict
     }
 }
 
-// ----------------------------------------------------------------- GEMV F32
-
-__global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__ w, const float* __restrict__ x,
-                                                       float* __restrict__ y, int N, int K) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const size_t m = blockIdx.y;
-    if (row >= N) return;
-    float acc = 0.0f;
-    for (int k = lane; k < K; k += 64) acc = fmaf(w[(size_t)row * K + k], x[m * K + k], acc);
-    acc = wave_sum_xor(acc, 64);
-    if (lane == 0) y[m * N + row] = acc;
-}
-
 // ------------------------------------------------------------- dispatch
 
 static int pick_lpr_log2(int nchunk, int target) {
@@ -524,7 +599,9 @@ bool gemv_supported(int type, size_t K, size_t M) {
     switch (type) {
     case kQ8_0: return K % 32 == 0 && K <= 8192;
     case kQ4_K: return K % 256 == 0 && K <= 16384;
-    case kF32: return K <= (1u << 20);
+    case kQ4_1: return K % 32 == 0 && K <= 8192;
+    case kQ6_K: return K % 256 == 0 && K <= 8192;
+    case kF32: return K % 4 == 0 && K <= 8192;
     default: return false;
     }
 }
@@ -583,8 +660,17 @@ hipError_t gemv(const DeviceWeight& w, size_t M, const void* prepared, float* y,
         }
 #undef ZG_Q4
     } else {
-        dim3 g((unsigned)((w.N + 3) / 4), (unsigned)M);
-        hipLaunchKernelGGL(gemv_f32_kernel, g, dim3(256), 0, s, (const float*)w.qs, xf, y, N, K);
+        // Q4_1, Q6_K and F32 over the f32 activation: the decode-step kernels
+        // with a plain prologue (activation coding in-kernel)
+        FusedGemvArgs f;
+        f.M = (int)M;
+        f.pro = PRO_PLAIN;
+        f.epi = EPI_STORE;
+        f.x = xf;
+        f.ldx = w.K;
+        f.y = y;
+        f.ldy = w.N;
+        return fused_gemv(w, f, s);
     }
     return hipGetLastError();
 }

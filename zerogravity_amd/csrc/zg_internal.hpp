@@ -6,7 +6,7 @@
 
 namespace zg {
 
-enum GgmlType { kF32 = 0, kF16 = 1, kQ8_0 = 8, kQ4_K = 12, kBF16 = 30 };
+enum GgmlType { kF32 = 0, kF16 = 1, kQ4_1 = 3, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14, kBF16 = 30 };
 
 // A registered weight matrix in its device layout.  The GGUF block stream is
 // split once at registration into a streaming payload and a small per-block
@@ -15,6 +15,10 @@ enum GgmlType { kF32 = 0, kF16 = 1, kQ8_0 = 8, kQ4_K = 12, kBF16 = 30 };
 //   Q4_K: qs  = nibbles [N][K/2]       hdr = 16-byte block header [N][K/256]
 //         (d, dmin, 12 packed 6-bit scale/min bytes, unchanged)
 //   F32 : qs  = float [N][K]           hdr = null
+//   Q4_1: qs  = nibble words in 8-row tiles (q41_word_index)
+//         hdr = uint32 d | m << 16 [N][K/32 rounded to 8 blocks]
+//   Q6_K: qs  = bit planes A and B in 8-row tiles (q6k_a_index, q6k_b_index)
+//         hdr = int8 local scales [N][K/256][16], then f32 d [N][K/256]
 // Algorithmic bytes are unchanged: 1.0625 B/elem (Q8_0), 0.5625 (Q4_K).
 struct DeviceWeight {
     int type = -1;

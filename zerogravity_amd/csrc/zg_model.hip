@@ -190,6 +190,31 @@ __global__ void fill_u32_kernel(uint32_t* __restrict__ p, size_t n, uint32_t v) 
 
 static unsigned blocks_for(size_t n, unsigned t = 256) { return (unsigned)((n + t - 1) / t); }
 
+// Q4_1 / Q6_K token rows decoded from the device layouts (exact, as the
+// reference's block decoders).
+__global__ void embed_codec_kernel(int type, const void* __restrict__ qs, const void* __restrict__ hdr,
+                                   const uint32_t* __restrict__ tokens, float* __restrict__ x, int K, int V,
+                                   int* __restrict__ status) {
+    const int b = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= K) return;
+    const uint32_t t = tokens[b];
+    if (t >= (uint32_t)V) {
+        if (i == 0) atomicOr(status, 2);
+        x[(size_t)b * K + i] = 0.0f;
+        return;
+    }
+    float v;
+    if (type == kQ4_1) {
+        v = q41_element((const uint16_t*)qs, (const uint32_t*)hdr, t, (size_t)i, (size_t)K);
+    } else {
+        const uint8_t* sc = (const uint8_t*)hdr;
+        const float* d = (const float*)(sc + (size_t)V * (K / 256) * 16);
+        v = q6k_element((const uint32_t*)qs, sc, d, t, (size_t)i, (size_t)V, (size_t)K);
+    }
+    x[(size_t)b * K + i] = v;
+}
+
 hipError_t embed(const DeviceWeight& w, const uint32_t* tokens, float* x, size_t B, int* status, hipStream_t s) {
     dim3 g(blocks_for(w.K), (unsigned)B);
     if (w.type == kQ8_0)
@@ -198,6 +223,9 @@ hipError_t embed(const DeviceWeight& w, const uint32_t* tokens, float* x, size_t
     else if (w.type == kQ4_K)
         hipLaunchKernelGGL(embed_q4k_kernel, g, dim3(256), 0, s, (const uint8_t*)w.qs, (const v4u*)w.hdr, tokens, x,
                            (int)w.K, (int)w.N, status);
+    else if (w.type == kQ4_1 || w.type == kQ6_K)
+        hipLaunchKernelGGL(embed_codec_kernel, g, dim3(256), 0, s, w.type, w.qs, w.hdr, tokens, x, (int)w.K, (int)w.N,
+                           status);
     else
         hipLaunchKernelGGL(embed_f32_kernel, g, dim3(256), 0, s, (const float*)w.qs, tokens, x, (int)w.K, (int)w.N,
                            status);

@@ -26,9 +26,25 @@ using namespace zgc;
 
 namespace {
 
+// Matrices that share an input are stacked by rows into one launch; where
+// their codecs differ the stack splits into runs of one codec, each written
+// at its column offset of the shared output row.
+struct Part {
+    zg_weight* w = nullptr;
+    uint64_t col = 0;
+};
+using Stack = std::vector<Part>;
+
+bool all_type(const Stack& st, int type) {
+    for (const Part& p : st)
+        if (!p.w || p.w->dw.type != type) return false;
+    return !st.empty();
+}
+
 struct LayerW {
     bool full = false;
-    zg_weight *in_proj = nullptr, *out_proj = nullptr, *ffn_gu = nullptr, *ffn_down = nullptr;
+    Stack in_proj, ffn_gu;
+    zg_weight *out_proj = nullptr, *ffn_down = nullptr;
     float *attn_norm = nullptr, *post_norm = nullptr, *conv_w = nullptr, *ssm_norm = nullptr, *ssm_a = nullptr,
           *ssm_dt = nullptr, *q_norm = nullptr, *k_norm = nullptr;
 };
@@ -44,6 +60,7 @@ struct zg_model {
     float* out_norm = nullptr;
     std::vector<void*> vecs;  // device copies of F32 parameter vectors
     size_t n_gdn = 0, n_attn = 0;
+    bool all_q4k = true;  // every projection Q4_K: batched split-K residuals allowed
 };
 
 struct zg_session {
@@ -84,13 +101,11 @@ const zg_tensor_desc* find_tensor(const zg_tensor_desc* t, size_t n, const std::
 
 std::string lname(unsigned i, const char* suffix) { return "blk." + std::to_string(i) + "." + suffix; }
 
-// Rows of several [K, N_i] GGUF matrices stacked into one registered weight.
-int load_stacked(zg_model* m, const zg_tensor_desc* ts, size_t n, const std::vector<std::string>& names, uint64_t K,
-                 const std::vector<uint64_t>& Ns, const std::string& key, int pro, zg_weight** out) {
+// Rows of several [K, N_i] GGUF matrices stacked into registered weights:
+// one per run of consecutive matrices sharing a codec, at its column offset.
+int load_stack(zg_model* m, const zg_tensor_desc* ts, size_t n, const std::vector<std::string>& names, uint64_t K,
+               const std::vector<uint64_t>& Ns, const std::string& key, int pro, Stack* out) {
     zg_ctx* ctx = m->ctx;
-    int type = -1;
-    uint64_t rows = 0;
-    size_t bytes = 0;
     std::vector<const zg_tensor_desc*> parts;
     for (size_t i = 0; i < names.size(); ++i) {
         const zg_tensor_desc* t = find_tensor(ts, n, names[i]);
@@ -100,24 +115,52 @@ int load_stacked(zg_model* m, const zg_tensor_desc* ts, size_t n, const std::vec
         int rc = check_matrix(ctx, t->ggml_type, K, Ns[i], t->data, t->nbytes);
         if (rc == ZG_UNSUPPORTED) return fail(ctx, ZG_E_UNSUPPORTED, "tensor " + names[i] + ": " + ctx->err);
         if (rc) return rc;
-        if (type >= 0 && t->ggml_type != type)
-            return fail(ctx, ZG_E_UNSUPPORTED, "tensors stacked with " + names[0] + " must share its codec");
-        type = t->ggml_type;
-        rows += Ns[i];
-        bytes += t->nbytes;
+        if (!zg::fused_gemv_supported(t->ggml_type, K, Ns[i], pro))
+            return fail(ctx, ZG_E_UNSUPPORTED, "resident decode has no projection kernel for " + names[i]);
         parts.push_back(t);
     }
-    if (!zg::fused_gemv_supported(type, K, rows, pro))
-        return fail(ctx, ZG_E_UNSUPPORTED, "resident decode needs Q8_0/Q4_K projections (" + names[0] + ")");
-    if (parts.size() == 1)
-        return lookup_or_register(ctx, m->source, key.c_str(), type, K, rows, parts[0]->data, parts[0]->nbytes, out);
-    std::vector<uint8_t> buf(bytes);
-    size_t at = 0;
-    for (const zg_tensor_desc* t : parts) {
-        memcpy(buf.data() + at, t->data, t->nbytes);
-        at += t->nbytes;
+    out->clear();
+    uint64_t col = 0;
+    for (size_t i = 0, run = 0; i < parts.size(); ++run) {
+        size_t j = i;
+        uint64_t rows = 0;
+        size_t bytes = 0;
+        while (j < parts.size() && parts[j]->ggml_type == parts[i]->ggml_type) {
+            rows += Ns[j];
+            bytes += parts[j]->nbytes;
+            ++j;
+        }
+        const int type = parts[i]->ggml_type;
+        if (type != ZG_Q4_K) m->all_q4k = false;
+        const std::string k = run == 0 ? key : key + "." + std::to_string(run);
+        Part p;
+        p.col = col;
+        int rc;
+        if (j == i + 1) {
+            rc = lookup_or_register(ctx, m->source, k.c_str(), type, K, rows, parts[i]->data, parts[i]->nbytes, &p.w);
+        } else {
+            std::vector<uint8_t> buf(bytes);
+            size_t at = 0;
+            for (size_t q = i; q < j; ++q) {
+                memcpy(buf.data() + at, parts[q]->data, parts[q]->nbytes);
+                at += parts[q]->nbytes;
+            }
+            rc = lookup_or_register(ctx, m->source, k.c_str(), type, K, rows, buf.data(), bytes, &p.w);
+        }
+        if (rc) return rc;
+        out->push_back(p);
+        col += rows;
+        i = j;
     }
-    return lookup_or_register(ctx, m->source, key.c_str(), type, K, rows, buf.data(), bytes, out);
+    return ZG_COMPLETED;
+}
+
+int load_single(zg_model* m, const zg_tensor_desc* ts, size_t n, const std::string& name, uint64_t K, uint64_t N,
+                int pro, zg_weight** out) {
+    Stack st;
+    int rc = load_stack(m, ts, n, {name}, K, {N}, name, pro, &st);
+    if (!rc) *out = st[0].w;
+    return rc;
 }
 
 int load_vector(zg_model* m, const zg_tensor_desc* ts, size_t n, const std::string& name, uint64_t len, float** out) {
@@ -193,7 +236,7 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
                 f.xw = s->x;
                 pending = 0;
             }
-            if (epi == zg::EPI_RESID && y == s->x) {
+            if (epi == zg::EPI_RESID && y == s->x && m->all_q4k) {
                 const int sp = zg::batched_splits(w->dw.N, w->dw.K);
                 if (sp > 1) {
                     f.parts = s->parts;
@@ -209,7 +252,8 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
     for (size_t i = 0; i < m->layers.size(); ++i) {
         LayerW& L = m->layers[i];
         const int slot = s->layer_slot[i];
-        ZG_HIP(gemv(L.in_proj, zg::PRO_RMS, s->x, H, nullptr, 0, L.attn_norm, zg::EPI_STORE, s->y0, s->y0w));
+        for (const Part& p : L.in_proj)
+            ZG_HIP(gemv(p.w, zg::PRO_RMS, s->x, H, nullptr, 0, L.attn_norm, zg::EPI_STORE, s->y0 + p.col, s->y0w));
         if (!L.full) {
             zg::GdnDecodeArgs d;
             d.proj = s->y0;
@@ -255,18 +299,19 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             ZG_HIP(zg::attn_decode(a, B, st));
             ZG_HIP(gemv(L.out_proj, zg::PRO_PLAIN, s->ao, QD, nullptr, 0, nullptr, zg::EPI_RESID, s->x, H));
         }
-        const zg::DeviceWeight& gu = L.ffn_gu->dw;
-        const bool glu = L.ffn_down->dw.type == zg::kQ4_K &&
+        const zg::DeviceWeight& gu = L.ffn_gu[0].w->dw;
+        const bool glu = L.ffn_gu.size() == 1 && L.ffn_down->dw.type == zg::kQ4_K &&
                          (B > 4 ? zg::batched_glu_supported(gu.type, gu.K, gu.N) : zg::fused_glu_supported(gu.type, gu.K, gu.N));
         if (glu) {
             // SwiGLU in the gate/up epilogue: the down projection takes the
             // product as a plain activation (f16 tiles when batched)
-            ZG_HIP(gemv(L.ffn_gu, zg::PRO_RMS, s->x, H, nullptr, 0, L.post_norm, zg::EPI_GLU, s->y0, s->y0w,
+            ZG_HIP(gemv(L.ffn_gu[0].w, zg::PRO_RMS, s->x, H, nullptr, 0, L.post_norm, zg::EPI_GLU, s->y0, s->y0w,
                         B > 4 ? s->xh2 : nullptr));
             ZG_HIP(gemv(L.ffn_down, zg::PRO_PLAIN, s->y0, s->y0w, nullptr, 0, nullptr, zg::EPI_RESID, s->x, H, nullptr,
                         B > 4 ? s->xh2 : nullptr));
         } else {
-            ZG_HIP(gemv(L.ffn_gu, zg::PRO_RMS, s->x, H, nullptr, 0, L.post_norm, zg::EPI_STORE, s->y0, s->y0w));
+            for (const Part& p : L.ffn_gu)
+                ZG_HIP(gemv(p.w, zg::PRO_RMS, s->x, H, nullptr, 0, L.post_norm, zg::EPI_STORE, s->y0 + p.col, s->y0w));
             ZG_HIP(gemv(L.ffn_down, zg::PRO_SILU_MUL, s->y0, s->y0w, s->y0 + F, s->y0w, nullptr, zg::EPI_RESID, s->x,
                         H));
         }
@@ -383,7 +428,7 @@ int zg_model_load(zg_ctx* ctx, uint64_t source_id, const zg_geometry* g, const z
     m->g = *g;
     const uint64_t H = g->hidden, F = g->ffn, V = g->vocab, W = (uint64_t)g->gdn_heads * g->gdn_dim;
     const uint64_t QD = (uint64_t)g->q_heads * g->head_dim, KD = (uint64_t)g->kv_heads * g->head_dim;
-    int rc = load_stacked(m, tensors, n, {"token_embd.weight"}, H, {V}, "token_embd.weight", zg::PRO_RMS, &m->embd);
+    int rc = load_single(m, tensors, n, "token_embd.weight", H, V, zg::PRO_RMS, &m->embd);
     if (!rc) rc = load_vector(m, tensors, n, "output_norm.weight", H, &m->out_norm);
     m->layers.resize(g->layers);
     for (unsigned i = 0; i < g->layers && !rc; ++i) {
@@ -393,30 +438,26 @@ int zg_model_load(zg_ctx* ctx, uint64_t source_id, const zg_geometry* g, const z
         rc = load_vector(m, tensors, n, lname(i, "attn_norm.weight"), H, &L.attn_norm);
         if (!rc) rc = load_vector(m, tensors, n, lname(i, "post_attention_norm.weight"), H, &L.post_norm);
         if (!rc)
-            rc = load_stacked(m, tensors, n, {lname(i, "ffn_gate.weight"), lname(i, "ffn_up.weight")}, H, {F, F},
-                              lname(i, "ffn_gate_up"), zg::PRO_RMS, &L.ffn_gu);
+            rc = load_stack(m, tensors, n, {lname(i, "ffn_gate.weight"), lname(i, "ffn_up.weight")}, H, {F, F},
+                            lname(i, "ffn_gate_up"), zg::PRO_RMS, &L.ffn_gu);
         if (!rc)
-            rc = load_stacked(m, tensors, n, {lname(i, "ffn_down.weight")}, F, {H}, lname(i, "ffn_down.weight"),
-                              zg::PRO_SILU_MUL, &L.ffn_down);
+            rc = load_single(m, tensors, n, lname(i, "ffn_down.weight"), F, H, zg::PRO_SILU_MUL, &L.ffn_down);
         if (rc) break;
         if (L.full) {
-            rc = load_stacked(m, tensors, n,
-                              {lname(i, "attn_q.weight"), lname(i, "attn_k.weight"), lname(i, "attn_v.weight")}, H,
-                              {2 * QD, KD, KD}, lname(i, "attn_qkv_in"), zg::PRO_RMS, &L.in_proj);
+            rc = load_stack(m, tensors, n,
+                            {lname(i, "attn_q.weight"), lname(i, "attn_k.weight"), lname(i, "attn_v.weight")}, H,
+                            {2 * QD, KD, KD}, lname(i, "attn_qkv_in"), zg::PRO_RMS, &L.in_proj);
             if (!rc)
-                rc = load_stacked(m, tensors, n, {lname(i, "attn_output.weight")}, QD, {H},
-                                  lname(i, "attn_output.weight"), zg::PRO_PLAIN, &L.out_proj);
+                rc = load_single(m, tensors, n, lname(i, "attn_output.weight"), QD, H, zg::PRO_PLAIN, &L.out_proj);
             if (!rc) rc = load_vector(m, tensors, n, lname(i, "attn_q_norm.weight"), g->head_dim, &L.q_norm);
             if (!rc) rc = load_vector(m, tensors, n, lname(i, "attn_k_norm.weight"), g->head_dim, &L.k_norm);
             m->n_attn++;
         } else {
-            rc = load_stacked(m, tensors, n,
-                              {lname(i, "attn_qkv.weight"), lname(i, "attn_gate.weight"), lname(i, "ssm_alpha.weight"),
-                               lname(i, "ssm_beta.weight")},
-                              H, {3 * W, W, g->gdn_heads, g->gdn_heads}, lname(i, "gdn_in"), zg::PRO_RMS, &L.in_proj);
-            if (!rc)
-                rc = load_stacked(m, tensors, n, {lname(i, "ssm_out.weight")}, W, {H}, lname(i, "ssm_out.weight"),
-                                  zg::PRO_GATED, &L.out_proj);
+            rc = load_stack(m, tensors, n,
+                            {lname(i, "attn_qkv.weight"), lname(i, "attn_gate.weight"), lname(i, "ssm_alpha.weight"),
+                             lname(i, "ssm_beta.weight")},
+                            H, {3 * W, W, g->gdn_heads, g->gdn_heads}, lname(i, "gdn_in"), zg::PRO_RMS, &L.in_proj);
+            if (!rc) rc = load_single(m, tensors, n, lname(i, "ssm_out.weight"), W, H, zg::PRO_GATED, &L.out_proj);
             if (!rc) rc = load_vector(m, tensors, n, lname(i, "ssm_conv1d.weight"), 4 * 3 * W, &L.conv_w);
             if (!rc) rc = load_vector(m, tensors, n, lname(i, "ssm_norm.weight"), g->gdn_dim, &L.ssm_norm);
             if (!rc) rc = load_vector(m, tensors, n, lname(i, "ssm_a"), g->gdn_heads, &L.ssm_a);
@@ -456,7 +497,11 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     if (max_batch > 4) {
         // the batched-row path reads Q4_K weights in MFMA tile order
         std::vector<zg_weight*> ws = {m->embd};
-        for (auto& L : m->layers) ws.insert(ws.end(), {L.in_proj, L.out_proj, L.ffn_gu, L.ffn_down});
+        for (auto& L : m->layers) {
+            ws.insert(ws.end(), {L.out_proj, L.ffn_down});
+            for (const Part& p : L.in_proj) ws.push_back(p.w);
+            for (const Part& p : L.ffn_gu) ws.push_back(p.w);
+        }
         for (zg_weight* w : ws)
             if (w && w->dw.type == zg::kQ4_K && !w->dw.qs_t) {
                 const hipError_t e = zg::ensure_mfma_tiles(w->dw, ctx->stream);
@@ -688,7 +733,11 @@ int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* toke
         g.q_heads / g.kv_heads > 4)
         return fail(ctx, ZG_E_UNSUPPORTED, "batched prefill geometry not supported: use zg_prefill");
     std::vector<zg_weight*> ws;
-    for (auto& L : m->layers) ws.insert(ws.end(), {L.in_proj, L.out_proj, L.ffn_gu, L.ffn_down});
+    for (auto& L : m->layers) {
+        if (L.in_proj.size() != 1 || L.ffn_gu.size() != 1)
+            return fail(ctx, ZG_E_UNSUPPORTED, "batched prefill needs Q4_K projections: use zg_prefill");
+        ws.insert(ws.end(), {L.in_proj[0].w, L.out_proj, L.ffn_gu[0].w, L.ffn_down});
+    }
     for (zg_weight* w : ws)
         if (!w || w->dw.type != zg::kQ4_K)
             return fail(ctx, ZG_E_UNSUPPORTED, "batched prefill needs Q4_K projections: use zg_prefill");
@@ -747,7 +796,7 @@ int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* toke
         LayerW& L = m->layers[i];
         const int slot = s->layer_slot[i];
         if (!L.full) {
-            ZG_HIP(gemm(L.in_proj, zg::PRO_RMS, x, H, nullptr, 0, L.attn_norm, zg::EPI_STORE, pj, ldp));
+            ZG_HIP(gemm(L.in_proj[0].w, zg::PRO_RMS, x, H, nullptr, 0, L.attn_norm, zg::EPI_STORE, pj, ldp));
             float* ring = s->ring[slot] + row * 3 * W * 4;
             float* state = s->rec[slot] + row * GH * g.gdn_dim * g.gdn_dim;
             ZG_HIP(zg::gdn_prefill_conv(pj, ldp, n, W, GH, L.conv_w, ring, pos0, L.ssm_dt, L.ssm_a, (float*)s->pf[Q],
@@ -759,7 +808,7 @@ int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* toke
             ZG_HIP(gemm(L.out_proj, zg::PRO_GATED, (const float*)s->pf[CORE], W, pj + 3 * W, ldp, L.ssm_norm,
                         zg::EPI_RESID, x, H));
         } else {
-            ZG_HIP(gemm(L.in_proj, zg::PRO_RMS, x, H, nullptr, 0, L.attn_norm, zg::EPI_STORE, pj, ldp));
+            ZG_HIP(gemm(L.in_proj[0].w, zg::PRO_RMS, x, H, nullptr, 0, L.attn_norm, zg::EPI_STORE, pj, ldp));
             zg::AttnPrefillArgs a;
             a.P = pj;
             a.ldp = ldp;
@@ -782,13 +831,13 @@ int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* toke
             ZG_HIP(gemm(L.out_proj, zg::PRO_PLAIN, (const float*)s->pf[OB], QD, nullptr, 0, nullptr, zg::EPI_RESID, x,
                         H));
         }
-        const zg::DeviceWeight& gu = L.ffn_gu->dw;
+        const zg::DeviceWeight& gu = L.ffn_gu[0].w->dw;
         if (zg::batched_glu_supported(gu.type, gu.K, gu.N)) {
-            ZG_HIP(gemm(L.ffn_gu, zg::PRO_RMS, x, H, nullptr, 0, L.post_norm, zg::EPI_GLU, pj, ldp, s->pf[XH2]));
+            ZG_HIP(gemm(L.ffn_gu[0].w, zg::PRO_RMS, x, H, nullptr, 0, L.post_norm, zg::EPI_GLU, pj, ldp, s->pf[XH2]));
             ZG_HIP(gemm(L.ffn_down, zg::PRO_PLAIN, pj, ldp, nullptr, 0, nullptr, zg::EPI_RESID, x, H, nullptr,
                         s->pf[XH2]));
         } else {
-            ZG_HIP(gemm(L.ffn_gu, zg::PRO_RMS, x, H, nullptr, 0, L.post_norm, zg::EPI_STORE, pj, ldp));
+            ZG_HIP(gemm(L.ffn_gu[0].w, zg::PRO_RMS, x, H, nullptr, 0, L.post_norm, zg::EPI_STORE, pj, ldp));
             ZG_HIP(gemm(L.ffn_down, zg::PRO_SILU_MUL, pj, ldp, pj + F, ldp, nullptr, zg::EPI_RESID, x, H));
         }
     }

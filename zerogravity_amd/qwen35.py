@@ -86,10 +86,19 @@ def geometry_from_config(cfg, gdn_dim=128):
     return g
 
 
-def synthetic_tensors(g, kind, seed):
+# A mixed-codec table in the manner of the published mixed-quant
+# checkpoints: Q6_K for the embedding, value and down projections, F32 for
+# the small GDN alpha/beta projections (the F32 ssm_alpha projection named
+# at cpu/src/source.rs:316-323), Q4_1 for the output gate.  Suffix -> codec;
+# everything else keeps `kind`.
+MIXED = {"token_embd.weight": gguf.Q6_K, "attn_v.weight": gguf.Q6_K, "ffn_down.weight": gguf.Q6_K,
+         "ssm_alpha.weight": gguf.F32, "ssm_beta.weight": gguf.F32, "attn_gate.weight": gguf.Q4_1}
+
+
+def synthetic_tensors(g, kind, seed, kinds=None):
     """Seeded random-init tensor table {name: (ggml_type, shape0, shape1, uint8 bytes)}.
 
-    Matrices use `kind` (Q8_0 or Q4_K) with row norms ~1 so activations stay
+    Matrices use `kind` (or kinds[suffix] when given, e.g. MIXED) with row norms ~1 so activations stay
     O(1) through the 24 layers; norms gamma ~ N(1, 0.1); ssm_a = -exp(N(0,0.5));
     ssm_dt ~ N(0, 1); conv taps ~ N(0, 0.5).  Shapes per
     model-qwen35/src/source/binding.rs:43-91 (GGML order [K, N]).
@@ -101,7 +110,10 @@ def synthetic_tensors(g, kind, seed):
     t = {}
 
     def mat(name, K, N):
-        t[name] = (kind, K, N, synth.random_matrix(rng, kind, N, K).reshape(-1))
+        k = kind
+        if kinds:
+            k = kinds.get(name.split(".", 2)[-1] if name.startswith("blk.") else name, kind)
+        t[name] = (k, K, N, synth.random_matrix(rng, k, N, K).reshape(-1))
 
     def vec(name, values):
         a = np.ascontiguousarray(values, np.float32)

@@ -2,11 +2,13 @@
 
 Block layouts follow ggml: Q8_0 = [f16 d][32 x i8] (34 B, core/src/encoding.rs:59);
 Q4_K = [f16 d][f16 dmin][12 B packed 6-bit scales/mins][128 B nibbles]
-(144 B, encoding.rs:60; unpack rule artifacts/src/codecs/q4.rs:39-70).
+(144 B, encoding.rs:60; unpack rule artifacts/src/codecs/q4.rs:39-70);
+Q4_1 = [f16 d][f16 m][16 B nibbles] (20 B); Q6_K = [128 B low nibbles][64 B
+high 2-bit pairs][16 x i8 scales][f16 d] (210 B, codecs/q6.rs).
 """
 import numpy as np
 
-Q8_0, Q4_K, F32 = 8, 12, 0
+Q8_0, Q4_K, F32, Q4_1, Q6_K = 8, 12, 0, 3, 14
 
 
 def _f16_bytes(values):
@@ -46,11 +48,42 @@ def random_q4_k(rng, rows, cols, d_scale=None):
     return out.reshape(rows, -1)
 
 
+def random_q4_1(rng, rows, cols):
+    """[rows, cols/32*20] uint8: random nibbles, d sized so outputs are
+    O(|x|), m = -7.5 d (zero-mean weights) with a little jitter."""
+    assert cols % 32 == 0
+    nb = rows * (cols // 32)
+    d = (1.7 / (4.6 * np.sqrt(cols)) * rng.uniform(0.5, 1.5, nb)).astype(np.float32)
+    m = (-7.5 * d * rng.uniform(0.9, 1.1, nb)).astype(np.float32)
+    out = np.empty((nb, 20), np.uint8)
+    out[:, 0:2] = _f16_bytes(d).reshape(nb, 2)
+    out[:, 2:4] = _f16_bytes(m).reshape(nb, 2)
+    out[:, 4:] = rng.integers(0, 256, size=(nb, 16), dtype=np.uint8)
+    return out.reshape(rows, -1)
+
+
+def random_q6_k(rng, rows, cols):
+    """[rows, cols/256*210] uint8: random 6-bit codes, signed local scales in
+    [-63, 63], d sized so outputs are O(|x|)."""
+    assert cols % 256 == 0
+    nb = rows * (cols // 256)
+    out = np.empty((nb, 210), np.uint8)
+    out[:, :192] = rng.integers(0, 256, size=(nb, 192), dtype=np.uint8)
+    out[:, 192:208] = rng.integers(-63, 64, size=(nb, 16), dtype=np.int8).view(np.uint8)
+    d = (1.0 / (18.5 * 36.0 * np.sqrt(cols)) * rng.uniform(0.5, 1.5, nb)).astype(np.float32)
+    out[:, 208:210] = _f16_bytes(d).reshape(nb, 2)
+    return out.reshape(rows, -1)
+
+
 def random_matrix(rng, kind, rows, cols):
     if kind == Q8_0:
         return random_q8_0(rng, rows, cols)
     if kind == Q4_K:
         return random_q4_k(rng, rows, cols)
+    if kind == Q4_1:
+        return random_q4_1(rng, rows, cols)
+    if kind == Q6_K:
+        return random_q6_k(rng, rows, cols)
     if kind == F32:
         return (rng.standard_normal((rows, cols)) / np.sqrt(cols)).astype(np.float32).view(np.uint8).reshape(rows, -1)
     raise ValueError(kind)
