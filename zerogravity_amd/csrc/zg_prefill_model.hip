@@ -152,70 +152,132 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(const float* __r
     }
 }
 
-// Grid (n, nkv), 64 * G threads: wave g is query head kvh*G + g of token t
-// over the keys 0 .. pos0 + t (causal).  Lane l holds dimensions 4l..4l+3;
-// keys and values stream in blocks of 16 with an online softmax (block max,
-// rescale), then o / l * sigmoid(gate) (forward.rs:751).
+typedef _Float16 ah4 __attribute__((ext_vector_type(4)));
+typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
+typedef float af16 __attribute__((ext_vector_type(16)));
+
+// Causal attention of 32 prompt tokens per workgroup on f16 MFMA.  Grid
+// (ceil(n/32), nkv), 64 * G threads: wave g is query head kvh*G + g for
+// tokens t0 .. t0+31, all G waves sharing each 32-key block of the KV head
+// staged in LDS (K row-major, V transposed, both rounded to f16).
+// v_mfma_f32_32x32x16_f16 lanes: A[m = l%32][k = 8(l/32) + e],
+// B[k = 8(l/32) + e][n = l%32], C register r = row (r%4) + 8(r/4) + 4(l/32),
+// column l%32.  Scores are formed transposed, S^T = K Q^T (query = column),
+// so each lane owns one query: the online softmax (block maximum, rescale,
+// forward.rs:700-751 semantics in another summation order) needs only the
+// partner lane l^32, and the probabilities are already the B operand of
+// O^T += V^T P^T when MFMA step s, half h, element e is taken to be key
+// 16s + (e%4) + 8(e/4) + 4h of the block (any fixed key order contracts to
+// the same sum).  q carries the 1/sqrt(d) scale before rounding to f16.
 template <typename KV, int G>
-__global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __restrict__ Q, const KV* __restrict__ kc,
-                                                              const KV* __restrict__ vc, int nq, int nkv, int pos0,
-                                                              float scale, const float* __restrict__ P, size_t ldp,
-                                                              float* __restrict__ out) {
-    constexpr int D = 256, KB = 16;
-    const int t = blockIdx.x, kvh = blockIdx.y, g = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int h = kvh * G + g;
-    const int T = pos0 + t + 1;
-    const v4f qv = *(const v4f*)(Q + ((size_t)t * nq + h) * D + 4 * lane);
-    const size_t kstep = (size_t)nkv * D;
-    const KV* kb = kc + (size_t)kvh * D + 4 * lane;
-    const KV* vb = vc + (size_t)kvh * D + 4 * lane;
-    float m = -INFINITY, l = 0.0f;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j0 = 0; j0 < T; j0 += KB) {
-        float kk[KB][4], vv[KB][4];
+__global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* __restrict__ Q,
+                                                                   const KV* __restrict__ kc,
+                                                                   const KV* __restrict__ vc, int n, int nq,
+                                                                   int nkv, int pos0, float scale,
+                                                                   const float* __restrict__ P, size_t ldp,
+                                                                   float* __restrict__ out) {
+    constexpr int QT = 32, KB = 32, D = 256;
+    constexpr int KROW = D + 8;   // halves per staged key row (16-byte pad)
+    constexpr int VROW = KB + 8;  // halves per staged value column
+    __shared__ _Float16 ks[KB * KROW];
+    __shared__ _Float16 vt[D * VROW];
+    const int kvh = blockIdx.y, g = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int h = kvh * G + g, t0 = blockIdx.x * QT;
+    const int hs = lane >> 5, c = lane & 31;
+    const int tq = min(t0 + c, n - 1);
+    ah8 qf[16];
+    {
+        const float* qrow = Q + ((size_t)tq * nq + h) * D + 8 * hs;
 #pragma unroll
-        for (int j = 0; j < KB; ++j) {
-            const int jj = min(j0 + j, T - 1);
-            kv_load4(kb + (size_t)jj * kstep, kk[j]);
-            kv_load4(vb + (size_t)jj * kstep, vv[j]);
+        for (int k = 0; k < 16; ++k) {
+            const v4f a = *(const v4f*)(qrow + 16 * k), b = *(const v4f*)(qrow + 16 * k + 4);
+            qf[k] = ah8{(_Float16)(a.x * scale), (_Float16)(a.y * scale), (_Float16)(a.z * scale),
+                        (_Float16)(a.w * scale), (_Float16)(b.x * scale), (_Float16)(b.y * scale),
+                        (_Float16)(b.z * scale), (_Float16)(b.w * scale)};
         }
-        float sc[KB];
-#pragma unroll
-        for (int j = 0; j < KB; ++j) {
-            float d = qv.x * kk[j][0];
-            d = fmaf(qv.y, kk[j][1], d);
-            d = fmaf(qv.z, kk[j][2], d);
-            d = fmaf(qv.w, kk[j][3], d);
-            sc[j] = d;
-        }
-#pragma unroll
-        for (int j = 0; j < KB; ++j) {
-            const float tot = group_sum_last<64>(sc[j]);
-            sc[j] = __shfl(tot, 63, 64) * scale;
-            if (j0 + j >= T) sc[j] = -INFINITY;
-        }
-        float bm = m;
-#pragma unroll
-        for (int j = 0; j < KB; ++j) bm = fmaxf(bm, sc[j]);
-        const float corr = __expf(m - bm);
-        l *= corr;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] *= corr;
-#pragma unroll
-        for (int j = 0; j < KB; ++j) {
-            const float pj = __expf(sc[j] - bm);
-            l += pj;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = fmaf(pj, vv[j][e], acc[e]);
-        }
-        m = bm;
     }
-    const float inv = 1.0f / l;
-    const float* gate = P + (size_t)t * ldp + (size_t)h * 2 * D + D + 4 * lane;
-    v4f o;
+    af16 o[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = acc[e] * inv * source_sigmoid(gate[e]);
-    *(v4f*)(out + ((size_t)t * nq + h) * D + 4 * lane) = o;
+    for (int d = 0; d < 8; ++d) o[d] = af16{};
+    float m = -INFINITY, l = 0.0f;
+    const bool qvalid = t0 + c < n;
+    const int tabs = pos0 + t0 + c;
+    const int kend = pos0 + min(t0 + QT, n);  // keys 0 .. kend-1 are seen by some query of the tile
+    const int nblk = (kend + KB - 1) / KB;
+    const size_t kstep = (size_t)nkv * D;
+    const KV* kb_ = kc + (size_t)kvh * D;
+    const KV* vb_ = vc + (size_t)kvh * D;
+    for (int b = 0; b < nblk; ++b) {
+        const int j0 = b * KB;
+        __syncthreads();  // the previous block's tiles are consumed
+        for (int idx = threadIdx.x; idx < KB * D / 4; idx += 64 * G) {
+            const int key = idx / (D / 4), d4 = (idx % (D / 4)) * 4;
+            const int j = min(j0 + key, kend - 1);  // past the last key: a copy, masked below
+            float kv4[4], vv4[4];
+            kv_load4(kb_ + (size_t)j * kstep + d4, kv4);
+            kv_load4(vb_ + (size_t)j * kstep + d4, vv4);
+            *(ah4*)(ks + key * KROW + d4) = ah4{(_Float16)kv4[0], (_Float16)kv4[1], (_Float16)kv4[2], (_Float16)kv4[3]};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vt[(d4 + i) * VROW + key] = (_Float16)vv4[i];
+        }
+        __syncthreads();
+        af16 sc = af16{};
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const ah8 ka = *(const ah8*)(ks + c * KROW + 16 * k + 8 * hs);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qf[k], sc, 0, 0, 0);
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = j0 + (r & 3) + 8 * (r >> 2) + 4 * hs;
+            if (!qvalid || key > tabs) sc[r] = -INFINITY;
+            bm = fmaxf(bm, sc[r]);
+        }
+        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+        const float mn = fmaxf(m, bm);
+        const bool none = mn == -INFINITY;
+        const float corr = none ? 1.0f : __expf(m - mn);
+        float ps = 0.0f;
+        ah8 pb[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float p = none ? 0.0f : __expf(sc[r] - mn);
+            ps += p;
+            pb[r >> 3][r & 7] = (_Float16)p;
+        }
+        ps += __shfl_xor(ps, 32, 64);
+        l = l * corr + ps;
+        m = mn;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[d][r] *= corr;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                const _Float16* vp = vt + (d * 32 + c) * VROW + 16 * st + 4 * hs;
+                const ah4 lo = *(const ah4*)vp, hi = *(const ah4*)(vp + 8);
+                const ah8 va = ah8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[st], o[d], 0, 0, 0);
+            }
+        }
+    }
+    if (qvalid) {
+        const float inv = 1.0f / l;
+        const float* gate = P + (size_t)(t0 + c) * ldp + (size_t)h * 2 * D + D;
+        float* orow = out + ((size_t)(t0 + c) * nq + h) * D;
+#pragma unroll
+        for (int d = 0; d < 8; ++d)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int dim = d * 32 + 8 * q + 4 * hs;
+                const v4f gv = *(const v4f*)(gate + dim);
+                v4f ov;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ov[e] = o[d][4 * q + e] * inv * source_sigmoid(gv[e]);
+                *(v4f*)(orow + dim) = ov;
+            }
+    }
 }
 
 hipError_t gdn_prefill_conv(const float* P, size_t ldp, size_t n, size_t W, size_t H, const float* conv_w,
@@ -241,10 +303,10 @@ hipError_t attn_prefill(const AttnPrefillArgs& a, hipStream_t s) {
                            0, s, a.P, a.ldp, a.nq, a.nkv, a.qnorm, a.knorm, a.eps, a.theta_scale, a.pos0,
                            (float*)a.kcache, (float*)a.vcache, a.Q);
     }
-    const dim3 grid((unsigned)a.n, (unsigned)a.nkv);
+    const dim3 grid((unsigned)((a.n + 31) / 32), (unsigned)a.nkv);
 #define ZG_AP(KV, GG)                                                                                              \
-    hipLaunchKernelGGL((attn_prefill_kernel<KV, GG>), grid, dim3(64 * GG), 0, s, a.Q, (const KV*)a.kcache,        \
-                       (const KV*)a.vcache, a.nq, a.nkv, a.pos0, a.scale, a.P, a.ldp, a.out)
+    hipLaunchKernelGGL((attn_prefill_mfma_kernel<KV, GG>), grid, dim3(64 * GG), 0, s, a.Q, (const KV*)a.kcache,   \
+                       (const KV*)a.vcache, (int)a.n, a.nq, a.nkv, a.pos0, a.scale, a.P, a.ldp, a.out)
 #define ZG_APG(KV)                  \
     switch (G) {                    \
     case 1: ZG_AP(KV, 1); break;    \
