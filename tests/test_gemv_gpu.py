@@ -125,11 +125,14 @@ def test_gemv_device_rms_prologue_bf16(kern, torch_cuda, kind, N, K, M):
 
 
 @pytest.mark.parametrize("kind", KINDS)
-@pytest.mark.parametrize("N,K", [(3584, 1024), (2048, 6144), (151936, 2048)])
-@pytest.mark.parametrize("M", [1, 3, 16, 32])
+@pytest.mark.parametrize("N,K,M", [(3584, 1024, m) for m in (1, 3, 16, 32, 1024, 1056)] +
+                         [(2048, 6144, m) for m in (1, 3, 16, 32, 2048)] +
+                         [(151936, 2048, m) for m in (1, 3, 16, 32)] + [(8224, 2048, 1088)])
 def test_gemv_device_f32_decode_kernels(kern, torch_cuda, kind, N, K, M):
     """f32 activations take the decode-step kernels (in-kernel RMS prologue;
-    Q4_K beyond 4 rows on the f16 MFMA path)."""
+    Q4_K beyond 4 rows on the f16 MFMA path, the LDS-staged variant from
+    1024 rows: 4, 1, 4 and 2 activation blocks per workgroup at M = 1024,
+    1056, 2048 and 1088)."""
     torch = torch_cuda
     w, h = weight(kern, kind, N, K)
     rng = np.random.default_rng(M * 11 + N)
@@ -144,7 +147,8 @@ def test_gemv_device_f32_decode_kernels(kern, torch_cuda, kind, N, K, M):
     torch.cuda.synchronize()
     y = y_d.cpu().numpy()
     worst = 0.0
-    for m in range(M):
+    check = range(M) if M <= 32 else sorted({0, 1, 31, 32, 63, 64, M // 2, M - 33, M - 1})
+    for m in check:
         xn = O.rms_norm(x[m], gamma, 1e-6)
         for rows in row_subset(N):
             ref = O.matvec(kind, w[rows].reshape(-1), rows.size, K, xn)

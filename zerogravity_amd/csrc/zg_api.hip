@@ -419,10 +419,9 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
     std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
     if (!w || !x || !y || (x_dtype != ZG_BF16 && x_dtype != ZG_F32)) return fail(ctx, ZG_E_MALFORMED, "invalid gemv arguments");
-    if (!zg::gemv_supported(w->dw.type, w->dw.K, m_rows)) return fail(ctx, ZG_UNSUPPORTED, "geometry not offered");
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     const int pro = gamma ? zg::PRO_RMS : zg::PRO_PLAIN;
-    if (x_dtype == ZG_F32 && zg::fused_gemv_supported(w->dw.type, w->dw.K, w->dw.N, pro)) {
+    if (x_dtype == ZG_F32 && m_rows > 0 && m_rows <= 65536 && zg::fused_gemv_supported(w->dw.type, w->dw.K, w->dw.N, pro)) {
         // f32 activations: the decode-step kernels themselves (activation
         // prologue in-kernel up to 4 rows, f16 MFMA beyond for Q4_K)
         zg::FusedGemvArgs f;
@@ -451,6 +450,7 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
         }
         return ZG_COMPLETED;
     }
+    if (!zg::gemv_supported(w->dw.type, w->dw.K, m_rows)) return fail(ctx, ZG_UNSUPPORTED, "geometry not offered");
     const size_t need = zg::prepared_bytes(w->dw.type, m_rows, w->dw.K);
     if (ctx->actbuf.bytes < need) {
         // Growing the buffer must not race work still queued on the caller stream.
