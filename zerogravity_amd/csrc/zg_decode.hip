@@ -946,8 +946,9 @@ hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* 
             else hipLaunchKernelGGL((mfma_q4k_wide_kernel<EPI_GLU, 2, 1>), g, dim3(256), 0, s, a, (const _Float16*)xh);
             return hipGetLastError();
         }
-        // two tiles per wave while that still leaves >= 256 workgroups
-        const int nt = ((tiles + 7) / 8) * (mblocks / mb) >= 256 ? 2 : 1;
+        // one weight tile per wave (measured: two per wave, which halves the
+        // LDS traffic per MFMA, costs occupancy and was 1-3% slower)
+        const int nt = 1;
         dim3 g((unsigned)((tiles + 4 * nt - 1) / (4 * nt)), (unsigned)(mblocks / mb), 1u);
 #define ZG_MW(E, NTV, MBV) hipLaunchKernelGGL((mfma_q4k_wide_kernel<E, NTV, MBV>), g, dim3(256), 0, s, a, (const _Float16*)xh)
 #define ZG_MWE(E)                                                       \
