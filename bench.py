@@ -225,6 +225,62 @@ def gdn_leg(ctx, torch, rows=(1, 8, 32, 64), reps=20, H=16):
     return out
 
 
+def attn_bytes(B, T, nq=8, nkv=2, d=256):
+    """Algorithmic HBM bytes of one attention decode step (one layer): K and
+    V of T tokens in bf16 per row, plus q/gate in and the output out (f32)."""
+    return B * (T * nkv * d * 2 * 2 + nq * d * 4 * 3)
+
+
+def attn_leg(ctx, torch, rows=(1, 32), T=2048, reps=20, nq=8, nkv=2):
+    """The attention decode step alone (zg_attn_decode_device: norms, RoPE,
+    K/V append, scores, softmax, values, gate) at B rows, each at position
+    T-1 of a bf16 cache; the caches rotate over distinct buffers totalling
+    > 2.2x the Infinity Cache."""
+    from zerogravity_amd import _lib as L
+    lib = L.lib()
+    s = torch.cuda.current_stream()
+    out = {}
+    d = 256
+    for B in rows:
+        g = torch.Generator(device="cuda")
+        g.manual_seed(100 + B)
+        stride = (2 * nq + 2 * nkv) * d
+        proj = torch.randn(B, stride, device="cuda", generator=g)
+        qn = 1 + 0.1 * torch.randn(d, device="cuda", generator=g)
+        kn = 1 + 0.1 * torch.randn(d, device="cuda", generator=g)
+        pos = torch.full((B,), T - 1, dtype=torch.int32, device="cuda")
+        ws = torch.empty(lib.zg_attn_decode_workspace_bytes(B, nq, T), dtype=torch.uint8, device="cuda")
+        o = torch.empty(B * nq * d, device="cuda")
+        cbytes = B * T * nkv * d * 2 * 2
+        copies = int(min(256, max(2, np.ceil(2.2 * MALL_BYTES / cbytes))))
+        caches = [(torch.randn(B * T * nkv * d, device="cuda", generator=g).bfloat16(),
+                   torch.randn(B * T * nkv * d, device="cuda", generator=g).bfloat16()) for _ in range(copies)]
+
+        def launch(i):
+            kc, vc = caches[i % copies]
+            ctx.check(lib.zg_attn_decode_device(ctx.h, B, nq, nkv, proj.data_ptr(), stride, qn.data_ptr(),
+                                                kn.data_ptr(), 1e-6, float(np.power(1e7, -2.0 / 64.0)),
+                                                pos.data_ptr(), kc.data_ptr(), vc.data_ptr(), T, L.BF16,
+                                                ws.data_ptr(), o.data_ptr(), s.cuda_stream))
+
+        for i in range(copies):
+            launch(i)
+        torch.cuda.synchronize()
+        n = max(reps, copies)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for i in range(n):
+            launch(i)
+        e1.record(s)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / n
+        gbs = attn_bytes(B, T, nq, nkv) / us / 1e3
+        out[B] = dict(us=round(us, 3), gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
+        log(f"attention decode B={B:2d} T={T}: {us:8.2f} us  {gbs:8.1f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+        del caches
+    return out
+
+
 def cpu_decode_baseline(g, tensors, prefix, seconds):
     """The oracle (C restatement of the reference CPU path, OpenMP over GEMV
     rows on every host core) decoding greedily at B=1 after importing a random
@@ -284,6 +340,7 @@ def bench_decode(args):
     log(f"Q4_K GEMV leg: {leg['launches']} launches {leg['us_per_step']:.1f} us/step, "
         f"{leg['us_per_launch']:.2f} us/launch, {leg['gbs']:.0f} GB/s")
     gdn = gdn_leg(kern.ctx, torch)
+    attn = attn_leg(kern.ctx, torch)
     line = {
         "metric": "decode tok/s @B=1 (2B-shaped Q4_K, 2048-token prefix, bf16 KV)",
         "value": round(res[1]["tok_s"], 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
@@ -292,7 +349,8 @@ def bench_decode(args):
         "data": "synthetic (seeded random-init Q4_K GGUF weights, random prefix state)",
         "config": {"workload": "2B-shaped Q4_K continuous-batch greedy decode", "prefix": prefix,
                    "kv_cache": "bf16", "b1": res[1], "b32": res[32],
-                   "b32_tok_s": round(res[32]["tok_s"], 1), "gdn_decode_leg": gdn},
+                   "b32_tok_s": round(res[32]["tok_s"], 1), "gdn_decode_leg": gdn,
+                   "attention_decode_leg": attn},
         "roofline": {"bound": "hbm", "achieved": round(leg["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(leg["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "fused_q4k_kernel (the B=1 decode step's stacked projections, one launch each)",

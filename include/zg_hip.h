@@ -173,6 +173,27 @@ int zg_gdn_decode_device(zg_ctx* ctx, size_t rows, size_t heads, const float* pr
                          const float* conv_w, float* ring, const int32_t* positions, const float* dt,
                          const float* ssm_a, float eps, float* state, float* core, void* stream);
 
+/* One attention layer's decode step for `rows` sequences on device buffers
+ * and the caller's stream: attention_layer (forward.rs:634-755) between its
+ * projections -- head RMSNorm of q and k (:680-695), RoPE on the first 64
+ * dimensions from each row's position (lib.rs:1552-1577), K/V appended at
+ * that position (host_math.rs:1055-1064, rounded to the cache type), scores
+ * (lib.rs:1427-1441, x 1/16), softmax (lib.rs:1352-1387), values
+ * (lib.rs:1276-1305) and the sigmoid gate (forward.rs:751).  Replaces the
+ * per-token RoPE/QK/softmax/value regions for a resident KV cache.
+ * head_dim 256, q_heads / kv_heads <= 4.  proj [rows][proj_stride] =
+ * [q | gate] per query head (2 x 256 each), then k (kv_heads x 256), then v;
+ * kcache, vcache [rows][max_ctx][kv_heads x 256] of kv_dtype (ZG_BF16 or
+ * ZG_F32); positions [rows], each < max_ctx; workspace of
+ * zg_attn_decode_workspace_bytes(rows, q_heads, max_ctx) bytes (scores and
+ * softmax statistics); out [rows][q_heads x 256].  A degenerate softmax sum
+ * raises the context's device flag.  Asynchronous. */
+size_t zg_attn_decode_workspace_bytes(size_t rows, size_t q_heads, size_t max_ctx);
+int zg_attn_decode_device(zg_ctx* ctx, size_t rows, size_t q_heads, size_t kv_heads, const float* proj,
+                          size_t proj_stride, const float* q_norm, const float* k_norm, float eps, float theta_scale,
+                          const int32_t* positions, void* kcache, void* vcache, size_t max_ctx, int kv_dtype,
+                          void* workspace, float* out, void* stream);
+
 /* Multi-chunk prefill on device buffers and the caller's stream (the same
  * kernels as zg_gdn_chunk; no reference counterpart takes more than one
  * chunk per call, core.rs:89).  Chunks of 64 tokens in order; query, key,

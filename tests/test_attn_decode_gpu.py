@@ -1,0 +1,102 @@
+"""GPU parity of the resident attention decode step (zg_attn_decode_device)
+against the CPU oracle's attention_layer (oracle/zg_oracle.c, the schedule of
+model-qwen35/src/forward.rs:634-755): head RMSNorm, RoPE at each row's
+position, K/V append (rounded to the cache type), 32-accumulator scores,
+8-lane softmax with f64 partials, padded 4x8-lane value chains and the
+sigmoid gate.  The device restates each step's order of operations, so the
+outputs and the appended K/V are required bit-identical, for a bf16 and an
+f32 cache, rows at different positions (T = 1, 300 and 2048)."""
+import math
+
+import numpy as np
+import pytest
+
+import zg_oracle as O
+from zerogravity_amd import _lib as L
+
+pytestmark = pytest.mark.gpu
+D = 256
+
+
+def bf16(x):
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+
+
+def to_bf16_bits(x):
+    return (bf16(x).view(np.uint32) >> 16).astype(np.uint16)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = L.Context(0)
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("kv", [L.BF16, L.F32])
+def test_attn_decode_device_matches_oracle(ctx, kv):
+    import torch
+    nq, nkv, eps = 8, 2, 1e-6
+    theta = math.pow(1e7, -2.0 / 64.0)
+    pos = np.array([0, 299, 2047], np.int32)
+    B, max_ctx = pos.size, 2048
+    rng = np.random.default_rng(41 + kv)
+    stride = (2 * nq + 2 * nkv) * D + 8
+    proj = rng.standard_normal((B, stride)).astype(np.float32)
+    qn_w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    kn_w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    kw = nkv * D
+    hist_k = bf16(rng.standard_normal((B, max_ctx, kw)))
+    hist_v = bf16(rng.standard_normal((B, max_ctx, kw)))
+    if kv == L.BF16:
+        kc = torch.from_numpy(to_bf16_bits(hist_k).view(np.int16)).cuda()
+        vc = torch.from_numpy(to_bf16_bits(hist_v).view(np.int16)).cuda()
+    else:
+        kc, vc = torch.from_numpy(hist_k.copy()).cuda(), torch.from_numpy(hist_v.copy()).cuda()
+    d_proj, d_pos = torch.from_numpy(proj).cuda(), torch.from_numpy(pos).cuda()
+    d_qn, d_kn = torch.from_numpy(qn_w).cuda(), torch.from_numpy(kn_w).cuda()
+    ws = torch.empty(L.lib().zg_attn_decode_workspace_bytes(B, nq, max_ctx), dtype=torch.uint8, device="cuda")
+    out = torch.empty((B, nq * D), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.check(L.lib().zg_attn_decode_device(ctx.h, B, nq, nkv, d_proj.data_ptr(), stride, d_qn.data_ptr(),
+                                            d_kn.data_ptr(), eps, theta, d_pos.data_ptr(), kc.data_ptr(),
+                                            vc.data_ptr(), max_ctx, kv, ws.data_ptr(), out.data_ptr(), None))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    if kv == L.BF16:
+        kd = (kc.cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+        vd = (vc.cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    else:
+        kd, vd = kc.cpu().numpy(), vc.cpu().numpy()
+    for b in range(B):
+        p = int(pos[b])
+        row = proj[b]
+        rq = np.concatenate([row[h * 2 * D:h * 2 * D + D] for h in range(nq)])
+        gates = np.concatenate([row[h * 2 * D + D:h * 2 * D + 2 * D] for h in range(nq)])
+        k = row[2 * nq * D:2 * nq * D + kw]
+        v = row[2 * nq * D + kw:2 * nq * D + 2 * kw]
+        qn = O.grouped_rms_norm(rq, qn_w, nq, eps)
+        kn = O.grouped_rms_norm(k, kn_w, nkv, eps)
+        qr, kr = O.rope_kv(qn, kn, D, nq, nkv, 64, p, np.float32(theta))
+        if kv == L.BF16:
+            kr, v = bf16(kr), bf16(v)
+        keys = np.concatenate([hist_k[b, :p], kr[None, :]])
+        vals = np.concatenate([hist_v[b, :p], v[None, :]])
+        _, scores = O.attention_qk(qr, keys, D, nq, nkv, 1.0 / 16.0)
+        probs, _, _ = O.attention_softmax(scores, nq, p + 1)
+        ref = O.binary(1, O.attention_value(probs, vals, D, nq, nkv), gates)
+        assert np.array_equal(kd[b, p].view(np.uint32), kr.view(np.uint32)), b
+        assert np.array_equal(vd[b, p].view(np.uint32), v.view(np.uint32)), b
+        assert np.array_equal(got[b].view(np.uint32), ref.view(np.uint32)), (b, float(np.abs(got[b] - ref).max()))
+        # history untouched
+        assert np.array_equal(kd[b, :p].view(np.uint32), hist_k[b, :p].view(np.uint32))
+
+
+def test_attn_decode_device_refusals(ctx):
+    for bad in (dict(q_heads=6, kv_heads=4), dict(q_heads=10, kv_heads=2), dict(max_ctx=0), dict(kv_dtype=8)):
+        args = dict(q_heads=8, kv_heads=2, max_ctx=64, kv_dtype=L.BF16)
+        args.update(bad)
+        rc = L.lib().zg_attn_decode_device(ctx.h, 1, args["q_heads"], args["kv_heads"], 1, 8192, 1, 1, 1e-6, 0.6,
+                                           1, 1, 1, args["max_ctx"], args["kv_dtype"], 1, 1, None)
+        assert rc == L.E_MALFORMED, bad

@@ -56,6 +56,9 @@ _SIGS = {
     "zg_decode_step": (C.c_int, [P, SZ, P, P, P]),
     "zg_prefill": (C.c_int, [P, SZ, SZ, P, P]),
     "zg_prefill_batched": (C.c_int, [P, SZ, SZ, P, P]),
+    "zg_attn_decode_workspace_bytes": (SZ, [SZ, SZ, SZ]),
+    "zg_attn_decode_device": (C.c_int, [P, SZ, SZ, SZ, P, SZ, P, P, C.c_float, C.c_float, P, P, P, SZ, C.c_int, P, P,
+                                        P]),
     "zg_session_reset_row": (C.c_int, [P, SZ]),
     "zg_session_copy_row": (C.c_int, [P, SZ, SZ]),
     "zg_decode_step_device": (C.c_int, [P, SZ, P, P, P, P]),

@@ -230,6 +230,49 @@ int zg_gdn_decode_device(zg_ctx* ctx, size_t rows, size_t heads, const float* pr
     return ZG_COMPLETED;
 }
 
+size_t zg_attn_decode_workspace_bytes(size_t rows, size_t q_heads, size_t max_ctx) {
+    return rows * q_heads * (max_ctx + 2) * 4;  // scores [rows][q_heads][max_ctx], then {max, 1/sum}
+}
+
+int zg_attn_decode_device(zg_ctx* ctx, size_t rows, size_t q_heads, size_t kv_heads, const float* proj,
+                          size_t proj_stride, const float* q_norm, const float* k_norm, float eps, float theta_scale,
+                          const int32_t* positions, void* kcache, void* vcache, size_t max_ctx, int kv_dtype,
+                          void* workspace, float* out, void* stream) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!proj || !q_norm || !k_norm || !positions || !kcache || !vcache || !workspace || !out || rows == 0 ||
+        rows > 65535 || kv_heads == 0 || q_heads % kv_heads || q_heads / kv_heads > 4 || max_ctx == 0 ||
+        max_ctx > (1u << 30) || proj_stride < (2 * q_heads + 2 * kv_heads) * 256 || !(eps > 0.0f) ||
+        !(theta_scale > 0.0f && theta_scale <= 1.0f) || (kv_dtype != ZG_BF16 && kv_dtype != ZG_F32))
+        return fail(ctx, ZG_E_MALFORMED, "attention decode geometry");
+    zg::AttnDecodeArgs a;
+    a.proj = proj;
+    a.proj_stride = proj_stride;
+    a.qnorm = q_norm;
+    a.knorm = k_norm;
+    a.eps = eps;
+    a.theta_scale = theta_scale;
+    a.scale = 1.0f / 16.0f;  // 1/sqrt(256)
+    a.pos = positions;
+    a.kcache = kcache;
+    a.vcache = vcache;
+    a.cache_row_stride = max_ctx * kv_heads * 256;
+    a.kv_bf16 = kv_dtype == ZG_BF16;
+    a.scores = (float*)workspace;
+    a.score_stride = q_heads * max_ctx;
+    a.head_stride = max_ctx;
+    a.stats = (float*)workspace + rows * q_heads * max_ctx;
+    a.out = out;
+    a.out_stride = q_heads * 256;
+    a.status = ctx->d_flag;
+    a.nq = (int)q_heads;
+    a.nkv = (int)kv_heads;
+    a.max_ctx = (int)max_ctx;
+    ZG_HIP(zg::attn_decode(a, rows, stream ? (hipStream_t)stream : ctx->stream));
+    return ZG_COMPLETED;
+}
+
 int zg_rope_kv(zg_ctx* ctx, const float* query, const float* key, const float* value, size_t head_width,
                size_t query_heads, size_t kv_heads, size_t rotate, size_t position, float theta_scale, float* query_out,
                float* key_out, float* value_out) {
