@@ -57,6 +57,19 @@ def gemv_bytes(kind, N, K, M):
 
 # ------------------------------------------------------------------ decode
 
+def measured_traffic(name="decode_2b_q4k_traffic.md"):
+    """HBM bytes per launch of the roofline kernel from the committed PMC
+    summary (FETCH_SIZE and WRITE_SIZE passes, copy-calibrated), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def decode_matrices(g):
     """The projections one decode step streams, in launch order, as the
     resident model registers them: (label, [tensor names stacked by rows], K,
@@ -352,7 +365,7 @@ def bench_decode(args):
                    "b32_tok_s": round(res[32]["tok_s"], 1), "gdn_decode_leg": gdn,
                    "attention_decode_leg": attn},
         "roofline": {"bound": "hbm", "achieved": round(leg["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(leg["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(leg["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "fused_q4k_kernel (the B=1 decode step's stacked projections, one launch each)",
                      "bytes_per_launch": round(leg["bytes_per_launch"]), "us_per_launch": round(leg["us_per_launch"], 3)},
     }
@@ -657,6 +670,33 @@ def bench_model_prefill(args):
     return line
 
 
+def bench_copy(args):
+    """A plain device copy of 256 MiB (one elementwise kernel reading and
+    writing 256 MiB): the calibration for the FETCH_SIZE / WRITE_SIZE
+    counters and a check of the achievable read+write bandwidth."""
+    import torch
+    n = (256 << 20) // 4
+    a = torch.randn(n, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(max(1, args.warmup)):
+        torch.add(a, 0.0, out=b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    steps = max(1, args.steps)
+    e0.record()
+    for _ in range(steps):
+        torch.add(a, 0.0, out=b)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    gbs = 2 * n * 4 / us / 1e3
+    log(f"copy 256 MiB: {us:.1f} us  {gbs:.0f} GB/s read+write")
+    return {"metric": "device copy GB/s (256 MiB read + 256 MiB written)", "value": round(gbs, 1), "unit": "GB/s",
+            "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(us / 1e3, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "calibration copy", "bytes_read": n * 4, "bytes_written": n * 4}}
+
+
 def bench_gdn(args):
     import torch
     from zerogravity_amd import _lib as L
@@ -682,7 +722,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "prefill", "gdn", "model_prefill"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "prefill", "gdn", "model_prefill", "copy"])
     ap.add_argument("--prefix", type=int, default=2048)
     ap.add_argument("--leg-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -693,7 +733,7 @@ def main():
               "sessions; see the sharding notes in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     bench = {"decode": bench_decode, "gemv": bench_gemv, "prefill": bench_prefill, "gdn": bench_gdn,
-             "model_prefill": bench_model_prefill}[args.workload]
+             "model_prefill": bench_model_prefill, "copy": bench_copy}[args.workload]
     line = bench(args)
     print(json.dumps(line), flush=True)
 
