@@ -697,6 +697,36 @@ def bench_copy(args):
             "config": {"workload": "calibration copy", "bytes_read": n * 4, "bytes_written": n * 4}}
 
 
+def cpu_gdn_baseline(seconds, H=16):
+    """The oracle's GDN decode step at B=1 (conv over 3 x 2048 channels, SiLU,
+    two-stage q/k L2, gates, the 16-head recurrence; one host thread, serial
+    per head as host_math.rs:1007-1016 runs it)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import zg_oracle as O
+    rng = np.random.default_rng(9)
+    W, D = H * 128, 128
+    conv_w = (0.5 * rng.standard_normal(3 * W * 4)).astype(np.float32)
+    hist = np.zeros(3 * W * 3, np.float32)
+    state = (0.02 * rng.standard_normal(H * D * D)).astype(np.float32)
+    dt, a = rng.standard_normal(H).astype(np.float32), -np.exp(rng.standard_normal(H)).astype(np.float32)
+    sc = np.full(D, 1.0 / np.sqrt(np.float32(D)), np.float32)
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < seconds or n < 2:
+        x = rng.standard_normal(4 * W + 2 * H).astype(np.float32)
+        raw, hist = O.gdn_conv_step(x[:3 * W], conv_w, hist)
+        mixed = O.silu(raw)
+        gain, beta = O.gdn_coefficients(x[4 * W:4 * W + H], x[4 * W + H:], dt, a, 1.0 / np.sqrt(D))[:2]
+        qk = O.grouped_rms_norm(mixed[:2 * W], sc, 2 * H, 1e-6 / D)
+        for h in range(H):
+            o, state[h * D * D:(h + 1) * D * D] = O.gdn_recurrent_step(
+                state[h * D * D:(h + 1) * D * D], qk[h * D:(h + 1) * D], qk[W + h * D:W + (h + 1) * D],
+                mixed[2 * W + h * D:2 * W + (h + 1) * D], float(gain[h]), float(beta[h]), 1.0 / np.sqrt(D))
+        n += 1
+    dt_s = (time.perf_counter() - t0) / n
+    return gdn_bytes(1, H) / dt_s / 1e9, 1, f"{n} GDN decode steps at B=1 (16 heads) through the oracle"
+
+
 def bench_gdn(args):
     import torch
     from zerogravity_amd import _lib as L
@@ -713,7 +743,65 @@ def bench_gdn(args):
         "roofline": {"bound": "hbm", "achieved": head["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": head["frac"], "traffic": None},
     }
+    if not args.no_cpu:
+        v, cores, sample = cpu_gdn_baseline(min(args.cpu_seconds, 10.0))
+        line["cpu_baseline"] = {"value": round(v, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+                                "sample": sample}
     ctx.close()
+    return line
+
+
+def bench_config1(args):
+    """Config 1: the 0.8B-shaped Q8_0 model, 32 seeded prompt ids through the
+    per-token prefill and 32 greedy decode steps at B=1 (tokens and logits
+    through the host API, as QwenDenseCpu runs it); the oracle runs the same
+    request on the host cores."""
+    from zerogravity_amd import _lib as L
+    from zerogravity_amd import gguf, qwen35
+    from zerogravity_amd import regions as R
+    kern = R.HipMatVecKernel(0)
+    g = dict(qwen35.QWEN35_0_8B)
+    tensors = qwen35.synthetic_tensors(g, gguf.Q8_0, seed=2025)
+    model = qwen35.QwenModelHip(g, tensors, kernel=kern)
+    prompt = np.random.default_rng(1).integers(0, g["vocab"], 32).astype(np.uint32)
+    times = []
+    for _ in range(max(1, min(args.steps, 5))):
+        sess = model.session(max_batch=1, max_context=128, kv_dtype=L.F32)
+        t0 = time.perf_counter()
+        lg = sess.prefill_transaction(prompt)
+        toks = []
+        for _ in range(32):
+            t = int(np.argmax(lg))
+            toks.append(t)
+            lg = sess.forward(t)
+        times.append(time.perf_counter() - t0)
+        sess.close()
+    model.close()
+    sec = float(np.median(times))
+    line = {
+        "metric": "config-1 request tok/s (0.8B-shaped Q8_0, 32 prompt + 32 greedy tokens, B=1)",
+        "value": round(64 / sec, 1), "unit": "tok/s", "n_gpus": 1, "steps": len(times), "warmup": 0,
+        "ms_per_step": round(sec * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q8_0 weights, int8 dot, f32 accumulate",
+        "data": "synthetic (seeded random-init Q8_0 GGUF weights, seeded prompt ids)",
+        "config": {"workload": "config 1 end to end (host API per token)", "greedy": toks[:8]},
+    }
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import zg_oracle as O
+        threads = host_threads()
+        o = O.Model(dict(g, max_context=128), tensors, threads).session()
+        t0 = time.perf_counter()
+        n = 0
+        for t in prompt:
+            o.forward(int(t), need_logits=n == 31)
+            n += 1
+            if time.perf_counter() - t0 > args.cpu_seconds:
+                break
+        dt = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+                                "sample": f"{n} prompt tokens of the same request through the oracle"}
+    kern.ctx.close()
     return line
 
 
@@ -722,7 +810,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "prefill", "gdn", "model_prefill", "copy"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "gemv", "prefill", "gdn", "model_prefill", "copy", "config1"])
     ap.add_argument("--prefix", type=int, default=2048)
     ap.add_argument("--leg-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -733,7 +821,7 @@ def main():
               "sessions; see the sharding notes in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     bench = {"decode": bench_decode, "gemv": bench_gemv, "prefill": bench_prefill, "gdn": bench_gdn,
-             "model_prefill": bench_model_prefill, "copy": bench_copy}[args.workload]
+             "model_prefill": bench_model_prefill, "copy": bench_copy, "config1": bench_config1}[args.workload]
     line = bench(args)
     print(json.dumps(line), flush=True)
 
