@@ -946,17 +946,14 @@ hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* 
             else hipLaunchKernelGGL((mfma_q4k_wide_kernel<EPI_GLU, 2, 1>), g, dim3(256), 0, s, a, (const _Float16*)xh);
             return hipGetLastError();
         }
-        // one weight tile per wave (measured: two per wave, which halves the
-        // LDS traffic per MFMA, costs occupancy and was 1-3% slower)
-        const int nt = 1;
-        dim3 g((unsigned)((tiles + 4 * nt - 1) / (4 * nt)), (unsigned)(mblocks / mb), 1u);
-#define ZG_MW(E, NTV, MBV) hipLaunchKernelGGL((mfma_q4k_wide_kernel<E, NTV, MBV>), g, dim3(256), 0, s, a, (const _Float16*)xh)
-#define ZG_MWE(E)                                                       \
-    if (nt == 2) {                                                      \
-        if (mb == 4) ZG_MW(E, 2, 4); else if (mb == 2) ZG_MW(E, 2, 2); else ZG_MW(E, 2, 1); \
-    } else {                                                            \
-        if (mb == 4) ZG_MW(E, 1, 4); else if (mb == 2) ZG_MW(E, 1, 2); else ZG_MW(E, 1, 1); \
-    }
+        // one weight tile per wave (two per wave, which halves the LDS
+        // traffic per MFMA, cost occupancy and measured 1-3% slower)
+        dim3 g((unsigned)((tiles + 3) / 4), (unsigned)(mblocks / mb), 1u);
+#define ZG_MW(E, MBV) hipLaunchKernelGGL((mfma_q4k_wide_kernel<E, 1, MBV>), g, dim3(256), 0, s, a, (const _Float16*)xh)
+#define ZG_MWE(E)                 \
+    if (mb == 4) ZG_MW(E, 4);      \
+    else if (mb == 2) ZG_MW(E, 2); \
+    else ZG_MW(E, 1);
         if (a.epi == EPI_RESID) {
             ZG_MWE(EPI_RESID)
         } else {
