@@ -40,12 +40,15 @@ __device__ __forceinline__ float prefill_rms_inv(double total, int n, float eps)
 
 }  // namespace
 
-// Grid ((3W + 255) / 256, n), 256 threads.  Token t, channel ch of the conv
-// input rows P[t][0:3W]: the causal 4-tap conv of cpu/src/ops/gdn.rs:7-44
-// (taps older than the prompt come from the row's ring: the token at
-// position p sits in slot p % 4), SiLU (forward.rs:548), split into q, k, v
-// [n][W].  Workgroups x = 0 also form the gates of lib.rs:339-362: beta =
-// sigmoid(beta projection) and the log decay softplus(alpha + dt) * a.
+// Grid ((3W + 255) / 256, ceil(n / TB)), 256 threads.  Thread = channel ch
+// of the conv input rows P[t][0:3W] for TB consecutive tokens: the causal
+// 4-tap conv of cpu/src/ops/gdn.rs:7-44 over a sliding window (each input
+// read once; taps older than the prompt come from the row's ring, where the
+// token at position p sits in slot p % 4), SiLU (forward.rs:548), split into
+// q, k, v [n][W].  Workgroups x = 0 also form the gates of lib.rs:339-362
+// for their tokens: beta = sigmoid(beta projection), log decay
+// softplus(alpha + dt) * a.
+template <int TB>
 __global__ __launch_bounds__(256) void gdn_prefill_conv_kernel(const float* __restrict__ P, size_t ldp, int n, int W,
                                                                int H, const float* __restrict__ conv_w,
                                                                const float* __restrict__ ring, int pos0,
@@ -53,32 +56,45 @@ __global__ __launch_bounds__(256) void gdn_prefill_conv_kernel(const float* __re
                                                                const float* __restrict__ ssm_a, float* __restrict__ q,
                                                                float* __restrict__ k, float* __restrict__ v,
                                                                float* __restrict__ beta, float* __restrict__ logd) {
-    const int t = blockIdx.y, ch = blockIdx.x * 256 + threadIdx.x;
-    const float* row = P + (size_t)t * ldp;
+    const int t0 = blockIdx.y * TB, ch = blockIdx.x * 256 + threadIdx.x;
+    const int t1 = min(t0 + TB, n);
     if (ch < 3 * W) {
-        float tap[3];
+        float w3[3];  // inputs of tokens t-3, t-2, t-1
 #pragma unroll
-        for (int j = 1; j <= 3; ++j)
-            tap[3 - j] = t - j >= 0 ? P[(size_t)(t - j) * ldp + ch] : ring[(size_t)ch * 4 + ((pos0 + t - j) & 3)];
+        for (int j = 1; j <= 3; ++j) {
+            const int t = t0 - j;
+            w3[3 - j] = t >= 0 ? P[(size_t)t * ldp + ch] : ring[(size_t)ch * 4 + ((pos0 + t) & 3)];
+        }
         const v4f w = *(const v4f*)(conv_w + (size_t)ch * 4);
-        const float t0 = tap[0] * w.x;
-        const float t1 = tap[1] * w.y;
-        const float t2 = tap[2] * w.z;
-        const float t3 = row[ch] * w.w;
-        float acc = t0 + t1;
-        acc = acc + t2;
-        acc = acc + t3;
-        const float o = ggml_silu(acc);
-        if (ch < W) q[(size_t)t * W + ch] = o;
-        else if (ch < 2 * W) k[(size_t)t * W + ch - W] = o;
-        else v[(size_t)t * W + ch - 2 * W] = o;
+        float* dst = ch < W ? q + ch : (ch < 2 * W ? k + (ch - W) : v + (ch - 2 * W));
+        float x[TB];
+#pragma unroll
+        for (int u = 0; u < TB; ++u) x[u] = t0 + u < t1 ? P[(size_t)(t0 + u) * ldp + ch] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < TB; ++u) {
+            if (t0 + u >= t1) break;
+            const float c0 = w3[0] * w.x;
+            const float c1 = w3[1] * w.y;
+            const float c2 = w3[2] * w.z;
+            const float c3 = x[u] * w.w;
+            float acc = c0 + c1;
+            acc = acc + c2;
+            acc = acc + c3;
+            dst[(size_t)(t0 + u) * W] = ggml_silu(acc);
+            w3[0] = w3[1];
+            w3[1] = w3[2];
+            w3[2] = x[u];
+        }
     }
     if (blockIdx.x == 0 && (int)threadIdx.x < H) {
         const int h = threadIdx.x;
-        float gain, bt, sp, gr;
-        gdn_coef(row[4 * W + h], row[4 * W + H + h], dt[h], ssm_a[h], gain, bt, sp, gr);
-        beta[(size_t)t * H + h] = bt;
-        logd[(size_t)t * H + h] = gr;
+        for (int t = t0; t < t1; ++t) {
+            const float* row = P + (size_t)t * ldp;
+            float gain, bt, sp, gr;
+            gdn_coef(row[4 * W + h], row[4 * W + H + h], dt[h], ssm_a[h], gain, bt, sp, gr);
+            beta[(size_t)t * H + h] = bt;
+            logd[(size_t)t * H + h] = gr;
+        }
     }
 }
 
@@ -284,8 +300,10 @@ hipError_t gdn_prefill_conv(const float* P, size_t ldp, size_t n, size_t W, size
                             float* ring, int pos0, const float* dt, const float* ssm_a, float* q, float* k, float* v,
                             float* beta, float* logd, hipStream_t s) {
     if (n == 0 || W == 0 || H == 0 || H > 256) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gdn_prefill_conv_kernel, dim3((unsigned)((3 * W + 255) / 256), (unsigned)n), dim3(256), 0, s, P,
-                       ldp, (int)n, (int)W, (int)H, conv_w, (const float*)ring, pos0, dt, ssm_a, q, k, v, beta, logd);
+    constexpr int TB = 16;
+    hipLaunchKernelGGL(gdn_prefill_conv_kernel<TB>, dim3((unsigned)((3 * W + 255) / 256), (unsigned)((n + TB - 1) / TB)),
+                       dim3(256), 0, s, P, ldp, (int)n, (int)W, (int)H, conv_w, (const float*)ring, pos0, dt, ssm_a, q,
+                       k, v, beta, logd);
     hipLaunchKernelGGL(gdn_prefill_ring_kernel, dim3((unsigned)((3 * W + 255) / 256)), dim3(256), 0, s, P, ldp,
                        (int)n, (int)W, ring, pos0);
     return hipGetLastError();
