@@ -559,7 +559,7 @@ __global__ __launch_bounds__(256) void act16_kernel(FusedGemvArgs a, _Float16* _
     }
 }
 
-// Y[m][n] = sum_k X[m][k] W[n][k] for up to 64 rows on v_mfma_f32_32x32x16_f16:
+// Y[m][n] = sum_k X[m][k] W[n][k] over 32-row activation blocks on v_mfma_f32_32x32x16_f16:
 // A = X tile (32 rows m x 16 k), B = dequantized weights (16 k x 32 rows n),
 // so D[i = m][j = n] and the lanes of a row store adjacent outputs.  Lane l
 // holds A[m = l%32][k = 8*(l/32) + e] and B[k = 8*(l/32) + e][n = l%32]

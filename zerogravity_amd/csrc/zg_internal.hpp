@@ -177,8 +177,9 @@ bool batched_glu_supported(int type, size_t K, size_t N);
 int batched_splits(size_t N, size_t K);
 bool fused_gemv_supported(int type, size_t K, size_t N, int pro);
 hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& a, hipStream_t s);
-// Batched rows (M <= 64, Q4_K): the prologue values rounded to f16 into
-// `scratch` (batched_scratch_bytes), then an f16 MFMA GEMM with the epilogue.
+// Batched rows (M > 4, Q4_K; decode batches and prompts): the prologue
+// values rounded to f16 into `scratch` (batched_scratch_bytes), then an f16
+// MFMA GEMM with the epilogue (LDS-staged from 1024 rows).
 size_t batched_scratch_bytes(size_t M, size_t K);
 // Builds w.qs_t / w.hdr_t (Q4_K) if absent: allocates, so call it outside
 // graph capture.  batched_gemv refuses a Q4_K weight without them.
