@@ -1711,17 +1711,16 @@ __global__ __launch_bounds__(256) void attn_decode_qk_kernel(AttnDecodeArgs a) {
 
 }
 
-// Grid (q_heads, B): softmax statistics of one head (lib.rs:1352-1387): max,
-// GGML exp, 8-wide f32 partials summed in f64, inv = (float)(1/sum), stored
-// as {max, inv} for the value kernel.  Thread t owns 8-element blocks t,
-// t+256, ...; each pass over a 4096-token span issues its loads together.
-__global__ __launch_bounds__(256) void attn_decode_stats_kernel(AttnDecodeArgs a) {
+// Softmax statistics of one head's T scores (lib.rs:1352-1387) by a
+// workgroup of 256 threads: max, GGML exp, 8-wide f32 partials summed in
+// f64, inv = (float)(1/sum).  Thread t owns 8-element blocks t, t+256, ...;
+// each pass over a 4096-token span issues its loads together.  Returns
+// {max, inv} to every thread and the f64 sum (for the degenerate check).
+__device__ __forceinline__ void softmax_stats(const float* row, int T, int max_ctx, float& m_out, float& inv_out,
+                                              double& total_out) {
     __shared__ float wmax[4];
     __shared__ double wsum[4];
-    const int h = blockIdx.x, b = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int T = a.pos[b] + 1;
-    const float* row = a.scores + (size_t)b * a.score_stride + (size_t)h * a.head_stride;
     float m = -INFINITY;
     double sum = 0.0;
     for (int pass = 0; pass < 2; ++pass) {
@@ -1732,7 +1731,7 @@ __global__ __launch_bounds__(256) void attn_decode_stats_kernel(AttnDecodeArgs a
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const int at = base + 8 * (tid + 256 * r) + i;
-                    const float sv = row[min(at, a.max_ctx - 1)];  // issued before T is known, no branch
+                    const float sv = row[min(at, max_ctx - 1)];  // issued before T is known, no branch
                     e[r][i] = at < T ? sv : -INFINITY;
                 }
 #pragma unroll
@@ -1759,10 +1758,24 @@ __global__ __launch_bounds__(256) void attn_decode_stats_kernel(AttnDecodeArgs a
     sum = wave_sum_xor<double>(sum, 64);
     if (lane == 0) wsum[wv] = sum;
     __syncthreads();
-    if (tid == 0) {
-        const double total = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    const double total = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    m_out = m;
+    inv_out = (float)(1.0 / total);
+    total_out = total;
+}
+
+// Grid (q_heads, B): the statistics of one head, stored as {max, inv} for
+// the value kernel (batches of 8 rows and more).
+__global__ __launch_bounds__(256) void attn_decode_stats_kernel(AttnDecodeArgs a) {
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int T = a.pos[b] + 1;
+    const float* row = a.scores + (size_t)b * a.score_stride + (size_t)h * a.head_stride;
+    float m, inv;
+    double total;
+    softmax_stats(row, T, a.max_ctx, m, inv, total);
+    if (threadIdx.x == 0) {
         a.stats[((size_t)b * a.nq + h) * 2] = m;
-        a.stats[((size_t)b * a.nq + h) * 2 + 1] = (float)(1.0 / total);
+        a.stats[((size_t)b * a.nq + h) * 2 + 1] = inv;
         if (!(total >= 1.0) || !(total < INFINITY)) atomicOr(a.status, 8);
     }
 }
@@ -1795,7 +1808,7 @@ __device__ __forceinline__ void kv_ldn(const KV* p, float (&o)[CPT]) {
 // the sigmoid output gate (forward.rs:751) finish.  The LDS barriers do not
 // wait for the value loads, which only the chains consume.  Few heads and
 // channels per workgroup spread a single row over many workgroups.
-template <typename KV, int HG, int CPT, int NV>
+template <typename KV, int HG, int CPT, int NV, bool FS>
 __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
     constexpr int D = 256, TT = 32 * NV, CB = 8 * CPT, NS = HG * TT / 256, HP = HG == 3 ? 4 : HG;
     __shared__ float pt[TT * HP];
@@ -1806,10 +1819,19 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
     const int T = a.pos[b] + 1;
     const float* sb = a.scores + (size_t)b * a.score_stride + (size_t)h0 * a.head_stride;
     float mx[HG], inv[HG];
+    if constexpr (FS) {
+        // small batches: the head's statistics computed here (the same code
+        // as attn_decode_stats_kernel, so the same values) instead of a launch
+        static_assert(HG == 1, "fused statistics are per head");
+        double total;
+        softmax_stats(sb, T, a.max_ctx, mx[0], inv[0], total);
+        if (blockIdx.x == 0 && tid == 0 && (!(total >= 1.0) || !(total < INFINITY))) atomicOr(a.status, 8);
+    } else {
 #pragma unroll
-    for (int g = 0; g < HG; ++g) {
-        mx[g] = a.stats[((size_t)b * a.nq + h0 + g) * 2];
-        inv[g] = a.stats[((size_t)b * a.nq + h0 + g) * 2 + 1];
+        for (int g = 0; g < HG; ++g) {
+            mx[g] = a.stats[((size_t)b * a.nq + h0 + g) * 2];
+            inv[g] = a.stats[((size_t)b * a.nq + h0 + g) * 2 + 1];
+        }
     }
     float gate = 0.0f;
     if (tid < HG * CB) {
@@ -1897,15 +1919,18 @@ static void launch_attn(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
     const size_t want = B >= 8 ? 8 : 64 / B;
     const unsigned nblk = (unsigned)std::min<size_t>((a.max_ctx + 31) / 32, want);
     hipLaunchKernelGGL((attn_decode_qk_kernel<KV, G>), dim3(nblk, a.nkv, (unsigned)B), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(attn_decode_stats_kernel, dim3(a.nq, (unsigned)B), dim3(256), 0, s, a);
-    // batch 1: one head and 8 channels per workgroup (a row over 32 x nq
-    // workgroups, each token tile in one burst); rows in numbers: the kv
-    // head's G heads and 32 channels per workgroup
-    if (B >= 8)
-        hipLaunchKernelGGL((attn_decode_pv_kernel<KV, G, 4, 16>), dim3(256 / 32, a.nq / G, (unsigned)B), dim3(256), 0, s,
+    // batch < 8: one head and 8 channels per workgroup (a row over 32 x nq
+    // workgroups, each token tile in one burst), the softmax statistics
+    // folded in; rows in numbers: a statistics launch, then the kv head's G
+    // heads and 32 channels per workgroup
+    if (B >= 8) {
+        hipLaunchKernelGGL(attn_decode_stats_kernel, dim3(a.nq, (unsigned)B), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((attn_decode_pv_kernel<KV, G, 4, 16, false>), dim3(256 / 32, a.nq / G, (unsigned)B), dim3(256),
+                           0, s, a);
+    } else {
+        hipLaunchKernelGGL((attn_decode_pv_kernel<KV, 1, 1, 96, true>), dim3(256 / 8, a.nq, (unsigned)B), dim3(256), 0, s,
                            a);
-    else
-        hipLaunchKernelGGL((attn_decode_pv_kernel<KV, 1, 1, 96>), dim3(256 / 8, a.nq, (unsigned)B), dim3(256), 0, s, a);
+    }
 }
 
 hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
