@@ -1391,13 +1391,19 @@ hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& args, hipStrea
 // one (quarter 0) that writes them.  conv: cpu/src/ops/gdn.rs:7-44 (left to
 // right, no FMA) + SiLU (forward.rs:548); L2, gates and recurrence as
 // gdn_recurrent_kernel<true>.
-__global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
+// HEAD: one workgroup of 4 x 256 threads per (head, row) -- quarter q is
+// threads 256q.. -- sharing the conv, norms and gates, and finishing with
+// the gated RMSNorm of the head's output into the next GEMM's f16 tiles.
+template <bool HEAD>
+__global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecodeArgs a) {
     constexpr int D = 128;
     __shared__ float qk[2 * D];
-    __shared__ float vv[32];
+    __shared__ float vv[HEAD ? D : 32];
     __shared__ float gates[2];
-    const int h = blockIdx.x >> 2, quarter = blockIdx.x & 3, b = blockIdx.y;
-    const int tid = threadIdx.x;
+    __shared__ float ob[HEAD ? D : 1];
+    const int h = HEAD ? blockIdx.x : blockIdx.x >> 2, b = blockIdx.y;
+    const int quarter = HEAD ? (int)(threadIdx.x >> 8) : (int)(blockIdx.x & 3);
+    const int tid = threadIdx.x & 255;
     const int W = a.H * D;
     // this thread's 16 state values (the bulk of the traffic) are requested
     // first, so that their latency overlaps the conv, norms and gates
@@ -1427,19 +1433,20 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
         acc = acc + t3;
         return acc;
     };
-    {
+    if (!HEAD || quarter == 0) {
         const int ch = tid < D ? h * D + tid : W + h * D + (tid - D);
         qk[tid] = ggml_silu(conv(ch));
         if (quarter == 0) ring[(size_t)ch * 4 + sw] = xin[ch];
     }
-    if (tid < 32) {
-        const int ch = 2 * W + h * D + quarter * 32 + tid;
-        vv[tid] = ggml_silu(conv(ch));
+    if (HEAD ? (quarter == 1 && tid < D) : tid < 32) {
+        const int vc = HEAD ? tid : quarter * 32 + tid;
+        const int ch = 2 * W + h * D + vc;
+        vv[HEAD ? vc : tid] = ggml_silu(conv(ch));
         ring[(size_t)ch * 4 + sw] = xin[ch];
     }
     // the head's gates (f64-evaluated transcendentals) once per workgroup,
     // by the wave without value channels
-    if (tid == 192) {
+    if (tid == 192 && (!HEAD || quarter == 0)) {
         float gn, bt, sp, gr;
         gdn_coef(xin[4 * W + h], xin[4 * W + a.H + h], a.dt[h], a.ssm_a[h], gn, bt, sp, gr);
         gates[0] = gn;
@@ -1482,7 +1489,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
             k[c][t] = tk * dsq;
         }
     const float gain = gates[0], beta = gates[1];
-    const float vj = vv[jl];
+    const float vj = vv[HEAD ? j : jl];
     float cv[4][4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -1499,11 +1506,48 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnDecodeArgs a) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) *(v4f*)(col + 32 * c) = v4f{cv[c][0], cv[c][1], cv[c][2], cv[c][3]};
     if (s == 0) a.core[(size_t)b * W + h * D + j] = o * a.scale;
+    if constexpr (HEAD) {
+        // gated RMSNorm of the head (forward.rs:586-594) in act16_kernel's
+        // arithmetic: 32 lanes of wave 0, elements 4t..4t+3 each, f64 sum of
+        // f32 squares over the group, then ((e * inv) * gamma) * silu(z)
+        if (s == 0) ob[j] = o * a.scale;
+        __syncthreads();
+        if (threadIdx.x < 64) {  // the whole wave runs the 32-lane tree; lanes 32.. repeat the group
+            const int t = threadIdx.x & 31;
+            float e[4];
+            double sq = 0.0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                e[i] = ob[4 * t + i];
+                const float q2 = e[i] * e[i];
+                sq += (double)q2;
+            }
+            sq = group_sum_last<32>(sq);
+            sq = __shfl(sq, ((int)threadIdx.x & 32) | 31, 64);
+            const float gi = rms_inv(sq, D, a.eps);
+            const v4f g = *(const v4f*)(a.norm + 4 * t);
+            const v4f z = *(const v4f*)(xin + 3 * W + h * D + 4 * t);
+            const float gg[4] = {g.x, g.y, g.z, g.w}, zz[4] = {z.x, z.y, z.z, z.w};
+            typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+            h4v hv4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) hv4[i] = (_Float16)(((e[i] * gi) * gg[i]) * ggml_silu(zz[i]));
+            const int k = h * D + 4 * t, m = b;
+            const size_t lane_t = (size_t)((k & 15) >> 3) * 32 + (m & 31);
+            const size_t at = ((((size_t)(m >> 5) * (W >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + lane_t) * 8 + (k & 7);
+            if (threadIdx.x < 32) *(h4v*)((_Float16*)a.xh + at) = hv4;
+        }
+    }
 }
 
 hipError_t gdn_decode(const GdnDecodeArgs& a, size_t B, hipStream_t s) {
     if (a.H <= 0 || B == 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gdn_decode_kernel, dim3((unsigned)(a.H * 4), (unsigned)B), dim3(256), 0, s, a);
+    if (a.xh) {
+        if (!a.norm || (a.H * 128) % 256) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(gdn_decode_kernel<true>, dim3((unsigned)a.H, (unsigned)B), dim3(1024), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(gdn_decode_kernel<false>, dim3((unsigned)(a.H * 4), (unsigned)B), dim3(256), 0, s, a);
+    }
     return hipGetLastError();
 }
 

@@ -199,6 +199,12 @@ struct GdnDecodeArgs {
     float* state = nullptr;  // [B][H][128][128] value-major
     float* core = nullptr;   // [B][W]
     int H = 0;
+    // batched rows (optional): the output projection's activation --
+    // gated RMSNorm (ssm_norm [128], z = proj[3W:4W]) x silu(z) -- written as
+    // f16 MFMA tiles for K = W (the layout act16_kernel writes), so that GEMM
+    // needs no activation launch.  One workgroup then holds a whole head.
+    void* xh = nullptr;
+    const float* norm = nullptr;
 };
 hipError_t gdn_decode(const GdnDecodeArgs& a, size_t B, hipStream_t s);
 

@@ -268,10 +268,18 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             d.state = s->rec[slot];
             d.core = s->core;
             d.H = (int)g.gdn_heads;
+            // batched rows: the kernel also writes ssm_out's gated-norm f16
+            // activation tiles (one workgroup per head), so the batched GEMM
+            // runs without an activation launch
+            const bool tiles = B > 4 && L.out_proj->dw.type == zg::kQ4_K;
+            if (tiles) {
+                d.xh = s->xh;
+                d.norm = L.ssm_norm;
+            }
             ZG_HIP(zg::gdn_decode(d, B, st));
             // gated RMSNorm (ssm_norm) * silu(z) -> ssm_out -> residual
             ZG_HIP(gemv(L.out_proj, zg::PRO_GATED, s->core, W, s->y0 + 3 * W, s->y0w, L.ssm_norm, zg::EPI_RESID, s->x,
-                        H));
+                        H, nullptr, tiles ? s->xh : nullptr));
         } else {
             zg::AttnDecodeArgs a;
             a.proj = s->y0;
