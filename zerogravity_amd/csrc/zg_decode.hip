@@ -1953,6 +1953,12 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
         float v = (h0s + h1) + (h2 + h3);
         v = v * source_sigmoid(gate);
         a.out[(size_t)b * a.out_stride + (size_t)(h0 + g) * D + blockIdx.x * CB + c] = v;
+        if (a.xh) {
+            const int k = (h0 + g) * D + blockIdx.x * CB + c, m = b, K = a.nq * D;
+            const size_t lane_t = (size_t)((k & 15) >> 3) * 32 + (m & 31);
+            const size_t at = ((((size_t)(m >> 5) * (K >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + lane_t) * 8 + (k & 7);
+            ((_Float16*)a.xh)[at] = (_Float16)v;
+        }
     }
 }
 

@@ -227,6 +227,10 @@ struct AttnDecodeArgs {
     int* status = nullptr;  // bit 3: degenerate softmax sum
     float* stats = nullptr;  // [B][nq][2] softmax {max, 1/sum}
     int nq = 0, nkv = 0, max_ctx = 0;
+    // batched rows (optional): the gated output also written as f16 MFMA
+    // tiles for K = nq*d (act16_kernel's plain layout), the output
+    // projection's activation
+    void* xh = nullptr;
 };
 hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s);
 

@@ -304,8 +304,12 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             a.nq = (int)g.q_heads;
             a.nkv = (int)g.kv_heads;
             a.max_ctx = (int)s->max_ctx;
+            // batched rows: the value kernel also writes o_proj's f16 tiles
+            const bool tiles = B > 4 && L.out_proj->dw.type == zg::kQ4_K;
+            if (tiles) a.xh = s->xh;
             ZG_HIP(zg::attn_decode(a, B, st));
-            ZG_HIP(gemv(L.out_proj, zg::PRO_PLAIN, s->ao, QD, nullptr, 0, nullptr, zg::EPI_RESID, s->x, H));
+            ZG_HIP(gemv(L.out_proj, zg::PRO_PLAIN, s->ao, QD, nullptr, 0, nullptr, zg::EPI_RESID, s->x, H, nullptr,
+                        tiles ? s->xh : nullptr));
         }
         const zg::DeviceWeight& gu = L.ffn_gu[0].w->dw;
         const bool glu = L.ffn_gu.size() == 1 && L.ffn_down->dw.type == zg::kQ4_K &&
