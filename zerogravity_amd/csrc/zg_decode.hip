@@ -64,23 +64,41 @@ constexpr int kRecWords = 36;  // Q4_K record: 32 dwords of int16 pairs + {xs_lo
 //     the pairing gemv_q4k_kernel expects (element e of a group goes to
 //     dword (e&1 ? 8 : 0) + e/4, half (e>>1)&1; high group +16).
 // Ends with a barrier.  K <= 1024 * JMAX, K % 32 == 0 (K % 256 for Q8_K).
-template <int PRO, int CODEC, int JMAX>
-__device__ void wg_prologue(const FusedGemvArgs& a, int m, bool valid, uint32_t* rec, int* codes, float* scales,
-                            float* extra = nullptr, int* bsums = nullptr) {
-    __shared__ double red[4];
-    const int tid = threadIdx.x, lane = tid & 63, K = a.K;
-    v4f v[JMAX], w[JMAX];
+//
+// The loads are a phase of their own (wg_prologue_load) so that a kernel can
+// issue them before its weight loads: a wave's vector loads complete in
+// issue order, so activation loads queued behind the weights would hold
+// the prologue until the weights have arrived.
+template <int JMAX>
+struct ProIn {
+    v4f v[JMAX], w[JMAX], g[JMAX];
+};
+
+template <int PRO, int JMAX>
+__device__ __forceinline__ void wg_prologue_load(const FusedGemvArgs& a, int m, bool valid, ProIn<JMAX>& in) {
+    const int tid = threadIdx.x, K = a.K;
 #pragma unroll
     for (int j = 0; j < JMAX; ++j) {
         const int k = 4 * tid + 1024 * j;
-        v[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-        w[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        in.v[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        in.w[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        in.g[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
         if (valid && k < K) {
-            v[j] = *(const v4f*)(a.x + (size_t)m * a.ldx + k);
-            if (PRO == PRO_RMS) w[j] = *(const v4f*)(a.gamma + k);
-            if (PRO == PRO_GATED || PRO == PRO_SILU_MUL) w[j] = *(const v4f*)(a.x2 + (size_t)m * a.ldx2 + k);
+            in.v[j] = *(const v4f*)(a.x + (size_t)m * a.ldx + k);
+            if (PRO == PRO_RMS) in.w[j] = *(const v4f*)(a.gamma + k);
+            if (PRO == PRO_GATED || PRO == PRO_SILU_MUL) in.w[j] = *(const v4f*)(a.x2 + (size_t)m * a.ldx2 + k);
         }
+        if (PRO == PRO_GATED && k < K) in.g[j] = *(const v4f*)(a.gamma + (k & (a.group - 1)));
     }
+}
+
+template <int PRO, int CODEC, int JMAX>
+__device__ void wg_prologue_code(const FusedGemvArgs& a, bool valid, const ProIn<JMAX>& in, uint32_t* rec, int* codes,
+                                 float* scales, float* extra = nullptr, int* bsums = nullptr) {
+    __shared__ double red[4];
+    const int tid = threadIdx.x, lane = tid & 63, K = a.K;
+    const v4f* v = in.v;
+    const v4f* w = in.w;
     float inv = 1.0f;
     if (PRO == PRO_RMS) {
         double s = 0.0;
@@ -117,8 +135,7 @@ __device__ void wg_prologue(const FusedGemvArgs& a, int m, bool valid, uint32_t*
             s = group_sum_last<32>(s);
             s = __shfl(s, (lane & 32) | 31, 64);
             const float gi = rms_inv(s, a.group, a.eps);
-            const v4f g = k < K ? *(const v4f*)(a.gamma + (k & (a.group - 1))) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
-            const float gg[4] = {g.x, g.y, g.z, g.w};
+            const float gg[4] = {in.g[j].x, in.g[j].y, in.g[j].z, in.g[j].w};
 #pragma unroll
             for (int t = 0; t < 4; ++t) e[t] = ((e[t] * gi) * gg[t]) * ggml_silu(o[t]);
         } else if (PRO == PRO_SILU_MUL) {
@@ -232,6 +249,14 @@ __device__ void wg_prologue(const FusedGemvArgs& a, int m, bool valid, uint32_t*
     __syncthreads();
 }
 
+template <int PRO, int CODEC, int JMAX>
+__device__ __forceinline__ void wg_prologue(const FusedGemvArgs& a, int m, bool valid, uint32_t* rec, int* codes,
+                                            float* scales, float* extra = nullptr, int* bsums = nullptr) {
+    ProIn<JMAX> in;
+    wg_prologue_load<PRO, JMAX>(a, m, valid, in);
+    wg_prologue_code<PRO, CODEC, JMAX>(a, valid, in, rec, codes, scales, extra, bsums);
+}
+
 // ============================================================= Q4_K GEMV
 
 // Lanes: `lpr` per row, chunk c = sub + i*lpr (i < CH) is the group pair
@@ -271,34 +296,36 @@ __global__ __launch_bounds__(256) void fused_q4k_kernel(FusedGemvArgs a, int lpr
         if (EPI == EPI_GLU) return rg * (rpw >> 1) + (rsub >> 1) < (N >> 1);
         return rg * rpw + rsub < N;
     };
-    // RG consecutive row groups per wave, all their loads issued together
+    // RG consecutive row groups per wave, all their loads issued together.
+    // The loads are unconditional: a row past N reads row 0 (its sums are
+    // never stored) and a chunk past the row end reads the row's last chunk
+    // (its activation record is zero, so it adds exactly nothing).  Branches
+    // around the loads would join with register copies that wait for them.
     v4i w0[RG][CH], w1[RG][CH];
     v4u h[RG][CH];
     auto load_rows = [&](int rg0) {
 #pragma unroll
         for (int r = 0; r < RG; ++r) {
-            const int row = row_of(rg0 + r);
-            const bool rok = row_ok(rg0 + r);
+            const int row = row_ok(rg0 + r) ? row_of(rg0 + r) : 0;
 #pragma unroll
             for (int i = 0; i < CH; ++i) {
-                const int c = sub + i * lpr;
-                if (rok && c < nchunk) {
-                    const uint8_t* base = qs + (size_t)row * (K >> 1) + (size_t)c * 32;
-                    w0[r][i] = load_nt(base);
-                    w1[r][i] = load_nt(base + 16);
-                    h[r][i] = hdr[(size_t)row * nbk + (c >> 2)];
-                } else {
-                    w0[r][i] = v4i{0, 0, 0, 0};
-                    w1[r][i] = v4i{0, 0, 0, 0};
-                    h[r][i] = v4u{0u, 0u, 0u, 0u};
-                }
+                const int c = min(sub + i * lpr, nchunk - 1);
+                const uint8_t* base = qs + (size_t)row * (K >> 1) + (size_t)c * 32;
+                w0[r][i] = load_nt(base);
+                w1[r][i] = load_nt(base + 16);
+                h[r][i] = hdr[(size_t)row * nbk + (c >> 2)];
             }
         }
     };
-    if (wave * RG * rpw < N) load_rows(wave * RG);
+    // activation row 0's loads go first, then the weights', so that its
+    // coding does not wait for the weights
+    ProIn<J> pin;
+    wg_prologue_load<PRO, J>(a, m0, m0 < a.M, pin);
+    load_rows(wave * RG);
 
+    wg_prologue_code<PRO, kCodecQ4K, J>(a, m0 < a.M, pin, lds_q4, nullptr, nullptr);
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
+    for (int m = 1; m < MT; ++m)
         wg_prologue<PRO, kCodecQ4K, J>(a, m0 + m, m0 + m < a.M, lds_q4 + (size_t)m * nchunk * kRecWords, nullptr,
                                     nullptr);
 
