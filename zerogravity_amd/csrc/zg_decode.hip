@@ -1677,6 +1677,23 @@ __global__ __launch_bounds__(256) void attn_decode_qk_kernel(AttnDecodeArgs a) {
 #pragma unroll
         for (int c = 0; c < 8; ++c) kn[c].load(kc + (size_t)t * tstep + 32 * c + 4 * s);
     };
+    // q heads (tasks 0..G-1) and the key (task G): wave w takes tasks w,
+    // w+4.  Their loads are issued before the first token block's keys (a
+    // wave's loads complete in issue order, so the normalisation waits only
+    // for its own inputs); a task past G loads task G's rows and is dropped.
+    constexpr int NR = G / 4 + 1;
+    float tv[NR][4], tg[NR][4];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int task = min(4 * i + wv, G);
+        const float* src = task < G ? proj + (size_t)(kvh * G + task) * 2 * D : proj + QD2 + (size_t)kvh * D;
+        const float* gamma = task < G ? a.qnorm : a.knorm;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            tv[i][r] = src[lane + 64 * r];
+            tg[i][r] = gamma[lane + 64 * r];
+        }
+    }
     load_keys(blockIdx.x);
 
     // rotation angles of this position, shared by every head
@@ -1686,19 +1703,12 @@ __global__ __launch_bounds__(256) void attn_decode_qk_kernel(AttnDecodeArgs a) {
         rsin[tid] = cr_sinf(angle);
         rcos[tid] = cr_cosf(angle);
     }
-    // q heads (tasks 0..G-1) and the key (task G): wave w takes tasks w, w+4
 #pragma unroll
-    for (int task0 = 0; task0 <= G; task0 += 4) {
-        const int task = task0 + wv;
+    for (int i = 0; i < NR; ++i) {
+        const int task = 4 * i + wv;
         if (task <= G) {
-            const float* src = task < G ? proj + (size_t)(kvh * G + task) * 2 * D : proj + QD2 + (size_t)kvh * D;
-            const float* gamma = task < G ? a.qnorm : a.knorm;
-            float v[4], gm[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                v[r] = src[lane + 64 * r];
-                gm[r] = gamma[lane + 64 * r];
-            }
+            const float* v = tv[i];
+            const float* gm = tg[i];
             double sq = 0.0;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -1784,11 +1794,68 @@ __global__ __launch_bounds__(256) void attn_decode_qk_kernel(AttnDecodeArgs a) {
 
 // Softmax statistics of one head's T scores (lib.rs:1352-1387) by a
 // workgroup of 256 threads: max, GGML exp, 8-wide f32 partials summed in
-// f64, inv = (float)(1/sum).  Thread t owns 8-element blocks t, t+256, ...;
-// each pass over a 4096-token span issues its loads together.  Returns
-// {max, inv} to every thread and the f64 sum (for the degenerate check).
+// f64, inv = (float)(1/sum).  Thread t owns 8-element blocks t, t+256, ...
+// of each 4096-token span.  Returns {max, inv} to every thread and the f64
+// sum (for the degenerate check).
+//
+// One span's scores in registers, -inf past T; loads bounded by the cache
+// size, not by T, so they are issued before T is known, without branches.
+__device__ __forceinline__ void softmax_span_load(const float* row, int base, int T, int max_ctx, float (&e)[2][8]) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int at = base + 8 * (tid + 256 * r) + i;
+            const float sv = row[min(at, max_ctx - 1)];
+            e[r][i] = at < T ? sv : -INFINITY;
+        }
+}
+
+// Statistics of a row that fits one span (T <= 4096), from its registers;
+// x returns GGML exp(score - max) per element, zero past T.
+__device__ __forceinline__ void softmax_span_stats(const float (&e)[2][8], int T, float& m_out, float& inv_out,
+                                                   double& total_out, float (&x)[2][8]) {
+    __shared__ float wmax[4];
+    __shared__ double wsum[4];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    float m = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, e[r][i]);
+    m = wave_max(m);
+    if (lane == 0) wmax[wv] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    double sum = 0.0;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[r][i] = 8 * (tid + 256 * r) + i < T ? ggml_exp(e[r][i] - m) : 0.0f;
+        if (8 * (tid + 256 * r) < T) {
+            const float partial =
+                ((x[r][0] + x[r][4]) + (x[r][2] + x[r][6])) + ((x[r][1] + x[r][5]) + (x[r][3] + x[r][7]));
+            sum += (double)partial;
+        }
+    }
+    sum = wave_sum_xor<double>(sum, 64);
+    if (lane == 0) wsum[wv] = sum;
+    __syncthreads();
+    const double total = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    m_out = m;
+    inv_out = (float)(1.0 / total);
+    total_out = total;
+}
+
 __device__ __forceinline__ void softmax_stats(const float* row, int T, int max_ctx, float& m_out, float& inv_out,
                                               double& total_out) {
+    if (T <= 4096) {  // one span: each score loaded once
+        float e[2][8], x[2][8];
+        softmax_span_load(row, 0, T, max_ctx, e);
+        softmax_span_stats(e, T, m_out, inv_out, total_out, x);
+        return;
+    }
     __shared__ float wmax[4];
     __shared__ double wsum[4];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -1797,14 +1864,7 @@ __device__ __forceinline__ void softmax_stats(const float* row, int T, int max_c
     for (int pass = 0; pass < 2; ++pass) {
         for (int base = 0; base < T; base += 4096) {
             float e[2][8];
-#pragma unroll
-            for (int r = 0; r < 2; ++r)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int at = base + 8 * (tid + 256 * r) + i;
-                    const float sv = row[min(at, max_ctx - 1)];  // issued before T is known, no branch
-                    e[r][i] = at < T ? sv : -INFINITY;
-                }
+            softmax_span_load(row, base, T, max_ctx, e);
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
                 if (pass == 0) {
@@ -1889,21 +1949,6 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int T = a.pos[b] + 1;
     const float* sb = a.scores + (size_t)b * a.score_stride + (size_t)h0 * a.head_stride;
-    float mx[HG], inv[HG];
-    if constexpr (FS) {
-        // small batches: the head's statistics computed here (the same code
-        // as attn_decode_stats_kernel, so the same values) instead of a launch
-        static_assert(HG == 1, "fused statistics are per head");
-        double total;
-        softmax_stats(sb, T, a.max_ctx, mx[0], inv[0], total);
-        if (blockIdx.x == 0 && tid == 0 && (!(total >= 1.0) || !(total < INFINITY))) atomicOr(a.status, 8);
-    } else {
-#pragma unroll
-        for (int g = 0; g < HG; ++g) {
-            mx[g] = a.stats[((size_t)b * a.nq + h0 + g) * 2];
-            inv[g] = a.stats[((size_t)b * a.nq + h0 + g) * 2 + 1];
-        }
-    }
     float gate = 0.0f;
     if (tid < HG * CB) {
         const int g = tid / CB, c = tid % CB;
@@ -1913,16 +1958,15 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
     const int j0 = blockIdx.x * CB + cq * CPT;
     const KV* vb = (const KV*)a.vcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D + j0;
     const size_t vstep = (size_t)a.nkv * D;
+    const int tmax = a.max_ctx - 1;
     float acc[HG][CPT];
 #pragma unroll
     for (int g = 0; g < HG; ++g)
 #pragma unroll
         for (int c = 0; c < CPT; ++c) acc[g][c] = 0.0f;
-    for (int t0 = 0; t0 < T; t0 += TT) {
-        // unconditional loads (no per-lane branches): token indices clamped
-        // to the cache, values past the position masked where they are used
-        const int tmax = a.max_ctx - 1;
-        float vv[NV][CPT];
+    // unconditional loads (no per-lane branches): token indices clamped to
+    // the cache, values past the position masked where they are used
+    auto load_values = [&](int t0, float (&vv)[NV][CPT]) {
         const KV* vt = vb + (size_t)(t0 + ai) * vstep;
         if (t0 + TT <= a.max_ctx) {
 #pragma unroll
@@ -1931,18 +1975,9 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
 #pragma unroll
             for (int n = 0; n < NV; ++n) kv_ldn<KV, CPT>(vb + (size_t)min(t0 + ai + 32 * n, tmax) * vstep, vv[n]);
         }
-        float sv[NS];
-#pragma unroll
-        for (int r = 0; r < NS; ++r) {
-            const int i = tid + 256 * r, g = i / TT, t = t0 + i % TT;
-            sv[r] = sb[(size_t)g * a.head_stride + min(t, tmax)];
-        }
-#pragma unroll
-        for (int r = 0; r < NS; ++r) {
-            const int i = tid + 256 * r, g = i / TT, tt = i % TT;
-            pt[tt * HP + g] = t0 + tt < T ? ggml_exp(sv[r] - mx[g]) * inv[g] : 0.0f;
-        }
-        lds_barrier();
+    };
+    // the chains over one tile, its probabilities staged in pt
+    auto run_chains = [&](int t0, const float (&vv)[NV][CPT]) {
 #pragma unroll
         for (int n = 0; n < NV; ++n) {
             const int tt = ai + 32 * n;
@@ -1963,6 +1998,61 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
                     acc[g][c] = live ? f : acc[g][c];
                 }
         }
+    };
+    float mx[HG], inv[HG];
+    bool tiled = true;
+    if constexpr (FS) {
+        // small batches: the head's statistics computed here (the same
+        // arithmetic as attn_decode_stats_kernel, so the same values) instead
+        // of a launch
+        static_assert(HG == 1, "fused statistics are per head");
+        static_assert(TT <= 4096, "one tile within one statistics span");
+        double total;
+        if (T <= TT) {
+            // one tile: each score loaded once for the statistics and the
+            // probabilities, the values issued right behind the scores so
+            // that their latency overlaps the statistics
+            float e[2][8], x[2][8], vv[NV][CPT];
+            softmax_span_load(sb, 0, T, a.max_ctx, e);
+            load_values(0, vv);
+            softmax_span_stats(e, T, mx[0], inv[0], total, x);
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int tt = 8 * (tid + 256 * r) + i;
+                    if (tt < TT) pt[tt] = x[r][i] * inv[0];
+                }
+            lds_barrier();
+            run_chains(0, vv);
+            tiled = false;
+        } else {
+            softmax_stats(sb, T, a.max_ctx, mx[0], inv[0], total);
+        }
+        if (blockIdx.x == 0 && tid == 0 && (!(total >= 1.0) || !(total < INFINITY))) atomicOr(a.status, 8);
+    } else {
+#pragma unroll
+        for (int g = 0; g < HG; ++g) {
+            mx[g] = a.stats[((size_t)b * a.nq + h0 + g) * 2];
+            inv[g] = a.stats[((size_t)b * a.nq + h0 + g) * 2 + 1];
+        }
+    }
+    for (int t0 = 0; tiled && t0 < T; t0 += TT) {
+        float vv[NV][CPT];
+        load_values(t0, vv);
+        float sv[NS];
+#pragma unroll
+        for (int r = 0; r < NS; ++r) {
+            const int i = tid + 256 * r, g = i / TT, t = t0 + i % TT;
+            sv[r] = sb[(size_t)g * a.head_stride + min(t, tmax)];
+        }
+#pragma unroll
+        for (int r = 0; r < NS; ++r) {
+            const int i = tid + 256 * r, g = i / TT, tt = i % TT;
+            pt[tt * HP + g] = t0 + tt < T ? ggml_exp(sv[r] - mx[g]) * inv[g] : 0.0f;
+        }
+        lds_barrier();
+        run_chains(t0, vv);
         lds_barrier();
     }
 #pragma unroll
