@@ -1432,50 +1432,78 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
     const int quarter = HEAD ? (int)(threadIdx.x >> 8) : (int)(blockIdx.x & 3);
     const int tid = threadIdx.x & 255;
     const int W = a.H * D;
-    // this thread's 16 state values (the bulk of the traffic) are requested
-    // first, so that their latency overlaps the conv, norms and gates
     const int lane = tid & 63, wv = tid >> 6;
     const int jl = wv * 8 + (lane >> 3);  // column within the quarter
     const int j = quarter * 32 + jl;
     const int s = lane & 7;
+    const float* xin = a.proj + (size_t)b * a.proj_stride;
+    float* ring = a.ring + (size_t)b * 3 * W * 4;
+    // The conv and gate inputs are requested first, then this thread's 16
+    // state values (the bulk of the traffic): a wave's loads complete in
+    // issue order, so the conv, norms and gates wait only for their own
+    // inputs while the state is in flight.  HEAD: threads 0..255 own the q/k
+    // channels and 256..383 the value channels, one each; else every thread
+    // owns q/k channel tid and threads < 32 also value channel
+    // quarter*32 + tid.  Loads are unconditional (clamped in range) and each
+    // sum is used on two paths, so that none moves behind the state loads.
+    struct ConvIn {
+        v4f r, w;
+        float x;
+    };
+    auto conv_load = [&](int ch) {
+        ConvIn c;
+        c.r = *(const v4f*)(ring + (size_t)ch * 4);
+        c.w = *(const v4f*)(a.conv_w + (size_t)ch * 4);
+        c.x = xin[ch];
+        return c;
+    };
+    const int ch_qk = tid < D ? h * D + tid : W + h * D + (tid - D);
+    const int vc = HEAD ? max(0, min((int)threadIdx.x - 256, D - 1)) : quarter * 32 + (tid & 31);
+    const int ch_v = 2 * W + h * D + vc;
+    const int ch_a = HEAD && threadIdx.x >= 256 ? ch_v : ch_qk;
+    const ConvIn in_a = conv_load(ch_a);
+    ConvIn in_v;
+    if constexpr (!HEAD) in_v = conv_load(ch_v);
+    const float g_a = xin[4 * W + h], g_b = xin[4 * W + a.H + h], g_dt = a.dt[h], g_sa = a.ssm_a[h];
     float* col = a.state + (((size_t)b * a.H + h) * D + j) * D + 4 * s;
     v4f sv[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) sv[c] = *(const v4f*)(col + 32 * c);
     const int p = a.pos[b];
     const int s0 = (p + 1) & 3, s1 = (p + 2) & 3, s2 = (p + 3) & 3, sw = p & 3;
-    const float* xin = a.proj + (size_t)b * a.proj_stride;
-    float* ring = a.ring + (size_t)b * 3 * W * 4;
-    auto conv = [&](int ch) {
-        const v4f r = *(const v4f*)(ring + (size_t)ch * 4);
-        const float hv[4] = {r.x, r.y, r.z, r.w};
-        const v4f w = *(const v4f*)(a.conv_w + (size_t)ch * 4);
-        const float x = xin[ch];
-        const float t0 = hv[s0] * w.x;
-        const float t1 = hv[s1] * w.y;
-        const float t2 = hv[s2] * w.z;
-        const float t3 = x * w.w;
+    auto conv = [&](const ConvIn& c) {
+        const float hv[4] = {c.r.x, c.r.y, c.r.z, c.r.w};
+        const float t0 = hv[s0] * c.w.x;
+        const float t1 = hv[s1] * c.w.y;
+        const float t2 = hv[s2] * c.w.z;
+        const float t3 = c.x * c.w.w;
         float acc = t0 + t1;
         acc = acc + t2;
         acc = acc + t3;
         return acc;
     };
-    if (!HEAD || quarter == 0) {
-        const int ch = tid < D ? h * D + tid : W + h * D + (tid - D);
-        qk[tid] = ggml_silu(conv(ch));
-        if (quarter == 0) ring[(size_t)ch * 4 + sw] = xin[ch];
-    }
-    if (HEAD ? (quarter == 1 && tid < D) : tid < 32) {
-        const int vc = HEAD ? tid : quarter * 32 + tid;
-        const int ch = 2 * W + h * D + vc;
-        vv[HEAD ? vc : tid] = ggml_silu(conv(ch));
-        ring[(size_t)ch * 4 + sw] = xin[ch];
+    if constexpr (HEAD) {
+        const float cv = conv(in_a);
+        if (threadIdx.x < 256) {
+            qk[threadIdx.x] = ggml_silu(cv);
+            ring[(size_t)ch_qk * 4 + sw] = in_a.x;
+        } else if (threadIdx.x < 256 + D) {
+            vv[vc] = ggml_silu(cv);
+            ring[(size_t)ch_v * 4 + sw] = in_a.x;
+        }
+    } else {
+        qk[tid] = ggml_silu(conv(in_a));
+        if (quarter == 0) ring[(size_t)ch_qk * 4 + sw] = in_a.x;
+        if (tid < 32) {
+            vv[tid] = ggml_silu(conv(in_v));
+            ring[(size_t)ch_v * 4 + sw] = in_v.x;
+        }
     }
     // the head's gates (f64-evaluated transcendentals) once per workgroup,
     // by the wave without value channels
     if (tid == 192 && (!HEAD || quarter == 0)) {
         float gn, bt, sp, gr;
-        gdn_coef(xin[4 * W + h], xin[4 * W + a.H + h], a.dt[h], a.ssm_a[h], gn, bt, sp, gr);
+        gdn_coef(g_a, g_b, g_dt, g_sa, gn, bt, sp, gr);
         gates[0] = gn;
         gates[1] = bt;
     }
