@@ -432,36 +432,50 @@ __global__ __launch_bounds__(256) void fused_q4k_kernel(FusedGemvArgs a, int lpr
 // ============================================================= Q8_0 GEMV
 
 // The workgroup codes MT activation rows into LDS (wg_prologue), then runs
-// gemv_q8_0_kernel's row loop: the bit-exact reference order.
+// gemv_q8_0_kernel's row loop: the bit-exact reference order.  A wave's
+// tiles stream in chunks of QC through two register buffers, the next
+// chunk's loads issued before the current one is consumed; activation row
+// 0's loads go out before the first chunk's and its coding overlaps them (a
+// wave's loads complete in issue order).  Loads are unconditional: a tile
+// past the row end reads the last one and is not consumed.
 template <int MT, int J, int PRO, int EPI>
 __global__ __launch_bounds__(256) void fused_q8_kernel(FusedGemvArgs a) {
+    constexpr int QC = 8;
     extern __shared__ int lds_f8[];
     const int K = a.K, N = a.N;
     const int nb = K >> 5, nbc = (nb + 3) >> 2;
     int* codes = lds_f8;                               // [MT][K/4] words
     float* scales = (float*)(lds_f8 + MT * (K >> 2));  // [MT][nb]
     const int m0 = blockIdx.y * MT;
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-        wg_prologue<PRO, kCodecQ8, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * (K >> 2), scales + m * nb);
     const v4i* qs = (const v4i*)a.qs;
     const uint16_t* hdr = (const uint16_t*)a.hdr;
     const int lane = threadIdx.x & 63;
     const int rl = lane >> 3, l = lane & 7;
     const int groups = (N + 7) >> 3;
     const int nwaves = gridDim.x * 4;
-    for (int R = blockIdx.x * 4 + (threadIdx.x >> 6); R < groups; R += nwaves) {
-        const int row = R * 8 + rl;
-        const uint16_t* hrow = hdr + (size_t)(row < N ? row : N - 1) * nbc * 4;
-        const v4i* tile = qs + (size_t)R * nbc * 64 + lane;
-        float acc[MT];
+    struct Chunk {
+        v4i w[QC];
+        uint2 h[QC];
+    };
+    auto load_chunk = [&](int R, int c0, Chunk& ck) {
+        const int row = min(R * 8 + rl, N - 1);
+        const uint16_t* hrow = hdr + (size_t)row * nbc * 4;
+        const v4i* tile = qs + (size_t)min(R, groups - 1) * nbc * 64 + lane;
 #pragma unroll
-        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
-        for (int c = 0; c < nbc; ++c) {
-            const v4i w4 = load_nt(tile + (size_t)c * 64);
-            const uint2 h2 = *(const uint2*)(hrow + 4 * c);
-            const int ww[4] = {w4.x, w4.y, w4.z, w4.w};
-            const uint32_t hw[4] = {h2.x & 0xffffu, h2.x >> 16, h2.y & 0xffffu, h2.y >> 16};
+        for (int i = 0; i < QC; ++i) {
+            const int c = min(c0 + i, nbc - 1);
+            ck.w[i] = load_nt(tile + (size_t)c * 64);
+            ck.h[i] = *(const uint2*)(hrow + 4 * c);
+        }
+    };
+    float acc[MT];
+    auto consume = [&](const Chunk& ck, int c0) {
+#pragma unroll
+        for (int i = 0; i < QC; ++i) {
+            const int c = c0 + i;
+            if (c >= nbc) break;  // uniform
+            const int ww[4] = {ck.w[i].x, ck.w[i].y, ck.w[i].z, ck.w[i].w};
+            const uint32_t hw[4] = {ck.h[i].x & 0xffffu, ck.h[i].x >> 16, ck.h[i].y & 0xffffu, ck.h[i].y >> 16};
 #pragma unroll
             for (int bi = 0; bi < 4; ++bi) {
                 const int b = 4 * c + bi;
@@ -475,6 +489,28 @@ __global__ __launch_bounds__(256) void fused_q8_kernel(FusedGemvArgs a) {
                     }
                 }
             }
+        }
+    };
+    ProIn<J> pin;
+    wg_prologue_load<PRO, J>(a, m0, m0 < a.M, pin);
+    const int R0 = blockIdx.x * 4 + (threadIdx.x >> 6);
+    Chunk ca, cb;
+    load_chunk(R0, 0, ca);
+    wg_prologue_code<PRO, kCodecQ8, J>(a, m0 < a.M, pin, nullptr, codes, scales);
+#pragma unroll
+    for (int m = 1; m < MT; ++m)
+        wg_prologue<PRO, kCodecQ8, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * (K >> 2), scales + m * nb);
+    for (int R = R0; R < groups; R += nwaves) {
+        if (R != R0) load_chunk(R, 0, ca);
+        const int row = R * 8 + rl;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+        for (int c0 = 0; c0 < nbc; c0 += 2 * QC) {
+            if (c0 + QC < nbc) load_chunk(R, c0 + QC, cb);
+            consume(ca, c0);
+            if (c0 + QC >= nbc) break;
+            if (c0 + 2 * QC < nbc) load_chunk(R, c0 + 2 * QC, ca);
+            consume(cb, c0 + QC);
         }
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[m] = group8_tree_last(acc[m]);  // the reference's lane tree, in lane 7
@@ -1284,12 +1320,13 @@ static hipError_t launch_q4k(const FusedGemvArgs& a, hipStream_t s) {
     if (ch > 2) return hipErrorInvalidValue;
     int mt = a.M == 1 ? 1 : (a.M == 2 ? 2 : 4);
     while (mt > 1 && ch * mt > 4) mt >>= 1;
-    // B=1: up to 4 row groups per wave so that ~2048 waves cover the matrix
-    // (fewer workgroups repeating the prologue, more loads in flight)
+    // B=1: up to 4 row groups per wave so that ~4096 waves cover the matrix
+    // (fewer workgroups repeating the prologue, more loads in flight per
+    // wave; measured best against ~2048 waves and one group per wave)
     const size_t rpw = 64u >> l, groups = (a.N + rpw - 1) / rpw;
     int rg = 1;
     if (mt == 1) {
-        while (rg < 4 && groups > (size_t)2048 * rg) rg *= 2;
+        while (rg < 4 && groups > (size_t)4096 * rg) rg *= 2;
     }
     const size_t waves = (groups + rg - 1) / rg;
     const unsigned wgs = (unsigned)std::min<size_t>((waves + 3) / 4, 256 * 8);
