@@ -2009,7 +2009,28 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
     constexpr int D = 256, TT = 32 * NV, CB = 8 * CPT, NS = HG * TT / 256, HP = HG == 3 ? 4 : HG;
     __shared__ float pt[TT * HP];
     __shared__ float red[HG][CB][33];
-    const int h0 = blockIdx.y * HG, b = blockIdx.z;
+    // XCD-aware order: workgroup L (dispatch order) runs on XCD L % 8, so the
+    // logical ids are dealt to give each XCD a contiguous range, in which the
+    // heads of one kv head vary fastest (HG == 1), then the channel groups:
+    // the workgroups that share V's cache lines (adjacent channel groups, the
+    // heads of a kv head) then share one XCD's L2 and each line is fetched
+    // once, not once per XCD.
+    const unsigned nx = gridDim.x, ny = gridDim.y, nwg = nx * ny * gridDim.z;
+    const unsigned lin = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+    const unsigned q = nwg % 8 ? lin : (lin % 8) * (nwg / 8) + lin / 8;
+    int cgx, h0, b;
+    if constexpr (HG == 1) {
+        const unsigned G = (unsigned)(a.nq / a.nkv);
+        const unsigned g = q % G, r = q / G;
+        cgx = (int)(r % nx);
+        const unsigned r2 = r / nx;
+        h0 = (int)((r2 % (unsigned)a.nkv) * G + g);
+        b = (int)(r2 / (unsigned)a.nkv);
+    } else {
+        cgx = (int)(q % nx);
+        h0 = (int)((q / nx) % ny) * HG;
+        b = (int)(q / (nx * ny));
+    }
     const int kvh = h0 / (a.nq / a.nkv);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int T = a.pos[b] + 1;
@@ -2017,10 +2038,10 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
     float gate = 0.0f;
     if (tid < HG * CB) {
         const int g = tid / CB, c = tid % CB;
-        gate = a.proj[(size_t)b * a.proj_stride + (size_t)(h0 + g) * 2 * D + D + blockIdx.x * CB + c];
+        gate = a.proj[(size_t)b * a.proj_stride + (size_t)(h0 + g) * 2 * D + D + cgx * CB + c];
     }
     const int cq = lane >> 3, ai = wv * 8 + (lane & 7);
-    const int j0 = blockIdx.x * CB + cq * CPT;
+    const int j0 = cgx * CB + cq * CPT;
     const KV* vb = (const KV*)a.vcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D + j0;
     const size_t vstep = (size_t)a.nkv * D;
     const int tmax = a.max_ctx - 1;
@@ -2094,7 +2115,7 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
         } else {
             softmax_stats(sb, T, a.max_ctx, mx[0], inv[0], total);
         }
-        if (blockIdx.x == 0 && tid == 0 && (!(total >= 1.0) || !(total < INFINITY))) atomicOr(a.status, 8);
+        if (cgx == 0 && tid == 0 && (!(total >= 1.0) || !(total < INFINITY))) atomicOr(a.status, 8);
     } else {
 #pragma unroll
         for (int g = 0; g < HG; ++g) {
@@ -2134,9 +2155,9 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
         const float h0s = comb[0] + comb[4], h1 = comb[1] + comb[5], h2 = comb[2] + comb[6], h3 = comb[3] + comb[7];
         float v = (h0s + h1) + (h2 + h3);
         v = v * source_sigmoid(gate);
-        a.out[(size_t)b * a.out_stride + (size_t)(h0 + g) * D + blockIdx.x * CB + c] = v;
+        a.out[(size_t)b * a.out_stride + (size_t)(h0 + g) * D + cgx * CB + c] = v;
         if (a.xh) {
-            const int k = (h0 + g) * D + blockIdx.x * CB + c, m = b, K = a.nq * D;
+            const int k = (h0 + g) * D + cgx * CB + c, m = b, K = a.nq * D;
             const size_t lane_t = (size_t)((k & 15) >> 3) * 32 + (m & 31);
             const size_t at = ((((size_t)(m >> 5) * (K >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + lane_t) * 8 + (k & 7);
             ((_Float16*)a.xh)[at] = (_Float16)v;
