@@ -1311,13 +1311,21 @@ static hipError_t launch_codec(const FusedGemvArgs& a, int type, hipStream_t s) 
 
 template <int PRO, int EPI>
 static hipError_t launch_q4k(const FusedGemvArgs& a, hipStream_t s) {
-    // one 64-element chunk per lane while the row fits 64 lanes (K <= 4096),
-    // else two; activation slabs J = ceil(K / 1024) rounded to 2, 4, 8
+    // lpr = 2^l lanes per row, ch 64-element chunks per lane: the pair with
+    // the fewest idle chunk slots (ch * lpr - nchunk), fewer chunks per lane
+    // on a tie (K = 6144: 32 lanes x 3 chunks, not 64 x 2 with a quarter
+    // idle); activation slabs J = ceil(K / 1024) rounded to 2, 4, 8
     const int nchunk = a.K / 64;
-    int l = 2;
-    while (l < 6 && (1 << l) < nchunk) ++l;
-    const int ch = (nchunk + (1 << l) - 1) >> l;
-    if (ch > 2) return hipErrorInvalidValue;
+    int l = -1, ch = 0;
+    for (int t = 6; t >= 2; --t) {
+        const int c = (nchunk + (1 << t) - 1) >> t;
+        if (c > 3) break;
+        if (l < 0 || c * (1 << t) - nchunk < ch * (1 << l) - nchunk) {
+            l = t;
+            ch = c;
+        }
+    }
+    if (l < 0 || a.K > 8192) return hipErrorInvalidValue;
     int mt = a.M == 1 ? 1 : (a.M == 2 ? 2 : 4);
     while (mt > 1 && ch * mt > 4) mt >>= 1;
     // B=1: up to 4 row groups per wave so that ~4096 waves cover the matrix
@@ -1337,7 +1345,13 @@ static hipError_t launch_q4k(const FusedGemvArgs& a, hipStream_t s) {
     if (rg == 1) ZG_F4(C, 1, JJ, 1);      \
     else if (rg == 2) ZG_F4(C, 1, JJ, 2); \
     else ZG_F4(C, 1, JJ, 4);
-    if (ch == 2) {
+    if (ch == 3) {
+        if (a.K <= 4096) {
+            ZG_F4R(3, 4)
+        } else {
+            ZG_F4R(3, 8)
+        }
+    } else if (ch == 2) {
         if (mt == 1) {
             ZG_F4R(2, 8)
         } else {
