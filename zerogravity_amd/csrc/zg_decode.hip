@@ -43,7 +43,7 @@ __device__ __forceinline__ void epilogue(const FusedGemvArgs& a, int m, int row,
 // ================================================ workgroup prologue
 
 constexpr int kCodecQ4K = 0, kCodecQ8 = 1, kCodecQ81 = 2, kCodecQ8K = 3, kCodecF32 = 4;
-constexpr int kRecWords = 36;  // Q4_K record: 32 dwords of int16 pairs + {xs_lo, xs_hi, sum_lo, sum_hi}
+constexpr int kRecWords = 36;  // Q4_K record: 32 dwords of code bytes + {xs_lo, xs_hi, sum_lo, sum_hi}
 
 // Activation row m prepared once per workgroup.  Thread t holds the float4
 // slabs k = 4t + 1024j (all loads issued together), so the 8 threads of a
@@ -60,9 +60,11 @@ constexpr int kRecWords = 36;  // Q4_K record: 32 dwords of int16 pairs + {xs_lo
 //     the sums of 16 codes in `bsums` [K/16].
 //   F32: the values themselves, floats [K] at `codes`.
 //   Q4_K: per 32-group int16 fixed point, xq = rint(v*32767/amax), with the
-//     group's scale amax/32767 and its f32 sum; records [K/64][36] dwords in
-//     the pairing gemv_q4k_kernel expects (element e of a group goes to
-//     dword (e&1 ? 8 : 0) + e/4, half (e>>1)&1; high group +16).
+//     group's scale amax/32767 and its f32 sum; records [K/64][36] dwords:
+//     xq = 256*hi + lo split into bytes, dword e/4 holding the signed high
+//     bytes of elements e..e+3 (e % 4 == 0), dword 8 + e/4 their unsigned
+//     low bytes, the pair's high group +16, then {scale lo, scale hi,
+//     sum lo, sum hi}.
 // Ends with a barrier.  K <= 1024 * JMAX, K % 32 == 0 (K % 256 for Q8_K).
 //
 // The loads are a phase of their own (wg_prologue_load) so that a kernel can
@@ -233,12 +235,18 @@ __device__ void wg_prologue_code(const FusedGemvArgs& a, bool valid, const ProIn
             sum = group8_sum_all(sum);
             if (k < K) {
                 const float qi = amax == 0.0f ? 0.0f : 32767.0f / amax;
-                const int q0 = (int)rintf(e[0] * qi), q1 = (int)rintf(e[1] * qi);
-                const int q2 = (int)rintf(e[2] * qi), q3 = (int)rintf(e[3] * qi);
+                const int q[4] = {(int)rintf(e[0] * qi), (int)rintf(e[1] * qi), (int)rintf(e[2] * qi),
+                                  (int)rintf(e[3] * qi)};
                 const int g = k >> 5, hi = g & 1;
                 uint32_t* r = rec + (size_t)(g >> 1) * kRecWords;
-                r[hi * 16 + l] = ((uint32_t)q0 & 0xffffu) | ((uint32_t)q2 << 16);
-                r[hi * 16 + 8 + l] = ((uint32_t)q1 & 0xffffu) | ((uint32_t)q3 << 16);
+                uint32_t hb = 0, lb = 0;  // q = 256 * (q >> 8) + (q & 255)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    hb |= ((uint32_t)(q[t] >> 8) & 0xffu) << (8 * t);
+                    lb |= ((uint32_t)q[t] & 0xffu) << (8 * t);
+                }
+                r[hi * 16 + l] = hb;
+                r[hi * 16 + 8 + l] = lb;
                 if (l == 0) {
                     r[32 + hi] = __float_as_uint(amax / 32767.0f);
                     r[34 + hi] = __float_as_uint(sum);
@@ -260,13 +268,16 @@ __device__ __forceinline__ void wg_prologue(const FusedGemvArgs& a, int m, bool 
 // ============================================================= Q4_K GEMV
 
 // Lanes: `lpr` per row, chunk c = sub + i*lpr (i < CH) is the group pair
-// (2p, 2p+1) of block c/4: elements 64c .. 64c+63; the nibble/int16 pairing
-// and the per-group epilogue are gemv_q4k_kernel's.  The workgroup codes the
-// activation into LDS once (its weight loads for the first row group are
-// already in flight), each lane copies its chunk records to registers.
+// (2p, 2p+1) of block c/4: elements 64c .. 64c+63; the per-group epilogue
+// is gemv_q4k_kernel's.  Weight byte e of the chunk holds element e of the
+// low group (low nibble) and of the high group (high nibble), so a weight
+// dword masked to its low or high nibbles meets the activation record's
+// byte dwords lane for lane in one signed and one unsigned 4-way dot.  The
+// workgroup codes the activation into LDS once (its weight loads for the
+// first row group are already in flight), each lane copies its chunk
+// records to registers.
 template <int CH, int MT, int J, int RG, int PRO, int EPI>
 __global__ __launch_bounds__(256) void fused_q4k_kernel(FusedGemvArgs a, int lpr_log2) {
-    typedef short v2s __attribute__((ext_vector_type(2)));
     extern __shared__ uint32_t lds_q4[];
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << lpr_log2;
@@ -374,23 +385,32 @@ __global__ __launch_bounds__(256) void fused_q4k_kernel(FusedGemvArgs a, int lpr
                 const uint32_t ww[8] = {(uint32_t)w0[r][i].x, (uint32_t)w0[r][i].y, (uint32_t)w0[r][i].z,
                                         (uint32_t)w0[r][i].w, (uint32_t)w1[r][i].x, (uint32_t)w1[r][i].y,
                                         (uint32_t)w1[r][i].z, (uint32_t)w1[r][i].w};
-                int ilo[MT], ihi[MT];
+                // sum of nibble * xq over each group, exactly: 256 * (nibbles .
+                // signed high bytes) + (nibbles . unsigned low bytes)
+                int ilo_h[MT], ihi_h[MT];
+                uint32_t ilo_l[MT], ihi_l[MT];
 #pragma unroll
-                for (int m = 0; m < MT; ++m) ilo[m] = ihi[m] = 0;
+                for (int m = 0; m < MT; ++m) {
+                    ilo_h[m] = ihi_h[m] = 0;
+                    ilo_l[m] = ihi_l[m] = 0u;
+                }
 #pragma unroll
                 for (int q = 0; q < 8; ++q) {
                     const uint32_t d = ww[q];
-                    const v2s L0 = __builtin_bit_cast(v2s, d & 0x000f000fu);
-                    const v2s L1 = __builtin_bit_cast(v2s, (d >> 8) & 0x000f000fu);
-                    const v2s H0 = __builtin_bit_cast(v2s, (d >> 4) & 0x000f000fu);
-                    const v2s H1 = __builtin_bit_cast(v2s, (d >> 12) & 0x000f000fu);
+                    const uint32_t wl = d & 0x0f0f0f0fu, wh = (d >> 4) & 0x0f0f0f0fu;
 #pragma unroll
                     for (int m = 0; m < MT; ++m) {
-                        ilo[m] = __builtin_amdgcn_sdot2(L0, __builtin_bit_cast(v2s, xl0[m][i][q]), ilo[m], false);
-                        ilo[m] = __builtin_amdgcn_sdot2(L1, __builtin_bit_cast(v2s, xl1[m][i][q]), ilo[m], false);
-                        ihi[m] = __builtin_amdgcn_sdot2(H0, __builtin_bit_cast(v2s, xh0[m][i][q]), ihi[m], false);
-                        ihi[m] = __builtin_amdgcn_sdot2(H1, __builtin_bit_cast(v2s, xh1[m][i][q]), ihi[m], false);
+                        ilo_h[m] = __builtin_amdgcn_sdot4((int)wl, xl0[m][i][q], ilo_h[m], false);
+                        ilo_l[m] = __builtin_amdgcn_udot4(wl, (uint32_t)xl1[m][i][q], ilo_l[m], false);
+                        ihi_h[m] = __builtin_amdgcn_sdot4((int)wh, xh0[m][i][q], ihi_h[m], false);
+                        ihi_l[m] = __builtin_amdgcn_udot4(wh, (uint32_t)xh1[m][i][q], ihi_l[m], false);
                     }
+                }
+                int ilo[MT], ihi[MT];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    ilo[m] = ilo_h[m] * 256 + (int)ilo_l[m];
+                    ihi[m] = ihi_h[m] * 256 + (int)ihi_l[m];
                 }
                 uint32_t sc0, mn0, sc1, mn1;
                 q4k_dev_scale_min(h[r][i], 2 * p, sc0, mn0);
