@@ -2084,16 +2084,18 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
     for (int g = 0; g < HG; ++g)
 #pragma unroll
         for (int c = 0; c < CPT; ++c) acc[g][c] = 0.0f;
-    // unconditional loads (no per-lane branches): token indices clamped to
-    // the cache, values past the position masked where they are used
+    // unconditional loads (no branches: a load in a branch is followed by a
+    // wait there), token indices clamped to the last token, so that rows
+    // past the position reread a line already in cache; their values are
+    // masked where they are used
     auto load_values = [&](int t0, float (&vv)[NV][CPT]) {
         const KV* vt = vb + (size_t)(t0 + ai) * vstep;
-        if (t0 + TT <= a.max_ctx) {
+        if (t0 + TT <= T) {
 #pragma unroll
             for (int n = 0; n < NV; ++n) kv_ldn<KV, CPT>(vt + (size_t)(32 * n) * vstep, vv[n]);
         } else {
 #pragma unroll
-            for (int n = 0; n < NV; ++n) kv_ldn<KV, CPT>(vb + (size_t)min(t0 + ai + 32 * n, tmax) * vstep, vv[n]);
+            for (int n = 0; n < NV; ++n) kv_ldn<KV, CPT>(vb + (size_t)min(t0 + ai + 32 * n, T - 1) * vstep, vv[n]);
         }
     };
     // the chains over one tile, its probabilities staged in pt
