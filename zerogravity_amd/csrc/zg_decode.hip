@@ -2123,6 +2123,7 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
     };
     float mx[HG], inv[HG];
     bool tiled = true;
+    float gate_s = 0.0f;
     if constexpr (FS) {
         // small batches: the head's statistics computed here (the same
         // arithmetic as attn_decode_stats_kernel, so the same values) instead
@@ -2137,6 +2138,9 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
             float e[2][8], x[2][8], vv[NV][CPT];
             softmax_span_load(sb, 0, T, a.max_ctx, e);
             load_values(0, vv);
+            // the output gate (an f64 exp) while the scores and values are
+            // in flight (the gate was loaded first)
+            gate_s = source_sigmoid(gate);
             softmax_span_stats(e, T, mx[0], inv[0], total, x);
 #pragma unroll
             for (int r = 0; r < 2; ++r)
@@ -2190,7 +2194,7 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
         for (int l = 0; l < 8; ++l) comb[l] = (r[l] + r[16 + l]) + (r[8 + l] + r[24 + l]);
         const float h0s = comb[0] + comb[4], h1 = comb[1] + comb[5], h2 = comb[2] + comb[6], h3 = comb[3] + comb[7];
         float v = (h0s + h1) + (h2 + h3);
-        v = v * source_sigmoid(gate);
+        v = v * (tiled ? source_sigmoid(gate) : gate_s);
         a.out[(size_t)b * a.out_stride + (size_t)(h0 + g) * D + cgx * CB + c] = v;
         if (a.xh) {
             const int k = (h0 + g) * D + cgx * CB + c, m = b, K = a.nq * D;
