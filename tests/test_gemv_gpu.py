@@ -127,12 +127,17 @@ def test_gemv_device_rms_prologue_bf16(kern, torch_cuda, kind, N, K, M):
 @pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("N,K,M", [(3584, 1024, m) for m in (1, 3, 16, 32, 1024, 1056)] +
                          [(2048, 6144, m) for m in (1, 3, 16, 32, 2048)] +
-                         [(151936, 2048, m) for m in (1, 3, 16, 32)] + [(8224, 2048, 1088)])
+                         [(151936, 2048, m) for m in (1, 3, 16, 32)] + [(8224, 2048, 1088)] +
+                         [(1000, 3072, m) for m in (1, 3)] + [(777, 5120, m) for m in (1, 4)] +
+                         [(513, 8192, 1), (1030, 1536, 1), (70, 256, 2)])
 def test_gemv_device_f32_decode_kernels(kern, torch_cuda, kind, N, K, M):
     """f32 activations take the decode-step kernels (in-kernel RMS prologue;
     Q4_K beyond 4 rows on the f16 MFMA path, the LDS-staged variant from
     1024 rows: 4, 1, 4 and 2 activation blocks per workgroup at M = 1024,
-    1056, 2048 and 1088)."""
+    1056, 2048 and 1088).  Up to 4 rows the Q4_K lanes per row and chunks
+    per lane follow K: 16 x 3 at K = 3072, 32 x 3 at 5120 and 6144, 64 x 2 at
+    8192, 32 x 1 at 1536 and 2048, 4 x 1 at 256; N not a multiple of the rows
+    per wave exercises the clamped loads of rows past N."""
     torch = torch_cuda
     w, h = weight(kern, kind, N, K)
     rng = np.random.default_rng(M * 11 + N)
