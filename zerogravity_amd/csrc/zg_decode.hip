@@ -636,7 +636,9 @@ __global__ __launch_bounds__(256) void act16_kernel(FusedGemvArgs a, _Float16* _
 #pragma unroll
             for (int t = 0; t < 4; ++t) hv4[t] = valid ? (_Float16)e[t] : (_Float16)0.0f;
             const size_t lane_t = (size_t)((k & 15) >> 3) * 32 + (m & 31);
-            const size_t at = ((((size_t)(m >> 5) * (K >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + lane_t) * 8 + (k & 7);
+            const size_t at = a.xh_rows ? (size_t)m * K + k
+                                        : ((((size_t)(m >> 5) * (K >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 +
+                                           lane_t) * 8 + (k & 7);
             *(h4v*)(xh + at) = hv4;
         }
     }
@@ -991,9 +993,63 @@ static void launch_act16(const FusedGemvArgs& a, int mpad, _Float16* xh, hipStre
     else hipLaunchKernelGGL((act16_kernel<PRO, 8>), dim3(mpad), dim3(256), 0, s, a, xh);
 }
 
+// up * silu(gate) of the library gate/up GEMM's f16 rows [M][2F] (gate
+// columns first), rounded to f16 row-major [M][F]: the down GEMM's operand
+// (the EPI_GLU epilogue's arithmetic on f16-rounded gate and up)
+__global__ void glu16_kernel(const _Float16* __restrict__ gu, size_t M, size_t F, _Float16* __restrict__ out) {
+    typedef _Float16 h8v_t __attribute__((ext_vector_type(8)));
+    const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (i >= M * F) return;
+    const size_t m = i / F, j = i % F;
+    const h8v_t g = *(const h8v_t*)(gu + m * 2 * F + j);
+    const h8v_t u = *(const h8v_t*)(gu + m * 2 * F + F + j);
+    h8v_t o;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) o[t] = (_Float16)((float)u[t] * ggml_silu((float)g[t]));
+    *(h8v_t*)(out + i) = o;
+}
+
+// Prompt-sized M with the f16 weight present: hipBLASLt on row-major f16
+// activations (the activation kernel's values in row order, or the previous
+// gate/up GEMM's product), f32 accumulation; EPI_RESID adds into y (beta 1).
+static hipError_t blas_batched(const DeviceWeight& w, FusedGemvArgs a, void* scratch, hipStream_t s) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const int mpad = (a.M + 31) / 32 * 32;
+    const _Float16* xh = (const _Float16*)a.xh_in;
+    if (!xh) {
+        a.xh_rows = 1;
+        switch (a.pro) {
+        case PRO_RMS: launch_act16<PRO_RMS>(a, mpad, (_Float16*)scratch, s); break;
+        case PRO_GATED: launch_act16<PRO_GATED>(a, mpad, (_Float16*)scratch, s); break;
+        case PRO_SILU_MUL: launch_act16<PRO_SILU_MUL>(a, mpad, (_Float16*)scratch, s); break;
+        case PRO_PLAIN: launch_act16<PRO_PLAIN>(a, mpad, (_Float16*)scratch, s); break;
+        default: return hipErrorInvalidValue;
+        }
+        xh = (const _Float16*)scratch;
+    }
+    if (a.epi == EPI_GLU) {
+        if (!a.xh_out || a.N % 16) return hipErrorInvalidValue;
+        e = blas_gemm_f16(dev, a.M, a.N, a.K, xh, w.w16, a.y, false, (size_t)a.N, 0.0f, s);
+        if (e != hipSuccess) return e;
+        const size_t F = (size_t)a.N / 2, n8 = (size_t)a.M * F / 8;
+        hipLaunchKernelGGL(glu16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const _Float16*)a.y,
+                           (size_t)a.M, F, (_Float16*)a.xh_out);
+        return hipGetLastError();
+    }
+    return blas_gemm_f16(dev, a.M, a.N, a.K, xh, w.w16, a.y, true, a.ldy, a.epi == EPI_RESID ? 1.0f : 0.0f, s);
+}
+
 hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* scratch, hipStream_t s) {
     if (w.type != kQ4_K || w.K % 256 || w.K > 8192 || args.M <= 0 || args.M > 65535 * 32) return hipErrorInvalidValue;
     if (args.pro == PRO_GATED && args.group != 128) return hipErrorInvalidValue;
+    if (w.w16 && args.M >= kBlasRows && !(args.epi == EPI_RESID && args.splits > 1 && args.parts)) {
+        FusedGemvArgs a = args;
+        a.K = (int)w.K;
+        a.N = (int)w.N;
+        return blas_batched(w, a, scratch, s);
+    }
     if (!w.qs_t || !w.hdr_t) return hipErrorNotReady;  // ensure_mfma_tiles first
     FusedGemvArgs a = args;
     a.qs = w.qs_t;

@@ -30,6 +30,10 @@ struct DeviceWeight {
     // headers in the MFMA operand order of 32-row tiles (ensure_mfma_tiles).
     void* qs_t = nullptr;
     void* hdr_t = nullptr;
+    // Q4_K only, built on demand for prompt-sized batched prefill: the exact
+    // dequantized weight rounded once to f16, row-major [N][K], the operand
+    // of the library GEMM (ensure_f16_weight).
+    void* w16 = nullptr;
 };
 
 size_t gguf_row_bytes(int type, size_t K);
@@ -41,6 +45,20 @@ hipError_t repack_weight(const uint8_t* d_gguf, DeviceWeight& w, int* d_bad, hip
 // Exact dequantization of rows [row0, row0+rows) of a registered weight into
 // f32 [rows][K].
 hipError_t dequantize_rows(const DeviceWeight& w, size_t row0, size_t rows, float* out, hipStream_t s);
+
+// Activation rows from which batched_gemv takes the library GEMM when the
+// weight's f16 copy exists.
+constexpr int kBlasRows = 512;
+
+// Q4_K: allocates and fills w.w16 (no-op when present).
+hipError_t ensure_f16_weight(DeviceWeight& w, hipStream_t s);
+
+// D (+)= A . W^T through hipBLASLt: A f16 row-major [M][K] (ld K), W f16
+// row-major [N][K] (ld K), D row-major [M][N] with leading dimension ldd,
+// f32 (beta 0 or 1, C = D) or f16 (beta 0); f32 accumulation.  One library
+// handle and 64 MB workspace per device, algorithms cached per shape.
+hipError_t blas_gemm_f16(int device, int M, int N, int K, const void* A, const void* W, void* D, bool d_f32,
+                         size_t ldd, float beta, hipStream_t s);
 
 // Activation preparation for M rows of width K: optional RMSNorm with gamma
 // (f64 sum of f32 squares, f32 mean, 1/sqrtf, (x*inv)*gamma), then any of:
@@ -168,6 +186,7 @@ struct FusedGemvArgs {
     float* xw = nullptr;
     void* xh_out = nullptr;      // EPI_GLU, batched: f16 tiled product
     const void* xh_in = nullptr;  // batched: f16 tiled activation ready (no activation kernel)
+    int xh_rows = 0;              // activation kernel: f16 row-major [M][K] instead of MFMA tiles
 };
 // EPI_GLU offered for these shapes (fused path: K <= 2048 so a row group
 // holds a gate and an up row; batched path: N/2 a multiple of 32).

@@ -756,6 +756,12 @@ int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* toke
     hipStream_t st = ctx->stream;
     for (zg_weight* w : ws)
         if (!w->dw.qs_t) ZG_HIP(zg::ensure_mfma_tiles(w->dw, st));
+    // prompt-sized calls run every projection through the library GEMM on
+    // f16 copies of the weights, made once (all four of a layer together, so
+    // that the gate/up and down GEMMs agree on the activation layout)
+    if (n >= (size_t)zg::kBlasRows)
+        for (zg_weight* w : ws)
+            if (!w->dw.w16) ZG_HIP(zg::ensure_f16_weight(w->dw, st));
     const size_t H = g.hidden, F = g.ffn, W = (size_t)g.gdn_heads * g.gdn_dim, GH = g.gdn_heads;
     const size_t QD = (size_t)g.q_heads * g.head_dim;
     const size_t mpad = (n + 31) / 32 * 32;
