@@ -8,6 +8,8 @@
 // to the end-to-end tolerance, not to the bits.
 #include <algorithm>
 
+#include <type_traits>
+
 #include "zg_device.hpp"
 #include "zg_internal.hpp"
 #include "zg_pointwise.hpp"
@@ -168,6 +170,26 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(const float* __r
     }
 }
 
+// Four cache elements in storage form (loaded ahead, converted when staged).
+template <typename KV>
+struct KVRaw4 {
+    typename std::conditional<sizeof(KV) == 2, uint2, v4f>::type v;
+    __device__ __forceinline__ void load(const KV* p) { v = *(const decltype(v)*)p; }
+    __device__ __forceinline__ void get(float (&o)[4]) const {
+        if constexpr (sizeof(KV) == 2) {
+            o[0] = __uint_as_float(v.x << 16);
+            o[1] = __uint_as_float(v.x & 0xffff0000u);
+            o[2] = __uint_as_float(v.y << 16);
+            o[3] = __uint_as_float(v.y & 0xffff0000u);
+        } else {
+            o[0] = v.x;
+            o[1] = v.y;
+            o[2] = v.z;
+            o[3] = v.w;
+        }
+    }
+};
+
 typedef _Float16 ah4 __attribute__((ext_vector_type(4)));
 typedef _Float16 ah8 __attribute__((ext_vector_type(8)));
 typedef float af16 __attribute__((ext_vector_type(16)));
@@ -197,8 +219,12 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
     constexpr int VROW = KB + 8;  // halves per staged value column
     __shared__ _Float16 ks[KB * KROW];
     __shared__ _Float16 vt[D * VROW];
-    const int kvh = blockIdx.y, g = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int h = kvh * G + g, t0 = blockIdx.x * QT;
+    // the heaviest (latest) query tiles first, both kv heads of a tile
+    // together, so that the causal tail is short
+    const int lin = blockIdx.x + gridDim.x * blockIdx.y;
+    const int kvh = lin % (int)gridDim.y, tile = (int)gridDim.x - 1 - lin / (int)gridDim.y;
+    const int g = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int h = kvh * G + g, t0 = tile * QT;
     const int hs = lane >> 5, c = lane & 31;
     const int tq = min(t0 + c, n - 1);
     ah8 qf[16];
@@ -223,18 +249,54 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
     const size_t kstep = (size_t)nkv * D;
     const KV* kb_ = kc + (size_t)kvh * D;
     const KV* vb_ = vc + (size_t)kvh * D;
+    // this thread's share of a 32-key block: PF (key, 4-dim) slots of K and
+    // V, kept in storage form; the next block's share is loaded while the
+    // current one is computed where the slots divide evenly over the threads
+    // and fit the registers (4 heads per kv head; 2 with a bf16 cache)
+    constexpr int PF = KB * D / 4 / (64 * G);
+    constexpr bool AHEAD = G == 4 || (G == 2 && sizeof(KV) == 2);
+    static_assert(!AHEAD || PF * 64 * G == KB * D / 4, "slots divide over the threads");
+    KVRaw4<KV> kr[AHEAD ? PF : 1], vr[AHEAD ? PF : 1];
+    auto load_share = [&](int b) {
+#pragma unroll
+        for (int it = 0; it < PF; ++it) {
+            const int idx = threadIdx.x + it * 64 * G;
+            const int key = idx / (D / 4), d4 = (idx % (D / 4)) * 4;
+            const int j = min(b * KB + key, kend - 1);  // past the last key: a copy, masked below
+            kr[it].load(kb_ + (size_t)j * kstep + d4);
+            vr[it].load(vb_ + (size_t)j * kstep + d4);
+        }
+    };
+    if constexpr (AHEAD) load_share(0);
     for (int b = 0; b < nblk; ++b) {
         const int j0 = b * KB;
         __syncthreads();  // the previous block's tiles are consumed
-        for (int idx = threadIdx.x; idx < KB * D / 4; idx += 64 * G) {
-            const int key = idx / (D / 4), d4 = (idx % (D / 4)) * 4;
-            const int j = min(j0 + key, kend - 1);  // past the last key: a copy, masked below
-            float kv4[4], vv4[4];
-            kv_load4(kb_ + (size_t)j * kstep + d4, kv4);
-            kv_load4(vb_ + (size_t)j * kstep + d4, vv4);
-            *(ah4*)(ks + key * KROW + d4) = ah4{(_Float16)kv4[0], (_Float16)kv4[1], (_Float16)kv4[2], (_Float16)kv4[3]};
+        if constexpr (AHEAD) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) vt[(d4 + i) * VROW + key] = (_Float16)vv4[i];
+            for (int it = 0; it < PF; ++it) {
+                const int idx = threadIdx.x + it * 64 * G;
+                const int key = idx / (D / 4), d4 = (idx % (D / 4)) * 4;
+                float kv4[4], vv4[4];
+                kr[it].get(kv4);
+                vr[it].get(vv4);
+                *(ah4*)(ks + key * KROW + d4) =
+                    ah4{(_Float16)kv4[0], (_Float16)kv4[1], (_Float16)kv4[2], (_Float16)kv4[3]};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) vt[(d4 + i) * VROW + key] = (_Float16)vv4[i];
+            }
+            if (b + 1 < nblk) load_share(b + 1);
+        } else {
+            for (int idx = threadIdx.x; idx < KB * D / 4; idx += 64 * G) {
+                const int key = idx / (D / 4), d4 = (idx % (D / 4)) * 4;
+                const int j = min(j0 + key, kend - 1);  // past the last key: a copy, masked below
+                float kv4[4], vv4[4];
+                kv_load4(kb_ + (size_t)j * kstep + d4, kv4);
+                kv_load4(vb_ + (size_t)j * kstep + d4, vv4);
+                *(ah4*)(ks + key * KROW + d4) =
+                    ah4{(_Float16)kv4[0], (_Float16)kv4[1], (_Float16)kv4[2], (_Float16)kv4[3]};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) vt[(d4 + i) * VROW + key] = (_Float16)vv4[i];
+            }
         }
         __syncthreads();
         af16 sc = af16{};
