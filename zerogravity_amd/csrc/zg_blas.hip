@@ -23,6 +23,7 @@ namespace zg {
 namespace {
 
 constexpr size_t kWorkspace = 64u << 20;
+constexpr size_t kMaxPlans = 256;  // (prompt length, projection) shapes kept planned
 
 struct Plan {
     hipblasLtMatmulDesc_t desc = nullptr;
@@ -61,6 +62,16 @@ hipError_t blas_gemm_f16(int device, int M, int N, int K, const void* A, const v
     }
     const auto key = std::make_tuple(M, N, K, d_f32, ldd, beta != 0.0f);
     auto it = db.plans.find(key);
+    if (it == db.plans.end() && db.plans.size() >= kMaxPlans) {
+        // prompt lengths vary without bound: start the cache over
+        for (auto& kv : db.plans) {
+            (void)hipblasLtMatrixLayoutDestroy(kv.second.ld);
+            (void)hipblasLtMatrixLayoutDestroy(kv.second.la);
+            (void)hipblasLtMatrixLayoutDestroy(kv.second.lw);
+            (void)hipblasLtMatmulDescDestroy(kv.second.desc);
+        }
+        db.plans.clear();
+    }
     if (it == db.plans.end()) {
         Plan p;
         hipError_t e = lt(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
