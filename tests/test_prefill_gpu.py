@@ -130,19 +130,22 @@ def test_prefill_batched_refusals(kern, tiny):
     m8.close()
 
 
-def test_prefill_batched_2b_shapes(kern):
+@pytest.mark.parametrize("kv", [L.BF16, L.F32])
+def test_prefill_batched_2b_shapes(kern, kv):
     """The 2B layer shapes (16 GDN heads, 8 query / 2 KV heads, FFN 6144) over
-    a 150-token prompt: three GDN chunks, the last ragged."""
+    a 150-token prompt: three GDN chunks, the last ragged; both cache types
+    (4 query heads per KV head: the attention kernel loads the next key block
+    ahead in either)."""
     t = qwen35.synthetic_tensors(WIDE, gguf.Q4_K, seed=21)
     m = qwen35.QwenModelHip(WIDE, t, kernel=kern)
-    s = m.session(max_batch=1, max_context=256, kv_dtype=L.BF16)
-    o = O.Model(WIDE, t).session(kv_bf16=True)
+    s = m.session(max_batch=1, max_context=256, kv_dtype=kv)
+    o = O.Model(WIDE, t).session(kv_bf16=kv == L.BF16)
     toks = _tokens(9, 150, WIDE["vocab"])
     lg = s.prefill_batched(toks)
     ref = _oracle_prefill(o, toks)
     e_state = rel_err(s.state(), o.state())
     worst = _greedy_tail(s, o, lg, ref, 4)
-    print(f"batched prefill 2B shapes n=150: logits/decode max-abs {worst:.3e}, state rel {e_state:.2e}")
+    print(f"batched prefill 2B shapes n=150 kv={kv}: logits/decode max-abs {worst:.3e}, state rel {e_state:.2e}")
     assert worst <= LOGIT_TOL
     assert e_state <= 1e-2
     m.close()
