@@ -861,8 +861,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (each GPU would run its own "
-              "sessions; see the sharding notes in DESIGN.md)", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (batch rows are independent and "
+              "the weights replicate, so each GPU would run its own sessions)", file=sys.stderr)
         sys.exit(2)
     bench = {"decode": bench_decode, "decode_q8": bench_decode_q8, "gemv": bench_gemv, "prefill": bench_prefill, "gdn": bench_gdn,
              "model_prefill": bench_model_prefill, "copy": bench_copy, "config1": bench_config1}[args.workload]
