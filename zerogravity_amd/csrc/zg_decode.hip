@@ -1592,6 +1592,14 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
     ConvIn in_v;
     if constexpr (!HEAD) in_v = conv_load(ch_v);
     const float g_a = xin[4 * W + h], g_b = xin[4 * W + a.H + h], g_dt = a.dt[h], g_sa = a.ssm_a[h];
+    // HEAD: wave 0's gated-norm inputs, requested now so that the tail does
+    // not wait for them (loads are not moved across the barriers below)
+    v4f tail_g = v4f{0.0f, 0.0f, 0.0f, 0.0f}, tail_z = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if (HEAD && threadIdx.x < 64) {
+        const int t = threadIdx.x & 31;
+        tail_g = *(const v4f*)(a.norm + 4 * t);
+        tail_z = *(const v4f*)(xin + 3 * W + h * D + 4 * t);
+    }
     float* col = a.state + (((size_t)b * a.H + h) * D + j) * D + 4 * s;
     v4f sv[4];
 #pragma unroll
@@ -1707,9 +1715,8 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
             sq = group_sum_last<32>(sq);
             sq = __shfl(sq, ((int)threadIdx.x & 32) | 31, 64);
             const float gi = rms_inv(sq, D, a.eps);
-            const v4f g = *(const v4f*)(a.norm + 4 * t);
-            const v4f z = *(const v4f*)(xin + 3 * W + h * D + 4 * t);
-            const float gg[4] = {g.x, g.y, g.z, g.w}, zz[4] = {z.x, z.y, z.z, z.w};
+            const float gg[4] = {tail_g.x, tail_g.y, tail_g.z, tail_g.w};
+            const float zz[4] = {tail_z.x, tail_z.y, tail_z.z, tail_z.w};
             typedef _Float16 h4v __attribute__((ext_vector_type(4)));
             h4v hv4;
 #pragma unroll
