@@ -51,7 +51,8 @@ constexpr int kRecWords = 36;  // Q4_K record: 32 dwords of code bytes + {xs_lo,
 // XOR shuffles.  The values are coded straight into LDS:
 //   Q8_0 (cpu/src/source/quantization.rs:37-61): per 32-block amax,
 //     d = amax/127, code = clamp(rint(v*127/amax)), d rounded to f16;
-//     codes [K/4] words, scales [K/32].
+//     codes [8][nbp] words (word l of block b at l * nbp + b, nbp = K/32
+//     rounded up to 4), scales [K/32].
 //   Q8_1 (quantization.rs:37-61, Q4_1 pairing): as Q8_0, plus per block
 //     s = f16(sum of codes * unrounded d) in `extra`.
 //   Q8_K (quantization.rs:66-92, Q6_K pairing): per 256-block (one
@@ -226,7 +227,10 @@ __device__ void wg_prologue_code(const FusedGemvArgs& a, bool valid, const ProIn
                     r = fminf(fmaxf(r, -128.0f), 127.0f);
                     word |= ((uint32_t)(int)r & 0xffu) << (8 * t);
                 }
-                codes[k >> 2] = (int)word;
+                // lane-major: word l * nbp + block (nbp = blocks rounded to
+                // 4), so that one 16-byte read serves four blocks
+                const int nbp = ((K >> 5) + 3) & ~3;
+                codes[(size_t)l * nbp + (k >> 5)] = (int)word;
                 if (l == 0) scales[k >> 5] = f16_roundtrip(d);
             }
         }
@@ -463,9 +467,9 @@ __global__ __launch_bounds__(256) void fused_q8_kernel(FusedGemvArgs a) {
     constexpr int QC = 8;
     extern __shared__ int lds_f8[];
     const int K = a.K, N = a.N;
-    const int nb = K >> 5, nbc = (nb + 3) >> 2;
-    int* codes = lds_f8;                               // [MT][K/4] words
-    float* scales = (float*)(lds_f8 + MT * (K >> 2));  // [MT][nb]
+    const int nb = K >> 5, nbc = (nb + 3) >> 2, nbp = nbc * 4;
+    int* codes = lds_f8;                                 // [MT][8][nbp] words
+    float* scales = (float*)(lds_f8 + MT * 8 * nbp);   // [MT][nbp]
     const int m0 = blockIdx.y * MT;
     const v4i* qs = (const v4i*)a.qs;
     const uint16_t* hdr = (const uint16_t*)a.hdr;
@@ -496,6 +500,13 @@ __global__ __launch_bounds__(256) void fused_q8_kernel(FusedGemvArgs a) {
             if (c >= nbc) break;  // uniform
             const int ww[4] = {ck.w[i].x, ck.w[i].y, ck.w[i].z, ck.w[i].w};
             const uint32_t hw[4] = {ck.h[i].x & 0xffffu, ck.h[i].x >> 16, ck.h[i].y & 0xffffu, ck.h[i].y >> 16};
+            v4i cw[MT];
+            v4f sw[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                cw[m] = *(const v4i*)(codes + (size_t)(m * 8 + l) * nbp + 4 * c);
+                sw[m] = *(const v4f*)(scales + (size_t)m * nbp + 4 * c);
+            }
 #pragma unroll
             for (int bi = 0; bi < 4; ++bi) {
                 const int b = 4 * c + bi;
@@ -503,8 +514,10 @@ __global__ __launch_bounds__(256) void fused_q8_kernel(FusedGemvArgs a) {
                     const float wd = f16_to_f32((uint16_t)hw[bi]);
 #pragma unroll
                     for (int m = 0; m < MT; ++m) {
-                        const int pair = __builtin_amdgcn_sdot4(ww[bi], codes[m * (K >> 2) + b * 8 + l], 0, false);
-                        const float scale = wd * scales[m * nb + b];
+                        const int xc = bi == 0 ? cw[m].x : bi == 1 ? cw[m].y : bi == 2 ? cw[m].z : cw[m].w;
+                        const float xs = bi == 0 ? sw[m].x : bi == 1 ? sw[m].y : bi == 2 ? sw[m].z : sw[m].w;
+                        const int pair = __builtin_amdgcn_sdot4(ww[bi], xc, 0, false);
+                        const float scale = wd * xs;
                         acc[m] = fmaf((float)pair, scale, acc[m]);
                     }
                 }
@@ -519,7 +532,8 @@ __global__ __launch_bounds__(256) void fused_q8_kernel(FusedGemvArgs a) {
     wg_prologue_code<PRO, kCodecQ8, J>(a, m0 < a.M, pin, nullptr, codes, scales);
 #pragma unroll
     for (int m = 1; m < MT; ++m)
-        wg_prologue<PRO, kCodecQ8, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * (K >> 2), scales + m * nb);
+        wg_prologue<PRO, kCodecQ8, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + (size_t)m * 8 * nbp,
+                                   scales + (size_t)m * nbp);
     for (int R = R0; R < groups; R += nwaves) {
         if (R != R0) load_chunk(R, 0, ca);
         const int row = R * 8 + rl;
@@ -1459,7 +1473,7 @@ template <int PRO, int EPI>
 static hipError_t launch_q8(const FusedGemvArgs& a, hipStream_t s) {
     const int K = a.K;
     int mt = a.M == 1 ? 1 : (a.M == 2 ? 2 : 4);
-    auto lds = [&](int t) { return (size_t)t * (K + (K / 32) * 4); };
+    auto lds = [&](int t) { return (size_t)t * ((K / 32 + 3) / 4 * 4) * 36; };  // codes 8 words + scale per block
     const size_t groups = (a.N + 7) / 8;
     const unsigned wgs = (unsigned)std::min<size_t>((groups + 3) / 4, 256 * 8);
     dim3 g(wgs, (unsigned)((a.M + mt - 1) / mt));
