@@ -9,6 +9,8 @@ Workloads (synthetic, seeded random-init weights in the named GGUF codec):
          feeding the next step's tokens.  value = B=1 tokens/s.
   decode_q8  the same model and step with Q8_0 weights (the codec of the
          reference's pinned checkpoints) at B=1 and B=4; value = B=1 tokens/s.
+  decode_mixed  as decode_q8 with the mixed-quant layout (Q6_K embedding and
+         LM head, V and FFN down, Q4_1 attention gate, F32 GDN alpha/beta).
   gemv   dequant-GEMV sweep (Q8_0/Q4_K, M in {1,4,16,32}) with the RMSNorm
          prologue; weights rotate across distinct buffers totalling > 2x the
          256 MB Infinity Cache.
@@ -97,11 +99,15 @@ def decode_matrices(g):
     return out
 
 
-def step_bytes(g, kind, B, T):
+def step_bytes(g, kind, B, T, tensors=None):
     """Algorithmic HBM bytes of one decode step at B rows, T cached tokens:
-    every weight once, GDN state read+write and conv history per row, K and
-    V of T tokens (bf16) per attention layer and row, activations ignored."""
-    w = sum(N * K * BPE[kind] for _, _, K, N in decode_matrices(g))
+    every weight once (its GGUF bytes when the tensor table is given, for
+    mixed codecs), GDN state read+write and conv history per row, K and V of
+    T tokens (bf16) per attention layer and row, activations ignored."""
+    if tensors is not None:
+        w = sum(len(tensors[n][3]) for _, names, _, _ in decode_matrices(g) for n in names)
+    else:
+        w = sum(N * K * BPE[kind] for _, _, K, N in decode_matrices(g))
     W = g["gdn_heads"] * g["gdn_dim"]
     n_attn = g["layers"] // g["full_attention_interval"]
     n_gdn = g["layers"] - n_attn
@@ -379,11 +385,12 @@ def bench_decode(args):
     return line
 
 
-def bench_decode_q8(args):
+def bench_decode_q8(args, mixed=False):
     """The decode step of the 2B-shaped model with Q8_0 weights (the codec of
     the reference's pinned checkpoints): B=1 and B=4 greedy positions after a
-    random 2048-token prefix, fused Q8_0 GEMVs in the reference's exact dot
-    order."""
+    random 2048-token prefix, fused GEMVs in the reference's exact dot order.
+    mixed: the mixed-quant layout (Q6_K embedding/LM head, V and FFN down,
+    Q4_1 attention gate, F32 GDN alpha/beta) over Q8_0."""
     import torch
     from zerogravity_amd import gguf, qwen35
     from zerogravity_amd import regions as R
@@ -391,28 +398,29 @@ def bench_decode_q8(args):
     torch.cuda.set_stream(torch.cuda.Stream())
     g = dict(qwen35.QWEN35_2B)
     t0 = time.perf_counter()
-    tensors = qwen35.synthetic_tensors(g, gguf.Q8_0, seed=2027)
+    tensors = qwen35.synthetic_tensors(g, gguf.Q8_0, seed=2027, kinds=qwen35.MIXED if mixed else None)
     model = qwen35.QwenModelHip(g, tensors, kernel=kern)
-    log(f"2B Q8_0 model resident ({time.perf_counter() - t0:.1f} s)")
+    name = "Q8_0 + Q6_K/Q4_1/F32" if mixed else "Q8_0"
+    log(f"2B {name} model resident ({time.perf_counter() - t0:.1f} s)")
     res = {}
     for B in (1, 4):
         total_ms, per = run_decode(model, torch, B, args.prefix, args.steps, args.warmup, seed=B)
         ms = total_ms / args.steps
-        byts = step_bytes(g, gguf.Q8_0, B, args.prefix + args.warmup + args.steps // 2)
+        byts = step_bytes(g, gguf.Q8_0, B, args.prefix + args.warmup + args.steps // 2, tensors if mixed else None)
         res[B] = dict(tok_s=B / ms * 1e3, ms_per_step=ms, p50_ms=float(np.median(per)), step_gb=byts / 1e9,
                       gbs=byts / ms / 1e6)
-        log(f"Q8_0 decode B={B}: {ms:.3f} ms/step  {B / ms * 1e3:8.1f} tok/s  {byts / ms / 1e6:7.0f} GB/s "
+        log(f"{name} decode B={B}: {ms:.3f} ms/step  {B / ms * 1e3:8.1f} tok/s  {byts / ms / 1e6:7.0f} GB/s "
             f"({byts / ms / 1e6 / HBM_PEAK_GBS:.1%} of HBM roofline)")
     model.close()
     kern.ctx.close()
     gbs = res[1]["gbs"]
     return {
-        "metric": "decode tok/s @B=1 (2B-shaped Q8_0, 2048-token prefix, bf16 KV)",
+        "metric": f"decode tok/s @B=1 (2B-shaped {name}, 2048-token prefix, bf16 KV)",
         "value": round(res[1]["tok_s"], 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(res[1]["ms_per_step"], 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "q8_0 weights, int8 dot, f32 accumulate",
-        "data": "synthetic (seeded random-init Q8_0 GGUF weights, random prefix state)",
-        "config": {"workload": "2B-shaped Q8_0 greedy decode", "prefix": args.prefix, "kv_cache": "bf16",
+        "scaling": "weak", "vs_baseline": None, "dtype": "integer codecs, int8 dots, f32 accumulate",
+        "data": f"synthetic (seeded random-init {name} GGUF weights, random prefix state)",
+        "config": {"workload": f"2B-shaped {name} greedy decode", "prefix": args.prefix, "kv_cache": "bf16",
                    "b1": res[1], "b4": res[4]},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
@@ -854,7 +862,7 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode_q8", "gemv", "prefill", "gdn", "model_prefill", "copy", "config1"])
+                    choices=["decode", "decode_q8", "decode_mixed", "gemv", "prefill", "gdn", "model_prefill", "copy", "config1"])
     ap.add_argument("--prefix", type=int, default=2048)
     ap.add_argument("--leg-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -864,7 +872,8 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path (batch rows are independent and "
               "the weights replicate, so each GPU would run its own sessions)", file=sys.stderr)
         sys.exit(2)
-    bench = {"decode": bench_decode, "decode_q8": bench_decode_q8, "gemv": bench_gemv, "prefill": bench_prefill, "gdn": bench_gdn,
+    bench = {"decode": bench_decode, "decode_q8": bench_decode_q8,
+             "decode_mixed": lambda a: bench_decode_q8(a, mixed=True), "gemv": bench_gemv, "prefill": bench_prefill, "gdn": bench_gdn,
              "model_prefill": bench_model_prefill, "copy": bench_copy, "config1": bench_config1}[args.workload]
     line = bench(args)
     print(json.dumps(line), flush=True)

@@ -1235,16 +1235,19 @@ __device__ __forceinline__ int sbyte(const v4u& v, int idx) {
 // 2L and 2L+1; lane = fma((float)int, d_a * d_w, lane); the Q8_0 lane tree.
 template <int MT, int J, int PRO, int EPI>
 __global__ __launch_bounds__(256) void fused_q6k_kernel(FusedGemvArgs a) {
+    // superblocks stream in chunks of QS through two register buffers, the
+    // next chunk's loads issued before the current one is consumed;
+    // activation row 0's loads go out first and its coding overlaps the
+    // first chunk's (a wave's loads complete in issue order).  Loads are
+    // unconditional: a superblock past the row end reads the last one and
+    // is not consumed.
+    constexpr int QS = 4;
     extern __shared__ int lds_f6[];
     const int K = a.K, N = a.N, nsb = K >> 8;
     int* codes = lds_f6;                                 // [MT][K/4] words
     float* dk = (float*)(lds_f6 + MT * (K >> 2));        // [MT][nsb]
     int* bs = (int*)(dk + MT * nsb);                     // [MT][K/16]
     const int m0 = blockIdx.y * MT;
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-        wg_prologue<PRO, kCodecQ8K, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * (K >> 2), nullptr,
-                                       dk + m * nsb, bs + m * (K >> 4));
     const uint32_t* qa = (const uint32_t*)a.qs;
     const uint32_t* qb = qa + q6k_b_offset((size_t)N, (size_t)K);
     const uint8_t* scl = (const uint8_t*)a.hdr;
@@ -1253,19 +1256,31 @@ __global__ __launch_bounds__(256) void fused_q6k_kernel(FusedGemvArgs a) {
     const int rl = lane >> 3, l = lane & 7;
     const int groups = (N + 7) >> 3;
     const int nwaves = gridDim.x * 4;
-    for (int R = blockIdx.x * 4 + (threadIdx.x >> 6); R < groups; R += nwaves) {
-        const int row = R * 8 + rl;
-        const size_t rr = (size_t)(row < N ? row : N - 1);
-        float acc[MT];
+    struct Chunk {
+        v4u A[QS], S[QS];
+        uint2 B[QS];
+        float wd[QS];
+    };
+    auto load_chunk = [&](int R, int sb0, Chunk& ck) {
+        const int row = min(R, groups - 1) * 8 + rl;  // tile rows past N exist (8-row tiles)
+        const size_t rr = (size_t)min(row, N - 1);
 #pragma unroll
-        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
-        for (int sb = 0; sb < nsb; ++sb) {
-            const v4u A = *(const v4u*)(qa + q6k_a_index((size_t)row, (size_t)sb, l, (size_t)nsb));
-            const uint2 B = *(const uint2*)(qb + q6k_b_index((size_t)row, (size_t)sb, l, (size_t)nsb));
-            const v4u S = *(const v4u*)(scl + (rr * nsb + sb) * 16);
-            const float wd = dw[rr * nsb + sb];
-            const uint32_t av[4] = {A.x, A.y, A.z, A.w};
-            const uint32_t bv[2] = {B.x, B.y};
+        for (int i = 0; i < QS; ++i) {
+            const int sb = min(sb0 + i, nsb - 1);
+            ck.A[i] = *(const v4u*)(qa + q6k_a_index((size_t)row, (size_t)sb, l, (size_t)nsb));
+            ck.B[i] = *(const uint2*)(qb + q6k_b_index((size_t)row, (size_t)sb, l, (size_t)nsb));
+            ck.S[i] = *(const v4u*)(scl + (rr * nsb + sb) * 16);
+            ck.wd[i] = dw[rr * nsb + sb];
+        }
+    };
+    float acc[MT];
+    auto consume = [&](const Chunk& ck, int sb0) {
+#pragma unroll
+        for (int i = 0; i < QS; ++i) {
+            const int sb = sb0 + i;
+            if (sb >= nsb) break;  // uniform
+            const uint32_t av[4] = {ck.A[i].x, ck.A[i].y, ck.A[i].z, ck.A[i].w};
+            const uint32_t bv[2] = {ck.B[i].x, ck.B[i].y};
             int code4[2][4], sub[2][4];
 #pragma unroll
             for (int h = 0; h < 2; ++h)
@@ -1274,9 +1289,9 @@ __global__ __launch_bounds__(256) void fused_q6k_kernel(FusedGemvArgs a) {
                     const uint32_t nib = (av[h * 2 + (g & 1)] >> (g >= 2 ? 4 : 0)) & 0x0f0f0f0fu;
                     const uint32_t hi = ((bv[h] >> (2 * g)) & 0x03030303u) << 4;
                     code4[h][g] = (int)(nib | hi);
-                    sub[h][g] = sbyte(S, h * 8 + g * 2 + (l >> 2));
+                    sub[h][g] = sbyte(ck.S[i], h * 8 + g * 2 + (l >> 2));
                 }
-            const int so0 = sbyte(S, 2 * l), so1 = sbyte(S, 2 * l + 1);
+            const int so0 = sbyte(ck.S[i], 2 * l), so1 = sbyte(ck.S[i], 2 * l + 1);
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 const int* cw = codes + m * (K >> 2) + sb * 64 + l;
@@ -1288,9 +1303,32 @@ __global__ __launch_bounds__(256) void fused_q6k_kernel(FusedGemvArgs a) {
                         iacc += sub[h][g] * __builtin_amdgcn_sdot4(code4[h][g], cw[h * 32 + g * 8], 0, false);
                 const int* bm = bs + m * (K >> 4) + sb * 16;
                 iacc -= 32 * (bm[2 * l] * so0 + bm[2 * l + 1] * so1);
-                const float scale = dk[m * nsb + sb] * wd;
+                const float scale = dk[m * nsb + sb] * ck.wd[i];
                 acc[m] = fmaf((float)iacc, scale, acc[m]);
             }
+        }
+    };
+    ProIn<J> pin;
+    wg_prologue_load<PRO, J>(a, m0, m0 < a.M, pin);
+    const int R0 = blockIdx.x * 4 + (threadIdx.x >> 6);
+    Chunk ca, cb;
+    load_chunk(R0, 0, ca);
+    wg_prologue_code<PRO, kCodecQ8K, J>(a, m0 < a.M, pin, nullptr, codes, nullptr, dk, bs);
+#pragma unroll
+    for (int m = 1; m < MT; ++m)
+        wg_prologue<PRO, kCodecQ8K, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * (K >> 2), nullptr,
+                                       dk + m * nsb, bs + m * (K >> 4));
+    for (int R = R0; R < groups; R += nwaves) {
+        if (R != R0) load_chunk(R, 0, ca);
+        const int row = R * 8 + rl;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+        for (int sb0 = 0; sb0 < nsb; sb0 += 2 * QS) {
+            if (sb0 + QS < nsb) load_chunk(R, sb0 + QS, cb);
+            consume(ca, sb0);
+            if (sb0 + QS >= nsb) break;
+            if (sb0 + 2 * QS < nsb) load_chunk(R, sb0 + 2 * QS, ca);
+            consume(cb, sb0 + QS);
         }
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[m] = group8_tree_last(acc[m]);
