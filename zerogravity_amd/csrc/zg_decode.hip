@@ -57,7 +57,8 @@ constexpr int kRecWords = 36;  // Q4_K record: 32 dwords of code bytes + {xs_lo,
 //     s = f16(sum of codes * unrounded d) in `extra`.
 //   Q8_K (quantization.rs:66-92, Q6_K pairing): per 256-block (one
 //     wavefront) the first element of largest magnitude gives the signed
-//     max, inv = -127/max, d = 1/inv in `extra` [K/256], codes as Q8_0, and
+//     max, inv = -127/max, d = 1/inv in `extra` [K/256], codes as Q8_0 laid
+//     out lane-major (word w of block sb at (w%8)*(K/32) + 8sb + w/8), and
 //     the sums of 16 codes in `bsums` [K/16].
 //   F32: the values themselves, floats [K] at `codes`.
 //   Q4_K: per 32-group int16 fixed point, xq = rint(v*32767/amax), with the
@@ -185,7 +186,10 @@ __device__ void wg_prologue_code(const FusedGemvArgs& a, bool valid, const ProIn
             csum += __shfl_xor(csum, 1, 64);
             csum += __shfl_xor(csum, 2, 64);
             if (k < K) {
-                codes[k >> 2] = (int)word;
+                // lane-major: the 8 words a consumer lane reads per 256-block
+                // (word w of block sb: lane w % 8, slot w / 8) are adjacent
+                const int w = (k >> 2) & 63, sb = k >> 8;
+                codes[(size_t)(w & 7) * (K >> 5) + sb * 8 + (w >> 3)] = (int)word;
                 if ((lane & 3) == 0) bsums[k >> 4] = csum;
                 if (lane == 0) extra[k >> 8] = d;
             }
@@ -1294,13 +1298,15 @@ __global__ __launch_bounds__(256) void fused_q6k_kernel(FusedGemvArgs a) {
             const int so0 = sbyte(ck.S[i], 2 * l), so1 = sbyte(ck.S[i], 2 * l + 1);
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                const int* cw = codes + m * (K >> 2) + sb * 64 + l;
+                const int* cl = codes + m * (K >> 2) + (size_t)l * (K >> 5) + sb * 8;
+                const v4i c0 = *(const v4i*)cl, c1 = *(const v4i*)(cl + 4);
+                const int cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
                 int iacc = 0;
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
 #pragma unroll
                     for (int g = 0; g < 4; ++g)
-                        iacc += sub[h][g] * __builtin_amdgcn_sdot4(code4[h][g], cw[h * 32 + g * 8], 0, false);
+                        iacc += sub[h][g] * __builtin_amdgcn_sdot4(code4[h][g], cw[h * 4 + g], 0, false);
                 const int* bm = bs + m * (K >> 4) + sb * 16;
                 iacc -= 32 * (bm[2 * l] * so0 + bm[2 * l + 1] * so1);
                 const float scale = dk[m * nsb + sb] * ck.wd[i];
