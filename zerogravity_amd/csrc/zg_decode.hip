@@ -1168,6 +1168,12 @@ hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* 
 // m_w * s_a) and join after the reference's lane tree.
 template <int MT, int J, int PRO, int EPI>
 __global__ __launch_bounds__(256) void fused_q41_kernel(FusedGemvArgs a) {
+    // 8-block chunks stream QC at a time through two register buffers, the
+    // next group's loads issued before the current one is consumed;
+    // activation row 0's loads go out first and its coding overlaps them (a
+    // wave's loads complete in issue order).  Loads are unconditional: a
+    // chunk past the row end reads the last one and is not consumed.
+    constexpr int QC = 4;
     extern __shared__ int lds_f41[];
     const int K = a.K, N = a.N;
     const int nb = K >> 5, nbc8 = (nb + 7) >> 3;
@@ -1175,28 +1181,38 @@ __global__ __launch_bounds__(256) void fused_q41_kernel(FusedGemvArgs a) {
     float* scales = (float*)(lds_f41 + MT * (K >> 2));  // [MT][nb]
     float* sums = scales + MT * nb;                     // [MT][nb]
     const int m0 = blockIdx.y * MT;
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-        wg_prologue<PRO, kCodecQ81, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * (K >> 2), scales + m * nb,
-                                       sums + m * nb);
     const v4i* qs = (const v4i*)a.qs;
     const uint32_t* hdr = (const uint32_t*)a.hdr;
     const int lane = threadIdx.x & 63;
     const int rl = lane >> 3, l = lane & 7;
     const int groups = (N + 7) >> 3;
     const int nwaves = gridDim.x * 4;
-    for (int R = blockIdx.x * 4 + (threadIdx.x >> 6); R < groups; R += nwaves) {
-        const int row = R * 8 + rl;
-        const uint32_t* hrow = hdr + (size_t)(row < N ? row : N - 1) * nbc8 * 8;
-        const v4i* tile = qs + (size_t)R * nbc8 * 64 + lane;
-        float acc[MT], summs[MT];
+    struct Chunk {
+        v4i w[QC];
+        v4u h0[QC], h1[QC];
+    };
+    auto load_chunk = [&](int R, int c0, Chunk& ck) {
+        const int Rc = min(R, groups - 1);
+        const uint32_t* hrow = hdr + (size_t)min(Rc * 8 + rl, N - 1) * nbc8 * 8;
+        const v4i* tile = qs + (size_t)Rc * nbc8 * 64 + lane;
 #pragma unroll
-        for (int m = 0; m < MT; ++m) acc[m] = summs[m] = 0.0f;
-        for (int c = 0; c < nbc8; ++c) {
-            const v4i w4 = load_nt(tile + (size_t)c * 64);
-            const v4u h0 = *(const v4u*)(hrow + 8 * c), h1 = *(const v4u*)(hrow + 8 * c + 4);
-            const uint32_t ww[4] = {(uint32_t)w4.x, (uint32_t)w4.y, (uint32_t)w4.z, (uint32_t)w4.w};
-            const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        for (int i = 0; i < QC; ++i) {
+            const int c = min(c0 + i, nbc8 - 1);
+            ck.w[i] = load_nt(tile + (size_t)c * 64);
+            ck.h0[i] = *(const v4u*)(hrow + 8 * c);
+            ck.h1[i] = *(const v4u*)(hrow + 8 * c + 4);
+        }
+    };
+    float acc[MT], summs[MT];
+    auto consume = [&](const Chunk& ck, int c0) {
+#pragma unroll
+        for (int i = 0; i < QC; ++i) {
+            const int c = c0 + i;
+            if (c >= nbc8) break;  // uniform
+            const uint32_t ww[4] = {(uint32_t)ck.w[i].x, (uint32_t)ck.w[i].y, (uint32_t)ck.w[i].z,
+                                    (uint32_t)ck.w[i].w};
+            const uint32_t hw[8] = {ck.h0[i].x, ck.h0[i].y, ck.h0[i].z, ck.h0[i].w,
+                                    ck.h1[i].x, ck.h1[i].y, ck.h1[i].z, ck.h1[i].w};
 #pragma unroll
             for (int bi = 0; bi < 8; ++bi) {
                 const int b = 8 * c + bi;
@@ -1215,6 +1231,29 @@ __global__ __launch_bounds__(256) void fused_q41_kernel(FusedGemvArgs a) {
                     }
                 }
             }
+        }
+    };
+    ProIn<J> pin;
+    wg_prologue_load<PRO, J>(a, m0, m0 < a.M, pin);
+    const int R0 = blockIdx.x * 4 + (threadIdx.x >> 6);
+    Chunk ca, cb;
+    load_chunk(R0, 0, ca);
+    wg_prologue_code<PRO, kCodecQ81, J>(a, m0 < a.M, pin, nullptr, codes, scales, sums);
+#pragma unroll
+    for (int m = 1; m < MT; ++m)
+        wg_prologue<PRO, kCodecQ81, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * (K >> 2), scales + m * nb,
+                                       sums + m * nb);
+    for (int R = R0; R < groups; R += nwaves) {
+        if (R != R0) load_chunk(R, 0, ca);
+        const int row = R * 8 + rl;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = summs[m] = 0.0f;
+        for (int c0 = 0; c0 < nbc8; c0 += 2 * QC) {
+            if (c0 + QC < nbc8) load_chunk(R, c0 + QC, cb);
+            consume(ca, c0);
+            if (c0 + QC >= nbc8) break;
+            if (c0 + 2 * QC < nbc8) load_chunk(R, c0 + 2 * QC, ca);
+            consume(cb, c0 + QC);
         }
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[m] = group8_tree_last(acc[m]);
