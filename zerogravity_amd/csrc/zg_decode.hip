@@ -53,8 +53,9 @@ constexpr int kRecWords = 36;  // Q4_K record: 32 dwords of code bytes + {xs_lo,
 //     d = amax/127, code = clamp(rint(v*127/amax)), d rounded to f16;
 //     codes [8][nbp] words (word l of block b at l * nbp + b, nbp = K/32
 //     rounded up to 4), scales [K/32].
-//   Q8_1 (quantization.rs:37-61, Q4_1 pairing): as Q8_0, plus per block
-//     s = f16(sum of codes * unrounded d) in `extra`.
+//   Q8_1 (quantization.rs:37-61, Q4_1 pairing): as Q8_0 (codes [8][nb8],
+//     nb8 = K/32 rounded up to 8), plus per block s = f16(sum of codes *
+//     unrounded d) in `extra`.
 //   Q8_K (quantization.rs:66-92, Q6_K pairing): per 256-block (one
 //     wavefront) the first element of largest magnitude gives the signed
 //     max, inv = -127/max, d = 1/inv in `extra` [K/256], codes as Q8_0 laid
@@ -212,7 +213,10 @@ __device__ void wg_prologue_code(const FusedGemvArgs& a, bool valid, const ProIn
             }
             csum = group8_sum_all(csum);
             if (k < K) {
-                codes[k >> 2] = (int)word;
+                // lane-major: word l * nb8 + block (nb8 = blocks rounded to
+                // 8), so that two 16-byte reads serve an 8-block chunk
+                const int nb8 = ((K >> 5) + 7) & ~7;
+                codes[(size_t)l * nb8 + (k >> 5)] = (int)word;
                 if (l == 0) {
                     scales[k >> 5] = f16_roundtrip(d);
                     extra[k >> 5] = f16_roundtrip(csum * d);
@@ -1176,10 +1180,10 @@ __global__ __launch_bounds__(256) void fused_q41_kernel(FusedGemvArgs a) {
     constexpr int QC = 4;
     extern __shared__ int lds_f41[];
     const int K = a.K, N = a.N;
-    const int nb = K >> 5, nbc8 = (nb + 7) >> 3;
-    int* codes = lds_f41;                               // [MT][K/4] words
-    float* scales = (float*)(lds_f41 + MT * (K >> 2));  // [MT][nb]
-    float* sums = scales + MT * nb;                     // [MT][nb]
+    const int nb = K >> 5, nbc8 = (nb + 7) >> 3, nb8 = nbc8 * 8;
+    int* codes = lds_f41;                                // [MT][8][nb8] words
+    float* scales = (float*)(lds_f41 + MT * 8 * nb8);    // [MT][nb8]
+    float* sums = scales + MT * nb8;                     // [MT][nb8]
     const int m0 = blockIdx.y * MT;
     const v4i* qs = (const v4i*)a.qs;
     const uint32_t* hdr = (const uint32_t*)a.hdr;
@@ -1213,6 +1217,22 @@ __global__ __launch_bounds__(256) void fused_q41_kernel(FusedGemvArgs a) {
                                     (uint32_t)ck.w[i].w};
             const uint32_t hw[8] = {ck.h0[i].x, ck.h0[i].y, ck.h0[i].z, ck.h0[i].w,
                                     ck.h1[i].x, ck.h1[i].y, ck.h1[i].z, ck.h1[i].w};
+            int xc[MT][8];
+            float xs[MT][8], xu[MT][8];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const v4i* cp = (const v4i*)(codes + (size_t)(m * 8 + l) * nb8 + 8 * c);
+                const v4f* sp = (const v4f*)(scales + (size_t)m * nb8 + 8 * c);
+                const v4f* up = (const v4f*)(sums + (size_t)m * nb8 + 8 * c);
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const v4i cv = cp[hh];
+                    const v4f sv = sp[hh], uv = up[hh];
+                    xc[m][4 * hh] = cv.x; xc[m][4 * hh + 1] = cv.y; xc[m][4 * hh + 2] = cv.z; xc[m][4 * hh + 3] = cv.w;
+                    xs[m][4 * hh] = sv.x; xs[m][4 * hh + 1] = sv.y; xs[m][4 * hh + 2] = sv.z; xs[m][4 * hh + 3] = sv.w;
+                    xu[m][4 * hh] = uv.x; xu[m][4 * hh + 1] = uv.y; xu[m][4 * hh + 2] = uv.z; xu[m][4 * hh + 3] = uv.w;
+                }
+            }
 #pragma unroll
             for (int bi = 0; bi < 8; ++bi) {
                 const int b = 8 * c + bi;
@@ -1223,10 +1243,10 @@ __global__ __launch_bounds__(256) void fused_q41_kernel(FusedGemvArgs a) {
                     const float mw = f16_to_f32((uint16_t)(hw[bi] >> 16));
 #pragma unroll
                     for (int m = 0; m < MT; ++m) {
-                        const int partial = __builtin_amdgcn_sdot4(w8, codes[m * (K >> 2) + b * 8 + l], 0, false);
-                        const float ms = mw * sums[m * nb + b];
+                        const int partial = __builtin_amdgcn_sdot4(w8, xc[m][bi], 0, false);
+                        const float ms = mw * xu[m][bi];
                         summs[m] = summs[m] + ms;
-                        const float scale = d0 * scales[m * nb + b];
+                        const float scale = d0 * xs[m][bi];
                         acc[m] = fmaf((float)partial, scale, acc[m]);
                     }
                 }
@@ -1241,8 +1261,8 @@ __global__ __launch_bounds__(256) void fused_q41_kernel(FusedGemvArgs a) {
     wg_prologue_code<PRO, kCodecQ81, J>(a, m0 < a.M, pin, nullptr, codes, scales, sums);
 #pragma unroll
     for (int m = 1; m < MT; ++m)
-        wg_prologue<PRO, kCodecQ81, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * (K >> 2), scales + m * nb,
-                                       sums + m * nb);
+        wg_prologue<PRO, kCodecQ81, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + (size_t)m * 8 * nb8,
+                                       scales + (size_t)m * nb8, sums + (size_t)m * nb8);
     for (int R = R0; R < groups; R += nwaves) {
         if (R != R0) load_chunk(R, 0, ca);
         const int row = R * 8 + rl;
@@ -1447,7 +1467,7 @@ static hipError_t launch_codec(const FusedGemvArgs& a, int type, hipStream_t s) 
     const int K = a.K;
     const int mt = type == kF32 ? 1 : (a.M == 1 ? 1 : (a.M == 2 ? 2 : 4));
     size_t per;
-    if (type == kQ4_1) per = (size_t)K + (size_t)(K / 32) * 8;
+    if (type == kQ4_1) per = (size_t)((K / 32 + 7) / 8 * 8) * 40;  // codes 8 words + scale + sum per block
     else if (type == kQ6_K) per = (size_t)K + (size_t)(K / 256) * 4 + (size_t)(K / 16) * 4;
     else per = (size_t)K * 4;
     const size_t lds = per * mt;
