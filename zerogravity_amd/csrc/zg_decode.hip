@@ -2401,8 +2401,14 @@ static void launch_attn(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
         hipLaunchKernelGGL((attn_decode_pv_kernel<KV, G, 4, 16, false>), dim3(256 / 32, a.nq / G, (unsigned)B), dim3(256),
                            0, s, a);
     } else {
-        hipLaunchKernelGGL((attn_decode_pv_kernel<KV, 1, 1, 96, true>), dim3(256 / 8, a.nq, (unsigned)B), dim3(256), 0, s,
-                           a);
+        // one tile of 72 x 32 tokens when it covers the whole cache (fewer
+        // clamped loads past the position than the 96 x 32 tile), else 96
+        if (a.max_ctx <= 72 * 32)
+            hipLaunchKernelGGL((attn_decode_pv_kernel<KV, 1, 1, 72, true>), dim3(256 / 8, a.nq, (unsigned)B), dim3(256), 0,
+                               s, a);
+        else
+            hipLaunchKernelGGL((attn_decode_pv_kernel<KV, 1, 1, 96, true>), dim3(256 / 8, a.nq, (unsigned)B), dim3(256), 0,
+                               s, a);
     }
 }
 
