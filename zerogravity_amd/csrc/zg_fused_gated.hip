@@ -1,0 +1,6 @@
+// Fused decode GEMV kernels with the PRO_GATED prologue.
+#include "zg_fused_kernels.hpp"
+
+namespace zg {
+template hipError_t launch_pro<PRO_GATED>(const FusedGemvArgs& a, int type, hipStream_t s);
+}  // namespace zg
