@@ -21,7 +21,8 @@
  * its resident program on.
  *
  * Thread safety: every entry point taking a zg_ctx serialises on that ctx
- * (the reference trait is Send + Sync, accelerator.rs:682).
+ * (the reference trait is Send + Sync, accelerator.rs:682), and failure
+ * text is kept per calling thread (zg_last_error).
  * No torch types appear in this ABI; streams are hipStream_t passed as void*.
  */
 #ifndef ZG_HIP_H
@@ -59,8 +60,8 @@ typedef struct zg_weight zg_weight;
  * stream.  Returns ZG_COMPLETED or ZG_E_DEVICE. */
 int zg_ctx_create(int device, zg_ctx** out);
 void zg_ctx_destroy(zg_ctx* ctx);
-/* Message for the last failing call on this ctx ("" if none).  Valid until
- * the next call on the ctx. */
+/* Message of the calling thread's last failing call on this ctx ("" if
+ * none).  Valid until that thread's next failing call on the ctx. */
 const char* zg_last_error(const zg_ctx* ctx);
 /* Version string of this library. */
 const char* zg_version(void);
@@ -78,7 +79,11 @@ const char* zg_version(void);
 int zg_weight_register(zg_ctx* ctx, uint64_t source_id, const char* name, int ggml_type,
                        size_t columns, size_t rows, const void* bytes, size_t len,
                        zg_weight** out);
-/* Drop every resident weight registered under source_id (model close). */
+/* Release the handles registered under source_id (model close).  A weight
+ * that a loaded model (zg_model_load) still uses stays resident until the
+ * last such model is destroyed; models take their own references, so
+ * destroying one model never frees a weight another model or a registered
+ * handle uses. */
 int zg_source_release(zg_ctx* ctx, uint64_t source_id);
 /* Device bytes held by a registered weight (payload + headers). */
 size_t zg_weight_device_bytes(const zg_weight* w);
@@ -89,6 +94,13 @@ size_t zg_weight_device_bytes(const zg_weight* w);
 int zg_weight_dequantize(zg_ctx* ctx, const zg_weight* w, float* out, size_t out_len);
 
 /* ------------------------------------------------------- boundary A regions */
+
+/* greedy_finite (core/src/numerics.rs:124-140) on the device: for each of
+ * `rows` rows of n logits (host, row-major), the index of the first maximum
+ * (ties, +0 vs -0 included, keep the lower index).  A nonfinite logit is
+ * ZG_E_STATE; n == 0 is ZG_E_LIMIT.  out[rows].  The decode step's greedy
+ * readout runs the same kernels. */
+int zg_greedy(zg_ctx* ctx, const float* logits, size_t rows, size_t n, uint32_t* out);
 
 /* MatVecRegion (core/src/accelerator.rs:61-75) -> MatVecKernel::try_execute
  * (:683).  Q8_0 runs against the dynamic Q8_0 activation coding
@@ -172,6 +184,20 @@ int zg_gdn_chunk(zg_ctx* ctx, size_t rows, size_t heads, const float* query, con
 int zg_gdn_decode_device(zg_ctx* ctx, size_t rows, size_t heads, const float* proj, size_t proj_stride,
                          const float* conv_w, float* ring, const int32_t* positions, const float* dt,
                          const float* ssm_a, float eps, float* state, float* core, void* stream);
+
+/* The batched-rows form of zg_gdn_decode_device (one workgroup per head and
+ * row, the kernel the decode step uses above 4 rows): the same core and
+ * state, plus ssm_out's activation -- the gated RMSNorm of each head's core
+ * with gamma norm[128], times silu(z) (forward.rs:586-594) -- rounded to f16
+ * into `tiles` in the batched projections' MFMA A-operand order: element
+ * (row m, channel k) at f16 index ((((m/32)*(W/256) + k/256)*16 + (k%256)/16)
+ * *64 + ((k%16)/8)*32 + m%32)*8 + k%8, W = heads*128, rows padded to 32
+ * (zg_gdn_decode_tiles_bytes).  heads even. */
+size_t zg_gdn_decode_tiles_bytes(size_t rows, size_t heads);
+int zg_gdn_decode_gated_device(zg_ctx* ctx, size_t rows, size_t heads, const float* proj, size_t proj_stride,
+                               const float* conv_w, float* ring, const int32_t* positions, const float* dt,
+                               const float* ssm_a, const float* norm, float eps, float* state, float* core,
+                               void* tiles, void* stream);
 
 /* One attention layer's decode step for `rows` sequences on device buffers
  * and the caller's stream: attention_layer (forward.rs:634-755) between its
@@ -285,27 +311,65 @@ int zg_session_position(const zg_session* s, size_t row);
 int zg_session_reset_row(zg_session* s, size_t row);
 int zg_session_copy_row(zg_session* s, size_t dst, size_t src);
 
-/* One forward_token for rows [0, rows): tokens[rows] host ids, logits
+/* Publication.  Every state-changing call is a transaction over rows
+ * [0, rows) (or its one row): it either completes and publishes, or fails
+ * and leaves every row's position, conv history, GDN state and KV prefix
+ * bit-identical to before (QwenDenseCpu: next_logits works on a draft,
+ * commit publishes it, prefill_transaction installs its state only if every
+ * token succeeds; lib.rs:1057-1070, 1114-1187, 1211-1225).  A failure that
+ * leaves the device state unknown (a HIP launch error, ZG_E_DEVICE) poisons
+ * the session until reset, import or restore.
+ *
+ * One forward_token for rows [0, rows): tokens[rows] host ids, logits
  * [rows][vocab] and/or greedy [rows] (first maximum, numerics.rs:126-140)
  * written to host memory when non-NULL.  Each row advances one position
- * (QwenDenseCpu::forward, lib.rs:1227-1232).  A nonfinite layer or logit is
- * ZG_E_STATE and poisons the session until reset or state import. */
+ * (QwenDenseCpu::forward = next_logits + commit, lib.rs:1227-1232).  A
+ * nonfinite layer or logit is ZG_E_STATE and publishes nothing. */
 int zg_decode_step(zg_session* s, size_t rows, const uint32_t* tokens, float* logits, uint32_t* greedy);
+/* QwenDenseCpu::next_logits (lib.rs:1057-1070): the step's logits/greedy
+ * on a draft; nothing is published until zg_session_commit.  Any other
+ * state-changing call on the session drops the proposal. */
+int zg_session_propose(zg_session* s, size_t rows, const uint32_t* tokens, float* logits, uint32_t* greedy);
+/* QwenDenseCpu::commit (lib.rs:1211-1225): publish the pending proposal.
+ * ZG_E_STATE when there is none (never made, already committed, or dropped). */
+int zg_session_commit(zg_session* s);
 /* n tokens per row (tokens[row*n + t]), logits of the last only
- * (QwenDenseCpu::prefill_transaction, lib.rs:1119-1187). */
+ * (QwenDenseCpu::prefill_transaction, lib.rs:1119-1187); atomic over the
+ * call. */
 int zg_prefill(zg_session* s, size_t rows, size_t n, const uint32_t* tokens, float* logits);
 /* n tokens of one row at once (QwenDenseCpu::prefill_transaction,
  * lib.rs:1119-1187, computed layer by layer over the whole prompt: batched
  * MFMA projections, the chunked GDN prefill (gdn/chunk.rs), causal attention
  * appending to the KV cache).  Logits of the last token to host when
  * non-NULL.  Same functions as zg_prefill in another order of summation;
- * needs Q4_K projections (ZG_E_UNSUPPORTED otherwise). */
+ * needs Q4_K projections (ZG_E_UNSUPPORTED otherwise).  Atomic: a failure
+ * leaves the row's published state as it was. */
 int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* tokens, float* logits);
 /* Device-side step: d_tokens/d_logits/d_greedy are device pointers, no host
- * synchronisation (zg_session_check reads the device status word). */
+ * synchronisation.  The step's last kernel publishes it only if the status
+ * word is clear, so after a failure every later queued step is a no-op on
+ * the published state until the failure is read: zg_session_check (or the
+ * next host-synchronous call on the session) waits for the queued steps,
+ * reports the failure and clears it.  One captured graph is kept per
+ * (rows, d_tokens, d_logits, d_greedy); reuse the same buffers every step
+ * (at most 16 graphs are cached, the least recently used is rebuilt). */
 int zg_decode_step_device(zg_session* s, size_t rows, const uint32_t* d_tokens, float* d_logits, uint32_t* d_greedy,
                           void* stream);
 int zg_session_check(zg_session* s, void* stream);
+
+/* Device-side snapshot of one row's published state (conv history, GDN
+ * state, KV prefix, position), the resident form of
+ * ResidentSession::snapshot / restore (gpu/src/resident_inference.rs:2766,
+ * 3258).  restore puts it into any row of any session of the same model
+ * with the same KV cache type (a fork when the row differs); a snapshot of
+ * another model is ZG_E_STATE ("foreign"), one longer than the session's
+ * context ZG_E_LIMIT.  Snapshots own device memory until destroyed. */
+typedef struct zg_snapshot zg_snapshot;
+int zg_session_snapshot(zg_session* s, size_t row, zg_snapshot** out);
+int zg_session_restore(zg_session* s, size_t row, const zg_snapshot* snap);
+size_t zg_snapshot_bytes(const zg_snapshot* snap);
+int zg_snapshot_position(const zg_snapshot* snap);
+void zg_snapshot_destroy(zg_snapshot* snap);
 
 /* State domains of one row in the reference order (lib.rs:112-150): per layer,
  * GDN conv history then recurrent state (value-major), or attention keys then

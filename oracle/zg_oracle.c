@@ -532,17 +532,24 @@ int zgo_grouped_rms_norm(const float* x, const float* w, size_t width, size_t gr
 
 /* --------------------------------------------------------- exp / SiLU / misc */
 
-/* f32 transcendentals of the reference's platform libm (Rust f32::exp, ln,
- * sin_cos, lib.rs:324-336, 357, 1566) evaluated in double and rounded once:
- * the correctly rounded f32 value (double exp/log/sin/cos are within an ulp
- * of double, far inside the f32 rounding interval except in measure-zero
- * ties).  glibc's f32 versions are not correctly rounded, and no reference
- * test pins their last bit; the HIP kernels use the same definition so the
- * two agree bit for bit. */
-static float cr_expf(float x) { return (float)exp((double)x); }
-static float cr_logf(float x) { return (float)log((double)x); }
-static float cr_sinf(float x) { return (float)sin((double)x); }
-static float cr_cosf(float x) { return (float)cos((double)x); }
+/* f32 transcendentals of the reference's platform libm: Rust f32::exp, ln,
+ * sin_cos (lib.rs:324-336, 357, 1566) call the C library's expf, logf, sinf
+ * and cosf on Linux, so the default mode (ZGO_LIBM_GLIBC) calls exactly
+ * those.  ZGO_LIBM_CORRECT evaluates in double and rounds once: the
+ * correctly rounded f32 value, which is what the HIP kernels compute; the
+ * bit-exact device regression tests select it.  glibc's f32 routines miss
+ * the correctly rounded value by one ulp on a small fraction of inputs. */
+static int g_libm_mode = ZGO_LIBM_GLIBC;
+int zgo_set_libm_mode(int mode) {
+    const int old = g_libm_mode;
+    if (mode == ZGO_LIBM_GLIBC || mode == ZGO_LIBM_CORRECT) g_libm_mode = mode;
+    return old;
+}
+int zgo_libm_mode(void) { return g_libm_mode; }
+static float cr_expf(float x) { return g_libm_mode == ZGO_LIBM_GLIBC ? expf(x) : (float)exp((double)x); }
+static float cr_logf(float x) { return g_libm_mode == ZGO_LIBM_GLIBC ? logf(x) : (float)log((double)x); }
+static float cr_sinf(float x) { return g_libm_mode == ZGO_LIBM_GLIBC ? sinf(x) : (float)sin((double)x); }
+static float cr_cosf(float x) { return g_libm_mode == ZGO_LIBM_GLIBC ? cosf(x) : (float)cos((double)x); }
 
 /* cpu/src/ops.rs:317-350: GGML Haswell vector exp, scalar form. */
 float zgo_ggml_exp(float x) {

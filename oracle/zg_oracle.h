@@ -29,10 +29,20 @@
  *   attention value ........ lib.rs:1738-1799 signed-zero padding table
  *   attention qk ........... core/src/accelerator.rs:1012-1054 (score = dot*scale)
  *   greedy ................. core/src/numerics.rs:146-162
+ *   gdn recurrence (real) .. the reference's pinned_cached_head0.f32le.bin vector
+ *                            (recurrent_tests.rs:14-76), at tolerance
  *   forward_token .......... composition of the above in forward.rs:451-755 order;
  *                            no reference-held end-to-end vector exists (all such
- *                            reference tests need private checkpoints), so the
- *                            composition itself is parity unpinned beyond its parts.
+ *                            reference tests need private checkpoints).  Pinned by an
+ *                            independent float64 numpy forward written from
+ *                            forward.rs and the closed-form GDN update
+ *                            (tests/test_forward_independent.py), which a planted
+ *                            [q|gate] swap is shown to fail.
+ *
+ * Transcendentals: ZGO_LIBM_GLIBC (default) calls glibc expf/logf/sinf/cosf,
+ * as Rust's f32::{exp, ln, sin_cos} do on Linux; ZGO_LIBM_CORRECT rounds the
+ * double result once (the correctly rounded value the HIP kernels compute),
+ * selected only by the bit-exact device regression tests.
  */
 #ifndef ZG_ORACLE_H
 #define ZG_ORACLE_H
@@ -43,6 +53,11 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+enum { ZGO_LIBM_GLIBC = 0, ZGO_LIBM_CORRECT = 1 };
+/* Select the transcendental mode (returns the previous one). */
+int zgo_set_libm_mode(int mode);
+int zgo_libm_mode(void);
 
 /* ggml type codes, core/src/encoding.rs:77-91 */
 enum { ZGO_F32 = 0, ZGO_F16 = 1, ZGO_Q4_0 = 2, ZGO_Q4_1 = 3, ZGO_Q8_0 = 8,

@@ -53,6 +53,8 @@ class Geometry(C.Structure):
 
 def _declare(L):
     sig = {
+        "zgo_set_libm_mode": (C.c_int, [C.c_int]),
+        "zgo_libm_mode": (C.c_int, []),
         "zgo_f16_to_f32": (C.c_float, [C.c_uint16]),
         "zgo_f32_to_f16_rne": (C.c_uint16, [C.c_float]),
         "zgo_dequantize": (C.c_int, [C.c_int, P, SZ, SZ, P]),
@@ -100,6 +102,30 @@ def _declare(L):
         fn = getattr(L, name)
         fn.restype = res
         fn.argtypes = args
+
+
+LIBM_GLIBC, LIBM_CORRECT = 0, 1
+
+
+def set_libm_mode(mode):
+    """Select glibc f32 transcendentals (LIBM_GLIBC, the default: what Rust's
+    f32::{exp, ln, sin_cos} call) or correctly rounded ones (LIBM_CORRECT: what
+    the HIP kernels compute).  Returns the previous mode."""
+    return lib().zgo_set_libm_mode(mode)
+
+
+class libm_mode:
+    """Context manager: run a block with the oracle in the given libm mode."""
+
+    def __init__(self, mode):
+        self.mode = mode
+
+    def __enter__(self):
+        self.old = set_libm_mode(self.mode)
+        return self
+
+    def __exit__(self, *exc):
+        set_libm_mode(self.old)
 
 
 def ptr(a):

@@ -5,7 +5,9 @@ position, K/V append (rounded to the cache type), 32-accumulator scores,
 8-lane softmax with f64 partials, padded 4x8-lane value chains and the
 sigmoid gate.  The device restates each step's order of operations, so the
 outputs and the appended K/V are required bit-identical, for a bf16 and an
-f32 cache, rows at different positions (T = 1, 300 and 2048)."""
+f32 cache, caches of 2048 to 8192 rows (the reference qualifies contexts
+through 8192 tokens, scripts/cpu-qualification-gate.py:5-6) and 3 or 32
+rows at positions up to 8191."""
 import math
 
 import numpy as np
@@ -14,7 +16,7 @@ import pytest
 import zg_oracle as O
 from zerogravity_amd import _lib as L
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("exact_libm")]
 D = 256
 
 
@@ -34,21 +36,38 @@ def ctx():
     c.close()
 
 
-@pytest.mark.parametrize("kv", [L.BF16, L.F32])
-def test_attn_decode_device_matches_oracle(ctx, kv):
+LONG32 = [0, 2303, 3100, 4100, 8191] + [int(p) for p in np.linspace(17, 8180, 27)]
+
+
+# Each case reaches one branch of the device kernels: a cache of <= 2304
+# rows (one 72 x 32 value tile), of <= 3072 (one 96 x 32 tile), beyond
+# (tiled values with the softmax statistics computed ahead), beyond 4096
+# (statistics over several score spans), and 8 rows or more (a statistics
+# launch, then 4 query heads x 16 channels per workgroup).
+@pytest.mark.parametrize("kv,max_ctx,positions", [
+    (L.BF16, 2048, [0, 299, 2047]),
+    (L.F32, 2048, [0, 299, 2047]),
+    (L.BF16, 3072, [0, 2303, 3071]),
+    (L.BF16, 4096, [0, 2303, 3100]),
+    (L.BF16, 8192, [4100, 8191, 2303]),
+    (L.F32, 8192, [8191, 4100, 0]),
+    (L.BF16, 8192, LONG32),
+    (L.BF16, 2048, [int(p) for p in np.linspace(0, 2047, 32)]),
+])
+def test_attn_decode_device_matches_oracle(ctx, kv, max_ctx, positions):
     import torch
     nq, nkv, eps = 8, 2, 1e-6
     theta = math.pow(1e7, -2.0 / 64.0)
-    pos = np.array([0, 299, 2047], np.int32)
-    B, max_ctx = pos.size, 2048
-    rng = np.random.default_rng(41 + kv)
+    pos = np.array(positions, np.int32)
+    B = pos.size
+    rng = np.random.default_rng(41 + kv + max_ctx + B)
     stride = (2 * nq + 2 * nkv) * D + 8
     proj = rng.standard_normal((B, stride)).astype(np.float32)
     qn_w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
     kn_w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
     kw = nkv * D
-    hist_k = bf16(rng.standard_normal((B, max_ctx, kw)))
-    hist_v = bf16(rng.standard_normal((B, max_ctx, kw)))
+    hist_k = bf16(rng.standard_normal((B, max_ctx, kw), dtype=np.float32))
+    hist_v = bf16(rng.standard_normal((B, max_ctx, kw), dtype=np.float32))
     if kv == L.BF16:
         kc = torch.from_numpy(to_bf16_bits(hist_k).view(np.int16)).cuda()
         vc = torch.from_numpy(to_bf16_bits(hist_v).view(np.int16)).cuda()

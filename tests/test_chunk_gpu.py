@@ -24,7 +24,7 @@ import zg_oracle as O
 from zerogravity_amd import _lib as L
 from zerogravity_amd import chunk as CH
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("exact_libm")]
 REL_TOL = 1e-3
 D = 128
 

@@ -24,7 +24,7 @@ from zerogravity_amd import gguf, qwen35
 from zerogravity_amd import regions as R
 from zerogravity_amd import synth
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("exact_libm")]
 KINDS = [synth.Q4_1, synth.Q6_K, synth.F32]
 
 

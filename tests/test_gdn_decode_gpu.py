@@ -13,7 +13,7 @@ import pytest
 import zg_oracle as O
 from zerogravity_amd import _lib as L
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("exact_libm")]
 D = 128
 
 

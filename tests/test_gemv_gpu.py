@@ -15,7 +15,7 @@ from zerogravity_amd import _lib as L
 from zerogravity_amd import regions as R
 from zerogravity_amd import synth
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("exact_libm")]
 
 SHAPES = [(3584, 1024), (1024, 3584), (6144, 2048), (2048, 6144), (151936, 2048)]
 KINDS = [synth.Q8_0, synth.Q4_K]

@@ -18,7 +18,7 @@ from zerogravity_amd import _lib as L
 from zerogravity_amd import gguf, qwen35
 from zerogravity_amd import regions as R
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("exact_libm")]
 REL_TOL = 1e-3
 LOGIT_TOL = 2e-2
 
@@ -288,19 +288,25 @@ def model_08b():
     return g, qwen35.synthetic_tensors(g, gguf.Q8_0, seed=2026)
 
 
+@pytest.mark.parametrize("libm", ["correct", "glibc"])
 @pytest.mark.parametrize("kv", [L.F32, L.BF16])
-def test_qwen35_08b_q8_0_prompt32_greedy32(kern, model_08b, kv):
+def test_qwen35_08b_q8_0_prompt32_greedy32(kern, model_08b, kv, libm):
     """0.8B-shaped Q8_0, batch 1, 32 seeded uniform prompt ids, 32 greedy
     steps: logits within 2e-2 max-abs at every step and the identical greedy
     sequence.  The device restates the CPU's order everywhere; the remaining
     freedom is the order of f64 sums (RMS, L2, softmax), which moves an f32
     result only when the f64 value lies within ~2^-40 of an f32 rounding
-    boundary, so nearly every step is bit-exact (counted and printed)."""
+    boundary, so nearly every step is bit-exact (counted and printed) against
+    the oracle with correctly rounded transcendentals.  Against the oracle
+    calling glibc's expf/logf/sinf/cosf, as the reference's Rust f32 functions
+    do, one-ulp differences in the GDN gates and RoPE propagate through the
+    Q8_0 activation codes, and the bar is the north star's."""
     g, t = model_08b
     prompt = _tokens(32, 32, g["vocab"])
     m = qwen35.QwenModelHip(g, t, kernel=kern)
     s = m.session(max_batch=1, max_context=128, kv_dtype=kv)
     o = _oracle(g, t).session(kv_bf16=kv == L.BF16)
+    mode = O.set_libm_mode(O.LIBM_GLIBC if libm == "glibc" else O.LIBM_CORRECT)
     for tok in prompt[:-1]:
         s.step([int(tok)], logits=False)
         o.forward(int(tok), need_logits=False)
@@ -314,7 +320,8 @@ def test_qwen35_08b_q8_0_prompt32_greedy32(kern, model_08b, kv):
         assert a == b, (step, a, b)
         lg, ref = s.forward(a), o.forward(b)
         worst = max(worst, float(np.max(np.abs(lg - ref))))
-    print(f"kv={kv} worst logit max-abs {worst:.3e}; bit-exact steps {exact}/32")
+    O.set_libm_mode(mode)
+    print(f"kv={kv} libm={libm} worst logit max-abs {worst:.3e}; bit-exact steps {exact}/32")
     assert worst <= LOGIT_TOL
     assert seq_gpu == seq_ref
     m.close()

@@ -19,7 +19,7 @@ from zerogravity_amd import _lib as L
 from zerogravity_amd import gguf, qwen35
 from zerogravity_amd import regions as R
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("exact_libm")]
 LOGIT_TOL = 2e-2
 
 TINY = dict(hidden=512, layers=4, ffn=512, vocab=1000, gdn_heads=2, gdn_dim=128, q_heads=2, kv_heads=1,

@@ -14,9 +14,27 @@
 
 namespace zgc {
 
+// Failure text per (thread, ctx): under the reference's Send + Sync
+// contract (core/src/accelerator.rs:682) two threads may fail on one ctx at
+// once, and each reads its own message back.
+thread_local std::map<const zg_ctx*, std::string> t_errors;
+
 int fail(zg_ctx* ctx, int code, const std::string& msg) {
-    if (ctx) ctx->err = msg;
+    if (ctx) {
+        ctx->err = msg;
+        t_errors[ctx] = msg;
+    }
     return code;
+}
+
+void drop_weight(zg_ctx* ctx, zg_weight* w) {
+    (void)hipDeviceSynchronize();
+    for (auto it = ctx->weights.begin(); it != ctx->weights.end(); ++it)
+        if (it->second.get() == w) {
+            free_weight(w);
+            ctx->weights.erase(it);
+            return;
+        }
 }
 
 
@@ -173,7 +191,11 @@ void zg_ctx_destroy(zg_ctx* ctx) {
     delete ctx;
 }
 
-const char* zg_last_error(const zg_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+const char* zg_last_error(const zg_ctx* ctx) {
+    if (!ctx) return "null context";
+    auto it = t_errors.find(ctx);
+    return it == t_errors.end() ? "" : it->second.c_str();
+}
 
 int zg_weight_register(zg_ctx* ctx, uint64_t source_id, const char* name, int ggml_type, size_t columns,
                        size_t rows, const void* bytes, size_t len, zg_weight** out) {
@@ -184,21 +206,28 @@ int zg_weight_register(zg_ctx* ctx, uint64_t source_id, const char* name, int gg
     int rc = check_matrix(ctx, ggml_type, columns, rows, bytes, len);
     if (rc == ZG_UNSUPPORTED) return fail(ctx, ZG_E_UNSUPPORTED, ctx->err);
     if (rc != ZG_COMPLETED) return rc;
-    return lookup_or_register(ctx, source_id, name, ggml_type, columns, rows, bytes, len, out);
+    rc = lookup_or_register(ctx, source_id, name, ggml_type, columns, rows, bytes, len, out);
+    if (rc == ZG_COMPLETED) (*out)->api_pinned = true;
+    return rc;
 }
 
 int zg_source_release(zg_ctx* ctx, uint64_t source_id) {
     if (!ctx) return ZG_E_MALFORMED;
     std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
-    ZG_HIP(hipStreamSynchronize(ctx->stream));
+    ZG_HIP(hipDeviceSynchronize());
+    // weights a loaded model still uses stay until its zg_model_destroy
     for (auto it = ctx->weights.begin(); it != ctx->weights.end();) {
+        zg_weight* w = it->second.get();
         if (std::get<0>(it->first) == source_id) {
-            free_weight(it->second.get());
-            it = ctx->weights.erase(it);
-        } else {
-            ++it;
+            w->api_pinned = false;
+            if (w->model_refs == 0) {
+                free_weight(w);
+                it = ctx->weights.erase(it);
+                continue;
+            }
         }
+        ++it;
     }
     return ZG_COMPLETED;
 }
@@ -236,6 +265,7 @@ int zg_matvec(zg_ctx* ctx, uint64_t source_id, const char* tensor_name, int ggml
     if (source_id != 0) {
         rc = lookup_or_register(ctx, source_id, tensor_name, ggml_type, columns, rows, packed_weights, packed_len, &w);
         if (rc) return rc;
+        w->api_pinned = true;  // resident for the bound source until zg_source_release
     } else {
         rc = build_weight(ctx, ggml_type, columns, rows, packed_weights, packed_len, temp);
         if (rc) return rc;
@@ -276,6 +306,7 @@ int zg_embedding(zg_ctx* ctx, uint64_t source_id, const char* tensor_name, int g
     if (source_id != 0) {
         rc = lookup_or_register(ctx, source_id, tensor_name, ggml_type, width, vocabulary, packed_weights, packed_len, &w);
         if (rc) return rc;
+        w->api_pinned = true;
     } else {
         // Unbound: upload only the selected row.
         const size_t rb = zg::gguf_row_bytes(ggml_type, width);

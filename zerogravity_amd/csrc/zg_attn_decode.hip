@@ -635,29 +635,49 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
     }
 }
 
+// The publication rule of a decode step (QwenDenseCpu::commit,
+// model-qwen35/src/lib.rs:1211-1225: the draft becomes the state only when
+// the whole step succeeded): with the status word clear, row b's position
+// moves on and its GDN state half flips to the draft the step wrote; else
+// nothing changes, so a failed step leaves the published state as it was.
+__device__ __forceinline__ void commit_row(const StepCommit& c, bool ok, int b) {
+    if (!ok) return;
+    const int np = c.pos[b] + 1;
+    c.pos[b] = np;
+    c.ntok[b] = np + 1;
+    if (c.cur) c.cur[b] ^= 1;
+}
+
 __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ pmax, const int* __restrict__ pidx,
-                                                          uint32_t* __restrict__ greedy, int* __restrict__ pos,
-                                                          int* __restrict__ ntok, int advance) {
+                                                          uint32_t* __restrict__ greedy, const int* __restrict__ status,
+                                                          StepCommit c) {
     const int b = blockIdx.x, lane = threadIdx.x;
     float m = lane < kArgBlocks ? pmax[b * kArgBlocks + lane] : -INFINITY;
     int mi = lane < kArgBlocks ? pidx[b * kArgBlocks + lane] : 0x7fffffff;
     for (int off = 32; off > 0; off >>= 1) argmax_merge(m, mi, __shfl_xor(m, off, 64), __shfl_xor(mi, off, 64));
     if (lane == 0) {
         greedy[b] = mi == 0x7fffffff ? 0u : (uint32_t)mi;
-        if (advance) {
-            const int np = pos[b] + 1;
-            pos[b] = np;
-            ntok[b] = np + 1;
-        }
+        if (c.pos) commit_row(c, *status == 0, b);
     }
 }
 
+__global__ __launch_bounds__(64) void commit_step_kernel(StepCommit c, const int* __restrict__ status, int B) {
+    const int b = threadIdx.x;
+    if (b < B) commit_row(c, *status == 0, b);
+}
+
 hipError_t argmax_step(const float* logits, size_t V, size_t ld, size_t B, uint32_t* greedy, int* status, float* pmax,
-                       int* pidx, unsigned* tickets, int* pos, int* ntok, int advance, hipStream_t s) {
-    (void)tickets;
+                       int* pidx, const StepCommit* commit, hipStream_t s) {
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgBlocks, (unsigned)B), dim3(256), 0, s, logits, (int)V, ld, status,
                        pmax, pidx);
-    hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)B), dim3(64), 0, s, pmax, pidx, greedy, pos, ntok, advance);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)B), dim3(64), 0, s, pmax, pidx, greedy, status,
+                       commit ? *commit : StepCommit{});
+    return hipGetLastError();
+}
+
+hipError_t commit_step(const StepCommit& c, const int* status, size_t B, hipStream_t s) {
+    if (B == 0 || B > 64) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(commit_step_kernel, dim3(1), dim3(64), 0, s, c, status, (int)B);
     return hipGetLastError();
 }
 

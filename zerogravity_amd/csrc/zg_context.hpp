@@ -13,6 +13,11 @@ struct zg_weight {
     zg::DeviceWeight dw;
     uint64_t source = 0;
     std::string name;
+    // Lifetime: loaded models hold references (model_refs); a handle given
+    // out by zg_weight_register / a bound zg_matvec pins the weight until
+    // zg_source_release.  It is freed when neither holds it.
+    int model_refs = 0;
+    bool api_pinned = false;
 };
 
 struct DeviceBuffer {
@@ -24,7 +29,7 @@ struct zg_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     std::recursive_mutex mu;
-    std::string err;
+    std::string err;  // last failure on this ctx from any thread (zg_last_error reads the caller's own)
     std::map<std::tuple<uint64_t, std::string, int, size_t, size_t>, std::unique_ptr<zg_weight>> weights;
     DeviceBuffer scratch;    // region calls: inputs/outputs staged here
     DeviceBuffer actbuf;     // zg_gemv_device: prepared activations
@@ -41,6 +46,8 @@ void free_weight(zg_weight* w);
 int check_matrix(zg_ctx* ctx, int type, size_t cols, size_t rows, const void* bytes, size_t len);
 int lookup_or_register(zg_ctx* ctx, uint64_t source, const char* name, int type, size_t cols, size_t rows,
                        const void* bytes, size_t len, zg_weight** out);
+// Free a weight and remove it from the ctx cache (caller holds the lock).
+void drop_weight(zg_ctx* ctx, zg_weight* w);
 int build_weight(zg_ctx* ctx, int type, size_t cols, size_t rows, const void* bytes, size_t len,
                  std::unique_ptr<zg_weight>& out);
 bool all_finite(const float* x, size_t n);

@@ -68,7 +68,13 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
         tail_g = *(const v4f*)(a.norm + 4 * t);
         tail_z = *(const v4f*)(xin + 3 * W + h * D + 4 * t);
     }
-    float* col = a.state + (((size_t)b * a.H + h) * D + j) * D + 4 * s;
+    // the row's state: read from half cur[b], written to the other half (the
+    // draft the step's commit publishes), or in place without cur
+    const size_t row_floats = a.state_row ? a.state_row : (size_t)a.H * D * D;
+    const int cb = a.cur ? a.cur[b] : 0;
+    const size_t within = ((size_t)h * D + j) * D + 4 * s;
+    const float* col = a.state + (size_t)b * row_floats + (size_t)cb * a.state_half + within;
+    float* col_out = a.state + (size_t)b * row_floats + (a.cur ? (size_t)(1 - cb) * a.state_half : 0) + within;
     v4f sv[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) sv[c] = *(const v4f*)(col + 32 * c);
@@ -162,7 +168,7 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
         for (int t = 0; t < 4; ++t) cv[c][t] = fmaf(k[c][t], delta, cv[c][t]);
     const float o = column_dot(cv, q);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) *(v4f*)(col + 32 * c) = v4f{cv[c][0], cv[c][1], cv[c][2], cv[c][3]};
+    for (int c = 0; c < 4; ++c) *(v4f*)(col_out + 32 * c) = v4f{cv[c][0], cv[c][1], cv[c][2], cv[c][3]};
     if (s == 0) a.core[(size_t)b * W + h * D + j] = o * a.scale;
     if constexpr (HEAD) {
         // gated RMSNorm of the head (forward.rs:586-594) in act16_kernel's

@@ -135,15 +135,12 @@ hipError_t softmax_rows(const float* scores, size_t score_stride, const int* nto
 // Model-step helpers (zg_model.hip).  `status` is a device word: bit 0
 // nonfinite residual, bit 1 out-of-vocabulary token, bit 2 nonfinite logits.
 hipError_t embed(const DeviceWeight& w, const uint32_t* tokens, float* x, size_t B, int* status, hipStream_t s);
-hipError_t residual_add(float* x, const float* y, size_t n, int* status, hipStream_t s);
-hipError_t argmax(const float* logits, size_t V, size_t B, uint32_t* out, int* status, hipStream_t s);
 hipError_t fill_normal(void* p, size_t n, bool bf16, uint64_t seed, float sigma, hipStream_t s);
 hipError_t convert_kv(const void* in, void* out, size_t n, bool to_f32, hipStream_t s);
 hipError_t fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
-hipError_t advance_positions(int* pos, int* ntok, size_t B, hipStream_t s);  // B <= 64
 
 // ---------------------------------------------------- fused decode step
-// (zg_decode.hip).  A GEMV launch with an activation prologue and an output
+// (zg_fused*.hip, zg_batched.hip, zg_gdn_decode.hip, zg_attn_decode.hip).  A GEMV launch with an activation prologue and an output
 // epilogue:
 //   PRO_RMS       x[m][0:K] -> (x*inv)*gamma            (RMSNorm, eps)
 //   PRO_GATED     per group of `group` elements: ((x*inv)*gamma[i % group])
@@ -215,9 +212,14 @@ struct GdnDecodeArgs {
     const int* pos = nullptr;       // [B] position of this step's token
     const float *dt = nullptr, *ssm_a = nullptr;
     float eps = 0.0f, scale = 0.0f;
-    float* state = nullptr;  // [B][H][128][128] value-major
+    float* state = nullptr;  // row b at state + b*state_row: [H][128][128] value-major
     float* core = nullptr;   // [B][W]
     int H = 0;
+    // optional double-buffered rows (the session's uncommitted draft): row b
+    // reads half cur[b] (at + cur[b]*state_half) and writes the other half;
+    // without cur the state is updated in place.  state_row 0 = H*128*128.
+    const int* cur = nullptr;
+    size_t state_row = 0, state_half = 0;
     // batched rows (optional): the output projection's activation --
     // gated RMSNorm (ssm_norm [128], z = proj[3W:4W]) x silu(z) -- written as
     // f16 MFMA tiles for K = W (the layout act16_kernel writes), so that GEMM
@@ -285,9 +287,20 @@ struct AttnPrefillArgs {
 hipError_t attn_prefill(const AttnPrefillArgs& a, hipStream_t s);
 
 // Greedy ids of B logit rows (leading dimension ld) through partials
-// [argmax_partials(B)]; when `advance`, pos/ntok move on (tickets unused).
+// [argmax_partials(B)] (core/src/numerics.rs:126-140: first maximum wins,
+// a nonfinite logit sets status bit 2).  With `commit` non-null the last
+// launch also publishes the step for rows [0, B) when the status word is
+// clear: pos and ntok move on and cur flips (commit_step's rule).
 size_t argmax_partials(size_t B);
+struct StepCommit {
+    int* pos = nullptr;
+    int* ntok = nullptr;
+    int* cur = nullptr;
+};
 hipError_t argmax_step(const float* logits, size_t V, size_t ld, size_t B, uint32_t* greedy, int* status, float* pmax,
-                       int* pidx, unsigned* tickets, int* pos, int* ntok, int advance, hipStream_t s);
+                       int* pidx, const StepCommit* commit, hipStream_t s);
+// Publish a decode step for rows [0, B) if *status == 0: positions advance
+// and each row's GDN state half flips to the draft the step wrote.
+hipError_t commit_step(const StepCommit& c, const int* status, size_t B, hipStream_t s);
 
 }  // namespace zg

@@ -92,60 +92,6 @@ __global__ void embed_f32_kernel(const float* __restrict__ w, const uint32_t* __
     x[(size_t)b * K + i] = w[(size_t)t * K + i];
 }
 
-// Residual add that also flags nonfinite values (forward.rs:502 assert_finite).
-__global__ void residual_add_kernel(float* __restrict__ x, const float* __restrict__ y, size_t n,
-                                    int* __restrict__ status) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const float v = x[i] + y[i];
-    x[i] = v;
-    if (!finite_f32(v)) atomicOr(status, 1);
-}
-
-// Greedy readout per row: first maximum wins; nonfinite logits flag status
-// (core/src/numerics.rs:126-140).
-__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ logits, int V, uint32_t* __restrict__ out,
-                                                     int* __restrict__ status) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
-    const int b = blockIdx.x, tid = threadIdx.x;
-    const float* row = logits + (size_t)b * V;
-    float best = -INFINITY;
-    int bi = 0x7fffffff;
-    bool bad = false;
-    for (int i = tid; i < V; i += 256) {
-        const float v = row[i];
-        if (!finite_f32(v)) bad = true;
-        if (v > best) {
-            best = v;
-            bi = i;
-        }
-    }
-    if (bad) atomicOr(status, 4);
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(best, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        if (ov > best || (ov == best && oi < bi)) {
-            best = ov;
-            bi = oi;
-        }
-    }
-    if ((tid & 63) == 0) {
-        sv[tid >> 6] = best;
-        si[tid >> 6] = bi;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        best = sv[0];
-        bi = si[0];
-        for (int w = 1; w < 4; ++w)
-            if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
-                best = sv[w];
-                bi = si[w];
-            }
-        out[b] = (uint32_t)bi;
-    }
-}
 
 // Seeded counter-based normal samples (splitmix64 + Box-Muller) for the
 // synthetic decode prefix.
@@ -232,16 +178,6 @@ hipError_t embed(const DeviceWeight& w, const uint32_t* tokens, float* x, size_t
     return hipGetLastError();
 }
 
-hipError_t residual_add(float* x, const float* y, size_t n, int* status, hipStream_t s) {
-    hipLaunchKernelGGL(residual_add_kernel, dim3(blocks_for(n)), dim3(256), 0, s, x, y, n, status);
-    return hipGetLastError();
-}
-
-hipError_t argmax(const float* logits, size_t V, size_t B, uint32_t* out, int* status, hipStream_t s) {
-    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)B), dim3(256), 0, s, logits, (int)V, out, status);
-    return hipGetLastError();
-}
-
 hipError_t fill_normal(void* p, size_t n, bool bf16, uint64_t seed, float sigma, hipStream_t s) {
     const unsigned g = (unsigned)std::min<size_t>(blocks_for(n), 4096);
     if (bf16)
@@ -256,21 +192,6 @@ hipError_t convert_kv(const void* in, void* out, size_t n, bool to_f32, hipStrea
         hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(blocks_for(n)), dim3(256), 0, s, (const uint16_t*)in, (float*)out, n);
     else
         hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(blocks_for(n)), dim3(256), 0, s, (const float*)in, (uint16_t*)out, n);
-    return hipGetLastError();
-}
-
-// Rows [0, B) move one token on: pos += 1, ntok = pos + 1.
-__global__ void advance_positions_kernel(int* __restrict__ pos, int* __restrict__ ntok, int B) {
-    const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b < B) {
-        const int p = pos[b] + 1;
-        pos[b] = p;
-        ntok[b] = p + 1;
-    }
-}
-
-hipError_t advance_positions(int* pos, int* ntok, size_t B, hipStream_t s) {
-    hipLaunchKernelGGL(advance_positions_kernel, dim3(1), dim3(64), 0, s, pos, ntok, (int)B);
     return hipGetLastError();
 }
 

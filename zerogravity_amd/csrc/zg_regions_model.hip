@@ -230,6 +230,42 @@ int zg_gdn_decode_device(zg_ctx* ctx, size_t rows, size_t heads, const float* pr
     return ZG_COMPLETED;
 }
 
+// The batched rows' form of the same step: one workgroup per (head, row)
+// that also applies the gated RMSNorm (forward.rs:586-594) to the head's
+// output and writes ssm_out's activation in f16, in the MFMA A-operand tile
+// order the batched projections read (zg_gdn_decode_tiles_bytes).
+size_t zg_gdn_decode_tiles_bytes(size_t rows, size_t heads) { return (rows + 31) / 32 * 32 * heads * 128 * 2; }
+
+int zg_gdn_decode_gated_device(zg_ctx* ctx, size_t rows, size_t heads, const float* proj, size_t proj_stride,
+                               const float* conv_w, float* ring, const int32_t* positions, const float* dt,
+                               const float* ssm_a, const float* norm, float eps, float* state, float* core,
+                               void* tiles, void* stream) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!proj || !conv_w || !ring || !positions || !dt || !ssm_a || !norm || !state || !core || !tiles || rows == 0 ||
+        heads == 0 || rows > 65535 || heads > 1024 || heads % 2 || proj_stride < heads * 128 * 4 + 2 * heads ||
+        !(eps > 0.0f))
+        return fail(ctx, ZG_E_MALFORMED, "GDN decode geometry");
+    zg::GdnDecodeArgs d;
+    d.proj = proj;
+    d.proj_stride = proj_stride;
+    d.conv_w = conv_w;
+    d.ring = ring;
+    d.pos = positions;
+    d.dt = dt;
+    d.ssm_a = ssm_a;
+    d.eps = eps;
+    d.scale = 1.0f / sqrtf(128.0f);
+    d.state = state;
+    d.core = core;
+    d.H = (int)heads;
+    d.xh = tiles;
+    d.norm = norm;
+    ZG_HIP(zg::gdn_decode(d, rows, stream ? (hipStream_t)stream : ctx->stream));
+    return ZG_COMPLETED;
+}
+
 size_t zg_attn_decode_workspace_bytes(size_t rows, size_t q_heads, size_t max_ctx) {
     return rows * q_heads * (max_ctx + 2) * 4;  // scores [rows][q_heads][max_ctx], then {max, 1/sum}
 }
@@ -445,6 +481,34 @@ int zg_attention_value(zg_ctx* ctx, const float* probabilities, const float* val
     if (rc) return rc;
     if (!all_finite(out, query_heads * head_width))
         return fail(ctx, ZG_E_STATE, "incomplete/nonfinite source attention value proposal");
+    return ZG_COMPLETED;
+}
+
+// greedy_finite (core/src/numerics.rs:124-140) on the device for `rows`
+// rows of n logits: the first maximum wins (a later equal value, +0 after
+// -0 included, never replaces it), a nonfinite logit is ZG_E_STATE and an
+// empty or over-long vocabulary ZG_E_LIMIT.  The decode step's own greedy
+// readout runs these kernels.  out[rows].
+int zg_greedy(zg_ctx* ctx, const float* logits, size_t rows, size_t n, uint32_t* out) {
+    if (!ctx || !logits || !out || rows == 0 || rows > 65535) return fail(ctx, ZG_E_MALFORMED, "invalid greedy arguments");
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (n == 0 || n > 0x7fffffffu) return fail(ctx, ZG_E_LIMIT, "greedy vocabulary extent");
+    const size_t o_pm = align256(rows * n * 4), o_pi = o_pm + align256(zg::argmax_partials(rows) * 4),
+                 o_gr = o_pi + align256(zg::argmax_partials(rows) * 4), o_st = o_gr + align256(rows * 4);
+    int rc = ensure(ctx, ctx->scratch, o_st + 256);
+    if (rc) return rc;
+    char* base = (char*)ctx->scratch.ptr;
+    hipStream_t st = ctx->stream;
+    ZG_HIP(hipMemsetAsync(base + o_st, 0, 4, st));
+    ZG_HIP(hipMemcpyAsync(base, logits, rows * n * 4, hipMemcpyHostToDevice, st));
+    ZG_HIP(zg::argmax_step((const float*)base, n, n, rows, (uint32_t*)(base + o_gr), (int*)(base + o_st),
+                           (float*)(base + o_pm), (int*)(base + o_pi), nullptr, st));
+    int status = 0;
+    ZG_HIP(hipMemcpyAsync(out, base + o_gr, rows * 4, hipMemcpyDeviceToHost, st));
+    ZG_HIP(hipMemcpyAsync(&status, base + o_st, 4, hipMemcpyDeviceToHost, st));
+    ZG_HIP(hipStreamSynchronize(st));
+    if (status) return fail(ctx, ZG_E_STATE, "greedy requires finite logits");
     return ZG_COMPLETED;
 }
 

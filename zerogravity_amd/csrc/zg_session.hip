@@ -8,10 +8,20 @@
 //   attn in-proj = [attn_q | attn_k | attn_v]
 //   FFN          = [ffn_gate | ffn_up]
 // A decode step is then 5 launches per GDN layer, 6 per attention layer and
-// 3 around them (zg_decode.hip), replayed as one HIP graph per
-// (rows, token/logit/greedy buffers): every kernel reads positions from
-// device memory, so the captured step is valid at any position.
+// 3 around them, replayed as one HIP graph per (rows, token/logit/greedy
+// buffers, commit): every kernel reads positions from device memory, so the
+// captured step is valid at any position.
+//
+// Publication (QwenDenseCpu::next_logits / commit, lib.rs:1057-1070,
+// 1211-1225; prefill_transaction, lib.rs:1114-1187): a step writes the KV
+// row at the position (outside the published prefix), the conv ring slot
+// p % 4 (whose old value, x[p-4], no tap reads any more) and the GDN state
+// into the draft half of a double-buffered per-row state.  Its last kernel
+// publishes it -- positions advance and each row's `cur` half flips -- only
+// when the step's status word is clear, so a failed step leaves position,
+// conv history, GDN state and KV prefix exactly as they were.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -54,6 +64,7 @@ struct LayerW {
 struct zg_model {
     zg_ctx* ctx = nullptr;
     uint64_t source = 0;
+    uint64_t serial = 0;  // distinguishes models for snapshot ownership
     zg_geometry g{};
     std::vector<LayerW> layers;
     zg_weight* embd = nullptr;
@@ -61,6 +72,7 @@ struct zg_model {
     std::vector<void*> vecs;  // device copies of F32 parameter vectors
     size_t n_gdn = 0, n_attn = 0;
     bool all_q4k = true;  // every projection Q4_K: batched split-K residuals allowed
+    std::vector<zg_weight*> refs;  // resident weights this model holds a reference on
 };
 
 struct zg_session {
@@ -82,10 +94,25 @@ struct zg_session {
     float* parts = nullptr;  // split-K partial tiles of residual projections (B > 4)
     void* xh2 = nullptr;     // the SwiGLU product in f16 tiles, down projection input (B > 4)
     size_t y0w = 0;
-    std::vector<float*> ring, rec;  // per GDN layer: conv ring [B][3W][4], state [B][H][128][128]
+    std::vector<float*> ring, rec;  // per GDN layer: conv ring [B][3W][4], state [B][2][H][128][128]
     std::vector<void*> kc, vc;      // per attention layer: [B][max_ctx][kv_heads*256]
     std::vector<int> layer_slot;    // layer -> index into ring/rec or kc/vc
-    std::map<std::tuple<size_t, const void*, const void*, const void*>, hipGraphExec_t> graphs;
+    // per-row GDN state half holding the published state (the other half is
+    // the draft a step writes); host mirror of d_cur
+    int* d_cur = nullptr;
+    std::vector<int> cur;
+    size_t pending_rows = 0;  // rows of an uncommitted zg_session_propose
+    // steps queued by zg_decode_step_device on a caller's stream: host
+    // entry points wait on this event and re-read positions from the device
+    hipEvent_t dev_ev = nullptr;
+    bool async_steps = false;
+    // captured steps, least recently used evicted beyond kGraphCache
+    struct GraphEntry {
+        hipGraphExec_t exec = nullptr;
+        uint64_t used = 0;
+    };
+    std::map<std::tuple<size_t, const void*, const void*, const void*, int>, GraphEntry> graphs;
+    uint64_t graph_clock = 0;
     // batched prefill buffers, sized for pf_cap prompt tokens
     size_t pf_cap = 0;
     std::vector<void*> pf;
@@ -100,6 +127,15 @@ const zg_tensor_desc* find_tensor(const zg_tensor_desc* t, size_t n, const std::
 }
 
 std::string lname(unsigned i, const char* suffix) { return "blk." + std::to_string(i) + "." + suffix; }
+
+// The model holds one reference on each resident weight it uses: the
+// weight is freed when its last model is destroyed, unless an API caller
+// registered it (then zg_source_release frees it).
+void take_ref(zg_model* m, zg_weight* w) {
+    if (std::find(m->refs.begin(), m->refs.end(), w) != m->refs.end()) return;
+    w->model_refs += 1;
+    m->refs.push_back(w);
+}
 
 // Rows of several [K, N_i] GGUF matrices stacked into registered weights:
 // one per run of consecutive matrices sharing a codec, at its column offset.
@@ -148,6 +184,7 @@ int load_stack(zg_model* m, const zg_tensor_desc* ts, size_t n, const std::vecto
             rc = lookup_or_register(ctx, m->source, k.c_str(), type, K, rows, buf.data(), bytes, &p.w);
         }
         if (rc) return rc;
+        take_ref(m, p.w);
         out->push_back(p);
         col += rows;
         i = j;
@@ -194,12 +231,20 @@ size_t conv_floats(const zg_geometry& g) { return (size_t)g.gdn_heads * g.gdn_di
 size_t ring_floats(const zg_geometry& g) { return (size_t)g.gdn_heads * g.gdn_dim * 3 * 4; }  // device ring
 size_t rec_floats(const zg_geometry& g) { return (size_t)g.gdn_heads * g.gdn_dim * g.gdn_dim; }
 size_t kvw(const zg_geometry& g) { return (size_t)g.kv_heads * g.head_dim; }
+// Row `row`'s GDN state half `half` of GDN layer slot `slot`.
+float* rec_half(zg_session* s, size_t slot, size_t row, int half) {
+    return s->rec[slot] + (row * 2 + (size_t)half) * rec_floats(s->m->g);
+}
+constexpr size_t kGraphCache = 16;  // captured step graphs kept per session
 
 // One decode step for rows [0, B): tokens in `tokens` (device), positions in
 // d_pos / d_ntok.  Logits to `logits` (may be the session buffer), greedy
-// ids to `greedy` (nullable); positions advance on the device as the last
-// launch.  Asynchronous on st, no host synchronisation, capturable.
-int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_t* greedy, hipStream_t st) {
+// ids to `greedy` (nullable).  With `commit` the last launch publishes the
+// step (positions advance, GDN halves flip) when the status word is clear;
+// without it the step stays a draft for zg_session_commit.  Asynchronous on
+// st, no host synchronisation, capturable.
+int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_t* greedy, bool commit,
+         hipStream_t st) {
     zg_model* m = s->m;
     zg_ctx* ctx = m->ctx;
     const zg_geometry& g = m->g;
@@ -266,6 +311,9 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             d.eps = g.eps;
             d.scale = 1.0f / sqrtf((float)g.gdn_dim);
             d.state = s->rec[slot];
+            d.cur = s->d_cur;
+            d.state_row = 2 * rec_floats(g);
+            d.state_half = rec_floats(g);
             d.core = s->core;
             d.H = (int)g.gdn_heads;
             // batched rows: the kernel also writes ssm_out's gated-norm f16
@@ -328,30 +376,45 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
                         H));
         }
     }
+    zg::StepCommit sc;
+    sc.pos = s->d_pos;
+    sc.ntok = s->d_ntok;
+    sc.cur = s->d_cur;
     if (logits || greedy) {
         float* lg = logits ? logits : s->logits;
         ZG_HIP(gemv(m->embd, zg::PRO_RMS, s->x, H, nullptr, 0, m->out_norm, zg::EPI_STORE, lg, V));
         if (greedy) {
-            ZG_HIP(zg::argmax_step(lg, V, V, B, greedy, s->d_status, s->pmax, s->pidx, s->tickets, s->d_pos, s->d_ntok, 1,
-                                   st));
+            ZG_HIP(zg::argmax_step(lg, V, V, B, greedy, s->d_status, s->pmax, s->pidx, commit ? &sc : nullptr, st));
             return ZG_COMPLETED;
         }
     }
-    ZG_HIP(zg::advance_positions(s->d_pos, s->d_ntok, B, st));
+    if (commit) ZG_HIP(zg::commit_step(sc, s->d_status, B, st));
     return ZG_COMPLETED;
 }
 
-// The step through a cached HIP graph (one per rows/buffer set), captured on
-// first use.  ZG_GRAPHS=0 in the environment launches the kernels directly.
-int run_step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_t* greedy, hipStream_t st) {
+// The step through a cached HIP graph (one per rows/buffer set/commit),
+// captured on first use; the least recently used graph is dropped beyond
+// kGraphCache.  ZG_GRAPHS=0 in the environment launches the kernels
+// directly.
+int run_step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_t* greedy, bool commit,
+             hipStream_t st) {
     zg_ctx* ctx = s->m->ctx;
-    if (!s->use_graphs) return step(s, B, tokens, logits, greedy, st);
-    const auto key = std::make_tuple(B, (const void*)tokens, (const void*)logits, (const void*)greedy);
+    if (!s->use_graphs) return step(s, B, tokens, logits, greedy, commit, st);
+    const auto key = std::make_tuple(B, (const void*)tokens, (const void*)logits, (const void*)greedy, (int)commit);
     auto it = s->graphs.find(key);
     if (it == s->graphs.end()) {
+        if (s->graphs.size() >= kGraphCache) {
+            auto old = s->graphs.begin();
+            for (auto g = s->graphs.begin(); g != s->graphs.end(); ++g)
+                if (g->second.used < old->second.used) old = g;
+            // an evicted graph may still be running on a stream
+            ZG_HIP(hipDeviceSynchronize());
+            (void)hipGraphExecDestroy(old->second.exec);
+            s->graphs.erase(old);
+        }
         hipGraph_t graph = nullptr;
         ZG_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
-        const int rc = step(s, B, tokens, logits, greedy, st);
+        const int rc = step(s, B, tokens, logits, greedy, commit, st);
         const hipError_t e = hipStreamEndCapture(st, &graph);
         if (rc) {
             if (e == hipSuccess && graph) (void)hipGraphDestroy(graph);
@@ -362,12 +425,38 @@ int run_step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uin
         const hipError_t e2 = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
         (void)hipGraphDestroy(graph);
         ZG_HIP(e2);
-        it = s->graphs.emplace(key, exec).first;
+        it = s->graphs.emplace(key, zg_session::GraphEntry{exec, 0}).first;
     }
-    ZG_HIP(hipGraphLaunch(it->second, st));
+    it->second.used = ++s->graph_clock;
+    ZG_HIP(hipGraphLaunch(it->second.exec, st));
     return ZG_COMPLETED;
 }
 
+// Host mirrors of positions and GDN halves re-read from the device (after
+// asynchronous steps, whose commits the host cannot see, or a failed step).
+int pull_positions(zg_session* s, hipStream_t st) {
+    zg_ctx* ctx = s->m->ctx;
+    const size_t B = s->max_batch;
+    ZG_HIP(hipMemcpyAsync(s->pos.data(), s->d_pos, B * sizeof(int), hipMemcpyDeviceToHost, st));
+    ZG_HIP(hipMemcpyAsync(s->cur.data(), s->d_cur, B * sizeof(int), hipMemcpyDeviceToHost, st));
+    ZG_HIP(hipStreamSynchronize(st));
+    return ZG_COMPLETED;
+}
+
+// Before any host-synchronous entry: steps queued on a caller's stream have
+// finished and the host mirrors are the device's.
+int settle(zg_session* s) {
+    if (!s->async_steps) return ZG_COMPLETED;
+    zg_ctx* ctx = s->m->ctx;
+    ZG_HIP(hipEventSynchronize(s->dev_ev));
+    s->async_steps = false;
+    return pull_positions(s, ctx->stream);
+}
+
+// The status word of the steps since the last check.  A failed step did
+// not publish (its commit is gated on this word), so the session keeps the
+// state before it: the host mirrors are re-read from the device, the word
+// is cleared, and the error is returned.
 int read_status(zg_session* s, hipStream_t st) {
     zg_ctx* ctx = s->m->ctx;
     int status = 0;
@@ -375,8 +464,9 @@ int read_status(zg_session* s, hipStream_t st) {
     ZG_HIP(hipStreamSynchronize(st));
     if (status) {
         ZG_HIP(hipMemsetAsync(s->d_status, 0, sizeof(int), st));
-        ZG_HIP(hipStreamSynchronize(st));
-        s->poisoned = true;
+        int rc = pull_positions(s, st);
+        if (rc) return rc;
+        s->pending_rows = 0;
         if (status & 2) return fail(ctx, ZG_E_MALFORMED, "decode step contains an out-of-vocabulary token id");
         if (status & 1) return fail(ctx, ZG_E_STATE, "nonfinite layer computation");
         if (status & 8) return fail(ctx, ZG_E_STATE, "degenerate attention softmax");
@@ -400,6 +490,7 @@ int sync_positions(zg_session* s, hipStream_t st) {
     }
     ZG_HIP(hipMemcpyAsync(s->d_pos, p.data(), B * sizeof(int), hipMemcpyHostToDevice, st));
     ZG_HIP(hipMemcpyAsync(s->d_ntok, t.data(), B * sizeof(int), hipMemcpyHostToDevice, st));
+    ZG_HIP(hipMemcpyAsync(s->d_cur, s->cur.data(), B * sizeof(int), hipMemcpyHostToDevice, st));
     // pageable source: make the copy complete before the vectors go away
     ZG_HIP(hipStreamSynchronize(st));
     s->pos_dirty = false;
@@ -408,7 +499,7 @@ int sync_positions(zg_session* s, hipStream_t st) {
 
 int check_rows(zg_session* s, size_t rows) {
     zg_ctx* ctx = s->m->ctx;
-    if (s->poisoned) return fail(ctx, ZG_E_STATE, "session poisoned by a failed step: reset or import state");
+    if (s->poisoned) return fail(ctx, ZG_E_STATE, "session poisoned by a failed launch: reset or import state");
     if (rows == 0 || rows > s->max_batch) return fail(ctx, ZG_E_LIMIT, "row count exceeds the session batch");
     for (size_t b = 0; b < rows; ++b)
         if ((size_t)s->pos[b] >= s->max_ctx) return fail(ctx, ZG_E_LIMIT, "model context capacity exhausted");
@@ -418,7 +509,90 @@ int check_rows(zg_session* s, size_t rows) {
 // Slot of the ring holding x[pos - 3 + k] (k = 0, 1, 2) at a row's position.
 inline size_t ring_slot(int pos, int k) { return (size_t)((pos + 1 + k) & 3); }
 
+// A device copy of one row's published state: per GDN layer the conv ring
+// and the published GDN half, and with_kv the K and V rows [0, pos) of each
+// attention layer.  Restored into half 0 of a row.
+struct RowImage {
+    void* dev = nullptr;
+    size_t bytes = 0;
+    int pos = 0;
+    bool with_kv = false;
+};
+
+size_t kv_row_bytes(const zg_session* s) { return s->max_ctx * kvw(s->m->g) * (s->kv_bf16 ? 2 : 4); }
+
+int save_row(zg_session* s, size_t row, bool with_kv, RowImage* img) {
+    zg_ctx* ctx = s->m->ctx;
+    const zg_geometry& g = s->m->g;
+    const size_t esz = s->kv_bf16 ? 2 : 4, kvb = (size_t)s->pos[row] * kvw(g) * esz;
+    img->pos = s->pos[row];
+    img->with_kv = with_kv;
+    img->bytes = s->ring.size() * (ring_floats(g) + rec_floats(g)) * 4 + (with_kv ? s->kc.size() * 2 * kvb : 0);
+    ZG_HIP(hipMalloc(&img->dev, std::max<size_t>(img->bytes, 256)));
+    char* at = (char*)img->dev;
+    hipStream_t st = ctx->stream;
+    for (size_t i = 0; i < s->ring.size(); ++i) {
+        ZG_HIP(hipMemcpyAsync(at, s->ring[i] + row * ring_floats(g), ring_floats(g) * 4, hipMemcpyDeviceToDevice, st));
+        at += ring_floats(g) * 4;
+        ZG_HIP(hipMemcpyAsync(at, rec_half(s, i, row, s->cur[row]), rec_floats(g) * 4, hipMemcpyDeviceToDevice, st));
+        at += rec_floats(g) * 4;
+    }
+    if (with_kv && kvb)
+        for (size_t i = 0; i < s->kc.size(); ++i)
+            for (void* cache : {s->kc[i], s->vc[i]}) {
+                ZG_HIP(hipMemcpyAsync(at, (char*)cache + row * kv_row_bytes(s), kvb, hipMemcpyDeviceToDevice, st));
+                at += kvb;
+            }
+    ZG_HIP(hipStreamSynchronize(st));
+    return ZG_COMPLETED;
+}
+
+// The row takes the image's state and position (its GDN state in half 0).
+// Without KV the row keeps its cache, whose prefix [0, pos) the image's
+// position must not exceed the row's own at save time.
+int load_row(zg_session* s, size_t row, const RowImage& img) {
+    zg_ctx* ctx = s->m->ctx;
+    const zg_geometry& g = s->m->g;
+    const size_t esz = s->kv_bf16 ? 2 : 4, kvb = (size_t)img.pos * kvw(g) * esz;
+    const char* at = (const char*)img.dev;
+    hipStream_t st = ctx->stream;
+    for (size_t i = 0; i < s->ring.size(); ++i) {
+        ZG_HIP(hipMemcpyAsync(s->ring[i] + row * ring_floats(g), at, ring_floats(g) * 4, hipMemcpyDeviceToDevice, st));
+        at += ring_floats(g) * 4;
+        ZG_HIP(hipMemcpyAsync(rec_half(s, i, row, 0), at, rec_floats(g) * 4, hipMemcpyDeviceToDevice, st));
+        at += rec_floats(g) * 4;
+    }
+    if (img.with_kv && kvb)
+        for (size_t i = 0; i < s->kc.size(); ++i)
+            for (void* cache : {s->kc[i], s->vc[i]}) {
+                ZG_HIP(hipMemcpyAsync((char*)cache + row * kv_row_bytes(s), at, kvb, hipMemcpyDeviceToDevice, st));
+                at += kvb;
+            }
+    ZG_HIP(hipStreamSynchronize(st));
+    s->pos[row] = img.pos;
+    s->cur[row] = 0;
+    s->pos_dirty = true;
+    s->pending_rows = 0;
+    return ZG_COMPLETED;
+}
+
+void free_image(RowImage& img) {
+    if (img.dev) (void)hipFree(img.dev);
+    img.dev = nullptr;
+}
+
+std::atomic<uint64_t> g_model_serial{1};
+
 }  // namespace
+
+struct zg_snapshot {
+    uint64_t model_serial = 0;
+    int device = 0;
+    int kv_bf16 = 0;
+    RowImage img;
+};
+
+namespace {}  // namespace
 
 extern "C" {
 
@@ -437,6 +611,7 @@ int zg_model_load(zg_ctx* ctx, uint64_t source_id, const zg_geometry* g, const z
     auto m = new zg_model();
     m->ctx = ctx;
     m->source = source_id;
+    m->serial = g_model_serial.fetch_add(1);
     m->g = *g;
     const uint64_t H = g->hidden, F = g->ffn, V = g->vocab, W = (uint64_t)g->gdn_heads * g->gdn_dim;
     const uint64_t QD = (uint64_t)g->q_heads * g->head_dim, KD = (uint64_t)g->kv_heads * g->head_dim;
@@ -490,9 +665,12 @@ void zg_model_destroy(zg_model* m) {
     zg_ctx* ctx = m->ctx;
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
     (void)hipSetDevice(ctx->device);
-    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipDeviceSynchronize();
     for (void* p : m->vecs) (void)hipFree(p);
-    zg_source_release(ctx, m->source);
+    for (zg_weight* w : m->refs) {
+        w->model_refs -= 1;
+        if (w->model_refs == 0 && !w->api_pinned) zgc::drop_weight(ctx, w);
+    }
     delete m;
 }
 
@@ -536,8 +714,14 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     auto A = [&](void** p, size_t bytes) {
         if (!rc) rc = dalloc(s, p, bytes);
     };
+    s->cur.assign(max_batch, 0);
+    if (hipEventCreateWithFlags(&s->dev_ev, hipEventDisableTiming) != hipSuccess) {
+        delete s;
+        return fail(ctx, ZG_E_DEVICE, "session event");
+    }
     A((void**)&s->d_pos, B * 4);
     A((void**)&s->d_ntok, B * 4);
+    A((void**)&s->d_cur, B * 4);
     A((void**)&s->d_status, 4);
     A((void**)&s->d_tokens, B * 4);
     A((void**)&s->d_greedy, B * 4);
@@ -568,7 +752,7 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
             s->layer_slot[i] = (int)s->ring.size();
             float *c = nullptr, *r = nullptr;
             A((void**)&c, B * ring_floats(g) * 4);
-            A((void**)&r, B * rec_floats(g) * 4);
+            A((void**)&r, B * 2 * rec_floats(g) * 4);  // published half + draft half per row
             s->ring.push_back(c);
             s->rec.push_back(r);
         }
@@ -587,9 +771,10 @@ void zg_session_destroy(zg_session* s) {
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
     (void)hipSetDevice(ctx->device);
     (void)hipDeviceSynchronize();
-    for (auto& kv : s->graphs) (void)hipGraphExecDestroy(kv.second);
+    for (auto& kv : s->graphs) (void)hipGraphExecDestroy(kv.second.exec);
     for (void* p : s->allocs) (void)hipFree(p);
     for (void* p : s->pf) (void)hipFree(p);
+    if (s->dev_ev) (void)hipEventDestroy(s->dev_ev);
     delete s;
 }
 
@@ -600,8 +785,10 @@ int zg_session_reset(zg_session* s) {
     (void)hipSetDevice(ctx->device);
     const zg_geometry& g = s->m->g;
     const size_t B = s->max_batch;
+    int rc = settle(s);
+    if (rc) return rc;
     for (float* c : s->ring) ZG_HIP(hipMemsetAsync(c, 0, B * ring_floats(g) * 4, ctx->stream));
-    for (float* r : s->rec) ZG_HIP(hipMemsetAsync(r, 0, B * rec_floats(g) * 4, ctx->stream));
+    for (float* r : s->rec) ZG_HIP(hipMemsetAsync(r, 0, B * 2 * rec_floats(g) * 4, ctx->stream));
     const size_t kvb = B * s->max_ctx * kvw(g) * (s->kv_bf16 ? 2 : 4);
     for (size_t i = 0; i < s->kc.size(); ++i) {
         ZG_HIP(hipMemsetAsync(s->kc[i], 0, kvb, ctx->stream));
@@ -611,8 +798,10 @@ int zg_session_reset(zg_session* s) {
     ZG_HIP(hipMemsetAsync(s->tickets, 0, B * 4, ctx->stream));
     ZG_HIP(hipStreamSynchronize(ctx->stream));
     std::fill(s->pos.begin(), s->pos.end(), 0);
+    std::fill(s->cur.begin(), s->cur.end(), 0);
     s->pos_dirty = true;
     s->poisoned = false;
+    s->pending_rows = 0;
     return ZG_COMPLETED;
 }
 
@@ -626,9 +815,10 @@ int zg_session_reset_row(zg_session* s, size_t row) {
     if (row >= s->max_batch) return fail(ctx, ZG_E_LIMIT, "row outside the session batch");
     const zg_geometry& g = s->m->g;
     hipStream_t st = ctx->stream;
-    ZG_HIP(hipDeviceSynchronize());  // work queued on a caller's stream (device entry points) lands first
+    int rc = settle(s);  // work queued on a caller's stream lands first
+    if (rc) return rc;
     for (float* c : s->ring) ZG_HIP(hipMemsetAsync(c + row * ring_floats(g), 0, ring_floats(g) * 4, st));
-    for (float* r : s->rec) ZG_HIP(hipMemsetAsync(r + row * rec_floats(g), 0, rec_floats(g) * 4, st));
+    for (float* r : s->rec) ZG_HIP(hipMemsetAsync(r + row * 2 * rec_floats(g), 0, 2 * rec_floats(g) * 4, st));
     const size_t rowb = s->max_ctx * kvw(g) * (s->kv_bf16 ? 2 : 4);
     for (size_t i = 0; i < s->kc.size(); ++i) {
         ZG_HIP(hipMemsetAsync((char*)s->kc[i] + row * rowb, 0, rowb, st));
@@ -636,7 +826,9 @@ int zg_session_reset_row(zg_session* s, size_t row) {
     }
     ZG_HIP(hipStreamSynchronize(st));
     s->pos[row] = 0;
+    s->cur[row] = 0;
     s->pos_dirty = true;
+    s->pending_rows = 0;
     return ZG_COMPLETED;
 }
 
@@ -654,12 +846,14 @@ int zg_session_copy_row(zg_session* s, size_t dst, size_t src) {
     if (dst == src) return ZG_COMPLETED;
     const zg_geometry& g = s->m->g;
     hipStream_t st = ctx->stream;
-    ZG_HIP(hipDeviceSynchronize());
+    int rc = settle(s);
+    if (rc) return rc;
     for (float* c : s->ring)
         ZG_HIP(hipMemcpyAsync(c + dst * ring_floats(g), c + src * ring_floats(g), ring_floats(g) * 4,
                               hipMemcpyDeviceToDevice, st));
-    for (float* r : s->rec)
-        ZG_HIP(hipMemcpyAsync(r + dst * rec_floats(g), r + src * rec_floats(g), rec_floats(g) * 4,
+    // src's published half becomes dst's half 0
+    for (size_t i = 0; i < s->rec.size(); ++i)
+        ZG_HIP(hipMemcpyAsync(rec_half(s, i, dst, 0), rec_half(s, i, src, s->cur[src]), rec_floats(g) * 4,
                               hipMemcpyDeviceToDevice, st));
     const size_t esz = s->kv_bf16 ? 2 : 4;
     const size_t rowb = s->max_ctx * kvw(g) * esz;
@@ -674,7 +868,9 @@ int zg_session_copy_row(zg_session* s, size_t dst, size_t src) {
     }
     ZG_HIP(hipStreamSynchronize(st));
     s->pos[dst] = s->pos[src];
+    s->cur[dst] = 0;
     s->pos_dirty = true;
+    s->pending_rows = 0;
     return ZG_COMPLETED;
 }
 
@@ -683,57 +879,124 @@ int zg_session_position(const zg_session* s, size_t row) {
     return s->pos[row];
 }
 
-int zg_decode_step(zg_session* s, size_t rows, const uint32_t* tokens, float* logits, uint32_t* greedy) {
-    if (!s || !tokens) return ZG_E_MALFORMED;
+namespace {
+
+// One step of rows [0, rows) from host tokens; with `commit` it publishes
+// (QwenDenseCpu::forward), else it leaves a proposal (next_logits).
+int host_step(zg_session* s, size_t rows, const uint32_t* tokens, float* logits, uint32_t* greedy, bool commit) {
     zg_ctx* ctx = s->m->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    (void)hipSetDevice(ctx->device);
-    int rc = check_rows(s, rows);
+    int rc = settle(s);
     if (rc) return rc;
+    if ((rc = check_rows(s, rows))) return rc;
     for (size_t b = 0; b < rows; ++b)
         if (tokens[b] >= s->m->g.vocab) return fail(ctx, ZG_E_MALFORMED, "decode step contains an out-of-vocabulary token id");
     hipStream_t st = ctx->stream;
+    s->pending_rows = 0;
     if ((rc = sync_positions(s, st))) return rc;
     ZG_HIP(hipMemcpyAsync(s->d_tokens, tokens, rows * 4, hipMemcpyHostToDevice, st));
     ZG_HIP(hipStreamSynchronize(st));
     const bool want = logits || greedy;
-    if ((rc = run_step(s, rows, s->d_tokens, want ? s->logits : nullptr, want ? s->d_greedy : nullptr, st))) {
-        s->poisoned = true;
+    if ((rc = run_step(s, rows, s->d_tokens, want ? s->logits : nullptr, want ? s->d_greedy : nullptr, commit, st))) {
+        s->poisoned = true;  // a launch failed: the device state is unknown
         return rc;
     }
-    for (size_t b = 0; b < rows; ++b) s->pos[b] += 1;
-    if ((rc = read_status(s, st))) return rc;
+    if ((rc = read_status(s, st))) return rc;  // nothing was published
+    if (commit) {
+        for (size_t b = 0; b < rows; ++b) {
+            s->pos[b] += 1;
+            s->cur[b] ^= 1;
+        }
+    } else {
+        s->pending_rows = rows;
+    }
     if (logits) ZG_HIP(hipMemcpyAsync(logits, s->logits, rows * s->m->g.vocab * 4, hipMemcpyDeviceToHost, st));
     if (greedy) ZG_HIP(hipMemcpyAsync(greedy, s->d_greedy, rows * 4, hipMemcpyDeviceToHost, st));
     ZG_HIP(hipStreamSynchronize(st));
     return ZG_COMPLETED;
 }
 
+}  // namespace
+
+int zg_decode_step(zg_session* s, size_t rows, const uint32_t* tokens, float* logits, uint32_t* greedy) {
+    if (!s || !tokens) return ZG_E_MALFORMED;
+    zg_ctx* ctx = s->m->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    return host_step(s, rows, tokens, logits, greedy, true);
+}
+
+int zg_session_propose(zg_session* s, size_t rows, const uint32_t* tokens, float* logits, uint32_t* greedy) {
+    if (!s || !tokens) return ZG_E_MALFORMED;
+    zg_ctx* ctx = s->m->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    return host_step(s, rows, tokens, logits, greedy, false);
+}
+
+int zg_session_commit(zg_session* s) {
+    if (!s) return ZG_E_MALFORMED;
+    zg_ctx* ctx = s->m->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    int rc = settle(s);
+    if (rc) return rc;
+    if (s->pending_rows == 0) return fail(ctx, ZG_E_STATE, "session holds no prepared proposal");
+    const size_t rows = s->pending_rows;
+    zg::StepCommit sc;
+    sc.pos = s->d_pos;
+    sc.ntok = s->d_ntok;
+    sc.cur = s->d_cur;
+    ZG_HIP(zg::commit_step(sc, s->d_status, rows, ctx->stream));
+    ZG_HIP(hipStreamSynchronize(ctx->stream));
+    for (size_t b = 0; b < rows; ++b) {
+        s->pos[b] += 1;
+        s->cur[b] ^= 1;
+    }
+    s->pending_rows = 0;
+    return ZG_COMPLETED;
+}
+
+// Per-token prefill, atomic over the whole call (prefill_transaction,
+// lib.rs:1114-1187): the rows' published state is saved on the device
+// first and restored if any token fails.
 int zg_prefill(zg_session* s, size_t rows, size_t n, const uint32_t* tokens, float* logits) {
     if (!s || !tokens || n == 0) return ZG_E_MALFORMED;
     zg_ctx* ctx = s->m->ctx;
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    int rc = settle(s);
+    if (rc) return rc;
+    if ((rc = check_rows(s, rows))) return rc;
+    for (size_t b = 0; b < rows; ++b)
+        if ((size_t)s->pos[b] + n > s->max_ctx) return fail(ctx, ZG_E_LIMIT, "prompt exceeds the session context");
+    for (size_t i = 0; i < rows * n; ++i)
+        if (tokens[i] >= s->m->g.vocab) return fail(ctx, ZG_E_MALFORMED, "prompt contains an out-of-vocabulary token id");
+    std::vector<RowImage> saved(rows);
+    for (size_t b = 0; b < rows && !rc; ++b) rc = save_row(s, b, false, &saved[b]);
     std::vector<uint32_t> col(rows);
-    for (size_t t = 0; t < n; ++t) {
+    for (size_t t = 0; t < n && !rc; ++t) {
         for (size_t b = 0; b < rows; ++b) col[b] = tokens[b * n + t];
-        int rc = zg_decode_step(s, rows, col.data(), t + 1 == n ? logits : nullptr, nullptr);
-        if (rc) return rc;
+        rc = host_step(s, rows, col.data(), t + 1 == n ? logits : nullptr, nullptr, true);
     }
-    return ZG_COMPLETED;
+    if (rc) {
+        const std::string msg = ctx->err;
+        for (size_t b = 0; b < rows; ++b)
+            if (saved[b].dev && load_row(s, b, saved[b])) s->poisoned = true;
+        zgc::fail(ctx, rc, msg);
+    }
+    for (RowImage& img : saved) free_image(img);
+    return rc;
 }
 
 // Batched prefill of one row: embed the n tokens, run every layer over all of
 // them (batched MFMA projections, chunked GDN prefill, causal attention with
 // the KV append), and the LM head on the last.  Same result as n decode
 // steps of that row up to the order of summation (end-to-end tolerance).
-int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* tokens, float* logits) {
-    if (!s || !tokens || n == 0) return ZG_E_MALFORMED;
+namespace {
+
+int prefill_batched_body(zg_session* s, size_t row, size_t n, const uint32_t* tokens, float* logits) {
     zg_model* m = s->m;
     zg_ctx* ctx = m->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    (void)hipSetDevice(ctx->device);
-    if (s->poisoned) return fail(ctx, ZG_E_STATE, "session poisoned by a failed step: reset or import state");
-    if (row >= s->max_batch) return fail(ctx, ZG_E_LIMIT, "row outside the session batch");
     const zg_geometry& g = m->g;
     if ((size_t)s->pos[row] + n > s->max_ctx) return fail(ctx, ZG_E_LIMIT, "prompt exceeds the session context");
     for (size_t i = 0; i < n; ++i)
@@ -816,7 +1079,7 @@ int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* toke
         if (!L.full) {
             ZG_HIP(gemm(L.in_proj[0].w, zg::PRO_RMS, x, H, nullptr, 0, L.attn_norm, zg::EPI_STORE, pj, ldp));
             float* ring = s->ring[slot] + row * 3 * W * 4;
-            float* state = s->rec[slot] + row * GH * g.gdn_dim * g.gdn_dim;
+            float* state = rec_half(s, (size_t)slot, row, s->cur[row]);
             ZG_HIP(zg::gdn_prefill_conv(pj, ldp, n, W, GH, L.conv_w, ring, pos0, L.ssm_dt, L.ssm_a, (float*)s->pf[Q],
                                         (float*)s->pf[K], (float*)s->pf[V], (float*)s->pf[BETA],
                                         (float*)s->pf[LOGD], st));
@@ -888,6 +1151,33 @@ int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* toke
     return ZG_COMPLETED;
 }
 
+}  // namespace
+
+// Atomic like prefill_transaction (lib.rs:1114-1187): the row's conv ring
+// and GDN state are saved on the device first and put back if the prompt
+// fails (its KV rows lie past the published position).
+int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* tokens, float* logits) {
+    if (!s || !tokens || n == 0) return ZG_E_MALFORMED;
+    zg_ctx* ctx = s->m->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (s->poisoned) return fail(ctx, ZG_E_STATE, "session poisoned by a failed launch: reset or import state");
+    if (row >= s->max_batch) return fail(ctx, ZG_E_LIMIT, "row outside the session batch");
+    int rc = settle(s);
+    if (rc) return rc;
+    s->pending_rows = 0;
+    RowImage saved;
+    if ((rc = save_row(s, row, false, &saved))) return rc;
+    rc = prefill_batched_body(s, row, n, tokens, logits);
+    if (rc) {
+        const std::string msg = ctx->err;
+        if (load_row(s, row, saved)) s->poisoned = true;
+        zgc::fail(ctx, rc, msg);
+    }
+    free_image(saved);
+    return rc;
+}
+
 int zg_decode_step_device(zg_session* s, size_t rows, const uint32_t* d_tokens, float* d_logits, uint32_t* d_greedy,
                           void* stream) {
     if (!s || !d_tokens) return ZG_E_MALFORMED;
@@ -897,12 +1187,21 @@ int zg_decode_step_device(zg_session* s, size_t rows, const uint32_t* d_tokens, 
     int rc = check_rows(s, rows);
     if (rc) return rc;
     hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
+    s->pending_rows = 0;
     if ((rc = sync_positions(s, st))) return rc;
-    if ((rc = run_step(s, rows, d_tokens, d_logits ? d_logits : (d_greedy ? s->logits : nullptr), d_greedy, st))) {
+    if ((rc = run_step(s, rows, d_tokens, d_logits ? d_logits : (d_greedy ? s->logits : nullptr), d_greedy, true,
+                       st))) {
         s->poisoned = true;
         return rc;
     }
-    for (size_t b = 0; b < rows; ++b) s->pos[b] += 1;
+    ZG_HIP(hipEventRecord(s->dev_ev, st));
+    s->async_steps = true;
+    // optimistic host mirrors (the device commits only a clean step; settle
+    // and zg_session_check re-read them)
+    for (size_t b = 0; b < rows; ++b) {
+        s->pos[b] += 1;
+        s->cur[b] ^= 1;
+    }
     return ZG_COMPLETED;
 }
 
@@ -910,7 +1209,15 @@ int zg_session_check(zg_session* s, void* stream) {
     if (!s) return ZG_E_MALFORMED;
     zg_ctx* ctx = s->m->ctx;
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    return read_status(s, stream ? (hipStream_t)stream : ctx->stream);
+    (void)hipSetDevice(ctx->device);
+    hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
+    if (s->async_steps) {
+        ZG_HIP(hipEventSynchronize(s->dev_ev));
+        s->async_steps = false;
+    }
+    int rc = read_status(s, st);
+    if (rc) return rc;
+    return pull_positions(s, st);
 }
 
 size_t zg_state_floats(const zg_session* s, size_t row) {
@@ -924,13 +1231,14 @@ int zg_state_export(zg_session* s, size_t row, float* out, size_t n) {
     zg_ctx* ctx = s->m->ctx;
     std::lock_guard<std::recursive_mutex> lock(ctx->mu);
     (void)hipSetDevice(ctx->device);
+    int rc = settle(s);
+    if (rc) return rc;
     if (row >= s->max_batch || n != zg_state_floats(s, row)) return fail(ctx, ZG_E_MALFORMED, "state length mismatch");
     const zg_geometry& g = s->m->g;
     hipStream_t st = ctx->stream;
-    ZG_HIP(hipDeviceSynchronize());
     const int P = s->pos[row];
     const size_t T = (size_t)P, kw = kvw(g), C = (size_t)g.gdn_heads * g.gdn_dim * 3;
-    int rc = ensure(ctx, ctx->scratch, std::max<size_t>(T * kw * 4, 256));
+    rc = ensure(ctx, ctx->scratch, std::max<size_t>(T * kw * 4, 256));
     if (rc) return rc;
     std::vector<float> ring(ring_floats(g));
     size_t at = 0;
@@ -942,7 +1250,8 @@ int zg_state_export(zg_session* s, size_t row, float* out, size_t n) {
             for (size_t c = 0; c < C; ++c)
                 for (int k = 0; k < 3; ++k) out[at + c * 3 + k] = ring[c * 4 + ring_slot(P, k)];
             at += conv_floats(g);
-            ZG_HIP(hipMemcpy(out + at, s->rec[slot] + row * rec_floats(g), rec_floats(g) * 4, hipMemcpyDeviceToHost));
+            ZG_HIP(hipMemcpy(out + at, rec_half(s, (size_t)slot, row, s->cur[row]), rec_floats(g) * 4,
+                             hipMemcpyDeviceToHost));
             at += rec_floats(g);
         } else {
             for (void* cache : {s->kc[slot], s->vc[slot]}) {
@@ -971,6 +1280,8 @@ int zg_state_import(zg_session* s, size_t row, const float* in, size_t n, int po
     (void)hipSetDevice(ctx->device);
     if (row >= s->max_batch || position < 0 || (size_t)position > s->max_ctx)
         return fail(ctx, ZG_E_MALFORMED, "invalid state import row or position");
+    int rc = settle(s);
+    if (rc) return rc;
     const int saved = s->pos[row];
     s->pos[row] = position;
     if (n != zg_state_floats(s, row) || !all_finite(in, n)) {
@@ -979,9 +1290,8 @@ int zg_state_import(zg_session* s, size_t row, const float* in, size_t n, int po
     }
     const zg_geometry& g = s->m->g;
     hipStream_t st = ctx->stream;
-    ZG_HIP(hipDeviceSynchronize());
     const size_t T = (size_t)position, kw = kvw(g), C = (size_t)g.gdn_heads * g.gdn_dim * 3;
-    int rc = ensure(ctx, ctx->scratch, std::max<size_t>(T * kw * 4, 256));
+    rc = ensure(ctx, ctx->scratch, std::max<size_t>(T * kw * 4, 256));
     if (rc) return rc;
     std::vector<float> ring(ring_floats(g));
     size_t at = 0;
@@ -993,7 +1303,7 @@ int zg_state_import(zg_session* s, size_t row, const float* in, size_t n, int po
                 for (int k = 0; k < 3; ++k) ring[c * 4 + ring_slot(position, k)] = in[at + c * 3 + k];
             ZG_HIP(hipMemcpy(s->ring[slot] + row * ring_floats(g), ring.data(), ring_floats(g) * 4, hipMemcpyHostToDevice));
             at += conv_floats(g);
-            ZG_HIP(hipMemcpy(s->rec[slot] + row * rec_floats(g), in + at, rec_floats(g) * 4, hipMemcpyHostToDevice));
+            ZG_HIP(hipMemcpy(rec_half(s, (size_t)slot, row, 0), in + at, rec_floats(g) * 4, hipMemcpyHostToDevice));
             at += rec_floats(g);
         } else {
             for (void* cache : {s->kc[slot], s->vc[slot]}) {
@@ -1012,8 +1322,10 @@ int zg_state_import(zg_session* s, size_t row, const float* in, size_t n, int po
         }
     }
     ZG_HIP(hipStreamSynchronize(st));
+    s->cur[row] = 0;
     s->pos_dirty = true;
     s->poisoned = false;
+    s->pending_rows = 0;
     return ZG_COMPLETED;
 }
 
@@ -1026,12 +1338,13 @@ int zg_session_fill_random(zg_session* s, size_t rows, size_t prefix, uint64_t s
         return fail(ctx, ZG_E_LIMIT, "random prefix exceeds the session");
     const zg_geometry& g = s->m->g;
     hipStream_t st = ctx->stream;
-    ZG_HIP(hipDeviceSynchronize());
+    int rc = settle(s);
+    if (rc) return rc;
     uint64_t k = seed * 0x9e3779b97f4a7c15ull;
     const size_t kw = kvw(g);
     for (size_t i = 0; i < s->ring.size(); ++i) {
         ZG_HIP(zg::fill_normal(s->ring[i], rows * ring_floats(g), false, ++k, 0.5f, st));
-        ZG_HIP(zg::fill_normal(s->rec[i], rows * rec_floats(g), false, ++k, 0.02f, st));
+        for (size_t b = 0; b < rows; ++b) ZG_HIP(zg::fill_normal(rec_half(s, i, b, 0), rec_floats(g), false, ++k, 0.02f, st));
     }
     for (size_t i = 0; i < s->kc.size(); ++i) {
         for (size_t b = 0; b < rows; ++b) {
@@ -1041,10 +1354,68 @@ int zg_session_fill_random(zg_session* s, size_t rows, size_t prefix, uint64_t s
         }
     }
     ZG_HIP(hipStreamSynchronize(st));
-    for (size_t b = 0; b < rows; ++b) s->pos[b] = (int)prefix;
+    for (size_t b = 0; b < rows; ++b) {
+        s->pos[b] = (int)prefix;
+        s->cur[b] = 0;
+    }
     s->pos_dirty = true;
     s->poisoned = false;
+    s->pending_rows = 0;
     return ZG_COMPLETED;
+}
+
+int zg_session_snapshot(zg_session* s, size_t row, zg_snapshot** out) {
+    if (!s || !out) return ZG_E_MALFORMED;
+    zg_ctx* ctx = s->m->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    *out = nullptr;
+    if (row >= s->max_batch) return fail(ctx, ZG_E_LIMIT, "row outside the session batch");
+    int rc = settle(s);
+    if (rc) return rc;
+    auto snap = new zg_snapshot();
+    snap->model_serial = s->m->serial;
+    snap->device = ctx->device;
+    snap->kv_bf16 = s->kv_bf16;
+    if ((rc = save_row(s, row, true, &snap->img))) {
+        free_image(snap->img);
+        delete snap;
+        return rc;
+    }
+    *out = snap;
+    return ZG_COMPLETED;
+}
+
+int zg_session_restore(zg_session* s, size_t row, const zg_snapshot* snap) {
+    if (!s || !snap) return ZG_E_MALFORMED;
+    zg_ctx* ctx = s->m->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (row >= s->max_batch) return fail(ctx, ZG_E_LIMIT, "row outside the session batch");
+    if (snap->model_serial != s->m->serial || snap->kv_bf16 != s->kv_bf16 || snap->device != ctx->device)
+        return fail(ctx, ZG_E_STATE, "foreign snapshot: another model, device or KV cache type");
+    if ((size_t)snap->img.pos > s->max_ctx) return fail(ctx, ZG_E_LIMIT, "snapshot exceeds the session context");
+    int rc = settle(s);
+    if (rc) return rc;
+    if ((rc = load_row(s, row, snap->img))) {
+        s->poisoned = true;
+        return rc;
+    }
+    s->poisoned = false;
+    return ZG_COMPLETED;
+}
+
+size_t zg_snapshot_bytes(const zg_snapshot* snap) { return snap ? snap->img.bytes : 0; }
+int zg_snapshot_position(const zg_snapshot* snap) { return snap ? snap->img.pos : -1; }
+
+void zg_snapshot_destroy(zg_snapshot* snap) {
+    if (!snap) return;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    (void)hipSetDevice(snap->device);
+    free_image(snap->img);
+    (void)hipSetDevice(dev);
+    delete snap;
 }
 
 }  // extern "C"

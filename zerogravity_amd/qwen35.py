@@ -178,12 +178,14 @@ def read_gguf(path, config_path=None):
 class QwenModelHip:
     """LoadedQwenModel on the device: weights resident once, sessions share them."""
 
-    def __init__(self, geometry: dict, tensors: dict, kernel=None, device=0):
+    def __init__(self, geometry: dict, tensors: dict, kernel=None, device=0, source_id=None):
         from .regions import HipMatVecKernel
         self.kernel = kernel or HipMatVecKernel(device)
         self.ctx = self.kernel.ctx
         self.g = dict(geometry)
-        self.source_id = next(_SOURCE_IDS)
+        # SourceIdentity of the tensor source (core/src/accelerator.rs:22-59):
+        # models loaded from the same source share its resident weights
+        self.source_id = next(_SOURCE_IDS) if source_id is None else int(source_id)
         descs = (TensorDesc * len(tensors))()
         keep = []
         for i, (name, (ty, s0, s1, data)) in enumerate(tensors.items()):
@@ -204,6 +206,26 @@ class QwenModelHip:
     def close(self):
         if getattr(self, "h", None) and getattr(self.ctx, "h", None):
             L.lib().zg_model_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+class Snapshot:
+    """A zg_snapshot: device memory holding one row's state and position."""
+
+    def __init__(self, session, row):
+        h = C.c_void_p()
+        session.model.ctx.check(L.lib().zg_session_snapshot(session.h, row, C.byref(h)))
+        self.h = h
+        self.position = L.lib().zg_snapshot_position(h)
+        self.nbytes = L.lib().zg_snapshot_bytes(h)
+        session.model.ctx.adopt(self)
+
+    def close(self):
+        if getattr(self, "h", None):
+            L.lib().zg_snapshot_destroy(self.h)
         self.h = None
 
     def __del__(self):
@@ -242,6 +264,29 @@ class QwenDenseHip:
     def forward(self, token):
         """QwenDenseCpu::forward (lib.rs:1227-1232): logits of one token on row 0."""
         return self.step([token])[0][0]
+
+    def next_logits(self, tokens, greedy=False):
+        """QwenDenseCpu::next_logits (lib.rs:1057-1070): logits of one token per
+        row [0, len(tokens)) on a draft; publish with commit()."""
+        toks = np.ascontiguousarray(np.atleast_1d(tokens), np.uint32)
+        n = toks.size
+        lg = np.empty((n, self.vocab), np.float32)
+        gr = np.empty(n, np.uint32) if greedy else None
+        self.model.ctx.check(L.lib().zg_session_propose(self.h, n, toks.ctypes.data, lg.ctypes.data,
+                                                        None if gr is None else gr.ctypes.data))
+        return (lg, gr) if greedy else lg
+
+    def commit(self):
+        """QwenDenseCpu::commit (lib.rs:1211-1225): publish the pending proposal."""
+        self.model.ctx.check(L.lib().zg_session_commit(self.h))
+
+    def snapshot(self, row=0):
+        """Device-side copy of one row's published state (ResidentSession::snapshot)."""
+        return Snapshot(self, row)
+
+    def restore(self, snap, row=0):
+        """Install a snapshot of this model into `row` (ResidentSession::restore)."""
+        self.model.ctx.check(L.lib().zg_session_restore(self.h, row, snap.h))
 
     def prefill_transaction(self, tokens):
         """Per-token prefill on row 0, logits of the last token (lib.rs:1119-1187)."""
