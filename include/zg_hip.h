@@ -399,6 +399,20 @@ int zg_session_fill_random(zg_session* s, size_t rows, size_t prefix, uint64_t s
 int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows,
                    const float* gamma, float eps, float* y, void* stream);
 
+/* zg_gemv_device without any allocation: no counterpart in the reference;
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and bit-identical results, with the activation scratch
+ * in a static per-device array of 4 MiB (held until the process ends)
+ * instead of a context buffer.  Limits: m_rows 1..64 and the prepared
+ * activation within 4 MiB (ZG_E_LIMIT otherwise); Q4_K with f32 input and
+ * more than 4 rows needs the weight's batched tile layout, which one
+ * zg_gemv_device call with more than 4 rows builds (ZG_E_STATE otherwise).
+ * Every call on a device shares that device's array: calls that overlap on
+ * one GPU (two streams, two threads with different contexts) race. */
+int zg_gemv_device_noalloc(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows,
+                           const float* gamma, float eps, float* y, void* stream);
+
 /* The two halves of zg_gemv_device, for callers that prepare one activation
  * and reuse it (and for timing the GEMV kernel alone).  The prepared buffer
  * is device memory of zg_act_prepared_bytes(w, m_rows) bytes holding the

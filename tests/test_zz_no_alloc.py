@@ -1,0 +1,77 @@
+"""The allocation-free GEMV entry (zg_gemv_device_noalloc): the same
+results as zg_gemv_device, bit for bit, on two calls in a row (the second
+with a smaller input, so the static scratch holds the first call's larger
+contents), for every codec path: bf16 input through the prepared
+activation, f32 input through the in-kernel prologue (up to 4 rows) and
+through the f16 MFMA tiles (Q4_K beyond 4 rows).  No counterpart in the
+reference: the entry exists for callers that cannot allocate."""
+import numpy as np
+import pytest
+
+from zerogravity_amd import _lib as L
+from zerogravity_amd import regions as R
+from zerogravity_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def kern():
+    k = R.HipMatVecKernel(0)
+    yield k
+    k.ctx.close()
+
+
+def _run(kern, fn, h, x, x_dtype, M, g, y):
+    import torch
+    kern.ctx.check(getattr(L.lib(), fn)(kern.ctx.h, h.h, x.data_ptr(), x_dtype, M, g.data_ptr(), 1e-6, y.data_ptr(),
+                                        None))
+    torch.cuda.synchronize()
+    return y.cpu().numpy().copy()
+
+
+@pytest.mark.parametrize("kind,N,K", [(synth.Q8_0, 3584, 1024), (synth.Q4_K, 2048, 6144), (synth.Q4_K, 6144, 2048),
+                                      (synth.Q6_K, 1024, 2048), (synth.Q4_1, 640, 1024), (synth.F32, 300, 2048)])
+@pytest.mark.parametrize("x_dtype", [L.F32, L.BF16])
+def test_noalloc_matches_gemv_device(kern, kind, N, K, x_dtype):
+    import torch
+    rng = np.random.default_rng(N + K + x_dtype)
+    w = synth.random_matrix(rng, kind, N, K)
+    h = kern.register(900 + kind, f"noalloc.{kind}.{N}.{K}", kind, K, N, w.reshape(-1))
+    g = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)).cuda()
+    # first call with 32 rows, second with 3 (in-kernel prologue for f32) or 9
+    for M in (32, 9, 3) if x_dtype == L.F32 else (32, 9):
+        xf = rng.standard_normal((M, K)).astype(np.float32)
+        if x_dtype == L.BF16:
+            _, xb = synth.bf16_round(xf)
+            x = torch.from_numpy(xb.view(np.int16)).cuda()
+        else:
+            x = torch.from_numpy(xf).cuda()
+        y0 = torch.full((M, N), np.nan, dtype=torch.float32, device="cuda")
+        y1 = torch.full((M, N), np.nan, dtype=torch.float32, device="cuda")
+        rc = L.lib().zg_gemv_device(kern.ctx.h, h.h, x.data_ptr(), x_dtype, M, g.data_ptr(), 1e-6, y0.data_ptr(), None)
+        if rc == L.UNSUPPORTED:
+            pytest.skip("geometry not offered by the GEMV")
+        kern.ctx.check(rc)
+        torch.cuda.synchronize()  # the call ran on the context's stream
+        want = y0.cpu().numpy()
+        got = _run(kern, "zg_gemv_device_noalloc", h, x, x_dtype, M, g, y1)
+        assert np.isfinite(want).all()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (M, x_dtype)
+
+
+def test_noalloc_limits(kern):
+    import torch
+    rng = np.random.default_rng(5)
+    K, N = 2048, 256
+    w = synth.random_matrix(rng, synth.Q4_K, N, K)
+    h = kern.register(950, "noalloc.limits", synth.Q4_K, K, N, w.reshape(-1))
+    x = torch.zeros((65, K), dtype=torch.float32, device="cuda")
+    y = torch.empty((65, N), dtype=torch.float32, device="cuda")
+    g = torch.ones(K, dtype=torch.float32, device="cuda")
+    rc = L.lib().zg_gemv_device_noalloc(kern.ctx.h, h.h, x.data_ptr(), L.F32, 65, g.data_ptr(), 1e-6, y.data_ptr(), None)
+    assert rc == L.E_LIMIT
+    # Q4_K beyond 4 rows before any zg_gemv_device call built the weight's tiles
+    rc = L.lib().zg_gemv_device_noalloc(kern.ctx.h, h.h, x.data_ptr(), L.F32, 8, g.data_ptr(), 1e-6, y.data_ptr(), None)
+    assert rc == L.E_STATE
+    assert "tile layout" in kern.ctx.error()

@@ -71,6 +71,7 @@ _SIGS = {
     "zg_act_prepare_device": (C.c_int, [P, P, P, C.c_int, SZ, P, C.c_float, P, SZ, P]),
     "zg_gemv_prepared_device": (C.c_int, [P, P, SZ, P, P, P]),
     "zg_greedy": (C.c_int, [P, P, SZ, SZ, P]),
+    "zg_gemv_device_noalloc": (C.c_int, [P, P, P, C.c_int, SZ, P, C.c_float, P, P]),
     "zg_gdn_decode_tiles_bytes": (SZ, [SZ, SZ]),
     "zg_gdn_decode_gated_device": (C.c_int, [P, SZ, SZ, P, SZ, P, P, P, P, P, P, C.c_float, P, P, P, P]),
     "zg_session_propose": (C.c_int, [P, SZ, P, P, P]),

@@ -12,6 +12,14 @@
 
 #include "zg_context.hpp"
 
+// Activation scratch of zg_gemv_device_noalloc: one array per GPU, held for
+// the life of the process.  Host code never passes `scratch` itself to a
+// kernel (the name is a host-side stand-in); zg_ctx_create looks up each
+// device's address with hipGetSymbolAddress and keeps it in the context.
+constexpr size_t kStaticScratchBytes = (size_t)4 << 20;
+constexpr size_t kStaticScratchRows = 64;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
 namespace zgc {
 
 // Failure text per (thread, ctx): under the reference's Send + Sync
@@ -166,7 +174,10 @@ int zg_ctx_create(int device, zg_ctx** out) {
     auto ctx = new zg_ctx();
     ctx->device = device;
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
-        hipMalloc(&ctx->d_flag, sizeof(int)) != hipSuccess) {
+        hipMalloc(&ctx->d_flag, sizeof(int)) != hipSuccess ||
+        hipGetSymbolAddress(&ctx->static_scratch, HIP_SYMBOL(scratch)) != hipSuccess || !ctx->static_scratch) {
+        if (ctx->d_flag) (void)hipFree(ctx->d_flag);
+        if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return ZG_E_DEVICE;
     }
@@ -492,6 +503,52 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
     if (rc) return rc;
     ZG_HIP(zg::act_prepare_for(w->dw.type, x, x_dtype == ZG_BF16, m_rows, w->dw.K, gamma, eps, ctx->actbuf.ptr, s));
     ZG_HIP(zg::gemv(w->dw, m_rows, ctx->actbuf.ptr, y, s));
+    return ZG_COMPLETED;
+}
+
+// zg_gemv_device with its activation scratch in the process-wide static
+// array instead of a context buffer: no allocation on any path.  The same
+// kernels in the same order, so the result is bit-identical.
+int zg_gemv_device_noalloc(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows,
+                           const float* gamma, float eps, float* y, void* stream) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!w || !x || !y || (x_dtype != ZG_BF16 && x_dtype != ZG_F32)) return fail(ctx, ZG_E_MALFORMED, "invalid gemv arguments");
+    if (m_rows == 0 || m_rows > kStaticScratchRows)
+        return fail(ctx, ZG_E_LIMIT, "allocation-free GEMV takes 1 to 64 activation rows");
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    void* sp = ctx->static_scratch;
+    const int pro = gamma ? zg::PRO_RMS : zg::PRO_PLAIN;
+    if (x_dtype == ZG_F32 && zg::fused_gemv_supported(w->dw.type, w->dw.K, w->dw.N, pro)) {
+        zg::FusedGemvArgs f;
+        f.M = (int)m_rows;
+        f.pro = pro;
+        f.epi = zg::EPI_STORE;
+        f.x = (const float*)x;
+        f.ldx = w->dw.K;
+        f.gamma = gamma;
+        f.eps = eps;
+        f.y = y;
+        f.ldy = w->dw.N;
+        f.status = ctx->d_flag;
+        if (m_rows > 4 && w->dw.type == zg::kQ4_K) {
+            if (!w->dw.qs_t)
+                return fail(ctx, ZG_E_STATE,
+                            "weight has no batched tile layout yet: a zg_gemv_device call with more than 4 rows builds it");
+            if (zg::batched_scratch_bytes(m_rows, w->dw.K) > kStaticScratchBytes)
+                return fail(ctx, ZG_E_LIMIT, "activation exceeds the 4 MiB static scratch");
+            ZG_HIP(zg::batched_gemv(w->dw, f, sp, s));
+        } else {
+            ZG_HIP(zg::fused_gemv(w->dw, f, s));
+        }
+        return ZG_COMPLETED;
+    }
+    if (!zg::gemv_supported(w->dw.type, w->dw.K, m_rows)) return fail(ctx, ZG_UNSUPPORTED, "geometry not offered");
+    if (zg::prepared_bytes(w->dw.type, m_rows, w->dw.K) > kStaticScratchBytes)
+        return fail(ctx, ZG_E_LIMIT, "activation exceeds the 4 MiB static scratch");
+    ZG_HIP(zg::act_prepare_for(w->dw.type, x, x_dtype == ZG_BF16, m_rows, w->dw.K, gamma, eps, sp, s));
+    ZG_HIP(zg::gemv(w->dw, m_rows, sp, y, s));
     return ZG_COMPLETED;
 }
 

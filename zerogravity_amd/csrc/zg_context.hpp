@@ -35,6 +35,9 @@ struct zg_ctx {
     DeviceBuffer actbuf;     // zg_gemv_device: prepared activations
     DeviceBuffer chunkbuf;   // zg_gdn_chunk_prefill_device: per-(chunk, head) records
     int* d_flag = nullptr;
+    // device address of this device's copy of the static scratch array used
+    // by zg_gemv_device_noalloc (set up at context creation)
+    void* static_scratch = nullptr;
 };
 
 namespace zgc {
