@@ -74,8 +74,7 @@ void free_weight(zg_weight* w) {
     if (w->dw.hdr) (void)hipFree(w->dw.hdr);
     if (w->dw.qs_t) (void)hipFree(w->dw.qs_t);
     if (w->dw.hdr_t) (void)hipFree(w->dw.hdr_t);
-    if (w->dw.w16) (void)hipFree(w->dw.w16);
-    w->dw.qs = w->dw.hdr = w->dw.qs_t = w->dw.hdr_t = w->dw.w16 = nullptr;
+    w->dw.qs = w->dw.hdr = w->dw.qs_t = w->dw.hdr_t = nullptr;
 }
 
 bool supported_type(int t) { return t == ZG_Q8_0 || t == ZG_Q4_K || t == ZG_F32 || t == ZG_Q4_1 || t == ZG_Q6_K; }

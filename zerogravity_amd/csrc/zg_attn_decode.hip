@@ -526,6 +526,7 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
             const int k = (h0 + g) * D + cgx * CB + c, m = b, K = a.nq * D;
             const size_t lane_t = (size_t)((k & 15) >> 3) * 32 + (m & 31);
             const size_t at = ((((size_t)(m >> 5) * (K >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + lane_t) * 8 + (k & 7);
+            if (a.status && !(fabsf(v) <= 65504.0f)) atomicOr(a.status, 16);
             ((_Float16*)a.xh)[at] = (_Float16)v;
         }
     }

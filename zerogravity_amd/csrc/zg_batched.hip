@@ -95,7 +95,11 @@ __global__ __launch_bounds__(256) void act16_kernel(FusedGemvArgs a, _Float16* _
             typedef _Float16 h4v __attribute__((ext_vector_type(4)));
             h4v hv4;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) hv4[t] = valid ? (_Float16)e[t] : (_Float16)0.0f;
+            for (int t = 0; t < 4; ++t) {
+                hv4[t] = valid ? (_Float16)e[t] : (_Float16)0.0f;
+                // past the f16 range: status bit 4 (the f32 paths carry it)
+                if (a.status && valid && !(fabsf(e[t]) <= 65504.0f)) atomicOr(a.status, 16);
+            }
             const size_t lane_t = (size_t)((k & 15) >> 3) * 32 + (m & 31);
             const size_t at = a.xh_rows ? (size_t)m * K + k
                                         : ((((size_t)(m >> 5) * (K >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 +
@@ -231,7 +235,9 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
                     const int j = nbase[0] + r32, nbk2 = (N >> 1) >> 8;
                     const size_t at = ((((size_t)(m >> 5) * nbk2 + (j >> 8)) * 16 + ((j & 255) >> 4)) * 64 +
                                        ((j & 15) >> 3) * 32 + (m & 31)) * 8 + (j & 7);
-                    ((_Float16*)a.xh_out)[at] = (_Float16)(m < a.M ? v * ggml_silu(vg[i]) : 0.0f);
+                    const float pr = m < a.M ? v * ggml_silu(vg[i]) : 0.0f;
+                    if (a.status && !(fabsf(pr) <= 65504.0f)) atomicOr(a.status, 16);
+                    ((_Float16*)a.xh_out)[at] = (_Float16)pr;
                 }
             } else if (gridDim.z > 1) {
                 if (nv[t]) a.parts[((size_t)blockIdx.z * 32 * gridDim.y + m) * N + nbase[t] + r32] = v;
@@ -240,151 +246,6 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
             }
         }
         __syncthreads();
-    }
-}
-
-// The same product for prompt-sized M (>= 1024 rows).  A workgroup of 4
-// waves covers MB activation blocks of 32 rows and 4*NT weight tiles (NT per
-// wave, K not split): each 256-element K block of the MB activation tiles
-// is staged once in LDS for the four waves (the next block's loads in
-// flight meanwhile), and every dequantized weight step feeds MB MFMAs.
-// Weights, headers, activations, the dequantization and the epilogues
-// (store, residual add, SwiGLU with NT = 2: gate tile x, up tile x + N/64)
-// are those of mfma_q4k_kernel.
-template <int EPI, int NT, int MB>
-__global__ __launch_bounds__(256) void mfma_q4k_wide_kernel(FusedGemvArgs a, const _Float16* __restrict__ xh) {
-    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
-    __shared__ h8v xs[MB * 1024];  // MB activation tiles of one K block (16 KB each)
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hsel = lane >> 5, r32 = lane & 31;
-    const int K = a.K, N = a.N, nbk = K >> 8;
-    const int mblk0 = blockIdx.y * MB;
-    bool nv[NT];
-    int nbase[NT];
-    const v4u* qtile[NT];
-    const v4u* htile[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const int tile = EPI == EPI_GLU ? blockIdx.x * 4 + wv + t * (N >> 6) : (blockIdx.x * 4 + wv) * NT + t;
-        nbase[t] = tile * 32;
-        nv[t] = nbase[t] + r32 < N;
-        const int tt = min(tile, (N - 1) >> 5);
-        qtile[t] = (const v4u*)a.qs + (size_t)tt * nbk * 256 + lane;
-        htile[t] = (const v4u*)a.hdr + (size_t)tt * nbk * 32 + r32;
-    }
-    const h8v* xg = (const h8v*)xh;
-    h8v stage[MB][4];
-    auto load_stage = [&](int kb) {
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) stage[mb][i] = xg[((size_t)(mblk0 + mb) * nbk + kb) * 1024 + tid + 256 * i];
-    };
-    auto store_stage = [&]() {
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) xs[mb * 1024 + tid + 256 * i] = stage[mb][i];
-    };
-    uint2 pc[NT][4][2];
-    v4u hd[NT];
-    auto load_w = [&](int kb) {
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-#pragma unroll
-            for (int c4 = 0; c4 < 4; ++c4) {
-                const v4u q = qtile[t][((size_t)kb * 4 + c4) * 64];
-                pc[t][c4][0] = make_uint2(q.x, q.y);
-                pc[t][c4][1] = make_uint2(q.z, q.w);
-            }
-            hd[t] = htile[t][(size_t)kb * 32];
-        }
-    };
-    f16v acc[NT][MB];
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[t][mb] = f16v{};
-    load_stage(0);
-    load_w(0);
-    store_stage();
-    __syncthreads();
-    for (int kb = 0; kb < nbk; ++kb) {
-        uint2 pcc[NT][4][2];
-        v4u hdc[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            hdc[t] = hd[t];
-#pragma unroll
-            for (int c4 = 0; c4 < 4; ++c4) {
-                pcc[t][c4][0] = pc[t][c4][0];
-                pcc[t][c4][1] = pc[t][c4][1];
-            }
-        }
-        if (kb + 1 < nbk) {
-            load_stage(kb + 1);
-            load_w(kb + 1);
-        }
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const float d = f16_to_f32((uint16_t)(hdc[t].x & 0xffffu));
-            const float dmin = f16_to_f32((uint16_t)(hdc[t].x >> 16));
-            h2v sc2[8], nm2[8];
-#pragma unroll
-            for (int g = 0; g < 8; ++g) {
-                uint32_t sc, mn;
-                q4k_dev_scale_min(hdc[t], g, sc, mn);
-                const _Float16 sh = (_Float16)(d * (float)sc), mh = (_Float16)(dmin * (float)mn);
-                sc2[g] = h2v{sh, sh};
-                nm2[g] = h2v{-mh, -mh};
-            }
-            const h2v bias = h2v{(_Float16)1024.0f, (_Float16)1024.0f};
-#pragma unroll
-            for (int st = 0; st < 16; ++st) {
-                const int g = st >> 1, nib = (st >> 1) & 1;
-                const uint2 pw = pcc[t][st >> 2][st & 1];
-                const uint32_t w0 = (nib ? (pw.x >> 4) : pw.x) & 0x0f0f0f0fu;
-                const uint32_t w1 = (nib ? (pw.y >> 4) : pw.y) & 0x0f0f0f0fu;
-                const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u);
-                const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u);
-                const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u);
-                const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u);
-                const h2v e0 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p0) - bias, sc2[g], nm2[g]);
-                const h2v e1 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p1) - bias, sc2[g], nm2[g]);
-                const h2v e2 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p2) - bias, sc2[g], nm2[g]);
-                const h2v e3 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p3) - bias, sc2[g], nm2[g]);
-                h8v wb = h8v{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
-                if (!nv[t]) wb = h8v{};
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb)
-                    acc[t][mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xs[mb * 1024 + st * 64 + lane], wb, acc[t][mb],
-                                                                         0, 0, 0);
-            }
-        }
-        __syncthreads();  // every wave is done with this K block's tiles
-        if (kb + 1 < nbk) {
-            store_stage();
-            __syncthreads();
-        }
-    }
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-        const int mrow0 = (mblk0 + mb) * 32;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int m = mrow0 + (r & 3) + 8 * (r >> 2) + 4 * hsel;
-            if (EPI == EPI_GLU) {
-                if (nv[1]) {
-                    const int j = nbase[0] + r32, nbk2 = (N >> 1) >> 8;
-                    const size_t at = ((((size_t)(m >> 5) * nbk2 + (j >> 8)) * 16 + ((j & 255) >> 4)) * 64 +
-                                       ((j & 15) >> 3) * 32 + (m & 31)) * 8 + (j & 7);
-                    ((_Float16*)a.xh_out)[at] = (_Float16)(m < a.M ? acc[1][mb][r] * ggml_silu(acc[0][mb][r]) : 0.0f);
-                }
-            } else {
-#pragma unroll
-                for (int t = 0; t < NT; ++t)
-                    if (nv[t] && m < a.M) epilogue(a, m, nbase[t] + r32, acc[t][mb][r], EPI);
-            }
-        }
     }
 }
 
@@ -454,63 +315,9 @@ static void launch_act16(const FusedGemvArgs& a, int mpad, _Float16* xh, hipStre
     else hipLaunchKernelGGL((act16_kernel<PRO, 8>), dim3(mpad), dim3(256), 0, s, a, xh);
 }
 
-// up * silu(gate) of the library gate/up GEMM's f16 rows [M][2F] (gate
-// columns first), rounded to f16 row-major [M][F]: the down GEMM's operand
-// (the EPI_GLU epilogue's arithmetic on f16-rounded gate and up)
-__global__ void glu16_kernel(const _Float16* __restrict__ gu, size_t M, size_t F, _Float16* __restrict__ out) {
-    typedef _Float16 h8v_t __attribute__((ext_vector_type(8)));
-    const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
-    if (i >= M * F) return;
-    const size_t m = i / F, j = i % F;
-    const h8v_t g = *(const h8v_t*)(gu + m * 2 * F + j);
-    const h8v_t u = *(const h8v_t*)(gu + m * 2 * F + F + j);
-    h8v_t o;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) o[t] = (_Float16)((float)u[t] * ggml_silu((float)g[t]));
-    *(h8v_t*)(out + i) = o;
-}
-
-// Prompt-sized M with the f16 weight present: hipBLASLt on row-major f16
-// activations (the activation kernel's values in row order, or the previous
-// gate/up GEMM's product), f32 accumulation; EPI_RESID adds into y (beta 1).
-static hipError_t blas_batched(const DeviceWeight& w, FusedGemvArgs a, void* scratch, hipStream_t s) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    const int mpad = (a.M + 31) / 32 * 32;
-    const _Float16* xh = (const _Float16*)a.xh_in;
-    if (!xh) {
-        a.xh_rows = 1;
-        switch (a.pro) {
-        case PRO_RMS: launch_act16<PRO_RMS>(a, mpad, (_Float16*)scratch, s); break;
-        case PRO_GATED: launch_act16<PRO_GATED>(a, mpad, (_Float16*)scratch, s); break;
-        case PRO_SILU_MUL: launch_act16<PRO_SILU_MUL>(a, mpad, (_Float16*)scratch, s); break;
-        case PRO_PLAIN: launch_act16<PRO_PLAIN>(a, mpad, (_Float16*)scratch, s); break;
-        default: return hipErrorInvalidValue;
-        }
-        xh = (const _Float16*)scratch;
-    }
-    if (a.epi == EPI_GLU) {
-        if (!a.xh_out || a.N % 16) return hipErrorInvalidValue;
-        e = blas_gemm_f16(dev, a.M, a.N, a.K, xh, w.w16, a.y, false, (size_t)a.N, 0.0f, s);
-        if (e != hipSuccess) return e;
-        const size_t F = (size_t)a.N / 2, n8 = (size_t)a.M * F / 8;
-        hipLaunchKernelGGL(glu16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const _Float16*)a.y,
-                           (size_t)a.M, F, (_Float16*)a.xh_out);
-        return hipGetLastError();
-    }
-    return blas_gemm_f16(dev, a.M, a.N, a.K, xh, w.w16, a.y, true, a.ldy, a.epi == EPI_RESID ? 1.0f : 0.0f, s);
-}
-
 hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* scratch, hipStream_t s) {
     if (w.type != kQ4_K || w.K % 256 || w.K > 8192 || args.M <= 0 || args.M > 65535 * 32) return hipErrorInvalidValue;
     if (args.pro == PRO_GATED && args.group != 128) return hipErrorInvalidValue;
-    if (w.w16 && args.M >= kBlasRows && !(args.epi == EPI_RESID && args.splits > 1 && args.parts)) {
-        FusedGemvArgs a = args;
-        a.K = (int)w.K;
-        a.N = (int)w.N;
-        return blas_batched(w, a, scratch, s);
-    }
     if (!w.qs_t || !w.hdr_t) return hipErrorNotReady;  // ensure_mfma_tiles first
     FusedGemvArgs a = args;
     a.qs = w.qs_t;
@@ -530,39 +337,10 @@ hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* 
         default: return hipErrorInvalidValue;
         }
     }
-    // prompt-sized M (>= 1024 rows; below, the K-split kernel keeps more
-    // workgroups busy): the LDS-staged variant, MB activation blocks per
-    // workgroup (MB divides the block count)
-    const int mblocks = mpad / 32;
+    // prompt-sized M: the register-blocked GEMM (zg_gemm.hip)
     const bool no_split = !(a.epi == EPI_RESID && a.splits > 1 && a.parts);
-    if (a.M >= 1024 && no_split) {
-        const int mb = mblocks % 4 == 0 ? 4 : (mblocks % 2 == 0 ? 2 : 1);
-        const int tiles = (a.N + 31) / 32;
-        if (a.epi == EPI_GLU) {
-            if (!batched_glu_supported(w.type, w.K, w.N) || !a.xh_out) return hipErrorInvalidValue;
-            dim3 g((unsigned)((a.N / 64 + 3) / 4), (unsigned)(mblocks / mb), 1u);
-            if (mb == 4) hipLaunchKernelGGL((mfma_q4k_wide_kernel<EPI_GLU, 2, 4>), g, dim3(256), 0, s, a, (const _Float16*)xh);
-            else if (mb == 2) hipLaunchKernelGGL((mfma_q4k_wide_kernel<EPI_GLU, 2, 2>), g, dim3(256), 0, s, a, (const _Float16*)xh);
-            else hipLaunchKernelGGL((mfma_q4k_wide_kernel<EPI_GLU, 2, 1>), g, dim3(256), 0, s, a, (const _Float16*)xh);
-            return hipGetLastError();
-        }
-        // one weight tile per wave (two per wave, which halves the LDS
-        // traffic per MFMA, cost occupancy and measured 1-3% slower)
-        dim3 g((unsigned)((tiles + 3) / 4), (unsigned)(mblocks / mb), 1u);
-#define ZG_MW(E, MBV) hipLaunchKernelGGL((mfma_q4k_wide_kernel<E, 1, MBV>), g, dim3(256), 0, s, a, (const _Float16*)xh)
-#define ZG_MWE(E)                 \
-    if (mb == 4) ZG_MW(E, 4);      \
-    else if (mb == 2) ZG_MW(E, 2); \
-    else ZG_MW(E, 1);
-        if (a.epi == EPI_RESID) {
-            ZG_MWE(EPI_RESID)
-        } else {
-            ZG_MWE(EPI_STORE)
-        }
-#undef ZG_MWE
-#undef ZG_MW
-        return hipGetLastError();
-    }
+    if (a.M >= kGemmRows && no_split && prompt_gemm_supported(w.type, w.K, w.N, a.epi))
+        return prompt_gemm(w, args, xh, s);
     if (a.epi == EPI_GLU) {
         if (!batched_glu_supported(w.type, w.K, w.N) || !a.xh_out) return hipErrorInvalidValue;
         dim3 g((unsigned)(a.N / 64), (unsigned)(mpad / 32), 1u);

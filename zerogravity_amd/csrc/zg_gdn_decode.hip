@@ -194,7 +194,11 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
             typedef _Float16 h4v __attribute__((ext_vector_type(4)));
             h4v hv4;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) hv4[i] = (_Float16)(((e[i] * gi) * gg[i]) * ggml_silu(zz[i]));
+            for (int i = 0; i < 4; ++i) {
+                const float y = ((e[i] * gi) * gg[i]) * ggml_silu(zz[i]);
+                if (a.status && threadIdx.x < 32 && !(fabsf(y) <= 65504.0f)) atomicOr(a.status, 16);
+                hv4[i] = (_Float16)y;
+            }
             const int k = h * D + 4 * t, m = b;
             const size_t lane_t = (size_t)((k & 15) >> 3) * 32 + (m & 31);
             const size_t at = ((((size_t)(m >> 5) * (W >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + lane_t) * 8 + (k & 7);

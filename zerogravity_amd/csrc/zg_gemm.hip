@@ -1,0 +1,259 @@
+// Prompt-sized projections (M >= kGemmRows rows): Y[m][n] (+)= sum_k X[m][k] W[n][k]
+// with X the f16 activation tiles act16_kernel writes and W the Q4_K weight
+// in MFMA tile order (ensure_mfma_tiles), dequantized in registers.
+//
+// Register-blocked on v_mfma_f32_32x32x16_f16: a workgroup of 4 waves, WN
+// along N and 4/WN along M; each wave owns MT x NT output tiles of 32 x 32
+// (MT*NT*16 accumulators).  The K loop walks 64-wide steps: the
+// workgroup's AT = (4/WN)*MT activation tiles of a step (AT x 4 KB) are
+// staged in LDS (two buffers, the next step's loads in flight during the
+// MFMAs), each wave loads its NT weight tiles' nibbles (one 16-byte load
+// per lane per tile) and dequantizes them once per step, so every
+// dequantized B fragment feeds MT MFMAs and every A fragment read from LDS
+// feeds NT.  The dequantization and the operand layouts are those of
+// mfma_q4k_kernel (the decode path's batched GEMM); its f16 rounding of the
+// weights and f32 accumulation make the result agree with the CPU's f32
+// dot within the per-op tolerance.
+#include "zg_decode_common.hpp"
+
+namespace zg {
+
+namespace {
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr float kF16Max = 65504.0f;
+
+// Element (m, k) of the f16 A tiles for K columns: the act16_kernel layout.
+__device__ __forceinline__ size_t a_tile_index(int m, int k, int K) {
+    return ((((size_t)(m >> 5) * (K >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + ((k & 15) >> 3) * 32 +
+            (m & 31)) * 8 + (k & 7);
+}
+
+template <int EPI, int MT, int NT, int WN, int WM>
+__global__ __launch_bounds__(64 * WN * WM, 1) void gemm_q4k_kernel(FusedGemvArgs a, const _Float16* __restrict__ xh) {
+    constexpr int AT = WM * MT, NTHR = 64 * WN * WM, APT = AT * 256 / NTHR;  // A slabs per thread
+    static_assert(EPI != EPI_GLU || NT % 2 == 0, "SwiGLU pairs gate and up tiles");
+    static_assert(AT * 256 % NTHR == 0, "whole activation slabs per thread");
+    __shared__ h8v xs[2][AT * 256];  // AT tiles x 4 steps x 64 lanes of 16 bytes
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, hsel = lane >> 5, r32 = lane & 31;
+    const int wm = wv / WN, wn = wv - wm * WN;
+    const int K = a.K, N = a.N, nbk = K >> 8, nsub = K >> 6;
+    const int mtiles = (a.M + 31) >> 5;
+    const int mt0 = blockIdx.y * AT;
+
+    // this wave's weight tiles; with SwiGLU the first NT/2 are gate tiles and
+    // the rest the up tiles N/64 later (rows j and N/2 + j pair up)
+    constexpr int NW = EPI == EPI_GLU ? NT / 2 : NT;
+    const int wtile0 = (blockIdx.x * WN + wn) * NW;
+    int nbase[NT];
+    bool nv[NT];
+    uint32_t qoff[NT], hoff[NT];  // byte offsets of this lane's weight / header runs
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int tile = EPI == EPI_GLU ? (t < NW ? wtile0 + t : wtile0 + t - NW + (N >> 6)) : wtile0 + t;
+        nbase[t] = tile * 32;
+        nv[t] = EPI == EPI_GLU ? (wtile0 + (t % NW)) * 32 + r32 < (N >> 1) : nbase[t] + r32 < N;
+        const int tt = min(tile, (N - 1) >> 5);  // tiles past the end read the last one (results dropped)
+        qoff[t] = ((uint32_t)tt * nbk * 256 + lane) * 16;
+        hoff[t] = ((uint32_t)tt * nbk * 32 + r32) * 16;
+    }
+    // buffer resources (32-bit offsets: every operand is < 4 GB)
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)a.qs, 0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)a.hdr, 0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)xh, 0, 0x7fffffff, 0x00020000);
+    // slab e (of AT*256) of a step: tile e/256, h8v e%256 of its 4-step run
+    uint32_t aoff[APT];
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+        const int e = tid + i * NTHR;
+        const int mt = min(mt0 + e / 256, mtiles - 1);  // tiles past the end read the last one (results dropped)
+        aoff[i] = ((uint32_t)mt * nbk * 16 * 64 + (e & 255)) * 16;
+    }
+
+    h8v ast[APT];
+    v4u wq[NT], wqn[NT], hc[NT], hn[NT];
+    auto load = [&](int sb) {
+        const uint32_t astep = (uint32_t)((sb >> 2) * 16 + 4 * (sb & 3)) * 64 * 16;
+#pragma unroll
+        for (int i = 0; i < APT; ++i)
+            ast[i] = __builtin_bit_cast(h8v, __builtin_amdgcn_raw_buffer_load_b128(rx, aoff[i] + astep, 0, 0));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) wqn[t] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[t] + (uint32_t)sb * 64 * 16, 0, 0);
+        if ((sb & 3) == 0) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                hn[t] = __builtin_amdgcn_raw_buffer_load_b128(rh, hoff[t] + (uint32_t)(sb >> 2) * 32 * 16, 0, 0);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < APT; ++i) xs[buf][tid + i * NTHR] = ast[i];
+    };
+
+    f16v acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[i][t] = f16v{};
+
+    load(0);
+    store(0);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        wq[t] = wqn[t];
+        hc[t] = hn[t];
+    }
+    __syncthreads();
+    const h2v bias = h2v{(_Float16)1024.0f, (_Float16)1024.0f};
+    for (int sb = 0; sb < nsub; ++sb) {
+        const int cur = sb & 1;
+        if (sb + 1 < nsub) load(sb + 1);
+        // the two 32-groups of this step: scale and min rounded once to f16
+        const int c4 = sb & 3;
+        h2v sc[NT][2], nm[NT][2];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const float d = f16_to_f32((uint16_t)(hc[t].x & 0xffffu));
+            const float dmin = f16_to_f32((uint16_t)(hc[t].x >> 16));
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t s, mn;
+                q4k_dev_scale_min(hc[t], 2 * c4 + h, s, mn);
+                const _Float16 sh = (_Float16)(d * (float)s), mh = (_Float16)(dmin * (float)mn);
+                sc[t][h] = h2v{sh, sh};
+                nm[t][h] = h2v{-mh, -mh};
+            }
+        }
+        // each weight dword's low and high nibbles, masked once per step:
+        // step j takes dwords (2 (j%2), 2 (j%2) + 1), low nibbles for j < 2
+        uint32_t nib[NT][2][4];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint32_t wd[4] = {wq[t].x, wq[t].y, wq[t].z, wq[t].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                nib[t][0][q] = wd[q] & 0x0f0f0f0fu;
+                nib[t][1][q] = (wd[q] >> 4) & 0x0f0f0f0fu;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h8v af[MT];
+#pragma unroll
+            for (int i = 0; i < MT; ++i) af[i] = xs[cur][(wm * MT + i) * 256 + j * 64 + lane];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                // step j: nibble half j/2 of the 8-byte piece j%2 (group 2*c4 + j/2)
+                const uint32_t w0 = nib[t][j >> 1][2 * (j & 1)], w1 = nib[t][j >> 1][2 * (j & 1) + 1];
+                // bytes (q, 0x64) pairs: the f16 bit patterns of 1024 + q
+                const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u);
+                const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u);
+                const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u);
+                const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u);
+                const h2v s2 = sc[t][j >> 1], n2 = nm[t][j >> 1];
+                const h2v e0 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p0) - bias, s2, n2);
+                const h2v e1 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p1) - bias, s2, n2);
+                const h2v e2 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p2) - bias, s2, n2);
+                const h2v e3 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p3) - bias, s2, n2);
+                // (a tile past N computes on a clamped copy; its columns are never stored)
+                const h8v wb = h8v{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
+#pragma unroll
+                for (int i = 0; i < MT; ++i) acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], wb, acc[i][t], 0, 0, 0);
+            }
+        }
+        if (sb + 1 < nsub) {
+            store(cur ^ 1);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) wq[t] = wqn[t];
+            if (((sb + 1) & 3) == 0) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) hc[t] = hn[t];
+            }
+        }
+        __syncthreads();
+    }
+
+    // D register r of tile (i, t) is row (r%4) + 8*(r/4) + 4*(lane/32) of the
+    // activation tile, column lane%32 of the weight tile
+    bool over = false;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        const int tile_m = mt0 + wm * MT + i;
+        if (tile_m >= mtiles) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = tile_m * 32 + (r & 3) + 8 * (r >> 2) + 4 * hsel;
+            if (EPI == EPI_GLU) {
+#pragma unroll
+                for (int t = 0; t < NW; ++t) {
+                    if (!nv[t]) continue;
+                    // up * silu(gate) in f32, rounded once to f16 into the down
+                    // projection's A tiles (K = N/2 columns); a value past the
+                    // f16 range raises status bit 4
+                    const float v = m < a.M ? acc[i][t + NW][r] * ggml_silu(acc[i][t][r]) : 0.0f;
+                    over |= !(fabsf(v) <= kF16Max);
+                    ((_Float16*)a.xh_out)[a_tile_index(m, nbase[t] + r32, N >> 1)] = (_Float16)v;
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+                    if (nv[t] && m < a.M) epilogue(a, m, nbase[t] + r32, acc[i][t][r], EPI);
+            }
+        }
+    }
+    if (EPI == EPI_GLU && over && a.status) atomicOr(a.status, 16);
+}
+
+}  // namespace
+
+bool prompt_gemm_supported(int type, size_t K, size_t N, int epi) {
+    if (type != kQ4_K || K % 256 || K > 8192 || N == 0) return false;
+    if (epi == EPI_GLU) return N % 64 == 0 && (N / 2) % 256 == 0;
+    return true;
+}
+
+// Shapes: per-wave MT x NT tiles; the largest workgroup tile that still
+// gives at least one workgroup per CU (256 CUs), else the smallest.
+// Measured (rocprofv3 counters, 2B-shaped prefill): the kernel is bound by
+// the VALU work of the in-register dequantization (about 5 VALU
+// instructions per MFMA with 4 M tiles per wave); 8-wave workgroups (two
+// waves per SIMD) and 8 M tiles per wave measured no faster.
+hipError_t prompt_gemm(const DeviceWeight& w, const FusedGemvArgs& args, const _Float16* xh, hipStream_t s) {
+    if (!prompt_gemm_supported(w.type, w.K, w.N, args.epi) || !w.qs_t || !w.hdr_t || args.M <= 0)
+        return hipErrorInvalidValue;
+    if (args.epi == EPI_GLU && !args.xh_out) return hipErrorInvalidValue;
+    FusedGemvArgs a = args;
+    a.qs = w.qs_t;
+    a.hdr = w.hdr_t;
+    a.K = (int)w.K;
+    a.N = (int)w.N;
+    const int mtiles = (a.M + 31) / 32;
+    const int ntiles = a.epi == EPI_GLU ? a.N / 64 : (a.N + 31) / 32;  // SwiGLU: gate/up tile pairs
+    auto grid = [&](int mt, int nt, int wn, int wm) {
+        const int nw = a.epi == EPI_GLU ? nt / 2 : nt;
+        return dim3((unsigned)((ntiles + wn * nw - 1) / (wn * nw)), (unsigned)((mtiles + wm * mt - 1) / (wm * mt)));
+    };
+    auto count = [&](dim3 g) { return (long)g.x * g.y; };
+#define ZG_GQ(E, MTV, NTV, WNV, WMV)                                                                                   \
+    hipLaunchKernelGGL((gemm_q4k_kernel<E, MTV, NTV, WNV, WMV>), grid(MTV, NTV, WNV, WMV), dim3(64 * WNV * WMV), 0, s, \
+                       a, xh)
+#define ZG_GQE(E)                                                  \
+    if (count(grid(4, 4, 4, 1)) >= 256) ZG_GQ(E, 4, 4, 4, 1);      \
+    else if (count(grid(2, 4, 4, 1)) >= 256) ZG_GQ(E, 2, 4, 4, 1); \
+    else ZG_GQ(E, 2, 2, 2, 2);
+    if (a.epi == EPI_GLU) {
+        ZG_GQE(EPI_GLU)
+    } else if (a.epi == EPI_RESID) {
+        ZG_GQE(EPI_RESID)
+    } else {
+        ZG_GQE(EPI_STORE)
+    }
+#undef ZG_GQE
+#undef ZG_GQ
+    return hipGetLastError();
+}
+
+}  // namespace zg

@@ -227,49 +227,6 @@ __global__ void dequant_q4k_kernel(const uint8_t* __restrict__ qs, const v4u* __
     }
 }
 
-// dequant_q4k_kernel's arithmetic, rounded once to f16: thread t writes the
-// 8 elements 8t..8t+7 (one 32-group's eighth, 16 bytes, coalesced)
-__global__ void q4k_to_f16_kernel(const uint8_t* __restrict__ qs, const v4u* __restrict__ hdr,
-                                  _Float16* __restrict__ out, size_t n8) {
-    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= n8) return;
-    const size_t e0 = t * 8, b = e0 >> 8;
-    const int g = (int)((e0 >> 5) & 7), i0 = (int)(e0 & 31);
-    const v4u h = hdr[b];
-    const float d = f16_to_f32((uint16_t)(h.x & 0xffffu));
-    const float dmin = f16_to_f32((uint16_t)(h.x >> 16));
-    uint32_t sc, mn;
-    q4k_dev_scale_min(h, g, sc, mn);
-    const float scale = d * (float)sc, mnf = dmin * (float)mn;
-    const uint2 q8 = *(const uint2*)(qs + b * 128 + (g >> 1) * 32 + i0);
-    typedef _Float16 h8v __attribute__((ext_vector_type(8)));
-    h8v o;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t byte = ((i < 4 ? q8.x : q8.y) >> (8 * (i & 3))) & 0xffu;
-        const uint32_t v = (g & 1) ? (byte >> 4) : (byte & 15u);
-        o[i] = (_Float16)(scale * (float)v - mnf);
-    }
-    *(h8v*)(out + e0) = o;
-}
-
-hipError_t ensure_f16_weight(DeviceWeight& w, hipStream_t s) {
-    if (w.w16) return hipSuccess;
-    if (w.type != kQ4_K || w.K % 256) return hipErrorInvalidValue;
-    void* p = nullptr;
-    hipError_t e = hipMalloc(&p, w.N * w.K * 2);
-    if (e != hipSuccess) return e;
-    const size_t n8 = w.N * w.K / 8;
-    hipLaunchKernelGGL(q4k_to_f16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const uint8_t*)w.qs,
-                       (const v4u*)w.hdr, (_Float16*)p, n8);
-    e = hipGetLastError();
-    if (e != hipSuccess) {
-        (void)hipFree(p);
-        return e;
-    }
-    w.w16 = p;
-    return hipSuccess;
-}
 
 hipError_t dequantize_rows(const DeviceWeight& w, size_t row0, size_t rows, float* out, hipStream_t s) {
     if (row0 + rows > w.N) return hipErrorInvalidValue;

@@ -30,10 +30,6 @@ struct DeviceWeight {
     // headers in the MFMA operand order of 32-row tiles (ensure_mfma_tiles).
     void* qs_t = nullptr;
     void* hdr_t = nullptr;
-    // Q4_K only, built on demand for prompt-sized batched prefill: the exact
-    // dequantized weight rounded once to f16, row-major [N][K], the operand
-    // of the library GEMM (ensure_f16_weight).
-    void* w16 = nullptr;
 };
 
 size_t gguf_row_bytes(int type, size_t K);
@@ -46,19 +42,9 @@ hipError_t repack_weight(const uint8_t* d_gguf, DeviceWeight& w, int* d_bad, hip
 // f32 [rows][K].
 hipError_t dequantize_rows(const DeviceWeight& w, size_t row0, size_t rows, float* out, hipStream_t s);
 
-// Activation rows from which batched_gemv takes the library GEMM when the
-// weight's f16 copy exists.
-constexpr int kBlasRows = 512;
-
-// Q4_K: allocates and fills w.w16 (no-op when present).
-hipError_t ensure_f16_weight(DeviceWeight& w, hipStream_t s);
-
-// D (+)= A . W^T through hipBLASLt: A f16 row-major [M][K] (ld K), W f16
-// row-major [N][K] (ld K), D row-major [M][N] with leading dimension ldd,
-// f32 (beta 0 or 1, C = D) or f16 (beta 0); f32 accumulation.  One library
-// handle and 64 MB workspace per device, algorithms cached per shape.
-hipError_t blas_gemm_f16(int device, int M, int N, int K, const void* A, const void* W, void* D, bool d_f32,
-                         size_t ldd, float beta, hipStream_t s);
+// Activation rows from which batched_gemv runs the register-blocked prompt
+// GEMM (zg_gemm.hip) instead of the decode-shaped MFMA kernel.
+constexpr int kGemmRows = 256;
 
 // Activation preparation for M rows of width K: optional RMSNorm with gamma
 // (f64 sum of f32 squares, f32 mean, 1/sqrtf, (x*inv)*gamma), then any of:
@@ -201,6 +187,11 @@ size_t batched_scratch_bytes(size_t M, size_t K);
 // graph capture.  batched_gemv refuses a Q4_K weight without them.
 hipError_t ensure_mfma_tiles(DeviceWeight& w, hipStream_t s);
 hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& a, void* scratch, hipStream_t s);
+// The prompt-sized GEMM on f16 A tiles `xh` (act16_kernel's layout, or the
+// previous gate/up GEMM's SwiGLU tiles): EPI_STORE / EPI_RESID into y, or
+// EPI_GLU into xh_out (a product past the f16 range sets status bit 4).
+bool prompt_gemm_supported(int type, size_t K, size_t N, int epi);
+hipError_t prompt_gemm(const DeviceWeight& w, const FusedGemvArgs& a, const _Float16* xh, hipStream_t s);
 
 // GDN decode: conv (4-slot ring per channel) + SiLU + q/k L2 + gates +
 // recurrence for B rows.  proj rows: [qkv (3W) | z (W) | alpha (H) | beta (H)].
@@ -213,6 +204,7 @@ struct GdnDecodeArgs {
     const float *dt = nullptr, *ssm_a = nullptr;
     float eps = 0.0f, scale = 0.0f;
     float* state = nullptr;  // row b at state + b*state_row: [H][128][128] value-major
+    int* status = nullptr;   // bit 4: the f16 tiles' value past the f16 range
     float* core = nullptr;   // [B][W]
     int H = 0;
     // optional double-buffered rows (the session's uncommitted draft): row b
@@ -245,7 +237,7 @@ struct AttnDecodeArgs {
     size_t score_stride = 0, head_stride = 0;
     float* out = nullptr;
     size_t out_stride = 0;
-    int* status = nullptr;  // bit 3: degenerate softmax sum
+    int* status = nullptr;  // bit 3: degenerate softmax sum; bit 4: a batched f16 operand past its range
     float* stats = nullptr;  // [B][nq][2] softmax {max, 1/sum}
     int nq = 0, nkv = 0, max_ctx = 0;
     // batched rows (optional): the gated output also written as f16 MFMA
@@ -282,6 +274,7 @@ struct AttnPrefillArgs {
     void *kcache = nullptr, *vcache = nullptr;  // this row's [max_ctx][nkv*256]
     float* Q = nullptr;                         // scratch [n][nq][256]
     float* out = nullptr;                       // [n][nq*256], gated
+    int* status = nullptr;                      // bit 4: a K or V value past the f16 range
 };
 // q/k norm + RoPE + KV append for the n tokens, then causal attention.
 hipError_t attn_prefill(const AttnPrefillArgs& a, hipStream_t s);

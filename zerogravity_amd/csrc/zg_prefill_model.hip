@@ -213,8 +213,9 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
                                                                    const KV* __restrict__ vc, int n, int nq,
                                                                    int nkv, int pos0, float scale,
                                                                    const float* __restrict__ P, size_t ldp,
-                                                                   float* __restrict__ out) {
+                                                                   float* __restrict__ out, int* __restrict__ status) {
     constexpr int QT = 32, KB = 32, D = 256;
+    bool over = false;  // a staged K or V value past the f16 range
     constexpr int KROW = D + 8;   // halves per staged key row (16-byte pad)
     constexpr int VROW = KB + 8;  // halves per staged value column
     __shared__ _Float16 ks[KB * KROW];
@@ -282,7 +283,10 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
                 *(ah4*)(ks + key * KROW + d4) =
                     ah4{(_Float16)kv4[0], (_Float16)kv4[1], (_Float16)kv4[2], (_Float16)kv4[3]};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) vt[(d4 + i) * VROW + key] = (_Float16)vv4[i];
+                for (int i = 0; i < 4; ++i) {
+                    vt[(d4 + i) * VROW + key] = (_Float16)vv4[i];
+                    over |= !(fabsf(vv4[i]) <= 65504.0f) || !(fabsf(kv4[i]) <= 65504.0f);
+                }
             }
             if (b + 1 < nblk) load_share(b + 1);
         } else {
@@ -295,7 +299,10 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
                 *(ah4*)(ks + key * KROW + d4) =
                     ah4{(_Float16)kv4[0], (_Float16)kv4[1], (_Float16)kv4[2], (_Float16)kv4[3]};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) vt[(d4 + i) * VROW + key] = (_Float16)vv4[i];
+                for (int i = 0; i < 4; ++i) {
+                    vt[(d4 + i) * VROW + key] = (_Float16)vv4[i];
+                    over |= !(fabsf(vv4[i]) <= 65504.0f) || !(fabsf(kv4[i]) <= 65504.0f);
+                }
             }
         }
         __syncthreads();
@@ -356,6 +363,7 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
                 *(v4f*)(orow + dim) = ov;
             }
     }
+    if (over && status) atomicOr(status, 16);
 }
 
 hipError_t gdn_prefill_conv(const float* P, size_t ldp, size_t n, size_t W, size_t H, const float* conv_w,
@@ -386,7 +394,7 @@ hipError_t attn_prefill(const AttnPrefillArgs& a, hipStream_t s) {
     const dim3 grid((unsigned)((a.n + 31) / 32), (unsigned)a.nkv);
 #define ZG_AP(KV, GG)                                                                                              \
     hipLaunchKernelGGL((attn_prefill_mfma_kernel<KV, GG>), grid, dim3(64 * GG), 0, s, a.Q, (const KV*)a.kcache,   \
-                       (const KV*)a.vcache, (int)a.n, a.nq, a.nkv, a.pos0, a.scale, a.P, a.ldp, a.out)
+                       (const KV*)a.vcache, (int)a.n, a.nq, a.nkv, a.pos0, a.scale, a.P, a.ldp, a.out, a.status)
 #define ZG_APG(KV)                  \
     switch (G) {                    \
     case 1: ZG_AP(KV, 1); break;    \

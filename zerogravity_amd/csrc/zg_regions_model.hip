@@ -262,6 +262,7 @@ int zg_gdn_decode_gated_device(zg_ctx* ctx, size_t rows, size_t heads, const flo
     d.H = (int)heads;
     d.xh = tiles;
     d.norm = norm;
+    d.status = ctx->d_flag;
     ZG_HIP(zg::gdn_decode(d, rows, stream ? (hipStream_t)stream : ctx->stream));
     return ZG_COMPLETED;
 }

@@ -311,6 +311,7 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             d.eps = g.eps;
             d.scale = 1.0f / sqrtf((float)g.gdn_dim);
             d.state = s->rec[slot];
+            d.status = s->d_status;
             d.cur = s->d_cur;
             d.state_row = 2 * rec_floats(g);
             d.state_half = rec_floats(g);
@@ -470,6 +471,10 @@ int read_status(zg_session* s, hipStream_t st) {
         if (status & 2) return fail(ctx, ZG_E_MALFORMED, "decode step contains an out-of-vocabulary token id");
         if (status & 1) return fail(ctx, ZG_E_STATE, "nonfinite layer computation");
         if (status & 8) return fail(ctx, ZG_E_STATE, "degenerate attention softmax");
+        if (status & 16)
+            return fail(ctx, ZG_E_LIMIT,
+                        "an activation exceeds the f16 range of the batched projections (zg_prefill and steps of at "
+                        "most 4 rows compute in f32)");
         return fail(ctx, ZG_E_STATE, "decoder produced nonfinite logits");
     }
     return ZG_COMPLETED;
@@ -1019,12 +1024,6 @@ int prefill_batched_body(zg_session* s, size_t row, size_t n, const uint32_t* to
     hipStream_t st = ctx->stream;
     for (zg_weight* w : ws)
         if (!w->dw.qs_t) ZG_HIP(zg::ensure_mfma_tiles(w->dw, st));
-    // prompt-sized calls run every projection through the library GEMM on
-    // f16 copies of the weights, made once (all four of a layer together, so
-    // that the gate/up and down GEMMs agree on the activation layout)
-    if (n >= (size_t)zg::kBlasRows)
-        for (zg_weight* w : ws)
-            if (!w->dw.w16) ZG_HIP(zg::ensure_f16_weight(w->dw, st));
     const size_t H = g.hidden, F = g.ffn, W = (size_t)g.gdn_heads * g.gdn_dim, GH = g.gdn_heads;
     const size_t QD = (size_t)g.q_heads * g.head_dim;
     const size_t mpad = (n + 31) / 32 * 32;
@@ -1108,6 +1107,7 @@ int prefill_batched_body(zg_session* s, size_t row, size_t n, const uint32_t* to
             a.vcache = (char*)s->vc[slot] + row * s->max_ctx * kvw(g) * esz;
             a.Q = (float*)s->pf[QB];
             a.out = (float*)s->pf[OB];
+            a.status = s->d_status;
             ZG_HIP(zg::attn_prefill(a, st));
             ZG_HIP(gemm(L.out_proj, zg::PRO_PLAIN, (const float*)s->pf[OB], QD, nullptr, 0, nullptr, zg::EPI_RESID, x,
                         H));
