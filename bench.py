@@ -748,6 +748,51 @@ def bench_copy(args):
             "config": {"workload": "calibration copy", "bytes_read": n * 4, "bytes_written": n * 4}}
 
 
+def bench_floors(args):
+    """The floors the decode step's design rests on, from libzg_probe.so
+    (kernels that only measure; nothing on the hot path calls them):
+    a graph chain of dependent launches vs the same dependency handed over
+    inside one persistent cooperative kernel, GEMV-shaped launches of the
+    decode step's weight sizes, and in-place read-modify-write."""
+    import ctypes
+    import torch
+    torch.cuda.init()
+    lib = ctypes.CDLL(os.path.join(ROOT, "zerogravity_amd", "libzg_probe.so"))
+    f = ctypes.c_float()
+    out = {"chain_us": {}, "handoff_us": {}, "stream_us": {}, "rmw_gbs": {}}
+
+    def call(fn, *a):
+        rc = fn(*a, ctypes.byref(f))
+        if rc < 0:
+            raise RuntimeError(f"{fn.__name__} failed ({rc})")
+        return rc, round(f.value, 3)
+
+    lib.zg_probe_stream.argtypes = [ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.zg_probe_rmw.argtypes = [ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+    for wgs in (8, 64, 256):
+        for N in (2048, 6144):
+            out["chain_us"][f"{wgs}wg_{N}"] = call(lib.zg_probe_chain, wgs, N, 512)[1]
+            log(f"chain {wgs} WGs N={N}: {out['chain_us'][f'{wgs}wg_{N}']} us/phase")
+    for mode, name in ((0, "ll_words"), (1, "counter_agent"), (2, "counter_fenced")):
+        for wgs in (8, 64, 256):
+            rc, us = call(lib.zg_probe_handoff, mode, wgs, 2048, 512)
+            out["handoff_us"][f"{name}_{wgs}wg"] = us if rc == 0 else None
+            log(f"handoff {name} {wgs} WGs: {us} us/phase" + (" (a bounded wait expired: void)" if rc else ""))
+    for mb in (1.2, 2.4, 4.7, 7.1, 14.2, 78.0):
+        b = int(mb * 1e6) // 4096 * 4096
+        wgs = max(256, min(4096, b // (256 * 16 * 4)))
+        out["stream_us"][f"{mb}MB"] = us = call(lib.zg_probe_stream, b, wgs, 200)[1]
+        log(f"stream {mb} MB: {us} us/launch = {b / us / 1e3:.0f} GB/s")
+    for mb in (1, 4, 16, 64, 256):
+        out["rmw_gbs"][f"{mb}MB"] = v = call(lib.zg_probe_rmw, mb << 20, 64)[1]
+        log(f"rmw {mb} MiB: {v} GB/s")
+    chain = out["chain_us"]["256wg_2048"]
+    return {"metric": "dependent-launch floor, us per phase (graph chain, 256 WGs, 2048 floats)", "value": chain,
+            "unit": "us", "n_gpus": 1, "steps": 512, "warmup": 1, "ms_per_step": round(chain / 1e3, 6),
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "launch and hand-off floors", **out}}
+
+
 def cpu_gdn_baseline(seconds, H=16):
     """The oracle's GDN decode step at B=1 (conv over 3 x 2048 channels, SiLU,
     two-stage q/k L2, gates, the 16-head recurrence; one host thread, serial
@@ -862,7 +907,7 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode_q8", "decode_mixed", "gemv", "prefill", "gdn", "model_prefill", "copy", "config1"])
+                    choices=["decode", "decode_q8", "decode_mixed", "gemv", "prefill", "gdn", "model_prefill", "copy", "config1", "floors"])
     ap.add_argument("--prefix", type=int, default=2048)
     ap.add_argument("--leg-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -874,7 +919,8 @@ def main():
         sys.exit(2)
     bench = {"decode": bench_decode, "decode_q8": bench_decode_q8,
              "decode_mixed": lambda a: bench_decode_q8(a, mixed=True), "gemv": bench_gemv, "prefill": bench_prefill, "gdn": bench_gdn,
-             "model_prefill": bench_model_prefill, "copy": bench_copy, "config1": bench_config1}[args.workload]
+             "model_prefill": bench_model_prefill, "copy": bench_copy, "config1": bench_config1,
+             "floors": bench_floors}[args.workload]
     line = bench(args)
     print(json.dumps(line), flush=True)
 
