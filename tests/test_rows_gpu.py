@@ -5,32 +5,48 @@ step), and forking a prefilled prompt into another row.
 
 Reference behaviour: each row of a cohort evolves as its own session
 (resident_inference.rs:1101-1111, private per-row state); a row's logits
-depend only on its own tokens.  Every row is therefore checked against its
-own one-row device session run on the same tokens (same fused kernels: the
-batched decode step at B <= 4 computes each row independently in the same
-order, 1e-3 bar as in test_model_gpu.py) and greedy tokens must agree.
+depend only on its own tokens.  Every row is therefore checked against the
+oracle's own session for its request (the north star's 2e-2 end-to-end bar,
+same greedy token; the oracle calls glibc's transcendentals as the
+reference's f32 functions do) and against its own one-row device session
+run on the same tokens.  One row takes the int8 matrix-core GEMV and 2..4
+rows the fused dot4 kernel, each with its own int16 activation coding, so
+the device pair agrees to the coding noise (ROW_TOL), far below what a leak
+between rows would show; prefill logits of the same prompt run the same
+kernels and agree bit for bit.
 """
 import numpy as np
 import pytest
 
+import zg_oracle as O
 from zerogravity_amd import _lib as L
 from zerogravity_amd import gguf, qwen35
 from zerogravity_amd import regions as R
 
-pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("exact_libm")]
-ROW_TOL = 1e-3
+pytestmark = pytest.mark.gpu
+ROW_TOL = 5e-3
+LOGIT_TOL = 2e-2
 
 TINY = dict(hidden=512, layers=4, ffn=512, vocab=1000, gdn_heads=2, gdn_dim=128, q_heads=2, kv_heads=1,
             head_dim=256, full_attention_interval=4, max_context=4096, eps=1e-6)
 
 
 @pytest.fixture(scope="module")
-def model():
+def tensors():
+    return qwen35.synthetic_tensors(TINY, gguf.Q4_K, seed=12)
+
+
+@pytest.fixture(scope="module")
+def model(tensors):
     kern = R.HipMatVecKernel(0)
-    t = qwen35.synthetic_tensors(TINY, gguf.Q4_K, seed=12)
-    m = qwen35.QwenModelHip(TINY, t, kernel=kern)
+    m = qwen35.QwenModelHip(TINY, tensors, kernel=kern)
     yield m
     m.close()
+
+
+@pytest.fixture(scope="module")
+def oracle(tensors):
+    return O.Model(TINY, tensors)
 
 
 def _toks(seed, n):
@@ -38,21 +54,39 @@ def _toks(seed, n):
 
 
 class Solo:
-    """One request on its own one-row session."""
+    """One request on its own one-row device session, with the oracle's
+    session for the same request beside it."""
 
-    def __init__(self, model, prompt):
+    def __init__(self, model, prompt, oracle=None):
         self.s = model.session(max_batch=1, max_context=256, kv_dtype=L.BF16)
         self.last = self.s.prefill_batched(prompt)
+        self.o = None
+        if oracle is not None:
+            self.o = oracle.session(kv_bf16=True)
+            with O.libm_mode(O.LIBM_GLIBC):
+                for t in prompt:
+                    self.ref = self.o.forward(int(t))
+            check_oracle(self.last, self.ref)
 
     def step(self, tok):
         self.last = self.s.forward(tok)
+        if self.o is not None:
+            with O.libm_mode(O.LIBM_GLIBC):
+                self.ref = self.o.forward(int(tok))
+            check_oracle(self.last, self.ref)
         return self.last
 
 
-def test_admit_decode_retire_compact(model):
+def check_oracle(lg, ref):
+    err = float(np.max(np.abs(lg - ref)))
+    assert err <= LOGIT_TOL, err
+    assert int(np.argmax(lg)) == O.greedy(ref)
+
+
+def test_admit_decode_retire_compact(model, oracle):
     prompts = [_toks(1, 40), _toks(2, 9), _toks(3, 70)]
     s = model.session(max_batch=4, max_context=256, kv_dtype=L.BF16)
-    solos = [Solo(model, p) for p in prompts]
+    solos = [Solo(model, p, oracle) for p in prompts]
     last = []
     for r, p in enumerate(prompts):
         last.append(s.prefill_batched(p, row=r))
@@ -70,16 +104,22 @@ def test_admit_decode_retire_compact(model):
             assert s.positions()[2] == 0 and np.all(s.state(row=2) == 0)
         lg, _ = s.step(np.array(toks, np.uint32))
         for r in range(active):
-            ref = solos[owner[r]].step(toks[r])
+            solo = solos[owner[r]]
+            ref = solo.step(toks[r])
             err = float(np.max(np.abs(lg[r] - ref)))
             assert err <= ROW_TOL, (step, r, err)
             assert int(np.argmax(lg[r])) == int(np.argmax(ref))
+            check_oracle(lg[r], solo.ref)  # the retired row's successor too
         toks = [int(np.argmax(lg[r])) for r in range(active)]
     pos = s.positions()
     assert pos[0] == 40 + 6 and pos[1] == 70 + 6 and pos[2] == 0
-    # admit a new request into the freed slot
+    # admit a new request into the freed slot: the same logits as its own
+    # session, and the oracle's for that prompt
     lg = s.prefill_batched(_toks(4, 33), row=2)
-    assert np.array_equal(lg, Solo(model, _toks(4, 33)).last)
+    admitted = Solo(model, _toks(4, 33), oracle)
+    assert np.array_equal(lg, admitted.last)
+    lg2, _ = s.step(np.array(toks + [int(np.argmax(lg))], np.uint32))
+    check_oracle(lg2[2], admitted.o.forward(int(np.argmax(lg))))
     s.close()
 
 

@@ -93,8 +93,9 @@ int build_weight(zg_ctx* ctx, int type, size_t cols, size_t rows, const void* by
         w->dw.qs_bytes = (rows + 7) / 8 * nbc * 1024;
         w->dw.hdr_bytes = rows * nbc * 4 * 2;
     } else if (type == ZG_Q4_K) {
-        w->dw.qs_bytes = rows * (cols / 2);
-        w->dw.hdr_bytes = rows * (cols / 256) * 16;
+        const size_t rows16 = (rows + 15) / 16 * 16;  // q4k_chunk_offset's 16-row tiles
+        w->dw.qs_bytes = rows16 * (cols / 2);
+        w->dw.hdr_bytes = rows16 * (cols / 256) * 16;
     } else if (type == ZG_Q4_1) {
         const size_t nbc8 = (cols / 32 + 7) / 8;
         w->dw.qs_bytes = (rows + 7) / 8 * nbc8 * 1024;

@@ -272,14 +272,14 @@ __global__ __launch_bounds__(256) void mfma_tile_q4k_kernel(const uint8_t* __res
     const int row = tile * 32 + (lane & 31), hsel = lane >> 5;
     v4u out = v4u{0u, 0u, 0u, 0u};
     if (row < N) {
-        const uint8_t* b = qs + (size_t)row * (K >> 1) + (size_t)kb * 128 + 32 * c4 + 8 * hsel;
-        const uint2 p0 = *(const uint2*)b, p1 = *(const uint2*)(b + 16);
+        const uint8_t* b = qs + q4k_chunk_offset(row, 4 * kb + c4, K) + 8 * hsel;
+        const uint2 p0 = *(const uint2*)b, p1 = *(const uint2*)(b + 256);
         out = v4u{p0.x, p0.y, p1.x, p1.y};
     }
     qs_t[(((size_t)tile * nbk + kb) * 4 + c4) * 64 + lane] = out;
     if (tid < 32) {
         const int r = tile * 32 + tid;
-        hdr_t[((size_t)tile * nbk + kb) * 32 + tid] = r < N ? hdr[(size_t)r * nbk + kb] : v4u{0u, 0u, 0u, 0u};
+        hdr_t[((size_t)tile * nbk + kb) * 32 + tid] = r < N ? hdr[q4k_hdr_index(r, kb, nbk)] : v4u{0u, 0u, 0u, 0u};
     }
 }
 

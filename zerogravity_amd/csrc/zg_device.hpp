@@ -151,6 +151,23 @@ __device__ __forceinline__ v4i load_nt(const void* p) {
     return __builtin_nontemporal_load((const v4i*)p);
 }
 
+// Q4_K device layout: tiles of 16 rows in the int8 MFMA operand order.  The
+// 64 bytes of unit q (elements 128q .. 128q+127) of rows 16t .. 16t+15 form
+// 1 KB at (t * K/128 + q) * 1024, with the 16-byte piece s (bytes 16s ..
+// 16s+15 of the unit) of row 16t + j at (j + 16 s) * 16 inside it, so one
+// wave instruction (lane j + 16 s) reads 1 KB contiguously; rows past N up
+// to the tile are zero.  Within a row the GGUF payload order is kept: byte e
+// of 64-element chunk c holds element 64c + e in its low nibble and
+// 64c + 32 + e in its high nibble.  Byte offset of bytes 0..15 of chunk c of
+// `row` (bytes 16..31 follow 256 bytes later):
+__host__ __device__ __forceinline__ size_t q4k_chunk_offset(size_t row, size_t c, size_t K) {
+    return (((row >> 4) * (K >> 7) + (c >> 1)) * 64 + (row & 15) + 32 * (c & 1)) * 16;
+}
+// Headers [tiles][K/256 blocks][16 rows] x 16 bytes: index of (row, block).
+__host__ __device__ __forceinline__ size_t q4k_hdr_index(size_t row, size_t blk, size_t nbk) {
+    return ((row >> 4) * nbk + blk) * 16 + (row & 15);
+}
+
 // Q8_0 device layout: tiles of 8 rows x 4 blocks, one 16-byte slot per
 // (row % 8, lane-of-block l) holding bytes 4l..4l+3 of the 4 blocks, so the
 // 64 lanes of a wavefront read one contiguous 1 KB tile.  Byte offset of

@@ -3,6 +3,7 @@
 // and their launch templates; zg_fused_<prologue>.hip instantiate one
 // prologue each so that the instantiations compile in parallel.
 #include "zg_decode_common.hpp"
+#include "zg_gemv1.hpp"
 
 namespace zg {
 
@@ -62,10 +63,10 @@ __global__ __launch_bounds__(256) void fused_q4k_kernel(FusedGemvArgs a, int lpr
 #pragma unroll
             for (int i = 0; i < CH; ++i) {
                 const int c = min(sub + i * lpr, nchunk - 1);
-                const uint8_t* base = qs + (size_t)row * (K >> 1) + (size_t)c * 32;
+                const uint8_t* base = qs + q4k_chunk_offset(row, c, K);
                 w0[r][i] = load_nt(base);
-                w1[r][i] = load_nt(base + 16);
-                h[r][i] = hdr[(size_t)row * nbk + (c >> 2)];
+                w1[r][i] = load_nt(base + 256);
+                h[r][i] = hdr[q4k_hdr_index(row, c >> 2, nbk)];
             }
         }
     };
@@ -730,8 +731,23 @@ hipError_t launch_q8(const FusedGemvArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// One activation row of a Q4_K weight with K a multiple of 512 (K / 512 of
+// 1..8, 12, 16) runs on the int8 matrix cores (zg_gemv1.hpp).
+inline bool gemv1_fits(const FusedGemvArgs& a, int type) {
+    const int wv = a.K / 512;
+    return type == kQ4_K && a.M == 1 && a.K % 512 == 0 && (wv <= 8 || wv == 12 || wv == 16) &&
+           (a.pro != PRO_GATED || a.group == 128) && (a.epi != EPI_GLU || a.N % 2 == 0);
+}
+
 template <int PRO>
 hipError_t launch_pro(const FusedGemvArgs& a, int type, hipStream_t s) {
+    if (gemv1_fits(a, type)) {
+        if (a.epi == EPI_GLU) {
+            if constexpr (PRO == PRO_RMS) return launch_gemv1_q4k<PRO_RMS, EPI_GLU>(a, s);
+            return hipErrorInvalidValue;
+        }
+        return a.epi == EPI_RESID ? launch_gemv1_q4k<PRO, EPI_RESID>(a, s) : launch_gemv1_q4k<PRO, EPI_STORE>(a, s);
+    }
     if (a.epi == EPI_GLU) {
         if constexpr (PRO == PRO_RMS) {
             if (type == kQ4_K) return launch_q4k<PRO_RMS, EPI_GLU>(a, s);

@@ -62,10 +62,13 @@ __device__ __forceinline__ void q4k_scale_min(const uint8_t* s, int g, uint32_t&
     }
 }
 
-__global__ void repack_q4k_kernel(const v4i* __restrict__ src, v4i* __restrict__ qs, v4u* __restrict__ hdr,
-                                  size_t nblocks, int* bad) {
+// One GGUF block (row b / nbk, block b % nbk) into the 16-row tile layout
+// (q4k_chunk_offset, q4k_hdr_index) with the header's scale bytes repacked.
+__global__ void repack_q4k_kernel(const v4i* __restrict__ src, uint8_t* __restrict__ qs, v4u* __restrict__ hdr,
+                                  size_t nblocks, size_t nbk, size_t K, int* bad) {
     size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
+    const size_t row = b / nbk, kb = b % nbk;
     const v4i* blk = src + b * 9;  // 144 bytes = 9 x 16
     v4i h = blk[0];
     uint32_t w0 = (uint32_t)h.x;
@@ -84,9 +87,10 @@ __global__ void repack_q4k_kernel(const v4i* __restrict__ src, v4i* __restrict__
         d2 |= (mn0 | (((mn1 >> 2) & 3u) << 6)) << (8 * p);
         d3 |= (sc1 | (((mn1 >> 4) & 3u) << 6)) << (8 * p);
     }
-    hdr[b] = v4u{w0, d1, d2, d3};
+    hdr[q4k_hdr_index(row, kb, nbk)] = v4u{w0, d1, d2, d3};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qs[b * 8 + i] = blk[1 + i];
+    for (int i = 0; i < 8; ++i)  // 16-byte half i % 2 of chunk 4 kb + i / 2
+        *(v4i*)(qs + q4k_chunk_offset(row, 4 * kb + (i >> 1), K) + 256 * (i & 1)) = blk[1 + i];
 }
 
 // GGUF Q4_1 block (codecs/q4.rs:22-36): d f16, m f16, 16 nibble bytes.
@@ -154,8 +158,12 @@ hipError_t repack_weight(const uint8_t* d_gguf, DeviceWeight& w, int* d_bad, hip
     } else if (w.type == kQ4_K) {
         size_t nb = w.N * (w.K / 256);
         unsigned grid = (unsigned)((nb + 255) / 256);
-        hipLaunchKernelGGL(repack_q4k_kernel, dim3(grid), dim3(256), 0, s, (const v4i*)d_gguf, (v4i*)w.qs,
-                           (v4u*)w.hdr, nb, d_bad);
+        // the rows completing the last tile stay zero (d = dmin = 0)
+        hipError_t e = hipMemsetAsync(w.qs, 0, w.qs_bytes, s);
+        if (e == hipSuccess) e = hipMemsetAsync(w.hdr, 0, w.hdr_bytes, s);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(repack_q4k_kernel, dim3(grid), dim3(256), 0, s, (const v4i*)d_gguf, (uint8_t*)w.qs,
+                           (v4u*)w.hdr, nb, w.K / 256, w.K, d_bad);
     } else if (w.type == kF32) {
         return hipMemcpyAsync(w.qs, d_gguf, w.qs_bytes, hipMemcpyDeviceToDevice, s);
     } else if (w.type == kQ4_1) {
@@ -207,20 +215,21 @@ __global__ void dequant_q8_0_kernel(const int8_t* __restrict__ qs, const uint16_
 }
 
 __global__ void dequant_q4k_kernel(const uint8_t* __restrict__ qs, const v4u* __restrict__ hdr,
-                                   float* __restrict__ out, size_t nblocks) {
+                                   float* __restrict__ out, size_t row0, size_t nblocks, size_t nbk, size_t K) {
     size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
-    const v4u h = hdr[b];
+    const size_t row = row0 + b / nbk, kb = b % nbk;
+    const v4u h = hdr[q4k_hdr_index(row, kb, nbk)];
     float d = f16_to_f32((uint16_t)(h.x & 0xffffu));
     float dmin = f16_to_f32((uint16_t)(h.x >> 16));
-    const uint8_t* q = qs + b * 128;
     for (int g = 0; g < 8; ++g) {
         uint32_t sc, mn;
         q4k_dev_scale_min(h, g, sc, mn);
         float scale = d * (float)sc;
         float mnf = dmin * (float)mn;
+        const uint8_t* q = qs + q4k_chunk_offset(row, 4 * kb + (g >> 1), K);
         for (int i = 0; i < 32; ++i) {
-            uint8_t byte = q[(g >> 1) * 32 + i];
+            uint8_t byte = q[i < 16 ? i : 256 + i - 16];
             uint32_t v = (g & 1) ? (byte >> 4) : (byte & 15);
             out[b * 256 + g * 32 + i] = scale * (float)v - mnf;
         }
@@ -237,7 +246,7 @@ hipError_t dequantize_rows(const DeviceWeight& w, size_t row0, size_t rows, floa
     } else if (w.type == kQ4_K) {
         const size_t bpr = w.K / 256, nb = rows * bpr;
         hipLaunchKernelGGL(dequant_q4k_kernel, dim3((unsigned)((nb + 63) / 64)), dim3(64), 0, s,
-                           (const uint8_t*)w.qs + row0 * (w.K / 2), (const v4u*)w.hdr + row0 * bpr, out, nb);
+                           (const uint8_t*)w.qs, (const v4u*)w.hdr, out, row0, nb, bpr, w.K);
     } else if (w.type == kF32) {
         return hipMemcpyAsync(out, (const float*)w.qs + row0 * w.K, rows * w.K * 4, hipMemcpyDeviceToDevice, s);
     } else if (w.type == kQ4_1 || w.type == kQ6_K) {
@@ -519,10 +528,10 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(const uint8_t* __restrict
         for (int i = 0; i < CH; ++i) {
             const int c = sub + i * lpr;
             if (rv && c < nchunk) {
-                const uint8_t* base = qs + (size_t)row * (K >> 1) + (size_t)c * 32;
+                const uint8_t* base = qs + q4k_chunk_offset(row, c, K);
                 w0[i] = load_nt(base);
-                w1[i] = load_nt(base + 16);
-                h[i] = hdr[(size_t)row * nbk + (c >> 2)];
+                w1[i] = load_nt(base + 256);
+                h[i] = hdr[q4k_hdr_index(row, c >> 2, nbk)];
             } else {
                 w0[i] = v4i{0, 0, 0, 0};
                 w1[i] = v4i{0, 0, 0, 0};

@@ -12,14 +12,16 @@ enum GgmlType { kF32 = 0, kF16 = 1, kQ4_1 = 3, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14
 // split once at registration into a streaming payload and a small per-block
 // header array so every wavefront load is a coalesced 16-byte load:
 //   Q8_0: qs  = int8 [N][K]            hdr = f16 scale [N][K/32]
-//   Q4_K: qs  = nibbles [N][K/2]       hdr = 16-byte block header [N][K/256]
-//         (d, dmin, 12 packed 6-bit scale/min bytes, unchanged)
+//   Q4_K: qs  = nibbles in 16-row tiles (q4k_chunk_offset)
+//         hdr = 16-byte block headers in 16-row tiles (q4k_hdr_index):
+//         d, dmin and the 12 scale/min bytes repacked (q4k_dev_scale_min)
 //   F32 : qs  = float [N][K]           hdr = null
 //   Q4_1: qs  = nibble words in 8-row tiles (q41_word_index)
 //         hdr = uint32 d | m << 16 [N][K/32 rounded to 8 blocks]
 //   Q6_K: qs  = bit planes A and B in 8-row tiles (q6k_a_index, q6k_b_index)
 //         hdr = int8 local scales [N][K/256][16], then f32 d [N][K/256]
-// Algorithmic bytes are unchanged: 1.0625 B/elem (Q8_0), 0.5625 (Q4_K).
+// Algorithmic bytes are unchanged: 1.0625 B/elem (Q8_0), 0.5625 (Q4_K; plus
+// the zero rows that complete the last 16-row tile).
 struct DeviceWeight {
     int type = -1;
     size_t K = 0, N = 0;

@@ -58,8 +58,7 @@ __global__ void embed_q4k_kernel(const uint8_t* __restrict__ qs, const v4u* __re
         x[(size_t)b * K + i] = 0.0f;
         return;
     }
-    const size_t blk = (size_t)t * (K / 256) + i / 256;
-    const v4u h = hdr[blk];
+    const v4u h = hdr[q4k_hdr_index(t, i / 256, K / 256)];
     const int e = i % 256, g = e / 32, pos = e % 32;
     const int sh = 8 * (g >> 1);
     const uint32_t b1 = (h.y >> sh) & 0xffu, b2 = (h.z >> sh) & 0xffu, b3 = (h.w >> sh) & 0xffu;
@@ -73,7 +72,7 @@ __global__ void embed_q4k_kernel(const uint8_t* __restrict__ qs, const v4u* __re
     }
     const float d = f16_to_f32((uint16_t)(h.x & 0xffffu)), dmin = f16_to_f32((uint16_t)(h.x >> 16));
     const float scale = d * (float)sc, mnf = dmin * (float)mn;
-    const uint8_t byte = qs[blk * 128 + (g >> 1) * 32 + pos];
+    const uint8_t byte = qs[q4k_chunk_offset(t, i / 64, K) + (pos < 16 ? pos : 256 + pos - 16)];
     const uint32_t v = (g & 1) ? (byte >> 4) : (byte & 15);
     x[(size_t)b * K + i] = scale * (float)v - mnf;
 }
