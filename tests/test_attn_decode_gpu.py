@@ -39,22 +39,9 @@ def ctx():
 LONG32 = [0, 2303, 3100, 4100, 8191] + [int(p) for p in np.linspace(17, 8180, 27)]
 
 
-# Each case reaches one branch of the device kernels: a cache of <= 2304
-# rows (one 72 x 32 value tile), of <= 3072 (one 96 x 32 tile), beyond
-# (tiled values with the softmax statistics computed ahead), beyond 4096
-# (statistics over several score spans), and 8 rows or more (a statistics
-# launch, then 4 query heads x 16 channels per workgroup).
-@pytest.mark.parametrize("kv,max_ctx,positions", [
-    (L.BF16, 2048, [0, 299, 2047]),
-    (L.F32, 2048, [0, 299, 2047]),
-    (L.BF16, 3072, [0, 2303, 3071]),
-    (L.BF16, 4096, [0, 2303, 3100]),
-    (L.BF16, 8192, [4100, 8191, 2303]),
-    (L.F32, 8192, [8191, 4100, 0]),
-    (L.BF16, 8192, LONG32),
-    (L.BF16, 2048, [int(p) for p in np.linspace(0, 2047, 32)]),
-])
-def test_attn_decode_device_matches_oracle(ctx, kv, max_ctx, positions):
+def _run_case(ctx, kv, max_ctx, positions, split):
+    """Device attention decode of one case and the oracle's reference per row:
+    returns (device output, reference outputs, appended-K/V checks done)."""
     import torch
     nq, nkv, eps = 8, 2, 1e-6
     theta = math.pow(1e7, -2.0 / 64.0)
@@ -75,12 +62,18 @@ def test_attn_decode_device_matches_oracle(ctx, kv, max_ctx, positions):
         kc, vc = torch.from_numpy(hist_k.copy()).cuda(), torch.from_numpy(hist_v.copy()).cuda()
     d_proj, d_pos = torch.from_numpy(proj).cuda(), torch.from_numpy(pos).cuda()
     d_qn, d_kn = torch.from_numpy(qn_w).cuda(), torch.from_numpy(kn_w).cuda()
-    ws = torch.empty(L.lib().zg_attn_decode_workspace_bytes(B, nq, max_ctx), dtype=torch.uint8, device="cuda")
+    if split:
+        nbytes = L.lib().zg_attn_decode_split_workspace_bytes(B, nq, nkv, max_ctx)
+        assert nbytes > 0
+        entry = L.lib().zg_attn_decode_split_device
+    else:
+        nbytes = L.lib().zg_attn_decode_workspace_bytes(B, nq, max_ctx)
+        entry = L.lib().zg_attn_decode_device
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
     out = torch.empty((B, nq * D), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
-    ctx.check(L.lib().zg_attn_decode_device(ctx.h, B, nq, nkv, d_proj.data_ptr(), stride, d_qn.data_ptr(),
-                                            d_kn.data_ptr(), eps, theta, d_pos.data_ptr(), kc.data_ptr(),
-                                            vc.data_ptr(), max_ctx, kv, ws.data_ptr(), out.data_ptr(), None))
+    ctx.check(entry(ctx.h, B, nq, nkv, d_proj.data_ptr(), stride, d_qn.data_ptr(), d_kn.data_ptr(), eps, theta,
+                    d_pos.data_ptr(), kc.data_ptr(), vc.data_ptr(), max_ctx, kv, ws.data_ptr(), out.data_ptr(), None))
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     if kv == L.BF16:
@@ -88,6 +81,7 @@ def test_attn_decode_device_matches_oracle(ctx, kv, max_ctx, positions):
         vd = (vc.cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
     else:
         kd, vd = kc.cpu().numpy(), vc.cpu().numpy()
+    refs = []
     for b in range(B):
         p = int(pos[b])
         row = proj[b]
@@ -104,12 +98,66 @@ def test_attn_decode_device_matches_oracle(ctx, kv, max_ctx, positions):
         vals = np.concatenate([hist_v[b, :p], v[None, :]])
         _, scores = O.attention_qk(qr, keys, D, nq, nkv, 1.0 / 16.0)
         probs, _, _ = O.attention_softmax(scores, nq, p + 1)
-        ref = O.binary(1, O.attention_value(probs, vals, D, nq, nkv), gates)
+        refs.append(O.binary(1, O.attention_value(probs, vals, D, nq, nkv), gates))
+        # K/V appended exactly in both forms, the history untouched
         assert np.array_equal(kd[b, p].view(np.uint32), kr.view(np.uint32)), b
         assert np.array_equal(vd[b, p].view(np.uint32), v.view(np.uint32)), b
-        assert np.array_equal(got[b].view(np.uint32), ref.view(np.uint32)), (b, float(np.abs(got[b] - ref).max()))
-        # history untouched
         assert np.array_equal(kd[b, :p].view(np.uint32), hist_k[b, :p].view(np.uint32))
+        assert np.array_equal(vd[b, :p].view(np.uint32), hist_v[b, :p].view(np.uint32))
+    return got, refs
+
+
+# Each case reaches one branch of the device kernels: a cache of <= 2304
+# rows (one 72 x 32 value tile), of <= 3072 (one 96 x 32 tile), beyond
+# (tiled values with the softmax statistics computed ahead), beyond 4096
+# (statistics over several score spans), and 8 rows or more (a statistics
+# launch, then 4 query heads x 16 channels per workgroup).
+@pytest.mark.parametrize("kv,max_ctx,positions", [
+    (L.BF16, 2048, [0, 299, 2047]),
+    (L.F32, 2048, [0, 299, 2047]),
+    (L.BF16, 3072, [0, 2303, 3071]),
+    (L.BF16, 4096, [0, 2303, 3100]),
+    (L.BF16, 8192, [4100, 8191, 2303]),
+    (L.F32, 8192, [8191, 4100, 0]),
+    (L.BF16, 8192, LONG32),
+    (L.BF16, 2048, [int(p) for p in np.linspace(0, 2047, 32)]),
+])
+def test_attn_decode_device_matches_oracle(ctx, kv, max_ctx, positions):
+    got, refs = _run_case(ctx, kv, max_ctx, positions, split=False)
+    for b, ref in enumerate(refs):
+        assert np.array_equal(got[b].view(np.uint32), ref.view(np.uint32)), (b, float(np.abs(got[b] - ref).max()))
+
+
+# The split-T form (1..4 rows): spans of T / chunks tokens, the owner of the
+# position among them; spans of one token block and of many, the position at
+# a span's first and last token, an empty tail of spans (T below the chunk
+# count), caches up to 8192 rows.  The output is held to the per-op bar,
+# 1e-3 relative to the row's largest magnitude.
+SPLIT_REL = 1e-3
+
+
+@pytest.mark.parametrize("kv,max_ctx,positions", [
+    (L.BF16, 2048, [0]),
+    (L.BF16, 2048, [2047]),
+    (L.F32, 2048, [31, 32, 63, 64]),
+    (L.BF16, 4096, [2047, 2048, 5, 4095]),
+    (L.BF16, 8192, [8191, 4100, 1023]),
+    (L.F32, 8192, [6000]),
+    (L.BF16, 300, [299, 150]),
+])
+def test_attn_decode_split_matches_oracle(ctx, kv, max_ctx, positions):
+    got, refs = _run_case(ctx, kv, max_ctx, positions, split=True)
+    for b, ref in enumerate(refs):
+        err = float(np.max(np.abs(got[b].astype(np.float64) - ref)) / np.max(np.abs(ref)))
+        assert err <= SPLIT_REL, (b, positions[b], err)
+    print(f"split attention kv={kv} max_ctx={max_ctx}: worst rel {max(float(np.max(np.abs(got[b] - r)) / np.max(np.abs(r))) for b, r in enumerate(refs)):.2e}")
+
+
+def test_attn_decode_split_refuses_more_than_four_rows(ctx):
+    assert L.lib().zg_attn_decode_split_workspace_bytes(5, 8, 2, 2048) == 0
+    rc = L.lib().zg_attn_decode_split_device(ctx.h, 5, 8, 2, 1, 8192, 1, 1, 1e-6, 0.6, 1, 1, 1, 2048, L.BF16, 1, 1,
+                                             None)
+    assert rc == L.E_LIMIT
 
 
 def test_attn_decode_device_refusals(ctx):

@@ -57,6 +57,9 @@ _SIGS = {
     "zg_prefill": (C.c_int, [P, SZ, SZ, P, P]),
     "zg_prefill_batched": (C.c_int, [P, SZ, SZ, P, P]),
     "zg_attn_decode_workspace_bytes": (SZ, [SZ, SZ, SZ]),
+    "zg_attn_decode_split_workspace_bytes": (SZ, [SZ, SZ, SZ, SZ]),
+    "zg_attn_decode_split_device": (C.c_int, [P, SZ, SZ, SZ, P, SZ, P, P, C.c_float, C.c_float, P, P, P, SZ, C.c_int,
+                                              P, P, P]),
     "zg_attn_decode_device": (C.c_int, [P, SZ, SZ, SZ, P, SZ, P, P, C.c_float, C.c_float, P, P, P, SZ, C.c_int, P, P,
                                         P]),
     "zg_session_reset_row": (C.c_int, [P, SZ]),

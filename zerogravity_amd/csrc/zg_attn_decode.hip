@@ -579,6 +579,347 @@ hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ============================================ split-T attention (B <= 4)
+//
+// Flash-decoding form of the same layer for a few rows: workgroup (c, kv
+// head, row) takes the c-th of nc equal spans of the row's T = pos + 1
+// tokens (a multiple of 32 long), normalises and ropes the G query heads and
+// the new key as attn_decode_qk_kernel does (the workgroup whose span holds
+// the position appends K/V and uses its own rounded copies for that token),
+// scores its tokens in the 32-accumulator order, and keeps per head the
+// span's max m, l = sum of GGML exp(s - m) and o = sum of exp(s - m) * v.
+// attn_combine_kernel then forms sum_c e^(m_c - M) o_c / sum_c e^(m_c - M)
+// l_c with M = max_c m_c and applies the sigmoid gate (forward.rs:751).
+// The reference (lib.rs:1276-1387) normalises with the global max first and
+// runs the value sums as token-ordered chains: this regrouping agrees with
+// it to f32 rounding (the per-op 1e-3 bar), not bit for bit.
+constexpr int kSplitMaxSpan = 1024;  // tokens per workgroup (LDS scores)
+constexpr int kSplitMaxChunks = 256;
+
+int attn_split_chunks(size_t B, int nkv, size_t max_ctx) {
+    // ~128 workgroups for a row, and no span longer than kSplitMaxSpan
+    const size_t want = (128 + B * nkv - 1) / (B * nkv);
+    const size_t need = (max_ctx + kSplitMaxSpan - 1) / kSplitMaxSpan;
+    return (int)std::max(want, need);
+}
+
+bool attn_split_supported(size_t B, int nq, int nkv, size_t max_ctx) {
+    return B >= 1 && B <= 4 && nkv > 0 && nq % nkv == 0 && nq / nkv <= 4 &&
+           attn_split_chunks(B, nkv, max_ctx) <= kSplitMaxChunks;
+}
+
+size_t attn_split_part_bytes(size_t B, int nq, int nkv, size_t max_ctx) {
+    return B * (size_t)nq * attn_split_chunks(B, nkv, max_ctx) * (256 + 2) * sizeof(float);
+}
+
+// Partials: {m, l} per (row, head, span) at part, then o [row][head][span][256].
+template <typename KV, int G>
+__global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int nc, float* __restrict__ part) {
+    constexpr int D = 256;
+    __shared__ float hv[G + 1][D];
+    __shared__ float rsin[32], rcos[32];
+    __shared__ v4f scp[kSplitMaxSpan];  // scores, then GGML exp(s - m): [token][head]
+    __shared__ float red[2][G][4];
+    __shared__ float vrow[D];
+    const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, s = tid & 7;
+    const float* proj = a.proj + (size_t)b * a.proj_stride;
+    const int QD2 = a.nq * 2 * D;
+    // q heads (tasks 0..G-1) and the key (task G), wave w taking tasks w,
+    // w+4: their loads do not depend on the position, so they go first
+    constexpr int NR = G / 4 + 1;
+    float tv[NR][4], tg[NR][4];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int task = min(4 * i + wv, G);
+        const float* src = task < G ? proj + (size_t)(kvh * G + task) * 2 * D : proj + QD2 + (size_t)kvh * D;
+        const float* gamma = task < G ? a.qnorm : a.knorm;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            tv[i][r] = src[lane + 64 * r];
+            tg[i][r] = gamma[lane + 64 * r];
+        }
+    }
+    const float vnew = proj[QD2 + (size_t)a.nkv * D + (size_t)kvh * D + tid];
+
+    const int p = a.pos[b], T = p + 1;
+    const int cs = (((T + nc - 1) / nc) + 31) & ~31;
+    const int t0 = min(c * cs, T), t1 = min(T, t0 + cs), n = t1 - t0;
+    const size_t nrow = (size_t)gridDim.z * a.nq * nc;
+    const size_t slot = ((size_t)b * a.nq + (size_t)kvh * G) * nc + c;  // head g at slot + g * nc
+    float* ml = part;
+    float* po = part + 2 * nrow;
+    if (n <= 0) {  // an empty span: weight zero in the combine
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            if (tid == 0) {
+                ml[2 * (slot + (size_t)g * nc)] = -INFINITY;
+                ml[2 * (slot + (size_t)g * nc) + 1] = 0.0f;
+            }
+            po[(slot + (size_t)g * nc) * D + tid] = 0.0f;
+        }
+        return;
+    }
+    KV* kc = (KV*)a.kcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D;
+    KV* vc = (KV*)a.vcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D;
+    const size_t tstep = (size_t)a.nkv * D;
+    const bool owner = t0 <= p && p < t1;
+
+    // keys of a 32-token tile: token t0 + 32 i + tid / 8, 32 dims per thread
+    KVPack<KV> kn[8];
+    auto load_keys = [&](int i) {
+        const int tk = min(t0 + 32 * i + (tid >> 3), a.max_ctx - 1);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) kn[q].load(kc + (size_t)tk * tstep + 32 * q + 4 * s);
+    };
+    load_keys(0);
+    if (tid < 32) {
+        float angle = (float)p;
+        for (int t = 0; t < tid; ++t) angle *= a.theta_scale;
+        rsin[tid] = cr_sinf(angle);
+        rcos[tid] = cr_cosf(angle);
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int task = 4 * i + wv;
+        if (task <= G) {
+            double sq = 0.0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float q = tv[i][r] * tv[i][r];
+                sq += (double)q;
+            }
+            const float inv = rms_inv(wave_sum_all(sq), D, a.eps);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) hv[task][lane + 64 * r] = (tv[i][r] * inv) * tg[i][r];
+        }
+    }
+    lds_barrier();  // the angles, and each head's normalised values for its wave
+#pragma unroll
+    for (int task0 = 0; task0 <= G; task0 += 4) {
+        const int task = task0 + wv;
+        if (task <= G) {
+            head_rope(hv[task], rsin, rcos, lane);
+            // the key as the cache holds it (the same wave reads it back)
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (task == G) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const KV st = kv_st<KV>(hv[G][lane + 64 * r]);
+                    if (owner) kc[(size_t)p * tstep + lane + 64 * r] = st;
+                    hv[G][lane + 64 * r] = kv_ld<KV>(&st);
+                }
+            }
+        }
+    }
+    const KV vst = kv_st<KV>(vnew);
+    vrow[tid] = kv_ld<KV>(&vst);  // the position's value as the cache holds it
+    if (owner) vc[(size_t)p * tstep + tid] = vst;
+    lds_barrier();
+
+    // ---- scores of the span's tiles
+    const int nb = (n + 31) >> 5;
+    {
+        float qv[G][8][4];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qv[g][q][e] = hv[g][32 * q + 4 * s + e];
+        for (int i = 0; i < nb; ++i) {
+            KVPack<KV> cur[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) cur[q] = kn[q];
+            if (i + 1 < nb) load_keys(i + 1);
+            const int t = t0 + 32 * i + (tid >> 3);
+            float kk[8][4];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                if (t == p) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) kk[q][e] = hv[G][32 * q + 4 * s + e];
+                } else {
+                    cur[q].unpack(kk[q]);
+                }
+            }
+            float acc[G][4];
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[g][e] = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(qv[g][q][e], kk[q][e], acc[g][e]);
+            float dv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[g][e] = group8_tree_last(acc[g][e]);
+                dv[g] = ((acc[g][0] + acc[g][1]) + (acc[g][2] + acc[g][3])) * a.scale;
+            }
+            if (t < t1 && s == 7) scp[t - t0] = v4f{dv[0], dv[1], dv[2], dv[3]};
+        }
+    }
+    // values of a tile: wave w takes tokens t0 + 32 i + 8 w + u (u < 8), lane
+    // l channels 4l .. 4l+3; loaded while the statistics form (the first
+    // tile) or the previous tile is summed
+    KVPack<KV> vn[8];
+    auto load_values = [&](int i) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            vn[u].load(vc + (size_t)min(t0 + 32 * i + 8 * wv + u, a.max_ctx - 1) * tstep + 4 * lane);
+    };
+    load_values(0);
+    lds_barrier();
+
+    // ---- span statistics per head: m, p = GGML exp(s - m), l
+    float m[G], l[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float v = -INFINITY;
+        for (int i = tid; i < n; i += 256) v = fmaxf(v, scp[i][g]);
+        v = wave_max_all(v);
+        if (lane == 0) red[0][g][wv] = v;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int g = 0; g < G; ++g) m[g] = fmaxf(fmaxf(red[0][g][0], red[0][g][1]), fmaxf(red[0][g][2], red[0][g][3]));
+    float sum[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) sum[g] = 0.0f;
+    for (int i = tid; i < n; i += 256) {
+        const v4f e4 = scp[i];
+        float e[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            e[g] = ggml_exp(e[g] - m[g]);
+            sum[g] += e[g];
+        }
+        scp[i] = v4f{e[0], e[1], e[2], e[3]};
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float v = wave_sum_all(sum[g]);
+        if (lane == 0) red[1][g][wv] = v;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int g = 0; g < G; ++g) l[g] = (red[1][g][0] + red[1][g][1]) + (red[1][g][2] + red[1][g][3]);
+
+    // ---- o = sum of p * v over the span: per wave its tokens, then the four
+    // waves added in wave order through LDS (the score LDS, once read)
+    float o[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[g][e] = 0.0f;
+    for (int i = 0; i < nb; ++i) {
+        float cv[8][4];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            vn[u].unpack(cv[u]);
+            if (t0 + 32 * i + 8 * wv + u == p) {  // the position's own value, as stored
+#pragma unroll
+                for (int e = 0; e < 4; ++e) cv[u][e] = vrow[4 * lane + e];
+            }
+        }
+        if (i + 1 < nb) load_values(i + 1);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int tt = 32 * i + 8 * wv + u;
+            if (tt < n) {
+                const v4f pr = scp[tt];
+                const float pp[4] = {pr.x, pr.y, pr.z, pr.w};
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[g][e] = fmaf(pp[g], cv[u][e], o[g][e]);
+            }
+        }
+    }
+    lds_barrier();
+    float* ro = (float*)scp;  // [wave][head][256]
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        *(v4f*)(ro + (wv * G + g) * D + 4 * lane) = v4f{o[g][0], o[g][1], o[g][2], o[g][3]};
+    lds_barrier();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float og = (ro[g * D + tid] + ro[(G + g) * D + tid]) + (ro[(2 * G + g) * D + tid] + ro[(3 * G + g) * D + tid]);
+        if (tid == 0) {
+            ml[2 * (slot + (size_t)g * nc)] = m[g];
+            ml[2 * (slot + (size_t)g * nc) + 1] = l[g];
+        }
+        po[(slot + (size_t)g * nc) * D + tid] = og;
+    }
+}
+
+// Grid (q_heads, B): the spans' partials of one head combined, gated.
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int nc, const float* __restrict__ part) {
+    constexpr int D = 256;
+    __shared__ float w[kSplitMaxChunks];
+    __shared__ float red[2][4];
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const size_t nrow = (size_t)gridDim.y * a.nq * nc, slot = ((size_t)b * a.nq + h) * nc;
+    const float* ml = part + 2 * slot;
+    const float* po = part + 2 * nrow + slot * D + tid;
+    const float gate = a.proj[(size_t)b * a.proj_stride + (size_t)h * 2 * D + D + tid];
+    // span c's {m, l} in thread c (nc <= 256); the first 64 spans' values
+    // are requested with them
+    const float mc = tid < nc ? ml[2 * tid] : -INFINITY, lc = tid < nc ? ml[2 * tid + 1] : 0.0f;
+    float ov[64];
+#pragma unroll
+    for (int k = 0; k < 64; ++k) ov[k] = po[(size_t)min(k, nc - 1) * D];
+    float mx = wave_max_all(mc);
+    if (lane == 0) red[0][wv] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    const float wc = mc == -INFINITY ? 0.0f : cr_expf(mc - mx);
+    if (tid < nc) w[tid] = wc;
+    const float ls = wave_sum_all(wc * lc);
+    if (lane == 0) red[1][wv] = ls;
+    __syncthreads();
+    const float L = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    float o = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 64; ++k)
+        if (k < nc) o = fmaf(w[k], ov[k], o);
+    for (int c0 = 64; c0 < nc; c0 += 64) {
+#pragma unroll
+        for (int k = 0; k < 64; ++k) ov[k] = po[(size_t)min(c0 + k, nc - 1) * D];
+#pragma unroll
+        for (int k = 0; k < 64; ++k)
+            if (c0 + k < nc) o = fmaf(w[c0 + k], ov[k], o);
+    }
+    a.out[(size_t)b * a.out_stride + (size_t)h * D + tid] = (o / L) * source_sigmoid(gate);
+    if (tid == 0 && !(L >= 1.0f && L < INFINITY)) atomicOr(a.status, 8);
+}
+
+hipError_t attn_decode_split(const AttnDecodeArgs& a, size_t B, float* part, hipStream_t s) {
+    if (!attn_split_supported(B, a.nq, a.nkv, (size_t)a.max_ctx) || !part) return hipErrorInvalidValue;
+    const int G = a.nq / a.nkv, nc = attn_split_chunks(B, a.nkv, (size_t)a.max_ctx);
+    const dim3 g((unsigned)nc, (unsigned)a.nkv, (unsigned)B);
+#define ZG_SP(KV)                                                                                      \
+    switch (G) {                                                                                       \
+    case 1: hipLaunchKernelGGL((attn_split_kernel<KV, 1>), g, dim3(256), 0, s, a, nc, part); break;    \
+    case 2: hipLaunchKernelGGL((attn_split_kernel<KV, 2>), g, dim3(256), 0, s, a, nc, part); break;    \
+    case 3: hipLaunchKernelGGL((attn_split_kernel<KV, 3>), g, dim3(256), 0, s, a, nc, part); break;    \
+    default: hipLaunchKernelGGL((attn_split_kernel<KV, 4>), g, dim3(256), 0, s, a, nc, part); break;   \
+    }
+    if (a.kv_bf16) {
+        ZG_SP(uint16_t)
+    } else {
+        ZG_SP(float)
+    }
+#undef ZG_SP
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.nq, (unsigned)B), dim3(256), 0, s, a, nc, (const float*)part);
+    return hipGetLastError();
+}
+
 // ================================================== greedy + position
 
 // Greedy id per row (core/src/numerics.rs:126-140: first maximum wins,

@@ -108,6 +108,35 @@ __device__ __forceinline__ double group_sum_last(double v) {
     if (W >= 64) v += dpp_d<0x143, 0xc>(v);
     return v;
 }
+// Max over groups of W lanes complete in the last lane (lanes without a
+// source keep their own value).
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ float dpp_keep(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWMASK, 0xf, false));
+}
+template <int W>
+__device__ __forceinline__ float group_max_last(float v) {
+    if (W >= 2) v = fmaxf(v, dpp_keep<0x111>(v));
+    if (W >= 4) v = fmaxf(v, dpp_keep<0x112>(v));
+    if (W >= 8) v = fmaxf(v, dpp_keep<0x114>(v));
+    if (W >= 16) v = fmaxf(v, dpp_keep<0x118>(v));
+    if (W >= 32) v = fmaxf(v, dpp_keep<0x142, 0xa>(v));
+    if (W >= 64) v = fmaxf(v, dpp_keep<0x143, 0xc>(v));
+    return v;
+}
+// Wave totals in every lane (DPP to lane 63, then a scalar broadcast).
+__device__ __forceinline__ float wave_sum_all(float v) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(group_sum_last<64>(v)), 63));
+}
+__device__ __forceinline__ float wave_max_all(float v) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(group_max_last<64>(v)), 63));
+}
+__device__ __forceinline__ double wave_sum_all(double v) {
+    const unsigned long long u = __double_as_longlong(group_sum_last<64>(v));
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(u & 0xffffffffu), 63);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(u >> 32), 63);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
 __device__ __forceinline__ double group8_sum_all(double v) {
     v += dpp_d<0xb1>(v);
     v += dpp_d<0x4e>(v);

@@ -310,6 +310,48 @@ int zg_attn_decode_device(zg_ctx* ctx, size_t rows, size_t q_heads, size_t kv_he
     return ZG_COMPLETED;
 }
 
+size_t zg_attn_decode_split_workspace_bytes(size_t rows, size_t q_heads, size_t kv_heads, size_t max_ctx) {
+    if (rows == 0 || kv_heads == 0 || !zg::attn_split_supported(rows, (int)q_heads, (int)kv_heads, max_ctx)) return 0;
+    return zg::attn_split_part_bytes(rows, (int)q_heads, (int)kv_heads, max_ctx);
+}
+
+int zg_attn_decode_split_device(zg_ctx* ctx, size_t rows, size_t q_heads, size_t kv_heads, const float* proj,
+                                size_t proj_stride, const float* q_norm, const float* k_norm, float eps,
+                                float theta_scale, const int32_t* positions, void* kcache, void* vcache,
+                                size_t max_ctx, int kv_dtype, void* workspace, float* out, void* stream) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!proj || !q_norm || !k_norm || !positions || !kcache || !vcache || !workspace || !out || rows == 0 ||
+        rows > 65535 || kv_heads == 0 || q_heads % kv_heads || q_heads / kv_heads > 4 || max_ctx == 0 ||
+        max_ctx > (1u << 30) || proj_stride < (2 * q_heads + 2 * kv_heads) * 256 || !(eps > 0.0f) ||
+        !(theta_scale > 0.0f && theta_scale <= 1.0f) || (kv_dtype != ZG_BF16 && kv_dtype != ZG_F32))
+        return fail(ctx, ZG_E_MALFORMED, "attention decode geometry");
+    if (!zg::attn_split_supported(rows, (int)q_heads, (int)kv_heads, max_ctx))
+        return fail(ctx, ZG_E_LIMIT, "split attention offered for 1..4 rows and up to 262144 cached tokens");
+    zg::AttnDecodeArgs a;
+    a.proj = proj;
+    a.proj_stride = proj_stride;
+    a.qnorm = q_norm;
+    a.knorm = k_norm;
+    a.eps = eps;
+    a.theta_scale = theta_scale;
+    a.scale = 1.0f / 16.0f;  // 1/sqrt(256)
+    a.pos = positions;
+    a.kcache = kcache;
+    a.vcache = vcache;
+    a.cache_row_stride = max_ctx * kv_heads * 256;
+    a.kv_bf16 = kv_dtype == ZG_BF16;
+    a.out = out;
+    a.out_stride = q_heads * 256;
+    a.status = ctx->d_flag;
+    a.nq = (int)q_heads;
+    a.nkv = (int)kv_heads;
+    a.max_ctx = (int)max_ctx;
+    ZG_HIP(zg::attn_decode_split(a, rows, (float*)workspace, stream ? (hipStream_t)stream : ctx->stream));
+    return ZG_COMPLETED;
+}
+
 int zg_rope_kv(zg_ctx* ctx, const float* query, const float* key, const float* value, size_t head_width,
                size_t query_heads, size_t kv_heads, size_t rotate, size_t position, float theta_scale, float* query_out,
                float* key_out, float* value_out) {

@@ -90,6 +90,8 @@ struct zg_session {
     uint32_t *d_tokens = nullptr, *d_greedy = nullptr;
     float *x = nullptr, *y0 = nullptr, *core = nullptr, *ao = nullptr, *logits = nullptr, *scores = nullptr,
           *pmax = nullptr, *att_stats = nullptr;
+    // split-T attention partials (all-Q4_K models at 1..4 rows; null otherwise)
+    float* att_part = nullptr;
     void* xh = nullptr;  // f16 activations of the batched (B > 4) projections
     float* parts = nullptr;  // split-K partial tiles of residual projections (B > 4)
     void* xh2 = nullptr;     // the SwiGLU product in f16 tiles, down projection input (B > 4)
@@ -356,7 +358,10 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             // batched rows: the value kernel also writes o_proj's f16 tiles
             const bool tiles = B > 4 && L.out_proj->dw.type == zg::kQ4_K;
             if (tiles) a.xh = s->xh;
-            ZG_HIP(zg::attn_decode(a, B, st));
+            if (s->att_part && zg::attn_split_supported(B, a.nq, a.nkv, s->max_ctx))
+                ZG_HIP(zg::attn_decode_split(a, B, s->att_part, st));
+            else
+                ZG_HIP(zg::attn_decode(a, B, st));
             ZG_HIP(gemv(L.out_proj, zg::PRO_PLAIN, s->ao, QD, nullptr, 0, nullptr, zg::EPI_RESID, s->x, H, nullptr,
                         tiles ? s->xh : nullptr));
         }
@@ -743,6 +748,16 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     A((void**)&s->ao, B * QD * 4);
     A((void**)&s->logits, B * V * 4);
     A((void**)&s->scores, B * g.q_heads * max_context * 4);
+    if (m->all_q4k) {
+        // the projections are tolerance-bound already: attention at 1..4
+        // rows takes the split-T form; models on exact codecs keep the
+        // reference's order end to end
+        size_t bytes = 0;
+        for (size_t r = 1; r <= std::min<size_t>(B, 4); ++r)
+            if (zg::attn_split_supported(r, (int)g.q_heads, (int)g.kv_heads, max_context))
+                bytes = std::max(bytes, zg::attn_split_part_bytes(r, (int)g.q_heads, (int)g.kv_heads, max_context));
+        if (bytes) A((void**)&s->att_part, bytes);
+    }
     s->layer_slot.resize(g.layers);
     for (size_t i = 0; i < m->layers.size() && !rc; ++i) {
         if (m->layers[i].full) {
