@@ -1017,6 +1017,38 @@ hipError_t argmax_step(const float* logits, size_t V, size_t ld, size_t B, uint3
     return hipGetLastError();
 }
 
+// One row's greedy id from `parts` (max, first index) partials, then the
+// commit rule of argmax_final_kernel.
+__global__ __launch_bounds__(256) void argmax_parts_kernel(const float* __restrict__ pmax, const int* __restrict__ pidx,
+                                                           int parts, uint32_t* __restrict__ greedy,
+                                                           const int* __restrict__ status, StepCommit c) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = tid; i < parts; i += 256) argmax_merge(best, bi, pmax[i], pidx[i]);
+    for (int off = 32; off > 0; off >>= 1) argmax_merge(best, bi, __shfl_xor(best, off, 64), __shfl_xor(bi, off, 64));
+    if (lane == 0) {
+        sv[wv] = best;
+        si[wv] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 4; ++w) argmax_merge(best, bi, sv[w], si[w]);
+        greedy[0] = bi == 0x7fffffff ? 0u : (uint32_t)bi;
+        if (c.pos) commit_row(c, *status == 0, 0);
+    }
+}
+
+hipError_t argmax_final(const float* pmax, const int* pidx, int parts, uint32_t* greedy, int* status,
+                        const StepCommit* commit, hipStream_t s) {
+    if (parts <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(argmax_parts_kernel, dim3(1), dim3(256), 0, s, pmax, pidx, parts, greedy, status,
+                       commit ? *commit : StepCommit{});
+    return hipGetLastError();
+}
+
 hipError_t commit_step(const StepCommit& c, const int* status, size_t B, hipStream_t s) {
     if (B == 0 || B > 64) return hipErrorInvalidValue;
     hipLaunchKernelGGL(commit_step_kernel, dim3(1), dim3(64), 0, s, c, status, (int)B);

@@ -1,5 +1,5 @@
 // Dispatch of the fused decode GEMV (zg_fused_*.hip hold the kernels).
-#include "zg_decode_common.hpp"
+#include "zg_fused_kernels.hpp"
 
 namespace zg {
 
@@ -28,6 +28,22 @@ bool fused_gemv_supported(int type, size_t K, size_t N, int pro) {
     if (type == kQ8_0 || type == kQ4_1) return K % 32 == 0;
     if (type == kF32) return K % 4 == 0;
     return false;
+}
+
+int gemv1_greedy_parts(const DeviceWeight& w, int pro) {
+    FusedGemvArgs a;
+    a.M = 1;
+    a.K = (int)w.K;
+    a.N = (int)w.N;
+    a.pro = pro;
+    a.epi = EPI_STORE;
+    if (!fused_gemv_supported(w.type, w.K, w.N, pro) || !gemv1_fits(a, w.type)) return 0;
+    return gemv1_grid((int)w.N, EPI_STORE);
+}
+
+bool gemv1_embed_supported(const DeviceWeight& w, const DeviceWeight& emb) {
+    return emb.type == kQ4_K && emb.K == w.K && emb.N > 0 && emb.N < (1u << 31) &&
+           gemv1_greedy_parts(w, PRO_RMS) > 0;
 }
 
 hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& args, hipStream_t s) {

@@ -741,6 +741,12 @@ inline bool gemv1_fits(const FusedGemvArgs& a, int type) {
 
 template <int PRO>
 hipError_t launch_pro(const FusedGemvArgs& a, int type, hipStream_t s) {
+    if constexpr (PRO == PRO_RMS) {
+        if (a.emb_qs) {  // the activation is an embedding row (matrix-core GEMV only)
+            if (!gemv1_fits(a, type) || a.epi != EPI_STORE) return hipErrorInvalidValue;
+            return launch_gemv1_q4k<PRO_EMBED_RMS, EPI_STORE>(a, s);
+        }
+    }
     if (gemv1_fits(a, type)) {
         if (a.epi == EPI_GLU) {
             if constexpr (PRO == PRO_RMS) return launch_gemv1_q4k<PRO_RMS, EPI_GLU>(a, s);

@@ -84,15 +84,49 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
     // ---- activation loads (issued first: a wave's loads complete in order)
     const int e = 512 * w + 8 * lane;
     v4f xv[2], ov[2], gv[2];
+    if (PRO == PRO_EMBED_RMS) {
+        // the token's embedding row: the weights go first (they do not
+        // depend on the token), then this lane's 8 elements (one 8-byte
+        // half-chunk piece and the block header) and gamma
+        const uint32_t t = *a.tok;
+        load_tile(blockIdx.x);
+        const bool ok = t < (uint32_t)a.emb_rows;
+        const size_t row = ok ? t : 0;
+        const uint8_t* eq = (const uint8_t*)a.emb_qs + q4k_chunk_offset(row, e >> 6, K) + ((e & 31) >= 16 ? 256 : 0) +
+                            (e & 15);
+        const uint2 nb = *(const uint2*)eq;
+        const v4u eh = ((const v4u*)a.emb_hdr)[q4k_hdr_index(row, e >> 8, nbk)];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        xv[q] = *(const v4f*)(a.x + e + 4 * q);
-        if (PRO == PRO_RMS) ov[q] = *(const v4f*)(a.gamma + e + 4 * q);
-        if (PRO == PRO_GATED || PRO == PRO_SILU_MUL) ov[q] = *(const v4f*)(a.x2 + e + 4 * q);
-        if (PRO == PRO_GATED) gv[q] = *(const v4f*)(a.gamma + ((e + 4 * q) & (a.group - 1)));
+        for (int q = 0; q < 2; ++q) ov[q] = *(const v4f*)(a.gamma + e + 4 * q);
+        uint32_t sc, mn;
+        q4k_dev_scale_min(eh, (e & 255) >> 5, sc, mn);
+        const float d = f16_to_f32((uint16_t)(eh.x & 0xffffu)), dm = f16_to_f32((uint16_t)(eh.x >> 16));
+        const float scale = d * (float)sc, mnf = dm * (float)mn;
+        const int sh = (e >> 5) & 1 ? 4 : 0;  // the high group's elements sit in the high nibbles
+        float xe[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const uint32_t byte = ((q < 4 ? nb.x : nb.y) >> (8 * (q & 3))) & 0xffu;
+            xe[q] = ok ? scale * (float)((byte >> sh) & 15u) - mnf : 0.0f;
+        }
+        xv[0] = v4f{xe[0], xe[1], xe[2], xe[3]};
+        xv[1] = v4f{xe[4], xe[5], xe[6], xe[7]};
+        if (blockIdx.x == 0) {
+            *(v4f*)(a.x_out + e) = xv[0];
+            *(v4f*)(a.x_out + e + 4) = xv[1];
+            if (!ok && tid == 0) atomicOr(a.status, 2);
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            xv[q] = *(const v4f*)(a.x + e + 4 * q);
+            if (PRO == PRO_RMS) ov[q] = *(const v4f*)(a.gamma + e + 4 * q);
+            if (PRO == PRO_GATED || PRO == PRO_SILU_MUL) ov[q] = *(const v4f*)(a.x2 + e + 4 * q);
+            if (PRO == PRO_GATED) gv[q] = *(const v4f*)(a.gamma + ((e + 4 * q) & (a.group - 1)));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_tile(blockIdx.x);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    load_tile(blockIdx.x);
 
     // ---- prologue values b (zg_decode_common.hpp's operations, without the
     // RMS factors)
@@ -106,11 +140,11 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             float v = xe[t];
-            if (PRO == PRO_RMS || PRO == PRO_GATED) {
+            if (PRO == PRO_RMS || PRO == PRO_GATED || PRO == PRO_EMBED_RMS) {
                 const float sqr = v * v;
                 sq += (double)sqr;
             }
-            if (PRO == PRO_RMS) v = v * oe[t];
+            if (PRO == PRO_RMS || PRO == PRO_EMBED_RMS) v = v * oe[t];
             else if (PRO == PRO_GATED) v = (v * ge[t]) * ggml_silu(oe[t]);
             else if (PRO == PRO_SILU_MUL) v = oe[t] * ggml_silu(v);
             b[4 * q + t] = v;
@@ -124,7 +158,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
         for (int o = 1; o < 16; o <<= 1) hs += __shfl_xor(hs, o, 64);
         fold = rms_inv(hs, a.group, a.eps);
     }
-    if (PRO == PRO_RMS) {
+    if (PRO == PRO_RMS || PRO == PRO_EMBED_RMS) {
         const double ws = group_sum_last<64>(sq);
         if (lane == 63) ssq[w] = ws;
     }
@@ -183,6 +217,9 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
     int pb = 0;
     float inv = 1.0f;
     bool first = true;
+    float best = -INFINITY;  // greedy partial (wave 0, lanes < 16)
+    int bi = 0x7fffffff;
+    bool bad = false;
     for (int t = blockIdx.x; t < ntiles; t += gridDim.x) {
         v4i D[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
@@ -212,7 +249,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
         if (lane < 16) part[pb][w][j] = acc;
         lds_barrier();
         if (w == 0 && lane < 16) {
-            if (PRO == PRO_RMS && first) {
+            if ((PRO == PRO_RMS || PRO == PRO_EMBED_RMS) && first) {
                 double tot = 0.0;
 #pragma unroll
                 for (int q = 0; q < W; ++q) tot += ssq[q];
@@ -228,12 +265,45 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
                 if (j < 8 && o < nout) a.y[o] = up * ggml_silu(v);
             } else {
                 const int o = t * 16 + j;
-                if (o < nout) epilogue(a, 0, o, v, EPI);
+                if (o < nout) {
+                    epilogue(a, 0, o, v, EPI);
+                    if (EPI == EPI_STORE && a.amax) {
+                        bad |= !finite_f32(v);
+                        if (v > best || (v == best && o < bi)) {
+                            best = v;
+                            bi = o;
+                        }
+                    }
+                }
             }
         }
         first = false;
         pb ^= 1;
     }
+    if (EPI == EPI_STORE && a.amax && w == 0) {
+        // lanes >= 16 hold (-inf, none): the first largest value of the
+        // workgroup's outputs
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(best, off, 64);
+            const int oi = __shfl_xor(bi, off, 64);
+            if (ov > best || (ov == best && oi < bi)) {
+                best = ov;
+                bi = oi;
+            }
+        }
+        if (bad) atomicOr(a.status, 4);
+        if (lane == 0) {
+            a.amax[blockIdx.x] = best;
+            a.aidx[blockIdx.x] = bi;
+        }
+    }
+}
+
+// Workgroups of launch_gemv1_q4k for N outputs (EPI_STORE).
+inline int gemv1_grid(int nout, int epi) {
+    const int tr = epi == EPI_GLU ? 8 : 16;
+    return std::min((nout + tr - 1) / tr, 2048);
 }
 
 // Grid: one workgroup per tile up to 2048, the rest in further passes of
@@ -242,9 +312,7 @@ template <int PRO, int EPI>
 hipError_t launch_gemv1_q4k(const FusedGemvArgs& a, hipStream_t s) {
     if (a.M != 1 || a.K % 512 || a.K > kGemv1MaxK || (EPI == EPI_GLU && a.N % 2)) return hipErrorInvalidValue;
     if (PRO == PRO_GATED && a.group != 128) return hipErrorInvalidValue;
-    const int nout = EPI == EPI_GLU ? a.N / 2 : a.N;
-    const int ntiles = (nout + (EPI == EPI_GLU ? 7 : 15)) / (EPI == EPI_GLU ? 8 : 16);
-    const dim3 g((unsigned)std::min(ntiles, 2048));
+    const dim3 g((unsigned)gemv1_grid(EPI == EPI_GLU ? a.N / 2 : a.N, EPI));
 #define ZG_G1(WV) hipLaunchKernelGGL((gemv1_q4k_kernel<WV, PRO, EPI>), g, dim3(64 * WV), 0, s, a)
     switch (a.K / 512) {
     case 1: ZG_G1(1); break;

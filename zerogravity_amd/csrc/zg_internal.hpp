@@ -141,7 +141,7 @@ hipError_t fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
 //                 y[m][j] = up_j * silu(gate_j) for j < N/2 (the SwiGLU
 //                 product the down projection takes, forward.rs ffn);
 //                 batched rows write it in f16 MFMA tile order to xh_out
-enum { PRO_RMS = 0, PRO_GATED = 1, PRO_SILU_MUL = 2, PRO_PLAIN = 3 };
+enum { PRO_RMS = 0, PRO_GATED = 1, PRO_SILU_MUL = 2, PRO_PLAIN = 3, PRO_EMBED_RMS = 4 };
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_GLU = 2 };
 struct FusedGemvArgs {
     const void* qs = nullptr;  // filled from the weight
@@ -172,6 +172,21 @@ struct FusedGemvArgs {
     void* xh_out = nullptr;      // EPI_GLU, batched: f16 tiled product
     const void* xh_in = nullptr;  // batched: f16 tiled activation ready (no activation kernel)
     int xh_rows = 0;              // activation kernel: f16 row-major [M][K] instead of MFMA tiles
+    // one activation row, EPI_STORE, matrix-core GEMV: each workgroup also
+    // leaves its outputs' greedy partial (largest value, first index; a
+    // nonfinite output sets status bit 2) at amax/aidx[blockIdx.x]
+    float* amax = nullptr;
+    int* aidx = nullptr;
+    // one activation row, PRO_RMS, matrix-core GEMV: the activation is the
+    // Q4_K embedding row (emb_qs/emb_hdr, emb_rows rows of width K) of the
+    // token at *tok, dequantised in the prologue (embed_q4k_kernel's
+    // arithmetic; a token past emb_rows sets status bit 1 and reads zeros),
+    // and workgroup 0 also stores it at x_out (the residual stream)
+    const uint32_t* tok = nullptr;
+    const void* emb_qs = nullptr;
+    const void* emb_hdr = nullptr;
+    int emb_rows = 0;
+    float* x_out = nullptr;
 };
 // EPI_GLU offered for these shapes (fused path: K <= 2048 so a row group
 // holds a gate and an up row; batched path: N/2 a multiple of 32).
@@ -180,6 +195,12 @@ bool batched_glu_supported(int type, size_t K, size_t N);
 // K splits for a residual batched GEMM of this shape (1: none).
 int batched_splits(size_t N, size_t K);
 bool fused_gemv_supported(int type, size_t K, size_t N, int pro);
+// Greedy partials the one-row matrix-core GEMV leaves for this weight with
+// EPI_STORE (0 when the weight takes another kernel).
+int gemv1_greedy_parts(const DeviceWeight& w, int pro);
+// Whether a one-row PRO_RMS projection of w can take its activation from a
+// Q4_K embedding (FusedGemvArgs::tok/emb_*) in its prologue.
+bool gemv1_embed_supported(const DeviceWeight& w, const DeviceWeight& emb);
 hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& a, hipStream_t s);
 // Batched rows (M > 4, Q4_K; decode batches and prompts): the prologue
 // values rounded to f16 into `scratch` (batched_scratch_bytes), then an f16
@@ -301,6 +322,10 @@ struct StepCommit {
 };
 hipError_t argmax_step(const float* logits, size_t V, size_t ld, size_t B, uint32_t* greedy, int* status, float* pmax,
                        int* pidx, const StepCommit* commit, hipStream_t s);
+// The greedy id of one row from `parts` partials a GEMV left (gemv1
+// amax/aidx), with the same commit rule as argmax_step.
+hipError_t argmax_final(const float* pmax, const int* pidx, int parts, uint32_t* greedy, int* status,
+                        const StepCommit* commit, hipStream_t s);
 // Publish a decode step for rows [0, B) if *status == 0: positions advance
 // and each row's GDN state half flips to the draft the step wrote.
 hipError_t commit_step(const StepCommit& c, const int* status, size_t B, hipStream_t s);

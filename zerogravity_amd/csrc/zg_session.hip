@@ -253,11 +253,29 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
     const size_t H = g.hidden, F = g.ffn, V = g.vocab, W = (size_t)g.gdn_heads * g.gdn_dim;
     const size_t QD = (size_t)g.q_heads * g.head_dim;
     int pending = 0;  // splits of a residual GEMM whose partial tiles the next RMS activation adds
+    // one row: the first projection dequantises the token's embedding in its
+    // prologue (and stores it as the residual stream) instead of an embedding launch
+    const zg::DeviceWeight* first_in = m->layers.empty() || m->layers[0].in_proj.size() != 1
+                                           ? nullptr : &m->layers[0].in_proj[0].w->dw;
+    const uint32_t* embed_tok =
+        B == 1 && first_in && zg::gemv1_embed_supported(*first_in, m->embd->dw) ? tokens : nullptr;
     auto gemv = [&](zg_weight* w, int pro, const float* x, size_t ldx, const float* x2, size_t ldx2,
                     const float* gamma, int epi, float* y, size_t ldy, void* xh_out = nullptr,
-                    const void* xh_in = nullptr) {
+                    const void* xh_in = nullptr, bool greedy_parts = false) {
         zg::FusedGemvArgs f;
         f.M = (int)B;
+        if (greedy_parts) {
+            f.amax = s->pmax;
+            f.aidx = s->pidx;
+        }
+        if (embed_tok && pro == zg::PRO_RMS && x == s->x) {
+            f.tok = embed_tok;
+            f.emb_qs = m->embd->dw.qs;
+            f.emb_hdr = m->embd->dw.hdr;
+            f.emb_rows = (int)m->embd->dw.N;
+            f.x_out = s->x;
+            embed_tok = nullptr;
+        }
         f.pro = pro;
         f.epi = epi;
         f.x = x;
@@ -295,7 +313,7 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
         }
         return zg::fused_gemv(w->dw, f, st);
     };
-    ZG_HIP(zg::embed(m->embd->dw, tokens, s->x, B, s->d_status, st));
+    if (!embed_tok) ZG_HIP(zg::embed(m->embd->dw, tokens, s->x, B, s->d_status, st));
     for (size_t i = 0; i < m->layers.size(); ++i) {
         LayerW& L = m->layers[i];
         const int slot = s->layer_slot[i];
@@ -388,9 +406,16 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
     sc.cur = s->d_cur;
     if (logits || greedy) {
         float* lg = logits ? logits : s->logits;
-        ZG_HIP(gemv(m->embd, zg::PRO_RMS, s->x, H, nullptr, 0, m->out_norm, zg::EPI_STORE, lg, V));
+        // one row: the LM head's workgroups leave the greedy partials
+        const int parts = B == 1 && greedy ? zg::gemv1_greedy_parts(m->embd->dw, zg::PRO_RMS) : 0;
+        ZG_HIP(gemv(m->embd, zg::PRO_RMS, s->x, H, nullptr, 0, m->out_norm, zg::EPI_STORE, lg, V, nullptr, nullptr,
+                    parts > 0));
         if (greedy) {
-            ZG_HIP(zg::argmax_step(lg, V, V, B, greedy, s->d_status, s->pmax, s->pidx, commit ? &sc : nullptr, st));
+            if (parts > 0)
+                ZG_HIP(zg::argmax_final(s->pmax, s->pidx, parts, greedy, s->d_status, commit ? &sc : nullptr, st));
+            else
+                ZG_HIP(zg::argmax_step(lg, V, V, B, greedy, s->d_status, s->pmax, s->pidx, commit ? &sc : nullptr,
+                                       st));
             return ZG_COMPLETED;
         }
     }
@@ -736,12 +761,14 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     A((void**)&s->d_tokens, B * 4);
     A((void**)&s->d_greedy, B * 4);
     A((void**)&s->tickets, B * 4);
-    A((void**)&s->pmax, zg::argmax_partials(B) * 4);
+    // greedy partials: argmax_step's, or one per workgroup of the one-row LM head
+    const size_t nparts = std::max<size_t>(zg::argmax_partials(B), 2048);
+    A((void**)&s->pmax, nparts * 4);
     A((void**)&s->att_stats, B * g.q_heads * 2 * 4);
     A(&s->xh, zg::batched_scratch_bytes(B, std::max({H, F, W, QD})));
     if (B > 4) A((void**)&s->parts, 8 * ((B + 31) / 32 * 32) * H * sizeof(float));
     if (B > 4) A(&s->xh2, zg::batched_scratch_bytes(B, F));
-    A((void**)&s->pidx, zg::argmax_partials(B) * 4);
+    A((void**)&s->pidx, nparts * 4);
     A((void**)&s->x, B * H * 4);
     A((void**)&s->y0, B * s->y0w * 4);
     A((void**)&s->core, B * W * 4);
