@@ -220,8 +220,8 @@ int zg_attn_decode_device(zg_ctx* ctx, size_t rows, size_t q_heads, size_t kv_he
                           const int32_t* positions, void* kcache, void* vcache, size_t max_ctx, int kv_dtype,
                           void* workspace, float* out, void* stream);
 
-/* The same attention layer in split-T form for 1..4 rows, as the decode
- * step of an all-Q4_K model runs it: each of ~128 workgroups scores one span
+/* The same attention layer in split-T form for 1..64 rows, as the decode
+ * step of an all-Q4_K model runs it: each of ~128 or more workgroups scores one span
  * of a row's tokens and keeps the span's max, sum of exp and exp-weighted
  * values; a second launch combines the spans and applies the gate.  The
  * operations are the reference's regrouped (no counterpart in the reference:
@@ -229,7 +229,7 @@ int zg_attn_decode_device(zg_ctx* ctx, size_t rows, size_t q_heads, size_t kv_he
  * output agrees to f32 rounding rather than bit for bit; K/V are appended
  * exactly as above.  Same arguments, with a workspace of
  * zg_attn_decode_split_workspace_bytes(rows, q_heads, kv_heads, max_ctx)
- * bytes; ZG_E_LIMIT beyond 4 rows or beyond 262144 cached tokens. */
+ * bytes; ZG_E_LIMIT beyond 64 rows or beyond 262144 cached tokens. */
 size_t zg_attn_decode_split_workspace_bytes(size_t rows, size_t q_heads, size_t kv_heads, size_t max_ctx);
 int zg_attn_decode_split_device(zg_ctx* ctx, size_t rows, size_t q_heads, size_t kv_heads, const float* proj,
                                 size_t proj_stride, const float* q_norm, const float* k_norm, float eps,

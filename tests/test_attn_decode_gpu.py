@@ -128,7 +128,7 @@ def test_attn_decode_device_matches_oracle(ctx, kv, max_ctx, positions):
         assert np.array_equal(got[b].view(np.uint32), ref.view(np.uint32)), (b, float(np.abs(got[b] - ref).max()))
 
 
-# The split-T form (1..4 rows): spans of T / chunks tokens, the owner of the
+# The split-T form (1..64 rows): spans of T / chunks tokens, the owner of the
 # position among them; spans of one token block and of many, the position at
 # a span's first and last token, an empty tail of spans (T below the chunk
 # count), caches up to 8192 rows.  The output is held to the per-op bar,
@@ -144,6 +144,9 @@ SPLIT_REL = 1e-3
     (L.BF16, 8192, [8191, 4100, 1023]),
     (L.F32, 8192, [6000]),
     (L.BF16, 300, [299, 150]),
+    (L.BF16, 4096, [int(p) for p in np.linspace(0, 4095, 8)]),
+    (L.BF16, 2304, [int(p) for p in np.linspace(17, 2303, 32)]),
+    (L.F32, 8192, LONG32),
 ])
 def test_attn_decode_split_matches_oracle(ctx, kv, max_ctx, positions):
     got, refs = _run_case(ctx, kv, max_ctx, positions, split=True)
@@ -153,9 +156,9 @@ def test_attn_decode_split_matches_oracle(ctx, kv, max_ctx, positions):
     print(f"split attention kv={kv} max_ctx={max_ctx}: worst rel {max(float(np.max(np.abs(got[b] - r)) / np.max(np.abs(r))) for b, r in enumerate(refs)):.2e}")
 
 
-def test_attn_decode_split_refuses_more_than_four_rows(ctx):
-    assert L.lib().zg_attn_decode_split_workspace_bytes(5, 8, 2, 2048) == 0
-    rc = L.lib().zg_attn_decode_split_device(ctx.h, 5, 8, 2, 1, 8192, 1, 1, 1e-6, 0.6, 1, 1, 1, 2048, L.BF16, 1, 1,
+def test_attn_decode_split_refuses_more_than_64_rows(ctx):
+    assert L.lib().zg_attn_decode_split_workspace_bytes(65, 8, 2, 2048) == 0
+    rc = L.lib().zg_attn_decode_split_device(ctx.h, 65, 8, 2, 1, 8192, 1, 1, 1e-6, 0.6, 1, 1, 1, 2048, L.BF16, 1, 1,
                                              None)
     assert rc == L.E_LIMIT
 

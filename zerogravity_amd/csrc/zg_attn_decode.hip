@@ -597,14 +597,16 @@ constexpr int kSplitMaxSpan = 1024;  // tokens per workgroup (LDS scores)
 constexpr int kSplitMaxChunks = 256;
 
 int attn_split_chunks(size_t B, int nkv, size_t max_ctx) {
-    // ~128 workgroups for a row, and no span longer than kSplitMaxSpan
-    const size_t want = (128 + B * nkv - 1) / (B * nkv);
+    // ~128 workgroups for up to 4 rows (short spans: the workgroup's fixed
+    // latency dominates), ~1024 for more (several waves of workgroups per
+    // CU hide each span's load latency), and no span beyond kSplitMaxSpan
+    const size_t want = ((B <= 4 ? 128 : 1024) + B * nkv - 1) / (B * nkv);
     const size_t need = (max_ctx + kSplitMaxSpan - 1) / kSplitMaxSpan;
     return (int)std::max(want, need);
 }
 
 bool attn_split_supported(size_t B, int nq, int nkv, size_t max_ctx) {
-    return B >= 1 && B <= 4 && nkv > 0 && nq % nkv == 0 && nq / nkv <= 4 &&
+    return B >= 1 && B <= 64 && nkv > 0 && nq % nkv == 0 && nq / nkv <= 4 &&
            attn_split_chunks(B, nkv, max_ctx) <= kSplitMaxChunks;
 }
 
@@ -895,8 +897,16 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int
         for (int k = 0; k < 64; ++k)
             if (c0 + k < nc) o = fmaf(w[c0 + k], ov[k], o);
     }
-    a.out[(size_t)b * a.out_stride + (size_t)h * D + tid] = (o / L) * source_sigmoid(gate);
+    const float v = (o / L) * source_sigmoid(gate);
+    a.out[(size_t)b * a.out_stride + (size_t)h * D + tid] = v;
     if (tid == 0 && !(L >= 1.0f && L < INFINITY)) atomicOr(a.status, 8);
+    if (a.xh) {  // batched rows: also the output projection's f16 A tiles (act16_kernel's layout)
+        const int k = h * D + tid, m = b, K = a.nq * D;
+        const size_t lane_t = (size_t)((k & 15) >> 3) * 32 + (m & 31);
+        const size_t at = ((((size_t)(m >> 5) * (K >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + lane_t) * 8 + (k & 7);
+        if (a.status && !(fabsf(v) <= 65504.0f)) atomicOr(a.status, 16);
+        ((_Float16*)a.xh)[at] = (_Float16)v;
+    }
 }
 
 hipError_t attn_decode_split(const AttnDecodeArgs& a, size_t B, float* part, hipStream_t s) {

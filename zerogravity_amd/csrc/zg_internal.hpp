@@ -269,10 +269,10 @@ struct AttnDecodeArgs {
     void* xh = nullptr;
 };
 hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s);
-// Split-T form for 1..4 rows (attn_split_kernel + attn_combine_kernel):
+// Split-T form for 1..64 rows (attn_split_kernel + attn_combine_kernel):
 // per-span partials in `part` (attn_split_part_bytes), then the combine
-// into out; the same operations regrouped, within f32 rounding of the
-// reference's order.  No xh tiles (the rows' projections are the fused ones).
+// into out (and the xh tiles when set); the same operations regrouped,
+// within f32 rounding of the reference's order.
 bool attn_split_supported(size_t B, int nq, int nkv, size_t max_ctx);
 size_t attn_split_part_bytes(size_t B, int nq, int nkv, size_t max_ctx);
 hipError_t attn_decode_split(const AttnDecodeArgs& a, size_t B, float* part, hipStream_t s);

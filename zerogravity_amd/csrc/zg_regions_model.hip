@@ -328,7 +328,7 @@ int zg_attn_decode_split_device(zg_ctx* ctx, size_t rows, size_t q_heads, size_t
         !(theta_scale > 0.0f && theta_scale <= 1.0f) || (kv_dtype != ZG_BF16 && kv_dtype != ZG_F32))
         return fail(ctx, ZG_E_MALFORMED, "attention decode geometry");
     if (!zg::attn_split_supported(rows, (int)q_heads, (int)kv_heads, max_ctx))
-        return fail(ctx, ZG_E_LIMIT, "split attention offered for 1..4 rows and up to 262144 cached tokens");
+        return fail(ctx, ZG_E_LIMIT, "split attention offered for 1..64 rows and up to 262144 cached tokens");
     zg::AttnDecodeArgs a;
     a.proj = proj;
     a.proj_stride = proj_stride;

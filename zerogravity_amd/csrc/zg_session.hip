@@ -776,11 +776,11 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     A((void**)&s->logits, B * V * 4);
     A((void**)&s->scores, B * g.q_heads * max_context * 4);
     if (m->all_q4k) {
-        // the projections are tolerance-bound already: attention at 1..4
-        // rows takes the split-T form; models on exact codecs keep the
-        // reference's order end to end
+        // the projections are tolerance-bound already: attention takes the
+        // split-T form; models on exact codecs keep the reference's order
+        // end to end
         size_t bytes = 0;
-        for (size_t r = 1; r <= std::min<size_t>(B, 4); ++r)
+        for (size_t r = 1; r <= B; ++r)
             if (zg::attn_split_supported(r, (int)g.q_heads, (int)g.kv_heads, max_context))
                 bytes = std::max(bytes, zg::attn_split_part_bytes(r, (int)g.q_heads, (int)g.kv_heads, max_context));
         if (bytes) A((void**)&s->att_part, bytes);
