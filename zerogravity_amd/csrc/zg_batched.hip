@@ -133,9 +133,26 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
     // order through LDS, so the result does not depend on timing.
     typedef _Float16 h2v __attribute__((ext_vector_type(2)));
     __shared__ float red[KS][16][64];
+    __shared__ float inv_s[32];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, hsel = lane >> 5, r32 = lane & 31;
     const int m0 = blockIdx.y * 32;
     const int K = a.K, N = a.N, nbk = K >> 8;
+    // an RMS projection on tiles a residual projection left (rms_ss_in):
+    // its per-tile sums of squares for the 32 rows are requested now (TPR
+    // adjacent threads per row, 8 each) and reduced after the main loop
+    constexpr int TPR = KS >= 8 ? 16 : 8;
+    const int srow = threadIdx.x / TPR, ssub = threadIdx.x % TPR;
+    double ssv[8];
+    if (a.rms_ss_in) {
+        const int n = a.rms_ss_n;
+        const double* ss = a.rms_ss_in + (size_t)(m0 + min(srow, 31)) * n;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int c = ssub + q * TPR;
+            const double x = ss[min(c, n - 1)];
+            ssv[q] = c < n && srow < 32 ? x : 0.0;
+        }
+    }
     bool nv[NT];
     int nbase[NT];
     const v4u* qtile[NT];
@@ -208,6 +225,13 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
             }
         }
     }
+    if (a.rms_ss_in) {  // (rms_ss_n <= 8 * TPR; the first barrier below orders inv_s)
+        double tot = 0.0;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) tot += ssv[q];
+        tot = group_sum_last<TPR>(tot);
+        if (srow < 32 && ssub == TPR - 1) inv_s[srow] = rms_inv(tot, K, a.eps);
+    }
     float vg[16 / KS];  // EPI_GLU: the gate tile's sums
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -226,6 +250,33 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
                     ((red[4][r][lane] + red[5][r][lane]) + (red[6][r][lane] + red[7][r][lane]));
             }
             const int m = m0 + (r & 3) + 8 * (r >> 2) + 4 * hsel;
+            if (a.rms_ss_in) v *= inv_s[m - m0];
+            if (EPI == EPI_RESID && a.rms_tiles_out) {
+                // the residual finished here, then the next RMS projection's
+                // A tile element (m, n): f16(x_new * gamma) (its 1/rms is
+                // applied after its dot), and this tile's f64 sum of the f32
+                // squares of x_new per row (lanes of one half share a row)
+                const int n = nbase[t] + r32;
+                const bool live = nv[t] && m < a.M;
+                float xn = 0.0f;
+                if (live) {
+                    float* p = a.y + (size_t)m * a.ldy + n;
+                    xn = *p + v;  // source_binary Add, lib.rs:1258-1271
+                    *p = xn;
+                    if (!finite_f32(xn)) atomicOr(a.status, 1);
+                }
+                if (nv[t]) {
+                    const float tv = live ? xn * a.rms_gamma[n] : 0.0f;
+                    if (!(fabsf(tv) <= 65504.0f)) atomicOr(a.status, 16);
+                    const size_t at = ((((size_t)(m >> 5) * (N >> 8) + (n >> 8)) * 16 + ((n & 255) >> 4)) * 64 +
+                                       ((n & 15) >> 3) * 32 + (m & 31)) * 8 + (n & 7);
+                    a.rms_tiles_out[at] = (_Float16)tv;
+                }
+                const float sq = xn * xn;
+                const double tot = group_sum_last<32>((double)sq);
+                if (r32 == 31 && nbase[t] < N) a.rms_ss_out[(size_t)m * (N >> 5) + (nbase[t] >> 5)] = tot;
+                continue;
+            }
             if (EPI == EPI_GLU) {
                 if (t == 0) {
                     vg[i] = v;
@@ -337,9 +388,12 @@ hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* 
         default: return hipErrorInvalidValue;
         }
     }
+    if ((a.rms_tiles_out || a.rms_ss_in) && a.splits > 1) return hipErrorInvalidValue;
+    if (a.rms_ss_in && a.rms_ss_n > 64) return hipErrorInvalidValue;  // 8 sums per thread, 8+ threads per row
     // prompt-sized M: the register-blocked GEMM (zg_gemm.hip)
     const bool no_split = !(a.epi == EPI_RESID && a.splits > 1 && a.parts);
-    if (a.M >= kGemmRows && no_split && prompt_gemm_supported(w.type, w.K, w.N, a.epi))
+    if (a.M >= kGemmRows && no_split && !a.rms_tiles_out && !a.rms_ss_in &&
+        prompt_gemm_supported(w.type, w.K, w.N, a.epi))
         return prompt_gemm(w, args, xh, s);
     if (a.epi == EPI_GLU) {
         if (!batched_glu_supported(w.type, w.K, w.N) || !a.xh_out) return hipErrorInvalidValue;

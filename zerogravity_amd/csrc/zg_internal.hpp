@@ -169,6 +169,18 @@ struct FusedGemvArgs {
     const float* rparts = nullptr;
     int rsplits = 0;
     float* xw = nullptr;
+    // batched rows, a residual projection without splits: with
+    // rms_tiles_out it also leaves the next RMS projection's input -- f16
+    // (x_new * rms_gamma) in MFMA A-tile order for K = N, and per row and
+    // 32-column tile the f64 sum of the f32 squares of x_new at
+    // rms_ss_out[m][N/32].  That RMS projection passes the tiles as xh_in
+    // and the sums as rms_ss_in (rms_ss_n per row) and scales each row's
+    // outputs by 1/rms (RMSNorm's factor moved past the dot).
+    _Float16* rms_tiles_out = nullptr;
+    const float* rms_gamma = nullptr;
+    double* rms_ss_out = nullptr;
+    const double* rms_ss_in = nullptr;
+    int rms_ss_n = 0;
     void* xh_out = nullptr;      // EPI_GLU, batched: f16 tiled product
     const void* xh_in = nullptr;  // batched: f16 tiled activation ready (no activation kernel)
     int xh_rows = 0;              // activation kernel: f16 row-major [M][K] instead of MFMA tiles

@@ -94,6 +94,8 @@ struct zg_session {
     float* att_part = nullptr;
     void* xh = nullptr;  // f16 activations of the batched (B > 4) projections
     float* parts = nullptr;  // split-K partial tiles of residual projections (B > 4)
+    void* xh3 = nullptr;     // the stream's RMS input tiles a residual projection leaves (B > 4)
+    double* rss = nullptr;   // and their per-tile sums of squares [rows][hidden/32]
     void* xh2 = nullptr;     // the SwiGLU product in f16 tiles, down projection input (B > 4)
     size_t y0w = 0;
     std::vector<float*> ring, rec;  // per GDN layer: conv ring [B][3W][4], state [B][2][H][128][128]
@@ -253,6 +255,10 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
     const size_t H = g.hidden, F = g.ffn, V = g.vocab, W = (size_t)g.gdn_heads * g.gdn_dim;
     const size_t QD = (size_t)g.q_heads * g.head_dim;
     int pending = 0;  // splits of a residual GEMM whose partial tiles the next RMS activation adds
+    // batched rows: a residual projection (K <= 2048, no splits) left the
+    // next RMS projection's f16 tiles (xh3) and per-tile sums of squares
+    // (rss) of the current stream
+    bool rms_ready = false;
     // one row: the first projection dequantises the token's embedding in its
     // prologue (and stores it as the residual stream) instead of an embedding launch
     const zg::DeviceWeight* first_in = m->layers.empty() || m->layers[0].in_proj.size() != 1
@@ -261,7 +267,7 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
         B == 1 && first_in && zg::gemv1_embed_supported(*first_in, m->embd->dw) ? tokens : nullptr;
     auto gemv = [&](zg_weight* w, int pro, const float* x, size_t ldx, const float* x2, size_t ldx2,
                     const float* gamma, int epi, float* y, size_t ldy, void* xh_out = nullptr,
-                    const void* xh_in = nullptr, bool greedy_parts = false) {
+                    const void* xh_in = nullptr, bool greedy_parts = false, const float* gamma_next = nullptr) {
         zg::FusedGemvArgs f;
         f.M = (int)B;
         if (greedy_parts) {
@@ -300,17 +306,32 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
                 f.rsplits = pending;
                 f.xw = s->x;
                 pending = 0;
+            } else if (rms_ready && pro == zg::PRO_RMS && x == s->x) {
+                f.xh_in = s->xh3;  // the stream's tiles and sums of squares
+                f.rms_ss_in = s->rss;
+                f.rms_ss_n = (int)(H / 32);
             }
             if (epi == zg::EPI_RESID && y == s->x && m->all_q4k) {
-                const int sp = zg::batched_splits(w->dw.N, w->dw.K);
-                if (sp > 1) {
+                // a short K reads its 32 activation rows quickly: no splits,
+                // and the next RMS projection's input in the epilogue; a long
+                // K splits (the next RMS activation launch adds the parts)
+                rms_ready = gamma_next && w->dw.K <= 2048 && H <= 2048 && H % 256 == 0 && ldy == H;
+                const int sp = rms_ready ? 1 : zg::batched_splits(w->dw.N, w->dw.K);
+                if (rms_ready) {
+                    f.rms_tiles_out = (_Float16*)s->xh3;
+                    f.rms_gamma = gamma_next;
+                    f.rms_ss_out = s->rss;
+                } else if (sp > 1) {
                     f.parts = s->parts;
                     f.splits = sp;
                     pending = sp;
                 }
+            } else if (epi == zg::EPI_RESID && y == s->x) {
+                rms_ready = false;
             }
             return zg::batched_gemv(w->dw, f, s->xh, st);
         }
+        if (epi == zg::EPI_RESID && y == s->x) rms_ready = false;
         return zg::fused_gemv(w->dw, f, st);
     };
     if (!embed_tok) ZG_HIP(zg::embed(m->embd->dw, tokens, s->x, B, s->d_status, st));
@@ -348,7 +369,7 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             ZG_HIP(zg::gdn_decode(d, B, st));
             // gated RMSNorm (ssm_norm) * silu(z) -> ssm_out -> residual
             ZG_HIP(gemv(L.out_proj, zg::PRO_GATED, s->core, W, s->y0 + 3 * W, s->y0w, L.ssm_norm, zg::EPI_RESID, s->x,
-                        H, nullptr, tiles ? s->xh : nullptr));
+                        H, nullptr, tiles ? s->xh : nullptr, false, L.post_norm));
         } else {
             zg::AttnDecodeArgs a;
             a.proj = s->y0;
@@ -381,7 +402,7 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             else
                 ZG_HIP(zg::attn_decode(a, B, st));
             ZG_HIP(gemv(L.out_proj, zg::PRO_PLAIN, s->ao, QD, nullptr, 0, nullptr, zg::EPI_RESID, s->x, H, nullptr,
-                        tiles ? s->xh : nullptr));
+                        tiles ? s->xh : nullptr, false, L.post_norm));
         }
         const zg::DeviceWeight& gu = L.ffn_gu[0].w->dw;
         const bool glu = L.ffn_gu.size() == 1 && L.ffn_down->dw.type == zg::kQ4_K &&
@@ -767,6 +788,8 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     A((void**)&s->att_stats, B * g.q_heads * 2 * 4);
     A(&s->xh, zg::batched_scratch_bytes(B, std::max({H, F, W, QD})));
     if (B > 4) A((void**)&s->parts, 8 * ((B + 31) / 32 * 32) * H * sizeof(float));
+    if (B > 4) A(&s->xh3, zg::batched_scratch_bytes(B, H));
+    if (B > 4) A((void**)&s->rss, (B + 31) / 32 * 32 * ((H + 31) / 32) * sizeof(double));
     if (B > 4) A(&s->xh2, zg::batched_scratch_bytes(B, F));
     A((void**)&s->pidx, nparts * 4);
     A((void**)&s->x, B * H * 4);
