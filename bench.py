@@ -53,6 +53,33 @@ def host_threads():
     return max(1, min(n, int(env))) if env and env.isdigit() else n
 
 
+def cpu_model():
+    """The host CPU's model string (first "model name" of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# How the oracle computes a Q4_K projection row, which sets its CPU cost: the
+# reference's dot_row rule (crates/zerogravity-cpu/src/source.rs:431-459).
+Q4K_CPU_RULE = ("Q4_K rows by the reference's dot_row rule: serial f32 sum of (q*scale - min)*x per "
+                "element, no FMA, rows spread over OpenMP threads")
+
+
+def cpu_base(value, unit, cores, sample, digits=3, rule=None):
+    """The cpu_baseline object: the C oracle timed on this host's cores."""
+    out = {"value": round(value, digits), "unit": unit, "cores": cores, "kind": "port",
+           "sample": sample, "cpu": cpu_model()}
+    if rule:
+        out["rule"] = rule
+    return out
+
+
 def gemv_bytes(kind, N, K, M):
     """Algorithmic bytes of one GEMV launch: weights once, bf16 activation
     rows in, f32 outputs out."""
@@ -150,11 +177,12 @@ def run_decode(model, torch, B, prefix, steps, warmup, seed):
 
 
 def gemv_leg(kern, torch, g, tensors, kind, reps):
-    """The dominant kernel: the Q4_K dequant-GEMV launches of one B=1 decode
-    step -- the same stacked matrices and the same fused kernel (activation
-    prologue in-kernel, f32 activation, RMSNorm) -- replayed `reps` times
-    with HIP events around each replay.  ~0.95 GB per replay, so nothing is
-    served from the 256 MB Infinity Cache."""
+    """The dominant kernel: the Q4_K GEMV launches of one B=1 decode step --
+    the same stacked matrices through the same one-row kernel
+    (gemv1_q4k_kernel: RMSNorm prologue in-kernel on an f32 activation, int8
+    matrix cores) -- replayed `reps` times with HIP events around each
+    replay.  ~0.95 GB per replay, so nothing is served from the 256 MB
+    Infinity Cache."""
     from zerogravity_amd import _lib as L
     lib, ctx = L.lib(), kern.ctx
     handles = []
@@ -367,6 +395,11 @@ def bench_decode(args):
         "value": round(res[1]["tok_s"], 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(res[1]["ms_per_step"], 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "q4_k weights, f32 accumulate",
+        "dtype_detail": {"b1": "Q4_K codes and int16-coded activations (per-row amax, split into two signed "
+                               "bytes) on int8 MFMA, i32 partials scaled and summed in f32",
+                         "b32": "Q4_K weights dequantised to f16 tiles, f16 activations, f16 MFMA with f32 "
+                                "accumulate",
+                         "state": "f32 GDN state and accumulators, bf16 KV cache"},
         "data": "synthetic (seeded random-init Q4_K GGUF weights, random prefix state)",
         "config": {"workload": "2B-shaped Q4_K continuous-batch greedy decode", "prefix": prefix,
                    "kv_cache": "bf16", "b1": res[1], "b32": res[32],
@@ -374,13 +407,12 @@ def bench_decode(args):
                    "attention_decode_leg": attn},
         "roofline": {"bound": "hbm", "achieved": round(leg["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(leg["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "fused_q4k_kernel (the B=1 decode step's stacked projections, one launch each)",
+                     "kernel": "gemv1_q4k_kernel (the B=1 decode step's 97 stacked Q4_K projections, one launch each, RMSNorm/gate prologue and residual/SwiGLU epilogue fused)",
                      "bytes_per_launch": round(leg["bytes_per_launch"]), "us_per_launch": round(leg["us_per_launch"], 3)},
     }
     if not args.no_cpu:
         v, cores, sample = cpu_decode_baseline(g, tensors, prefix, args.cpu_seconds)
-        line["cpu_baseline"] = {"value": round(v, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-                                "sample": sample}
+        line["cpu_baseline"] = cpu_base(v, "tok/s", cores, sample, 3, rule=Q4K_CPU_RULE)
     kern.ctx.close()
     return line
 
@@ -524,8 +556,7 @@ def bench_gemv(args):
     }
     if not args.no_cpu:
         v, cores, sample = cpu_gemv_baseline(Q4_K, 151936, 2048, args.cpu_seconds)
-        line["cpu_baseline"] = {"value": round(v, 2), "unit": "GB/s", "cores": cores, "kind": "port",
-                                "sample": sample}
+        line["cpu_baseline"] = cpu_base(v, "GB/s", cores, sample, 2, rule=Q4K_CPU_RULE)
     kern.ctx.close()
     return line
 
@@ -630,8 +661,7 @@ def bench_prefill(args):
     }
     if not args.no_cpu:
         v, cores, sample = cpu_prefill_baseline(2048, H, args.cpu_seconds)
-        line["cpu_baseline"] = {"value": round(v, 2), "unit": "tok/s", "cores": cores, "kind": "port",
-                                "sample": sample}
+        line["cpu_baseline"] = cpu_base(v, "tok/s", cores, sample, 2)
     ctx.close()
     return line
 
@@ -715,8 +745,7 @@ def bench_model_prefill(args):
     }
     if not args.no_cpu:
         v, cores, sample = cpu_model_prefill_baseline(g, tensors, args.cpu_seconds)
-        line["cpu_baseline"] = {"value": round(v, 2), "unit": "tok/s", "cores": cores, "kind": "port",
-                                "sample": sample}
+        line["cpu_baseline"] = cpu_base(v, "tok/s", cores, sample, 2, rule=Q4K_CPU_RULE)
     kern.ctx.close()
     return line
 
@@ -841,8 +870,7 @@ def bench_gdn(args):
     }
     if not args.no_cpu:
         v, cores, sample = cpu_gdn_baseline(min(args.cpu_seconds, 10.0))
-        line["cpu_baseline"] = {"value": round(v, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-                                "sample": sample}
+        line["cpu_baseline"] = cpu_base(v, "GB/s", cores, sample, 3)
     ctx.close()
     return line
 
@@ -895,8 +923,7 @@ def bench_config1(args):
             if time.perf_counter() - t0 > args.cpu_seconds:
                 break
         dt = time.perf_counter() - t0
-        line["cpu_baseline"] = {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-                                "sample": f"{n} prompt tokens of the same request through the oracle"}
+        line["cpu_baseline"] = cpu_base(n / dt, "tok/s", threads, f"{n} prompt tokens of the same request through the oracle", 3)
     kern.ctx.close()
     return line
 
