@@ -189,10 +189,13 @@ int zg_gdn_decode_device(zg_ctx* ctx, size_t rows, size_t heads, const float* pr
  * row, the kernel the decode step uses above 4 rows): the same core and
  * state, plus ssm_out's activation -- the gated RMSNorm of each head's core
  * with gamma norm[128], times silu(z) (forward.rs:586-594) -- rounded to f16
- * into `tiles` in the batched projections' MFMA A-operand order: element
- * (row m, channel k) at f16 index ((((m/32)*(W/256) + k/256)*16 + (k%256)/16)
- * *64 + ((k%16)/8)*32 + m%32)*8 + k%8, W = heads*128, rows padded to 32
- * (zg_gdn_decode_tiles_bytes).  heads even. */
+ * into `tiles` in the batched projections' MFMA A-operand order, W =
+ * heads*128, rows padded to 32 (zg_gdn_decode_tiles_bytes).  With rows < 256
+ * and W a multiple of 1024 up to 6144 (the 16-row decode kernel's layout),
+ * element (row m, channel k) is at f16 index ((((m/16)*(W/128) + k/128)*4 +
+ * 2*((k/32)%2) + (k/8)%2)*64 + m%16 + 16*((k/16)%2 + 2*((k/64)%2)))*8 + k%8;
+ * otherwise at ((((m/32)*(W/256) + k/256)*16 + (k%256)/16)*64 +
+ * ((k%16)/8)*32 + m%32)*8 + k%8.  heads even. */
 size_t zg_gdn_decode_tiles_bytes(size_t rows, size_t heads);
 int zg_gdn_decode_gated_device(zg_ctx* ctx, size_t rows, size_t heads, const float* proj, size_t proj_stride,
                                const float* conv_w, float* ring, const int32_t* positions, const float* dt,

@@ -134,9 +134,15 @@ def _oracle_gdn_row(proj, conv_w, hist, state, dt, a, H, eps):
 
 
 def _tile_index(B, W):
-    """f16 index of (row m, channel k) in the batched projections' A tiles."""
+    """f16 index of (row m, channel k) in the batched projections' A tiles:
+    the 16-row decode kernel's layout for B < 256 rows and W a multiple of
+    1024 up to 6144, else the 32-row layout (include/zg_hip.h)."""
     m = np.arange(B)[:, None]
     k = np.arange(W)[None, :]
+    if B < 256 and W % 1024 == 0 and W <= 6144:
+        op = 2 * ((k >> 5) & 1) + ((k >> 3) & 1)
+        lane = (m & 15) + 16 * (((k >> 4) & 1) + 2 * ((k >> 6) & 1))
+        return ((((m >> 4) * (W >> 7) + (k >> 7)) * 4 + op) * 64 + lane) * 8 + (k & 7)
     lane = ((k & 15) >> 3) * 32 + (m & 31)
     return ((((m >> 5) * (W >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + lane) * 8 + (k & 7)
 

@@ -3,7 +3,7 @@ results as zg_gemv_device, bit for bit, on two calls in a row (the second
 with a smaller input, so the static scratch holds the first call's larger
 contents), for every codec path: bf16 input through the prepared
 activation, f32 input through the in-kernel prologue (up to 4 rows) and
-through the f16 MFMA tiles (Q4_K beyond 4 rows).  No counterpart in the
+through the f16 MFMA kernels (Q4_K beyond 4 rows).  No counterpart in the
 reference: the entry exists for callers that cannot allocate."""
 import numpy as np
 import pytest
@@ -71,7 +71,22 @@ def test_noalloc_limits(kern):
     g = torch.ones(K, dtype=torch.float32, device="cuda")
     rc = L.lib().zg_gemv_device_noalloc(kern.ctx.h, h.h, x.data_ptr(), L.F32, 65, g.data_ptr(), 1e-6, y.data_ptr(), None)
     assert rc == L.E_LIMIT
-    # Q4_K beyond 4 rows before any zg_gemv_device call built the weight's tiles
-    rc = L.lib().zg_gemv_device_noalloc(kern.ctx.h, h.h, x.data_ptr(), L.F32, 8, g.data_ptr(), 1e-6, y.data_ptr(), None)
+    # Q4_K beyond 4 rows on the 32-row kernel (K = 1536) before any
+    # zg_gemv_device call built the weight's 32-row tiles
+    K2 = 1536
+    w2 = synth.random_matrix(rng, synth.Q4_K, N, K2)
+    h2 = kern.register(951, "noalloc.limits.k1536", synth.Q4_K, K2, N, w2.reshape(-1))
+    x2 = torch.zeros((8, K2), dtype=torch.float32, device="cuda")
+    g2 = torch.ones(K2, dtype=torch.float32, device="cuda")
+    rc = L.lib().zg_gemv_device_noalloc(kern.ctx.h, h2.h, x2.data_ptr(), L.F32, 8, g2.data_ptr(), 1e-6, y.data_ptr(),
+                                        None)
     assert rc == L.E_STATE
     assert "tile layout" in kern.ctx.error()
+    # the 16-row kernel (K = 2048) reads the weight's own layout: no tiles needed
+    xr = torch.from_numpy(rng.standard_normal((8, K)).astype(np.float32)).cuda()
+    got = _run(kern, "zg_gemv_device_noalloc", h, xr, L.F32, 8, g, torch.empty((8, N), device="cuda"))
+    want = torch.empty((8, N), device="cuda")
+    kern.ctx.check(L.lib().zg_gemv_device(kern.ctx.h, h.h, xr.data_ptr(), L.F32, 8, g.data_ptr(), 1e-6, want.data_ptr(),
+                                          None))
+    torch.cuda.synchronize()
+    assert np.array_equal(got.view(np.uint32), want.cpu().numpy().view(np.uint32))

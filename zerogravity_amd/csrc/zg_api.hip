@@ -479,7 +479,8 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
         f.ldy = w->dw.N;
         f.status = ctx->d_flag;
         if (m_rows > 4 && w->dw.type == zg::kQ4_K) {
-            if (!w->dw.qs_t) {
+            // the 32-row weight tiles, unless the 16-row kernel takes this shape
+            if (!w->dw.qs_t && !zg::batched16_supported(m_rows, w->dw.K, w->dw.N, zg::EPI_STORE)) {
                 ZG_HIP(hipStreamSynchronize(s));
                 ZG_HIP(zg::ensure_mfma_tiles(const_cast<zg_weight*>(w)->dw, s));
             }
@@ -533,7 +534,7 @@ int zg_gemv_device_noalloc(zg_ctx* ctx, const zg_weight* w, const void* x, int x
         f.ldy = w->dw.N;
         f.status = ctx->d_flag;
         if (m_rows > 4 && w->dw.type == zg::kQ4_K) {
-            if (!w->dw.qs_t)
+            if (!w->dw.qs_t && !zg::batched16_supported(m_rows, w->dw.K, w->dw.N, zg::EPI_STORE))
                 return fail(ctx, ZG_E_STATE,
                             "weight has no batched tile layout yet: a zg_gemv_device call with more than 4 rows builds it");
             if (zg::batched_scratch_bytes(m_rows, w->dw.K) > kStaticScratchBytes)

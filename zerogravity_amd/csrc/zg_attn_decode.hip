@@ -524,8 +524,7 @@ __global__ __launch_bounds__(256) void attn_decode_pv_kernel(AttnDecodeArgs a) {
         a.out[(size_t)b * a.out_stride + (size_t)(h0 + g) * D + cgx * CB + c] = v;
         if (a.xh) {
             const int k = (h0 + g) * D + cgx * CB + c, m = b, K = a.nq * D;
-            const size_t lane_t = (size_t)((k & 15) >> 3) * 32 + (m & 31);
-            const size_t at = ((((size_t)(m >> 5) * (K >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + lane_t) * 8 + (k & 7);
+            const size_t at = xh_tile_index(m, k, K, gridDim.z);  // B rows = gridDim.z
             if (a.status && !(fabsf(v) <= 65504.0f)) atomicOr(a.status, 16);
             ((_Float16*)a.xh)[at] = (_Float16)v;
         }
@@ -598,9 +597,11 @@ constexpr int kSplitMaxChunks = 256;
 
 int attn_split_chunks(size_t B, int nkv, size_t max_ctx) {
     // ~128 workgroups for up to 4 rows (short spans: the workgroup's fixed
-    // latency dominates), ~1024 for more (several waves of workgroups per
-    // CU hide each span's load latency), and no span beyond kSplitMaxSpan
-    const size_t want = ((B <= 4 ? 128 : 1024) + B * nkv - 1) / (B * nkv);
+    // latency dominates), ~512 for more (measured at 5-64 rows and 2049
+    // cached tokens: each workgroup's prologue -- projections, norms, RoPE --
+    // costs more than a longer span, beyond two workgroups per CU), and no
+    // span beyond kSplitMaxSpan
+    const size_t want = ((B <= 4 ? 128 : 512) + B * nkv - 1) / (B * nkv);
     const size_t need = (max_ctx + kSplitMaxSpan - 1) / kSplitMaxSpan;
     return (int)std::max(want, need);
 }
@@ -900,10 +901,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int
     const float v = (o / L) * source_sigmoid(gate);
     a.out[(size_t)b * a.out_stride + (size_t)h * D + tid] = v;
     if (tid == 0 && !(L >= 1.0f && L < INFINITY)) atomicOr(a.status, 8);
-    if (a.xh) {  // batched rows: also the output projection's f16 A tiles (act16_kernel's layout)
+    if (a.xh) {  // batched rows: also the output projection's f16 A tiles
         const int k = h * D + tid, m = b, K = a.nq * D;
-        const size_t lane_t = (size_t)((k & 15) >> 3) * 32 + (m & 31);
-        const size_t at = ((((size_t)(m >> 5) * (K >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + lane_t) * 8 + (k & 7);
+        const size_t at = xh_tile_index(m, k, K, gridDim.y);  // B rows = gridDim.y
         if (a.status && !(fabsf(v) <= 65504.0f)) atomicOr(a.status, 16);
         ((_Float16*)a.xh)[at] = (_Float16)v;
     }

@@ -9,11 +9,10 @@ typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
 // One workgroup per activation row (rows M..Mpad-1 zero): the prologue
-// values of wg_prologue, rounded once to f16, into xh in the MFMA A-operand
-// order of 32-row tiles: element (m, k) of tile mt = m/32 sits at
-// ((mt*(K/256) + k/256)*16 + (k%256)/16)*64 + (k%16)/8*32 + m%32, times 8,
-// plus k%8, so that lane l of the MFMA kernel loads step s of its K block
-// as 16 contiguous bytes and a wave-instruction reads 1 KB contiguous.
+// values of wg_prologue, rounded once to f16, into xh in the A-operand order
+// of the kernel that consumes them (xh_tile_index: 16-row tiles for decode
+// batches, else 32-row tiles), so that each lane of the MFMA kernel loads 16
+// contiguous bytes and a wave-instruction reads 1 KB contiguous.
 template <int PRO, int JMAX>
 __global__ __launch_bounds__(256) void act16_kernel(FusedGemvArgs a, _Float16* __restrict__ xh) {
     __shared__ double red[4];
@@ -100,10 +99,7 @@ __global__ __launch_bounds__(256) void act16_kernel(FusedGemvArgs a, _Float16* _
                 // past the f16 range: status bit 4 (the f32 paths carry it)
                 if (a.status && valid && !(fabsf(e[t]) <= 65504.0f)) atomicOr(a.status, 16);
             }
-            const size_t lane_t = (size_t)((k & 15) >> 3) * 32 + (m & 31);
-            const size_t at = a.xh_rows ? (size_t)m * K + k
-                                        : ((((size_t)(m >> 5) * (K >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 +
-                                           lane_t) * 8 + (k & 7);
+            const size_t at = a.xh_rows ? (size_t)m * K + k : xh_tile_index(m, k, K, a.M);
             *(h4v*)(xh + at) = hv4;
         }
     }
@@ -268,9 +264,7 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
                 if (nv[t]) {
                     const float tv = live ? xn * a.rms_gamma[n] : 0.0f;
                     if (!(fabsf(tv) <= 65504.0f)) atomicOr(a.status, 16);
-                    const size_t at = ((((size_t)(m >> 5) * (N >> 8) + (n >> 8)) * 16 + ((n & 255) >> 4)) * 64 +
-                                       ((n & 15) >> 3) * 32 + (m & 31)) * 8 + (n & 7);
-                    a.rms_tiles_out[at] = (_Float16)tv;
+                    a.rms_tiles_out[xh_tile_index(m, n, N, a.M)] = (_Float16)tv;
                 }
                 const float sq = xn * xn;
                 const double tot = group_sum_last<32>((double)sq);
@@ -283,12 +277,10 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
                 } else if (nv[t]) {
                     // up * silu(gate), rounded to f16 into the down
                     // projection's activation tiles (K2 = N/2 columns)
-                    const int j = nbase[0] + r32, nbk2 = (N >> 1) >> 8;
-                    const size_t at = ((((size_t)(m >> 5) * nbk2 + (j >> 8)) * 16 + ((j & 255) >> 4)) * 64 +
-                                       ((j & 15) >> 3) * 32 + (m & 31)) * 8 + (j & 7);
+                    const int j = nbase[0] + r32;
                     const float pr = m < a.M ? v * ggml_silu(vg[i]) : 0.0f;
                     if (a.status && !(fabsf(pr) <= 65504.0f)) atomicOr(a.status, 16);
-                    ((_Float16*)a.xh_out)[at] = (_Float16)pr;
+                    ((_Float16*)a.xh_out)[xh_tile_index(m, j, N >> 1, a.M)] = (_Float16)pr;
                 }
             } else if (gridDim.z > 1) {
                 if (nv[t]) a.parts[((size_t)blockIdx.z * 32 * gridDim.y + m) * N + nbase[t] + r32] = v;
@@ -298,6 +290,340 @@ __global__ __launch_bounds__(64 * KS) void mfma_q4k_kernel(FusedGemvArgs a, cons
         }
         __syncthreads();
     }
+}
+
+// ====================================== decode batches: Q4_K 16-row tiles
+//
+// Y[m][n] = sum_k X[m][k] W[n][k] for a decode batch (M < kGemmRows, K a
+// multiple of 1024 up to 6144) on v_mfma_f32_16x16x32_f16, reading the
+// weights in their Q4_K 16-row tile layout (q4k_chunk_offset) directly.
+//
+// Rows n are dealt to the workgroups in balanced runs of 16-row tiles,
+// 16 MBW activation rows per workgroup (blockIdx.y), about 256 workgroups in
+// all (one per CU).  Every CU must take in its whole 16 MBW x K activation
+// block besides its share of the weights, so the CUs stream evenly and all
+// of a workgroup's loads are issued before its first product; with few
+// tiles (N/16 <= 256) a workgroup takes one 16-row half (MBW = 1): twice the
+// workgroups, each taking in half the activations, and the two halves of a
+// tile, gridDim.x workgroups apart, run on one XCD (dispatch deals
+// workgroups to the 8 XCDs in turn), where the second read of the weights
+// can hit L2.  Eight waves split K: wave w holds the A operands of units
+// [w*UPW, (w+1)*UPW) (a unit is 128 columns) for its row halves in
+// registers and multiplies them with every tile of its run.  For a unit, lane l of the weight operand
+// takes the 16-byte piece (row l%16, half h = (l/16)&1, run 2u + l/32) of
+// the 1 KB unit block (one contiguous wave load); its low and high nibbles,
+// bytes 0-7 and 8-15, give the four 8-element B operands i = 2 nib + sub,
+// dequantised on packed f16 as the 32-row kernel does (the nibble q becomes
+// 1024 + q by a byte permute, 1024 is subtracted exactly, w = fma(q, scale,
+// -min) with the group's scale and min rounded once to f16).  The A
+// operands hold the same columns in the same lanes (xh16_index).  D
+// register r of lane l is (m = 4 (l/16) + r, n = l%16).  The eight waves'
+// partial tiles are summed in wave order through LDS.
+//
+// SwiGLU (EPI_GLU): a tile is 8 gate rows j and their 8 up rows N/2 + j
+// (lanes l%16 < 8 and >= 8), so each output pairs lanes l and l ^ 8.
+// Residual (EPI_RESID) with rms_tiles_out: as the 32-row kernel, with the
+// sums of squares per 16-column tile (rms_ss_out[m][N/16]).
+// TMAX tiles per pass.  LOOP 0: one pass; 1: passes over a longer run,
+// each pass's weights requested after the previous pass; 2 (UPW <= 2): the
+// next pass's weights requested before the current pass is multiplied.
+constexpr int kM16Waves = 8;
+// Tiles per pass that keep a wave's operands in registers (512 threads:
+// 256 registers a lane); the A operands weigh UPW * MBW.
+constexpr int m16_tiles_per_pass(int upw, int loop, int mbw) {
+    const int ue = (upw * mbw + 1) / 2;
+    return ue >= 5 || (loop == 1 && ue >= 3) ? 1 : (ue == 4 ? 2 : 3);
+}
+
+template <int EPI, int UPW, int LOOP, int MBW>
+__global__ __launch_bounds__(64 * kM16Waves) __attribute__((amdgpu_waves_per_eu(2, 2))) void mfma16_q4k_kernel(
+    FusedGemvArgs a, const h8v* __restrict__ xh) {
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    constexpr int KW = kM16Waves, VR = EPI == EPI_GLU ? 8 : 16;
+    constexpr int TMAX = m16_tiles_per_pass(UPW, LOOP, MBW);
+    // block headers: one per block when a wave's units pair into blocks
+    // (UPW even: units 2b, 2b+1 of block b), else one per unit
+    constexpr int NH = UPW % 2 == 0 ? UPW / 2 : UPW;
+    static_assert(MBW * TMAX <= KW, "a finishing wave per (tile, row half)");
+    __shared__ v4f red[KW][MBW * TMAX][64];
+    __shared__ float inv_s[16 * MBW];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, L = lane >> 4, r16 = lane & 15;
+    const int K = a.K, N = a.N, nunits = K >> 7, nbk = K >> 8;
+    const int nout = EPI == EPI_GLU ? N >> 1 : N, nvt = (nout + VR - 1) / VR;
+    const int t0 = (int)((long long)blockIdx.x * nvt / gridDim.x);
+    const int t1 = (int)((long long)(blockIdx.x + 1) * nvt / gridDim.x);
+    const int m0 = 16 * MBW * blockIdx.y, ub = w * UPW, h = L & 1, cp = L >> 1;
+    const uint8_t* qs = (const uint8_t*)a.qs;
+    const v4u* hdr = (const v4u*)a.hdr;
+
+    // ---- loads, in the order of use: the producer's per-tile sums of
+    // squares (TPR threads per row, SSV each: 128 per row at most), the A
+    // operands, the weights
+    constexpr int TPR = 32 / MBW, SSV = 4 * MBW;
+    double ssv[SSV];
+    const int srow = tid / TPR, ssub = tid % TPR;
+    auto reduce_ss = [&]() {  // (the first barrier of a pass orders inv_s)
+        double tot = 0.0;
+#pragma unroll
+        for (int q = 0; q < SSV; ++q) tot += ssv[q];
+        tot = group_sum_last<TPR>(tot);
+        if (ssub == TPR - 1) inv_s[srow] = rms_inv(tot, K, a.eps);
+    };
+    if (a.rms_ss_in) {
+        const int n = a.rms_ss_n;
+        const double* ss = a.rms_ss_in + (size_t)(m0 + srow) * n;
+#pragma unroll
+        for (int q = 0; q < SSV; ++q) {
+            const int c = ssub + TPR * q;
+            const double x = ss[min(c, n - 1)];
+            ssv[q] = c < n ? x : 0.0;
+        }
+        if (UPW * MBW >= 10) reduce_ss();  // wide units: before the main loads hold their registers
+    }
+    h8v xa[UPW][MBW][4];
+#pragma unroll
+    for (int u = 0; u < UPW; ++u)
+#pragma unroll
+        for (int mb = 0; mb < MBW; ++mb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                xa[u][mb][i] = xh[(((size_t)(MBW * blockIdx.y + mb) * nunits + ub + u) * 4 + i) * 64 + lane];
+    auto wrow = [&](int vt) {
+        if (EPI == EPI_GLU) {
+            const int j = min(vt * 8 + (r16 & 7), nout - 1);
+            return r16 < 8 ? j : nout + j;
+        }
+        return vt * 16 + r16;  // < 16 * nvt: inside the zero-padded last tile
+    };
+    auto issue = [&](v4u (&wq)[UPW][TMAX], v4u (&hd)[NH][TMAX], int tb) {
+#pragma unroll
+        for (int t = 0; t < TMAX; ++t) {
+            if (tb + t < t1) {
+                const int row = wrow(tb + t);
+                const size_t tile = (size_t)(row >> 4);
+#pragma unroll
+                for (int u = 0; u < UPW; ++u) {
+                    if (NH == UPW || u % 2 == 0)
+                        hd[NH == UPW ? u : u / 2][t] = hdr[(tile * nbk + ((ub + u) >> 1)) * 16 + (row & 15)];
+                    wq[u][t] = *(const v4u*)(qs + ((tile * nunits + ub + u) * 64 + (row & 15) + 16 * h + 32 * cp) * 16);
+                }
+            }
+        }
+    };
+    // a residual projection's own outputs, requested up front: wave w adds
+    // into (tile t0 + w/MBW, row half w%MBW) -- the single-pass shapes
+    float yv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, gn = 0.0f;
+    const bool ypre = EPI == EPI_RESID && LOOP == 0 && w < MBW * min(TMAX, t1 - t0);
+    if (ypre) {
+        const int n = (t0 + w / MBW) * 16 + r16;
+        if (n < N) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + 16 * (w % MBW) + 4 * L + r;
+                if (m < a.M) yv[r] = a.y[(size_t)m * a.ldy + n];
+            }
+            if (a.rms_tiles_out) gn = a.rms_gamma[n];
+        }
+    }
+    v4u wA[UPW][TMAX], hA[NH][TMAX];
+    issue(wA, hA, t0);
+    __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before the first product
+
+    if (a.rms_ss_in && UPW * MBW < 10) reduce_ss();
+
+    const h2v bias = h2v{(_Float16)1024.0f, (_Float16)1024.0f};
+    auto pass = [&](const v4u (&wq)[UPW][TMAX], const v4u (&hd)[NH][TMAX], int tb) {
+        const int ntb = min(TMAX, t1 - tb);
+        v4f acc[TMAX][MBW];
+#pragma unroll
+        for (int t = 0; t < TMAX; ++t)
+#pragma unroll
+            for (int mb = 0; mb < MBW; ++mb) acc[t][mb] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < UPW; ++u) {
+            const int gl = 2 * (2 * ((ub + u) & 1) + cp);  // low-nibble group of the lane's run in its block
+#pragma unroll
+            for (int t = 0; t < TMAX; ++t) {
+                if (t < ntb) {
+                    const v4u hh = hd[NH == UPW ? u : u / 2][t];
+                    const float d = f16_to_f32((uint16_t)(hh.x & 0xffffu));
+                    const float dm = f16_to_f32((uint16_t)(hh.x >> 16));
+                    h2v sc2[2], nm2[2];
+#pragma unroll
+                    for (int nib = 0; nib < 2; ++nib) {
+                        uint32_t sc, mn;
+                        q4k_dev_scale_min(hh, gl + nib, sc, mn);
+                        const _Float16 sh = (_Float16)(d * (float)sc), mh = (_Float16)(dm * (float)mn);
+                        sc2[nib] = h2v{sh, sh};
+                        nm2[nib] = h2v{-mh, -mh};
+                    }
+                    const v4u q = wq[u][t];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int nib = i >> 1, sub = i & 1;
+                        const uint32_t d0 = sub ? q.z : q.x, d1 = sub ? q.w : q.y;
+                        const uint32_t w0 = (nib ? (d0 >> 4) : d0) & 0x0f0f0f0fu;
+                        const uint32_t w1 = (nib ? (d1 >> 4) : d1) & 0x0f0f0f0fu;
+                        // bytes (q, 0x64) pairs: the f16 bit patterns of 1024 + q
+                        const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u);
+                        const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u);
+                        const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u);
+                        const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u);
+                        const h2v e0 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p0) - bias, sc2[nib], nm2[nib]);
+                        const h2v e1 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p1) - bias, sc2[nib], nm2[nib]);
+                        const h2v e2 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p2) - bias, sc2[nib], nm2[nib]);
+                        const h2v e3 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p3) - bias, sc2[nib], nm2[nib]);
+                        const h8v wb = h8v{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
+#pragma unroll
+                        for (int mb = 0; mb < MBW; ++mb)
+                            acc[t][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[u][mb][i], wb, acc[t][mb], 0, 0, 0);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TMAX; ++t)
+#pragma unroll
+            for (int mb = 0; mb < MBW; ++mb) red[w][MBW * t + mb][lane] = acc[t][mb];
+        __syncthreads();
+        // wave w finishes (tile t = w/MBW, row half w%MBW)
+        if (w < MBW * ntb) {
+            v4f v = red[0][w][lane];
+#pragma unroll
+            for (int q = 1; q < KW; ++q) v = v + red[q][w][lane];
+            const int vt = tb + w / MBW, mh = 16 * (w % MBW);
+            float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (a.rms_ss_in) vv[r] *= inv_s[mh + 4 * L + r];
+            if (EPI == EPI_GLU) {
+                const int j = vt * 8 + (r16 & 7);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float up = __shfl_xor(vv[r], 8, 16);  // the up row's sum (lane l ^ 8)
+                    const int m = m0 + mh + 4 * L + r;
+                    if (r16 < 8 && j < nout) {
+                        // up * silu(gate), rounded to f16 into the down
+                        // projection's activation tiles (K2 = N/2 columns)
+                        const float pr = m < a.M ? up * ggml_silu(vv[r]) : 0.0f;
+                        if (a.status && !(fabsf(pr) <= 65504.0f)) atomicOr(a.status, 16);
+                        ((_Float16*)a.xh_out)[xh_tile_index(m, j, nout, a.M)] = (_Float16)pr;
+                    }
+                }
+            } else if (EPI == EPI_RESID) {
+                const int n = vt * 16 + r16;
+                const bool nv = n < N;
+                float g = gn;
+                if (!ypre && nv && a.rms_tiles_out) g = a.rms_gamma[n];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = m0 + mh + 4 * L + r;
+                    const bool live = nv && m < a.M;
+                    float xn = 0.0f;
+                    if (live) {
+                        float* p = a.y + (size_t)m * a.ldy + n;
+                        xn = (ypre ? yv[r] : *p) + vv[r];  // source_binary Add, lib.rs:1258-1271
+                        *p = xn;
+                        if (!finite_f32(xn)) atomicOr(a.status, 1);
+                    }
+                    if (a.rms_tiles_out) {
+                        // the next RMS projection's A tile element (m, n):
+                        // f16(x_new * gamma) (its 1/rms is applied after its
+                        // dot), and this 16-column tile's f64 sum of the f32
+                        // squares of x_new (the 16 lanes of a row)
+                        if (nv) {
+                            const float tv = live ? xn * g : 0.0f;
+                            if (!(fabsf(tv) <= 65504.0f)) atomicOr(a.status, 16);
+                            a.rms_tiles_out[xh_tile_index(m, n, N, a.M)] = (_Float16)tv;
+                        }
+                        const float sq = xn * xn;
+                        const double tot = group_sum_last<16>((double)sq);
+                        if (r16 == 15) a.rms_ss_out[(size_t)m * (N >> 4) + vt] = tot;
+                    }
+                }
+            } else {
+                const int n = vt * 16 + r16;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = m0 + mh + 4 * L + r;
+                    if (n < N && m < a.M) a.y[(size_t)m * a.ldy + n] = vv[r];
+                }
+            }
+        }
+        __syncthreads();
+    };
+    if constexpr (LOOP == 0) {
+        pass(wA, hA, t0);
+    } else if constexpr (LOOP == 1) {
+        for (int tb = t0; tb < t1; tb += TMAX) {
+            if (tb > t0) {
+                issue(wA, hA, tb);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            pass(wA, hA, tb);
+        }
+    } else {
+        static_assert(LOOP != 2 || UPW <= 2, "two weight buffers fit the registers up to UPW = 2");
+        v4u wB[UPW][TMAX], hB[NH][TMAX];
+        for (int tb = t0; tb < t1; tb += 2 * TMAX) {
+            const int tb2 = tb + TMAX;
+            issue(wB, hB, tb2);
+            __builtin_amdgcn_sched_barrier(0);
+            pass(wA, hA, tb);
+            if (tb2 >= t1) break;
+            issue(wA, hA, tb2 + TMAX);
+            __builtin_amdgcn_sched_barrier(0);
+            pass(wB, hB, tb2);
+        }
+    }
+}
+
+bool batched16_supported(size_t M, size_t K, size_t N, int epi) {
+    // every shape of the 16-row layout: producers write it whenever
+    // xh16_layout(M, K) holds, so this kernel must take them all
+    if (!xh16_layout(M, K) || N == 0 || N > (1u << 30)) return false;
+    return epi != EPI_GLU || (N % 16 == 0 && (N / 2) % 128 == 0);
+}
+
+template <int EPI, int MBW>
+static hipError_t launch_mfma16_m(const FusedGemvArgs& a, const _Float16* xh, hipStream_t s) {
+    const int upw = a.K / 1024, nout = EPI == EPI_GLU ? a.N / 2 : a.N, vr = EPI == EPI_GLU ? 8 : 16;
+    const int gy = (a.M + 16 * MBW - 1) / (16 * MBW);
+    const int nvt = (nout + vr - 1) / vr, G = std::min(nvt, std::max(1, 256 / gy)), per = (nvt + G - 1) / G;
+    const int loop = per <= m16_tiles_per_pass(upw, 0, MBW) ? 0 : (upw <= 2 ? 2 : 1);
+    const dim3 g((unsigned)G, (unsigned)gy);
+    const h8v* x = (const h8v*)xh;
+#define ZG_M16(U)                                                                                                  \
+    case U:                                                                                                        \
+        if (loop == 0) {                                                                                           \
+            hipLaunchKernelGGL((mfma16_q4k_kernel<EPI, U, 0, MBW>), g, dim3(64 * kM16Waves), 0, s, a, x);          \
+        } else if (loop == 1) {                                                                                    \
+            hipLaunchKernelGGL((mfma16_q4k_kernel<EPI, U, 1, MBW>), g, dim3(64 * kM16Waves), 0, s, a, x);          \
+        } else {                                                                                                   \
+            if constexpr (U <= 2)                                                                                  \
+                hipLaunchKernelGGL((mfma16_q4k_kernel<EPI, U, 2, MBW>), g, dim3(64 * kM16Waves), 0, s, a, x);      \
+        }                                                                                                          \
+        break;
+    switch (upw) {
+        ZG_M16(1)
+        ZG_M16(2)
+        ZG_M16(3)
+        ZG_M16(4)
+        ZG_M16(5)
+        ZG_M16(6)
+    default: return hipErrorInvalidValue;
+    }
+#undef ZG_M16
+    return hipGetLastError();
+}
+
+// One 16-row half per workgroup when the rows are few (M <= 16) or the
+// tiles are (N/16 <= 256: the whole-block workgroups would leave CUs idle).
+template <int EPI>
+static hipError_t launch_mfma16(const FusedGemvArgs& a, const _Float16* xh, hipStream_t s) {
+    const int nvt = EPI == EPI_GLU ? (a.N / 2 + 7) / 8 : (a.N + 15) / 16;
+    if (a.M <= 16 || nvt <= 256) return launch_mfma16_m<EPI, 1>(a, xh, s);
+    return launch_mfma16_m<EPI, 2>(a, xh, s);
 }
 
 size_t batched_scratch_bytes(size_t M, size_t K) { return ((M + 31) / 32) * 32 * K * 2; }
@@ -369,12 +695,18 @@ static void launch_act16(const FusedGemvArgs& a, int mpad, _Float16* xh, hipStre
 hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* scratch, hipStream_t s) {
     if (w.type != kQ4_K || w.K % 256 || w.K > 8192 || args.M <= 0 || args.M > 65535 * 32) return hipErrorInvalidValue;
     if (args.pro == PRO_GATED && args.group != 128) return hipErrorInvalidValue;
-    if (!w.qs_t || !w.hdr_t) return hipErrorNotReady;  // ensure_mfma_tiles first
+    const bool m16 = batched16_supported((size_t)args.M, w.K, w.N, args.epi);
+    if (!m16 && (!w.qs_t || !w.hdr_t)) return hipErrorNotReady;  // ensure_mfma_tiles first
     FusedGemvArgs a = args;
-    a.qs = w.qs_t;
-    a.hdr = w.hdr_t;
+    a.qs = m16 ? w.qs : w.qs_t;  // the 16-row kernel reads the Q4_K tile layout itself
+    a.hdr = m16 ? w.hdr : w.hdr_t;
     a.K = (int)w.K;
     a.N = (int)w.N;
+    if (m16) {  // no split-K; the sums of squares fit 8 per thread
+        if ((a.epi == EPI_RESID && a.splits > 1 && a.parts) || (a.rms_ss_in && a.rms_ss_n > 128) ||
+            (a.rms_tiles_out && (a.epi != EPI_RESID || a.N % 128)) || (a.epi == EPI_GLU && !a.xh_out))
+            return hipErrorInvalidValue;
+    }
     const int mpad = (a.M + 31) / 32 * 32;
     _Float16* xh = (_Float16*)scratch;
     if (a.xh_in) {
@@ -386,6 +718,13 @@ hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* 
         case PRO_SILU_MUL: launch_act16<PRO_SILU_MUL>(a, mpad, xh, s); break;
         case PRO_PLAIN: launch_act16<PRO_PLAIN>(a, mpad, xh, s); break;
         default: return hipErrorInvalidValue;
+        }
+    }
+    if (m16) {
+        switch (a.epi) {
+        case EPI_GLU: return launch_mfma16<EPI_GLU>(a, xh, s);
+        case EPI_RESID: return launch_mfma16<EPI_RESID>(a, xh, s);
+        default: return launch_mfma16<EPI_STORE>(a, xh, s);
         }
     }
     if ((a.rms_tiles_out || a.rms_ss_in) && a.splits > 1) return hipErrorInvalidValue;

@@ -200,8 +200,7 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
                 hv4[i] = (_Float16)y;
             }
             const int k = h * D + 4 * t, m = b;
-            const size_t lane_t = (size_t)((k & 15) >> 3) * 32 + (m & 31);
-            const size_t at = ((((size_t)(m >> 5) * (W >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + lane_t) * 8 + (k & 7);
+            const size_t at = xh_tile_index(m, k, W, gridDim.y);  // B rows = gridDim.y; 4 columns in one 8-run
             if (threadIdx.x < 32) *(h4v*)((_Float16*)a.xh + at) = hv4;
         }
     }

@@ -48,6 +48,34 @@ hipError_t dequantize_rows(const DeviceWeight& w, size_t row0, size_t rows, floa
 // GEMM (zg_gemm.hip) instead of the decode-shaped MFMA kernel.
 constexpr int kGemmRows = 256;
 
+// f16 activation tiles of the batched GEMMs, element (m, k) for K columns.
+// 32-row layout (the prompt GEMM and the 32-row decode kernel): lane l of a
+// v_mfma_f32_32x32x16_f16 A operand loads 16 contiguous bytes.
+__host__ __device__ inline size_t xh32_index(size_t m, size_t k, size_t K) {
+    return ((((m >> 5) * (K >> 8) + (k >> 8)) * 16 + ((k & 255) >> 4)) * 64 + ((k & 15) >> 3) * 32 + (m & 31)) * 8 +
+           (k & 7);
+}
+// 16-row layout (the decode kernel on Q4_K 16-row tiles): per 16 rows mb and
+// 128-column unit u, four 1 KB v_mfma_f32_16x16x32_f16 A operands i; lane
+// (m % 16) + 16 (h + 2 cp) of operand i = 2 nib + sub holds the 8 columns
+// whose weights the same lane of the weight operand dequantises from the
+// Q4_K tile layout: run 2u + cp of the row, bytes 16 h + 8 sub .. + 7, low
+// (nib 0) or high (nib 1) nibbles, i.e. k = 128 u + 64 cp + 32 nib + 16 h +
+// 8 sub + e.
+__host__ __device__ inline size_t xh16_index(size_t m, size_t k, size_t K) {
+    const size_t u = k >> 7, cp = (k >> 6) & 1, nib = (k >> 5) & 1, h = (k >> 4) & 1, sub = (k >> 3) & 1;
+    return ((((m >> 4) * (K >> 7) + u) * 4 + 2 * nib + sub) * 64 + (m & 15) + 16 * (h + 2 * cp)) * 8 + (k & 7);
+}
+// Decode-sized batches (M < kGemmRows) whose K is a multiple of 1024 up to
+// 6144 run the 16-row kernel, so their activations use the 16-row layout;
+// every producer of batched activation tiles picks the layout with this.
+__host__ __device__ inline bool xh16_layout(size_t M, size_t K) {
+    return M < (size_t)kGemmRows && K % 1024 == 0 && K <= 6144;
+}
+__host__ __device__ inline size_t xh_tile_index(size_t m, size_t k, size_t K, size_t M) {
+    return xh16_layout(M, K) ? xh16_index(m, k, K) : xh32_index(m, k, K);
+}
+
 // Activation preparation for M rows of width K: optional RMSNorm with gamma
 // (f64 sum of f32 squares, f32 mean, 1/sqrtf, (x*inv)*gamma), then any of:
 // f32 output (xf); the dynamic Q8_0 coding (aq codes, ad f16-rounded
@@ -171,11 +199,12 @@ struct FusedGemvArgs {
     float* xw = nullptr;
     // batched rows, a residual projection without splits: with
     // rms_tiles_out it also leaves the next RMS projection's input -- f16
-    // (x_new * rms_gamma) in MFMA A-tile order for K = N, and per row and
-    // 32-column tile the f64 sum of the f32 squares of x_new at
-    // rms_ss_out[m][N/32].  That RMS projection passes the tiles as xh_in
-    // and the sums as rms_ss_in (rms_ss_n per row) and scales each row's
-    // outputs by 1/rms (RMSNorm's factor moved past the dot).
+    // (x_new * rms_gamma) in MFMA A-tile order for K = N (xh_tile_index),
+    // and per row and 32-column tile (16-column on the 16-row kernel) the
+    // f64 sum of the f32 squares of x_new at rms_ss_out[m][N/32 or N/16].
+    // That RMS projection passes the tiles as xh_in and the sums as
+    // rms_ss_in (rms_ss_n per row) and scales each row's outputs by 1/rms
+    // (RMSNorm's factor moved past the dot).
     _Float16* rms_tiles_out = nullptr;
     const float* rms_gamma = nullptr;
     double* rms_ss_out = nullptr;
@@ -206,6 +235,10 @@ bool fused_glu_supported(int type, size_t K, size_t N);
 bool batched_glu_supported(int type, size_t K, size_t N);
 // K splits for a residual batched GEMM of this shape (1: none).
 int batched_splits(size_t N, size_t K);
+// Whether batched_gemv runs M rows of this shape on the 16-row Q4_K kernel
+// (no split-K; xh16_layout(M, K) holds, and a residual projection with
+// rms_tiles_out leaves rms_ss_out[m][N/16]).
+bool batched16_supported(size_t M, size_t K, size_t N, int epi);
 bool fused_gemv_supported(int type, size_t K, size_t N, int pro);
 // Greedy partials the one-row matrix-core GEMV leaves for this weight with
 // EPI_STORE (0 when the weight takes another kernel).

@@ -95,7 +95,7 @@ struct zg_session {
     void* xh = nullptr;  // f16 activations of the batched (B > 4) projections
     float* parts = nullptr;  // split-K partial tiles of residual projections (B > 4)
     void* xh3 = nullptr;     // the stream's RMS input tiles a residual projection leaves (B > 4)
-    double* rss = nullptr;   // and their per-tile sums of squares [rows][hidden/32]
+    double* rss = nullptr;   // and their per-tile sums of squares [rows][hidden/16 or hidden/32]
     void* xh2 = nullptr;     // the SwiGLU product in f16 tiles, down projection input (B > 4)
     size_t y0w = 0;
     std::vector<float*> ring, rec;  // per GDN layer: conv ring [B][3W][4], state [B][2][H][128][128]
@@ -259,6 +259,7 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
     // next RMS projection's f16 tiles (xh3) and per-tile sums of squares
     // (rss) of the current stream
     bool rms_ready = false;
+    int rss_n = 0;  // sums of squares per row in rss
     // one row: the first projection dequantises the token's embedding in its
     // prologue (and stores it as the residual stream) instead of an embedding launch
     const zg::DeviceWeight* first_in = m->layers.empty() || m->layers[0].in_proj.size() != 1
@@ -309,14 +310,20 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             } else if (rms_ready && pro == zg::PRO_RMS && x == s->x) {
                 f.xh_in = s->xh3;  // the stream's tiles and sums of squares
                 f.rms_ss_in = s->rss;
-                f.rms_ss_n = (int)(H / 32);
+                f.rms_ss_n = rss_n;
             }
             if (epi == zg::EPI_RESID && y == s->x && m->all_q4k) {
-                // a short K reads its 32 activation rows quickly: no splits,
-                // and the next RMS projection's input in the epilogue; a long
-                // K splits (the next RMS activation launch adds the parts)
-                rms_ready = gamma_next && w->dw.K <= 2048 && H <= 2048 && H % 256 == 0 && ldy == H;
-                const int sp = rms_ready ? 1 : zg::batched_splits(w->dw.N, w->dw.K);
+                // the next RMS projection's input in the epilogue, without
+                // K splits: on the 16-row kernel (which never splits K) when
+                // the stream's width takes its layout, else for a short K
+                // (32 activation rows read quickly); a long K otherwise
+                // splits (the next RMS activation launch adds the parts)
+                const bool k16 = zg::batched16_supported(B, w->dw.K, w->dw.N, zg::EPI_RESID);
+                const bool h16 = zg::xh16_layout(B, H);
+                rms_ready = gamma_next && H % 256 == 0 && H <= 2048 && ldy == H &&
+                            (h16 ? k16 : !k16 && w->dw.K <= 2048);
+                rss_n = (int)(k16 ? H / 16 : H / 32);
+                const int sp = rms_ready || k16 ? 1 : zg::batched_splits(w->dw.N, w->dw.K);
                 if (rms_ready) {
                     f.rms_tiles_out = (_Float16*)s->xh3;
                     f.rms_gamma = gamma_next;
@@ -404,6 +411,9 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             ZG_HIP(gemv(L.out_proj, zg::PRO_PLAIN, s->ao, QD, nullptr, 0, nullptr, zg::EPI_RESID, s->x, H, nullptr,
                         tiles ? s->xh : nullptr, false, L.post_norm));
         }
+        // the RMSNorm weight of the next projection that reads the stream
+        const float* next_norm = i + 1 < m->layers.size() ? m->layers[i + 1].attn_norm
+                                                          : (logits || greedy ? m->out_norm : nullptr);
         const zg::DeviceWeight& gu = L.ffn_gu[0].w->dw;
         const bool glu = L.ffn_gu.size() == 1 && L.ffn_down->dw.type == zg::kQ4_K &&
                          (B > 4 ? zg::batched_glu_supported(gu.type, gu.K, gu.N) : zg::fused_glu_supported(gu.type, gu.K, gu.N));
@@ -413,7 +423,7 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             ZG_HIP(gemv(L.ffn_gu[0].w, zg::PRO_RMS, s->x, H, nullptr, 0, L.post_norm, zg::EPI_GLU, s->y0, s->y0w,
                         B > 4 ? s->xh2 : nullptr));
             ZG_HIP(gemv(L.ffn_down, zg::PRO_PLAIN, s->y0, s->y0w, nullptr, 0, nullptr, zg::EPI_RESID, s->x, H, nullptr,
-                        B > 4 ? s->xh2 : nullptr));
+                        B > 4 ? s->xh2 : nullptr, false, next_norm));
         } else {
             for (const Part& p : L.ffn_gu)
                 ZG_HIP(gemv(p.w, zg::PRO_RMS, s->x, H, nullptr, 0, L.post_norm, zg::EPI_STORE, s->y0 + p.col, s->y0w));
@@ -789,7 +799,7 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     A(&s->xh, zg::batched_scratch_bytes(B, std::max({H, F, W, QD})));
     if (B > 4) A((void**)&s->parts, 8 * ((B + 31) / 32 * 32) * H * sizeof(float));
     if (B > 4) A(&s->xh3, zg::batched_scratch_bytes(B, H));
-    if (B > 4) A((void**)&s->rss, (B + 31) / 32 * 32 * ((H + 31) / 32) * sizeof(double));
+    if (B > 4) A((void**)&s->rss, (B + 31) / 32 * 32 * ((H + 15) / 16) * sizeof(double));
     if (B > 4) A(&s->xh2, zg::batched_scratch_bytes(B, F));
     A((void**)&s->pidx, nparts * 4);
     A((void**)&s->x, B * H * 4);
