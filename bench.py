@@ -283,8 +283,10 @@ def attn_bytes(B, T, nq=8, nkv=2, d=256):
 def attn_leg(ctx, torch, rows=(1, 32), T=2048, reps=20, nq=8, nkv=2):
     """The attention decode step alone (zg_attn_decode_device: norms, RoPE,
     K/V append, scores, softmax, values, gate) at B rows, each at position
-    T-1 of a bf16 cache; the caches rotate over distinct buffers totalling
-    > 2.2x the Infinity Cache."""
+    T-1 of a bf16 cache, and its split-T form (zg_attn_decode_split_device,
+    the form the decode step of an all-Q4_K model runs: span workgroups and
+    the combine); the caches rotate over distinct buffers totalling > 2.2x
+    the Infinity Cache."""
     from zerogravity_amd import _lib as L
     lib = L.lib()
     s = torch.cuda.current_stream()
@@ -305,27 +307,36 @@ def attn_leg(ctx, torch, rows=(1, 32), T=2048, reps=20, nq=8, nkv=2):
         caches = [(torch.randn(B * T * nkv * d, device="cuda", generator=g).bfloat16(),
                    torch.randn(B * T * nkv * d, device="cuda", generator=g).bfloat16()) for _ in range(copies)]
 
-        def launch(i):
-            kc, vc = caches[i % copies]
-            ctx.check(lib.zg_attn_decode_device(ctx.h, B, nq, nkv, proj.data_ptr(), stride, qn.data_ptr(),
-                                                kn.data_ptr(), 1e-6, float(np.power(1e7, -2.0 / 64.0)),
-                                                pos.data_ptr(), kc.data_ptr(), vc.data_ptr(), T, L.BF16,
-                                                ws.data_ptr(), o.data_ptr(), s.cuda_stream))
+        sws = torch.empty(lib.zg_attn_decode_split_workspace_bytes(B, nq, nkv, T), dtype=torch.uint8, device="cuda")
+        theta = float(np.power(1e7, -2.0 / 64.0))
 
-        for i in range(copies):
-            launch(i)
-        torch.cuda.synchronize()
-        n = max(reps, copies)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        for i in range(n):
-            launch(i)
-        e1.record(s)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / n
-        gbs = attn_bytes(B, T, nq, nkv) / us / 1e3
-        out[B] = dict(us=round(us, 3), gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
-        log(f"attention decode B={B:2d} T={T}: {us:8.2f} us  {gbs:8.1f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+        def launch(i, split=False):
+            kc, vc = caches[i % copies]
+            fn = lib.zg_attn_decode_split_device if split else lib.zg_attn_decode_device
+            ctx.check(fn(ctx.h, B, nq, nkv, proj.data_ptr(), stride, qn.data_ptr(), kn.data_ptr(), 1e-6, theta,
+                         pos.data_ptr(), kc.data_ptr(), vc.data_ptr(), T, L.BF16,
+                         (sws if split else ws).data_ptr(), o.data_ptr(), s.cuda_stream))
+
+        res = {}
+        for split in (False, True):
+            for i in range(copies):
+                launch(i, split)
+            torch.cuda.synchronize()
+            n = max(reps, copies)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for i in range(n):
+                launch(i, split)
+            e1.record(s)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / n
+            gbs = attn_bytes(B, T, nq, nkv) / us / 1e3
+            res[split] = (us, gbs)
+            log(f"attention decode{' split-T' if split else ''} B={B:2d} T={T}: {us:8.2f} us  {gbs:8.1f} GB/s "
+                f"({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+        (us, gbs), (sus, sgbs) = res[False], res[True]
+        out[B] = dict(us=round(us, 3), gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4),
+                      split_us=round(sus, 3), split_gbs=round(sgbs, 1), split_frac=round(sgbs / HBM_PEAK_GBS, 4))
         del caches
     return out
 

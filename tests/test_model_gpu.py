@@ -335,25 +335,36 @@ WIDE = dict(hidden=2048, layers=4, ffn=6144, vocab=1000, gdn_heads=16, gdn_dim=1
             head_dim=256, full_attention_interval=4, max_context=4096, eps=1e-6)
 
 
-def test_batched_split_k_rows_match_oracle(kern):
-    """The 2B layer shapes at B=32: the 2048-row residual projections split
-    K over workgroups (ssm_out and o-proj 2 ways, the FFN down projection 6
-    ways) and the next RMS activation kernel adds the partial tiles into the
-    residual stream; every row must track its CPU session within the
-    end-to-end bound with the same greedy tokens."""
-    t = qwen35.synthetic_tensors(WIDE, gguf.Q4_K, seed=21)
+# hidden 1024, FFN 3584: the down projection (K = 3584) stays on the 32-row
+# kernel with K split over workgroups, every other projection runs the
+# 16-row kernel, so activation tiles cross between the two layouts
+MIXED = dict(WIDE, hidden=1024, ffn=3584, gdn_heads=8, q_heads=4, kv_heads=2)
+
+
+@pytest.mark.parametrize("geom", ["2b", "mixed"])
+def test_batched_rows_match_oracle(kern, geom):
+    """Batched rows (B=32) at two layer geometries, every row tracking its
+    CPU session within the end-to-end bound with the same greedy tokens.
+    2B widths: every projection on the 16-row kernel; the residual
+    projections (ssm_out and o-proj, K = 2048; the FFN down, K = 6144, one
+    16-row half per workgroup) finish the residual and leave the next RMS
+    projection's f16 tiles and per-16-column sums of squares.  Mixed: the
+    32-row kernel's split-K down projection, whose partial tiles the next
+    RMS activation kernel adds, next to 16-row projections."""
+    g = WIDE if geom == "2b" else MIXED
+    t = qwen35.synthetic_tensors(g, gguf.Q4_K, seed=21)
     B, steps = 32, 3
-    m = qwen35.QwenModelHip(WIDE, t, kernel=kern)
+    m = qwen35.QwenModelHip(g, t, kernel=kern)
     s = m.session(max_batch=B, max_context=64, kv_dtype=L.F32)
-    toks = _tokens(17, B * steps, WIDE["vocab"]).reshape(steps, B)
+    toks = _tokens(17, B * steps, g["vocab"]).reshape(steps, B)
     got = [s.step(toks[i])[0] for i in range(steps)]
     worst = 0.0
     for b in range(0, B, 5):
-        o = _oracle(WIDE, t).session()
+        o = _oracle(g, t).session()
         for i in range(steps):
             ref = o.forward(int(toks[i, b]))
             worst = max(worst, float(np.max(np.abs(got[i][b] - ref))))
             assert int(np.argmax(got[i][b])) == int(np.argmax(ref)), (b, i)
-    print(f"batched split-K B={B}: worst logit max-abs {worst:.3e}")
+    print(f"batched rows ({geom}) B={B}: worst logit max-abs {worst:.3e}")
     assert worst <= LOGIT_TOL
     m.close()
