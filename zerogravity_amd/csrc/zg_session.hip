@@ -751,7 +751,10 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
         return fail(ctx, ZG_E_LIMIT, "session batch must be 1..64 and context within the model's");
     if (kv_dtype != ZG_BF16 && kv_dtype != ZG_F32) return fail(ctx, ZG_E_MALFORMED, "KV cache dtype must be BF16 or F32");
     if (max_batch > 4) {
-        // the batched-row path reads Q4_K weights in MFMA tile order
+        // the batched rows' 32-row kernel reads Q4_K weights in its MFMA
+        // tile order; the 16-row kernel (K a multiple of 1024 up to 6144)
+        // reads the weight's own layout, and zg_prefill_batched builds the
+        // prompt GEMM's tiles when it first needs them
         std::vector<zg_weight*> ws = {m->embd};
         for (auto& L : m->layers) {
             ws.insert(ws.end(), {L.out_proj, L.ffn_down});
@@ -759,7 +762,7 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
             for (const Part& p : L.ffn_gu) ws.push_back(p.w);
         }
         for (zg_weight* w : ws)
-            if (w && w->dw.type == zg::kQ4_K && !w->dw.qs_t) {
+            if (w && w->dw.type == zg::kQ4_K && !w->dw.qs_t && !zg::xh16_layout(max_batch, w->dw.K)) {
                 const hipError_t e = zg::ensure_mfma_tiles(w->dw, ctx->stream);
                 if (e != hipSuccess) return fail(ctx, ZG_E_RESOURCE, "MFMA tile layout of a Q4_K weight");
             }
