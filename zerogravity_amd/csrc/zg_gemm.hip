@@ -215,12 +215,14 @@ bool prompt_gemm_supported(int type, size_t K, size_t N, int epi) {
     return true;
 }
 
-// Shapes: per-wave MT x NT tiles; the largest workgroup tile that still
-// gives at least one workgroup per CU (256 CUs), else the smallest.
-// Measured (rocprofv3 counters, 2B-shaped prefill): the kernel is bound by
-// the VALU work of the in-register dequantization (about 5 VALU
-// instructions per MFMA with 4 M tiles per wave); 8-wave workgroups (two
-// waves per SIMD) and 8 M tiles per wave measured no faster.
+// Shapes: two weight tiles per wave (NT = 2), four waves along N, and the
+// most activation tiles per wave (MT = 3, 2, 1) that still gives at least one
+// workgroup per CU (256), else one.  Measured over M = 512, 2048, 8192 and
+// the 2B-shaped projections (gate/up 12288 x 2048, GDN in 8224 x 2048, out
+// 2048 x 2048, down 2048 x 6144): NT = 4 tiles with MT = 4 left a
+// workgroup's 256 accumulators to one wave per SIMD and ran 1.3-1.6x
+// slower (gate/up at M = 2048: 176 against 127 us); with NT = 2 the choice
+// among MT = 1-4 and 2-8 waves moves the time by about 10%.
 hipError_t prompt_gemm(const DeviceWeight& w, const FusedGemvArgs& args, const _Float16* xh, hipStream_t s) {
     if (!prompt_gemm_supported(w.type, w.K, w.N, args.epi) || !w.qs_t || !w.hdr_t || args.M <= 0)
         return hipErrorInvalidValue;
@@ -241,9 +243,9 @@ hipError_t prompt_gemm(const DeviceWeight& w, const FusedGemvArgs& args, const _
     hipLaunchKernelGGL((gemm_q4k_kernel<E, MTV, NTV, WNV, WMV>), grid(MTV, NTV, WNV, WMV), dim3(64 * WNV * WMV), 0, s, \
                        a, xh)
 #define ZG_GQE(E)                                                  \
-    if (count(grid(4, 4, 4, 1)) >= 256) ZG_GQ(E, 4, 4, 4, 1);      \
-    else if (count(grid(2, 4, 4, 1)) >= 256) ZG_GQ(E, 2, 4, 4, 1); \
-    else ZG_GQ(E, 2, 2, 2, 2);
+    if (count(grid(3, 2, 4, 1)) >= 256) ZG_GQ(E, 3, 2, 4, 1);      \
+    else if (count(grid(2, 2, 4, 1)) >= 256) ZG_GQ(E, 2, 2, 4, 1); \
+    else ZG_GQ(E, 1, 2, 4, 1);
     if (a.epi == EPI_GLU) {
         ZG_GQE(EPI_GLU)
     } else if (a.epi == EPI_RESID) {
