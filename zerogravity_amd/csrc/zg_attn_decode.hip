@@ -677,10 +677,16 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
     };
     load_keys(0);
     if (tid < 32) {
-        float angle = (float)p;
-        for (int t = 0; t < tid; ++t) angle *= a.theta_scale;
-        rsin[tid] = cr_sinf(angle);
-        rcos[tid] = cr_cosf(angle);
+        if (a.rope) {  // the session's table: the same angles and rounding
+            const float2 cs = ((const float2*)a.rope)[(size_t)p * 32 + tid];
+            rcos[tid] = cs.x;
+            rsin[tid] = cs.y;
+        } else {
+            float angle = (float)p;
+            for (int t = 0; t < tid; ++t) angle *= a.theta_scale;
+            rsin[tid] = cr_sinf(angle);
+            rcos[tid] = cr_cosf(angle);
+        }
     }
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
@@ -907,6 +913,25 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int
         if (a.status && !(fabsf(v) <= 65504.0f)) atomicOr(a.status, 16);
         ((_Float16*)a.xh)[at] = (_Float16)v;
     }
+}
+
+// RoPE angles of positions [0, n): entry 32 p + t is (cos, sin) of p times
+// theta_scale^t, the angle formed by repeated f32 products as the decode
+// kernels form it, with the same correctly rounded cos and sin.
+__global__ __launch_bounds__(256) void rope_table_kernel(float2* __restrict__ tab, int n, float theta_scale) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n * 32) return;
+    const int p = i >> 5, t = i & 31;
+    float angle = (float)p;
+    for (int q = 0; q < t; ++q) angle *= theta_scale;
+    tab[i] = make_float2(cr_cosf(angle), cr_sinf(angle));
+}
+
+hipError_t rope_table(float* tab, size_t n, float theta_scale, hipStream_t s) {
+    if (!tab || n == 0 || n > (1u << 24)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n * 32 + 255) / 256)), dim3(256), 0, s, (float2*)tab, (int)n,
+                       theta_scale);
+    return hipGetLastError();
 }
 
 hipError_t attn_decode_split(const AttnDecodeArgs& a, size_t B, float* part, hipStream_t s) {

@@ -309,10 +309,13 @@ struct AttnDecodeArgs {
     float* stats = nullptr;  // [B][nq][2] softmax {max, 1/sum}
     int nq = 0, nkv = 0, max_ctx = 0;
     // batched rows (optional): the gated output also written as f16 MFMA
-    // tiles for K = nq*d (act16_kernel's plain layout), the output
-    // projection's activation
+    // tiles for K = nq*d (xh_tile_index), the output projection's activation
     void* xh = nullptr;
+    // split form (optional): the RoPE table of rope_table, [max_ctx][32]
+    // (cos, sin) pairs for this theta_scale
+    const float* rope = nullptr;
 };
+hipError_t rope_table(float* tab, size_t n, float theta_scale, hipStream_t s);
 hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s);
 // Split-T form for 1..64 rows (attn_split_kernel + attn_combine_kernel):
 // per-span partials in `part` (attn_split_part_bytes), then the combine

@@ -92,6 +92,7 @@ struct zg_session {
           *pmax = nullptr, *att_stats = nullptr;
     // split-T attention partials (all-Q4_K models at 1..4 rows; null otherwise)
     float* att_part = nullptr;
+    float* rope = nullptr;  // (cos, sin) of every position's 32 angles, with att_part
     void* xh = nullptr;  // f16 activations of the batched (B > 4) projections
     float* parts = nullptr;  // split-K partial tiles of residual projections (B > 4)
     void* xh3 = nullptr;     // the stream's RMS input tiles a residual projection leaves (B > 4)
@@ -404,8 +405,10 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             // batched rows: the value kernel also writes o_proj's f16 tiles
             const bool tiles = B > 4 && L.out_proj->dw.type == zg::kQ4_K;
             if (tiles) a.xh = s->xh;
-            if (s->att_part && zg::attn_split_supported(B, a.nq, a.nkv, s->max_ctx))
+            if (s->att_part && zg::attn_split_supported(B, a.nq, a.nkv, s->max_ctx)) {
+                a.rope = s->rope;
                 ZG_HIP(zg::attn_decode_split(a, B, s->att_part, st));
+            }
             else
                 ZG_HIP(zg::attn_decode(a, B, st));
             ZG_HIP(gemv(L.out_proj, zg::PRO_PLAIN, s->ao, QD, nullptr, 0, nullptr, zg::EPI_RESID, s->x, H, nullptr,
@@ -819,7 +822,13 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
         for (size_t r = 1; r <= B; ++r)
             if (zg::attn_split_supported(r, (int)g.q_heads, (int)g.kv_heads, max_context))
                 bytes = std::max(bytes, zg::attn_split_part_bytes(r, (int)g.q_heads, (int)g.kv_heads, max_context));
-        if (bytes) A((void**)&s->att_part, bytes);
+        if (bytes) {
+            A((void**)&s->att_part, bytes);
+            A((void**)&s->rope, max_context * 32 * 2 * sizeof(float));
+            if (!rc && zg::rope_table(s->rope, max_context, powf(10000000.0f, -2.0f / 64.0f), ctx->stream) !=
+                           hipSuccess)
+                rc = ZG_E_DEVICE;
+        }
     }
     s->layer_slot.resize(g.layers);
     for (size_t i = 0; i < m->layers.size() && !rc; ++i) {
