@@ -353,9 +353,13 @@ struct AttnPrefillArgs {
     float* Q = nullptr;                         // scratch [n][nq][256]
     float* out = nullptr;                       // [n][nq*256], gated
     int* status = nullptr;                      // bit 4: a K or V value past the f16 range
+    // optional key-chunk partials, attn_prefill_part_bytes(n, nq) bytes: long
+    // prompts split each query tile's keys over several workgroups
+    float* part = nullptr;
 };
 // q/k norm + RoPE + KV append for the n tokens, then causal attention.
 hipError_t attn_prefill(const AttnPrefillArgs& a, hipStream_t s);
+size_t attn_prefill_part_bytes(size_t n, int nq);
 
 // Greedy ids of B logit rows (leading dimension ld) through partials
 // [argmax_partials(B)] (core/src/numerics.rs:126-140: first maximum wins,

@@ -207,13 +207,18 @@ typedef float af16 __attribute__((ext_vector_type(16)));
 // O^T += V^T P^T when MFMA step s, half h, element e is taken to be key
 // 16s + (e%4) + 8(e/4) + 4h of the block (any fixed key order contracts to
 // the same sum).  q carries the 1/sqrt(d) scale before rounding to f16.
+// Key chunks: a query tile's key blocks are split into chunks of kch blocks,
+// one workgroup each (grid x = tiles * ns); a tile whose keys fit one chunk
+// writes its output, the others write {m, l, unnormalised o} per (chunk,
+// head, query) to `part` for attn_prefill_combine_kernel.
 template <typename KV, int G>
 __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* __restrict__ Q,
                                                                    const KV* __restrict__ kc,
                                                                    const KV* __restrict__ vc, int n, int nq,
                                                                    int nkv, int pos0, float scale,
                                                                    const float* __restrict__ P, size_t ldp,
-                                                                   float* __restrict__ out, int* __restrict__ status) {
+                                                                   float* __restrict__ out, int* __restrict__ status,
+                                                                   int ns, int kch, float* __restrict__ part) {
     constexpr int QT = 32, KB = 32, D = 256;
     bool over = false;  // a staged K or V value past the f16 range
     constexpr int KROW = D + 8;   // halves per staged key row (16-byte pad)
@@ -223,7 +228,8 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
     // the heaviest (latest) query tiles first, both kv heads of a tile
     // together, so that the causal tail is short
     const int lin = blockIdx.x + gridDim.x * blockIdx.y;
-    const int kvh = lin % (int)gridDim.y, tile = (int)gridDim.x - 1 - lin / (int)gridDim.y;
+    const int kvh = lin % (int)gridDim.y, rest = lin / (int)gridDim.y;
+    const int ntiles = (int)gridDim.x / ns, tile = ntiles - 1 - rest / ns, chunk = rest % ns;
     const int g = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int h = kvh * G + g, t0 = tile * QT;
     const int hs = lane >> 5, c = lane & 31;
@@ -246,7 +252,10 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
     const bool qvalid = t0 + c < n;
     const int tabs = pos0 + t0 + c;
     const int kend = pos0 + min(t0 + QT, n);  // keys 0 .. kend-1 are seen by some query of the tile
-    const int nblk = (kend + KB - 1) / KB;
+    const int nblk_t = (kend + KB - 1) / KB;
+    const int nsplit = (nblk_t + kch - 1) / kch;  // this tile's chunks
+    const int bstart = chunk * kch, nblk = min(nblk_t, bstart + kch);
+    if (bstart >= nblk) return;  // a chunk past this tile's keys (uniform over the workgroup)
     const size_t kstep = (size_t)nkv * D;
     const KV* kb_ = kc + (size_t)kvh * D;
     const KV* vb_ = vc + (size_t)kvh * D;
@@ -268,8 +277,8 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
             vr[it].load(vb_ + (size_t)j * kstep + d4);
         }
     };
-    if constexpr (AHEAD) load_share(0);
-    for (int b = 0; b < nblk; ++b) {
+    if constexpr (AHEAD) load_share(bstart);
+    for (int b = bstart; b < nblk; ++b) {
         const int j0 = b * KB;
         __syncthreads();  // the previous block's tiles are consumed
         if constexpr (AHEAD) {
@@ -347,7 +356,20 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
             }
         }
     }
-    if (qvalid) {
+    if (nsplit > 1) {  // this chunk's partial: {m, l} then o for the combine
+        float* rec = part + ((((size_t)tile * ns + chunk) * nq + h) * QT + c) * (D + 2);
+        if (hs == 0) {
+            rec[0] = m;
+            rec[1] = l;
+        }
+#pragma unroll
+        for (int d = 0; d < 8; ++d)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int dim = d * 32 + 8 * q + 4 * hs;
+                *(v4f*)(rec + 2 + dim) = v4f{o[d][4 * q], o[d][4 * q + 1], o[d][4 * q + 2], o[d][4 * q + 3]};
+            }
+    } else if (qvalid) {
         const float inv = 1.0f / l;
         const float* gate = P + (size_t)(t0 + c) * ldp + (size_t)h * 2 * D + D;
         float* orow = out + ((size_t)(t0 + c) * nq + h) * D;
@@ -364,6 +386,71 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
             }
     }
     if (over && status) atomicOr(status, 16);
+}
+
+// Grid (tiles * 4, nq), 256 threads: thread t takes query 8 (x % 4) + t / 32
+// of tile x / 4 and dimensions 8 (t % 32) .. +7, combining the chunks'
+// partials weighted by exp(m_c - M), divided by the weighted sum of l_c,
+// gated; every load is issued before the first use.  Tiles of one chunk
+// were written directly.
+__global__ __launch_bounds__(256) void attn_prefill_combine_kernel(int n, int nq, int pos0, int ns, int kch,
+                                                                   const float* __restrict__ part,
+                                                                   const float* __restrict__ P, size_t ldp,
+                                                                   float* __restrict__ out) {
+    constexpr int QT = 32, KB = 32, D = 256, NSMAX = 4;
+    const int tile = blockIdx.x >> 2, h = blockIdx.y;
+    const int c = 8 * (blockIdx.x & 3) + (threadIdx.x >> 5), d0 = 8 * (threadIdx.x & 31);
+    const int t0 = tile * QT;
+    const int kend = pos0 + min(t0 + QT, n);
+    const int nsplit = ((kend + KB - 1) / KB + kch - 1) / kch;
+    if (nsplit <= 1 || t0 + c >= n) return;
+    const size_t cstride = (size_t)nq * QT * (D + 2);  // next chunk's record of the same (head, query)
+    const float* rec0 = part + (((size_t)tile * ns * nq + h) * QT + c) * (D + 2);
+    float mk[NSMAX], lk[NSMAX];
+    v4f ok[NSMAX][2];
+#pragma unroll
+    for (int k = 0; k < NSMAX; ++k) {
+        const float* rec = rec0 + (size_t)min(k, nsplit - 1) * cstride;
+        mk[k] = rec[0];
+        lk[k] = rec[1];
+        ok[k][0] = *(const v4f*)(rec + 2 + d0);
+        ok[k][1] = *(const v4f*)(rec + 2 + d0 + 4);
+    }
+    const float* gp = P + (size_t)(t0 + c) * ldp + (size_t)h * 2 * D + D + d0;
+    const v4f g0 = *(const v4f*)gp, g1 = *(const v4f*)(gp + 4);
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < NSMAX; ++k)
+        if (k < nsplit) M = fmaxf(M, mk[k]);
+    float L = 0.0f, o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < NSMAX; ++k) {
+        if (k < nsplit) {
+            const float w = mk[k] == -INFINITY ? 0.0f : __expf(mk[k] - M);
+            L += w * lk[k];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                o[e] += w * ok[k][0][e];
+                o[4 + e] += w * ok[k][1][e];
+            }
+        }
+    }
+    const float inv = 1.0f / L;
+    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    v4f r0, r1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        r0[e] = o[e] * inv * source_sigmoid(gv[e]);
+        r1[e] = o[4 + e] * inv * source_sigmoid(gv[4 + e]);
+    }
+    float* orow = out + ((size_t)(t0 + c) * nq + h) * D + d0;
+    *(v4f*)orow = r0;
+    *(v4f*)(orow + 4) = r1;
+}
+
+size_t attn_prefill_part_bytes(size_t n, int nq) {
+    const size_t ns = n >= 128 ? 4 : 1;
+    return ns == 1 ? 0 : (n + 31) / 32 * ns * (size_t)nq * 32 * (256 + 2) * sizeof(float);
 }
 
 hipError_t gdn_prefill_conv(const float* P, size_t ldp, size_t n, size_t W, size_t H, const float* conv_w,
@@ -391,10 +478,20 @@ hipError_t attn_prefill(const AttnPrefillArgs& a, hipStream_t s) {
                            0, s, a.P, a.ldp, a.nq, a.nkv, a.qnorm, a.knorm, a.eps, a.theta_scale, a.pos0,
                            (float*)a.kcache, (float*)a.vcache, a.Q);
     }
-    const dim3 grid((unsigned)((a.n + 31) / 32), (unsigned)a.nkv);
+    // key chunks: 4 per query tile while the tiles give fewer than 256
+    // workgroups (measured at 2048 tokens: one workgroup per tile left the
+    // heaviest tiles' 64 key blocks on 128 workgroups, 260 us against 167;
+    // at 8192 tokens the split ran slower), as many blocks each as the
+    // longest tile needs
+    const int ntiles = (int)((a.n + 31) / 32);
+    const int ns = a.part && attn_prefill_part_bytes(a.n, a.nq) && ntiles * a.nkv < 256 ? 4 : 1;
+    const int nblk_max = (int)((a.pos0 + a.n + 31) / 32);
+    const int kch = (nblk_max + ns - 1) / ns;
+    const dim3 grid((unsigned)(ntiles * ns), (unsigned)a.nkv);
 #define ZG_AP(KV, GG)                                                                                              \
     hipLaunchKernelGGL((attn_prefill_mfma_kernel<KV, GG>), grid, dim3(64 * GG), 0, s, a.Q, (const KV*)a.kcache,   \
-                       (const KV*)a.vcache, (int)a.n, a.nq, a.nkv, a.pos0, a.scale, a.P, a.ldp, a.out, a.status)
+                       (const KV*)a.vcache, (int)a.n, a.nq, a.nkv, a.pos0, a.scale, a.P, a.ldp, a.out, a.status, ns, \
+                       kch, a.part)
 #define ZG_APG(KV)                  \
     switch (G) {                    \
     case 1: ZG_AP(KV, 1); break;    \
@@ -409,6 +506,9 @@ hipError_t attn_prefill(const AttnPrefillArgs& a, hipStream_t s) {
     }
 #undef ZG_APG
 #undef ZG_AP
+    if (ns > 1)
+        hipLaunchKernelGGL(attn_prefill_combine_kernel, dim3((unsigned)(ntiles * 4), (unsigned)a.nq), dim3(256), 0, s,
+                           (int)a.n, a.nq, a.pos0, ns, kch, (const float*)a.part, a.P, a.ldp, a.out);
     return hipGetLastError();
 }
 

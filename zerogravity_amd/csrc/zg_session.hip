@@ -1115,7 +1115,7 @@ int prefill_batched_body(zg_session* s, size_t row, size_t n, const uint32_t* to
     const size_t QD = (size_t)g.q_heads * g.head_dim;
     const size_t mpad = (n + 31) / 32 * 32;
     const size_t ldp = s->y0w;
-    enum { X, P, Q, K, V, BETA, LOGD, CORE, QB, OB, XH, XH2, CHUNK, TOK, NBUF };
+    enum { X, P, Q, K, V, BETA, LOGD, CORE, QB, OB, XH, XH2, CHUNK, TOK, ATTP, NBUF };
     if (n > s->pf_cap) {
         ZG_HIP(hipStreamSynchronize(st));
         for (void* p : s->pf) (void)hipFree(p);
@@ -1124,7 +1124,8 @@ int prefill_batched_body(zg_session* s, size_t row, size_t n, const uint32_t* to
         const size_t bytes[NBUF] = {mpad * H * 4, mpad * ldp * 4, n * W * 4, n * W * 4, n * W * 4, n * GH * 4,
                                     n * GH * 4, mpad * W * 4, n * QD * 4, mpad * QD * 4,
                                     zg::batched_scratch_bytes(n, std::max({H, F, W, QD})),
-                                    zg::batched_scratch_bytes(n, F), zg::gdn_chunk_scratch_bytes(n, GH), n * 4};
+                                    zg::batched_scratch_bytes(n, F), zg::gdn_chunk_scratch_bytes(n, GH), n * 4,
+                                    zg::attn_prefill_part_bytes(n, (int)g.q_heads)};
         for (int i = 0; i < NBUF; ++i) {
             ZG_HIP(hipMalloc(&s->pf[i], std::max<size_t>(bytes[i], 256)));
             ZG_HIP(hipMemsetAsync(s->pf[i], 0, std::max<size_t>(bytes[i], 256), st));  // stream-ordered
@@ -1195,6 +1196,7 @@ int prefill_batched_body(zg_session* s, size_t row, size_t n, const uint32_t* to
             a.Q = (float*)s->pf[QB];
             a.out = (float*)s->pf[OB];
             a.status = s->d_status;
+            a.part = (float*)s->pf[ATTP];
             ZG_HIP(zg::attn_prefill(a, st));
             ZG_HIP(gemm(L.out_proj, zg::PRO_PLAIN, (const float*)s->pf[OB], QD, nullptr, 0, nullptr, zg::EPI_RESID, x,
                         H));
