@@ -266,7 +266,13 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
     constexpr int PF = KB * D / 4 / (64 * G);
     constexpr bool AHEAD = G == 4 || (G == 2 && sizeof(KV) == 2);
     static_assert(!AHEAD || PF * 64 * G == KB * D / 4, "slots divide over the threads");
-    KVRaw4<KV> kr[AHEAD ? PF : 1], vr[AHEAD ? PF : 1];
+    // V goes to LDS transposed, as dwords of two keys' halves: item it of
+    // wave w takes key pair lane % 16 and dimensions 4 dg .. 4 dg + 3,
+    // dg = 4 (w NI + it) + lane / 16, so the 64 lanes of a store hit 32 banks
+    // twice (one key per lane and 2-byte stores put 16 lanes on one bank)
+    constexpr int NI = AHEAD ? KB / 2 * (D / 4) / (64 * G) : 1;
+    KVRaw4<KV> kr[AHEAD ? PF : 1], vr[NI][2];
+    const int vpair = lane & 15, vdg = lane >> 4;
     auto load_share = [&](int b) {
 #pragma unroll
         for (int it = 0; it < PF; ++it) {
@@ -274,7 +280,15 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
             const int key = idx / (D / 4), d4 = (idx % (D / 4)) * 4;
             const int j = min(b * KB + key, kend - 1);  // past the last key: a copy, masked below
             kr[it].load(kb_ + (size_t)j * kstep + d4);
-            vr[it].load(vb_ + (size_t)j * kstep + d4);
+        }
+#pragma unroll
+        for (int it = 0; it < NI; ++it) {
+            const int d4 = 4 * (4 * (g * NI + it) + vdg);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int j = min(b * KB + 2 * vpair + e, kend - 1);
+                vr[it][e].load(vb_ + (size_t)j * kstep + d4);
+            }
         }
     };
     if constexpr (AHEAD) load_share(bstart);
@@ -286,15 +300,26 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
             for (int it = 0; it < PF; ++it) {
                 const int idx = threadIdx.x + it * 64 * G;
                 const int key = idx / (D / 4), d4 = (idx % (D / 4)) * 4;
-                float kv4[4], vv4[4];
+                float kv4[4];
                 kr[it].get(kv4);
-                vr[it].get(vv4);
                 *(ah4*)(ks + key * KROW + d4) =
                     ah4{(_Float16)kv4[0], (_Float16)kv4[1], (_Float16)kv4[2], (_Float16)kv4[3]};
 #pragma unroll
+                for (int i = 0; i < 4; ++i) over |= !(fabsf(kv4[i]) <= 65504.0f);
+            }
+#pragma unroll
+            for (int it = 0; it < NI; ++it) {
+                const int d4 = 4 * (4 * (g * NI + it) + vdg);
+                float v0[4], v1[4];
+                vr[it][0].get(v0);
+                vr[it][1].get(v1);
+#pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    vt[(d4 + i) * VROW + key] = (_Float16)vv4[i];
-                    over |= !(fabsf(vv4[i]) <= 65504.0f) || !(fabsf(kv4[i]) <= 65504.0f);
+                    const _Float16 lo = (_Float16)v0[i], hi = (_Float16)v1[i];
+                    const uint32_t w = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+                                       ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+                    *(uint32_t*)(vt + (d4 + i) * VROW + 2 * vpair) = w;
+                    over |= !(fabsf(v0[i]) <= 65504.0f) || !(fabsf(v1[i]) <= 65504.0f);
                 }
             }
             if (b + 1 < nblk) load_share(b + 1);
