@@ -354,24 +354,37 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_mfma_kernel(const float* 
             bm = fmaxf(bm, sc[r]);
         }
         bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-        const float mn = fmaxf(m, bm);
-        const bool none = mn == -INFINITY;
-        const float corr = none ? 1.0f : __expf(m - mn);
+        // The reference maximum m moves (and o, l are rescaled) only when
+        // some query's block maximum passes it by more than 8: until then
+        // the probabilities exp(s - m) stay below e^8, well inside f16, and
+        // o / l is the same quotient (the rescale costs as much as the
+        // block's products: o lives in 128 accumulator registers).
+        const bool raise = __ballot(bm > m + 8.0f) != 0;  // also every first finite block (m = -inf)
+        float corr = 1.0f;
+        if (raise) {
+            const float mn = fmaxf(m, bm);
+            corr = mn == -INFINITY ? 1.0f : __expf(m - mn);
+            m = mn;
+        }
+        const bool none = m == -INFINITY;
         float ps = 0.0f;
         ah8 pb[2];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const float p = none ? 0.0f : __expf(sc[r] - mn);
+            const float p = none ? 0.0f : __expf(sc[r] - m);
             ps += p;
             pb[r >> 3][r & 7] = (_Float16)p;
         }
         ps += __shfl_xor(ps, 32, 64);
         l = l * corr + ps;
-        m = mn;
+        if (raise) {
+#pragma unroll
+            for (int d = 0; d < 8; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[d][r] *= corr;
+        }
 #pragma unroll
         for (int d = 0; d < 8; ++d) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[d][r] *= corr;
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
                 const _Float16* vp = vt + (d * 32 + c) * VROW + 16 * st + 4 * hs;
