@@ -73,20 +73,31 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void gemm_q4k_kernel(FusedGemvArgs
         aoff[i] = ((uint32_t)mt * nbk * 16 * 64 + (e & 255)) * 16;
     }
 
+    // Weights two steps ahead in a two-slot ring (slot = step parity), the
+    // activation slab and the next block's headers one step / one block
+    // ahead.  Requests past the end re-read the last step or block, so every
+    // path issues the same loads and the compiler's load counting never
+    // waits on a later request.  (Measured at the 2B shapes against one
+    // step ahead: L=8192 model prefill 1% faster, L=2048 unchanged.)
     h8v ast[APT];
-    v4u wq[NT], wqn[NT], hc[NT], hn[NT];
-    auto load = [&](int sb) {
+    v4u wq[2][NT], hc[NT], hn[NT];
+    auto load_a = [&](int sb) {
+        sb = min(sb, nsub - 1);
         const uint32_t astep = (uint32_t)((sb >> 2) * 16 + 4 * (sb & 3)) * 64 * 16;
 #pragma unroll
         for (int i = 0; i < APT; ++i)
             ast[i] = __builtin_bit_cast(h8v, __builtin_amdgcn_raw_buffer_load_b128(rx, aoff[i] + astep, 0, 0));
+    };
+    auto load_w = [&](int sb, v4u (&dst)[NT]) {
+        sb = min(sb, nsub - 1);
 #pragma unroll
-        for (int t = 0; t < NT; ++t) wqn[t] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[t] + (uint32_t)sb * 64 * 16, 0, 0);
-        if ((sb & 3) == 0) {
+        for (int t = 0; t < NT; ++t) dst[t] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[t] + (uint32_t)sb * 64 * 16, 0, 0);
+    };
+    auto load_h = [&](int blk, v4u (&dst)[NT]) {
+        blk = min(blk, nbk - 1);
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
-                hn[t] = __builtin_amdgcn_raw_buffer_load_b128(rh, hoff[t] + (uint32_t)(sb >> 2) * 32 * 16, 0, 0);
-        }
+        for (int t = 0; t < NT; ++t)
+            dst[t] = __builtin_amdgcn_raw_buffer_load_b128(rh, hoff[t] + (uint32_t)blk * 32 * 16, 0, 0);
     };
     auto store = [&](int buf) {
 #pragma unroll
@@ -99,81 +110,77 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void gemm_q4k_kernel(FusedGemvArgs
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[i][t] = f16v{};
 
-    load(0);
+    load_a(0);
+    load_h(0, hc);
+    load_w(0, wq[0]);
+    load_w(1, wq[1]);
     store(0);
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        wq[t] = wqn[t];
-        hc[t] = hn[t];
-    }
     __syncthreads();
     const h2v bias = h2v{(_Float16)1024.0f, (_Float16)1024.0f};
-    for (int sb = 0; sb < nsub; ++sb) {
-        const int cur = sb & 1;
-        if (sb + 1 < nsub) load(sb + 1);
-        // the two 32-groups of this step: scale and min rounded once to f16
-        const int c4 = sb & 3;
-        h2v sc[NT][2], nm[NT][2];
+    for (int blk = 0; blk < nbk; ++blk) {
+        load_h(blk + 1, hn);
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const float d = f16_to_f32((uint16_t)(hc[t].x & 0xffffu));
-            const float dmin = f16_to_f32((uint16_t)(hc[t].x >> 16));
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                uint32_t s, mn;
-                q4k_dev_scale_min(hc[t], 2 * c4 + h, s, mn);
-                const _Float16 sh = (_Float16)(d * (float)s), mh = (_Float16)(dmin * (float)mn);
-                sc[t][h] = h2v{sh, sh};
-                nm[t][h] = h2v{-mh, -mh};
-            }
-        }
-        // each weight dword's low and high nibbles, masked once per step:
-        // step j takes dwords (2 (j%2), 2 (j%2) + 1), low nibbles for j < 2
-        uint32_t nib[NT][2][4];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const uint32_t wd[4] = {wq[t].x, wq[t].y, wq[t].z, wq[t].w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                nib[t][0][q] = wd[q] & 0x0f0f0f0fu;
-                nib[t][1][q] = (wd[q] >> 4) & 0x0f0f0f0fu;
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            h8v af[MT];
-#pragma unroll
-            for (int i = 0; i < MT; ++i) af[i] = xs[cur][(wm * MT + i) * 256 + j * 64 + lane];
+        for (int c4 = 0; c4 < 4; ++c4) {
+            const int sb = 4 * blk + c4, cur = c4 & 1;
+            load_a(sb + 1);
+            // the two 32-groups of this step: scale and min rounded once to f16
+            h2v sc[NT][2], nm[NT][2];
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                // step j: nibble half j/2 of the 8-byte piece j%2 (group 2*c4 + j/2)
-                const uint32_t w0 = nib[t][j >> 1][2 * (j & 1)], w1 = nib[t][j >> 1][2 * (j & 1) + 1];
-                // bytes (q, 0x64) pairs: the f16 bit patterns of 1024 + q
-                const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u);
-                const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u);
-                const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u);
-                const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u);
-                const h2v s2 = sc[t][j >> 1], n2 = nm[t][j >> 1];
-                const h2v e0 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p0) - bias, s2, n2);
-                const h2v e1 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p1) - bias, s2, n2);
-                const h2v e2 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p2) - bias, s2, n2);
-                const h2v e3 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p3) - bias, s2, n2);
-                // (a tile past N computes on a clamped copy; its columns are never stored)
-                const h8v wb = h8v{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
+                const float d = f16_to_f32((uint16_t)(hc[t].x & 0xffffu));
+                const float dmin = f16_to_f32((uint16_t)(hc[t].x >> 16));
 #pragma unroll
-                for (int i = 0; i < MT; ++i) acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], wb, acc[i][t], 0, 0, 0);
+                for (int h = 0; h < 2; ++h) {
+                    uint32_t s, mn;
+                    q4k_dev_scale_min(hc[t], 2 * c4 + h, s, mn);
+                    const _Float16 sh = (_Float16)(d * (float)s), mh = (_Float16)(dmin * (float)mn);
+                    sc[t][h] = h2v{sh, sh};
+                    nm[t][h] = h2v{-mh, -mh};
+                }
             }
-        }
-        if (sb + 1 < nsub) {
-            store(cur ^ 1);
+            // each weight dword's low and high nibbles, masked once per step:
+            // step j takes dwords (2 (j%2), 2 (j%2) + 1), low nibbles for j < 2
+            uint32_t nib[NT][2][4];
 #pragma unroll
-            for (int t = 0; t < NT; ++t) wq[t] = wqn[t];
-            if (((sb + 1) & 3) == 0) {
+            for (int t = 0; t < NT; ++t) {
+                const uint32_t wd[4] = {wq[cur][t].x, wq[cur][t].y, wq[cur][t].z, wq[cur][t].w};
 #pragma unroll
-                for (int t = 0; t < NT; ++t) hc[t] = hn[t];
+                for (int q = 0; q < 4; ++q) {
+                    nib[t][0][q] = wd[q] & 0x0f0f0f0fu;
+                    nib[t][1][q] = (wd[q] >> 4) & 0x0f0f0f0fu;
+                }
             }
+            load_w(sb + 2, wq[cur]);  // the slot is free once its nibbles are out
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                h8v af[MT];
+#pragma unroll
+                for (int i = 0; i < MT; ++i) af[i] = xs[cur][(wm * MT + i) * 256 + j * 64 + lane];
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    // step j: nibble half j/2 of the 8-byte piece j%2 (group 2*c4 + j/2)
+                    const uint32_t w0 = nib[t][j >> 1][2 * (j & 1)], w1 = nib[t][j >> 1][2 * (j & 1) + 1];
+                    // bytes (q, 0x64) pairs: the f16 bit patterns of 1024 + q
+                    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u);
+                    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u);
+                    const uint32_t p2 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u);
+                    const uint32_t p3 = __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u);
+                    const h2v s2 = sc[t][j >> 1], n2 = nm[t][j >> 1];
+                    const h2v e0 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p0) - bias, s2, n2);
+                    const h2v e1 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p1) - bias, s2, n2);
+                    const h2v e2 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p2) - bias, s2, n2);
+                    const h2v e3 = __builtin_elementwise_fma(__builtin_bit_cast(h2v, p3) - bias, s2, n2);
+                    // (a tile past N computes on a clamped copy; its columns are never stored)
+                    const h8v wb = h8v{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
+#pragma unroll
+                    for (int i = 0; i < MT; ++i) acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], wb, acc[i][t], 0, 0, 0);
+                }
+            }
+            store(cur ^ 1);  // (past the last step: a copy of it into the idle buffer)
+            __syncthreads();
         }
-        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < NT; ++t) hc[t] = hn[t];
     }
 
     // D register r of tile (i, t) is row (r%4) + 8*(r/4) + 4*(lane/32) of the
