@@ -42,14 +42,14 @@ __device__ __forceinline__ float prefill_rms_inv(double total, int n, float eps)
 
 }  // namespace
 
-// Grid ((3W + 255) / 256, ceil(n / TB)), 256 threads.  Thread = channel ch
-// of the conv input rows P[t][0:3W] for TB consecutive tokens: the causal
+// Grid ((3W + 255) / 256 + 1, ceil(n / TB)), 256 threads.  Thread = channel
+// ch of the conv input rows P[t][0:3W] for TB consecutive tokens: the causal
 // 4-tap conv of cpu/src/ops/gdn.rs:7-44 over a sliding window (each input
 // read once; taps older than the prompt come from the row's ring, where the
 // token at position p sits in slot p % 4), SiLU (forward.rs:548), split into
-// q, k, v [n][W].  Workgroups x = 0 also form the gates of lib.rs:339-362
-// for their tokens: beta = sigmoid(beta projection), log decay
-// softplus(alpha + dt) * a.
+// q, k, v [n][W].  The last workgroup column forms the gates of
+// lib.rs:339-362 for its TB tokens, one (token, head) per thread: beta =
+// sigmoid(beta projection), log decay softplus(alpha + dt) * a.
 template <int TB>
 __global__ __launch_bounds__(256) void gdn_prefill_conv_kernel(const float* __restrict__ P, size_t ldp, int n, int W,
                                                                int H, const float* __restrict__ conv_w,
@@ -60,6 +60,22 @@ __global__ __launch_bounds__(256) void gdn_prefill_conv_kernel(const float* __re
                                                                float* __restrict__ beta, float* __restrict__ logd) {
     const int t0 = blockIdx.y * TB, ch = blockIdx.x * 256 + threadIdx.x;
     const int t1 = min(t0 + TB, n);
+    if (blockIdx.x == gridDim.x - 1) {
+        // the gates: one (token, head) per thread (the f64 transcendentals
+        // of gdn_coef are the slowest work of the launch; one thread per
+        // head running TB tokens in turn held the whole grid back)
+        for (int i = threadIdx.x; i < TB * H; i += 256) {
+            const int t = t0 + i / H, h = i % H;
+            if (t < t1) {
+                const float* row = P + (size_t)t * ldp;
+                float gain, bt, sp, gr;
+                gdn_coef(row[4 * W + h], row[4 * W + H + h], dt[h], ssm_a[h], gain, bt, sp, gr);
+                beta[(size_t)t * H + h] = bt;
+                logd[(size_t)t * H + h] = gr;
+            }
+        }
+        return;
+    }
     if (ch < 3 * W) {
         float w3[3];  // inputs of tokens t-3, t-2, t-1
 #pragma unroll
@@ -86,16 +102,6 @@ __global__ __launch_bounds__(256) void gdn_prefill_conv_kernel(const float* __re
             w3[0] = w3[1];
             w3[1] = w3[2];
             w3[2] = x[u];
-        }
-    }
-    if (blockIdx.x == 0 && (int)threadIdx.x < H) {
-        const int h = threadIdx.x;
-        for (int t = t0; t < t1; ++t) {
-            const float* row = P + (size_t)t * ldp;
-            float gain, bt, sp, gr;
-            gdn_coef(row[4 * W + h], row[4 * W + H + h], dt[h], ssm_a[h], gain, bt, sp, gr);
-            beta[(size_t)t * H + h] = bt;
-            logd[(size_t)t * H + h] = gr;
         }
     }
 }
@@ -496,7 +502,7 @@ hipError_t gdn_prefill_conv(const float* P, size_t ldp, size_t n, size_t W, size
                             float* beta, float* logd, hipStream_t s) {
     if (n == 0 || W == 0 || H == 0 || H > 256) return hipErrorInvalidValue;
     constexpr int TB = 16;
-    hipLaunchKernelGGL(gdn_prefill_conv_kernel<TB>, dim3((unsigned)((3 * W + 255) / 256), (unsigned)((n + TB - 1) / TB)),
+    hipLaunchKernelGGL(gdn_prefill_conv_kernel<TB>, dim3((unsigned)((3 * W + 255) / 256 + 1), (unsigned)((n + TB - 1) / TB)),
                        dim3(256), 0, s, P, ldp, (int)n, (int)W, (int)H, conv_w, (const float*)ring, pos0, dt, ssm_a, q,
                        k, v, beta, logd);
     hipLaunchKernelGGL(gdn_prefill_ring_kernel, dim3((unsigned)((3 * W + 255) / 256)), dim3(256), 0, s, P, ldp,
