@@ -356,6 +356,8 @@ struct AttnPrefillArgs {
     // optional key-chunk partials, attn_prefill_part_bytes(n, nq) bytes: long
     // prompts split each query tile's keys over several workgroups
     float* part = nullptr;
+    // optional RoPE table of rope_table covering positions pos0 .. pos0+n-1
+    const float* rope = nullptr;
 };
 // q/k norm + RoPE + KV append for the n tokens, then causal attention.
 hipError_t attn_prefill(const AttnPrefillArgs& a, hipStream_t s);

@@ -124,7 +124,8 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(const float* __r
                                                                 int nkv, const float* __restrict__ qnorm,
                                                                 const float* __restrict__ knorm, float eps,
                                                                 float theta_scale, int pos0, KV* __restrict__ kc,
-                                                                KV* __restrict__ vc, float* __restrict__ Q) {
+                                                                KV* __restrict__ vc, float* __restrict__ Q,
+                                                                const float* __restrict__ rope) {
     constexpr int D = 256;
     __shared__ double red[4];
     __shared__ float hv[D];
@@ -136,10 +137,16 @@ __global__ __launch_bounds__(256) void attn_prefill_prep_kernel(const float* __r
     const float x = isq ? row[(size_t)task * 2 * D + tid] : row[(size_t)nq * 2 * D + (size_t)(task - nq) * D + tid];
     const float gm = isq ? qnorm[tid] : knorm[tid];
     if (tid < 32) {
-        float angle = (float)p;
-        for (int i = 0; i < tid; ++i) angle *= theta_scale;
-        rs[tid] = cr_sinf(angle);
-        rc[tid] = cr_cosf(angle);
+        if (rope) {  // the session's table: the same angles and rounding
+            const float2 cs = ((const float2*)rope)[(size_t)p * 32 + tid];
+            rc[tid] = cs.x;
+            rs[tid] = cs.y;
+        } else {
+            float angle = (float)p;
+            for (int i = 0; i < tid; ++i) angle *= theta_scale;
+            rs[tid] = cr_sinf(angle);
+            rc[tid] = cr_cosf(angle);
+        }
     }
     const float sq = x * x;
     double s = wave_sum_xor<double>((double)sq, 64);
@@ -516,11 +523,11 @@ hipError_t attn_prefill(const AttnPrefillArgs& a, hipStream_t s) {
     if (a.kv_bf16) {
         hipLaunchKernelGGL(attn_prefill_prep_kernel<uint16_t>, dim3((unsigned)a.n, (unsigned)(a.nq + a.nkv)),
                            dim3(256), 0, s, a.P, a.ldp, a.nq, a.nkv, a.qnorm, a.knorm, a.eps, a.theta_scale, a.pos0,
-                           (uint16_t*)a.kcache, (uint16_t*)a.vcache, a.Q);
+                           (uint16_t*)a.kcache, (uint16_t*)a.vcache, a.Q, a.rope);
     } else {
         hipLaunchKernelGGL(attn_prefill_prep_kernel<float>, dim3((unsigned)a.n, (unsigned)(a.nq + a.nkv)), dim3(256),
                            0, s, a.P, a.ldp, a.nq, a.nkv, a.qnorm, a.knorm, a.eps, a.theta_scale, a.pos0,
-                           (float*)a.kcache, (float*)a.vcache, a.Q);
+                           (float*)a.kcache, (float*)a.vcache, a.Q, a.rope);
     }
     // key chunks: 4 per query tile while the tiles give fewer than 256
     // workgroups (measured at 2048 tokens: one workgroup per tile left the

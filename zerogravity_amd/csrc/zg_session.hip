@@ -1197,6 +1197,7 @@ int prefill_batched_body(zg_session* s, size_t row, size_t n, const uint32_t* to
             a.out = (float*)s->pf[OB];
             a.status = s->d_status;
             a.part = (float*)s->pf[ATTP];
+            a.rope = s->rope;  // (null unless the session holds the split-T attention buffers)
             ZG_HIP(zg::attn_prefill(a, st));
             ZG_HIP(gemm(L.out_proj, zg::PRO_PLAIN, (const float*)s->pf[OB], QD, nullptr, 0, nullptr, zg::EPI_RESID, x,
                         H));
