@@ -684,8 +684,81 @@ hipError_t ensure_mfma_tiles(DeviceWeight& w, hipStream_t s) {
     return hipSuccess;
 }
 
+// Prompt-sized rows in the 32-row tile layout (plain or RMSNorm prologue, no
+// pending split-K residual): four rows per workgroup, thread t taking row
+// t % 4 and the 8-column groups t / 4 + 64 i, so that the four rows' 16-byte
+// runs of a group sit side by side in the tiles and a wave's stores fill
+// whole 64-byte spans (one row per workgroup scattered 16-byte stores 512
+// bytes apart).  Same arithmetic as act16_kernel: f64 sum of the f32
+// squares per row (in a fixed order), (x * inv) * gamma, f16.
+template <int PRO, int NG>
+__global__ __launch_bounds__(256) void act16_rows_kernel(FusedGemvArgs a, _Float16* __restrict__ xh) {
+    __shared__ double red[4][4];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r = tid & 3, gi = tid >> 2;
+    const int m = blockIdx.x * 4 + r, K = a.K;
+    const bool valid = m < a.M;
+    v4f v[NG][2], w[NG][2];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        const int k = 8 * (gi + 64 * i);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            v[i][h] = valid ? *(const v4f*)(a.x + (size_t)m * a.ldx + k + 4 * h) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (PRO == PRO_RMS) w[i][h] = *(const v4f*)(a.gamma + k + 4 * h);
+        }
+    }
+    float inv = 1.0f;
+    if (PRO == PRO_RMS) {
+        double s = 0.0;
+#pragma unroll
+        for (int i = 0; i < NG; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float q = v[i][h][e] * v[i][h][e];
+                    s += (double)q;
+                }
+        // the 16 lanes of this row in the wave (lane bits 2..5), then the waves
+#pragma unroll
+        for (int o = 4; o < 64; o <<= 1) s += __shfl_xor(s, o, 64);
+        if (lane < 4) red[wv][lane] = s;
+        __syncthreads();
+        inv = rms_inv((red[0][r] + red[1][r]) + (red[2][r] + red[3][r]), K, a.eps);
+    }
+    bool over = false;
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        const int k = 8 * (gi + 64 * i);
+        typedef _Float16 h8v_ __attribute__((ext_vector_type(8)));
+        h8v_ o8;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float y = v[i][h][e];
+                if (PRO == PRO_RMS) y = (y * inv) * w[i][h][e];
+                over |= valid && !(fabsf(y) <= 65504.0f);
+                o8[4 * h + e] = valid ? (_Float16)y : (_Float16)0.0f;
+            }
+        *(h8v_*)(xh + xh_tile_index(m, k, K, a.M)) = o8;
+    }
+    // past the f16 range: status bit 4 (the f32 paths carry it)
+    if (over && a.status) atomicOr(a.status, 16);
+}
+
 template <int PRO>
 static void launch_act16(const FusedGemvArgs& a, int mpad, _Float16* xh, hipStream_t s) {
+    if ((PRO == PRO_RMS || PRO == PRO_PLAIN) && !a.xh_rows && a.rsplits <= 0 && !xh16_layout(a.M, a.K) &&
+        a.K % 512 == 0) {
+        switch (a.K / 512) {
+        case 2: hipLaunchKernelGGL((act16_rows_kernel<PRO, 2>), dim3(mpad / 4), dim3(256), 0, s, a, xh); return;
+        case 4: hipLaunchKernelGGL((act16_rows_kernel<PRO, 4>), dim3(mpad / 4), dim3(256), 0, s, a, xh); return;
+        case 8: hipLaunchKernelGGL((act16_rows_kernel<PRO, 8>), dim3(mpad / 4), dim3(256), 0, s, a, xh); return;
+        case 12: hipLaunchKernelGGL((act16_rows_kernel<PRO, 12>), dim3(mpad / 4), dim3(256), 0, s, a, xh); return;
+        default: break;
+        }
+    }
     if (a.K <= 1024) hipLaunchKernelGGL((act16_kernel<PRO, 1>), dim3(mpad), dim3(256), 0, s, a, xh);
     else if (a.K <= 2048) hipLaunchKernelGGL((act16_kernel<PRO, 2>), dim3(mpad), dim3(256), 0, s, a, xh);
     else if (a.K <= 4096) hipLaunchKernelGGL((act16_kernel<PRO, 4>), dim3(mpad), dim3(256), 0, s, a, xh);
