@@ -174,12 +174,15 @@ def test_prefill_batched_repeatable_and_tracks_token_prefill(kern):
     m.close()
 
 
-@pytest.mark.parametrize("n", [600, 2048])
+@pytest.mark.parametrize("n", [400, 600, 2048])
 def test_prefill_batched_prompt_gemm_matches_oracle(kern, n):
     """From 256 prompt rows every projection runs through the register-
     blocked prompt GEMM (zg_gemm.hip: Q4_K dequantized in registers, f16
     MFMA, f32 accumulation; SwiGLU on the f32 gate/up sums, rounded once to
-    f16 for the down projection).  At the 2B layer shapes against the
+    f16 for the down projection).  The lengths cover the residual
+    projections' split over K (four runs at 400 rows, two at 600 and at
+    2048 for K >= 4096) and the prompt attention's key chunks (below 256
+    tile workgroups).  At the 2B layer shapes against the
     oracle's token-by-token prefill with glibc transcendentals (the
     reference's): last logits within 2e-2 max-abs, the same greedy token,
     state within 1e-2 relative, and the first decoded token after it the
