@@ -301,6 +301,7 @@ hipError_t prompt_gemm(const DeviceWeight& w, const FusedGemvArgs& args, const _
         if (c2 <= 64 && (a.K / 256) % 4 == 0) S = 4;
         else if ((c2 < 256 || (c2 == 256 && a.K >= 4096)) && (a.K / 256) % 2 == 0) S = 2;
     }
+    if (S > 1 && (size_t)S * a.M * a.N > a.prompt_parts_n) S = 1;
     if (S > 1) {
         a.splits = S;
         a.parts = a.prompt_parts;

@@ -196,10 +196,12 @@ struct FusedGemvArgs {
     int splits = 0;
     const float* rparts = nullptr;
     int rsplits = 0;
-    // prompt-sized residual projections (optional): workspace of 4 x M x N
-    // floats for the prompt GEMM's own split over K (two or four runs),
-    // summed into y by a second launch in a fixed order
+    // prompt-sized residual projections (optional): workspace of
+    // prompt_parts_n floats for the prompt GEMM's own split over K (two or
+    // four runs of S x M x N partial sums), summed into y by a second launch
+    // in a fixed order; a split that would not fit is not taken
     float* prompt_parts = nullptr;
+    size_t prompt_parts_n = 0;
     float* xw = nullptr;
     // batched rows, a residual projection without splits: with
     // rms_tiles_out it also leaves the next RMS projection's input -- f16

@@ -1116,6 +1116,10 @@ int prefill_batched_body(zg_session* s, size_t row, size_t n, const uint32_t* to
     const size_t mpad = (n + 31) / 32 * 32;
     const size_t ldp = s->y0w;
     enum { X, P, Q, K, V, BETA, LOGD, CORE, QB, OB, XH, XH2, CHUNK, TOK, ATTP, RPARTS, NBUF };
+    // the split residual projections' partial sums: a split is taken only
+    // while the tiles give at most 256 workgroups of 64 x 256 outputs, so two
+    // runs of those (or four of a quarter as many) bound it
+    const size_t kSplitParts = 2 * 256 * 64 * 256;
     if (n > s->pf_cap) {
         ZG_HIP(hipStreamSynchronize(st));
         for (void* p : s->pf) (void)hipFree(p);
@@ -1125,7 +1129,7 @@ int prefill_batched_body(zg_session* s, size_t row, size_t n, const uint32_t* to
                                     n * GH * 4, mpad * W * 4, n * QD * 4, mpad * QD * 4,
                                     zg::batched_scratch_bytes(n, std::max({H, F, W, QD})),
                                     zg::batched_scratch_bytes(n, F), zg::gdn_chunk_scratch_bytes(n, GH), n * 4,
-                                    zg::attn_prefill_part_bytes(n, (int)g.q_heads), 4 * mpad * H * 4};
+                                    zg::attn_prefill_part_bytes(n, (int)g.q_heads), kSplitParts * 4};
         for (int i = 0; i < NBUF; ++i) {
             ZG_HIP(hipMalloc(&s->pf[i], std::max<size_t>(bytes[i], 256)));
             ZG_HIP(hipMemsetAsync(s->pf[i], 0, std::max<size_t>(bytes[i], 256), st));  // stream-ordered
@@ -1158,7 +1162,10 @@ int prefill_batched_body(zg_session* s, size_t row, size_t n, const uint32_t* to
         f.status = s->d_status;
         f.xh_out = xh_out;
         f.xh_in = xh_in;
-        if (epi == zg::EPI_RESID && ldy == H) f.prompt_parts = (float*)s->pf[RPARTS];
+        if (epi == zg::EPI_RESID && ldy == H) {
+            f.prompt_parts = (float*)s->pf[RPARTS];
+            f.prompt_parts_n = kSplitParts;
+        }
         return zg::batched_gemv(w->dw, f, s->pf[XH], st);
     };
     for (size_t i = 0; i < m->layers.size(); ++i) {
