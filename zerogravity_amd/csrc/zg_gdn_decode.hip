@@ -118,55 +118,110 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
     }
     lds_barrier();  // the state loads stay in flight
 
-    float q[4][4], k[4][4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            q[c][t] = qk[32 * c + 4 * s + t];
-            k[c][t] = qk[D + 32 * c + 4 * s + t];
-        }
-    // two-stage L2 (forward.rs:564-576)
-    double sq = 0.0, sk = 0.0;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const float a2 = q[c][t] * q[c][t];
-            const float b2 = k[c][t] * k[c][t];
-            sq += (double)a2;
-            sk += (double)b2;
-        }
-    sq = group8_sum_all(sq);
-    sk = group8_sum_all(sk);
     const float dsq = 1.0f / sqrtf((float)D);
     const float eps_d = a.eps / (float)D;
-    const float iq = 1.0f / sqrtf((float)(sq / (double)D) + eps_d);
-    const float ik = 1.0f / sqrtf((float)(sk / (double)D) + eps_d);
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const float tq = q[c][t] * iq;
-            q[c][t] = tq * dsq;
-            const float tk = k[c][t] * ik;
-            k[c][t] = tk * dsq;
-        }
     const float gain = gates[0], beta = gates[1];
     const float vj = vv[HEAD ? j : jl];
     float cv[4][4];
+    float o;
+    if constexpr (HEAD) {
+        // the same arithmetic with q and k re-read from LDS where they are
+        // used rather than held in registers across the recurrence: 1024
+        // threads then fit in 64 registers, two (head, row) workgroups per CU
+        auto qk4 = [&](int base, int c) { return *(const v4f*)(qk + base + 32 * c + 4 * s); };
+        double sq = 0.0, sk = 0.0;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const v4f v = sv[c];
-        cv[c][0] = v.x * gain; cv[c][1] = v.y * gain; cv[c][2] = v.z * gain; cv[c][3] = v.w * gain;
+        for (int c = 0; c < 4; ++c) {
+            const v4f qv = qk4(0, c), kv = qk4(D, c);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float a2 = qv[t] * qv[t];
+                const float b2 = kv[t] * kv[t];
+                sq += (double)a2;
+                sk += (double)b2;
+            }
+        }
+        sq = group8_sum_all(sq);
+        sk = group8_sum_all(sk);
+        const float iq = 1.0f / sqrtf((float)(sq / (double)D) + eps_d);
+        const float ik = 1.0f / sqrtf((float)(sk / (double)D) + eps_d);
+        auto normed = [&](int base, float inv, float (&r)[4][4]) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const v4f v = qk4(base, c);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const float tv = v[t] * inv;
+                    r[c][t] = tv * dsq;
+                }
+            }
+        };
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const v4f v = sv[c];
+            cv[c][0] = v.x * gain; cv[c][1] = v.y * gain; cv[c][2] = v.z * gain; cv[c][3] = v.w * gain;
+        }
+        // the empty asm with a memory clobber makes the compiler load q and
+        // k again below instead of keeping the values read for the sums
+        asm volatile("" ::: "memory");
+        float k[4][4];
+        normed(D, ik, k);
+        const float prev = column_dot(cv, k);
+        const float delta = (vj - prev) * beta;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) cv[c][t] = fmaf(k[c][t], delta, cv[c][t]);
+        asm volatile("" ::: "memory");
+        float q[4][4];
+        normed(0, iq, q);
+        o = column_dot(cv, q);
+    } else {
+        float q[4][4], k[4][4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                q[c][t] = qk[32 * c + 4 * s + t];
+                k[c][t] = qk[D + 32 * c + 4 * s + t];
+            }
+        // two-stage L2 (forward.rs:564-576)
+        double sq = 0.0, sk = 0.0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float a2 = q[c][t] * q[c][t];
+                const float b2 = k[c][t] * k[c][t];
+                sq += (double)a2;
+                sk += (double)b2;
+            }
+        sq = group8_sum_all(sq);
+        sk = group8_sum_all(sk);
+        const float iq = 1.0f / sqrtf((float)(sq / (double)D) + eps_d);
+        const float ik = 1.0f / sqrtf((float)(sk / (double)D) + eps_d);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float tq = q[c][t] * iq;
+                q[c][t] = tq * dsq;
+                const float tk = k[c][t] * ik;
+                k[c][t] = tk * dsq;
+            }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const v4f v = sv[c];
+            cv[c][0] = v.x * gain; cv[c][1] = v.y * gain; cv[c][2] = v.z * gain; cv[c][3] = v.w * gain;
+        }
+        const float prev = column_dot(cv, k);
+        const float delta = (vj - prev) * beta;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) cv[c][t] = fmaf(k[c][t], delta, cv[c][t]);
+        o = column_dot(cv, q);
     }
-    const float prev = column_dot(cv, k);
-    const float delta = (vj - prev) * beta;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) cv[c][t] = fmaf(k[c][t], delta, cv[c][t]);
-    const float o = column_dot(cv, q);
 #pragma unroll
     for (int c = 0; c < 4; ++c) *(v4f*)(col_out + 32 * c) = v4f{cv[c][0], cv[c][1], cv[c][2], cv[c][3]};
     if (s == 0) a.core[(size_t)b * W + h * D + j] = o * a.scale;

@@ -68,8 +68,10 @@ __device__ __forceinline__ void gdn_coef(float alpha, float beta_p, float dt, fl
 // halves[m] = combined[m] + combined[m+4], (h0+h1)+(h2+h3).
 // Lane s of the column holds accumulators 4s..4s+3, i.e. elements
 // 32c + 4s + t (c, t in 0..3): one float4 per c, coalesced across the 8
-// lanes.  XOR-4 then XOR-2 shuffles form `combined`, XOR-1 forms `halves`
+// lanes.  XOR-4 then XOR-2 exchanges form `combined`, XOR-1 forms `halves`
 // and the last two levels are local: the dot is bit-identical to the CPU.
+// The XOR-4 exchange is a ds_swizzle in bit-mask mode (and 0x1f, xor 4),
+// the XOR-2 and XOR-1 ones DPP quad permutes: no lane-index registers.
 __device__ __forceinline__ float column_dot(const float (&a)[4][4], const float (&b)[4][4]) {
     float acc[4];
 #pragma unroll
@@ -81,9 +83,9 @@ __device__ __forceinline__ float column_dot(const float (&a)[4][4], const float 
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        acc[t] = acc[t] + __shfl_xor(acc[t], 4, 64);
-        acc[t] = acc[t] + __shfl_xor(acc[t], 2, 64);
-        acc[t] = acc[t] + __shfl_xor(acc[t], 1, 64);
+        acc[t] = acc[t] + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(acc[t]), 0x101f));
+        acc[t] = acc[t] + dpp_f<kDppXor2>(acc[t]);
+        acc[t] = acc[t] + dpp_f<kDppXor1>(acc[t]);
     }
     return (acc[0] + acc[1]) + (acc[2] + acc[3]);
 }
