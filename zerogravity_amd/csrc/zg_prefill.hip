@@ -246,11 +246,20 @@ __global__ __launch_bounds__(128) void gdn_chunk_solve_kernel(const float* __res
                                                               const float* __restrict__ beta,
                                                               const float* __restrict__ amat, int T, int H,
                                                               float* __restrict__ scratch) {
+    // A is staged in LDS and read there as broadcast 16-byte reads: read
+    // from memory as scalar loads its 2016 coefficients outgrew the scalar
+    // registers, and the compiler parked them in vector-register lanes
+    // (a write and a read instruction per coefficient)
+    __shared__ float As[kC * kC];
     const int c = blockIdx.x, h = blockIdx.y, z = blockIdx.z;
     const int col = threadIdx.x;
     const int t0 = c * kC, rows = min(kC, T - t0);
     float* rec = scratch + ((size_t)c * H + h) * kRec;
     const float* A = amat + ((size_t)c * H + h) * kRec + kOffA;
+#pragma unroll
+    for (int i = 0; i < kC * kC / (4 * 128); ++i)
+        *(v4f*)(As + 4 * (col + 128 * i)) = *(const v4f*)(A + 4 * (col + 128 * i));
+    __syncthreads();
     float xr[kC];
     if (z == 0) {
 #pragma unroll
@@ -269,13 +278,14 @@ __global__ __launch_bounds__(128) void gdn_chunk_solve_kernel(const float* __res
 #pragma unroll
     for (int row = 0; row < kC; ++row) {
         const int vend = row / 4 * 4;
-        const float* arow = A + row * kC;
+        const float* arow = As + row * kC;
         float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int st = 0; st < vend; st += 4) {
+            const v4f a4 = *(const v4f*)(arow + st);
 #pragma unroll
             for (int l = 0; l < 4; ++l) {
-                const float p = arow[st + l] * xr[st + l];
+                const float p = a4[l] * xr[st + l];
                 s4[l] = s4[l] + p;
             }
         }
@@ -286,6 +296,10 @@ __global__ __launch_bounds__(128) void gdn_chunk_solve_kernel(const float* __res
             sum = sum + p;
         }
         xr[row] = xr[row] - sum;
+        // the next row's coefficients are read only once the row before this
+        // one is solved (the asm takes that value and orders the LDS reads):
+        // hoisted further, the reads held most of A in registers
+        if (row >= 1) asm volatile("" ::"v"(xr[row - 1]) : "memory");
     }
     float* dst = rec + (z == 0 ? kOffU : kOffW);
 #pragma unroll
