@@ -30,6 +30,7 @@
 // chain of fused multiply-adds, so each output equals the reference's FMA
 // chain (chunk/core.rs:277-310) bit for bit.
 #include <algorithm>
+#include <atomic>
 
 #include "zg_device.hpp"
 #include "zg_internal.hpp"
@@ -491,96 +492,132 @@ __global__ __launch_bounds__(512) void gdn_chunk_scan_kernel(float* __restrict__
     }
 }
 
-// Grid (chunks, H), 512 threads: o = intra corr + dq S for one (chunk,
-// head), S the state entering the chunk (chunk/core.rs:236-252: the intra
-// product, then the inter product added).  Wave w computes rows
-// 16 (w % 4) .. +15 of columns 64 (w / 4) .. +63.  round_bf16 rounds each
-// output to the nearest bf16, ties to even, as the reference's output_bf16
-// does (gdn.rs:69-76).
+// Persistent, one 512-thread workgroup per CU (its LDS holds one item):
+// o = intra corr + dq S for (chunk, head) items blockIdx.x, + gridDim.x, ...
+// in turn, S the state entering the chunk (chunk/core.rs:236-252: the intra
+// product, then the inter product added).  The next item's operands (S,
+// corr, dq, intra: 144 KB) are requested into registers before the current
+// item's products, so a CU's loads overlap its MFMA chains.  Wave w
+// computes rows 16 (w % 4) .. +15 of columns 64 (w / 4) .. +63.
+// round_bf16 rounds each output to the nearest bf16, ties to even, as the
+// reference's output_bf16 does (gdn.rs:69-76).
 __global__ __launch_bounds__(512) void gdn_chunk_out_kernel(const float* __restrict__ scratch, int T, int H,
                                                             float* __restrict__ out, int round_bf16) {
     __shared__ float Sc[kD * kPad];
     __shared__ float Cr[kC * kPad];
     __shared__ float Dq[kC * kPad];
     __shared__ float In[kC * kApad];
-    const int c = blockIdx.x, h = blockIdx.y;
+    const int nitems = (T + kC - 1) / kC * H;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int t0 = c * kC, rows = min(kC, T - t0);
     const int i0 = 16 * (wv & 3), c0 = 64 * (wv >> 2), jl = lane & 15, kq = lane >> 4;
-    const float* rec = scratch + ((size_t)c * H + h) * kRec;
+    constexpr int NS = kD * kD / 4 / 512, NC = kC * kD / 4 / 512, NI = kC * kC / 4 / 512;
+    v4f ps[NS], pc[NC], pd[NC], pi[NI];
+    auto fetch = [&](int item) {  // item = chunk * H + head, the record's index
+        const float* rec = scratch + (size_t)item * kRec;
 #pragma unroll
-    for (int i = 0; i < kD * kD / 4 / 512; ++i) {
-        const int f = tid + 512 * i;
-        *(v4f*)&Sc[(f >> 5) * kPad + 4 * (f & 31)] = *(const v4f*)(rec + kOffS + 4 * f);
-    }
+        for (int i = 0; i < NS; ++i) ps[i] = *(const v4f*)(rec + kOffS + 4 * (tid + 512 * i));
 #pragma unroll
-    for (int i = 0; i < kC * kD / 4 / 512; ++i) {
-        const int f = tid + 512 * i;
-        *(v4f*)&Cr[(f >> 5) * kPad + 4 * (f & 31)] = *(const v4f*)(rec + kOffU + 4 * f);
-        *(v4f*)&Dq[(f >> 5) * kPad + 4 * (f & 31)] = *(const v4f*)(rec + kOffDq + 4 * f);
-    }
-#pragma unroll
-    for (int i = 0; i < kC * kC / 4 / 512; ++i) {
-        const int f = tid + 512 * i;
-        *(v4f*)&In[(f >> 4) * kApad + 4 * (f & 15)] = *(const v4f*)(rec + kOffIntra + 4 * f);
-    }
-    __syncthreads();
-    f4m oo[4], it[4];
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-        oo[jt] = f4m{0.0f, 0.0f, 0.0f, 0.0f};
-        it[jt] = oo[jt];
-    }
-    {
-        float ia[kC / 4];
-#pragma unroll
-        for (int s = 0; s < kC / 4; ++s) ia[s] = In[(i0 + jl) * kApad + 4 * s + kq];
-#pragma unroll
-        for (int s0 = 0; s0 < kC / 4; s0 += 8) {
-            float cb[8][4];
-#pragma unroll
-            for (int s = 0; s < 8; ++s)
-#pragma unroll
-                for (int jt = 0; jt < 4; ++jt) cb[s][jt] = Cr[(4 * (s0 + s) + kq) * kPad + c0 + 16 * jt + jl];
-            __builtin_amdgcn_sched_barrier(0);  // a block of operand reads, then its MFMAs
-#pragma unroll
-            for (int s = 0; s < 8; ++s)
-#pragma unroll
-                for (int jt = 0; jt < 4; ++jt) oo[jt] = mfma4(ia[s0 + s], cb[s][jt], oo[jt]);
+        for (int i = 0; i < NC; ++i) {
+            pc[i] = *(const v4f*)(rec + kOffU + 4 * (tid + 512 * i));
+            pd[i] = *(const v4f*)(rec + kOffDq + 4 * (tid + 512 * i));
         }
-    }
-    {
-        float da[kD / 4];
 #pragma unroll
-        for (int s = 0; s < kD / 4; ++s) da[s] = Dq[(i0 + jl) * kPad + 4 * s + kq];
+        for (int i = 0; i < NI; ++i) pi[i] = *(const v4f*)(rec + kOffIntra + 4 * (tid + 512 * i));
+    };
+    fetch(blockIdx.x);  // the grid never exceeds the item count
+    for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+        const int c = item / H, h = item - c * H;
+        const int t0 = c * kC, rows = min(kC, T - t0);
+        lds_barrier();  // every wave is done reading the previous item
 #pragma unroll
-        for (int s0 = 0; s0 < kD / 4; s0 += 8) {
-            float sb[8][4];
-#pragma unroll
-            for (int s = 0; s < 8; ++s)
-#pragma unroll
-                for (int jt = 0; jt < 4; ++jt) sb[s][jt] = Sc[(4 * (s0 + s) + kq) * kPad + c0 + 16 * jt + jl];
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int s = 0; s < 8; ++s)
-#pragma unroll
-                for (int jt = 0; jt < 4; ++jt) it[jt] = mfma4(da[s0 + s], sb[s][jt], it[jt]);
+        for (int i = 0; i < NS; ++i) {
+            const int f = tid + 512 * i;
+            *(v4f*)&Sc[(f >> 5) * kPad + 4 * (f & 31)] = ps[i];
         }
-    }
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
+        for (int i = 0; i < NC; ++i) {
+            const int f = tid + 512 * i;
+            *(v4f*)&Cr[(f >> 5) * kPad + 4 * (f & 31)] = pc[i];
+            *(v4f*)&Dq[(f >> 5) * kPad + 4 * (f & 31)] = pd[i];
+        }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = i0 + 4 * kq + r;
-            if (t < rows) {
-                float o = oo[jt][r] + it[jt][r];
-                if (round_bf16) {
-                    const unsigned b = __float_as_uint(o);
-                    o = __uint_as_float((b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u);
-                }
-                out[((size_t)(t0 + t) * H + h) * kD + c0 + 16 * jt + jl] = o;
+        for (int i = 0; i < NI; ++i) {
+            const int f = tid + 512 * i;
+            *(v4f*)&In[(f >> 4) * kApad + 4 * (f & 15)] = pi[i];
+        }
+        lds_barrier();
+        fetch(min(item + (int)gridDim.x, nitems - 1));  // in flight during the products
+        f4m oo[4], it[4];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            oo[jt] = f4m{0.0f, 0.0f, 0.0f, 0.0f};
+            it[jt] = oo[jt];
+        }
+        {
+            float ia[kC / 4];
+#pragma unroll
+            for (int s = 0; s < kC / 4; ++s) ia[s] = In[(i0 + jl) * kApad + 4 * s + kq];
+#pragma unroll
+            for (int s0 = 0; s0 < kC / 4; s0 += 8) {
+                float cb[8][4];
+#pragma unroll
+                for (int s = 0; s < 8; ++s)
+#pragma unroll
+                    for (int jt = 0; jt < 4; ++jt) cb[s][jt] = Cr[(4 * (s0 + s) + kq) * kPad + c0 + 16 * jt + jl];
+                __builtin_amdgcn_sched_barrier(0);  // a block of operand reads, then its MFMAs
+#pragma unroll
+                for (int s = 0; s < 8; ++s)
+#pragma unroll
+                    for (int jt = 0; jt < 4; ++jt) oo[jt] = mfma4(ia[s0 + s], cb[s][jt], oo[jt]);
             }
         }
+        {
+            float da[kD / 4];
+#pragma unroll
+            for (int s = 0; s < kD / 4; ++s) da[s] = Dq[(i0 + jl) * kPad + 4 * s + kq];
+#pragma unroll
+            for (int s0 = 0; s0 < kD / 4; s0 += 8) {
+                float sb[8][4];
+#pragma unroll
+                for (int s = 0; s < 8; ++s)
+#pragma unroll
+                    for (int jt = 0; jt < 4; ++jt) sb[s][jt] = Sc[(4 * (s0 + s) + kq) * kPad + c0 + 16 * jt + jl];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int s = 0; s < 8; ++s)
+#pragma unroll
+                    for (int jt = 0; jt < 4; ++jt) it[jt] = mfma4(da[s0 + s], sb[s][jt], it[jt]);
+            }
+        }
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = i0 + 4 * kq + r;
+                if (t < rows) {
+                    float o = oo[jt][r] + it[jt][r];
+                    if (round_bf16) {
+                        const unsigned b = __float_as_uint(o);
+                        o = __uint_as_float((b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u);
+                    }
+                    out[((size_t)(t0 + t) * H + h) * kD + c0 + 16 * jt + jl] = o;
+                }
+            }
+    }
+}
+
+// Compute units of the current device (persistent launches), cached per
+// device.
+static int device_cus() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v <= 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cache[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
 }
 
 size_t gdn_chunk_scratch_bytes(size_t T, size_t H) { return ((T + kC - 1) / kC) * H * kRec * sizeof(float); }
@@ -596,8 +633,9 @@ hipError_t gdn_chunk_prefill(const float* q, const float* k, const float* v, con
                        (const float*)scratch, (int)T, (int)H, scratch);
     hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3((unsigned)H, kD / kSW), dim3(512), 0, s, scratch, (int)T, (int)H,
                        state, key_major ? 1 : 0);
-    hipLaunchKernelGGL(gdn_chunk_out_kernel, dim3(nch, (unsigned)H), dim3(512), 0, s, scratch, (int)T, (int)H, out,
-                       round_bf16 ? 1 : 0);
+    const unsigned items = nch * (unsigned)H;
+    hipLaunchKernelGGL(gdn_chunk_out_kernel, dim3(std::min(items, (unsigned)device_cus())), dim3(512), 0, s, scratch,
+                       (int)T, (int)H, out, round_bf16 ? 1 : 0);
     return hipGetLastError();
 }
 
