@@ -498,7 +498,15 @@ __global__ __launch_bounds__(512) void gdn_chunk_scan_kernel(float* __restrict__
 // product, then the inter product added).  The next item's operands (S,
 // corr, dq, intra: 144 KB) are requested into registers before the current
 // item's products, so a CU's loads overlap its MFMA chains.  Wave w
-// computes rows 16 (w % 4) .. +15 of columns 64 (w / 4) .. +63.
+// computes row tile r = w (w < 4) or 7 - w (rows 16 r .. +15) of columns
+// 64 (w / 4) .. +63, lane n of MFMA tile j holding column 64 (w / 4) + 4 n
+// + j: the two waves sharing a SIMD take tiles r and 3 - r, and a lane's
+// four columns are adjacent, read as one 16-byte word and stored as one.
+// The intra product's chain stops after key 16 r + 15: intra is zero past
+// the diagonal (the reference's pairwise decay is exp(-inf) there), so the
+// remaining steps add only zeros, which change no finite sum but a zero's
+// sign, and the reference's own `output += sum` into 0.0 (core.rs:288-318)
+// clears that sign too, as (0 + intra) + inter does here.
 // round_bf16 rounds each output to the nearest bf16, ties to even, as the
 // reference's output_bf16 does (gdn.rs:69-76).
 __global__ __launch_bounds__(512) void gdn_chunk_out_kernel(const float* __restrict__ scratch, int T, int H,
@@ -509,7 +517,13 @@ __global__ __launch_bounds__(512) void gdn_chunk_out_kernel(const float* __restr
     __shared__ float In[kC * kApad];
     const int nitems = (T + kC - 1) / kC * H;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int i0 = 16 * (wv & 3), c0 = 64 * (wv >> 2), jl = lane & 15, kq = lane >> 4;
+    const int rt = wv < 4 ? wv : 7 - wv;
+    const int i0 = 16 * rt, c0 = 64 * (wv >> 2), jl = lane & 15, kq = lane >> 4;
+    // raw buffer over out's T x H x 128 floats (under 2 GiB, checked by the
+    // host, so offset 0x80000000 lies outside it); 0x00020000 is the gfx9
+    // descriptor word for 32-bit raw access
+    const __amdgpu_buffer_rsrc_t out_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(out, (short)0, (int)((unsigned)T * (unsigned)H * kD * 4u), 0x00020000);
     constexpr int NS = kD * kD / 4 / 512, NC = kC * kD / 4 / 512, NI = kC * kC / 4 / 512;
     v4f ps[NS], pc[NC], pd[NC], pi[NI];
     auto fetch = [&](int item) {  // item = chunk * H + head, the record's index
@@ -524,11 +538,7 @@ __global__ __launch_bounds__(512) void gdn_chunk_out_kernel(const float* __restr
 #pragma unroll
         for (int i = 0; i < NI; ++i) pi[i] = *(const v4f*)(rec + kOffIntra + 4 * (tid + 512 * i));
     };
-    fetch(blockIdx.x);  // the grid never exceeds the item count
-    for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
-        const int c = item / H, h = item - c * H;
-        const int t0 = c * kC, rows = min(kC, T - t0);
-        lds_barrier();  // every wave is done reading the previous item
+    auto stage = [&]() {
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
             const int f = tid + 512 * i;
@@ -545,7 +555,10 @@ __global__ __launch_bounds__(512) void gdn_chunk_out_kernel(const float* __restr
             const int f = tid + 512 * i;
             *(v4f*)&In[(f >> 4) * kApad + 4 * (f & 15)] = pi[i];
         }
-        lds_barrier();
+    };
+    auto item_body = [&](int item) {
+        const int c = item / H, h = item - c * H;
+        const int t0 = c * kC;
         fetch(min(item + (int)gridDim.x, nitems - 1));  // in flight during the products
         f4m oo[4], it[4];
 #pragma unroll
@@ -558,15 +571,14 @@ __global__ __launch_bounds__(512) void gdn_chunk_out_kernel(const float* __restr
 #pragma unroll
             for (int s = 0; s < kC / 4; ++s) ia[s] = In[(i0 + jl) * kApad + 4 * s + kq];
 #pragma unroll
-            for (int s0 = 0; s0 < kC / 4; s0 += 8) {
-                float cb[8][4];
+            for (int s0 = 0; s0 < kC / 4; s0 += 4) {
+                if (s0 >= 4 * (rt + 1)) break;  // keys past the tile's last row
+                v4f cb[4];
 #pragma unroll
-                for (int s = 0; s < 8; ++s)
-#pragma unroll
-                    for (int jt = 0; jt < 4; ++jt) cb[s][jt] = Cr[(4 * (s0 + s) + kq) * kPad + c0 + 16 * jt + jl];
+                for (int s = 0; s < 4; ++s) cb[s] = *(const v4f*)&Cr[(4 * (s0 + s) + kq) * kPad + c0 + 4 * jl];
                 __builtin_amdgcn_sched_barrier(0);  // a block of operand reads, then its MFMAs
 #pragma unroll
-                for (int s = 0; s < 8; ++s)
+                for (int s = 0; s < 4; ++s)
 #pragma unroll
                     for (int jt = 0; jt < 4; ++jt) oo[jt] = mfma4(ia[s0 + s], cb[s][jt], oo[jt]);
             }
@@ -577,11 +589,9 @@ __global__ __launch_bounds__(512) void gdn_chunk_out_kernel(const float* __restr
             for (int s = 0; s < kD / 4; ++s) da[s] = Dq[(i0 + jl) * kPad + 4 * s + kq];
 #pragma unroll
             for (int s0 = 0; s0 < kD / 4; s0 += 8) {
-                float sb[8][4];
+                v4f sb[8];
 #pragma unroll
-                for (int s = 0; s < 8; ++s)
-#pragma unroll
-                    for (int jt = 0; jt < 4; ++jt) sb[s][jt] = Sc[(4 * (s0 + s) + kq) * kPad + c0 + 16 * jt + jl];
+                for (int s = 0; s < 8; ++s) sb[s] = *(const v4f*)&Sc[(4 * (s0 + s) + kq) * kPad + c0 + 4 * jl];
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int s = 0; s < 8; ++s)
@@ -589,20 +599,40 @@ __global__ __launch_bounds__(512) void gdn_chunk_out_kernel(const float* __restr
                     for (int jt = 0; jt < 4; ++jt) it[jt] = mfma4(da[s0 + s], sb[s][jt], it[jt]);
             }
         }
+        // unconditional buffer stores: the rows past the prompt's end fall
+        // outside the buffer's range and the hardware drops them, so every
+        // item issues the same 4 stores and the wait for the next item's
+        // operands does not also wait for these
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
+        for (int r = 0; r < 4; ++r) {
+            const int t = t0 + i0 + 4 * kq + r;
+            v4f o4;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = i0 + 4 * kq + r;
-                if (t < rows) {
-                    float o = oo[jt][r] + it[jt][r];
-                    if (round_bf16) {
-                        const unsigned b = __float_as_uint(o);
-                        o = __uint_as_float((b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u);
-                    }
-                    out[((size_t)(t0 + t) * H + h) * kD + c0 + 16 * jt + jl] = o;
-                }
+            for (int jt = 0; jt < 4; ++jt) {
+                const float intra = 0.0f + oo[jt][r];
+                float o = intra + it[jt][r];
+                const unsigned b = __float_as_uint(o);
+                const float ob = __uint_as_float((b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u);
+                o4[jt] = round_bf16 ? ob : o;
             }
+            const unsigned at = (unsigned)((((size_t)t * H + h) * kD + c0 + 4 * jl) * 4);
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, o4), out_rsrc, (int)at, 0, 0);
+        }
+    };
+    // Each pass requests the next item's operands, forms and stores this
+    // item's outputs, then stages the next operands: the requests and the 4
+    // stores sit in one block in that order, so the wait before the staging
+    // covers the operands only (vmcnt(4)), not this item's stores.  The
+    // last pass re-requests and stages the last item (clamped), unused.
+    fetch(blockIdx.x);  // the grid never exceeds the item count
+    stage();
+    lds_barrier();
+    for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+        item_body(item);
+        lds_barrier();  // every wave is done reading this item
+        stage();
+        lds_barrier();
     }
 }
 
@@ -625,7 +655,7 @@ size_t gdn_chunk_scratch_bytes(size_t T, size_t H) { return ((T + kC - 1) / kC) 
 hipError_t gdn_chunk_prefill(const float* q, const float* k, const float* v, const float* beta, const float* logd,
                              size_t T, size_t H, float* state, float* out, float* scratch, bool key_major,
                              bool round_bf16, hipStream_t s) {
-    if (T == 0 || H == 0) return hipErrorInvalidValue;
+    if (T == 0 || H == 0 || T * H * kD * 4 >= ((size_t)1 << 31)) return hipErrorInvalidValue;
     const unsigned nch = (unsigned)((T + kC - 1) / kC);
     hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(nch, (unsigned)H), dim3(256), 0, s, q, k, beta, logd, (int)T,
                        (int)H, scratch);
