@@ -57,28 +57,12 @@ __device__ __forceinline__ f4m mfma4(float a, float b, f4m c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// 16x16 output tiles of X Y^T over K = kD (X, Y: rows of 128 in LDS with
-// pitch kPad), one MFMA chain each.  Lane l supplies X[i0 + l%16][4s + l/16]
-// and Y[j0 + l%16][4s + l/16]; result register r is
-// (i0 + 4(l/16) + r, j0 + l%16).  Operands are read into registers first so
-// that the chain does not wait on LDS between steps.
-__device__ __forceinline__ f4m tile_xyT(const float* X, const float* Y, int i0, int j0, int lane, float xscale_row) {
-    const float* xr = X + (i0 + (lane & 15)) * kPad + (lane >> 4);
-    const float* yr = Y + (j0 + (lane & 15)) * kPad + (lane >> 4);
-    float xa[kD / 4], yb[kD / 4];
-#pragma unroll
-    for (int s = 0; s < kD / 4; ++s) {
-        xa[s] = xr[4 * s] * xscale_row;
-        yb[s] = yr[4 * s];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    f4m acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int s = 0; s < kD / 4; ++s) acc = mfma4(xa[s], yb[s], acc);
-    return acc;
-}
-
-// Both products of a lower tile: (beta k) k^T and q k^T, interleaved.
+// Both products of a lower 16x16 tile over K = kD, (beta k) k^T and q k^T,
+// as two interleaved MFMA chains (rows of 128 in LDS with pitch kPad).
+// Lane l supplies row i0 + l%16 of beta k and q and row j0 + l%16 of k at
+// column 4s + l/16; result register r is (i0 + 4(l/16) + r, j0 + l%16).
+// Operands are read into registers first so that the chains do not wait on
+// LDS between steps.
 __device__ __forceinline__ void tile_pair(const float* Q, const float* K, int i0, int j0, int lane, float brow,
                                           f4m& a4, f4m& q4) {
     const float* kr = K + (i0 + (lane & 15)) * kPad + (lane >> 4);
@@ -185,10 +169,12 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const float* __rest
     __syncthreads();
 
     // A = (beta k) k^T and intra = q k^T, decayed by exp(g_t - g_s) on and
-    // below the diagonal (0 * the product above it, as the reference's
-    // exp(-inf) factor gives).  A is read only strictly below the diagonal,
-    // so its tiles above are skipped.  Lower tile pairs go round-robin over
-    // the waves, the six upper intra tiles to waves 2 and 3.
+    // below the diagonal (0 * the product above it within the diagonal
+    // tiles, as the reference's exp(-inf) factor gives).  Neither is read
+    // above the diagonal tiles (the solve reads A strictly below the
+    // diagonal, the output kernel's intra chains stop at each row tile's
+    // diagonal), so those tiles are neither formed nor written.  Lower tile
+    // pairs go round-robin over the waves.
     if (tid < kC) {
         const float last = gs[kC - 1];
         eg[tid] = cr_expf(gs[tid]);
@@ -210,17 +196,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(const float* __rest
             const float decay = s2 <= t ? cr_expf(gs[t] - gs[s2]) : 0.0f;
             rec[kOffA + t * kC + s2] = a4[r] * decay;
             rec[kOffIntra + t * kC + s2] = q4[r] * decay;
-        }
-    }
-    if (wv >= 2) {
-        for (int n = 3 * (wv - 2); n < 3 * (wv - 1); ++n) {
-            const int ti = n < 3 ? 0 : n < 5 ? 1 : 2;  // upper tiles (ti, tj), tj > ti
-            const int tj = ti + 1 + (n - (ti == 0 ? 0 : ti == 1 ? 3 : 5));
-            const int i0 = 16 * ti, j0 = 16 * tj;
-            const f4m q4 = tile_xyT(qs, ks, i0, j0, lane, 1.0f);
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                rec[kOffIntra + (i0 + 4 * (lane >> 4) + r) * kC + j0 + (lane & 15)] = q4[r] * 0.0f;
         }
     }
     __syncthreads();
@@ -502,8 +477,9 @@ __global__ __launch_bounds__(512) void gdn_chunk_scan_kernel(float* __restrict__
 // 64 (w / 4) .. +63, lane n of MFMA tile j holding column 64 (w / 4) + 4 n
 // + j: the two waves sharing a SIMD take tiles r and 3 - r, and a lane's
 // four columns are adjacent, read as one 16-byte word and stored as one.
-// The intra product's chain stops after key 16 r + 15: intra is zero past
-// the diagonal (the reference's pairwise decay is exp(-inf) there), so the
+// The intra product's chain stops after key 16 r + 15 (the record holds no
+// tiles above the diagonal ones): intra is zero past the diagonal (the
+// reference's pairwise decay is exp(-inf) there), so the
 // remaining steps add only zeros, which change no finite sum but a zero's
 // sign, and the reference's own `output += sum` into 0.0 (core.rs:288-318)
 // clears that sign too, as (0 + intra) + inter does here.
