@@ -246,7 +246,8 @@ int zg_attn_decode_split_device(zg_ctx* ctx, size_t rows, size_t q_heads, size_t
  * state value-major [heads][128 value][128 key] (the decode recurrence's
  * layout, lib.rs:81-83), updated in place; output f32 before rounding.
  * Inputs are not inspected on the host.  zg_gdn_chunk_scratch_bytes is the
- * size of the context-owned record buffer a call of this size uses. */
+ * size of the context-owned record buffer a call of this size uses.
+ * ZG_E_LIMIT when (tokens + 64) * heads * 512 bytes reaches 4 GiB. */
 size_t zg_gdn_chunk_scratch_bytes(size_t tokens, size_t heads);
 int zg_gdn_chunk_prefill_device(zg_ctx* ctx, size_t tokens, size_t heads, const float* query, const float* key,
                                 const float* value, const float* beta, const float* log_decay, float* state,

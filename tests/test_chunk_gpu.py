@@ -180,3 +180,16 @@ def test_prefill_long_state_properties(ctx, torch_cuda):
     assert np.array_equal(out, np.concatenate([o1, o2]))
     assert np.isfinite(out).all() and np.isfinite(st).all()
     assert float(np.abs(st).max()) < 1e3
+
+
+def test_prefill_device_refuses_oversized_output(ctx):
+    """(tokens + 64) * heads * 512 bytes of output at 4 GiB or more is
+    refused on the host with ZG_E_LIMIT before any device memory is read
+    (the output kernel's 32-bit buffer offsets, rows past the end included,
+    must not wrap).  The pointers are never dereferenced on the refused
+    call."""
+    fake = 256
+    tokens = (1 << 23) - 64  # (tokens + 64) * 1 head * 512 = 2^32
+    rc = L.lib().zg_gdn_chunk_prefill_device(ctx.h, tokens, 1, *([fake] * 7), None)
+    assert rc == L.E_LIMIT
+    assert "4 GiB" in ctx.error()

@@ -495,9 +495,10 @@ __global__ __launch_bounds__(512) void gdn_chunk_out_kernel(const float* __restr
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int rt = wv < 4 ? wv : 7 - wv;
     const int i0 = 16 * rt, c0 = 64 * (wv >> 2), jl = lane & 15, kq = lane >> 4;
-    // raw buffer over out's T x H x 128 floats (under 2 GiB, checked by the
-    // host, so offset 0x80000000 lies outside it); 0x00020000 is the gfx9
-    // descriptor word for 32-bit raw access
+    // raw buffer over out's T x H x 128 floats; the host checks that even
+    // the last chunk's rows past T have byte offsets below 2^32 (unsigned
+    // 32-bit offsets that cannot wrap back into range); 0x00020000 is the
+    // gfx9 descriptor word for 32-bit raw access
     const __amdgpu_buffer_rsrc_t out_rsrc =
         __builtin_amdgcn_make_buffer_rsrc(out, (short)0, (int)((unsigned)T * (unsigned)H * kD * 4u), 0x00020000);
     constexpr int NS = kD * kD / 4 / 512, NC = kC * kD / 4 / 512, NI = kC * kC / 4 / 512;
@@ -631,7 +632,7 @@ size_t gdn_chunk_scratch_bytes(size_t T, size_t H) { return ((T + kC - 1) / kC) 
 hipError_t gdn_chunk_prefill(const float* q, const float* k, const float* v, const float* beta, const float* logd,
                              size_t T, size_t H, float* state, float* out, float* scratch, bool key_major,
                              bool round_bf16, hipStream_t s) {
-    if (T == 0 || H == 0 || T * H * kD * 4 >= ((size_t)1 << 31)) return hipErrorInvalidValue;
+    if (T == 0 || H == 0 || (T + kC) * H * kD * 4 >= ((size_t)1 << 32)) return hipErrorInvalidValue;
     const unsigned nch = (unsigned)((T + kC - 1) / kC);
     hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(nch, (unsigned)H), dim3(256), 0, s, q, k, beta, logd, (int)T,
                        (int)H, scratch);

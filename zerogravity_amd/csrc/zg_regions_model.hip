@@ -192,6 +192,8 @@ int zg_gdn_chunk_prefill_device(zg_ctx* ctx, size_t tokens, size_t heads, const 
     if (!query || !key || !value || !beta || !log_decay || !state || !output || tokens == 0 || heads == 0 ||
         tokens > (1u << 24) || heads > 4096)
         return fail(ctx, ZG_E_MALFORMED, "chunk prefill geometry");
+    if ((tokens + 64) * heads * 128 * 4 >= ((size_t)1 << 32))
+        return fail(ctx, ZG_E_LIMIT, "chunk output (with one chunk of padding) of 4 GiB or more");
     hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
     const size_t need = zg::gdn_chunk_scratch_bytes(tokens, heads);
     if (ctx->chunkbuf.bytes < need) ZG_HIP(hipStreamSynchronize(st));
