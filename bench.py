@@ -176,49 +176,124 @@ def run_decode(model, torch, B, prefix, steps, warmup, seed):
     return total_ms, per
 
 
+# Prologue / epilogue codes of zg_gemv_device_fused (include/zg_hip.h)
+PRO_RMS, PRO_GATED, PRO_SILU_MUL, PRO_PLAIN = 0, 1, 2, 3
+EPI_STORE, EPI_RESID, EPI_GLU = 0, 1, 2
+
+
+def step_projections(g):
+    """The B=1 decode step's projections in launch order, each with the
+    prologue and epilogue the step runs it with (zg_session.hip step(), an
+    all-Q4_K model): (label, [names stacked by rows], K, N, prologue,
+    epilogue, role).  role: "embed" the first input projection (the token's
+    embedding dequantised in its prologue), "lm" the LM head (greedy
+    partials), "" otherwise."""
+    H, F, V = g["hidden"], g["ffn"], g["vocab"]
+    W = g["gdn_heads"] * g["gdn_dim"]
+    QD, KD = g["q_heads"] * g["head_dim"], g["kv_heads"] * g["head_dim"]
+    out = []
+    for i in range(g["layers"]):
+        p = f"blk.{i}."
+        role = "embed" if i == 0 else ""
+        if (i + 1) % g["full_attention_interval"] == 0:
+            out.append((p + "attn_in", [p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"], H,
+                        2 * QD + 2 * KD, PRO_RMS, EPI_STORE, role))
+            out.append((p + "attn_output", [p + "attn_output.weight"], QD, H, PRO_PLAIN, EPI_RESID, ""))
+        else:
+            out.append((p + "gdn_in", [p + "attn_qkv.weight", p + "attn_gate.weight", p + "ssm_alpha.weight",
+                                       p + "ssm_beta.weight"], H, 4 * W + 2 * g["gdn_heads"], PRO_RMS, EPI_STORE,
+                        role))
+            out.append((p + "ssm_out", [p + "ssm_out.weight"], W, H, PRO_GATED, EPI_RESID, ""))
+        out.append((p + "ffn_gate_up", [p + "ffn_gate.weight", p + "ffn_up.weight"], H, 2 * F, PRO_RMS, EPI_GLU,
+                    ""))
+        out.append((p + "ffn_down", [p + "ffn_down.weight"], F, H, PRO_PLAIN, EPI_RESID, ""))
+    out.append(("token_embd", ["token_embd.weight"], H, V, PRO_RMS, EPI_STORE, "lm"))
+    return out
+
+
 def gemv_leg(kern, torch, g, tensors, kind, reps):
-    """The dominant kernel: the Q4_K GEMV launches of one B=1 decode step --
-    the same stacked matrices through the same one-row kernel
-    (gemv1_q4k_kernel: RMSNorm prologue in-kernel on an f32 activation, int8
-    matrix cores) -- replayed `reps` times with HIP events around each
-    replay.  ~0.95 GB per replay, so nothing is served from the 256 MB
-    Infinity Cache."""
+    """The dominant kernel: the Q4_K projections of one B=1 decode step,
+    replayed exactly as the step launches them -- the same stacked matrices,
+    the same prologue and epilogue per projection (zg_gemv_device_fused ->
+    the step's own dispatcher, so the same kernel template variants: the
+    embedding prologue on the first, the gated RMSNorm on ssm_out, SwiGLU
+    into the down projection's input, residual adds, greedy partials on the
+    LM head) -- captured once in a HIP graph as the step is, and the graph
+    replayed `reps` times between HIP events on its stream.  ~0.95 GB per
+    replay, so the weights stream from HBM, not the 256 MB Infinity Cache.
+    The GDN, attention and argmax launches between them are not replayed:
+    the leg times the projection kernel alone."""
     from zerogravity_amd import _lib as L
     lib, ctx = L.lib(), kern.ctx
-    handles = []
-    for label, names, K, N in decode_matrices(g):
+    H, F, V = g["hidden"], g["ffn"], g["vocab"]
+    W = g["gdn_heads"] * g["gdn_dim"]
+    plan = step_projections(g)
+    handles = {}
+    embd = None
+    for label, names, K, N, pro, epi, role in plan:
         parts = [tensors[n] for n in names]
         assert all(p[0] == kind and p[1] == K for p in parts), label
-        data = np.concatenate([p[3] for p in parts])
-        handles.append((kern.register(4243, "leg." + label, kind, K, N, data), K, N))
-    s = torch.cuda.current_stream()
+        h = kern.register(4243, "leg." + label, kind, K, N, np.concatenate([p[3] for p in parts]))
+        handles[label] = h
+        if role == "lm":
+            embd = h
     rng = np.random.default_rng(7)
-    xs = {}
-    for _, K, _ in handles:
-        if K not in xs:
-            xs[K] = (torch.from_numpy(rng.standard_normal(K).astype(np.float32)).cuda(),
-                     torch.from_numpy((1 + 0.1 * rng.standard_normal(K)).astype(np.float32)).cuda())
-    y = torch.empty(max(N for _, _, N in handles), dtype=torch.float32, device="cuda")
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    ymax = max(N for _, _, _, N, _, _, _ in plan)
+    bufs = dict(x=dev(rng.standard_normal(H)), x_emb=dev(np.zeros(H)), gamma=dev(1 + 0.1 * rng.standard_normal(F)),
+                core=dev(rng.standard_normal(W)), z=dev(rng.standard_normal(W)),
+                norm=dev(1 + 0.1 * rng.standard_normal(g["gdn_dim"])), glu=dev(rng.standard_normal(F)),
+                attn=dev(rng.standard_normal(g["q_heads"] * g["head_dim"])),
+                resid=dev(rng.standard_normal(H)), y=torch.empty(ymax, dtype=torch.float32, device="cuda"),
+                logits=torch.empty(V, dtype=torch.float32, device="cuda"))
+    tok = torch.tensor([1234], dtype=torch.int32, device="cuda")
+    parts = int(lib.zg_gemv_greedy_parts(embd.h))
+    gmax = torch.empty(max(parts, 1), dtype=torch.float32, device="cuda")
+    gidx = torch.empty(max(parts, 1), dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
 
-    def replay():
-        for h, K, N in handles:
-            x_d, g_d = xs[K]
-            ctx.check(lib.zg_gemv_device(ctx.h, h.h, x_d.data_ptr(), L.F32, 1, g_d.data_ptr(), 1e-6, y.data_ptr(),
-                                         s.cuda_stream))
+    def launch(s):
+        for label, names, K, N, pro, epi, role in plan:
+            h = handles[label]
+            x, x2, gam, y, ldy = bufs["x"], None, bufs["gamma"], bufs["y"], N
+            emb, tk, gm, gi = None, None, None, None
+            if role == "embed":
+                x, emb, tk = bufs["x_emb"], embd.h, tok.data_ptr()
+            if label.endswith("ssm_out"):
+                x, x2, gam = bufs["core"], bufs["z"], bufs["norm"]
+            elif label.endswith("attn_output"):
+                x, gam = bufs["attn"], None
+            elif label.endswith("ffn_down"):
+                x, gam = bufs["glu"], None
+            if epi == EPI_RESID:
+                y, ldy = bufs["resid"], H
+            elif epi == EPI_GLU:
+                y, ldy = bufs["glu"], N // 2
+            if role == "lm":
+                y, gm, gi = bufs["logits"], gmax.data_ptr(), gidx.data_ptr()
+            ctx.check(lib.zg_gemv_device_fused(ctx.h, h.h, 1, pro, epi, x.data_ptr(), K,
+                                               None if x2 is None else x2.data_ptr(), 0 if x2 is None else W,
+                                               None if gam is None else gam.data_ptr(), 1e-6, g["gdn_dim"],
+                                               y.data_ptr(), ldy, emb, tk, gm, gi, s.cuda_stream))
 
-    replay()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch(torch.cuda.current_stream())
+    s = torch.cuda.current_stream()
+    graph.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(s)
     for _ in range(reps):
-        replay()
+        graph.replay()
     e1.record(s)
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / reps
-    byts = sum(gemv_bytes(kind, N, K, 1) for _, K, N in handles)
+    byts = sum(gemv_bytes(kind, N, K, 1) for _, _, K, N, _, _, _ in plan)
+    del graph
     kern.release_source(4243)
-    return dict(launches=len(handles), us_per_step=us, us_per_launch=us / len(handles),
-                bytes_per_launch=byts / len(handles), gbs=byts / us / 1e3)
+    return dict(launches=len(plan), us_per_step=us, us_per_launch=us / len(plan),
+                bytes_per_launch=byts / len(plan), gbs=byts / us / 1e3)
 
 
 def gdn_bytes(B, H=16, dk=128, dv=128):
@@ -406,8 +481,9 @@ def bench_decode(args):
         "value": round(res[1]["tok_s"], 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(res[1]["ms_per_step"], 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "q4_k weights, f32 accumulate",
-        "dtype_detail": {"b1": "Q4_K codes and int16-coded activations (per-row amax, split into two signed "
-                               "bytes) on int8 MFMA, i32 partials scaled and summed in f32",
+        "dtype_detail": {"b1": "Q4_K codes and int16-coded activations (scale per 32-element group from its "
+                               "largest magnitude, each code split into two signed bytes) on int8 MFMA, i32 "
+                               "partials scaled and summed in f32",
                          "b32": "Q4_K weights dequantised to f16 tiles, f16 activations, f16 MFMA with f32 "
                                 "accumulate",
                          "state": "f32 GDN state and accumulators, bf16 KV cache"},
@@ -418,7 +494,8 @@ def bench_decode(args):
                    "attention_decode_leg": attn},
         "roofline": {"bound": "hbm", "achieved": round(leg["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(leg["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel": "gemv1_q4k_kernel (the B=1 decode step's 97 stacked Q4_K projections, one launch each, RMSNorm/gate prologue and residual/SwiGLU epilogue fused)",
+                     "kernel": "gemv1_q4k_kernel (the B=1 decode step's 97 stacked Q4_K projections replayed "
+                               "as the step launches them: same prologue/epilogue variants, one HIP graph)",
                      "bytes_per_launch": round(leg["bytes_per_launch"]), "us_per_launch": round(leg["us_per_launch"], 3)},
     }
     if not args.no_cpu:
@@ -788,51 +865,6 @@ def bench_copy(args):
             "config": {"workload": "calibration copy", "bytes_read": n * 4, "bytes_written": n * 4}}
 
 
-def bench_floors(args):
-    """The floors the decode step's design rests on, from libzg_probe.so
-    (kernels that only measure; nothing on the hot path calls them):
-    a graph chain of dependent launches vs the same dependency handed over
-    inside one persistent cooperative kernel, GEMV-shaped launches of the
-    decode step's weight sizes, and in-place read-modify-write."""
-    import ctypes
-    import torch
-    torch.cuda.init()
-    lib = ctypes.CDLL(os.path.join(ROOT, "zerogravity_amd", "libzg_probe.so"))
-    f = ctypes.c_float()
-    out = {"chain_us": {}, "handoff_us": {}, "stream_us": {}, "rmw_gbs": {}}
-
-    def call(fn, *a):
-        rc = fn(*a, ctypes.byref(f))
-        if rc < 0:
-            raise RuntimeError(f"{fn.__name__} failed ({rc})")
-        return rc, round(f.value, 3)
-
-    lib.zg_probe_stream.argtypes = [ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
-    lib.zg_probe_rmw.argtypes = [ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
-    for wgs in (8, 64, 256):
-        for N in (2048, 6144):
-            out["chain_us"][f"{wgs}wg_{N}"] = call(lib.zg_probe_chain, wgs, N, 512)[1]
-            log(f"chain {wgs} WGs N={N}: {out['chain_us'][f'{wgs}wg_{N}']} us/phase")
-    for mode, name in ((0, "ll_words"), (1, "counter_agent"), (2, "counter_fenced")):
-        for wgs in (8, 64, 256):
-            rc, us = call(lib.zg_probe_handoff, mode, wgs, 2048, 512)
-            out["handoff_us"][f"{name}_{wgs}wg"] = us if rc == 0 else None
-            log(f"handoff {name} {wgs} WGs: {us} us/phase" + (" (a bounded wait expired: void)" if rc else ""))
-    for mb in (1.2, 2.4, 4.7, 7.1, 14.2, 78.0):
-        b = int(mb * 1e6) // 4096 * 4096
-        wgs = max(256, min(4096, b // (256 * 16 * 4)))
-        out["stream_us"][f"{mb}MB"] = us = call(lib.zg_probe_stream, b, wgs, 200)[1]
-        log(f"stream {mb} MB: {us} us/launch = {b / us / 1e3:.0f} GB/s")
-    for mb in (1, 4, 16, 64, 256):
-        out["rmw_gbs"][f"{mb}MB"] = v = call(lib.zg_probe_rmw, mb << 20, 64)[1]
-        log(f"rmw {mb} MiB: {v} GB/s")
-    chain = out["chain_us"]["256wg_2048"]
-    return {"metric": "dependent-launch floor, us per phase (graph chain, 256 WGs, 2048 floats)", "value": chain,
-            "unit": "us", "n_gpus": 1, "steps": 512, "warmup": 1, "ms_per_step": round(chain / 1e3, 6),
-            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-            "config": {"workload": "launch and hand-off floors", **out}}
-
-
 def cpu_gdn_baseline(seconds, H=16):
     """The oracle's GDN decode step at B=1 (conv over 3 x 2048 channels, SiLU,
     two-stage q/k L2, gates, the 16-head recurrence; one host thread, serial
@@ -945,7 +977,7 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "decode_q8", "decode_mixed", "gemv", "prefill", "gdn", "model_prefill", "copy", "config1", "floors"])
+                    choices=["decode", "decode_q8", "decode_mixed", "gemv", "prefill", "gdn", "model_prefill", "copy", "config1"])
     ap.add_argument("--prefix", type=int, default=2048)
     ap.add_argument("--leg-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -957,8 +989,7 @@ def main():
         sys.exit(2)
     bench = {"decode": bench_decode, "decode_q8": bench_decode_q8,
              "decode_mixed": lambda a: bench_decode_q8(a, mixed=True), "gemv": bench_gemv, "prefill": bench_prefill, "gdn": bench_gdn,
-             "model_prefill": bench_model_prefill, "copy": bench_copy, "config1": bench_config1,
-             "floors": bench_floors}[args.workload]
+             "model_prefill": bench_model_prefill, "copy": bench_copy, "config1": bench_config1}[args.workload]
     line = bench(args)
     print(json.dumps(line), flush=True)
 

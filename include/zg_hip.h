@@ -306,6 +306,30 @@ typedef struct zg_geometry { /* ModelGeometry, model-qwen35/src/config.rs:51-182
     float eps;                            /* 1e-6 (lib.rs:505) */
 } zg_geometry;
 
+/* Numerical profiles a ForwardPlan carries, in the order of
+ * ProgramNumericalProfile (core/src/numerics.rs:30-40). */
+enum {
+    ZG_PROFILE_GGUF_SOURCE_V1 = 0,
+    ZG_PROFILE_TORCH_CPU_BF16_AVX2_MIXED_SOURCE_V1 = 1,
+    ZG_PROFILE_SOURCE_CUDA_SM86_BF16_V1 = 2,
+    ZG_PROFILE_ANALYTIC_F32_TEXT_V1 = 3,
+    ZG_PROFILE_DIRECT_GAMMA_BF16_TEXT_CANDIDATE_V1 = 4
+};
+
+/* Admission of a plan before any device work: whether its numerical profile
+ * (ForwardPlan::numerical_profile, core/src/accelerator/program/
+ * source_program.rs:1178) and tensor table are the schedule this backend
+ * runs.  Only ZG_PROFILE_GGUF_SOURCE_V1 is, as LoadedQwenModel::
+ * require_execution_profile admits only GgufSourceV1 (model-qwen35/src/
+ * source/binding.rs:363-371); a provider prepares whatever plan it is given
+ * (core/src/provider.rs:38-42), so the refusal is made here.  Host only: no
+ * context, no device.  ZG_COMPLETED; ZG_E_UNSUPPORTED for another profile,
+ * a geometry outside the schedule or a codec the role's kernels do not
+ * take; ZG_E_MALFORMED for a missing tensor, a shape that differs from the
+ * geometry or a wrong packed length.  The reason goes to msg (msg_len bytes,
+ * NUL-terminated; may be NULL).  zg_model_load applies the same check. */
+int zg_model_admit(int profile, const zg_geometry* geometry, const zg_tensor_desc* tensors, size_t n_tensors,
+                   char* msg, size_t msg_len);
 int zg_model_load(zg_ctx* ctx, uint64_t source_id, const zg_geometry* geometry, const zg_tensor_desc* tensors,
                   size_t n_tensors, zg_model** out);
 void zg_model_destroy(zg_model* model);
@@ -338,7 +362,9 @@ int zg_session_copy_row(zg_session* s, size_t dst, size_t src);
  * commit publishes it, prefill_transaction installs its state only if every
  * token succeeds; lib.rs:1057-1070, 1114-1187, 1211-1225).  A failure that
  * leaves the device state unknown (a HIP launch error, ZG_E_DEVICE) poisons
- * the session until reset, import or restore.
+ * the session: every row is marked unknown, and the session refuses work
+ * until each marked row has been reset (zg_session_reset_row), restored or
+ * imported, or the whole session reset.
  *
  * One forward_token for rows [0, rows): tokens[rows] host ids, logits
  * [rows][vocab] and/or greedy [rows] (first maximum, numerics.rs:126-140)
@@ -363,7 +389,12 @@ int zg_prefill(zg_session* s, size_t rows, size_t n, const uint32_t* tokens, flo
  * appending to the KV cache).  Logits of the last token to host when
  * non-NULL.  Same functions as zg_prefill in another order of summation;
  * needs Q4_K projections (ZG_E_UNSUPPORTED otherwise).  Atomic: a failure
- * leaves the row's published state as it was. */
+ * leaves the row's published state as it was, and the other rows' state and
+ * positions untouched.  ZG_E_LIMIT when an operand of the prompt's
+ * projections would reach 4 GiB (32-bit offsets: 32-row f16 activation
+ * tiles of n x K, e.g. n >= 349,526 at K = 6144), or when the chunked GDN
+ * prefill's output would (zg_gdn_chunk_prefill_device); split such a
+ * prompt over several calls. */
 int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* tokens, float* logits);
 /* Device-side step: d_tokens/d_logits/d_greedy are device pointers, no host
  * synchronisation.  The step's last kernel publishes it only if the status
@@ -396,6 +427,9 @@ void zg_snapshot_destroy(zg_snapshot* snap);
  * values (token-major, f32). */
 size_t zg_state_floats(const zg_session* s, size_t row);
 int zg_state_export(zg_session* s, size_t row, float* out, size_t n);
+/* The row takes the image and position (published GDN half 0), or on a
+ * refusal (length, nonfinite value) or an allocation failure nothing
+ * changes; a device copy failing midway poisons the session. */
 int zg_state_import(zg_session* s, size_t row, const float* in, size_t n, int position);
 /* Seeded synthetic prefix for benchmarking: rows [0, rows) get `prefix`
  * random tokens of KV (N(0,1)), recurrent state N(0,0.02) and conv history
@@ -419,6 +453,40 @@ int zg_session_fill_random(zg_session* s, size_t rows, size_t prefix, uint64_t s
 int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows,
                    const float* gamma, float eps, float* y, void* stream);
 
+/* Prologue and epilogue forms of the decode step's projections. */
+enum { ZG_PRO_RMS = 0, ZG_PRO_GATED = 1, ZG_PRO_SILU_MUL = 2, ZG_PRO_PLAIN = 3 };
+enum { ZG_EPI_STORE = 0, ZG_EPI_RESID = 1, ZG_EPI_GLU = 2 };
+
+/* One projection of the resident decode step with the operations around it
+ * fused, on the kernels the step itself launches, for 1..4 f32 activation
+ * rows x[m][0:K] (device memory, row stride ldx; the caller's stream,
+ * asynchronous):
+ *   prologue ZG_PRO_RMS       RMSNorm(x, gamma, eps) (model-qwen35/src/lib.rs:263-284)
+ *            ZG_PRO_GATED     grouped RMSNorm(x, gamma[group], eps) * silu(x2) (forward.rs:586-594)
+ *            ZG_PRO_SILU_MUL  x2 * silu(x) (forward.rs:498)
+ *            ZG_PRO_PLAIN     x
+ *   epilogue ZG_EPI_STORE     y = W a
+ *            ZG_EPI_RESID     y = y + W a, the residual add (forward.rs:489,501)
+ *            ZG_EPI_GLU       w stacks [gate | up] (N even): y[0:N/2] = up * silu(gate)
+ * For one row also: `embedding` (a Q4_K token_embd of width K) with `token`
+ * (device, one id): the activation is that token's embedding row,
+ * dequantised in the prologue and also stored at x (the step's residual
+ * stream; ZG_PRO_RMS); `greedy_max`/`greedy_idx` (device,
+ * zg_gemv_greedy_parts(w) entries; ZG_PRO_RMS with ZG_EPI_STORE): each
+ * workgroup's largest output and its first index (greedy_finite,
+ * core/src/numerics.rs:126-140, over the workgroup's outputs).  The
+ * arithmetic is the decode step's (Q4_K within 1e-3 relative of the CPU,
+ * the other codecs bit-identical).  ZG_UNSUPPORTED for a shape without
+ * such a kernel.  No counterpart in the reference beyond the regions it
+ * fuses; the form a whole-program provider composes its step from. */
+int zg_gemv_device_fused(zg_ctx* ctx, const zg_weight* w, size_t m_rows, int prologue, int epilogue, float* x,
+                         size_t ldx, const float* x2, size_t ldx2, const float* gamma, float eps, size_t group,
+                         float* y, size_t ldy, const zg_weight* embedding, const uint32_t* token, float* greedy_max,
+                         int32_t* greedy_idx, void* stream);
+/* Workgroup partials zg_gemv_device_fused leaves for greedy readout of one
+ * row through w (0: w takes another kernel and offers none). */
+size_t zg_gemv_greedy_parts(const zg_weight* w);
+
 /* zg_gemv_device without any allocation: no counterpart in the reference;
  * for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
@@ -428,8 +496,12 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
  * activation within 4 MiB (ZG_E_LIMIT otherwise); Q4_K with f32 input and
  * more than 4 rows needs the weight's batched tile layout, which one
  * zg_gemv_device call with more than 4 rows builds (ZG_E_STATE otherwise).
- * Every call on a device shares that device's array: calls that overlap on
- * one GPU (two streams, two threads with different contexts) race. */
+ * Every call on a device shares that device's array, which keeps the last
+ * call's contents.  Calls are ordered on it: each waits on an event the
+ * previous call on that device (any stream, thread or context) recorded
+ * after its kernels.  A call made while its stream is captured into a graph
+ * is ordered only by the graph's own stream order: replaying that graph
+ * while other calls use the array on the same GPU races. */
 int zg_gemv_device_noalloc(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows,
                            const float* gamma, float eps, float* y, void* stream);
 

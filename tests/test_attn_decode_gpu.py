@@ -156,10 +156,31 @@ def test_attn_decode_split_matches_oracle(ctx, kv, max_ctx, positions):
     print(f"split attention kv={kv} max_ctx={max_ctx}: worst rel {max(float(np.max(np.abs(got[b] - r)) / np.max(np.abs(r))) for b, r in enumerate(refs)):.2e}")
 
 
+def _refusal_buffers(rows, q_heads, kv_heads, max_ctx):
+    """Device buffers as large as a launch with these arguments would touch
+    (f32 caches cover bf16 too), so a refusal test whose host check
+    regressed reads and writes in bounds and fails instead of faulting."""
+    import torch
+    stride = 2 * q_heads * 256 + 2 * kv_heads * 256
+    bufs = dict(proj=torch.zeros(rows * stride, dtype=torch.float32, device="cuda"),
+                qn=torch.zeros(256, dtype=torch.float32, device="cuda"),
+                kn=torch.zeros(256, dtype=torch.float32, device="cuda"),
+                pos=torch.zeros(rows, dtype=torch.int32, device="cuda"),
+                kc=torch.zeros(rows * max(max_ctx, 1) * kv_heads * 256, dtype=torch.float32, device="cuda"),
+                vc=torch.zeros(rows * max(max_ctx, 1) * kv_heads * 256, dtype=torch.float32, device="cuda"),
+                ws=torch.zeros(64 << 20, dtype=torch.uint8, device="cuda"),
+                out=torch.zeros(rows * q_heads * 256, dtype=torch.float32, device="cuda"))
+    torch.cuda.synchronize()
+    return stride, bufs
+
+
 def test_attn_decode_split_refuses_more_than_64_rows(ctx):
     assert L.lib().zg_attn_decode_split_workspace_bytes(65, 8, 2, 2048) == 0
-    rc = L.lib().zg_attn_decode_split_device(ctx.h, 65, 8, 2, 1, 8192, 1, 1, 1e-6, 0.6, 1, 1, 1, 2048, L.BF16, 1, 1,
-                                             None)
+    stride, b = _refusal_buffers(65, 8, 2, 64)
+    rc = L.lib().zg_attn_decode_split_device(ctx.h, 65, 8, 2, b["proj"].data_ptr(), stride, b["qn"].data_ptr(),
+                                             b["kn"].data_ptr(), 1e-6, 0.6, b["pos"].data_ptr(), b["kc"].data_ptr(),
+                                             b["vc"].data_ptr(), 64, L.BF16, b["ws"].data_ptr(),
+                                             b["out"].data_ptr(), None)
     assert rc == L.E_LIMIT
 
 
@@ -167,6 +188,9 @@ def test_attn_decode_device_refusals(ctx):
     for bad in (dict(q_heads=6, kv_heads=4), dict(q_heads=10, kv_heads=2), dict(max_ctx=0), dict(kv_dtype=8)):
         args = dict(q_heads=8, kv_heads=2, max_ctx=64, kv_dtype=L.BF16)
         args.update(bad)
-        rc = L.lib().zg_attn_decode_device(ctx.h, 1, args["q_heads"], args["kv_heads"], 1, 8192, 1, 1, 1e-6, 0.6,
-                                           1, 1, 1, args["max_ctx"], args["kv_dtype"], 1, 1, None)
+        stride, b = _refusal_buffers(1, args["q_heads"], args["kv_heads"], args["max_ctx"])
+        rc = L.lib().zg_attn_decode_device(ctx.h, 1, args["q_heads"], args["kv_heads"], b["proj"].data_ptr(), stride,
+                                           b["qn"].data_ptr(), b["kn"].data_ptr(), 1e-6, 0.6, b["pos"].data_ptr(),
+                                           b["kc"].data_ptr(), b["vc"].data_ptr(), args["max_ctx"],
+                                           args["kv_dtype"], b["ws"].data_ptr(), b["out"].data_ptr(), None)
         assert rc == L.E_MALFORMED, bad

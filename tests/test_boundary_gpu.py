@@ -120,6 +120,47 @@ def test_failed_step_and_prefill_publish_nothing(kern, fragile):
     m.close()
 
 
+def test_failed_batched_prefill_keeps_other_rows(kern, fragile):
+    """A batched prefill that fails on one row (its f16 projections overflow
+    on every token of this model) leaves the other rows as the host has
+    them, including a row imported since the last step, whose host position
+    and published GDN half are newer than the device's copies."""
+    m = qwen35.QwenModelHip(TINY, fragile, kernel=kern)
+    donor = m.session(max_batch=1, max_context=256, kv_dtype=L.F32)
+    for i in range(2):
+        donor.forward(_probe(donor, True, 53 * i + 7))
+    image = donor.state()
+    s = m.session(max_batch=2, max_context=256, kv_dtype=L.F32)
+    for i in range(3):  # row 0 steps: its position and published half move on the device
+        s.forward(_probe(s, True, 91 * i + 5))
+    s.load_state(image, 2, row=0)
+    with pytest.raises(L.ZgError):
+        s.prefill_batched([1, 2, 3], row=1)
+    assert s.positions() == [2, 0]
+    assert np.array_equal(s.state(0).view(np.uint32), image.view(np.uint32))
+    # row 0 decodes as the donor does
+    t = _probe(donor, True, 400)
+    assert np.array_equal(s.forward(t).view(np.uint32), donor.forward(t).view(np.uint32))
+    m.close()
+
+
+def test_batched_prefill_refuses_32bit_operands(kern):
+    """An operand of the prompt GEMM reaching 4 GiB (here the f16 activation
+    tiles of the FFN down projection, 262144 rows x K = 8192) is ZG_E_LIMIT
+    before any projection runs; the session is untouched."""
+    g = dict(TINY, ffn=8192, max_context=262400)
+    m = qwen35.QwenModelHip(g, qwen35.synthetic_tensors(g, gguf.Q4_K, seed=33), kernel=kern)
+    s = m.session(max_batch=1, max_context=262400, kv_dtype=L.BF16)
+    with pytest.raises(L.ZgError) as e:
+        s.prefill_batched(np.ones(262144, np.uint32))
+    assert e.value.code == L.E_LIMIT
+    assert s.position == 0
+    assert np.all(s.state() == 0.0)
+    s.forward(1)
+    assert s.position == 1
+    m.close()
+
+
 def test_propose_and_commit(kern, tiny):
     m = qwen35.QwenModelHip(TINY, tiny, kernel=kern)
     s = m.session(max_batch=2, max_context=64, kv_dtype=L.F32)

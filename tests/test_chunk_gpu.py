@@ -186,10 +186,20 @@ def test_prefill_device_refuses_oversized_output(ctx):
     """(tokens + 64) * heads * 512 bytes of output at 4 GiB or more is
     refused on the host with ZG_E_LIMIT before any device memory is read
     (the output kernel's 32-bit buffer offsets, rows past the end included,
-    must not wrap).  The pointers are never dereferenced on the refused
-    call."""
-    fake = 256
+    must not wrap).  The buffers are allocated at the full size the call
+    names (16 GiB in all), so a regression of the host check would compute
+    in bounds and fail this test instead of faulting."""
+    import torch
     tokens = (1 << 23) - 64  # (tokens + 64) * 1 head * 512 = 2^32
-    rc = L.lib().zg_gdn_chunk_prefill_device(ctx.h, tokens, 1, *([fake] * 7), None)
+    qkv = [torch.empty(tokens * 128, dtype=torch.float32, device="cuda") for _ in range(3)]
+    beta = torch.zeros(tokens, dtype=torch.float32, device="cuda")
+    logd = torch.zeros(tokens, dtype=torch.float32, device="cuda")
+    state = torch.zeros(128 * 128, dtype=torch.float32, device="cuda")
+    out = torch.empty((tokens + 64) * 128, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    rc = L.lib().zg_gdn_chunk_prefill_device(ctx.h, tokens, 1, *[t.data_ptr() for t in qkv], beta.data_ptr(),
+                                             logd.data_ptr(), state.data_ptr(), out.data_ptr(), None)
     assert rc == L.E_LIMIT
     assert "4 GiB" in ctx.error()
+    del qkv, out
+    torch.cuda.empty_cache()

@@ -62,52 +62,76 @@ def _seeded_state(g, prefix, seed):
     return np.concatenate(parts)
 
 
-@pytest.mark.parametrize("B,checked", [(1, (0,)), (32, (0, 9, 18, 31))])
-def test_config5_2b_q4k_decode_from_2048_prefix(model_2b, B, checked):
+STEPS = 128  # 128 greedy steps
+CHECKED = {1: (0,), 32: (0, 4, 9, 13, 18, 22, 27, 31)}
+_RUNS = {}
+
+
+def _device_run(model_2b, B):
+    """The device's 128 greedy steps at B rows from the seeded 2048-token
+    state, the device greedy feeding the next step (zg_decode_step_device);
+    logits of the checked rows and every row's greedy token per step.  Run
+    once per B and shared by the tests that check its rows."""
+    if B in _RUNS:
+        return _RUNS[B]
     import torch
     g, t = model_2b
-    prefix, steps, nstate = 2048, 16, 8
+    prefix, nstate = 2048, 8
     kern = R.HipMatVecKernel(0)
     m = qwen35.QwenModelHip(g, t, kernel=kern)
-    s = m.session(max_batch=B, max_context=prefix + steps + 8, kv_dtype=L.BF16)
+    s = m.session(max_batch=B, max_context=prefix + STEPS + 8, kv_dtype=L.BF16)
     states = [_seeded_state(g, prefix, 100 + i) for i in range(min(B, nstate))]
     for r in range(B):
         s.load_state(states[r % nstate], prefix, row=r)
-    rng = np.random.default_rng(B)
-    first = rng.integers(0, g["vocab"], B).astype(np.uint32)
-    oracle = O.Model(g, t)
-    sess = {}
-    for r in checked:
-        o = oracle.session(kv_bf16=True)
-        o.load_state(states[r % nstate], prefix)
-        sess[r] = o
+    first = np.random.default_rng(B).integers(0, g["vocab"], B).astype(np.uint32)
     d_tok = torch.from_numpy(first.view(np.int32).copy()).cuda()
     d_logits = torch.empty((B, g["vocab"]), dtype=torch.float32, device="cuda")
     d_greedy = torch.empty(B, dtype=torch.int32, device="cuda")
-    ref_tok = {r: int(first[r]) for r in checked}
+    rows = list(CHECKED[B])
+    logits = np.empty((STEPS, len(rows), g["vocab"]), np.float32)
+    greedy = np.empty((STEPS, B), np.uint32)
+    for step in range(STEPS):
+        torch.cuda.synchronize()
+        kern.ctx.check(L.lib().zg_decode_step_device(s.h, B, d_tok.data_ptr(), d_logits.data_ptr(),
+                                                     d_greedy.data_ptr(), None))
+        kern.ctx.check(L.lib().zg_session_check(s.h, None))
+        logits[step] = d_logits[rows].cpu().numpy()
+        greedy[step] = d_greedy.cpu().numpy().view(np.uint32)
+        d_tok.copy_(d_greedy)
+    assert s.positions() == [prefix + STEPS] * B
+    m.close()
+    kern.ctx.close()
+    _RUNS[B] = dict(first=first, states=states, rows=rows, logits=logits, greedy=greedy)
+    return _RUNS[B]
+
+
+@pytest.mark.parametrize("B,checked", [(1, (0,)), (32, (0, 4)), (32, (9, 13)), (32, (18, 22)), (32, (27, 31))])
+def test_config5_2b_q4k_decode_from_2048_prefix(model_2b, B, checked):
+    """128 greedy steps; each checked row against its own oracle session
+    (split over several tests so that each stays within the per-test time
+    limit: the oracle decodes about 8 tokens/s on 16 cores)."""
+    g, t = model_2b
+    run = _device_run(model_2b, B)
+    oracle = O.Model(g, t)
     worst = 0.0
-    with O.libm_mode(O.LIBM_GLIBC):
-        for step in range(steps):
-            torch.cuda.synchronize()
-            kern.ctx.check(L.lib().zg_decode_step_device(s.h, B, d_tok.data_ptr(), d_logits.data_ptr(),
-                                                         d_greedy.data_ptr(), None))
-            kern.ctx.check(L.lib().zg_session_check(s.h, None))
-            lg = d_logits.cpu().numpy()
-            gr = d_greedy.cpu().numpy().view(np.uint32)
-            for r in checked:
-                ref = sess[r].forward(ref_tok[r])
-                err = float(np.max(np.abs(lg[r] - ref)))
+    for r in checked:
+        o = oracle.session(kv_bf16=True)
+        o.load_state(run["states"][r % len(run["states"])], 2048)
+        tok = int(run["first"][r])
+        k = run["rows"].index(r)
+        with O.libm_mode(O.LIBM_GLIBC):
+            for step in range(STEPS):
+                ref = o.forward(tok)
+                lg = run["logits"][step, k]
+                err = float(np.max(np.abs(lg - ref)))
                 worst = max(worst, err)
                 assert err <= LOGIT_TOL, (step, r, err)
                 want = O.greedy(ref)
-                assert int(gr[r]) == want, (step, r, int(gr[r]), want)
-                assert int(gr[r]) == O.greedy(lg[r])  # the device readout is greedy_finite of its own logits
-                ref_tok[r] = want
-            d_tok.copy_(d_greedy)
-    assert s.positions() == [prefix + steps] * B
-    print(f"config 5 B={B}: {steps} greedy steps, rows {checked}, worst logit max-abs {worst:.3e}")
-    m.close()
-    kern.ctx.close()
+                got = int(run["greedy"][step, r])
+                assert got == want, (step, r, got, want)
+                assert got == O.greedy(lg)  # the device readout is greedy_finite of its own logits
+                tok = want
+    print(f"config 5 B={B}: {STEPS} greedy steps, rows {checked}, worst logit max-abs {worst:.3e}")
 
 
 # ------------------------------------------------------------ config 3

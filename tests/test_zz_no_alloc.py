@@ -5,6 +5,8 @@ contents), for every codec path: bf16 input through the prepared
 activation, f32 input through the in-kernel prologue (up to 4 rows) and
 through the f16 MFMA kernels (Q4_K beyond 4 rows).  No counterpart in the
 reference: the entry exists for callers that cannot allocate."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -90,3 +92,37 @@ def test_noalloc_limits(kern):
                                           None))
     torch.cuda.synchronize()
     assert np.array_equal(got.view(np.uint32), want.cpu().numpy().view(np.uint32))
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(kern):
+    """Calls on two streams, submitted back to back without a host wait,
+    share the one static array: each must wait for the previous call's
+    kernels, so both results still equal zg_gemv_device's bit for bit."""
+    import torch
+    rng = np.random.default_rng(77)
+    K, N = 2048, 6144
+    w = synth.random_matrix(rng, synth.Q4_K, N, K)
+    h = kern.register(960, "noalloc.streams", synth.Q4_K, K, N, w.reshape(-1))
+    g = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)).cuda()
+    xs, wants = [], []
+    for M in (32, 16, 8, 24):
+        x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()
+        y = torch.full((M, N), np.nan, dtype=torch.float32, device="cuda")
+        kern.ctx.check(L.lib().zg_gemv_device(kern.ctx.h, h.h, x.data_ptr(), L.F32, M, g.data_ptr(), 1e-6,
+                                              y.data_ptr(), None))
+        torch.cuda.synchronize()
+        xs.append(x)
+        wants.append(y.cpu().numpy())
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [torch.full(tuple(v.shape), np.nan, dtype=torch.float32, device="cuda") for v in wants]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i, (x, y) in enumerate(zip(xs, outs)):
+            st = streams[i % 2]
+            kern.ctx.check(L.lib().zg_gemv_device_noalloc(kern.ctx.h, h.h, x.data_ptr(), L.F32, x.shape[0],
+                                                          g.data_ptr(), 1e-6, y.data_ptr(),
+                                                          ctypes.c_void_p(st.cuda_stream)))
+        torch.cuda.synchronize()
+        for i, (y, want) in enumerate(zip(outs, wants)):
+            got = y.cpu().numpy()
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (rep, i)

@@ -36,6 +36,9 @@ _SIGS = {
     "zg_silu": (C.c_int, [P, P, P, SZ, P]),
     "zg_binary": (C.c_int, [P, C.c_int, P, P, SZ, P]),
     "zg_gemv_device": (C.c_int, [P, P, P, C.c_int, SZ, P, C.c_float, P, P]),
+    "zg_gemv_device_fused": (C.c_int, [P, P, SZ, C.c_int, C.c_int, P, SZ, P, SZ, P, C.c_float, SZ, P, SZ, P, P, P,
+                                       P, P]),
+    "zg_gemv_greedy_parts": (SZ, [P]),
     "zg_gdn_conv": (C.c_int, [P, P, P, P, SZ, P, P]),
     "zg_gdn_coefficients": (C.c_int, [P, P, P, P, P, SZ, C.c_float, P, P, P, P]),
     "zg_gdn_recurrent": (C.c_int, [P, SZ, SZ, P, P, P, P, P, P, P]),
@@ -47,6 +50,7 @@ _SIGS = {
     "zg_attention_qk": (C.c_int, [P, P, P, SZ, SZ, SZ, SZ, C.c_float, P, P]),
     "zg_attention_softmax": (C.c_int, [P, P, SZ, SZ, P]),
     "zg_attention_value": (C.c_int, [P, P, P, SZ, SZ, SZ, SZ, P]),
+    "zg_model_admit": (C.c_int, [C.c_int, P, P, SZ, C.c_char_p, SZ]),
     "zg_model_load": (C.c_int, [P, C.c_uint64, P, P, SZ, C.POINTER(P)]),
     "zg_model_destroy": (None, [P]),
     "zg_session_create": (C.c_int, [P, SZ, SZ, C.c_int, C.POINTER(P)]),

@@ -14,7 +14,6 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libzg_hip.so")
-PROBE_LIB = os.path.join(HERE, "libzg_probe.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -52,14 +51,6 @@ def build(verbose=True):
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, LIB)
-    # the measurement kernels (bench.py --workload floors), a library of their own
-    probe_src = os.path.join(HERE, "probe", "zg_probe.hip")
-    probe_tmp = PROBE_LIB + ".tmp"
-    cmd = [HIPCC] + FLAGS + ["-shared", "-o", probe_tmp, probe_src]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError("probe library build failed:\n" + r.stdout + r.stderr)
-    os.replace(probe_tmp, PROBE_LIB)
     if verbose:
         print(f"built {LIB}")
     return LIB

@@ -2,6 +2,7 @@
 // cache, boundary-A region entry points and the device GEMV API.
 #include <cmath>
 #include <cstdio>
+#include <atomic>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -20,19 +21,46 @@ constexpr size_t kStaticScratchBytes = (size_t)4 << 20;
 constexpr size_t kStaticScratchRows = 64;
 static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 
+// Per device: the event recorded after the last use of that device's array
+// (created with the first context on the device, kept for the process).
+constexpr int kMaxDevices = 64;
+struct ScratchOrder {
+    std::mutex mu;
+    hipEvent_t ev = nullptr;
+    bool used = false;
+};
+static ScratchOrder g_scratch_order[kMaxDevices];
+
+// The device's scratch-order event, created once (with that device current).
+static bool scratch_order_event(int device) {
+    ScratchOrder& so = g_scratch_order[device];
+    std::lock_guard<std::mutex> lk(so.mu);
+    if (!so.ev && hipEventCreateWithFlags(&so.ev, hipEventDisableTiming) != hipSuccess) {
+        so.ev = nullptr;
+        return false;
+    }
+    return true;
+}
+
 namespace zgc {
 
 // Failure text per (thread, ctx): under the reference's Send + Sync
 // contract (core/src/accelerator.rs:682) two threads may fail on one ctx at
-// once, and each reads its own message back.
-thread_local std::map<const zg_ctx*, std::string> t_errors;
+// once, and each reads its own message back.  Only thread-local data is
+// written, so fail() needs no lock; entries are keyed by the context's
+// serial number, never reused within a process.
+thread_local std::map<uint64_t, std::string> t_errors;
+std::atomic<uint64_t> g_ctx_serial{1};
 
 int fail(zg_ctx* ctx, int code, const std::string& msg) {
-    if (ctx) {
-        ctx->err = msg;
-        t_errors[ctx] = msg;
-    }
+    if (ctx) t_errors[ctx->serial] = msg;
     return code;
+}
+
+std::string last_message(const zg_ctx* ctx) {
+    if (!ctx) return "";
+    auto it = t_errors.find(ctx->serial);
+    return it == t_errors.end() ? std::string() : it->second;
 }
 
 void drop_weight(zg_ctx* ctx, zg_weight* w) {
@@ -169,13 +197,16 @@ int zg_ctx_create(int device, zg_ctx** out) {
     if (!out) return ZG_E_MALFORMED;
     *out = nullptr;
     int count = 0;
-    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return ZG_E_DEVICE;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count || device >= kMaxDevices)
+        return ZG_E_DEVICE;
     if (hipSetDevice(device) != hipSuccess) return ZG_E_DEVICE;
     auto ctx = new zg_ctx();
     ctx->device = device;
+    ctx->serial = g_ctx_serial.fetch_add(1);
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
         hipMalloc(&ctx->d_flag, sizeof(int)) != hipSuccess ||
-        hipGetSymbolAddress(&ctx->static_scratch, HIP_SYMBOL(scratch)) != hipSuccess || !ctx->static_scratch) {
+        hipGetSymbolAddress(&ctx->static_scratch, HIP_SYMBOL(scratch)) != hipSuccess || !ctx->static_scratch ||
+        !scratch_order_event(device)) {
         if (ctx->d_flag) (void)hipFree(ctx->d_flag);
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
         delete ctx;
@@ -199,12 +230,13 @@ void zg_ctx_destroy(zg_ctx* ctx) {
         if (ctx->d_flag) (void)hipFree(ctx->d_flag);
         (void)hipStreamDestroy(ctx->stream);
     }
+    t_errors.erase(ctx->serial);
     delete ctx;
 }
 
 const char* zg_last_error(const zg_ctx* ctx) {
     if (!ctx) return "null context";
-    auto it = t_errors.find(ctx);
+    auto it = t_errors.find(ctx->serial);
     return it == t_errors.end() ? "" : it->second.c_str();
 }
 
@@ -215,7 +247,7 @@ int zg_weight_register(zg_ctx* ctx, uint64_t source_id, const char* name, int gg
     (void)hipSetDevice(ctx->device);
     if (source_id == 0) return fail(ctx, ZG_E_MALFORMED, "unbound source identity cannot key a resident weight");
     int rc = check_matrix(ctx, ggml_type, columns, rows, bytes, len);
-    if (rc == ZG_UNSUPPORTED) return fail(ctx, ZG_E_UNSUPPORTED, ctx->err);
+    if (rc == ZG_UNSUPPORTED) return fail(ctx, ZG_E_UNSUPPORTED, last_message(ctx));
     if (rc != ZG_COMPLETED) return rc;
     rc = lookup_or_register(ctx, source_id, name, ggml_type, columns, rows, bytes, len, out);
     if (rc == ZG_COMPLETED) (*out)->api_pinned = true;
@@ -507,6 +539,77 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
     return ZG_COMPLETED;
 }
 
+static_assert(ZG_PRO_RMS == zg::PRO_RMS && ZG_PRO_GATED == zg::PRO_GATED && ZG_PRO_SILU_MUL == zg::PRO_SILU_MUL &&
+                  ZG_PRO_PLAIN == zg::PRO_PLAIN && ZG_EPI_STORE == zg::EPI_STORE && ZG_EPI_RESID == zg::EPI_RESID &&
+                  ZG_EPI_GLU == zg::EPI_GLU,
+              "C-ABI prologue/epilogue codes are the kernels' own");
+
+size_t zg_gemv_greedy_parts(const zg_weight* w) {
+    return w ? (size_t)zg::gemv1_greedy_parts(w->dw, zg::PRO_RMS) : 0;
+}
+
+// One projection of the decode step with its fused prologue and epilogue,
+// through the dispatcher the step itself calls (zg::fused_gemv), so the
+// same kernel and template variant runs for the same (weight, prologue,
+// epilogue, rows).
+int zg_gemv_device_fused(zg_ctx* ctx, const zg_weight* w, size_t m_rows, int prologue, int epilogue, float* x,
+                         size_t ldx, const float* x2, size_t ldx2, const float* gamma, float eps, size_t group,
+                         float* y, size_t ldy, const zg_weight* embedding, const uint32_t* token, float* greedy_max,
+                         int32_t* greedy_idx, void* stream) {
+    if (!ctx) return ZG_E_MALFORMED;
+    std::lock_guard<std::recursive_mutex> g(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (!w || !x || !y || m_rows == 0 || m_rows > 4 || prologue < ZG_PRO_RMS || prologue > ZG_PRO_PLAIN ||
+        epilogue < ZG_EPI_STORE || epilogue > ZG_EPI_GLU)
+        return fail(ctx, ZG_E_MALFORMED, "invalid fused gemv arguments");
+    const size_t K = w->dw.K, N = w->dw.N;
+    const bool needs_x2 = prologue == ZG_PRO_GATED || prologue == ZG_PRO_SILU_MUL;
+    const bool needs_gamma = prologue == ZG_PRO_RMS || prologue == ZG_PRO_GATED;
+    if ((needs_x2 && !x2) || (needs_gamma && !gamma) || ldx < K || (needs_x2 && ldx2 < K) ||
+        ldy < (epilogue == ZG_EPI_GLU ? N / 2 : N) || !(eps > 0.0f || !needs_gamma))
+        return fail(ctx, ZG_E_MALFORMED, "fused gemv operand missing or stride too short");
+    if (prologue == ZG_PRO_GATED && (group == 0 || K % group)) return fail(ctx, ZG_E_MALFORMED, "gated norm group");
+    if (!zg::fused_gemv_supported(w->dw.type, K, N, prologue))
+        return fail(ctx, ZG_UNSUPPORTED, "no fused projection kernel for this weight and prologue");
+    if (epilogue == ZG_EPI_GLU && !zg::fused_glu_supported(w->dw.type, K, N))
+        return fail(ctx, ZG_UNSUPPORTED, "no SwiGLU epilogue for this weight");
+    const bool greedy = greedy_max || greedy_idx;
+    if (greedy && (!greedy_max || !greedy_idx || m_rows != 1 || epilogue != ZG_EPI_STORE ||
+                   prologue != ZG_PRO_RMS || zg::gemv1_greedy_parts(w->dw, zg::PRO_RMS) <= 0))
+        return fail(ctx, ZG_UNSUPPORTED, "greedy partials: one row, RMS prologue, store epilogue, matrix-core GEMV");
+    if ((embedding || token) && (!embedding || !token || m_rows != 1 || prologue != ZG_PRO_RMS ||
+                                 !zg::gemv1_embed_supported(w->dw, embedding->dw)))
+        return fail(ctx, ZG_UNSUPPORTED, "embedding prologue: one row, RMS prologue, Q4_K embedding of width K");
+    zg::FusedGemvArgs f;
+    f.M = (int)m_rows;
+    f.pro = prologue;
+    f.epi = epilogue;
+    f.x = x;
+    f.ldx = ldx;
+    f.x2 = x2;
+    f.ldx2 = ldx2;
+    f.gamma = gamma;
+    f.eps = eps;
+    f.group = (int)group;
+    f.y = y;
+    f.ldy = ldy;
+    f.status = ctx->d_flag;
+    if (greedy) {
+        f.amax = greedy_max;
+        f.aidx = greedy_idx;
+    }
+    if (embedding) {
+        f.tok = token;
+        f.emb_qs = embedding->dw.qs;
+        f.emb_hdr = embedding->dw.hdr;
+        f.emb_rows = (int)embedding->dw.N;
+        f.x_out = x;
+    }
+    ZG_HIP(zg::fused_gemv(w->dw, f, stream ? (hipStream_t)stream : ctx->stream));
+    return ZG_COMPLETED;
+}
+
+
 // zg_gemv_device with its activation scratch in the process-wide static
 // array instead of a context buffer: no allocation on any path.  The same
 // kernels in the same order, so the result is bit-identical.
@@ -521,7 +624,34 @@ int zg_gemv_device_noalloc(zg_ctx* ctx, const zg_weight* w, const void* x, int x
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     void* sp = ctx->static_scratch;
     const int pro = gamma ? zg::PRO_RMS : zg::PRO_PLAIN;
-    if (x_dtype == ZG_F32 && zg::fused_gemv_supported(w->dw.type, w->dw.K, w->dw.N, pro)) {
+    const bool fused = x_dtype == ZG_F32 && zg::fused_gemv_supported(w->dw.type, w->dw.K, w->dw.N, pro);
+    const bool batched = fused && m_rows > 4 && w->dw.type == zg::kQ4_K;
+    if (batched) {
+        if (!w->dw.qs_t && !zg::batched16_supported(m_rows, w->dw.K, w->dw.N, zg::EPI_STORE))
+            return fail(ctx, ZG_E_STATE,
+                        "weight has no batched tile layout yet: a zg_gemv_device call with more than 4 rows builds it");
+        if (zg::batched_scratch_bytes(m_rows, w->dw.K) > kStaticScratchBytes)
+            return fail(ctx, ZG_E_LIMIT, "activation exceeds the 4 MiB static scratch");
+    } else if (!fused) {
+        if (!zg::gemv_supported(w->dw.type, w->dw.K, m_rows)) return fail(ctx, ZG_UNSUPPORTED, "geometry not offered");
+        if (zg::prepared_bytes(w->dw.type, m_rows, w->dw.K) > kStaticScratchBytes)
+            return fail(ctx, ZG_E_LIMIT, "activation exceeds the 4 MiB static scratch");
+    }
+    // Uses of the device's array are ordered across streams, threads and
+    // contexts: each call waits on the event the previous call recorded
+    // after its kernels and records it after its own.  A call made while
+    // its stream is being captured into a graph is ordered by the graph's
+    // stream order instead (an event recorded outside a capture cannot be
+    // waited on inside it); replaying such a graph beside other uses of the
+    // array on the device races.
+    ScratchOrder& so = g_scratch_order[ctx->device];
+    std::lock_guard<std::mutex> order_lock(so.mu);
+    if (!so.ev) return fail(ctx, ZG_E_STATE, "static scratch order event missing for this device");
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    ZG_HIP(hipStreamIsCapturing(s, &cs));
+    const bool ordered = cs == hipStreamCaptureStatusNone;
+    if (ordered && so.used) ZG_HIP(hipStreamWaitEvent(s, so.ev, 0));
+    if (fused) {
         zg::FusedGemvArgs f;
         f.M = (int)m_rows;
         f.pro = pro;
@@ -533,23 +663,16 @@ int zg_gemv_device_noalloc(zg_ctx* ctx, const zg_weight* w, const void* x, int x
         f.y = y;
         f.ldy = w->dw.N;
         f.status = ctx->d_flag;
-        if (m_rows > 4 && w->dw.type == zg::kQ4_K) {
-            if (!w->dw.qs_t && !zg::batched16_supported(m_rows, w->dw.K, w->dw.N, zg::EPI_STORE))
-                return fail(ctx, ZG_E_STATE,
-                            "weight has no batched tile layout yet: a zg_gemv_device call with more than 4 rows builds it");
-            if (zg::batched_scratch_bytes(m_rows, w->dw.K) > kStaticScratchBytes)
-                return fail(ctx, ZG_E_LIMIT, "activation exceeds the 4 MiB static scratch");
-            ZG_HIP(zg::batched_gemv(w->dw, f, sp, s));
-        } else {
-            ZG_HIP(zg::fused_gemv(w->dw, f, s));
-        }
-        return ZG_COMPLETED;
+        if (batched) ZG_HIP(zg::batched_gemv(w->dw, f, sp, s));
+        else ZG_HIP(zg::fused_gemv(w->dw, f, s));
+    } else {
+        ZG_HIP(zg::act_prepare_for(w->dw.type, x, x_dtype == ZG_BF16, m_rows, w->dw.K, gamma, eps, sp, s));
+        ZG_HIP(zg::gemv(w->dw, m_rows, sp, y, s));
     }
-    if (!zg::gemv_supported(w->dw.type, w->dw.K, m_rows)) return fail(ctx, ZG_UNSUPPORTED, "geometry not offered");
-    if (zg::prepared_bytes(w->dw.type, m_rows, w->dw.K) > kStaticScratchBytes)
-        return fail(ctx, ZG_E_LIMIT, "activation exceeds the 4 MiB static scratch");
-    ZG_HIP(zg::act_prepare_for(w->dw.type, x, x_dtype == ZG_BF16, m_rows, w->dw.K, gamma, eps, sp, s));
-    ZG_HIP(zg::gemv(w->dw, m_rows, sp, y, s));
+    if (ordered) {
+        ZG_HIP(hipEventRecord(so.ev, s));
+        so.used = true;
+    }
     return ZG_COMPLETED;
 }
 

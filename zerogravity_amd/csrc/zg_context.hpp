@@ -29,7 +29,10 @@ struct zg_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     std::recursive_mutex mu;
-    std::string err;  // last failure on this ctx from any thread (zg_last_error reads the caller's own)
+    // unique per context for the life of the process: failure texts are kept
+    // per (thread, serial), so a context created later at a reused address
+    // never reads an earlier one's message
+    uint64_t serial = 0;
     std::map<std::tuple<uint64_t, std::string, int, size_t, size_t>, std::unique_ptr<zg_weight>> weights;
     DeviceBuffer scratch;    // region calls: inputs/outputs staged here
     DeviceBuffer actbuf;     // zg_gemv_device: prepared activations
@@ -43,6 +46,8 @@ struct zg_ctx {
 namespace zgc {
 
 int fail(zg_ctx* ctx, int code, const std::string& msg);
+// The calling thread's last failure text on ctx ("" if none).
+std::string last_message(const zg_ctx* ctx);
 int ensure(zg_ctx* ctx, DeviceBuffer& b, size_t bytes);
 size_t align256(size_t n);
 void free_weight(zg_weight* w);
@@ -54,6 +59,9 @@ void drop_weight(zg_ctx* ctx, zg_weight* w);
 int build_weight(zg_ctx* ctx, int type, size_t cols, size_t rows, const void* bytes, size_t len,
                  std::unique_ptr<zg_weight>& out);
 bool all_finite(const float* x, size_t n);
+// ggml codecs with device kernels here, and their block length in elements
+bool supported_type(int t);
+size_t block_elems(int t);
 
 }  // namespace zgc
 

@@ -14,6 +14,8 @@
 // mfma_q4k_kernel (the decode path's batched GEMM); its f16 rounding of the
 // weights and f32 accumulation make the result agree with the CPU's f32
 // dot within the per-op tolerance.
+#include <algorithm>
+
 #include "zg_decode_common.hpp"
 
 namespace zg {
@@ -65,10 +67,15 @@ __global__ __launch_bounds__(64 * WN * WM, 1) void gemm_q4k_kernel(FusedGemvArgs
         qoff[t] = ((uint32_t)tt * nbk * 256 + lane) * 16;
         hoff[t] = ((uint32_t)tt * nbk * 32 + r32) * 16;
     }
-    // buffer resources (32-bit offsets: every operand is < 4 GB)
-    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)a.qs, 0, 0x7fffffff, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)a.hdr, 0, 0x7fffffff, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)xh, 0, 0x7fffffff, 0x00020000);
+    // buffer resources sized to each operand (32-bit byte offsets: the host
+    // refuses an operand of 4 GiB or more, prompt_gemm_bytes)
+    const uint32_t ntl = (uint32_t)((N + 31) >> 5);
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.qs, 0, (int)(ntl * (uint32_t)nbk * 4096u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rh =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.hdr, 0, (int)(ntl * (uint32_t)nbk * 512u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void*)xh, 0, (int)((uint32_t)mtiles * (uint32_t)K * 64u), 0x00020000);
     // slab e (of AT*256) of a step: tile e/256, h8v e%256 of its 4-step run
     uint32_t aoff[APT];
 #pragma unroll
@@ -253,6 +260,14 @@ __global__ __launch_bounds__(256) void split_resid_kernel(FusedGemvArgs a) {
 
 }  // namespace
 
+// Largest operand of the prompt GEMM in bytes: the f16 activation tiles
+// (32 rows x K per tile), the 32-row weight tiles and their headers.  Every
+// one must stay below 4 GiB (32-bit buffer offsets).
+uint64_t prompt_gemm_bytes(size_t M, size_t K, size_t N) {
+    const uint64_t mt = (M + 31) / 32, nt = (N + 31) / 32, nbk = K / 256;
+    return std::max({mt * K * 64, nt * nbk * 4096, nt * nbk * 512});
+}
+
 bool prompt_gemm_supported(int type, size_t K, size_t N, int epi) {
     if (type != kQ4_K || K % 256 || K > 8192 || N == 0) return false;
     if (epi == EPI_GLU) return N % 64 == 0 && (N / 2) % 256 == 0;
@@ -271,6 +286,7 @@ hipError_t prompt_gemm(const DeviceWeight& w, const FusedGemvArgs& args, const _
     if (!prompt_gemm_supported(w.type, w.K, w.N, args.epi) || !w.qs_t || !w.hdr_t || args.M <= 0)
         return hipErrorInvalidValue;
     if (args.epi == EPI_GLU && !args.xh_out) return hipErrorInvalidValue;
+    if (prompt_gemm_bytes((size_t)args.M, w.K, w.N) >= ((uint64_t)1 << 32)) return hipErrorInvalidValue;
     FusedGemvArgs a = args;
     a.qs = w.qs_t;
     a.hdr = w.hdr_t;

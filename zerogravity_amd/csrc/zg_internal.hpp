@@ -266,6 +266,7 @@ hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& a, void* scr
 // EPI_GLU into xh_out (a product past the f16 range sets status bit 4).
 bool prompt_gemm_supported(int type, size_t K, size_t N, int epi);
 hipError_t prompt_gemm(const DeviceWeight& w, const FusedGemvArgs& a, const _Float16* xh, hipStream_t s);
+uint64_t prompt_gemm_bytes(size_t M, size_t K, size_t N);
 
 // GDN decode: conv (4-slot ring per channel) + SiLU + q/k L2 + gates +
 // recurrence for B rows.  proj rows: [qkv (3W) | z (W) | alpha (H) | beta (H)].

@@ -80,7 +80,11 @@ struct zg_session {
     size_t max_batch = 0, max_ctx = 0;
     int kv_bf16 = 1;
     std::vector<int> pos;  // host copy of each row's next position
+    // A failed launch leaves every row's device state unknown: all rows are
+    // marked, and the session is usable again once each marked row has been
+    // reset, restored or imported (or the whole session reset).
     bool poisoned = false;
+    std::vector<uint8_t> row_bad;
     bool pos_dirty = true;  // device positions must be re-uploaded from pos
     bool use_graphs = true;
     // device buffers
@@ -154,7 +158,7 @@ int load_stack(zg_model* m, const zg_tensor_desc* ts, size_t n, const std::vecto
         if (t->shape0 != K || t->shape1 != Ns[i])
             return fail(ctx, ZG_E_MALFORMED, "tensor " + names[i] + " geometry differs from the model configuration");
         int rc = check_matrix(ctx, t->ggml_type, K, Ns[i], t->data, t->nbytes);
-        if (rc == ZG_UNSUPPORTED) return fail(ctx, ZG_E_UNSUPPORTED, "tensor " + names[i] + ": " + ctx->err);
+        if (rc == ZG_UNSUPPORTED) return fail(ctx, ZG_E_UNSUPPORTED, "tensor " + names[i] + ": " + last_message(ctx));
         if (rc) return rc;
         if (!zg::fused_gemv_supported(t->ggml_type, K, Ns[i], pro))
             return fail(ctx, ZG_E_UNSUPPORTED, "resident decode has no projection kernel for " + names[i]);
@@ -218,6 +222,84 @@ int load_vector(zg_model* m, const zg_tensor_desc* ts, size_t n, const std::stri
     ZG_HIP(hipMemcpy(d, t->data, len * 4, hipMemcpyHostToDevice));
     *out = (float*)d;
     return ZG_COMPLETED;
+}
+
+// Boundary B admission: the numerical profile and tensor table the plan
+// hands over must be the schedule step() runs (the GGUF source profile,
+// LoadedQwenModel::require_execution_profile, model-qwen35/src/source/
+// binding.rs:363-371; a provider prepares whatever plan it is given,
+// core/src/provider.rs:38-42, so the refusal is the backend's).  Host only:
+// no device, no context.  Every tensor the schedule reads must be present
+// with the role's shape, a codec the role's kernels take and its exact
+// packed length; values (finite scales, finite parameters) are checked when
+// zg_model_load uploads them.
+int admit_model(int profile, const zg_geometry* g, const zg_tensor_desc* ts, size_t n, std::string* why) {
+    auto no = [&](int code, const std::string& m) {
+        *why = m;
+        return code;
+    };
+    if (profile != ZG_PROFILE_GGUF_SOURCE_V1)
+        return no(ZG_E_UNSUPPORTED, "numerical profile " + std::to_string(profile) +
+                                        " is not the GGUF source profile this backend runs");
+    if (!g || !ts) return no(ZG_E_MALFORMED, "missing geometry or tensor table");
+    if (g->layers == 0 || g->layers > 4096 || g->full_attention_interval == 0 || g->gdn_dim != 128 ||
+        g->head_dim != 256 || g->q_heads == 0 || g->kv_heads == 0 || g->q_heads % g->kv_heads ||
+        g->q_heads / g->kv_heads > 4 || g->gdn_heads == 0 || g->gdn_heads > 64 || !(g->eps > 0.0f) ||
+        g->max_context == 0 || g->hidden % 256 || g->ffn % 256 || g->vocab == 0)
+        return no(ZG_E_UNSUPPORTED, "model geometry outside the resident decode path (gdn_dim 128, head_dim 256)");
+    auto matrix = [&](const std::string& name, uint64_t K, uint64_t N, int pro) {
+        const zg_tensor_desc* t = find_tensor(ts, n, name);
+        if (!t) return no(ZG_E_MALFORMED, "missing tensor " + name);
+        if (t->shape0 != K || t->shape1 != N)
+            return no(ZG_E_MALFORMED, "tensor " + name + " geometry differs from the model configuration");
+        if (!t->data) return no(ZG_E_MALFORMED, "tensor " + name + " has no data");
+        if (!supported_type(t->ggml_type))
+            return no(ZG_E_UNSUPPORTED, "tensor " + name + ": ggml type " + std::to_string(t->ggml_type) +
+                                            " not offered by this backend");
+        if (K % block_elems(t->ggml_type) || zg::gguf_row_bytes(t->ggml_type, K) * N != t->nbytes)
+            return no(ZG_E_MALFORMED, "tensor " + name + ": packed byte length mismatch");
+        if (!zg::fused_gemv_supported(t->ggml_type, K, N, pro))
+            return no(ZG_E_UNSUPPORTED, "resident decode has no projection kernel for " + name);
+        return (int)ZG_COMPLETED;
+    };
+    auto vector = [&](const std::string& name, uint64_t len) {
+        const zg_tensor_desc* t = find_tensor(ts, n, name);
+        if (!t) return no(ZG_E_MALFORMED, "missing tensor " + name);
+        if (t->ggml_type != ZG_F32 || t->shape0 * t->shape1 != len || t->nbytes != len * 4 || !t->data)
+            return no(ZG_E_MALFORMED, "parameter " + name + " must be F32 of " + std::to_string(len) + " values");
+        return (int)ZG_COMPLETED;
+    };
+    const uint64_t H = g->hidden, F = g->ffn, V = g->vocab, W = (uint64_t)g->gdn_heads * g->gdn_dim;
+    const uint64_t QD = (uint64_t)g->q_heads * g->head_dim, KD = (uint64_t)g->kv_heads * g->head_dim;
+    int rc = matrix("token_embd.weight", H, V, zg::PRO_RMS);
+    if (!rc) rc = vector("output_norm.weight", H);
+    for (unsigned i = 0; i < g->layers && !rc; ++i) {
+        const bool full = ((i + 1) % g->full_attention_interval) == 0;  // config.rs:146-167
+        rc = vector(lname(i, "attn_norm.weight"), H);
+        if (!rc) rc = vector(lname(i, "post_attention_norm.weight"), H);
+        if (!rc) rc = matrix(lname(i, "ffn_gate.weight"), H, F, zg::PRO_RMS);
+        if (!rc) rc = matrix(lname(i, "ffn_up.weight"), H, F, zg::PRO_RMS);
+        if (!rc) rc = matrix(lname(i, "ffn_down.weight"), F, H, zg::PRO_SILU_MUL);
+        if (full) {
+            if (!rc) rc = matrix(lname(i, "attn_q.weight"), H, 2 * QD, zg::PRO_RMS);
+            if (!rc) rc = matrix(lname(i, "attn_k.weight"), H, KD, zg::PRO_RMS);
+            if (!rc) rc = matrix(lname(i, "attn_v.weight"), H, KD, zg::PRO_RMS);
+            if (!rc) rc = matrix(lname(i, "attn_output.weight"), QD, H, zg::PRO_PLAIN);
+            if (!rc) rc = vector(lname(i, "attn_q_norm.weight"), g->head_dim);
+            if (!rc) rc = vector(lname(i, "attn_k_norm.weight"), g->head_dim);
+        } else {
+            if (!rc) rc = matrix(lname(i, "attn_qkv.weight"), H, 3 * W, zg::PRO_RMS);
+            if (!rc) rc = matrix(lname(i, "attn_gate.weight"), H, W, zg::PRO_RMS);
+            if (!rc) rc = matrix(lname(i, "ssm_alpha.weight"), H, g->gdn_heads, zg::PRO_RMS);
+            if (!rc) rc = matrix(lname(i, "ssm_beta.weight"), H, g->gdn_heads, zg::PRO_RMS);
+            if (!rc) rc = matrix(lname(i, "ssm_out.weight"), W, H, zg::PRO_GATED);
+            if (!rc) rc = vector(lname(i, "ssm_conv1d.weight"), 4 * 3 * W);
+            if (!rc) rc = vector(lname(i, "ssm_norm.weight"), g->gdn_dim);
+            if (!rc) rc = vector(lname(i, "ssm_a"), g->gdn_heads);
+            if (!rc) rc = vector(lname(i, "ssm_dt.bias"), g->gdn_heads);
+        }
+    }
+    return rc;
 }
 
 int dalloc(zg_session* s, void** p, size_t bytes) {
@@ -497,6 +579,19 @@ int run_step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uin
     return ZG_COMPLETED;
 }
 
+// Poison: every row's device state is unknown after a failed launch.
+void poison(zg_session* s) {
+    std::fill(s->row_bad.begin(), s->row_bad.end(), 1);
+    s->poisoned = true;
+}
+
+// A row whose state was just rewritten from a known source is trusted again;
+// the session is usable when no row is left unknown.
+void clear_poison(zg_session* s, size_t row) {
+    s->row_bad[row] = 0;
+    s->poisoned = std::find(s->row_bad.begin(), s->row_bad.end(), 1) != s->row_bad.end();
+}
+
 // Host mirrors of positions and GDN halves re-read from the device (after
 // asynchronous steps, whose commits the host cannot see, or a failed step).
 int pull_positions(zg_session* s, hipStream_t st) {
@@ -520,8 +615,10 @@ int settle(zg_session* s) {
 
 // The status word of the steps since the last check.  A failed step did
 // not publish (its commit is gated on this word), so the session keeps the
-// state before it: the host mirrors are re-read from the device, the word
-// is cleared, and the error is returned.
+// state before it: the word is cleared, the host mirrors are re-read from
+// the device unless the host copy is the newer one (pos_dirty: a reset,
+// copy, restore, import or batched prefill since the last upload, which
+// the device positions have not seen), and the error is returned.
 int read_status(zg_session* s, hipStream_t st) {
     zg_ctx* ctx = s->m->ctx;
     int status = 0;
@@ -529,8 +626,10 @@ int read_status(zg_session* s, hipStream_t st) {
     ZG_HIP(hipStreamSynchronize(st));
     if (status) {
         ZG_HIP(hipMemsetAsync(s->d_status, 0, sizeof(int), st));
-        int rc = pull_positions(s, st);
-        if (rc) return rc;
+        if (!s->pos_dirty) {
+            int rc = pull_positions(s, st);
+            if (rc) return rc;
+        }
         s->pending_rows = 0;
         if (status & 2) return fail(ctx, ZG_E_MALFORMED, "decode step contains an out-of-vocabulary token id");
         if (status & 1) return fail(ctx, ZG_E_STATE, "nonfinite layer computation");
@@ -665,6 +764,18 @@ namespace {}  // namespace
 
 extern "C" {
 
+int zg_model_admit(int profile, const zg_geometry* g, const zg_tensor_desc* tensors, size_t n, char* msg,
+                   size_t msg_len) {
+    std::string why;
+    const int rc = admit_model(profile, g, tensors, n, &why);
+    if (msg && msg_len) {
+        const size_t k = std::min(why.size(), msg_len - 1);
+        memcpy(msg, why.data(), k);
+        msg[k] = 0;
+    }
+    return rc;
+}
+
 int zg_model_load(zg_ctx* ctx, uint64_t source_id, const zg_geometry* g, const zg_tensor_desc* tensors, size_t n,
                   zg_model** out) {
     if (!ctx || !g || !tensors || !out) return fail(ctx, ZG_E_MALFORMED, "invalid model load arguments");
@@ -672,11 +783,11 @@ int zg_model_load(zg_ctx* ctx, uint64_t source_id, const zg_geometry* g, const z
     (void)hipSetDevice(ctx->device);
     *out = nullptr;
     if (source_id == 0) return fail(ctx, ZG_E_MALFORMED, "unbound source identity cannot own a resident model");
-    if (g->layers == 0 || g->layers > 4096 || g->full_attention_interval == 0 || g->gdn_dim != 128 ||
-        g->head_dim != 256 || g->q_heads == 0 || g->kv_heads == 0 || g->q_heads % g->kv_heads ||
-        g->q_heads / g->kv_heads > 4 || g->gdn_heads == 0 || g->gdn_heads > 64 || !(g->eps > 0.0f) ||
-        g->max_context == 0 || g->hidden % 256 || g->ffn % 256)
-        return fail(ctx, ZG_E_UNSUPPORTED, "model geometry outside the resident decode path (gdn_dim 128, head_dim 256)");
+    {
+        std::string why;
+        const int rc = admit_model(ZG_PROFILE_GGUF_SOURCE_V1, g, tensors, n, &why);
+        if (rc) return fail(ctx, rc, why);
+    }
     auto m = new zg_model();
     m->ctx = ctx;
     m->source = source_id;
@@ -777,6 +888,7 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     s->max_ctx = max_context;
     s->kv_bf16 = kv_dtype == ZG_BF16;
     s->pos.assign(max_batch, 0);
+    s->row_bad.assign(max_batch, 0);
     const char* env = getenv("ZG_GRAPHS");
     s->use_graphs = !(env && env[0] == '0');
     const size_t B = max_batch, H = g.hidden, F = g.ffn, V = g.vocab, W = (size_t)g.gdn_heads * g.gdn_dim;
@@ -892,6 +1004,7 @@ int zg_session_reset(zg_session* s) {
     std::fill(s->pos.begin(), s->pos.end(), 0);
     std::fill(s->cur.begin(), s->cur.end(), 0);
     s->pos_dirty = true;
+    std::fill(s->row_bad.begin(), s->row_bad.end(), 0);
     s->poisoned = false;
     s->pending_rows = 0;
     return ZG_COMPLETED;
@@ -920,6 +1033,7 @@ int zg_session_reset_row(zg_session* s, size_t row) {
     s->pos[row] = 0;
     s->cur[row] = 0;
     s->pos_dirty = true;
+    clear_poison(s, row);
     s->pending_rows = 0;
     return ZG_COMPLETED;
 }
@@ -989,7 +1103,7 @@ int host_step(zg_session* s, size_t rows, const uint32_t* tokens, float* logits,
     ZG_HIP(hipStreamSynchronize(st));
     const bool want = logits || greedy;
     if ((rc = run_step(s, rows, s->d_tokens, want ? s->logits : nullptr, want ? s->d_greedy : nullptr, commit, st))) {
-        s->poisoned = true;  // a launch failed: the device state is unknown
+        poison(s);  // a launch failed: the device state is unknown
         return rc;
     }
     if ((rc = read_status(s, st))) return rc;  // nothing was published
@@ -1071,9 +1185,9 @@ int zg_prefill(zg_session* s, size_t rows, size_t n, const uint32_t* tokens, flo
         rc = host_step(s, rows, col.data(), t + 1 == n ? logits : nullptr, nullptr, true);
     }
     if (rc) {
-        const std::string msg = ctx->err;
+        const std::string msg = last_message(ctx);
         for (size_t b = 0; b < rows; ++b)
-            if (saved[b].dev && load_row(s, b, saved[b])) s->poisoned = true;
+            if (saved[b].dev && load_row(s, b, saved[b])) poison(s);
         zgc::fail(ctx, rc, msg);
     }
     for (RowImage& img : saved) free_image(img);
@@ -1109,12 +1223,21 @@ int prefill_batched_body(zg_session* s, size_t row, size_t n, const uint32_t* to
         if (!w || w->dw.type != zg::kQ4_K)
             return fail(ctx, ZG_E_UNSUPPORTED, "batched prefill needs Q4_K projections: use zg_prefill");
     hipStream_t st = ctx->stream;
+    // the device positions take the host's (a status failure below re-reads
+    // them, and must find every other row as the host has it)
+    int rc0 = sync_positions(s, st);
+    if (rc0) return rc0;
     for (zg_weight* w : ws)
         if (!w->dw.qs_t) ZG_HIP(zg::ensure_mfma_tiles(w->dw, st));
     const size_t H = g.hidden, F = g.ffn, W = (size_t)g.gdn_heads * g.gdn_dim, GH = g.gdn_heads;
     const size_t QD = (size_t)g.q_heads * g.head_dim;
     const size_t mpad = (n + 31) / 32 * 32;
     const size_t ldp = s->y0w;
+    // the prompt GEMM addresses each operand with 32-bit byte offsets
+    for (zg_weight* w : ws)
+        if (zg::prompt_gemm_bytes(n, w->dw.K, w->dw.N) >= ((uint64_t)1 << 32))
+            return fail(ctx, ZG_E_LIMIT, "prompt too long for the batched prefill (an operand of its projections "
+                                         "would reach 4 GiB): split it over several calls");
     enum { X, P, Q, K, V, BETA, LOGD, CORE, QB, OB, XH, XH2, CHUNK, TOK, ATTP, RPARTS, NBUF };
     // the split residual projections' partial sums: a split is taken only
     // while the tiles give at most 256 workgroups of 64 x 256 outputs, so two
@@ -1268,8 +1391,8 @@ int zg_prefill_batched(zg_session* s, size_t row, size_t n, const uint32_t* toke
     if ((rc = save_row(s, row, false, &saved))) return rc;
     rc = prefill_batched_body(s, row, n, tokens, logits);
     if (rc) {
-        const std::string msg = ctx->err;
-        if (load_row(s, row, saved)) s->poisoned = true;
+        const std::string msg = last_message(ctx);
+        if (load_row(s, row, saved)) poison(s);
         zgc::fail(ctx, rc, msg);
     }
     free_image(saved);
@@ -1289,7 +1412,7 @@ int zg_decode_step_device(zg_session* s, size_t rows, const uint32_t* d_tokens, 
     if ((rc = sync_positions(s, st))) return rc;
     if ((rc = run_step(s, rows, d_tokens, d_logits ? d_logits : (d_greedy ? s->logits : nullptr), d_greedy, true,
                        st))) {
-        s->poisoned = true;
+        poison(s);
         return rc;
     }
     ZG_HIP(hipEventRecord(s->dev_ev, st));
@@ -1371,26 +1494,15 @@ int zg_state_export(zg_session* s, size_t row, float* out, size_t n) {
     return ZG_COMPLETED;
 }
 
-int zg_state_import(zg_session* s, size_t row, const float* in, size_t n, int position) {
-    if (!s || !in) return ZG_E_MALFORMED;
+namespace {
+
+// The row's device state from a host image in the export order; on error
+// the row may be partly written (the caller poisons the session).
+int import_row(zg_session* s, size_t row, const float* in, int position) {
     zg_ctx* ctx = s->m->ctx;
-    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
-    (void)hipSetDevice(ctx->device);
-    if (row >= s->max_batch || position < 0 || (size_t)position > s->max_ctx)
-        return fail(ctx, ZG_E_MALFORMED, "invalid state import row or position");
-    int rc = settle(s);
-    if (rc) return rc;
-    const int saved = s->pos[row];
-    s->pos[row] = position;
-    if (n != zg_state_floats(s, row) || !all_finite(in, n)) {
-        s->pos[row] = saved;
-        return fail(ctx, ZG_E_MALFORMED, "state import length mismatch or nonfinite state");
-    }
     const zg_geometry& g = s->m->g;
     hipStream_t st = ctx->stream;
     const size_t T = (size_t)position, kw = kvw(g), C = (size_t)g.gdn_heads * g.gdn_dim * 3;
-    rc = ensure(ctx, ctx->scratch, std::max<size_t>(T * kw * 4, 256));
-    if (rc) return rc;
     std::vector<float> ring(ring_floats(g));
     size_t at = 0;
     for (size_t i = 0; i < s->m->layers.size(); ++i) {
@@ -1420,9 +1532,40 @@ int zg_state_import(zg_session* s, size_t row, const float* in, size_t n, int po
         }
     }
     ZG_HIP(hipStreamSynchronize(st));
+    return ZG_COMPLETED;
+}
+
+}  // namespace
+
+// Either the row takes the image (state, position, published half 0) or,
+// on a refusal or an allocation failure, nothing changes; a device copy
+// that fails midway leaves the row partly written, which poisons the
+// session until the row is reset, restored or imported again.
+int zg_state_import(zg_session* s, size_t row, const float* in, size_t n, int position) {
+    if (!s || !in) return ZG_E_MALFORMED;
+    zg_ctx* ctx = s->m->ctx;
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipSetDevice(ctx->device);
+    if (row >= s->max_batch || position < 0 || (size_t)position > s->max_ctx)
+        return fail(ctx, ZG_E_MALFORMED, "invalid state import row or position");
+    int rc = settle(s);
+    if (rc) return rc;
+    const int saved = s->pos[row];
+    s->pos[row] = position;  // zg_state_floats sizes the KV part by the row's position
+    const size_t want = zg_state_floats(s, row);
+    s->pos[row] = saved;
+    if (n != want || !all_finite(in, n))
+        return fail(ctx, ZG_E_MALFORMED, "state import length mismatch or nonfinite state");
+    const size_t T = (size_t)position, kw = kvw(s->m->g);
+    if ((rc = ensure(ctx, ctx->scratch, std::max<size_t>(T * kw * 4, 256)))) return rc;
+    if ((rc = import_row(s, row, in, position))) {
+        poison(s);
+        return rc;
+    }
+    s->pos[row] = position;
     s->cur[row] = 0;
     s->pos_dirty = true;
-    s->poisoned = false;
+    clear_poison(s, row);
     s->pending_rows = 0;
     return ZG_COMPLETED;
 }
@@ -1455,9 +1598,9 @@ int zg_session_fill_random(zg_session* s, size_t rows, size_t prefix, uint64_t s
     for (size_t b = 0; b < rows; ++b) {
         s->pos[b] = (int)prefix;
         s->cur[b] = 0;
+        clear_poison(s, b);
     }
     s->pos_dirty = true;
-    s->poisoned = false;
     s->pending_rows = 0;
     return ZG_COMPLETED;
 }
@@ -1496,10 +1639,10 @@ int zg_session_restore(zg_session* s, size_t row, const zg_snapshot* snap) {
     int rc = settle(s);
     if (rc) return rc;
     if ((rc = load_row(s, row, snap->img))) {
-        s->poisoned = true;
+        poison(s);
         return rc;
     }
-    s->poisoned = false;
+    clear_poison(s, row);
     return ZG_COMPLETED;
 }
 

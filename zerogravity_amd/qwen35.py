@@ -175,24 +175,53 @@ def read_gguf(path, config_path=None):
     return g, t, f
 
 
+# ProgramNumericalProfile (core/src/numerics.rs:30-40), in its order
+PROFILES = {"GgufSourceV1": 0, "TorchCpuBf16Avx2MixedSourceV1": 1, "SourceCudaSm86Bf16V1": 2,
+            "AnalyticF32TextV1": 3, "DirectGammaBf16TextCandidateV1": 4}
+
+
+def _tensor_table(tensors):
+    """zg_tensor_desc[] over the host arrays of {name: (type, ne0, ne1, bytes)};
+    the second value keeps the arrays alive while the table is used."""
+    descs = (TensorDesc * len(tensors))()
+    keep = []
+    for i, (name, (ty, s0, s1, data)) in enumerate(tensors.items()):
+        data = np.ascontiguousarray(data)
+        nb = name.encode()
+        keep += [data, nb]
+        descs[i] = TensorDesc(nb, ty, s0, s1, data.ctypes.data, data.nbytes)
+    return descs, keep
+
+
+def admit(geometry: dict, tensors: dict, profile="GgufSourceV1"):
+    """Plan admission before any device work (zg_model_admit): raises ZgError
+    E_UNSUPPORTED unless the plan's numerical profile is GgufSourceV1 and its
+    tensors carry codecs the schedule's kernels take (LoadedQwenModel::
+    require_execution_profile, model-qwen35/src/source/binding.rs:363-371),
+    E_MALFORMED for a missing tensor or a shape that differs from the
+    geometry.  Host only: runs without a GPU."""
+    code = PROFILES[profile] if isinstance(profile, str) else int(profile)
+    descs, keep = _tensor_table(tensors)
+    msg = C.create_string_buffer(512)
+    rc = L.lib().zg_model_admit(code, C.byref(Geometry(**geometry)), descs, len(tensors), msg, len(msg))
+    if rc != L.COMPLETED:
+        raise L.ZgError(rc, msg.value.decode(errors="replace"))
+
+
 class QwenModelHip:
     """LoadedQwenModel on the device: weights resident once, sessions share them."""
 
-    def __init__(self, geometry: dict, tensors: dict, kernel=None, device=0, source_id=None):
+    def __init__(self, geometry: dict, tensors: dict, kernel=None, device=0, source_id=None, profile="GgufSourceV1"):
         from .regions import HipMatVecKernel
+        # a plan of another numerical profile is refused before any device work
+        admit(geometry, tensors, profile)
         self.kernel = kernel or HipMatVecKernel(device)
         self.ctx = self.kernel.ctx
         self.g = dict(geometry)
         # SourceIdentity of the tensor source (core/src/accelerator.rs:22-59):
         # models loaded from the same source share its resident weights
         self.source_id = next(_SOURCE_IDS) if source_id is None else int(source_id)
-        descs = (TensorDesc * len(tensors))()
-        keep = []
-        for i, (name, (ty, s0, s1, data)) in enumerate(tensors.items()):
-            data = np.ascontiguousarray(data)
-            nb = name.encode()
-            keep += [data, nb]
-            descs[i] = TensorDesc(nb, ty, s0, s1, data.ctypes.data, data.nbytes)
+        descs, keep = _tensor_table(tensors)
         geo = Geometry(**self.g)
         h = C.c_void_p()
         self.ctx.check(L.lib().zg_model_load(self.ctx.h, self.source_id, C.byref(geo), descs, len(tensors),
