@@ -271,10 +271,12 @@ def gemv_leg(kern, torch, g, tensors, kind, reps):
                 y, ldy = bufs["glu"], N // 2
             if role == "lm":
                 y, gm, gi = bufs["logits"], gmax.data_ptr(), gidx.data_ptr()
-            ctx.check(lib.zg_gemv_device_fused(ctx.h, h.h, 1, pro, epi, x.data_ptr(), K,
-                                               None if x2 is None else x2.data_ptr(), 0 if x2 is None else W,
-                                               None if gam is None else gam.data_ptr(), 1e-6, g["gdn_dim"],
-                                               y.data_ptr(), ldy, emb, tk, gm, gi, s.cuda_stream))
+            rc = lib.zg_gemv_device_fused(ctx.h, h.h, 1, pro, epi, x.data_ptr(), K,
+                                          None if x2 is None else x2.data_ptr(), 0 if x2 is None else W,
+                                          None if gam is None else gam.data_ptr(), 1e-6, g["gdn_dim"],
+                                          y.data_ptr(), ldy, emb, tk, gm, gi, s.cuda_stream)
+            if rc != L.COMPLETED:
+                raise L.ZgError(rc, f"{label}: {ctx.error()}")
 
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):

@@ -128,11 +128,12 @@ def test_attn_decode_device_matches_oracle(ctx, kv, max_ctx, positions):
         assert np.array_equal(got[b].view(np.uint32), ref.view(np.uint32)), (b, float(np.abs(got[b] - ref).max()))
 
 
-# The split-T form (1..64 rows): spans of T / chunks tokens, the owner of the
-# position among them; spans of one token block and of many, the position at
-# a span's first and last token, an empty tail of spans (T below the chunk
-# count), caches up to 8192 rows.  The output is held to the per-op bar,
-# 1e-3 relative to the row's largest magnitude.
+# The split-T form (1..64 rows): spans of a fixed token count per launch
+# (32 at one row and a 2k cache, up to 1024), the owner of the position
+# among them; spans of one token block and of many, the position at a span's
+# first and last token, spans past a row's tokens (rows at different
+# positions), caches up to 8192 rows.  The output is held to the per-op
+# bar, 1e-3 relative to the row's largest magnitude.
 SPLIT_REL = 1e-3
 
 

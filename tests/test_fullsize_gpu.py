@@ -107,13 +107,21 @@ def _device_run(model_2b, B):
 
 @pytest.mark.parametrize("B,checked", [(1, (0,)), (32, (0, 4)), (32, (9, 13)), (32, (18, 22)), (32, (27, 31))])
 def test_config5_2b_q4k_decode_from_2048_prefix(model_2b, B, checked):
-    """128 greedy steps; each checked row against its own oracle session
+    """128 greedy steps, each checked row against its own oracle session
     (split over several tests so that each stays within the per-test time
-    limit: the oracle decodes about 8 tokens/s on 16 cores)."""
+    limit: the oracle decodes about 8 tokens/s on 16 cores).  The device
+    decodes free-running (its greedy feeds its next step); the oracle takes
+    the device's tokens, so every step compares the same history.  Every
+    step: logits within 2e-2 max-abs, and the device's token is greedy_finite
+    of its own logits.  The north star's greedy bar, identical tokens over
+    32 steps, holds exactly for the first 32; beyond them a different token
+    is allowed only at a near-tie, where the device's choice scores within
+    the logit tolerance of the oracle's maximum (the per-op error of the f16
+    batched projections can order two logits that close either way)."""
     g, t = model_2b
     run = _device_run(model_2b, B)
     oracle = O.Model(g, t)
-    worst = 0.0
+    worst, ties = 0.0, []
     for r in checked:
         o = oracle.session(kv_bf16=True)
         o.load_state(run["states"][r % len(run["states"])], 2048)
@@ -126,12 +134,16 @@ def test_config5_2b_q4k_decode_from_2048_prefix(model_2b, B, checked):
                 err = float(np.max(np.abs(lg - ref)))
                 worst = max(worst, err)
                 assert err <= LOGIT_TOL, (step, r, err)
-                want = O.greedy(ref)
                 got = int(run["greedy"][step, r])
-                assert got == want, (step, r, got, want)
                 assert got == O.greedy(lg)  # the device readout is greedy_finite of its own logits
-                tok = want
-    print(f"config 5 B={B}: {STEPS} greedy steps, rows {checked}, worst logit max-abs {worst:.3e}")
+                want = O.greedy(ref)
+                if got != want:
+                    margin = float(ref[want] - ref[got])
+                    assert step >= 32 and margin <= LOGIT_TOL, (step, r, got, want, margin)
+                    ties.append((step, r, margin))
+                tok = got
+    print(f"config 5 B={B}: {STEPS} greedy steps, rows {checked}, worst logit max-abs {worst:.3e}, "
+          f"near-ties {ties}")
 
 
 # ------------------------------------------------------------ config 3

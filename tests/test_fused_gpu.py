@@ -44,8 +44,10 @@ def _fused(kern, h, M, pro, epi, x, x2, gamma, y, ldy, group=128, emb=None, tok=
     rc = L.lib().zg_gemv_device_fused(kern.ctx.h, h.h, M, pro, epi, x.data_ptr(), x.shape[-1], p(x2),
                                       0 if x2 is None else x2.shape[-1], p(gamma), 1e-6, group, y.data_ptr(), ldy,
                                       None if emb is None else emb.h, p(tok), p(gmax), p(gidx), None)
-    kern.ctx.check(rc)
+    if rc != L.UNSUPPORTED:
+        kern.ctx.check(rc)
     torch.cuda.synchronize()
+    return rc
 
 
 @pytest.mark.parametrize("kind", [synth.Q8_0, synth.Q4_K])
@@ -87,8 +89,14 @@ def test_fused_forms_match_oracle(kern, kind, M, form):
     dg = torch.from_numpy(g_use.copy()).cuda()
     ncol = N // 2 if epi == EPI_GLU else N
     dy = torch.from_numpy(y0[:, :ncol].copy() if epi == EPI_RESID else np.full((M, ncol), np.nan, np.float32)).cuda()
-    _fused(kern, h, M, pro, epi, dx, dx2 if pro in (PRO_GATED, PRO_SILU_MUL) else None,
-           dg if pro in (PRO_RMS, PRO_GATED) else None, dy, ncol)
+    rc = _fused(kern, h, M, pro, epi, dx, dx2 if pro in (PRO_GATED, PRO_SILU_MUL) else None,
+                dg if pro in (PRO_RMS, PRO_GATED) else None, dy, ncol)
+    if kind == synth.Q8_0 and epi == EPI_GLU:
+        # the step fuses SwiGLU into Q4_K projections only (Q8_0 models run
+        # the product in the down projection's prologue)
+        assert rc == L.UNSUPPORTED
+        return
+    assert rc == L.COMPLETED
     _check(kind, dy.cpu().numpy(), ref)
 
 

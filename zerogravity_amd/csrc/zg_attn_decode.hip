@@ -1,4 +1,6 @@
 // Resident attention decode step and the greedy argmax.
+#include <algorithm>
+
 #include "zg_decode_common.hpp"
 
 namespace zg {
@@ -578,46 +580,59 @@ hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
     return hipGetLastError();
 }
 
-// ============================================ split-T attention (B <= 4)
+// ============================================ split-T attention (1..64 rows)
 //
-// Flash-decoding form of the same layer for a few rows: workgroup (c, kv
-// head, row) takes the c-th of nc equal spans of the row's T = pos + 1
-// tokens (a multiple of 32 long), normalises and ropes the G query heads and
-// the new key as attn_decode_qk_kernel does (the workgroup whose span holds
-// the position appends K/V and uses its own rounded copies for that token),
+// Flash-decoding form of the same layer: workgroup (c, kv head, row) takes
+// the tokens [c S, (c + 1) S) of the row (S = attn_split_span, a multiple
+// of 32 fixed per launch, so a workgroup's key and value addresses do not
+// depend on the position: its first tile of each is requested before the
+// position arrives, and a span at or past the row's T = pos + 1 tokens
+// ends at once).  It normalises and ropes the G query heads and the new
+// key as attn_decode_qk_kernel does (the workgroup whose span holds the
+// position appends K/V and uses its own rounded copies for that token),
 // scores its tokens in the 32-accumulator order, and keeps per head the
 // span's max m, l = sum of GGML exp(s - m) and o = sum of exp(s - m) * v.
 // attn_combine_kernel then forms sum_c e^(m_c - M) o_c / sum_c e^(m_c - M)
-// l_c with M = max_c m_c and applies the sigmoid gate (forward.rs:751).
-// The reference (lib.rs:1276-1387) normalises with the global max first and
-// runs the value sums as token-ordered chains: this regrouping agrees with
-// it to f32 rounding (the per-op 1e-3 bar), not bit for bit.
+// l_c over the row's live spans c < ceil(T / S), M = max_c m_c, and applies
+// the sigmoid gate (forward.rs:751).  The reference (lib.rs:1276-1387)
+// normalises with the global max first and runs the value sums as
+// token-ordered chains: this regrouping agrees with it to f32 rounding (the
+// per-op 1e-3 bar), not bit for bit.
 constexpr int kSplitMaxSpan = 1024;  // tokens per workgroup (LDS scores)
 constexpr int kSplitMaxChunks = 256;
 
+// Tokens per span, a multiple of 32: about 256 workgroups over the batch at
+// a full context up to 4 rows (short spans: each workgroup's dependent
+// chain is short, and at a 2k context one row gets one 32-token tile per
+// workgroup), about 512 beyond (two per CU: a workgroup's prologue -- the
+// q/k norms and RoPE -- costs more than a longer span); never more than
+// kSplitMaxChunks spans.
+int attn_split_span(size_t B, int nkv, size_t max_ctx) {
+    const size_t target = B <= 4 ? 256 : 512;
+    const size_t want = (max_ctx * B * (size_t)nkv + target - 1) / target;
+    const size_t floor = (max_ctx + kSplitMaxChunks - 1) / kSplitMaxChunks;
+    const size_t s = std::max({want, floor, (size_t)32});
+    return (int)((s + 31) / 32 * 32);
+}
+
 int attn_split_chunks(size_t B, int nkv, size_t max_ctx) {
-    // ~128 workgroups for up to 4 rows (short spans: the workgroup's fixed
-    // latency dominates), ~512 for more (measured at 5-64 rows and 2049
-    // cached tokens: each workgroup's prologue -- projections, norms, RoPE --
-    // costs more than a longer span, beyond two workgroups per CU), and no
-    // span beyond kSplitMaxSpan
-    const size_t want = ((B <= 4 ? 128 : 512) + B * nkv - 1) / (B * nkv);
-    const size_t need = (max_ctx + kSplitMaxSpan - 1) / kSplitMaxSpan;
-    return (int)std::max(want, need);
+    const size_t S = (size_t)attn_split_span(B, nkv, max_ctx);
+    return (int)((max_ctx + S - 1) / S);
 }
 
 bool attn_split_supported(size_t B, int nq, int nkv, size_t max_ctx) {
-    return B >= 1 && B <= 64 && nkv > 0 && nq % nkv == 0 && nq / nkv <= 4 &&
-           attn_split_chunks(B, nkv, max_ctx) <= kSplitMaxChunks;
+    return B >= 1 && B <= 64 && nkv > 0 && nq % nkv == 0 && nq / nkv <= 4 && max_ctx > 0 &&
+           attn_split_span(B, nkv, max_ctx) <= kSplitMaxSpan && attn_split_chunks(B, nkv, max_ctx) <= kSplitMaxChunks;
 }
 
 size_t attn_split_part_bytes(size_t B, int nq, int nkv, size_t max_ctx) {
     return B * (size_t)nq * attn_split_chunks(B, nkv, max_ctx) * (256 + 2) * sizeof(float);
 }
 
-// Partials: {m, l} per (row, head, span) at part, then o [row][head][span][256].
+// Partials: {m, l} per (row, head, span) at part, then o [row][head][span][256];
+// only the live spans of a row are written.
 template <typename KV, int G>
-__global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int nc, float* __restrict__ part) {
+__global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int nc, int span, float* __restrict__ part) {
     constexpr int D = 256;
     __shared__ float hv[G + 1][D];
     __shared__ float rsin[32], rcos[32];
@@ -626,10 +641,32 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
     __shared__ float vrow[D];
     const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, s = tid & 7;
+    const int t0 = c * span;
+    KV* kc = (KV*)a.kcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D;
+    KV* vc = (KV*)a.vcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D;
+    const size_t tstep = (size_t)a.nkv * D;
+    // keys of a 32-token tile: token t0 + 32 i + tid / 8, 32 dims per thread;
+    // values: wave w takes tokens t0 + 32 i + 8 w + u (u < 8), lane l
+    // channels 4l .. 4l+3.  Addresses clamped into the cache (rows past the
+    // position are read and never used).
+    KVPack<KV> kn[8], vn[8];
+    auto load_keys = [&](int i) {
+        const int tk = min(t0 + 32 * i + (tid >> 3), a.max_ctx - 1);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) kn[q].load(kc + (size_t)tk * tstep + 32 * q + 4 * s);
+    };
+    auto load_values = [&](int i) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            vn[u].load(vc + (size_t)min(t0 + 32 * i + 8 * wv + u, a.max_ctx - 1) * tstep + 4 * lane);
+    };
+    // the position, the span's first key and value tiles, then the q heads
+    // (tasks 0..G-1) and the key (task G), wave w taking tasks w, w+4
+    const int p = a.pos[b];
+    load_keys(0);
+    load_values(0);
     const float* proj = a.proj + (size_t)b * a.proj_stride;
     const int QD2 = a.nq * 2 * D;
-    // q heads (tasks 0..G-1) and the key (task G), wave w taking tasks w,
-    // w+4: their loads do not depend on the position, so they go first
     constexpr int NR = G / 4 + 1;
     float tv[NR][4], tg[NR][4];
 #pragma unroll
@@ -645,37 +682,15 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
     }
     const float vnew = proj[QD2 + (size_t)a.nkv * D + (size_t)kvh * D + tid];
 
-    const int p = a.pos[b], T = p + 1;
-    const int cs = (((T + nc - 1) / nc) + 31) & ~31;
-    const int t0 = min(c * cs, T), t1 = min(T, t0 + cs), n = t1 - t0;
+    const int T = p + 1;
+    const int t1 = min(T, t0 + span), n = t1 - t0;
+    if (n <= 0) return;  // past the row's tokens: the combine reads spans [0, ceil(T / span))
     const size_t nrow = (size_t)gridDim.z * a.nq * nc;
     const size_t slot = ((size_t)b * a.nq + (size_t)kvh * G) * nc + c;  // head g at slot + g * nc
     float* ml = part;
     float* po = part + 2 * nrow;
-    if (n <= 0) {  // an empty span: weight zero in the combine
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            if (tid == 0) {
-                ml[2 * (slot + (size_t)g * nc)] = -INFINITY;
-                ml[2 * (slot + (size_t)g * nc) + 1] = 0.0f;
-            }
-            po[(slot + (size_t)g * nc) * D + tid] = 0.0f;
-        }
-        return;
-    }
-    KV* kc = (KV*)a.kcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D;
-    KV* vc = (KV*)a.vcache + (size_t)b * a.cache_row_stride + (size_t)kvh * D;
-    const size_t tstep = (size_t)a.nkv * D;
     const bool owner = t0 <= p && p < t1;
 
-    // keys of a 32-token tile: token t0 + 32 i + tid / 8, 32 dims per thread
-    KVPack<KV> kn[8];
-    auto load_keys = [&](int i) {
-        const int tk = min(t0 + 32 * i + (tid >> 3), a.max_ctx - 1);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) kn[q].load(kc + (size_t)tk * tstep + 32 * q + 4 * s);
-    };
-    load_keys(0);
     if (tid < 32) {
         if (a.rope) {  // the session's table: the same angles and rounding
             const float2 cs = ((const float2*)a.rope)[(size_t)p * 32 + tid];
@@ -729,13 +744,8 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
     // ---- scores of the span's tiles
     const int nb = (n + 31) >> 5;
     {
-        float qv[G][8][4];
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int q = 0; q < 8; ++q)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) qv[g][q][e] = hv[g][32 * q + 4 * s + e];
+        // the queries are read from LDS at each use (held in registers beside
+        // the key and value tiles in flight they would halve the occupancy)
         for (int i = 0; i < nb; ++i) {
             KVPack<KV> cur[8];
 #pragma unroll
@@ -760,9 +770,12 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
 #pragma unroll
             for (int q = 0; q < 8; ++q)
 #pragma unroll
-                for (int g = 0; g < G; ++g)
+                for (int g = 0; g < G; ++g) {
+                    const v4f qq = *(const v4f*)&hv[g][32 * q + 4 * s];
+                    const float qe[4] = {qq.x, qq.y, qq.z, qq.w};
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(qv[g][q][e], kk[q][e], acc[g][e]);
+                    for (int e = 0; e < 4; ++e) acc[g][e] = fmaf(qe[e], kk[q][e], acc[g][e]);
+                }
             float dv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int g = 0; g < G; ++g) {
@@ -773,16 +786,6 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
             if (t < t1 && s == 7) scp[t - t0] = v4f{dv[0], dv[1], dv[2], dv[3]};
         }
     }
-    // values of a tile: wave w takes tokens t0 + 32 i + 8 w + u (u < 8), lane
-    // l channels 4l .. 4l+3; loaded while the statistics form (the first
-    // tile) or the previous tile is summed
-    KVPack<KV> vn[8];
-    auto load_values = [&](int i) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-            vn[u].load(vc + (size_t)min(t0 + 32 * i + 8 * wv + u, a.max_ctx - 1) * tstep + 4 * lane);
-    };
-    load_values(0);
     lds_barrier();
 
     // ---- span statistics per head: m, p = GGML exp(s - m), l
@@ -819,8 +822,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
 #pragma unroll
     for (int g = 0; g < G; ++g) l[g] = (red[1][g][0] + red[1][g][1]) + (red[1][g][2] + red[1][g][3]);
 
-    // ---- o = sum of p * v over the span: per wave its tokens, then the four
-    // waves added in wave order through LDS (the score LDS, once read)
+    // ---- o = sum of p * v over the span: per wave its tokens (the next
+    // tile's values requested while a tile is summed), then the four waves
+    // added in wave order through LDS (the score LDS, once read)
     float o[G][4];
 #pragma unroll
     for (int g = 0; g < G; ++g)
@@ -867,8 +871,8 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
     }
 }
 
-// Grid (q_heads, B): the spans' partials of one head combined, gated.
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int nc, const float* __restrict__ part) {
+// Grid (q_heads, B): the live spans' partials of one head combined, gated.
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int nc, int span, const float* __restrict__ part) {
     constexpr int D = 256;
     __shared__ float w[kSplitMaxChunks];
     __shared__ float red[2][4];
@@ -877,18 +881,19 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int
     const float* ml = part + 2 * slot;
     const float* po = part + 2 * nrow + slot * D + tid;
     const float gate = a.proj[(size_t)b * a.proj_stride + (size_t)h * 2 * D + D + tid];
+    const int na = min(nc, (a.pos[b] + span) / span);  // live spans: ceil((pos + 1) / span)
     // span c's {m, l} in thread c (nc <= 256); the first 64 spans' values
     // are requested with them
-    const float mc = tid < nc ? ml[2 * tid] : -INFINITY, lc = tid < nc ? ml[2 * tid + 1] : 0.0f;
+    const float mc = tid < na ? ml[2 * tid] : -INFINITY, lc = tid < na ? ml[2 * tid + 1] : 0.0f;
     float ov[64];
 #pragma unroll
-    for (int k = 0; k < 64; ++k) ov[k] = po[(size_t)min(k, nc - 1) * D];
+    for (int k = 0; k < 64; ++k) ov[k] = po[(size_t)min(k, na - 1) * D];
     float mx = wave_max_all(mc);
     if (lane == 0) red[0][wv] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
     const float wc = mc == -INFINITY ? 0.0f : cr_expf(mc - mx);
-    if (tid < nc) w[tid] = wc;
+    if (tid < na) w[tid] = wc;
     const float ls = wave_sum_all(wc * lc);
     if (lane == 0) red[1][wv] = ls;
     __syncthreads();
@@ -896,13 +901,13 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int
     float o = 0.0f;
 #pragma unroll
     for (int k = 0; k < 64; ++k)
-        if (k < nc) o = fmaf(w[k], ov[k], o);
-    for (int c0 = 64; c0 < nc; c0 += 64) {
+        if (k < na) o = fmaf(w[k], ov[k], o);
+    for (int c0 = 64; c0 < na; c0 += 64) {
 #pragma unroll
-        for (int k = 0; k < 64; ++k) ov[k] = po[(size_t)min(c0 + k, nc - 1) * D];
+        for (int k = 0; k < 64; ++k) ov[k] = po[(size_t)min(c0 + k, na - 1) * D];
 #pragma unroll
         for (int k = 0; k < 64; ++k)
-            if (c0 + k < nc) o = fmaf(w[c0 + k], ov[k], o);
+            if (c0 + k < na) o = fmaf(w[c0 + k], ov[k], o);
     }
     const float v = (o / L) * source_sigmoid(gate);
     a.out[(size_t)b * a.out_stride + (size_t)h * D + tid] = v;
@@ -937,13 +942,14 @@ hipError_t rope_table(float* tab, size_t n, float theta_scale, hipStream_t s) {
 hipError_t attn_decode_split(const AttnDecodeArgs& a, size_t B, float* part, hipStream_t s) {
     if (!attn_split_supported(B, a.nq, a.nkv, (size_t)a.max_ctx) || !part) return hipErrorInvalidValue;
     const int G = a.nq / a.nkv, nc = attn_split_chunks(B, a.nkv, (size_t)a.max_ctx);
+    const int span = attn_split_span(B, a.nkv, (size_t)a.max_ctx);
     const dim3 g((unsigned)nc, (unsigned)a.nkv, (unsigned)B);
-#define ZG_SP(KV)                                                                                      \
-    switch (G) {                                                                                       \
-    case 1: hipLaunchKernelGGL((attn_split_kernel<KV, 1>), g, dim3(256), 0, s, a, nc, part); break;    \
-    case 2: hipLaunchKernelGGL((attn_split_kernel<KV, 2>), g, dim3(256), 0, s, a, nc, part); break;    \
-    case 3: hipLaunchKernelGGL((attn_split_kernel<KV, 3>), g, dim3(256), 0, s, a, nc, part); break;    \
-    default: hipLaunchKernelGGL((attn_split_kernel<KV, 4>), g, dim3(256), 0, s, a, nc, part); break;   \
+#define ZG_SP(KV)                                                                                            \
+    switch (G) {                                                                                             \
+    case 1: hipLaunchKernelGGL((attn_split_kernel<KV, 1>), g, dim3(256), 0, s, a, nc, span, part); break;    \
+    case 2: hipLaunchKernelGGL((attn_split_kernel<KV, 2>), g, dim3(256), 0, s, a, nc, span, part); break;    \
+    case 3: hipLaunchKernelGGL((attn_split_kernel<KV, 3>), g, dim3(256), 0, s, a, nc, span, part); break;    \
+    default: hipLaunchKernelGGL((attn_split_kernel<KV, 4>), g, dim3(256), 0, s, a, nc, span, part); break;   \
     }
     if (a.kv_bf16) {
         ZG_SP(uint16_t)
@@ -951,7 +957,8 @@ hipError_t attn_decode_split(const AttnDecodeArgs& a, size_t B, float* part, hip
         ZG_SP(float)
     }
 #undef ZG_SP
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.nq, (unsigned)B), dim3(256), 0, s, a, nc, (const float*)part);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.nq, (unsigned)B), dim3(256), 0, s, a, nc, span,
+                       (const float*)part);
     return hipGetLastError();
 }
 
