@@ -861,10 +861,48 @@ def bench_copy(args):
     us = e0.elapsed_time(e1) * 1e3 / steps
     gbs = 2 * n * 4 / us / 1e3
     log(f"copy 256 MiB: {us:.1f} us  {gbs:.0f} GB/s read+write")
+    del a, b
+    ceilings = bandwidth_ceilings(torch) if args.ceilings else None
     return {"metric": "device copy GB/s (256 MiB read + 256 MiB written)", "value": round(gbs, 1), "unit": "GB/s",
             "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(us / 1e3, 4),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-            "config": {"workload": "calibration copy", "bytes_read": n * 4, "bytes_written": n * 4}}
+            "config": {"workload": "calibration copy", "bytes_read": n * 4, "bytes_written": n * 4,
+                       "ceilings_gbs": ceilings}}
+
+
+def bandwidth_ceilings(torch, reps=20):
+    """Read + write bandwidth of this box for the two patterns the GDN decode
+    state can take: a copy (read one buffer, write another: the double-
+    buffered state of a session step) and an in-place read-modify-write (the
+    region entry's state).  One vectorised elementwise kernel per buffer,
+    rotating over buffers totalling more than 1 GiB so that nothing is served
+    from the 256 MB Infinity Cache; GB/s counts bytes read plus written."""
+    out = {"copy": {}, "rmw": {}}
+    for mib in (16, 64, 256):
+        n = (mib << 20) // 4
+        k = max(2, (1024 // mib) + 1)
+        src = [torch.randn(n, device="cuda") for _ in range(k)]
+        dst = [torch.empty_like(src[0]) for _ in range(k)]
+        for kind in ("copy", "rmw"):
+            def run(i):
+                if kind == "copy":
+                    torch.mul(src[i % k], 1.0001, out=dst[i % k])
+                else:
+                    src[i % k].mul_(0.9999)
+            for i in range(k):
+                run(i)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(reps * k):
+                run(i)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (reps * k)
+            out[kind][f"{mib}MiB"] = round(2 * n * 4 / us / 1e3, 1)
+            log(f"{kind} {mib} MiB: {us:.1f} us  {out[kind][f'{mib}MiB']:.0f} GB/s read+write")
+        del src, dst
+    return out
 
 
 def cpu_gdn_baseline(seconds, H=16):
@@ -984,6 +1022,8 @@ def main():
     ap.add_argument("--leg-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="copy workload: also the copy and in-place read-modify-write ceilings at 16-256 MiB")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (batch rows are independent and "

@@ -440,6 +440,48 @@ float zgo_dot_f32_row(const uint8_t* row, const float* x, size_t n) {
     return result;
 }
 
+/* dot_row (cpu/src/source.rs:431-459) of four rows at once: each row keeps
+ * its own serial chain with exactly zgo_dot_q4k_row's operations and order
+ * (so each result is bit-identical to it); interleaving four independent
+ * chains only lets one core overlap their add latencies. */
+static void dot_q4k_rows4(const uint8_t* const row[4], const float* x, size_t nblocks, float out[4]) {
+    float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (size_t b = 0; b < nblocks; ++b) {
+        const float* inp = x + b * 256;
+        float d[4], dm[4];
+        const uint8_t* sc4[4];
+        const uint8_t* q4[4];
+        for (int r = 0; r < 4; ++r) {
+            const uint8_t* blk = row[r] + b * 144;
+            d[r] = zgo_f16_to_f32(rd16(blk));
+            dm[r] = zgo_f16_to_f32(rd16(blk + 2));
+            sc4[r] = blk + 4;
+            q4[r] = blk + 16;
+        }
+        for (int g = 0; g < 8; ++g) {
+            float scale[4], mnf[4];
+            for (int r = 0; r < 4; ++r) {
+                uint8_t sc, mn;
+                q4k_scale_min(sc4[r], g, &sc, &mn);
+                scale[r] = d[r] * (float)sc;
+                mnf[r] = dm[r] * (float)mn;
+            }
+            const float* gx = inp + g * 32;
+            for (int i = 0; i < 32; ++i) {
+                for (int r = 0; r < 4; ++r) {
+                    const uint8_t byte = q4[r][(g / 2) * 32 + i];
+                    const uint8_t v = (g & 1) ? (byte >> 4) : (byte & 15);
+                    float t = (float)v * scale[r];
+                    t = t - mnf[r];
+                    t = t * gx[i];
+                    sum[r] = sum[r] + t;
+                }
+            }
+        }
+    }
+    for (int r = 0; r < 4; ++r) out[r] = sum[r];
+}
+
 /* cpu/src/source.rs:234-313 (Source profile) with the pairing of
  * core/src/numerics.rs:96-122.  Q8_0 and Q4_0 pair with the dynamic Q8_0
  * activation (Q4_0 in the repacked schedule when rows % 8 == 0,
@@ -481,8 +523,17 @@ int zgo_matvec(int t, const uint8_t* w, size_t wbytes, size_t rows, size_t cols,
 #endif
     for (long long r = 0; r < nrows; ++r) {
         const uint8_t* row = w + (size_t)r * row_bytes;
-        if (t == ZGO_Q8_0) y[r] = zgo_dot_q8_0_row(row, qs, dd, cols / 32);
-        else if (t == ZGO_Q4_K) y[r] = zgo_dot_q4k_row(row, x, cols / 256);
+        if (t == ZGO_Q4_K) {
+            /* rows in groups of four per iteration (the whole group belongs
+             * to the thread holding its first row) */
+            if (r % 4) continue;
+            if (r + 4 <= nrows) {
+                const uint8_t* rows4[4] = {row, row + row_bytes, row + 2 * row_bytes, row + 3 * row_bytes};
+                dot_q4k_rows4(rows4, x, cols / 256, y + r);
+            } else {
+                for (long long q = r; q < nrows; ++q) y[q] = zgo_dot_q4k_row(w + (size_t)q * row_bytes, x, cols / 256);
+            }
+        } else if (t == ZGO_Q8_0) y[r] = zgo_dot_q8_0_row(row, qs, dd, cols / 32);
         else if (t == ZGO_Q4_0 && rows % 8 == 0) y[r] = zgo_dot_q4_0_repacked_row(row, qs, dd, cols / 32);
         else if (t == ZGO_Q4_0) y[r] = zgo_dot_q4_0_row(row, qs, dd, cols / 32);
         else if (t == ZGO_Q4_1) y[r] = zgo_dot_q4_1_row(row, qs, dd, ss, cols / 32);

@@ -208,3 +208,36 @@ def test_prefill_batched_prompt_gemm_matches_oracle(kern, n):
         tok = int(np.argmax(ref))
         assert int(np.argmax(s.forward(tok))) == int(np.argmax(o.forward(tok)))
     m.close()
+
+
+def test_prefill_batched_8192_matches_oracle(kern):
+    """The longest prompt the bench times: 8192 tokens at the 2B widths (4
+    layers, bf16 KV) through zg_prefill_batched -- prompt GEMM, chunked GDN
+    prefill over 128 chunks, prompt attention -- against the oracle's
+    token-by-token prefill of the same seeded model and prompt with glibc's
+    transcendentals (lib.rs:1119-1187; the expected values are the committed
+    fixture tests/golden/prefill_8192_oracle.npz, written by
+    tests/golden/make_prefill_8192.py because the oracle needs minutes for
+    this prompt): last logits within 2e-2 max-abs, the same greedy token,
+    the state (a fixed subsample of the export) within 1e-2 relative."""
+    import os
+    import sys
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    sys.path.insert(0, here)
+    import make_prefill_8192 as G
+    ref = np.load(os.path.join(here, "prefill_8192_oracle.npz"))
+    t = qwen35.synthetic_tensors(G.GEOMETRY, gguf.Q4_K, seed=G.WEIGHT_SEED)
+    m = qwen35.QwenModelHip(G.GEOMETRY, t, kernel=kern)
+    s = m.session(max_batch=1, max_context=G.GEOMETRY["max_context"], kv_dtype=L.BF16)
+    lg = s.prefill_batched(G.prompt())
+    assert s.position == G.N_PROMPT
+    st = s.state()
+    idx, total = G.state_index(G.GEOMETRY, G.N_PROMPT)
+    assert st.size == total and np.array_equal(idx, ref["state_idx"])
+    worst = float(np.max(np.abs(lg - ref["logits"])))
+    e_state = rel_err(st[idx], ref["state"])
+    print(f"batched prefill n=8192: logits max-abs {worst:.3e} vs the oracle, state rel {e_state:.2e}")
+    assert worst <= LOGIT_TOL
+    assert int(np.argmax(lg)) == int(ref["greedy"][0])
+    assert e_state <= 1e-2
+    m.close()

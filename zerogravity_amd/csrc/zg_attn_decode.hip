@@ -882,12 +882,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int
     const float* po = part + 2 * nrow + slot * D + tid;
     const float gate = a.proj[(size_t)b * a.proj_stride + (size_t)h * 2 * D + D + tid];
     const int na = min(nc, (a.pos[b] + span) / span);  // live spans: ceil((pos + 1) / span)
-    // span c's {m, l} in thread c (nc <= 256); the first 64 spans' values
-    // are requested with them
+    // span c's {m, l} in thread c (nc <= 256); the first 128 spans' values
+    // are requested with them (one round trip up to 128 live spans)
     const float mc = tid < na ? ml[2 * tid] : -INFINITY, lc = tid < na ? ml[2 * tid + 1] : 0.0f;
-    float ov[64];
+    float ov[128];
 #pragma unroll
-    for (int k = 0; k < 64; ++k) ov[k] = po[(size_t)min(k, na - 1) * D];
+    for (int k = 0; k < 128; ++k) ov[k] = po[(size_t)min(k, na - 1) * D];  // unconditional: issued back to back
     float mx = wave_max_all(mc);
     if (lane == 0) red[0][wv] = mx;
     __syncthreads();
@@ -900,13 +900,13 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int
     const float L = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
     float o = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 64; ++k)
+    for (int k = 0; k < 128; ++k)
         if (k < na) o = fmaf(w[k], ov[k], o);
-    for (int c0 = 64; c0 < na; c0 += 64) {
+    for (int c0 = 128; c0 < na; c0 += 128) {
 #pragma unroll
-        for (int k = 0; k < 64; ++k) ov[k] = po[(size_t)min(c0 + k, na - 1) * D];
+        for (int k = 0; k < 128; ++k) ov[k] = po[(size_t)min(c0 + k, na - 1) * D];
 #pragma unroll
-        for (int k = 0; k < 64; ++k)
+        for (int k = 0; k < 128; ++k)
             if (c0 + k < na) o = fmaf(w[c0 + k], ov[k], o);
     }
     const float v = (o / L) * source_sigmoid(gate);

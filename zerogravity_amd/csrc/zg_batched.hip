@@ -395,6 +395,8 @@ __global__ __launch_bounds__(64 * kM16Waves) __attribute__((amdgpu_waves_per_eu(
         }
         return vt * 16 + r16;  // < 16 * nvt: inside the zero-padded last tile
     };
+    // weights and headers stream (read once per step): non-temporal loads
+    // keep the activation block, which every workgroup re-reads, in L2
     auto issue = [&](v4u (&wq)[UPW][TMAX], v4u (&hd)[NH][TMAX], int tb) {
 #pragma unroll
         for (int t = 0; t < TMAX; ++t) {
@@ -404,8 +406,8 @@ __global__ __launch_bounds__(64 * kM16Waves) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
                 for (int u = 0; u < UPW; ++u) {
                     if (NH == UPW || u % 2 == 0)
-                        hd[NH == UPW ? u : u / 2][t] = hdr[(tile * nbk + ((ub + u) >> 1)) * 16 + (row & 15)];
-                    wq[u][t] = *(const v4u*)(qs + ((tile * nunits + ub + u) * 64 + (row & 15) + 16 * h + 32 * cp) * 16);
+                        hd[NH == UPW ? u : u / 2][t] = __builtin_nontemporal_load(hdr + (tile * nbk + ((ub + u) >> 1)) * 16 + (row & 15));
+                    wq[u][t] = __builtin_nontemporal_load((const v4u*)(qs + ((tile * nunits + ub + u) * 64 + (row & 15) + 16 * h + 32 * cp) * 16));
                 }
             }
         }

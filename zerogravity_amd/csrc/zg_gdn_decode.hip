@@ -75,9 +75,13 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
     const size_t within = ((size_t)h * D + j) * D + 4 * s;
     const float* col = a.state + (size_t)b * row_floats + (size_t)cb * a.state_half + within;
     float* col_out = a.state + (size_t)b * row_floats + (a.cur ? (size_t)(1 - cb) * a.state_half : 0) + within;
+    // a row's state (1 MB per layer) is read once and written once per step
+    // and the step's states outgrow the 256 MB Infinity Cache from B = 8
+    // on: non-temporal loads and stores leave L2 and the Infinity Cache to
+    // the step's other operands
     v4f sv[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) sv[c] = *(const v4f*)(col + 32 * c);
+    for (int c = 0; c < 4; ++c) sv[c] = __builtin_nontemporal_load((const v4f*)(col + 32 * c));
     const int p = a.pos[b];
     const int s0 = (p + 1) & 3, s1 = (p + 2) & 3, s2 = (p + 3) & 3, sw = p & 3;
     auto conv = [&](const ConvIn& c) {
@@ -223,7 +227,7 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
         o = column_dot(cv, q);
     }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) *(v4f*)(col_out + 32 * c) = v4f{cv[c][0], cv[c][1], cv[c][2], cv[c][3]};
+    for (int c = 0; c < 4; ++c) __builtin_nontemporal_store(v4f{cv[c][0], cv[c][1], cv[c][2], cv[c][3]}, (v4f*)(col_out + 32 * c));
     if (s == 0) a.core[(size_t)b * W + h * D + j] = o * a.scale;
     if constexpr (HEAD) {
         // gated RMSNorm of the head (forward.rs:586-594) in act16_kernel's
