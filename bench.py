@@ -177,7 +177,7 @@ def run_decode(model, torch, B, prefix, steps, warmup, seed):
 
 
 # Prologue / epilogue codes of zg_gemv_device_fused (include/zg_hip.h)
-PRO_RMS, PRO_GATED, PRO_SILU_MUL, PRO_PLAIN = 0, 1, 2, 3
+PRO_RMS, PRO_GATED, PRO_SILU_MUL, PRO_PLAIN, PRO_GATED_PRE = 0, 1, 2, 3, 5
 EPI_STORE, EPI_RESID, EPI_GLU = 0, 1, 2
 
 
@@ -203,7 +203,8 @@ def step_projections(g):
             out.append((p + "gdn_in", [p + "attn_qkv.weight", p + "attn_gate.weight", p + "ssm_alpha.weight",
                                        p + "ssm_beta.weight"], H, 4 * W + 2 * g["gdn_heads"], PRO_RMS, EPI_STORE,
                         role))
-            out.append((p + "ssm_out", [p + "ssm_out.weight"], W, H, PRO_GATED, EPI_RESID, ""))
+            # (the GDN kernel forms the gated product; ssm_out applies the 1/rms)
+            out.append((p + "ssm_out", [p + "ssm_out.weight"], W, H, PRO_GATED_PRE, EPI_RESID, ""))
         out.append((p + "ffn_gate_up", [p + "ffn_gate.weight", p + "ffn_up.weight"], H, 2 * F, PRO_RMS, EPI_GLU,
                     ""))
         out.append((p + "ffn_down", [p + "ffn_down.weight"], F, H, PRO_PLAIN, EPI_RESID, ""))
@@ -216,8 +217,9 @@ def gemv_leg(kern, torch, g, tensors, kind, reps):
     replayed exactly as the step launches them -- the same stacked matrices,
     the same prologue and epilogue per projection (zg_gemv_device_fused ->
     the step's own dispatcher, so the same kernel template variants: the
-    embedding prologue on the first, the gated RMSNorm on ssm_out, SwiGLU
-    into the down projection's input, residual adds, greedy partials on the
+    embedding prologue on the first, the gated RMSNorm's 1/rms on ssm_out
+    (whose product the GDN kernel forms), SwiGLU into the down projection's
+    input, residual adds, greedy partials on the
     LM head) -- captured once in a HIP graph as the step is, and the graph
     replayed `reps` times between HIP events on its stream.  ~0.95 GB per
     replay, so the weights stream from HBM, not the 256 MB Infinity Cache.
@@ -260,7 +262,7 @@ def gemv_leg(kern, torch, g, tensors, kind, reps):
             if role == "embed":
                 x, emb, tk = bufs["x_emb"], embd.h, tok.data_ptr()
             if label.endswith("ssm_out"):
-                x, x2, gam = bufs["core"], bufs["z"], bufs["norm"]
+                x, x2, gam = bufs["core"], bufs["z"], None
             elif label.endswith("attn_output"):
                 x, gam = bufs["attn"], None
             elif label.endswith("ffn_down"):

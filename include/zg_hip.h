@@ -454,7 +454,7 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
                    const float* gamma, float eps, float* y, void* stream);
 
 /* Prologue and epilogue forms of the decode step's projections. */
-enum { ZG_PRO_RMS = 0, ZG_PRO_GATED = 1, ZG_PRO_SILU_MUL = 2, ZG_PRO_PLAIN = 3 };
+enum { ZG_PRO_RMS = 0, ZG_PRO_GATED = 1, ZG_PRO_SILU_MUL = 2, ZG_PRO_PLAIN = 3, ZG_PRO_GATED_PRE = 5 };
 enum { ZG_EPI_STORE = 0, ZG_EPI_RESID = 1, ZG_EPI_GLU = 2 };
 
 /* One projection of the resident decode step with the operations around it
@@ -465,6 +465,11 @@ enum { ZG_EPI_STORE = 0, ZG_EPI_RESID = 1, ZG_EPI_GLU = 2 };
  *            ZG_PRO_GATED     grouped RMSNorm(x, gamma[group], eps) * silu(x2) (forward.rs:586-594)
  *            ZG_PRO_SILU_MUL  x2 * silu(x) (forward.rs:498)
  *            ZG_PRO_PLAIN     x
+ *            ZG_PRO_GATED_PRE ZG_PRO_GATED with the product (x * gamma[i % group])
+ *                             * silu(z) already formed by the producer in x2
+ *                             (x the norm input); one row of a Q4_K weight
+ *                             with K a multiple of 512, group 128 -- the
+ *                             one-row step's ssm_out, after the GDN kernel
  *   epilogue ZG_EPI_STORE     y = W a
  *            ZG_EPI_RESID     y = y + W a, the residual add (forward.rs:489,501)
  *            ZG_EPI_GLU       w stacks [gate | up] (N even): y[0:N/2] = up * silu(gate)

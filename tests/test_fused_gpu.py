@@ -100,6 +100,47 @@ def test_fused_forms_match_oracle(kern, kind, M, form):
     _check(kind, dy.cpu().numpy(), ref)
 
 
+PRO_GATED_PRE = 5
+
+
+@pytest.mark.parametrize("kind", [synth.Q8_0, synth.Q4_K])
+def test_fused_gated_pre_is_the_gated_form(kern, kind):
+    """ZG_PRO_GATED_PRE, the one-row step's ssm_out (the GDN kernel forms
+    (x * gamma) * silu(z) once, the projection applies the per-head 1/rms):
+    with x2 holding that product formed by the same float operations (the
+    oracle's silu is the device's bit for bit) the result is ZG_PRO_GATED's
+    bit for bit, and within 1e-3 of the reference's order.  N = 2048 takes
+    the 8-row tiles.  Other codecs and several rows are refused."""
+    import torch
+    rng = np.random.default_rng(1717)
+    K, N = 2048, 2048
+    w = synth.random_matrix(rng, kind, N, K)
+    h = kern.register(730 + kind, f"fused.pre.{kind}", kind, K, N, w.reshape(-1))
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    z = rng.standard_normal((1, K)).astype(np.float32)
+    g = (1.0 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    y0 = rng.standard_normal((1, N)).astype(np.float32)
+    u = O.silu(z[0], mult=x[0] * np.tile(g, K // 128))[None]
+    dx, dz, du, dg = (torch.from_numpy(a.copy()).cuda() for a in (x, z, u, g))
+    if kind != synth.Q4_K:
+        dy = torch.from_numpy(y0.copy()).cuda()
+        assert _fused(kern, h, 1, PRO_GATED_PRE, EPI_RESID, dx, du, None, dy, N) == L.UNSUPPORTED
+        return
+    dy_g = torch.from_numpy(y0.copy()).cuda()
+    assert _fused(kern, h, 1, PRO_GATED, EPI_RESID, dx, dz, dg, dy_g, N) == L.COMPLETED
+    dy_p = torch.from_numpy(y0.copy()).cuda()
+    assert _fused(kern, h, 1, PRO_GATED_PRE, EPI_RESID, dx, du, None, dy_p, N) == L.COMPLETED
+    got_g, got_p = dy_g.cpu().numpy(), dy_p.cpu().numpy()
+    assert np.array_equal(got_p.view(np.uint32), got_g.view(np.uint32))
+    a = O.silu(z[0], mult=O.grouped_rms_norm(x[0], g, K // 128, 1e-6))
+    ref = O.binary(0, y0[0], O.matvec(kind, w.reshape(-1), N, K, a))[None]
+    _check(kind, got_p, ref)
+    x3 = torch.from_numpy(np.repeat(x, 3, 0)).cuda()
+    u3 = torch.from_numpy(np.repeat(u, 3, 0)).cuda()
+    y3 = torch.from_numpy(np.repeat(y0, 3, 0)).cuda()
+    assert _fused(kern, h, 3, PRO_GATED_PRE, EPI_RESID, x3, u3, None, y3, N) == L.UNSUPPORTED
+
+
 def test_fused_embedding_prologue_and_greedy_partials(kern):
     """One row: the token's Q4_K embedding row dequantised in the prologue
     (stored at x bit-exactly) feeding an RMS projection, and an LM-head

@@ -540,7 +540,8 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
 }
 
 static_assert(ZG_PRO_RMS == zg::PRO_RMS && ZG_PRO_GATED == zg::PRO_GATED && ZG_PRO_SILU_MUL == zg::PRO_SILU_MUL &&
-                  ZG_PRO_PLAIN == zg::PRO_PLAIN && ZG_EPI_STORE == zg::EPI_STORE && ZG_EPI_RESID == zg::EPI_RESID &&
+                  ZG_PRO_PLAIN == zg::PRO_PLAIN && ZG_PRO_GATED_PRE == zg::PRO_GATED_PRE &&
+                  ZG_EPI_STORE == zg::EPI_STORE && ZG_EPI_RESID == zg::EPI_RESID &&
                   ZG_EPI_GLU == zg::EPI_GLU,
               "C-ABI prologue/epilogue codes are the kernels' own");
 
@@ -559,16 +560,21 @@ int zg_gemv_device_fused(zg_ctx* ctx, const zg_weight* w, size_t m_rows, int pro
     if (!ctx) return ZG_E_MALFORMED;
     std::lock_guard<std::recursive_mutex> g(ctx->mu);
     (void)hipSetDevice(ctx->device);
-    if (!w || !x || !y || m_rows == 0 || m_rows > 4 || prologue < ZG_PRO_RMS || prologue > ZG_PRO_PLAIN ||
+    if (!w || !x || !y || m_rows == 0 || m_rows > 4 ||
+        !(prologue == ZG_PRO_RMS || prologue == ZG_PRO_GATED || prologue == ZG_PRO_SILU_MUL ||
+          prologue == ZG_PRO_PLAIN || prologue == ZG_PRO_GATED_PRE) ||
         epilogue < ZG_EPI_STORE || epilogue > ZG_EPI_GLU)
         return fail(ctx, ZG_E_MALFORMED, "invalid fused gemv arguments");
     const size_t K = w->dw.K, N = w->dw.N;
-    const bool needs_x2 = prologue == ZG_PRO_GATED || prologue == ZG_PRO_SILU_MUL;
+    const bool needs_x2 = prologue == ZG_PRO_GATED || prologue == ZG_PRO_SILU_MUL || prologue == ZG_PRO_GATED_PRE;
     const bool needs_gamma = prologue == ZG_PRO_RMS || prologue == ZG_PRO_GATED;
     if ((needs_x2 && !x2) || (needs_gamma && !gamma) || ldx < K || (needs_x2 && ldx2 < K) ||
         ldy < (epilogue == ZG_EPI_GLU ? N / 2 : N) || !(eps > 0.0f || !needs_gamma))
         return fail(ctx, ZG_E_MALFORMED, "fused gemv operand missing or stride too short");
     if (prologue == ZG_PRO_GATED && (group == 0 || K % group)) return fail(ctx, ZG_E_MALFORMED, "gated norm group");
+    if (prologue == ZG_PRO_GATED_PRE && (m_rows != 1 || group != 128 || epilogue == ZG_EPI_GLU ||
+                                         !zg::gated_pre_supported(w->dw)))
+        return fail(ctx, ZG_UNSUPPORTED, "formed gated product: one row, group 128, matrix-core Q4_K GEMV");
     if (!zg::fused_gemv_supported(w->dw.type, K, N, prologue))
         return fail(ctx, ZG_UNSUPPORTED, "no fused projection kernel for this weight and prologue");
     if (epilogue == ZG_EPI_GLU && !zg::fused_glu_supported(w->dw.type, K, N))

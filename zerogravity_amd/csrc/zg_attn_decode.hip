@@ -587,14 +587,15 @@ hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
 // of 32 fixed per launch, so a workgroup's key and value addresses do not
 // depend on the position: its first tile of each is requested before the
 // position arrives, and a span at or past the row's T = pos + 1 tokens
-// ends at once).  It normalises and ropes the G query heads and the new
+// records itself empty, m = -inf and l = 0, and ends).  It normalises and ropes the G query heads and the new
 // key as attn_decode_qk_kernel does (the workgroup whose span holds the
 // position appends K/V and uses its own rounded copies for that token),
 // scores its tokens in the 32-accumulator order, and keeps per head the
 // span's max m, l = sum of GGML exp(s - m) and o = sum of exp(s - m) * v.
 // attn_combine_kernel then forms sum_c e^(m_c - M) o_c / sum_c e^(m_c - M)
-// l_c over the row's live spans c < ceil(T / S), M = max_c m_c, and applies
-// the sigmoid gate (forward.rs:751).  The reference (lib.rs:1276-1387)
+// l_c over the row's spans (the empty ones weigh 0), M = max_c m_c, wave w
+// summing spans w, w + 4, ... and the four waves' sums added in a fixed
+// order, and applies the sigmoid gate (forward.rs:751).  The reference (lib.rs:1276-1387)
 // normalises with the global max first and runs the value sums as
 // token-ordered chains: this regrouping agrees with it to f32 rounding (the
 // per-op 1e-3 bar), not bit for bit.
@@ -630,7 +631,7 @@ size_t attn_split_part_bytes(size_t B, int nq, int nkv, size_t max_ctx) {
 }
 
 // Partials: {m, l} per (row, head, span) at part, then o [row][head][span][256];
-// only the live spans of a row are written.
+// o is written for the spans that hold tokens of the row only.
 template <typename KV, int G>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int nc, int span, float* __restrict__ part) {
     constexpr int D = 256;
@@ -684,11 +685,17 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
 
     const int T = p + 1;
     const int t1 = min(T, t0 + span), n = t1 - t0;
-    if (n <= 0) return;  // past the row's tokens: the combine reads spans [0, ceil(T / span))
     const size_t nrow = (size_t)gridDim.z * a.nq * nc;
     const size_t slot = ((size_t)b * a.nq + (size_t)kvh * G) * nc + c;  // head g at slot + g * nc
     float* ml = part;
     float* po = part + 2 * nrow;
+    if (n <= 0) {  // past the row's tokens: an empty span, m = -inf and l = 0 (its o is never read)
+        if (tid < G) {
+            ml[2 * (slot + (size_t)tid * nc)] = -INFINITY;
+            ml[2 * (slot + (size_t)tid * nc) + 1] = 0.0f;
+        }
+        return;
+    }
     const bool owner = t0 <= p && p < t1;
 
     if (tid < 32) {
@@ -871,45 +878,63 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
     }
 }
 
-// Grid (q_heads, B): the live spans' partials of one head combined, gated.
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int nc, int span, const float* __restrict__ part) {
-    constexpr int D = 256;
+// Grid (q_heads, B): the spans' partials of one head combined, gated.
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int nc, const float* __restrict__ part) {
+    constexpr int D = 256, CB = 16;  // spans per wave per batch of loads
     __shared__ float w[kSplitMaxChunks];
     __shared__ float red[2][4];
+    __shared__ v4f ow[4][D / 4];
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const size_t nrow = (size_t)gridDim.y * a.nq * nc, slot = ((size_t)b * a.nq + h) * nc;
     const float* ml = part + 2 * slot;
-    const float* po = part + 2 * nrow + slot * D + tid;
+    const v4f* po = (const v4f*)(part + 2 * nrow + slot * D) + lane;
+    // every span has {m, l} (an empty one -inf, 0), so no load waits on the
+    // position: span c's {m, l} in thread c (nc <= 256), and wave w's first
+    // CB spans w, w + 4, ... (lane l: channels 4l .. 4l+3) requested at once
+    const float mc = tid < nc ? ml[2 * tid] : -INFINITY, lc = tid < nc ? ml[2 * tid + 1] : 0.0f;
     const float gate = a.proj[(size_t)b * a.proj_stride + (size_t)h * 2 * D + D + tid];
-    const int na = min(nc, (a.pos[b] + span) / span);  // live spans: ceil((pos + 1) / span)
-    // span c's {m, l} in thread c (nc <= 256); the first 128 spans' values
-    // are requested with them (one round trip up to 128 live spans)
-    const float mc = tid < na ? ml[2 * tid] : -INFINITY, lc = tid < na ? ml[2 * tid + 1] : 0.0f;
-    float ov[128];
+    const int nw = (nc - wv + 3) / 4;  // this wave's spans
+    v4f ov[CB];
 #pragma unroll
-    for (int k = 0; k < 128; ++k) ov[k] = po[(size_t)min(k, na - 1) * D];  // unconditional: issued back to back
+    for (int k = 0; k < CB; ++k)
+        if (k < nw) ov[k] = po[(size_t)(wv + 4 * k) * (D / 4)];
     float mx = wave_max_all(mc);
     if (lane == 0) red[0][wv] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
     const float wc = mc == -INFINITY ? 0.0f : cr_expf(mc - mx);
-    if (tid < na) w[tid] = wc;
+    w[tid] = wc;
     const float ls = wave_sum_all(wc * lc);
     if (lane == 0) red[1][wv] = ls;
     __syncthreads();
     const float L = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
-    float o = 0.0f;
+    // wave w's sum over its spans in span order; an empty span (weight 0)
+    // is skipped, its o never having been written
+    v4f o = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < nw; k0 += CB) {
+        if (k0) {
 #pragma unroll
-    for (int k = 0; k < 128; ++k)
-        if (k < na) o = fmaf(w[k], ov[k], o);
-    for (int c0 = 128; c0 < na; c0 += 128) {
+            for (int k = 0; k < CB; ++k)
+                if (k0 + k < nw) ov[k] = po[(size_t)(wv + 4 * (k0 + k)) * (D / 4)];
+        }
 #pragma unroll
-        for (int k = 0; k < 128; ++k) ov[k] = po[(size_t)min(c0 + k, na - 1) * D];
-#pragma unroll
-        for (int k = 0; k < 128; ++k)
-            if (c0 + k < na) o = fmaf(w[c0 + k], ov[k], o);
+        for (int k = 0; k < CB; ++k) {
+            if (k0 + k < nw) {
+                const float wk = w[wv + 4 * (k0 + k)];
+                if (wk != 0.0f) {
+                    o.x = fmaf(wk, ov[k].x, o.x);
+                    o.y = fmaf(wk, ov[k].y, o.y);
+                    o.z = fmaf(wk, ov[k].z, o.z);
+                    o.w = fmaf(wk, ov[k].w, o.w);
+                }
+            }
+        }
     }
-    const float v = (o / L) * source_sigmoid(gate);
+    ow[wv][lane] = o;
+    __syncthreads();
+    const float* of = (const float*)ow;  // [wave][channel]
+    const float ot = (of[tid] + of[D + tid]) + (of[2 * D + tid] + of[3 * D + tid]);
+    const float v = (ot / L) * source_sigmoid(gate);
     a.out[(size_t)b * a.out_stride + (size_t)h * D + tid] = v;
     if (tid == 0 && !(L >= 1.0f && L < INFINITY)) atomicOr(a.status, 8);
     if (a.xh) {  // batched rows: also the output projection's f16 A tiles
@@ -957,8 +982,7 @@ hipError_t attn_decode_split(const AttnDecodeArgs& a, size_t B, float* part, hip
         ZG_SP(float)
     }
 #undef ZG_SP
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.nq, (unsigned)B), dim3(256), 0, s, a, nc, span,
-                       (const float*)part);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.nq, (unsigned)B), dim3(256), 0, s, a, nc, (const float*)part);
     return hipGetLastError();
 }
 

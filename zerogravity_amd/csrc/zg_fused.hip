@@ -9,6 +9,7 @@ extern template hipError_t launch_pro<PRO_RMS>(const FusedGemvArgs&, int, hipStr
 extern template hipError_t launch_pro<PRO_GATED>(const FusedGemvArgs&, int, hipStream_t);
 extern template hipError_t launch_pro<PRO_SILU_MUL>(const FusedGemvArgs&, int, hipStream_t);
 extern template hipError_t launch_pro<PRO_PLAIN>(const FusedGemvArgs&, int, hipStream_t);
+hipError_t launch_gated_pre(const FusedGemvArgs& a, int type, hipStream_t s);
 
 bool fused_glu_supported(int type, size_t K, size_t N) {
     // a row group must hold whole (gate, up) pairs: 64 lanes over <= 32
@@ -23,6 +24,7 @@ bool batched_glu_supported(int type, size_t K, size_t N) {
 bool fused_gemv_supported(int type, size_t K, size_t N, int pro) {
     if (N == 0 || K == 0 || N > (1u << 30)) return false;
     if (pro == PRO_GATED && (K % 128 || K / 128 > 256 || 256 % (K / 128))) return false;
+    if (pro == PRO_GATED_PRE && (type != kQ4_K || K % 512)) return false;
     if (K > 8192) return false;  // prologue slabs
     if (type == kQ4_K || type == kQ6_K) return K % 256 == 0;
     if (type == kQ8_0 || type == kQ4_1) return K % 32 == 0;
@@ -41,6 +43,17 @@ int gemv1_greedy_parts(const DeviceWeight& w, int pro) {
     return gemv1_grid((int)w.N, EPI_STORE);
 }
 
+bool gated_pre_supported(const DeviceWeight& w) {
+    FusedGemvArgs a;
+    a.M = 1;
+    a.K = (int)w.K;
+    a.N = (int)w.N;
+    a.pro = PRO_GATED_PRE;
+    a.epi = EPI_RESID;
+    a.group = 128;
+    return fused_gemv_supported(w.type, w.K, w.N, PRO_GATED_PRE) && gemv1_fits(a, w.type);
+}
+
 bool gemv1_embed_supported(const DeviceWeight& w, const DeviceWeight& emb) {
     return emb.type == kQ4_K && emb.K == w.K && emb.N > 0 && emb.N < (1u << 31) &&
            gemv1_greedy_parts(w, PRO_RMS) > 0;
@@ -48,7 +61,8 @@ bool gemv1_embed_supported(const DeviceWeight& w, const DeviceWeight& emb) {
 
 hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& args, hipStream_t s) {
     if (!fused_gemv_supported(w.type, w.K, w.N, args.pro) || args.M <= 0) return hipErrorInvalidValue;
-    if (args.pro == PRO_GATED && args.group != 128) return hipErrorInvalidValue;  // 32 lanes x 4 per group
+    if ((args.pro == PRO_GATED || args.pro == PRO_GATED_PRE) && args.group != 128)
+        return hipErrorInvalidValue;  // 32 lanes x 4 per group
     if (args.epi == EPI_GLU && !fused_glu_supported(w.type, w.K, w.N)) return hipErrorInvalidValue;
     FusedGemvArgs a = args;
     a.qs = w.qs;
@@ -60,6 +74,7 @@ hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& args, hipStrea
     case PRO_GATED: return launch_pro<PRO_GATED>(a, w.type, s);
     case PRO_SILU_MUL: return launch_pro<PRO_SILU_MUL>(a, w.type, s);
     case PRO_PLAIN: return launch_pro<PRO_PLAIN>(a, w.type, s);
+    case PRO_GATED_PRE: return launch_gated_pre(a, w.type, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -736,7 +736,7 @@ hipError_t launch_q8(const FusedGemvArgs& a, hipStream_t s) {
 inline bool gemv1_fits(const FusedGemvArgs& a, int type) {
     const int wv = a.K / 512;
     return type == kQ4_K && a.M == 1 && a.K % 512 == 0 && (wv <= 8 || wv == 12 || wv == 16) &&
-           (a.pro != PRO_GATED || a.group == 128) && (a.epi != EPI_GLU || a.N % 2 == 0);
+           ((a.pro != PRO_GATED && a.pro != PRO_GATED_PRE) || a.group == 128) && (a.epi != EPI_GLU || a.N % 2 == 0);
 }
 
 template <int PRO>

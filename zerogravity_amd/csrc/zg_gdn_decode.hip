@@ -68,6 +68,13 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
         tail_g = *(const v4f*)(a.norm + 4 * t);
         tail_z = *(const v4f*)(xin + 3 * W + h * D + 4 * t);
     }
+    // one workgroup per quarter with `gated`: the column's z and norm
+    // weight for the output projection's product, requested now as well
+    float gz = 0.0f, gg = 0.0f;
+    if (!HEAD && a.gated) {
+        gz = xin[3 * W + h * D + j];
+        gg = a.norm[j];
+    }
     // the row's state: read from half cur[b], written to the other half (the
     // draft the step's commit publishes), or in place without cur
     const size_t row_floats = a.state_row ? a.state_row : (size_t)a.H * D * D;
@@ -228,7 +235,12 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) __builtin_nontemporal_store(v4f{cv[c][0], cv[c][1], cv[c][2], cv[c][3]}, (v4f*)(col_out + 32 * c));
-    if (s == 0) a.core[(size_t)b * W + h * D + j] = o * a.scale;
+    const float core = o * a.scale;
+    if (s == 0) a.core[(size_t)b * W + h * D + j] = core;
+    // (core * norm) * silu(z): PRO_GATED's product (forward.rs:586-594
+    // before the 1/rms), once per element instead of in every workgroup of
+    // the output projection
+    if (!HEAD && a.gated && s == 0) a.gated[(size_t)b * W + h * D + j] = (core * gg) * ggml_silu(gz);
     if constexpr (HEAD) {
         // gated RMSNorm of the head (forward.rs:586-594) in act16_kernel's
         // arithmetic: 32 lanes of wave 0, elements 4t..4t+3 each, f64 sum of
@@ -266,7 +278,7 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
 }
 
 hipError_t gdn_decode(const GdnDecodeArgs& a, size_t B, hipStream_t s) {
-    if (a.H <= 0 || B == 0) return hipErrorInvalidValue;
+    if (a.H <= 0 || B == 0 || (a.gated && !a.norm)) return hipErrorInvalidValue;
     if (a.xh) {
         if (!a.norm || (a.H * 128) % 256) return hipErrorInvalidValue;
         hipLaunchKernelGGL(gdn_decode_kernel<true>, dim3((unsigned)a.H, (unsigned)B), dim3(1024), 0, s, a);

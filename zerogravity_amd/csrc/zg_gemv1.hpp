@@ -48,9 +48,13 @@ __device__ __forceinline__ v4i g1_mfma(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-template <int W, int PRO, int EPI>
+template <int W, int PRO, int EPI, int R>
 __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
+    static_assert(R == 16 || (R == 8 && EPI != EPI_GLU), "16-row tiles, or 8-row tiles without the GLU pairing");
     constexpr int K = 512 * W, nbk = K / 256;
+    // R = 8: lanes j < 8 carry units 4w, 4w+1 and lanes j >= 8 units 4w+2,
+    // 4w+3 of the same 8 rows (g = j / 8 picks the pair); U MFMAs per nibble
+    constexpr int U = R == 16 ? 4 : 2;
     __shared__ __align__(16) int8_t cod[W][2][512];  // per wave: high bytes, low bytes, element order
     __shared__ float gmeta[W][16][2];                // per wave group: {scale, sum}
     __shared__ float part[2][W][16];
@@ -58,7 +62,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int j = lane & 15, s = lane >> 4;
     const int nout = EPI == EPI_GLU ? (a.N >> 1) : a.N;
-    constexpr int TR = EPI == EPI_GLU ? 8 : 16;  // outputs per tile
+    constexpr int TR = EPI == EPI_GLU ? 8 : R;  // outputs per tile
     const int ntiles = (nout + TR - 1) / TR;
     const uint8_t* qs = (const uint8_t*)a.qs;
     const v4u* hdr = (const v4u*)a.hdr;
@@ -68,17 +72,24 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
             const int o = min(t * 8 + (j & 7), nout - 1);
             return j < 8 ? o : nout + o;  // up rows follow the N/2 gate rows
         }
-        return min(t * 16 + j, nout - 1);  // past the end: re-read the last row, never stored
+        return min(t * R + (R == 16 ? j : (j & 7)), nout - 1);  // past the end: re-read the last row, never stored
     };
-    v4u nib[4], hl;
-    // piece s of units 4w .. 4w+3 of the lane's row: in the 16-row tile
-    // layout (q4k_chunk_offset) a wave instruction reads 1 KB contiguously
+    // the unit (of the wave's four) whose partial sums the lane's D rows
+    // hold: s for R = 16; (s >> 1) + 2 (s & 1) for R = 8, valid on the lanes
+    // whose pair g = j >> 3 is s & 1
+    const int ue = R == 16 ? s : (s >> 1) + 2 * (s & 1);
+    const bool lane_valid = R == 16 || (s & 1) == (j >> 3);
+    v4u nib[U], hl;
+    // piece s of units 4w .. 4w+3 (R = 8: of units 4w + 2g, 4w + 2g + 1) of
+    // the lane's row: in the 16-row tile layout (q4k_chunk_offset) a wave
+    // instruction reads 1 KB contiguously (R = 8: eight 128-byte runs)
     auto load_tile = [&](int t) {
         const size_t row = (size_t)row_of(t);
-        const uint8_t* rp = qs + (((row >> 4) * (K / 128) + 4 * w) * 64 + (row & 15) + 16 * s) * 16;
+        const int u0 = 4 * w + (R == 16 ? 0 : 2 * (j >> 3));
+        const uint8_t* rp = qs + (((row >> 4) * (K / 128) + u0) * 64 + (row & 15) + 16 * s) * 16;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) nib[u] = (v4u)load_nt(rp + 1024 * u);
-        hl = hdr[q4k_hdr_index(row, 2 * w + (s >> 1), nbk)];  // the block of unit s
+        for (int u = 0; u < U; ++u) nib[u] = (v4u)load_nt(rp + 1024 * u);
+        hl = hdr[q4k_hdr_index(row, (4 * w + ue) >> 1, nbk)];  // the block of unit ue
     };
 
     // ---- activation loads (issued first: a wave's loads complete in order)
@@ -121,11 +132,19 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
         for (int q = 0; q < 2; ++q) {
             xv[q] = *(const v4f*)(a.x + e + 4 * q);
             if (PRO == PRO_RMS) ov[q] = *(const v4f*)(a.gamma + e + 4 * q);
-            if (PRO == PRO_GATED || PRO == PRO_SILU_MUL) ov[q] = *(const v4f*)(a.x2 + e + 4 * q);
+            if (PRO == PRO_GATED || PRO == PRO_SILU_MUL || PRO == PRO_GATED_PRE) ov[q] = *(const v4f*)(a.x2 + e + 4 * q);
             if (PRO == PRO_GATED) gv[q] = *(const v4f*)(a.gamma + ((e + 4 * q) & (a.group - 1)));
         }
         __builtin_amdgcn_sched_barrier(0);
         load_tile(blockIdx.x);
+    }
+    // a residual projection's outputs of the first tile, requested now (the
+    // add at the end then waits on no further load); a wave's loads
+    // complete in order, and the prologue waits only for the activation
+    float ypre = 0.0f;
+    if (EPI == EPI_RESID && w == 0 && lane < TR) {
+        const int o = min((int)blockIdx.x * TR + j, nout - 1);
+        ypre = a.y[o];
     }
 
     // ---- prologue values b (zg_decode_common.hpp's operations, without the
@@ -140,18 +159,19 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             float v = xe[t];
-            if (PRO == PRO_RMS || PRO == PRO_GATED || PRO == PRO_EMBED_RMS) {
+            if (PRO == PRO_RMS || PRO == PRO_GATED || PRO == PRO_GATED_PRE || PRO == PRO_EMBED_RMS) {
                 const float sqr = v * v;
                 sq += (double)sqr;
             }
             if (PRO == PRO_RMS || PRO == PRO_EMBED_RMS) v = v * oe[t];
             else if (PRO == PRO_GATED) v = (v * ge[t]) * ggml_silu(oe[t]);
             else if (PRO == PRO_SILU_MUL) v = oe[t] * ggml_silu(v);
+            else if (PRO == PRO_GATED_PRE) v = oe[t];  // (x * gamma) * silu(z), formed by the producer
             b[4 * q + t] = v;
         }
     }
     float fold = 1.0f;
-    if (PRO == PRO_GATED) {
+    if (PRO == PRO_GATED || PRO == PRO_GATED_PRE) {
         // per head of 128 elements: 16 lanes
         double hs = sq;
 #pragma unroll
@@ -192,26 +212,31 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
     // this wave's LDS writes complete before its own reads below
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
-    // ---- A operands: unit u = j / 4 in rows 4u..4u+3
-    v4i A[4][2];
+    // ---- A operands.  R = 16: unit u = j / 4 in rows 4u..4u+3 of MFMA u.
+    // R = 8: MFMA u carries in rows 8u..8u+3 unit u (for the columns of
+    // pair 0) and in rows 8u+4..8u+7 unit u + 2 (pair 1); the products of
+    // a row with the other pair's columns are never read.
+    v4i A[U][2];
     {
+        const int ua = R == 16 ? (j >> 2) : (j >> 3) + 2 * ((j >> 2) & 1);  // the unit of A row j
+        const int ma = R == 16 ? (j >> 2) : (j >> 3);                        // the MFMA that carries it
         const bool mine = ((j >> 1) & 1) == (s >> 1);
-        const int8_t* src = cod[w][j & 1] + 128 * (j >> 2) + 64 * (s >> 1) + 16 * (s & 1);
+        const int8_t* src = cod[w][j & 1] + 128 * ua + 64 * (s >> 1) + 16 * (s & 1);
         const v4i z = {0, 0, 0, 0};
         const v4i v0 = mine ? *(const v4i*)src : z;
         const v4i v1 = mine ? *(const v4i*)(src + 32) : z;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            A[u][0] = (j >> 2) == u ? v0 : z;
-            A[u][1] = (j >> 2) == u ? v1 : z;
+        for (int u = 0; u < U; ++u) {
+            A[u][0] = ma == u ? v0 : z;
+            A[u][1] = ma == u ? v1 : z;
         }
     }
-    // the lane's epilogue groups: G = 4 s + 2 hh + n of this wave
+    // the lane's epilogue groups: G = 4 ue + 2 hh + n of this wave
     float gsc[4], gsm[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        gsc[q] = gmeta[w][4 * s + q][0];
-        gsm[q] = gmeta[w][4 * s + q][1];
+        gsc[q] = gmeta[w][4 * ue + q][0];
+        gsm[q] = gmeta[w][4 * ue + q][1];
     }
 
     int pb = 0;
@@ -223,7 +248,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
     for (int t = blockIdx.x; t < ntiles; t += gridDim.x) {
         v4i D[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < U; ++u) {
             const v4i lo = (v4i)(nib[u] & 0x0f0f0f0fu);
             const v4i hi = (v4i)((nib[u] >> 4) & 0x0f0f0f0fu);
             D[0] = g1_mfma(A[u][0], lo, D[0]);
@@ -238,17 +263,23 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
             for (int hh = 0; hh < 2; ++hh) {
                 const int dot = 256 * D[n][2 * hh] + D[n][2 * hh + 1];
                 uint32_t sc, mn;
-                q4k_dev_scale_min(h, 4 * (s & 1) + 2 * hh + n, sc, mn);
+                q4k_dev_scale_min(h, 4 * (ue & 1) + 2 * hh + n, sc, mn);
                 const int q = 2 * hh + n;
                 acc += (d * (float)sc) * (gsc[q] * (float)dot) - (dm * (float)mn) * gsm[q];
             }
         const int next = t + gridDim.x;
         if (next < ntiles) load_tile(next);
+        if (R == 8) {
+            // row r's four units sit on lanes (r, 0), (r, 2), (r + 8, 1),
+            // (r + 8, 3): the others add zero
+            acc = lane_valid ? acc : 0.0f;
+            acc += __shfl_xor(acc, 8, 64);
+        }
         acc += __shfl_xor(acc, 16, 64);
         acc += __shfl_xor(acc, 32, 64);
-        if (lane < 16) part[pb][w][j] = acc;
+        if (lane < R) part[pb][w][j] = acc;
         lds_barrier();
-        if (w == 0 && lane < 16) {
+        if (w == 0 && lane < R) {
             if ((PRO == PRO_RMS || PRO == PRO_EMBED_RMS) && first) {
                 double tot = 0.0;
 #pragma unroll
@@ -264,9 +295,15 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
                 const int o = t * 8 + j;
                 if (j < 8 && o < nout) a.y[o] = up * ggml_silu(v);
             } else {
-                const int o = t * 16 + j;
+                const int o = t * R + j;
                 if (o < nout) {
-                    epilogue(a, 0, o, v, EPI);
+                    if (EPI == EPI_RESID && first) {
+                        const float nv = ypre + v;  // source_binary Add, lib.rs:1258-1271
+                        a.y[o] = nv;
+                        if (!finite_f32(nv)) atomicOr(a.status, 1);
+                    } else {
+                        epilogue(a, 0, o, v, EPI);
+                    }
                     if (EPI == EPI_STORE && a.amax) {
                         bad |= !finite_f32(v);
                         if (v > best || (v == best && o < bi)) {
@@ -281,7 +318,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
         pb ^= 1;
     }
     if (EPI == EPI_STORE && a.amax && w == 0) {
-        // lanes >= 16 hold (-inf, none): the first largest value of the
+        // lanes >= R hold (-inf, none): the first largest value of the
         // workgroup's outputs
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) {
@@ -300,9 +337,13 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
     }
 }
 
-// Workgroups of launch_gemv1_q4k for N outputs (EPI_STORE).
+// Rows per tile: 8 where 16-row tiles would leave more than half of the
+// 256 CUs without a workgroup (the N = 2048 projections), else 16.
+inline int gemv1_tile_rows(int nout, int epi) { return epi != EPI_GLU && nout <= 2048 ? 8 : 16; }
+
+// Workgroups of launch_gemv1_q4k for N outputs.
 inline int gemv1_grid(int nout, int epi) {
-    const int tr = epi == EPI_GLU ? 8 : 16;
+    const int tr = epi == EPI_GLU ? 8 : gemv1_tile_rows(nout, epi);
     return std::min((nout + tr - 1) / tr, 2048);
 }
 
@@ -311,9 +352,16 @@ inline int gemv1_grid(int nout, int epi) {
 template <int PRO, int EPI>
 hipError_t launch_gemv1_q4k(const FusedGemvArgs& a, hipStream_t s) {
     if (a.M != 1 || a.K % 512 || a.K > kGemv1MaxK || (EPI == EPI_GLU && a.N % 2)) return hipErrorInvalidValue;
-    if (PRO == PRO_GATED && a.group != 128) return hipErrorInvalidValue;
-    const dim3 g((unsigned)gemv1_grid(EPI == EPI_GLU ? a.N / 2 : a.N, EPI));
-#define ZG_G1(WV) hipLaunchKernelGGL((gemv1_q4k_kernel<WV, PRO, EPI>), g, dim3(64 * WV), 0, s, a)
+    if ((PRO == PRO_GATED || PRO == PRO_GATED_PRE) && a.group != 128) return hipErrorInvalidValue;
+    const int nout = EPI == EPI_GLU ? a.N / 2 : a.N;
+    const dim3 g((unsigned)gemv1_grid(nout, EPI));
+    constexpr int R8 = EPI == EPI_GLU ? 16 : 8;  // (GLU tiles stay at 16 rows)
+    const bool r8 = gemv1_tile_rows(nout, EPI) == 8;
+#define ZG_G1(WV)                                                                           \
+    if (r8)                                                                                 \
+        hipLaunchKernelGGL((gemv1_q4k_kernel<WV, PRO, EPI, R8>), g, dim3(64 * WV), 0, s, a); \
+    else                                                                                    \
+        hipLaunchKernelGGL((gemv1_q4k_kernel<WV, PRO, EPI, 16>), g, dim3(64 * WV), 0, s, a)
     switch (a.K / 512) {
     case 1: ZG_G1(1); break;
     case 2: ZG_G1(2); break;

@@ -163,13 +163,17 @@ hipError_t fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
 //                 * silu(x2)                            (gated RMSNorm)
 //   PRO_SILU_MUL  x2 * silu(x)                          (x = gate, x2 = up)
 //   PRO_PLAIN     x
+//   PRO_GATED_PRE PRO_GATED with the product (x*gamma[i % group])*silu(z)
+//                 already formed (GdnDecodeArgs::gated) in x2; x is the
+//                 norm input (its per-group sums of squares).  One row on
+//                 the matrix-core Q4_K GEMV only (gated_pre_supported).
 //   EPI_STORE     y[m][n] = W a
 //   EPI_RESID     y[m][n] += W a, nonfinite -> status bit 0
 //   EPI_GLU       stacked [gate (N/2 rows) | up (N/2 rows)]:
 //                 y[m][j] = up_j * silu(gate_j) for j < N/2 (the SwiGLU
 //                 product the down projection takes, forward.rs ffn);
 //                 batched rows write it in f16 MFMA tile order to xh_out
-enum { PRO_RMS = 0, PRO_GATED = 1, PRO_SILU_MUL = 2, PRO_PLAIN = 3, PRO_EMBED_RMS = 4 };
+enum { PRO_RMS = 0, PRO_GATED = 1, PRO_SILU_MUL = 2, PRO_PLAIN = 3, PRO_EMBED_RMS = 4, PRO_GATED_PRE = 5 };
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_GLU = 2 };
 struct FusedGemvArgs {
     const void* qs = nullptr;  // filled from the weight
@@ -252,6 +256,8 @@ int gemv1_greedy_parts(const DeviceWeight& w, int pro);
 // Whether a one-row PRO_RMS projection of w can take its activation from a
 // Q4_K embedding (FusedGemvArgs::tok/emb_*) in its prologue.
 bool gemv1_embed_supported(const DeviceWeight& w, const DeviceWeight& emb);
+// Whether a one-row projection of w can take PRO_GATED_PRE (group 128).
+bool gated_pre_supported(const DeviceWeight& w);
 hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& a, hipStream_t s);
 // Batched rows (M > 4, Q4_K; decode batches and prompts): the prologue
 // values rounded to f16 into `scratch` (batched_scratch_bytes), then an f16
@@ -293,6 +299,10 @@ struct GdnDecodeArgs {
     // needs no activation launch.  One workgroup then holds a whole head.
     void* xh = nullptr;
     const float* norm = nullptr;
+    // one-workgroup-per-quarter rows (optional, with norm): [B][W] the gated
+    // norm's product before its 1/rms, (core * norm[j % 128]) * silu(z),
+    // for the output projection's PRO_GATED_PRE prologue
+    float* gated = nullptr;
 };
 hipError_t gdn_decode(const GdnDecodeArgs& a, size_t B, hipStream_t s);
 

@@ -94,6 +94,7 @@ struct zg_session {
     uint32_t *d_tokens = nullptr, *d_greedy = nullptr;
     float *x = nullptr, *y0 = nullptr, *core = nullptr, *ao = nullptr, *logits = nullptr, *scores = nullptr,
           *pmax = nullptr, *att_stats = nullptr;
+    float* gated = nullptr;  // one-row steps: ssm_out's gated product, written by the GDN kernel
     // split-T attention partials (all-Q4_K models at 1..4 rows; null otherwise)
     float* att_part = nullptr;
     float* rope = nullptr;  // (cos, sin) of every position's 32 angles, with att_part
@@ -456,10 +457,21 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
                 d.xh = s->xh;
                 d.norm = L.ssm_norm;
             }
+            // one row: the kernel also forms (core * ssm_norm) * silu(z), and
+            // ssm_out's prologue only applies the per-head 1/rms
+            const bool pre = B == 1 && zg::gated_pre_supported(L.out_proj->dw);
+            if (pre) {
+                d.gated = s->gated;
+                d.norm = L.ssm_norm;
+            }
             ZG_HIP(zg::gdn_decode(d, B, st));
             // gated RMSNorm (ssm_norm) * silu(z) -> ssm_out -> residual
-            ZG_HIP(gemv(L.out_proj, zg::PRO_GATED, s->core, W, s->y0 + 3 * W, s->y0w, L.ssm_norm, zg::EPI_RESID, s->x,
-                        H, nullptr, tiles ? s->xh : nullptr, false, L.post_norm));
+            if (pre)
+                ZG_HIP(gemv(L.out_proj, zg::PRO_GATED_PRE, s->core, W, s->gated, W, nullptr, zg::EPI_RESID, s->x, H,
+                            nullptr, nullptr, false, L.post_norm));
+            else
+                ZG_HIP(gemv(L.out_proj, zg::PRO_GATED, s->core, W, s->y0 + 3 * W, s->y0w, L.ssm_norm, zg::EPI_RESID,
+                            s->x, H, nullptr, tiles ? s->xh : nullptr, false, L.post_norm));
         } else {
             zg::AttnDecodeArgs a;
             a.proj = s->y0;
@@ -923,6 +935,7 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     A((void**)&s->x, B * H * 4);
     A((void**)&s->y0, B * s->y0w * 4);
     A((void**)&s->core, B * W * 4);
+    A((void**)&s->gated, W * 4);
     A((void**)&s->ao, B * QD * 4);
     A((void**)&s->logits, B * V * 4);
     A((void**)&s->scores, B * g.q_heads * max_context * 4);
