@@ -562,37 +562,65 @@ def register_copies(kern, kind, N, K, rng):
     return [kern.register(4242, f"bench.{kind}.{N}.{K}.{i}", kind, K, N, w) for i in range(copies)]
 
 
-def bench_gemv_one(kern, torch, handles, kind, N, K, M, steps, warmup, rng):
+def bench_gemv_one(kern, torch, handles, kind, N, K, M, steps, warmup, rng, path="fused"):
+    """One (codec, N, K, M) point of the sweep, rotating over the weight
+    copies.  path "fused": zg_gemv_device on the f32 values of the bf16
+    activation -- the decode step's kernels, the RMSNorm in their prologue
+    (one row: the int8-MFMA GEMV; 2-4 rows: the fused GEMV; more, Q4_K: the
+    f16 activation tiles and the f16 MFMA GEMM, two launches), all timed.
+    path "prepared": the region path, the bf16 activation RMS-normalised and
+    coded once (zg_act_prepare_device, untimed), then zg_gemv_prepared_device
+    timed alone.  After a warm pass, `steps` launches are captured in one
+    HIP graph and the graph replayed between HIP events, so the figure is
+    the device's time per launch in a dependent chain, not the host's
+    submission rate."""
     from zerogravity_amd import _lib as L
     from zerogravity_amd import synth
     copies = len(handles)
     xf, xb = synth.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
     gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
     x_d = torch.from_numpy(xb.view(np.int16)).cuda()
+    x_f = torch.from_numpy(np.ascontiguousarray(xf, np.float32)).cuda()  # the same values, exactly
     g_d = torch.from_numpy(gamma).cuda()
     y = torch.empty((M, N), dtype=torch.float32, device="cuda")
     s = torch.cuda.current_stream()
     assert s.cuda_stream != 0, "launch and event stream must be a real stream"
     lib, ctx = L.lib(), kern.ctx
-    nbytes = lib.zg_act_prepared_bytes(handles[0].h, M)
-    prep = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
-    ctx.check(lib.zg_act_prepare_device(ctx.h, handles[0].h, x_d.data_ptr(), L.BF16, M, g_d.data_ptr(), 1e-6,
-                                        prep.data_ptr(), nbytes, s.cuda_stream))
+    if path == "prepared":
+        nbytes = lib.zg_act_prepared_bytes(handles[0].h, M)
+        prep = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        ctx.check(lib.zg_act_prepare_device(ctx.h, handles[0].h, x_d.data_ptr(), L.BF16, M, g_d.data_ptr(), 1e-6,
+                                            prep.data_ptr(), nbytes, s.cuda_stream))
 
-    def launch(i):
+    def launch(i, st):
         h = handles[i % copies]
-        ctx.check(lib.zg_gemv_prepared_device(ctx.h, h.h, M, prep.data_ptr(), y.data_ptr(), s.cuda_stream))
+        if path == "prepared":
+            ctx.check(lib.zg_gemv_prepared_device(ctx.h, h.h, M, prep.data_ptr(), y.data_ptr(), st))
+        else:
+            ctx.check(lib.zg_gemv_device(ctx.h, h.h, x_f.data_ptr(), L.F32, M, g_d.data_ptr(), 1e-6, y.data_ptr(),
+                                         st))
 
+    for i in range(copies):  # every copy once (a first batched call may lay out its tiles)
+        launch(i, s.cuda_stream)
     for i in range(warmup):
-        launch(i)
+        launch(i, s.cuda_stream)
     torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cs = torch.cuda.current_stream().cuda_stream
+        for i in range(steps):
+            launch(i, cs)
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = 4
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(s)
-    for i in range(steps):
-        launch(i)
+    for _ in range(reps):
+        graph.replay()
     e1.record(s)
     torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / steps
+    del graph
+    us = e0.elapsed_time(e1) * 1e3 / (steps * reps)
     return us, gemv_bytes(kind, N, K, M) / us / 1e3
 
 
@@ -629,16 +657,19 @@ def bench_gemv(args):
         for (N, K) in shapes:
             handles = register_copies(kern, kind, N, K, rng)
             for M in (1, 4, 16, 32):
-                us, gbs = bench_gemv_one(kern, torch, handles, kind, N, K, M, args.steps, args.warmup, rng)
-                name = "Q4_K" if kind == Q4_K else "Q8_0"
-                log(f"gemv {name} N={N:6d} K={K:5d} M={M:2d}: {us:9.2f} us  {gbs:8.1f} GB/s  "
-                    f"({gbs / HBM_PEAK_GBS:.1%} of HBM)")
-                results.append(dict(kind=name, N=N, K=K, M=M, us=round(us, 3), gbs=round(gbs, 1)))
+                for path in ("fused", "prepared"):
+                    us, gbs = bench_gemv_one(kern, torch, handles, kind, N, K, M, args.steps, args.warmup, rng,
+                                             path)
+                    name = "Q4_K" if kind == Q4_K else "Q8_0"
+                    log(f"gemv {name} N={N:6d} K={K:5d} M={M:2d} {path:>8}: {us:9.2f} us  {gbs:8.1f} GB/s  "
+                        f"({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+                    results.append(dict(kind=name, N=N, K=K, M=M, path=path, us=round(us, 3), gbs=round(gbs, 1)))
             del handles
             kern.release_source(4242)
-    head = next(r for r in results if r["kind"] == "Q4_K" and r["N"] == 151936 and r["M"] == 1)
+    head = next(r for r in results if r["kind"] == "Q4_K" and r["N"] == 151936 and r["M"] == 1
+                and r["path"] == "fused")
     line = {
-        "metric": "dequant-GEMV achieved HBM GB/s (Q4_K 151936x2048, M=1, RMSNorm-prepared bf16 activation)",
+        "metric": "dequant-GEMV achieved HBM GB/s (Q4_K 151936x2048, M=1, fused RMSNorm prologue)",
         "value": head["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": head["us"] / 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "q4_k x f32", "data": "synthetic (seeded random GGUF blocks)",

@@ -445,9 +445,10 @@ int zg_session_fill_random(zg_session* s, size_t rows, size_t prefix, uint64_t s
  * `stream` (hipStream_t) or the ctx stream when NULL; asynchronous.  M <= 64
  * for bf16 activations, M <= 65536 for f32.  f32 activations run the decode
  * step's own kernels: the prologue inside the GEMV (Q8_0, Q4_1, Q6_K and F32
- * bit-identical to the CPU at any M; Q4_K for M <= 4), and for Q4_K with
- * M > 4 the activation rounded to f16 and an f16 MFMA GEMM (f32 accumulate;
- * within 1e-3 relative of the CPU), LDS-staged for prompt-sized M >= 1024.
+ * bit-identical to the CPU at any M; Q4_K for one row, on the int8 matrix
+ * cores), and for Q4_K with M >= 2 the activation rounded to f16 and an f16
+ * MFMA GEMM (f32 accumulate; within 1e-3 relative of the CPU), LDS-staged
+ * for prompt-sized M >= 1024.
  * No counterpart in the reference beyond MatVecKernel::try_execute; this is
  * the resident form the whole-program provider uses. */
 int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows,

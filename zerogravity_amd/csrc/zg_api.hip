@@ -488,6 +488,11 @@ int zg_gemv_prepared_device(zg_ctx* ctx, const zg_weight* w, size_t m_rows, cons
     return ZG_COMPLETED;
 }
 
+// f32 activations of a Q4_K weight from two rows on take the f16 MFMA
+// kernels (weights read and dequantised once for all rows); measured per
+// launch they beat the byte-dot kernel from two rows on.
+static bool device_batched(const zg_weight* w, size_t m_rows) { return m_rows >= 2 && w->dw.type == zg::kQ4_K; }
+
 int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows, const float* gamma,
                    float eps, float* y, void* stream) {
     if (!ctx) return ZG_E_MALFORMED;
@@ -497,8 +502,9 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     const int pro = gamma ? zg::PRO_RMS : zg::PRO_PLAIN;
     if (x_dtype == ZG_F32 && m_rows > 0 && m_rows <= 65536 && zg::fused_gemv_supported(w->dw.type, w->dw.K, w->dw.N, pro)) {
-        // f32 activations: the decode-step kernels themselves (activation
-        // prologue in-kernel up to 4 rows, f16 MFMA beyond for Q4_K)
+        // f32 activations: the decode-step kernels themselves (one row: the
+        // int8-MFMA GEMV; Q4_K from two rows: f16 MFMA; other codecs: the
+        // activation prologue in-kernel)
         zg::FusedGemvArgs f;
         f.M = (int)m_rows;
         f.pro = pro;
@@ -510,7 +516,7 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
         f.y = y;
         f.ldy = w->dw.N;
         f.status = ctx->d_flag;
-        if (m_rows > 4 && w->dw.type == zg::kQ4_K) {
+        if (device_batched(w, m_rows)) {
             // the 32-row weight tiles, unless the 16-row kernel takes this shape
             if (!w->dw.qs_t && !zg::batched16_supported(m_rows, w->dw.K, w->dw.N, zg::EPI_STORE)) {
                 ZG_HIP(hipStreamSynchronize(s));
@@ -631,7 +637,7 @@ int zg_gemv_device_noalloc(zg_ctx* ctx, const zg_weight* w, const void* x, int x
     void* sp = ctx->static_scratch;
     const int pro = gamma ? zg::PRO_RMS : zg::PRO_PLAIN;
     const bool fused = x_dtype == ZG_F32 && zg::fused_gemv_supported(w->dw.type, w->dw.K, w->dw.N, pro);
-    const bool batched = fused && m_rows > 4 && w->dw.type == zg::kQ4_K;
+    const bool batched = fused && device_batched(w, m_rows);
     if (batched) {
         if (!w->dw.qs_t && !zg::batched16_supported(m_rows, w->dw.K, w->dw.N, zg::EPI_STORE))
             return fail(ctx, ZG_E_STATE,
