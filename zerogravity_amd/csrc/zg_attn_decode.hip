@@ -879,37 +879,43 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
 }
 
 // Grid (q_heads, B): the spans' partials of one head combined, gated.
+// Every wave forms the spans' maximum and weighted exp-sum itself (lane l
+// holds spans l, l + 64, ...), so the only barrier is the one before the
+// four waves' value sums are added.  The weights e^(m_c - M) and the gate's
+// sigmoid take the hardware exp2 (a few ulp): this form is held to the
+// reference at f32 rounding, not bit for bit.
+__device__ __forceinline__ float combine_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int nc, const float* __restrict__ part) {
     constexpr int D = 256, CB = 16;  // spans per wave per batch of loads
-    __shared__ float w[kSplitMaxChunks];
-    __shared__ float red[2][4];
     __shared__ v4f ow[4][D / 4];
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const size_t nrow = (size_t)gridDim.y * a.nq * nc, slot = ((size_t)b * a.nq + h) * nc;
     const float* ml = part + 2 * slot;
     const v4f* po = (const v4f*)(part + 2 * nrow + slot * D) + lane;
     // every span has {m, l} (an empty one -inf, 0), so no load waits on the
-    // position: span c's {m, l} in thread c (nc <= 256), and wave w's first
-    // CB spans w, w + 4, ... (lane l: channels 4l .. 4l+3) requested at once
-    const float mc = tid < nc ? ml[2 * tid] : -INFINITY, lc = tid < nc ? ml[2 * tid + 1] : 0.0f;
+    // position; wave w's first CB spans w, w + 4, ... (lane l: channels
+    // 4l .. 4l+3) are requested with them
+    float mc[4], lc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // nc <= 256
+        const int c = lane + 64 * i;
+        mc[i] = c < nc ? ml[2 * c] : -INFINITY;
+        lc[i] = c < nc ? ml[2 * c + 1] : 0.0f;
+    }
     const float gate = a.proj[(size_t)b * a.proj_stride + (size_t)h * 2 * D + D + tid];
     const int nw = (nc - wv + 3) / 4;  // this wave's spans
     v4f ov[CB];
 #pragma unroll
     for (int k = 0; k < CB; ++k)
         if (k < nw) ov[k] = po[(size_t)(wv + 4 * k) * (D / 4)];
-    float mx = wave_max_all(mc);
-    if (lane == 0) red[0][wv] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-    const float wc = mc == -INFINITY ? 0.0f : cr_expf(mc - mx);
-    w[tid] = wc;
-    const float ls = wave_sum_all(wc * lc);
-    if (lane == 0) red[1][wv] = ls;
-    __syncthreads();
-    const float L = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
-    // wave w's sum over its spans in span order; an empty span (weight 0)
-    // is skipped, its o never having been written
+    const float mx = wave_max_all(fmaxf(fmaxf(mc[0], mc[1]), fmaxf(mc[2], mc[3])));
+    float wc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wc[i] = mc[i] == -INFINITY ? 0.0f : combine_exp(mc[i] - mx);
+    const float L = wave_sum_all((wc[0] * lc[0] + wc[1] * lc[1]) + (wc[2] * lc[2] + wc[3] * lc[3]));
+    // wave w's sum over its spans in span order (span c's weight from lane
+    // c % 64); an empty span (weight 0) is skipped, its o never written
     v4f o = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int k0 = 0; k0 < nw; k0 += CB) {
         if (k0) {
@@ -920,7 +926,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int
 #pragma unroll
         for (int k = 0; k < CB; ++k) {
             if (k0 + k < nw) {
-                const float wk = w[wv + 4 * (k0 + k)];
+                const int c = wv + 4 * (k0 + k), q = c >> 6;
+                const float src = q == 0 ? wc[0] : q == 1 ? wc[1] : q == 2 ? wc[2] : wc[3];
+                const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(src), c & 63));
                 if (wk != 0.0f) {
                     o.x = fmaf(wk, ov[k].x, o.x);
                     o.y = fmaf(wk, ov[k].y, o.y);
@@ -934,7 +942,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int
     __syncthreads();
     const float* of = (const float*)ow;  // [wave][channel]
     const float ot = (of[tid] + of[D + tid]) + (of[2 * D + tid] + of[3 * D + tid]);
-    const float v = (ot / L) * source_sigmoid(gate);
+    const float v = (ot / L) * (1.0f / (1.0f + combine_exp(-gate)));
     a.out[(size_t)b * a.out_stride + (size_t)h * D + tid] = v;
     if (tid == 0 && !(L >= 1.0f && L < INFINITY)) atomicOr(a.status, 8);
     if (a.xh) {  // batched rows: also the output projection's f16 A tiles

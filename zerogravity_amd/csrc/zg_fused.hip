@@ -69,6 +69,10 @@ hipError_t fused_gemv(const DeviceWeight& w, const FusedGemvArgs& args, hipStrea
     a.hdr = w.hdr;
     a.K = (int)w.K;
     a.N = (int)w.N;
+    // formed GDN gates: only the one-row matrix-core GEMV's store epilogue does it
+    if (a.gate_dt && (a.epi != EPI_STORE || !gemv1_fits(a, w.type) || !a.gate_a || a.gate_heads <= 0 ||
+                      a.gate_row < 0 || a.gate_row + 2 * a.gate_heads > a.N))
+        return hipErrorInvalidValue;
     switch (a.pro) {
     case PRO_RMS: return launch_pro<PRO_RMS>(a, w.type, s);
     case PRO_GATED: return launch_pro<PRO_GATED>(a, w.type, s);

@@ -120,8 +120,8 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
         }
     }
     // the head's gates (f64-evaluated transcendentals) once per workgroup,
-    // by the wave without value channels
-    if (tid == 192 && (!HEAD || quarter == 0)) {
+    // by the wave without value channels, unless the projection formed them
+    if (!a.gates_formed && tid == 192 && (!HEAD || quarter == 0)) {
         float gn, bt, sp, gr;
         gdn_coef(g_a, g_b, g_dt, g_sa, gn, bt, sp, gr);
         gates[0] = gn;
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
 
     const float dsq = 1.0f / sqrtf((float)D);
     const float eps_d = a.eps / (float)D;
-    const float gain = gates[0], beta = gates[1];
+    const float gain = a.gates_formed ? g_a : gates[0], beta = a.gates_formed ? g_b : gates[1];
     const float vj = vv[HEAD ? j : jl];
     float cv[4][4];
     float o;

@@ -64,6 +64,11 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
     const int nout = EPI == EPI_GLU ? (a.N >> 1) : a.N;
     constexpr int TR = EPI == EPI_GLU ? 8 : R;  // outputs per tile
     const int ntiles = (nout + TR - 1) / TR;
+    // the GDN input projection's gate tiles go to the first workgroups, whose
+    // weights arrive first, so the gates' f64 transcendentals end before the
+    // last workgroups do (gate_dt); otherwise tiles in order
+    const int tshift = (EPI == EPI_STORE && a.gate_dt) ? a.gate_row / TR : 0;
+    auto tile_of = [&](int k) { return tshift ? (k + tshift) % ntiles : k; };
     const uint8_t* qs = (const uint8_t*)a.qs;
     const v4u* hdr = (const v4u*)a.hdr;
 
@@ -100,7 +105,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
         // depend on the token), then this lane's 8 elements (one 8-byte
         // half-chunk piece and the block header) and gamma
         const uint32_t t = *a.tok;
-        load_tile(blockIdx.x);
+        load_tile(tile_of(blockIdx.x));
         const bool ok = t < (uint32_t)a.emb_rows;
         const size_t row = ok ? t : 0;
         const uint8_t* eq = (const uint8_t*)a.emb_qs + q4k_chunk_offset(row, e >> 6, K) + ((e & 31) >= 16 ? 256 : 0) +
@@ -136,7 +141,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
             if (PRO == PRO_GATED) gv[q] = *(const v4f*)(a.gamma + ((e + 4 * q) & (a.group - 1)));
         }
         __builtin_amdgcn_sched_barrier(0);
-        load_tile(blockIdx.x);
+        load_tile(tile_of(blockIdx.x));
     }
     // a residual projection's outputs of the first tile, requested now (the
     // add at the end then waits on no further load); a wave's loads
@@ -245,7 +250,8 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
     float best = -INFINITY;  // greedy partial (wave 0, lanes < 16)
     int bi = 0x7fffffff;
     bool bad = false;
-    for (int t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    for (int k = blockIdx.x; k < ntiles; k += gridDim.x) {
+        const int t = tile_of(k);
         v4i D[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -267,8 +273,8 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
                 const int q = 2 * hh + n;
                 acc += (d * (float)sc) * (gsc[q] * (float)dot) - (dm * (float)mn) * gsm[q];
             }
-        const int next = t + gridDim.x;
-        if (next < ntiles) load_tile(next);
+        const int next = k + gridDim.x;
+        if (next < ntiles) load_tile(tile_of(next));
         if (R == 8) {
             // row r's four units sit on lanes (r, 0), (r, 2), (r + 8, 1),
             // (r + 8, 3): the others add zero
@@ -296,6 +302,12 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
                 if (j < 8 && o < nout) a.y[o] = up * ggml_silu(v);
             } else {
                 const int o = t * R + j;
+                if (EPI == EPI_STORE && a.gate_dt && o >= a.gate_row && o < a.gate_row + 2 * a.gate_heads) {
+                    // the GDN gates from this output (alpha or the beta projection)
+                    const int g = o - a.gate_row;
+                    v = g < a.gate_heads ? gdn_gain(v, a.gate_dt[g], a.gate_a[g])
+                                         : source_sigmoid(v);
+                }
                 if (o < nout) {
                     if (EPI == EPI_RESID && first) {
                         const float nv = ypre + v;  // source_binary Add, lib.rs:1258-1271

@@ -238,6 +238,15 @@ struct FusedGemvArgs {
     const void* emb_hdr = nullptr;
     int emb_rows = 0;
     float* x_out = nullptr;
+    // one activation row, EPI_STORE, matrix-core GEMV, the GDN input
+    // projection: outputs gate_row + h (h < gate_heads, alpha) are stored as
+    // the gain gdn_gain(alpha, gate_dt[h], gate_a[h]) and outputs gate_row +
+    // gate_heads + h (beta) as source_sigmoid(beta), the GDN gates formed by
+    // the same functions the GDN kernel would apply (GdnDecodeArgs::
+    // gates_formed); the workgroups holding those rows run first
+    const float* gate_dt = nullptr;
+    const float* gate_a = nullptr;
+    int gate_row = 0, gate_heads = 0;
 };
 // EPI_GLU offered for these shapes (fused path: K <= 2048 so a row group
 // holds a gate and an up row; batched path: N/2 a multiple of 32).
@@ -303,6 +312,10 @@ struct GdnDecodeArgs {
     // norm's product before its 1/rms, (core * norm[j % 128]) * silu(z),
     // for the output projection's PRO_GATED_PRE prologue
     float* gated = nullptr;
+    // the projection already holds the gain at proj[4W + h] and beta at
+    // proj[4W + H + h] (FusedGemvArgs::gate_dt) instead of alpha and the
+    // beta projection
+    int gates_formed = 0;
 };
 hipError_t gdn_decode(const GdnDecodeArgs& a, size_t B, hipStream_t s);
 

@@ -50,6 +50,15 @@ __device__ __forceinline__ float source_softplus(float x) {
     return cr_logf(1.0f + cr_expf(x));
 }
 
+// The GDN gain alone, lib.rs:339-362: exp(softplus(alpha + dt) * a), the
+// same operations as gdn_coef's gain.
+__device__ __forceinline__ float gdn_gain(float alpha, float dt, float a) {
+    const float biased = alpha + dt;
+    const float sp = source_softplus(biased);
+    const float gate_raw = sp * a;
+    return cr_expf(gate_raw);
+}
+
 // GDN gates, lib.rs:339-362: sp = softplus(alpha + dt), gate_raw = sp * a,
 // gain = exp(gate_raw), beta = sigmoid(beta projection).
 __device__ __forceinline__ void gdn_coef(float alpha, float beta_p, float dt, float a, float& gain, float& beta,

@@ -350,11 +350,24 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
                                            ? nullptr : &m->layers[0].in_proj[0].w->dw;
     const uint32_t* embed_tok =
         B == 1 && first_in && zg::gemv1_embed_supported(*first_in, m->embd->dw) ? tokens : nullptr;
+    // one row: the GDN input projection forms the layer's gates in its
+    // epilogue (FusedGemvArgs::gate_dt) for the next projection launched
+    struct {
+        const float *dt = nullptr, *a = nullptr;
+        int row = 0, heads = 0;
+    } gate_req;
     auto gemv = [&](zg_weight* w, int pro, const float* x, size_t ldx, const float* x2, size_t ldx2,
                     const float* gamma, int epi, float* y, size_t ldy, void* xh_out = nullptr,
                     const void* xh_in = nullptr, bool greedy_parts = false, const float* gamma_next = nullptr) {
         zg::FusedGemvArgs f;
         f.M = (int)B;
+        if (gate_req.dt) {
+            f.gate_dt = gate_req.dt;
+            f.gate_a = gate_req.a;
+            f.gate_row = gate_req.row;
+            f.gate_heads = gate_req.heads;
+            gate_req.dt = nullptr;
+        }
         if (greedy_parts) {
             f.amax = s->pmax;
             f.aidx = s->pidx;
@@ -429,8 +442,18 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
     for (size_t i = 0; i < m->layers.size(); ++i) {
         LayerW& L = m->layers[i];
         const int slot = s->layer_slot[i];
-        for (const Part& p : L.in_proj)
+        // one row through the matrix-core GEMV: the GDN gates come formed
+        const bool gates = !L.full && B == 1 && L.in_proj.size() == 1 && L.in_proj[0].col == 0 &&
+                           zg::gemv1_greedy_parts(L.in_proj[0].w->dw, zg::PRO_RMS) > 0;
+        for (const Part& p : L.in_proj) {
+            if (gates) {
+                gate_req.dt = L.ssm_dt;
+                gate_req.a = L.ssm_a;
+                gate_req.row = (int)(4 * W);
+                gate_req.heads = (int)g.gdn_heads;
+            }
             ZG_HIP(gemv(p.w, zg::PRO_RMS, s->x, H, nullptr, 0, L.attn_norm, zg::EPI_STORE, s->y0 + p.col, s->y0w));
+        }
         if (!L.full) {
             zg::GdnDecodeArgs d;
             d.proj = s->y0;
@@ -449,6 +472,7 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             d.state_half = rec_floats(g);
             d.core = s->core;
             d.H = (int)g.gdn_heads;
+            d.gates_formed = gates ? 1 : 0;
             // batched rows: the kernel also writes ssm_out's gated-norm f16
             // activation tiles (one workgroup per head), so the batched GEMM
             // runs without an activation launch
