@@ -1101,7 +1101,21 @@ __global__ __launch_bounds__(256) void argmax_parts_kernel(const float* __restri
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     float best = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = tid; i < parts; i += 256) argmax_merge(best, bi, pmax[i], pidx[i]);
+    // the first 8 x 256 partials requested at once (one round trip for the
+    // one-row LM head's 2048), then merged: the merge keeps the largest
+    // value and on a tie the smaller index, so its order does not matter
+    constexpr int PER = 8;
+    float pv[PER];
+    int pi[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        const int i = tid + 256 * q;
+        pv[q] = i < parts ? pmax[min(i, parts - 1)] : -INFINITY;
+        pi[q] = i < parts ? pidx[min(i, parts - 1)] : 0x7fffffff;
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) argmax_merge(best, bi, pv[q], pi[q]);
+    for (int i = tid + 256 * PER; i < parts; i += 256) argmax_merge(best, bi, pmax[i], pidx[i]);
     for (int off = 32; off > 0; off >>= 1) argmax_merge(best, bi, __shfl_xor(best, off, 64), __shfl_xor(bi, off, 64));
     if (lane == 0) {
         sv[wv] = best;
