@@ -97,8 +97,7 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
         hl = hdr[q4k_hdr_index(row, (4 * w + ue) >> 1, nbk)];  // the block of unit ue
     };
 
-    // ---- activation loads (issued first: a wave's loads complete in order,
-    // so the prologue waits only for its own)
+    // ---- activation loads (issued first: a wave's loads complete in order)
     const int e = 512 * w + 8 * lane;
     v4f xv[2], ov[2], gv[2];
     if (PRO == PRO_EMBED_RMS) {
@@ -141,10 +140,8 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
             if (PRO == PRO_GATED || PRO == PRO_SILU_MUL || PRO == PRO_GATED_PRE) ov[q] = *(const v4f*)(a.x2 + e + 4 * q);
             if (PRO == PRO_GATED) gv[q] = *(const v4f*)(a.gamma + ((e + 4 * q) & (a.group - 1)));
         }
-        // the other prologues request the weights now; the RMS ones after
-        // their coding (below)
         __builtin_amdgcn_sched_barrier(0);
-        if (PRO != PRO_RMS) load_tile(tile_of(blockIdx.x));
+        load_tile(tile_of(blockIdx.x));
     }
     // a residual projection's outputs of the first tile, requested now (the
     // add at the end then waits on no further load); a wave's loads
@@ -216,16 +213,6 @@ __global__ __launch_bounds__(64 * W) void gemv1_q4k_kernel(FusedGemvArgs a) {
     if ((lane & 3) == 0) {
         gmeta[w][lane >> 2][0] = (amax / 32639.0f) * fold;
         gmeta[w][lane >> 2][1] = gsum * fold;
-    }
-    // The RMS projections (the step's widest launches) request their
-    // weights only now: requested before the coding, a wave's weight loads
-    // stall its issue while the memory system drains every workgroup's
-    // requests, and the coding -- whose operands arrived long before --
-    // waits behind them (measured: 4.5 us per one-row step)
-    if (PRO == PRO_RMS) {
-        __builtin_amdgcn_sched_barrier(0);
-        load_tile(tile_of(blockIdx.x));
-        __builtin_amdgcn_sched_barrier(0);
     }
     // this wave's LDS writes complete before its own reads below
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
