@@ -640,6 +640,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
     __shared__ v4f scp[kSplitMaxSpan];  // scores, then GGML exp(s - m): [token][head]
     __shared__ float red[2][G][4];
     __shared__ float vrow[D];
+    __shared__ float rob[4 * G * D];  // the waves' value sums of a short span
     const int c = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, s = tid & 7;
     const int t0 = c * span;
@@ -794,6 +795,68 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
         }
     }
     lds_barrier();
+
+    if (n <= 64) {
+        // ---- a span of at most 64 tokens: every wave forms the statistics
+        // itself, lane i holding token i (the values below: there wave 0
+        // holds every token and the other waves add zeros), and keeps p in
+        // its lanes, read back per token with readlane, so no barrier
+        // separates the scores from the value sums
+        const v4f s4 = scp[lane];
+        const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+        const bool live = lane < n;
+        float m[G], l[G], pe[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            m[g] = wave_max_all(live ? sv[g] : -INFINITY);
+            pe[g] = live ? ggml_exp(sv[g] - m[g]) : 0.0f;
+            l[g] = wave_sum_all(pe[g]);  // >= 1, so adding the other waves' +0 sums changes no bit
+        }
+        const int ws = __builtin_amdgcn_readfirstlane(wv);
+        float o[G][4];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[g][e] = 0.0f;
+        for (int i = 0; i < nb; ++i) {
+            float cv[8][4];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                vn[u].unpack(cv[u]);
+                if (t0 + 32 * i + 8 * ws + u == p) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) cv[u][e] = vrow[4 * lane + e];
+                }
+            }
+            if (i + 1 < nb) load_values(i + 1);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int tt = 32 * i + 8 * ws + u;
+                if (tt < n) {
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        const float pg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe[g]), tt));
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) o[g][e] = fmaf(pg, cv[u][e], o[g][e]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+            *(v4f*)(rob + (wv * G + g) * D + 4 * lane) = v4f{o[g][0], o[g][1], o[g][2], o[g][3]};
+        lds_barrier();
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float og = (rob[g * D + tid] + rob[(G + g) * D + tid]) + (rob[(2 * G + g) * D + tid] + rob[(3 * G + g) * D + tid]);
+            if (tid == 0) {
+                ml[2 * (slot + (size_t)g * nc)] = m[g];
+                ml[2 * (slot + (size_t)g * nc) + 1] = l[g];
+            }
+            po[(slot + (size_t)g * nc) * D + tid] = og;
+        }
+        return;
+    }
 
     // ---- span statistics per head: m, p = GGML exp(s - m), l
     float m[G], l[G];
