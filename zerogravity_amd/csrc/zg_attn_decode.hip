@@ -595,7 +595,9 @@ hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
 // attn_combine_kernel then forms sum_c e^(m_c - M) o_c / sum_c e^(m_c - M)
 // l_c over the row's spans (the empty ones weigh 0), M = max_c m_c, wave w
 // summing spans w, w + 4, ... and the four waves' sums added in a fixed
-// order, and applies the sigmoid gate (forward.rs:751).  The reference (lib.rs:1276-1387)
+// order (attn_combine_quarter_kernel: a quarter of the channels per
+// workgroup, for few rows with many spans), and applies the sigmoid gate
+// (forward.rs:751).  The reference (lib.rs:1276-1387)
 // normalises with the global max first and runs the value sums as
 // token-ordered chains: this regrouping agrees with it to f32 rounding (the
 // per-op 1e-3 bar), not bit for bit.
@@ -1016,6 +1018,68 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int
     }
 }
 
+// Grid (q_heads, 4, B), for up to 4 rows with more than 48 spans each (the
+// batched rows' f16 tiles are not written here): workgroup
+// (h, d, b) takes the 64 channels [64 d, 64 d + 64) of head h, so each
+// workgroup reads a quarter of the head's partials.  Lane l of wave w holds
+// channels 64 d + 4 (l & 15) .. + 3 and sums the spans r, r + 16, r + 32,
+// ... in span order, r = 4 w + (l >> 4); the four lane groups of a wave are
+// added as (g0 + g1) + (g2 + g3) and the four waves' sums in wave order.
+// The statistics, weights and gate are those of attn_combine_kernel.
+__global__ __launch_bounds__(256) void attn_combine_quarter_kernel(AttnDecodeArgs a, int nc, const float* __restrict__ part) {
+    constexpr int D = 256, CB = 16;  // nc <= 256: at most 16 spans per lane
+    __shared__ float ow[4][64];
+    const int h = blockIdx.x, dq = blockIdx.y, b = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int r = 4 * wv + (lane >> 4);
+    const size_t nrow = (size_t)gridDim.z * a.nq * nc, slot = ((size_t)b * a.nq + h) * nc;
+    const float* ml = part + 2 * slot;
+    const v4f* po = (const v4f*)(part + 2 * nrow + slot * D + 64 * dq) + (lane & 15);
+    float mc[4], lc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = lane + 64 * i;
+        mc[i] = c < nc ? ml[2 * c] : -INFINITY;
+        lc[i] = c < nc ? ml[2 * c + 1] : 0.0f;
+    }
+    const float gate = tid < 64 ? a.proj[(size_t)b * a.proj_stride + (size_t)h * 2 * D + D + 64 * dq + tid] : 0.0f;
+    const int nw = (nc - r + 15) >> 4;  // this lane's spans (r < 16 <= nc)
+    v4f ov[CB];
+#pragma unroll
+    for (int k = 0; k < CB; ++k)
+        if (k < nw) ov[k] = po[(size_t)(r + 16 * k) * (D / 4)];
+    const float mx = wave_max_all(fmaxf(fmaxf(mc[0], mc[1]), fmaxf(mc[2], mc[3])));
+    float wc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wc[i] = mc[i] == -INFINITY ? 0.0f : combine_exp(mc[i] - mx);
+    const float L = wave_sum_all((wc[0] * lc[0] + wc[1] * lc[1]) + (wc[2] * lc[2] + wc[3] * lc[3]));
+    v4f o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < CB; ++k) {
+        // span c = r + 16 k sits in lane c & 63 of wc[k >> 2] (r < 16)
+        const int c = r + 16 * k;
+        const float wk = __shfl(wc[k >> 2], c & 63, kWave);
+        if (k < nw && wk != 0.0f) {
+            o.x = fmaf(wk, ov[k].x, o.x);
+            o.y = fmaf(wk, ov[k].y, o.y);
+            o.z = fmaf(wk, ov[k].z, o.z);
+            o.w = fmaf(wk, ov[k].w, o.w);
+        }
+    }
+    float e[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        e[i] += __shfl_xor(e[i], 16, kWave);
+        e[i] += __shfl_xor(e[i], 32, kWave);
+    }
+    if (lane < 16) *(v4f*)&ow[wv][4 * lane] = v4f{e[0], e[1], e[2], e[3]};
+    __syncthreads();
+    if (tid >= 64) return;
+    const float ot = (ow[0][tid] + ow[1][tid]) + (ow[2][tid] + ow[3][tid]);
+    const float v = (ot / L) * (1.0f / (1.0f + combine_exp(-gate)));
+    a.out[(size_t)b * a.out_stride + (size_t)h * D + 64 * dq + tid] = v;
+    if (tid == 0 && !(L >= 1.0f && L < INFINITY)) atomicOr(a.status, 8);
+}
+
 // RoPE angles of positions [0, n): entry 32 p + t is (cos, sin) of p times
 // theta_scale^t, the angle formed by repeated f32 products as the decode
 // kernels form it, with the same correctly rounded cos and sin.
@@ -1053,7 +1117,12 @@ hipError_t attn_decode_split(const AttnDecodeArgs& a, size_t B, float* part, hip
         ZG_SP(float)
     }
 #undef ZG_SP
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.nq, (unsigned)B), dim3(256), 0, s, a, nc, (const float*)part);
+    if (B <= 4 && nc > 48 && !a.xh)  // a quarter of the head's channels per workgroup: a quarter of its partials to read
+        hipLaunchKernelGGL(attn_combine_quarter_kernel, dim3((unsigned)a.nq, 4, (unsigned)B), dim3(256), 0, s, a, nc,
+                           (const float*)part);
+    else
+        hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)a.nq, (unsigned)B), dim3(256), 0, s, a, nc,
+                           (const float*)part);
     return hipGetLastError();
 }
 
