@@ -1196,16 +1196,41 @@ __device__ __forceinline__ void commit_row(const StepCommit& c, bool ok, int b) 
     if (c.cur) c.cur[b] ^= 1;
 }
 
+// The same rule with the status word, position and half read when the
+// kernel starts (no kernel of the step writes them while the greedy
+// kernels run), so those reads overlap the partials' instead of following
+// the reduction.
+struct CommitRead {
+    int status = 0, pos = 0, cur = 0;
+};
+__device__ __forceinline__ CommitRead commit_read(const StepCommit& c, const int* status, int b) {
+    CommitRead r;
+    if (c.pos) {
+        r.status = *status;
+        r.pos = c.pos[b];
+        if (c.cur) r.cur = c.cur[b];
+    }
+    return r;
+}
+__device__ __forceinline__ void commit_row(const StepCommit& c, const CommitRead& r, int b) {
+    if (!c.pos || r.status != 0) return;
+    const int np = r.pos + 1;
+    c.pos[b] = np;
+    c.ntok[b] = np + 1;
+    if (c.cur) c.cur[b] = r.cur ^ 1;
+}
+
 __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ pmax, const int* __restrict__ pidx,
                                                           uint32_t* __restrict__ greedy, const int* __restrict__ status,
                                                           StepCommit c) {
     const int b = blockIdx.x, lane = threadIdx.x;
     float m = lane < kArgBlocks ? pmax[b * kArgBlocks + lane] : -INFINITY;
     int mi = lane < kArgBlocks ? pidx[b * kArgBlocks + lane] : 0x7fffffff;
+    const CommitRead cr = commit_read(c, status, b);
     for (int off = 32; off > 0; off >>= 1) argmax_merge(m, mi, __shfl_xor(m, off, 64), __shfl_xor(mi, off, 64));
     if (lane == 0) {
         greedy[b] = mi == 0x7fffffff ? 0u : (uint32_t)mi;
-        if (c.pos) commit_row(c, *status == 0, b);
+        commit_row(c, cr, b);
     }
 }
 
@@ -1245,6 +1270,7 @@ __global__ __launch_bounds__(256) void argmax_parts_kernel(const float* __restri
         pv[q] = i < parts ? pmax[min(i, parts - 1)] : -INFINITY;
         pi[q] = i < parts ? pidx[min(i, parts - 1)] : 0x7fffffff;
     }
+    const CommitRead cr = commit_read(c, status, 0);
 #pragma unroll
     for (int q = 0; q < PER; ++q) argmax_merge(best, bi, pv[q], pi[q]);
     for (int i = tid + 256 * PER; i < parts; i += 256) argmax_merge(best, bi, pmax[i], pidx[i]);
@@ -1257,7 +1283,7 @@ __global__ __launch_bounds__(256) void argmax_parts_kernel(const float* __restri
     if (tid == 0) {
         for (int w = 1; w < 4; ++w) argmax_merge(best, bi, sv[w], si[w]);
         greedy[0] = bi == 0x7fffffff ? 0u : (uint32_t)bi;
-        if (c.pos) commit_row(c, *status == 0, 0);
+        commit_row(c, cr, 0);
     }
 }
 
