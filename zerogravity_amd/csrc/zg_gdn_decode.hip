@@ -33,6 +33,14 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
     const int s = lane & 7;
     const float* xin = a.proj + (size_t)b * a.proj_stride;
     float* ring = a.ring + (size_t)b * 3 * W * 4;
+    // one workgroup per quarter: every argument the prologue uses in one
+    // round trip (loaded where first used, they would take several), the
+    // conv and gate inputs requested, then the row's state half and
+    // position in the next round trip (a scalar wait covers every scalar
+    // load in flight)
+    if constexpr (!HEAD)
+        asm volatile("" ::"s"(a.norm), "s"(a.gated), "s"(a.state), "s"(a.cur), "s"(a.pos), "s"(a.dt), "s"(a.ssm_a),
+                     "s"(a.state_row), "s"(a.state_half), "s"(a.conv_w), "s"(a.H));
     // The conv and gate inputs are requested first, then this thread's 16
     // state values (the bulk of the traffic): a wave's loads complete in
     // issue order, so the conv, norms and gates wait only for their own
@@ -76,9 +84,13 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
         gg = a.norm[j];
     }
     // the row's state: read from half cur[b], written to the other half (the
-    // draft the step's commit publishes), or in place without cur
+    // draft the step's commit publishes), or in place without cur; one
+    // workgroup per quarter reads cur and pos through the scalar unit
+    // (nothing writes them while the step's kernels run)
+    typedef const __attribute__((address_space(4))) int* const_int;
+    const int cb = !a.cur ? 0 : HEAD ? a.cur[b] : ((const_int)a.cur)[b];
+    const int pq = HEAD ? 0 : ((const_int)a.pos)[b];
     const size_t row_floats = a.state_row ? a.state_row : (size_t)a.H * D * D;
-    const int cb = a.cur ? a.cur[b] : 0;
     const size_t within = ((size_t)h * D + j) * D + 4 * s;
     const float* col = a.state + (size_t)b * row_floats + (size_t)cb * a.state_half + within;
     float* col_out = a.state + (size_t)b * row_floats + (a.cur ? (size_t)(1 - cb) * a.state_half : 0) + within;
@@ -89,7 +101,7 @@ __global__ __launch_bounds__(HEAD ? 1024 : 256) void gdn_decode_kernel(GdnDecode
     v4f sv[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) sv[c] = __builtin_nontemporal_load((const v4f*)(col + 32 * c));
-    const int p = a.pos[b];
+    const int p = HEAD ? a.pos[b] : pq;
     const int s0 = (p + 1) & 3, s1 = (p + 2) & 3, s2 = (p + 3) & 3, sw = p & 3;
     auto conv = [&](const ConvIn& c) {
         const float hv[4] = {c.r.x, c.r.y, c.r.z, c.r.w};
