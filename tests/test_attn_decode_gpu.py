@@ -140,6 +140,7 @@ SPLIT_REL = 1e-3
 @pytest.mark.parametrize("kv,max_ctx,positions", [
     (L.BF16, 2048, [0]),
     (L.BF16, 2048, [2047]),
+    (L.BF16, 2048, [2047, 700]),  # two rows over 64 spans each: the quarter-channel combine
     (L.F32, 2048, [31, 32, 63, 64]),
     (L.BF16, 4096, [2047, 2048, 5, 4095]),
     (L.BF16, 8192, [8191, 4100, 1023]),
