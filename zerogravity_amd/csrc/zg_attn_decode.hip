@@ -591,7 +591,8 @@ hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
 // key as attn_decode_qk_kernel does (the workgroup whose span holds the
 // position appends K/V and uses its own rounded copies for that token),
 // scores its tokens in the 32-accumulator order, and keeps per head the
-// span's max m, l = sum of GGML exp(s - m) and o = sum of exp(s - m) * v.
+// span's max m, l = sum of exp(s - m) and o = sum of exp(s - m) * v (exp
+// through the hardware exp2, combine_exp).
 // attn_combine_kernel then forms sum_c e^(m_c - M) o_c / sum_c e^(m_c - M)
 // l_c over the row's spans (the empty ones weigh 0), M = max_c m_c, wave w
 // summing spans w, w + 4, ... and the four waves' sums added in a fixed
@@ -602,6 +603,9 @@ hipError_t attn_decode(const AttnDecodeArgs& a, size_t B, hipStream_t s) {
 // token-ordered chains: this regrouping agrees with it to f32 rounding (the
 // per-op 1e-3 bar), not bit for bit.
 constexpr int kSplitMaxSpan = 1024;  // tokens per workgroup (LDS scores)
+// e^x through the hardware exp2 (a few ulp): the split form's weights, held
+// to the reference at f32 rounding rather than bit for bit
+__device__ __forceinline__ float combine_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 constexpr int kSplitMaxChunks = 256;
 
 // Tokens per span, a multiple of 32: about 256 workgroups over the batch at
@@ -639,7 +643,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
     constexpr int D = 256;
     __shared__ float hv[G + 1][D];
     __shared__ float rsin[32], rcos[32];
-    __shared__ v4f scp[kSplitMaxSpan];  // scores, then GGML exp(s - m): [token][head]
+    __shared__ v4f scp[kSplitMaxSpan];  // scores, then exp(s - m): [token][head]
     __shared__ float red[2][G][4];
     __shared__ float vrow[D];
     __shared__ float rob[4 * G * D];  // the waves' value sums of a short span
@@ -811,7 +815,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             m[g] = wave_max_all(live ? sv[g] : -INFINITY);
-            pe[g] = live ? ggml_exp(sv[g] - m[g]) : 0.0f;
+            pe[g] = live ? combine_exp(sv[g] - m[g]) : 0.0f;
             l[g] = wave_sum_all(pe[g]);  // >= 1, so adding the other waves' +0 sums changes no bit
         }
         const int ws = __builtin_amdgcn_readfirstlane(wv);
@@ -860,7 +864,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
         return;
     }
 
-    // ---- span statistics per head: m, p = GGML exp(s - m), l
+    // ---- span statistics per head: m, p = exp(s - m), l
     float m[G], l[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -880,7 +884,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
         float e[4] = {e4.x, e4.y, e4.z, e4.w};
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            e[g] = ggml_exp(e[g] - m[g]);
+            e[g] = combine_exp(e[g] - m[g]);
             sum[g] += e[g];
         }
         scp[i] = v4f{e[0], e[1], e[2], e[3]};
@@ -947,9 +951,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnDecodeArgs a, int n
 // Every wave forms the spans' maximum and weighted exp-sum itself (lane l
 // holds spans l, l + 64, ...), so the only barrier is the one before the
 // four waves' value sums are added.  The weights e^(m_c - M) and the gate's
-// sigmoid take the hardware exp2 (a few ulp): this form is held to the
-// reference at f32 rounding, not bit for bit.
-__device__ __forceinline__ float combine_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+// sigmoid take combine_exp too.
 
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnDecodeArgs a, int nc, const float* __restrict__ part) {
     constexpr int D = 256, CB = 16;  // spans per wave per batch of loads
