@@ -459,9 +459,10 @@ enum { ZG_PRO_RMS = 0, ZG_PRO_GATED = 1, ZG_PRO_SILU_MUL = 2, ZG_PRO_PLAIN = 3, 
 enum { ZG_EPI_STORE = 0, ZG_EPI_RESID = 1, ZG_EPI_GLU = 2 };
 
 /* One projection of the resident decode step with the operations around it
- * fused, on the kernels the step itself launches, for 1..4 f32 activation
- * rows x[m][0:K] (device memory, row stride ldx; the caller's stream,
- * asynchronous):
+ * fused, for 1..4 f32 activation rows x[m][0:K] (device memory, row stride
+ * ldx; the caller's stream, asynchronous), on the kernels the step itself
+ * launches for one row and for rows of the codecs other than Q4_K (a
+ * step's 2-4 Q4_K rows take its batched f16 kernels instead):
  *   prologue ZG_PRO_RMS       RMSNorm(x, gamma, eps) (model-qwen35/src/lib.rs:263-284)
  *            ZG_PRO_GATED     grouped RMSNorm(x, gamma[group], eps) * silu(x2) (forward.rs:586-594)
  *            ZG_PRO_SILU_MUL  x2 * silu(x) (forward.rs:498)

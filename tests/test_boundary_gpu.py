@@ -216,8 +216,9 @@ def test_snapshot_restore_and_fork(kern, tiny):
     fork.restore(snap, 1)
     assert fork.positions() == [0, 5]
     lg, _ = fork.step([int(toks[0]), int(toks[5])])
-    # two rows take the fused dot4 GEMV, one row the matrix-core GEMV: the
-    # two int16 activation codings agree to ~1e-3
+    # two rows take the batched f16 MFMA kernels, one row the int8
+    # matrix-core GEMV: the f16 and int16 activation codings agree to a few
+    # 1e-3
     assert float(np.max(np.abs(lg[1] - first[0]))) <= 5e-3
     # a snapshot of another model, or of another KV type, is foreign
     m2 = qwen35.QwenModelHip(TINY, tiny, kernel=kern)

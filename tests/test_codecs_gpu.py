@@ -165,9 +165,11 @@ def test_mixed_integer_codec_batched_rows_bit_exact(kern):
     m.close()
 
 
-def test_mixed_q4k_model_greedy_matches_oracle(kern):
-    """Q4_K projections beside the integer codecs, at B = 1 and B = 6 (the
-    Q4_K runs of each stack on the batched MFMA path).  Q4_K is held to
+@pytest.mark.parametrize("B", [3, 6])
+def test_mixed_q4k_model_greedy_matches_oracle(kern, B):
+    """Q4_K projections beside the integer codecs, at B = 1 and B = 3 or 6
+    (from two rows the Q4_K runs of each stack take the batched MFMA path,
+    the integer codecs the fused kernels at up to 4 rows).  Q4_K is held to
     1e-3 per op, and its small differences move some downstream Q8_1/Q8_K
     activation codes across a rounding boundary, so the logits are not held
     to bits here; the greedy tokens must agree.  The reference's pinned
@@ -175,13 +177,13 @@ def test_mixed_q4k_model_greedy_matches_oracle(kern):
     g = dict(TINY, hidden=512, ffn=512)
     t = qwen35.synthetic_tensors(g, gguf.Q4_K, seed=32, kinds=qwen35.MIXED)
     m = qwen35.QwenModelHip(g, t, kernel=kern)
-    B, steps = 6, 5
+    steps = 5
     s = m.session(max_batch=B, max_context=64, kv_dtype=L.BF16)
     one = m.session(max_batch=1, max_context=64, kv_dtype=L.BF16)
     toks = np.random.default_rng(5).integers(0, g["vocab"], (steps, B)).astype(np.uint32)
     got = [s.step(toks[i])[0] for i in range(steps)]
     worst = 0.0
-    for b in (0, 5):
+    for b in (0, B - 1):
         o = O.Model(g, t).session(kv_bf16=True)
         for i in range(steps):
             ref = o.forward(int(toks[i, b]))
@@ -189,7 +191,7 @@ def test_mixed_q4k_model_greedy_matches_oracle(kern):
             worst = max(worst, float(np.max(np.abs(got[i][b] - ref))))
             if b == 0:
                 assert int(np.argmax(one.forward(int(toks[i, 0])))) == int(np.argmax(ref)), i
-    print(f"mixed-codec Q4_K model: greedy identical, worst logit max-abs {worst:.3e}")
+    print(f"mixed-codec Q4_K model B={B}: greedy identical, worst logit max-abs {worst:.3e}")
     with pytest.raises(L.ZgError) as e:
         one.prefill_batched(np.zeros(4, np.uint32))
     assert e.value.code == L.E_UNSUPPORTED

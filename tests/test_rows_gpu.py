@@ -9,11 +9,13 @@ depend only on its own tokens.  Every row is therefore checked against the
 oracle's own session for its request (the north star's 2e-2 end-to-end bar,
 same greedy token; the oracle calls glibc's transcendentals as the
 reference's f32 functions do) and against its own one-row device session
-run on the same tokens.  One row takes the int8 matrix-core GEMV and 2..4
-rows the fused dot4 kernel, each with its own int16 activation coding, so
-the device pair agrees to the coding noise (ROW_TOL), far below what a leak
-between rows would show; prefill logits of the same prompt run the same
-kernels and agree bit for bit.
+run on the same tokens.  One row takes the int8 matrix-core GEMV (int16
+activation codes) and two or more rows of Q4_K weights the batched f16
+MFMA kernels (the activation rounded to f16), so the device pair agrees to
+the two codings' noise: up to ~6e-3 on these logits, within ROW_TOL (half
+the end-to-end bar), far below the O(1) difference a leak between rows
+would show; prefill logits of the same prompt run the same kernels and
+agree bit for bit.
 """
 import numpy as np
 import pytest
@@ -24,7 +26,7 @@ from zerogravity_amd import gguf, qwen35
 from zerogravity_amd import regions as R
 
 pytestmark = pytest.mark.gpu
-ROW_TOL = 5e-3
+ROW_TOL = 1e-2
 LOGIT_TOL = 2e-2
 
 TINY = dict(hidden=512, layers=4, ffn=512, vocab=1000, gdn_heads=2, gdn_dim=128, q_heads=2, kv_heads=1,

@@ -1,5 +1,7 @@
 #pragma once
-// Kernels of the fused decode GEMV (one launch per projection at B <= 4)
+// Kernels of the fused decode GEMV (one launch per projection at B <= 4,
+// except one Q4_K row, which takes the int8 GEMV, and a session step's 2-4
+// Q4_K rows, which take the batched f16 kernels)
 // and their launch templates; zg_fused_<prologue>.hip instantiate one
 // prologue each so that the instantiations compile in parallel.
 #include "zg_decode_common.hpp"

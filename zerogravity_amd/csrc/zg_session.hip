@@ -95,14 +95,14 @@ struct zg_session {
     float *x = nullptr, *y0 = nullptr, *core = nullptr, *ao = nullptr, *logits = nullptr, *scores = nullptr,
           *pmax = nullptr, *att_stats = nullptr;
     float* gated = nullptr;  // one-row steps: ssm_out's gated product, written by the GDN kernel
-    // split-T attention partials (all-Q4_K models at 1..4 rows; null otherwise)
+    // split-T attention partials (all-Q4_K models, 1..64 rows; null otherwise)
     float* att_part = nullptr;
     float* rope = nullptr;  // (cos, sin) of every position's 32 angles, with att_part
-    void* xh = nullptr;  // f16 activations of the batched (B > 4) projections
-    float* parts = nullptr;  // split-K partial tiles of residual projections (B > 4)
-    void* xh3 = nullptr;     // the stream's RMS input tiles a residual projection leaves (B > 4)
+    void* xh = nullptr;  // f16 activations of the batched (B > 1) projections
+    float* parts = nullptr;  // split-K partial tiles of residual projections (B > 1)
+    void* xh3 = nullptr;     // the stream's RMS input tiles a residual projection leaves (B > 1)
     double* rss = nullptr;   // and their per-tile sums of squares [rows][hidden/16 or hidden/32]
-    void* xh2 = nullptr;     // the SwiGLU product in f16 tiles, down projection input (B > 4)
+    void* xh2 = nullptr;     // the SwiGLU product in f16 tiles, down projection input (B > 1)
     size_t y0w = 0;
     std::vector<float*> ring, rec;  // per GDN layer: conv ring [B][3W][4], state [B][2][H][128][128]
     std::vector<void*> kc, vc;      // per attention layer: [B][max_ctx][kv_heads*256]
@@ -394,11 +394,12 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
         f.status = s->d_status;
         f.xh_out = xh_out;
         f.xh_in = xh_in;
-        // one launch with the prologue in-kernel up to 4 rows; beyond, the
-        // activation in f16 and the MFMA GEMM (weights read once)
-        if (pending && !(B > 4 && w->dw.type == zg::kQ4_K && pro == zg::PRO_RMS && x == s->x))
+        // one row: one launch with the prologue in-kernel (the int8 matrix-core
+        // GEMV); more rows of Q4_K weights: the activation in f16 and the MFMA
+        // GEMM (weights read once); other codecs: the fused 1-4 row kernels
+        if (pending && !(B > 1 && w->dw.type == zg::kQ4_K && pro == zg::PRO_RMS && x == s->x))
             return hipErrorInvalidValue;  // a pending split-K residual must be consumed by the next RMS projection
-        if (B > 4 && w->dw.type == zg::kQ4_K) {
+        if (B > 1 && w->dw.type == zg::kQ4_K) {
             if (pending && pro == zg::PRO_RMS && x == s->x) {
                 f.rparts = s->parts;
                 f.rsplits = pending;
@@ -476,7 +477,7 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             // batched rows: the kernel also writes ssm_out's gated-norm f16
             // activation tiles (one workgroup per head), so the batched GEMM
             // runs without an activation launch
-            const bool tiles = B > 4 && L.out_proj->dw.type == zg::kQ4_K;
+            const bool tiles = B > 1 && L.out_proj->dw.type == zg::kQ4_K;
             if (tiles) {
                 d.xh = s->xh;
                 d.norm = L.ssm_norm;
@@ -521,7 +522,7 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             a.nkv = (int)g.kv_heads;
             a.max_ctx = (int)s->max_ctx;
             // batched rows: the value kernel also writes o_proj's f16 tiles
-            const bool tiles = B > 4 && L.out_proj->dw.type == zg::kQ4_K;
+            const bool tiles = B > 1 && L.out_proj->dw.type == zg::kQ4_K;
             if (tiles) a.xh = s->xh;
             if (s->att_part && zg::attn_split_supported(B, a.nq, a.nkv, s->max_ctx)) {
                 a.rope = s->rope;
@@ -537,14 +538,14 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
                                                           : (logits || greedy ? m->out_norm : nullptr);
         const zg::DeviceWeight& gu = L.ffn_gu[0].w->dw;
         const bool glu = L.ffn_gu.size() == 1 && L.ffn_down->dw.type == zg::kQ4_K &&
-                         (B > 4 ? zg::batched_glu_supported(gu.type, gu.K, gu.N) : zg::fused_glu_supported(gu.type, gu.K, gu.N));
+                         (B > 1 ? zg::batched_glu_supported(gu.type, gu.K, gu.N) : zg::fused_glu_supported(gu.type, gu.K, gu.N));
         if (glu) {
             // SwiGLU in the gate/up epilogue: the down projection takes the
             // product as a plain activation (f16 tiles when batched)
             ZG_HIP(gemv(L.ffn_gu[0].w, zg::PRO_RMS, s->x, H, nullptr, 0, L.post_norm, zg::EPI_GLU, s->y0, s->y0w,
-                        B > 4 ? s->xh2 : nullptr));
+                        B > 1 ? s->xh2 : nullptr));
             ZG_HIP(gemv(L.ffn_down, zg::PRO_PLAIN, s->y0, s->y0w, nullptr, 0, nullptr, zg::EPI_RESID, s->x, H, nullptr,
-                        B > 4 ? s->xh2 : nullptr, false, next_norm));
+                        B > 1 ? s->xh2 : nullptr, false, next_norm));
         } else {
             for (const Part& p : L.ffn_gu)
                 ZG_HIP(gemv(p.w, zg::PRO_RMS, s->x, H, nullptr, 0, L.post_norm, zg::EPI_STORE, s->y0 + p.col, s->y0w));
@@ -900,7 +901,7 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     if (max_batch == 0 || max_batch > 64 || max_context == 0 || max_context > g.max_context)
         return fail(ctx, ZG_E_LIMIT, "session batch must be 1..64 and context within the model's");
     if (kv_dtype != ZG_BF16 && kv_dtype != ZG_F32) return fail(ctx, ZG_E_MALFORMED, "KV cache dtype must be BF16 or F32");
-    if (max_batch > 4) {
+    if (max_batch > 1) {
         // the batched rows' 32-row kernel reads Q4_K weights in its MFMA
         // tile order; the 16-row kernel (K a multiple of 1024 up to 6144)
         // reads the weight's own layout, and zg_prefill_batched builds the
@@ -951,10 +952,10 @@ int zg_session_create(zg_model* m, size_t max_batch, size_t max_context, int kv_
     A((void**)&s->pmax, nparts * 4);
     A((void**)&s->att_stats, B * g.q_heads * 2 * 4);
     A(&s->xh, zg::batched_scratch_bytes(B, std::max({H, F, W, QD})));
-    if (B > 4) A((void**)&s->parts, 8 * ((B + 31) / 32 * 32) * H * sizeof(float));
-    if (B > 4) A(&s->xh3, zg::batched_scratch_bytes(B, H));
-    if (B > 4) A((void**)&s->rss, (B + 31) / 32 * 32 * ((H + 15) / 16) * sizeof(double));
-    if (B > 4) A(&s->xh2, zg::batched_scratch_bytes(B, F));
+    if (B > 1) A((void**)&s->parts, 8 * ((B + 31) / 32 * 32) * H * sizeof(float));
+    if (B > 1) A(&s->xh3, zg::batched_scratch_bytes(B, H));
+    if (B > 1) A((void**)&s->rss, (B + 31) / 32 * 32 * ((H + 15) / 16) * sizeof(double));
+    if (B > 1) A(&s->xh2, zg::batched_scratch_bytes(B, F));
     A((void**)&s->pidx, nparts * 4);
     A((void**)&s->x, B * H * 4);
     A((void**)&s->y0, B * s->y0w * 4);
