@@ -2,8 +2,9 @@
 results as zg_gemv_device, bit for bit, on two calls in a row (the second
 with a smaller input, so the static scratch holds the first call's larger
 contents), for every codec path: bf16 input through the prepared
-activation, f32 input through the in-kernel prologue (up to 4 rows) and
-through the f16 MFMA kernels (Q4_K beyond 4 rows).  No counterpart in the
+activation, f32 input through the in-kernel prologue (up to 4 rows),
+through the f16 MFMA kernels (Q4_K beyond 4 rows) and through the
+coded-once activation of the Q8_0 rows kernel (beyond 4 rows).  No counterpart in the
 reference: the entry exists for callers that cannot allocate."""
 import ctypes
 

@@ -490,8 +490,12 @@ int zg_gemv_prepared_device(zg_ctx* ctx, const zg_weight* w, size_t m_rows, cons
 
 // f32 activations of a Q4_K weight from two rows on take the f16 MFMA
 // kernels (weights read and dequantised once for all rows); measured per
-// launch they beat the byte-dot kernel from two rows on.
-static bool device_batched(const zg_weight* w, size_t m_rows) { return m_rows >= 2 && w->dw.type == zg::kQ4_K; }
+// launch they beat the byte-dot kernel from two rows on.  Q8_0 beyond four
+// rows takes the coded-once activation and one weight stream per 16 rows.
+static bool device_batched(const zg_weight* w, size_t m_rows, int pro) {
+    return (m_rows >= 2 && w->dw.type == zg::kQ4_K) ||
+           (m_rows > 4 && w->dw.type == zg::kQ8_0 && zg::q8_rows_supported(w->dw.K, w->dw.N, pro));
+}
 
 int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows, const float* gamma,
                    float eps, float* y, void* stream) {
@@ -503,8 +507,9 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
     const int pro = gamma ? zg::PRO_RMS : zg::PRO_PLAIN;
     if (x_dtype == ZG_F32 && m_rows > 0 && m_rows <= 65536 && zg::fused_gemv_supported(w->dw.type, w->dw.K, w->dw.N, pro)) {
         // f32 activations: the decode-step kernels themselves (one row: the
-        // int8-MFMA GEMV; Q4_K from two rows: f16 MFMA; other codecs: the
-        // activation prologue in-kernel)
+        // int8-MFMA GEMV; Q4_K from two rows: f16 MFMA; Q8_0 beyond four
+        // rows: the coded-once activation; otherwise the activation prologue
+        // in-kernel)
         zg::FusedGemvArgs f;
         f.M = (int)m_rows;
         f.pro = pro;
@@ -516,9 +521,10 @@ int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, 
         f.y = y;
         f.ldy = w->dw.N;
         f.status = ctx->d_flag;
-        if (device_batched(w, m_rows)) {
-            // the 32-row weight tiles, unless the 16-row kernel takes this shape
-            if (!w->dw.qs_t && !zg::batched16_supported(m_rows, w->dw.K, w->dw.N, zg::EPI_STORE)) {
+        if (device_batched(w, m_rows, pro)) {
+            // Q4_K: the 32-row weight tiles, unless the 16-row kernel takes this shape
+            if (w->dw.type == zg::kQ4_K && !w->dw.qs_t &&
+                !zg::batched16_supported(m_rows, w->dw.K, w->dw.N, zg::EPI_STORE)) {
                 ZG_HIP(hipStreamSynchronize(s));
                 ZG_HIP(zg::ensure_mfma_tiles(const_cast<zg_weight*>(w)->dw, s));
             }
@@ -637,9 +643,9 @@ int zg_gemv_device_noalloc(zg_ctx* ctx, const zg_weight* w, const void* x, int x
     void* sp = ctx->static_scratch;
     const int pro = gamma ? zg::PRO_RMS : zg::PRO_PLAIN;
     const bool fused = x_dtype == ZG_F32 && zg::fused_gemv_supported(w->dw.type, w->dw.K, w->dw.N, pro);
-    const bool batched = fused && device_batched(w, m_rows);
+    const bool batched = fused && device_batched(w, m_rows, pro);
     if (batched) {
-        if (!w->dw.qs_t && !zg::batched16_supported(m_rows, w->dw.K, w->dw.N, zg::EPI_STORE))
+        if (w->dw.type == zg::kQ4_K && !w->dw.qs_t && !zg::batched16_supported(m_rows, w->dw.K, w->dw.N, zg::EPI_STORE))
             return fail(ctx, ZG_E_STATE,
                         "weight has no batched tile layout yet: a zg_gemv_device call with more than 4 rows builds it");
         if (zg::batched_scratch_bytes(m_rows, w->dw.K) > kStaticScratchBytes)

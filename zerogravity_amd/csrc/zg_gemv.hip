@@ -626,6 +626,8 @@ hipError_t gemv(const DeviceWeight& w, size_t M, const void* prepared, float* y,
     const float* ad = (const float*)(base + a(M * w.K));
     const int16_t* x4 = (const int16_t*)base;
     const float* m4 = (const float*)(base + a(M * w.K * 2));
+    if (w.type == kQ8_0 && M > 4 && q8_rows_supported(w.K, w.N, PRO_PLAIN))
+        return q8_rows_prepared(w, M, prepared, y, s);  // weights streamed once per 16 rows
     if (w.type == kQ8_0) {
         int mt = M == 1 ? 1 : (M == 2 ? 2 : (M <= 4 ? 4 : 8));
         while (mt > 1 && (size_t)mt * (K + (K / 32) * 4) > 65536) mt >>= 1;

@@ -276,6 +276,15 @@ size_t batched_scratch_bytes(size_t M, size_t K);
 // graph capture.  batched_gemv refuses a Q4_K weight without them.
 hipError_t ensure_mfma_tiles(DeviceWeight& w, hipStream_t s);
 hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& a, void* scratch, hipStream_t s);
+// Q8_0 beyond 4 rows (zg_q8rows.hip): every activation row coded once into
+// `scratch` in act_prepare_for's layout (prepared_bytes(kQ8_0, M, K), within
+// batched_scratch_bytes), then the weights streamed once per 16 rows;
+// bit-identical to the fused kernels.  Prologues RMS, GATED, SILU_MUL,
+// PLAIN; epilogues STORE and RESID.  batched_gemv routes Q8_0 here.
+bool q8_rows_supported(size_t K, size_t N, int pro);
+hipError_t q8_rows_gemv(const DeviceWeight& w, const FusedGemvArgs& a, void* scratch, hipStream_t s);
+// The same GEMV on an activation act_prepare_for already prepared.
+hipError_t q8_rows_prepared(const DeviceWeight& w, size_t M, const void* prepared, float* y, hipStream_t s);
 // The prompt-sized GEMM on f16 A tiles `xh` (act16_kernel's layout, or the
 // previous gate/up GEMM's SwiGLU tiles): EPI_STORE / EPI_RESID into y, or
 // EPI_GLU into xh_out (a product past the f16 range sets status bit 4).

@@ -1,0 +1,300 @@
+// Q8_0 projections of more than 4 activation rows: the weights streamed
+// once for up to 16 rows per workgroup.
+//
+// Arithmetic (cpu/src/source/quantization.rs:171-196, as gemv_q8_0_kernel
+// and fused_q8_kernel restate it): per (activation row m, output row n)
+// eight f32 accumulators; accumulator l takes, block after block, the int32
+// dot of block elements 4l..4l+3 with the activation codes, fused-multiply-
+// added with scale = f16(w.d) * act.d, and the value is the tree
+// ((l0+l4)+(l2+l6))+((l1+l5)+(l3+l7)).  Lane (r8, l) of a wave is
+// accumulator l of weight row 8 g + r8 for each of its R row groups g and
+// each of the MT activation rows, so the per-(m, n) chain and the final
+// tree are the reference's: bit-identical to the one-to-four-row kernels.
+//
+// Two launches.  q8_act_rows_kernel codes every activation row once (one
+// workgroup per row, the fused kernels' own prologue function, so the codes
+// and scales are theirs) into the prepared layout of act_prepare_for: int8
+// codes [M][K], then per block the f16-rounded scale [M][K/32] at the next
+// 256-byte boundary.  q8_rows_kernel stages MT rows of it into LDS (word l
+// of block b at (m * 8 + l) * nbs + b, nbs = nbp + 4 so that the 8 words of
+// a block fall in different banks: one 16-byte read gives a lane four
+// blocks of its word) and streams its row groups' weight tiles through two
+// register buffers, the next QC chunks requested before the current ones
+// are multiplied.  Every activation word read from LDS serves R weight rows
+// and every weight word MT activation rows: the fused kernels read all the
+// weights again for each group of four rows.
+#include <type_traits>
+
+#include "zg_decode_common.hpp"
+
+namespace zg {
+
+namespace {
+
+constexpr int kQ8RowsQC = 2;  // 4-block chunks per register buffer
+
+template <int PRO, int J>
+__global__ __launch_bounds__(256) void q8_act_rows_kernel(FusedGemvArgs a, int8_t* __restrict__ aq,
+                                                          float* __restrict__ ad) {
+    extern __shared__ int lds_q8a[];
+    const int K = a.K, nb = K >> 5, nbp = (nb + 3) & ~3;
+    int* codes = lds_q8a;                         // [8][nbp] words, the prologue's layout
+    float* scales = (float*)(lds_q8a + 8 * nbp);  // [nbp]
+    const int m = blockIdx.x;
+    wg_prologue<PRO, kCodecQ8, J>(a, m, true, nullptr, codes, scales);  // ends with a barrier
+    int* out = (int*)(aq + (size_t)m * K);
+    for (int wd = threadIdx.x; wd < (K >> 2); wd += blockDim.x) out[wd] = codes[(wd & 7) * nbp + (wd >> 3)];
+    for (int b = threadIdx.x; b < nb; b += blockDim.x) ad[(size_t)m * nb + b] = scales[b];
+}
+
+template <int MT, int R, int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void q8_rows_kernel(
+    FusedGemvArgs a, const int8_t* __restrict__ aq, const float* __restrict__ ad) {
+    constexpr int QC = kQ8RowsQC;
+    extern __shared__ int lds_q8r[];
+    const int K = a.K, N = a.N, M = a.M;
+    const int nb = K >> 5, nbc = (nb + 3) >> 2, nbp = nbc * 4, nbs = nbp + 4, kw = K >> 2;
+    int* codes = lds_q8r;                               // [MT][8][nbs] words
+    float* scales = (float*)(lds_q8r + MT * 8 * nbs);   // [MT][nbp]
+    const int m0 = blockIdx.y * MT;
+    const int lane = threadIdx.x & 63, r8 = lane >> 3, l = lane & 7;
+    const int groups = (N + 7) >> 3, tasks = (groups + R - 1) / R;
+    const int nwaves = gridDim.x * 4;
+    const v4i* qs = (const v4i*)a.qs;
+    const uint16_t* hdr = (const uint16_t*)a.hdr;
+
+    struct Chunk {
+        v4i w[QC][R];
+        uint2 h[QC][R];
+    };
+    // row groups past the end re-read the last group, blocks past the end
+    // the last chunk: loaded, never consumed
+    auto load = [&](int T, int c0, Chunk& ck) {
+#pragma unroll
+        for (int q = 0; q < QC; ++q) {
+            const int c = min(c0 + q, nbc - 1);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int g = min(T * R + r, groups - 1);
+                const int row = min(g * 8 + r8, N - 1);
+                ck.w[q][r] = load_nt(qs + ((size_t)g * nbc + c) * 64 + lane);
+                ck.h[q][r] = *(const uint2*)(hdr + (size_t)row * nbp + 4 * c);
+            }
+        }
+    };
+    const int T0 = blockIdx.x * 4 + (threadIdx.x >> 6);
+    Chunk ca, cb;
+    if (T0 < tasks) load(T0, 0, ca);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- stage the MT activation rows (zero past M) into LDS
+    const int nq = MT * (kw >> 2);  // 16-byte pieces: words 4p .. 4p+3 of a row (one block half)
+    for (int p = threadIdx.x; p < nq; p += blockDim.x) {
+        const int m = p / (kw >> 2), wd = 4 * (p - m * (kw >> 2));
+        v4i v = {0, 0, 0, 0};
+        if (m0 + m < M) v = *(const v4i*)(aq + (size_t)(m0 + m) * K + 4 * wd);
+        const int b = wd >> 3, l0 = wd & 7;
+        int* dst = codes + (m * 8 + l0) * nbs + b;
+        dst[0] = v.x;
+        dst[nbs] = v.y;
+        dst[2 * nbs] = v.z;
+        dst[3 * nbs] = v.w;
+    }
+    for (int i = threadIdx.x; i < MT * nbp; i += blockDim.x) {
+        const int m = i / nbp, b = i - m * nbp;
+        scales[i] = (m0 + m < M && b < nb) ? ad[(size_t)(m0 + m) * nb + b] : 0.0f;
+    }
+    __syncthreads();
+
+    float acc[R][MT];
+    auto consume = [&](const Chunk& ck, int c0) {
+#pragma unroll
+        for (int q = 0; q < QC; ++q) {
+            const int c = c0 + q;
+            if (c >= nbc) break;  // uniform
+            float wd[R][4];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                wd[r][0] = f16_to_f32((uint16_t)(ck.h[q][r].x & 0xffffu));
+                wd[r][1] = f16_to_f32((uint16_t)(ck.h[q][r].x >> 16));
+                wd[r][2] = f16_to_f32((uint16_t)(ck.h[q][r].y & 0xffffu));
+                wd[r][3] = f16_to_f32((uint16_t)(ck.h[q][r].y >> 16));
+            }
+            // a whole chunk runs unguarded; only a last chunk past nb checks
+            // each block (uniform)
+            const int nbi = min(4, nb - 4 * c);
+            auto blocks = [&](auto full) {
+                // row m + 1's codes and scales are requested before row m's
+                // products, so the LDS latency hides behind them
+                v4i cwn = *(const v4i*)(codes + l * nbs + 4 * c);
+                v4f swn = *(const v4f*)(scales + 4 * c);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const v4i cw = cwn;
+                    const v4f sw = swn;
+                    if (m + 1 < MT) {
+                        cwn = *(const v4i*)(codes + ((m + 1) * 8 + l) * nbs + 4 * c);
+                        swn = *(const v4f*)(scales + (m + 1) * nbp + 4 * c);
+                    }
+                    const int xc[4] = {cw.x, cw.y, cw.z, cw.w};
+                    const float xs[4] = {sw.x, sw.y, sw.z, sw.w};
+#pragma unroll
+                    for (int bi = 0; bi < 4; ++bi) {
+                        if (decltype(full)::value || bi < nbi) {
+#pragma unroll
+                            for (int r = 0; r < R; ++r) {
+                                const int ww = bi == 0 ? ck.w[q][r].x
+                                             : bi == 1 ? ck.w[q][r].y
+                                             : bi == 2 ? ck.w[q][r].z
+                                                       : ck.w[q][r].w;
+                                const int pair = __builtin_amdgcn_sdot4(ww, xc[bi], 0, false);
+                                const float scale = wd[r][bi] * xs[bi];
+                                acc[r][m] = fmaf((float)pair, scale, acc[r][m]);
+                            }
+                        }
+                    }
+                }
+            };
+            if (nbi == 4) blocks(std::true_type{});
+            else blocks(std::false_type{});
+        }
+    };
+
+    for (int T = T0; T < tasks; T += nwaves) {
+        if (T != T0) load(T, 0, ca);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+        for (int c0 = 0; c0 < nbc; c0 += 2 * QC) {
+            if (c0 + QC < nbc) load(T, c0 + QC, cb);
+            consume(ca, c0);
+            if (c0 + QC >= nbc) break;
+            if (c0 + 2 * QC < nbc) load(T, c0 + 2 * QC, ca);
+            consume(cb, c0 + QC);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int g = T * R + r, row = g * 8 + r8;
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const float v = group8_tree_last(acc[r][m]);  // the reference's lane tree, in lane 7
+                if (l == 7 && g < groups && row < N && m0 + m < M) epilogue(a, m0 + m, row, v, EPI);
+            }
+        }
+    }
+}
+
+size_t rows_lds(int mt, int K) {
+    const int nbp = ((K >> 5) + 3) & ~3;
+    return (size_t)mt * (8 * (nbp + 4) + nbp) * 4;  // 8 code words (padded rows) and a scale per block
+}
+
+template <int EPI>
+hipError_t launch_rows(const FusedGemvArgs& a, const int8_t* aq, const float* ad, hipStream_t s) {
+    const int M = a.M, K = a.K;
+    const size_t groups = ((size_t)a.N + 7) / 8;
+    // R rows groups per wave while the waves stay plentiful: an activation
+    // word read from LDS then serves R weight rows
+    int R = groups >= 4 * 4096 ? 4 : (groups >= 2 * 2048 ? 2 : 1);
+    // MT activation rows per workgroup: as many as M needs up to 16, within
+    // 64 KB of LDS (two workgroups per CU), and fewer when the row groups
+    // alone would leave CUs idle (more workgroups along M, each re-reading
+    // the weights from cache)
+    int mt = 16;
+    auto wgs_of = [&](int r) { return (unsigned)std::min<size_t>(((groups + r - 1) / r + 3) / 4, 1024); };
+    while (mt > 4 && mt / 2 >= M) mt >>= 1;
+    while (mt > 4 && rows_lds(mt, K) > 65536) mt >>= 1;
+    while (mt > 4 && (size_t)wgs_of(mt == 16 ? std::min(R, 2) : R) * ((M + mt - 1) / mt) < 256) mt >>= 1;
+    if (mt == 16) R = std::min(R, 2);
+    const unsigned wgs = wgs_of(R);
+    if (rows_lds(mt, K) > 65536) return hipErrorInvalidValue;
+    const unsigned gy = (unsigned)((M + mt - 1) / mt);
+    if (gy > 65535) return hipErrorInvalidValue;
+    const dim3 g(wgs, gy);
+    const size_t lds = rows_lds(mt, K);
+#define ZG_Q8R(MT_, R_) hipLaunchKernelGGL((q8_rows_kernel<MT_, R_, EPI>), g, dim3(256), lds, s, a, aq, ad)
+#define ZG_Q8R_R(MT_)              \
+    if (R == 4) ZG_Q8R(MT_, 4);    \
+    else if (R == 2) ZG_Q8R(MT_, 2); \
+    else ZG_Q8R(MT_, 1);
+    if (mt == 16) {
+        // four row groups of 16 rows would spill: two
+        if (R >= 2) ZG_Q8R(16, 2);
+        else ZG_Q8R(16, 1);
+    } else if (mt == 8) {
+        ZG_Q8R_R(8)
+    } else {
+        ZG_Q8R_R(4)
+    }
+#undef ZG_Q8R_R
+#undef ZG_Q8R
+    return hipGetLastError();
+}
+
+template <int PRO>
+hipError_t launch_act_rows(const FusedGemvArgs& a, int8_t* aq, float* ad, hipStream_t s) {
+    const int K = a.K, nbp = ((K >> 5) + 3) & ~3;
+    const size_t lds = (size_t)nbp * 36;
+    const dim3 g((unsigned)a.M);
+#define ZG_Q8A(J) hipLaunchKernelGGL((q8_act_rows_kernel<PRO, J>), g, dim3(256), lds, s, a, aq, ad)
+    if (K <= 1024) ZG_Q8A(1);
+    else if (K <= 2048) ZG_Q8A(2);
+    else if (K <= 4096) ZG_Q8A(4);
+    else ZG_Q8A(8);
+#undef ZG_Q8A
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool q8_rows_supported(size_t K, size_t N, int pro) {
+    return pro != PRO_GATED_PRE && fused_gemv_supported(kQ8_0, K, N, pro) && rows_lds(4, (int)K) <= 65536;
+}
+
+hipError_t q8_rows_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* scratch, hipStream_t s) {
+    if (w.type != kQ8_0 || !q8_rows_supported(w.K, w.N, args.pro) || args.M <= 0 || !scratch ||
+        (args.epi != EPI_STORE && args.epi != EPI_RESID) || args.xh_in || args.xh_out || args.rparts ||
+        (args.parts && args.splits > 1) || args.rms_tiles_out || args.rms_ss_in || args.amax || args.emb_qs ||
+        args.gate_dt)
+        return hipErrorInvalidValue;
+    if (args.pro == PRO_GATED && (args.group <= 0 || args.group > 1024 || (args.group & (args.group - 1)) ||
+                                  w.K % (size_t)args.group))
+        return hipErrorInvalidValue;
+    FusedGemvArgs a = args;
+    a.qs = w.qs;
+    a.hdr = w.hdr;
+    a.K = (int)w.K;
+    a.N = (int)w.N;
+    int8_t* aq = (int8_t*)scratch;
+    float* ad = (float*)((char*)scratch + (((size_t)a.M * w.K + 255) & ~(size_t)255));
+    hipError_t e;
+    switch (a.pro) {
+    case PRO_RMS: e = launch_act_rows<PRO_RMS>(a, aq, ad, s); break;
+    case PRO_GATED: e = launch_act_rows<PRO_GATED>(a, aq, ad, s); break;
+    case PRO_SILU_MUL: e = launch_act_rows<PRO_SILU_MUL>(a, aq, ad, s); break;
+    case PRO_PLAIN: e = launch_act_rows<PRO_PLAIN>(a, aq, ad, s); break;
+    default: return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return e;
+    return a.epi == EPI_RESID ? launch_rows<EPI_RESID>(a, aq, ad, s) : launch_rows<EPI_STORE>(a, aq, ad, s);
+}
+
+hipError_t q8_rows_prepared(const DeviceWeight& w, size_t M, const void* prepared, float* y, hipStream_t s) {
+    if (w.type != kQ8_0 || !q8_rows_supported(w.K, w.N, PRO_PLAIN) || M == 0 || M > (size_t)65535 * 4)
+        return hipErrorInvalidValue;
+    FusedGemvArgs a;
+    a.qs = w.qs;
+    a.hdr = w.hdr;
+    a.K = (int)w.K;
+    a.N = (int)w.N;
+    a.M = (int)M;
+    a.epi = EPI_STORE;
+    a.y = y;
+    a.ldy = w.N;
+    const int8_t* aq = (const int8_t*)prepared;
+    const float* ad = (const float*)((const char*)prepared + ((M * w.K + 255) & ~(size_t)255));
+    return launch_rows<EPI_STORE>(a, aq, ad, s);
+}
+
+}  // namespace zg
