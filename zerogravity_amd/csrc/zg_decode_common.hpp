@@ -52,8 +52,9 @@ constexpr int kRecWords = 36;  // Q4_K record: 32 dwords of code bytes + {xs_lo,
 // XOR shuffles.  The values are coded straight into LDS:
 //   Q8_0 (cpu/src/source/quantization.rs:37-61): per 32-block amax,
 //     d = amax/127, code = clamp(rint(v*127/amax)), d rounded to f16;
-//     codes [8][nbp] words (word l of block b at l * nbp + b, nbp = K/32
-//     rounded up to 4), scales [K/32].
+//     codes [8][nbp + 4] words (word l of block b at l * (nbp + 4) + b,
+//     nbp = K/32 rounded up to 4; the 4 words of padding put the 8 words of
+//     a block in different LDS banks), scales [K/32].
 //   Q8_1 (quantization.rs:37-61, Q4_1 pairing): as Q8_0 (codes [8][nb8],
 //     nb8 = K/32 rounded up to 8), plus per block s = f16(sum of codes *
 //     unrounded d) in `extra`.
@@ -236,10 +237,10 @@ __device__ void wg_prologue_code(const FusedGemvArgs& a, bool valid, const ProIn
                     r = fminf(fmaxf(r, -128.0f), 127.0f);
                     word |= ((uint32_t)(int)r & 0xffu) << (8 * t);
                 }
-                // lane-major: word l * nbp + block (nbp = blocks rounded to
-                // 4), so that one 16-byte read serves four blocks
+                // lane-major: word l * (nbp + 4) + block (nbp = blocks
+                // rounded to 4), so that one 16-byte read serves four blocks
                 const int nbp = ((K >> 5) + 3) & ~3;
-                codes[(size_t)l * nbp + (k >> 5)] = (int)word;
+                codes[(size_t)l * (nbp + 4) + (k >> 5)] = (int)word;
                 if (l == 0) scales[k >> 5] = f16_roundtrip(d);
             }
         }

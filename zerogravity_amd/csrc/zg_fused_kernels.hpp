@@ -207,9 +207,9 @@ __global__ __launch_bounds__(256) void fused_q8_kernel(FusedGemvArgs a) {
     constexpr int QC = 8;
     extern __shared__ int lds_f8[];
     const int K = a.K, N = a.N;
-    const int nb = K >> 5, nbc = (nb + 3) >> 2, nbp = nbc * 4;
-    int* codes = lds_f8;                                 // [MT][8][nbp] words
-    float* scales = (float*)(lds_f8 + MT * 8 * nbp);   // [MT][nbp]
+    const int nb = K >> 5, nbc = (nb + 3) >> 2, nbp = nbc * 4, nbs = nbp + 4;
+    int* codes = lds_f8;                                 // [MT][8][nbs] words (wg_prologue's Q8_0 layout)
+    float* scales = (float*)(lds_f8 + MT * 8 * nbs);   // [MT][nbp]
     const int m0 = blockIdx.y * MT;
     const v4i* qs = (const v4i*)a.qs;
     const uint16_t* hdr = (const uint16_t*)a.hdr;
@@ -244,7 +244,7 @@ __global__ __launch_bounds__(256) void fused_q8_kernel(FusedGemvArgs a) {
             v4f sw[MT];
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                cw[m] = *(const v4i*)(codes + (size_t)(m * 8 + l) * nbp + 4 * c);
+                cw[m] = *(const v4i*)(codes + (size_t)(m * 8 + l) * nbs + 4 * c);
                 sw[m] = *(const v4f*)(scales + (size_t)m * nbp + 4 * c);
             }
 #pragma unroll
@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256) void fused_q8_kernel(FusedGemvArgs a) {
     wg_prologue_code<PRO, kCodecQ8, J>(a, m0 < a.M, pin, nullptr, codes, scales);
 #pragma unroll
     for (int m = 1; m < MT; ++m)
-        wg_prologue<PRO, kCodecQ8, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + (size_t)m * 8 * nbp,
+        wg_prologue<PRO, kCodecQ8, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + (size_t)m * 8 * nbs,
                                    scales + (size_t)m * nbp);
     for (int R = R0; R < groups; R += nwaves) {
         if (R != R0) load_chunk(R, 0, ca);
@@ -710,7 +710,8 @@ template <int PRO, int EPI>
 hipError_t launch_q8(const FusedGemvArgs& a, hipStream_t s) {
     const int K = a.K;
     int mt = a.M == 1 ? 1 : (a.M == 2 ? 2 : 4);
-    auto lds = [&](int t) { return (size_t)t * ((K / 32 + 3) / 4 * 4) * 36; };  // codes 8 words + scale per block
+    // codes 8 words per block (rows padded by 4 words) + a scale per block
+    auto lds = [&](int t) { return (size_t)t * (8 * ((K / 32 + 3) / 4 * 4 + 4) + (K / 32 + 3) / 4 * 4) * 4; };
     const size_t groups = (a.N + 7) / 8;
     const unsigned wgs = (unsigned)std::min<size_t>((groups + 3) / 4, 256 * 8);
     dim3 g(wgs, (unsigned)((a.M + mt - 1) / mt));

@@ -37,13 +37,13 @@ template <int PRO, int J>
 __global__ __launch_bounds__(256) void q8_act_rows_kernel(FusedGemvArgs a, int8_t* __restrict__ aq,
                                                           float* __restrict__ ad) {
     extern __shared__ int lds_q8a[];
-    const int K = a.K, nb = K >> 5, nbp = (nb + 3) & ~3;
-    int* codes = lds_q8a;                         // [8][nbp] words, the prologue's layout
-    float* scales = (float*)(lds_q8a + 8 * nbp);  // [nbp]
+    const int K = a.K, nb = K >> 5, nbp = (nb + 3) & ~3, nbs = nbp + 4;
+    int* codes = lds_q8a;                         // [8][nbs] words, the prologue's layout
+    float* scales = (float*)(lds_q8a + 8 * nbs);  // [nbp]
     const int m = blockIdx.x;
     wg_prologue<PRO, kCodecQ8, J>(a, m, true, nullptr, codes, scales);  // ends with a barrier
     int* out = (int*)(aq + (size_t)m * K);
-    for (int wd = threadIdx.x; wd < (K >> 2); wd += blockDim.x) out[wd] = codes[(wd & 7) * nbp + (wd >> 3)];
+    for (int wd = threadIdx.x; wd < (K >> 2); wd += blockDim.x) out[wd] = codes[(wd & 7) * nbs + (wd >> 3)];
     for (int b = threadIdx.x; b < nb; b += blockDim.x) ad[(size_t)m * nb + b] = scales[b];
 }
 
@@ -235,7 +235,7 @@ hipError_t launch_rows(const FusedGemvArgs& a, const int8_t* aq, const float* ad
 template <int PRO>
 hipError_t launch_act_rows(const FusedGemvArgs& a, int8_t* aq, float* ad, hipStream_t s) {
     const int K = a.K, nbp = ((K >> 5) + 3) & ~3;
-    const size_t lds = (size_t)nbp * 36;
+    const size_t lds = (size_t)(8 * (nbp + 4) + nbp) * 4;
     const dim3 g((unsigned)a.M);
 #define ZG_Q8A(J) hipLaunchKernelGGL((q8_act_rows_kernel<PRO, J>), g, dim3(256), lds, s, a, aq, ad)
     if (K <= 1024) ZG_Q8A(1);
