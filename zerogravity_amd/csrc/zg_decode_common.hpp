@@ -55,13 +55,13 @@ constexpr int kRecWords = 36;  // Q4_K record: 32 dwords of code bytes + {xs_lo,
 //     codes [8][nbp + 4] words (word l of block b at l * (nbp + 4) + b,
 //     nbp = K/32 rounded up to 4; the 4 words of padding put the 8 words of
 //     a block in different LDS banks), scales [K/32].
-//   Q8_1 (quantization.rs:37-61, Q4_1 pairing): as Q8_0 (codes [8][nb8],
-//     nb8 = K/32 rounded up to 8), plus per block s = f16(sum of codes *
+//   Q8_1 (quantization.rs:37-61, Q4_1 pairing): as Q8_0 (codes [8][nb8 + 4],
+//     nb8 = K/32 rounded up to 8, the rows padded out of one bank), plus per block s = f16(sum of codes *
 //     unrounded d) in `extra`.
 //   Q8_K (quantization.rs:66-92, Q6_K pairing): per 256-block (one
 //     wavefront) the first element of largest magnitude gives the signed
 //     max, inv = -127/max, d = 1/inv in `extra` [K/256], codes as Q8_0 laid
-//     out lane-major (word w of block sb at (w%8)*(K/32) + 8sb + w/8), and
+//     out lane-major (word w of block sb at (w%8)*(K/32 + 4) + 8sb + w/8), and
 //     the sums of 16 codes in `bsums` [K/16].
 //   F32: the values themselves, floats [K] at `codes`.
 //   Q4_K: per 32-group int16 fixed point, xq = rint(v*32767/amax), with the
@@ -190,9 +190,10 @@ __device__ void wg_prologue_code(const FusedGemvArgs& a, bool valid, const ProIn
             csum += __shfl_xor(csum, 2, 64);
             if (k < K) {
                 // lane-major: the 8 words a consumer lane reads per 256-block
-                // (word w of block sb: lane w % 8, slot w / 8) are adjacent
+                // (word w of block sb: lane w % 8, slot w / 8) are adjacent;
+                // lane rows K/32 + 4 words apart (out of one bank)
                 const int w = (k >> 2) & 63, sb = k >> 8;
-                codes[(size_t)(w & 7) * (K >> 5) + sb * 8 + (w >> 3)] = (int)word;
+                codes[(size_t)(w & 7) * ((K >> 5) + 4) + sb * 8 + (w >> 3)] = (int)word;
                 if ((lane & 3) == 0) bsums[k >> 4] = csum;
                 if (lane == 0) extra[k >> 8] = d;
             }
@@ -215,10 +216,11 @@ __device__ void wg_prologue_code(const FusedGemvArgs& a, bool valid, const ProIn
             }
             csum = group8_sum_all(csum);
             if (k < K) {
-                // lane-major: word l * nb8 + block (nb8 = blocks rounded to
-                // 8), so that two 16-byte reads serve an 8-block chunk
+                // lane-major: word l * (nb8 + 4) + block (nb8 = blocks
+                // rounded to 8), so that two 16-byte reads serve an 8-block
+                // chunk
                 const int nb8 = ((K >> 5) + 7) & ~7;
-                codes[(size_t)l * nb8 + (k >> 5)] = (int)word;
+                codes[(size_t)l * (nb8 + 4) + (k >> 5)] = (int)word;
                 if (l == 0) {
                     scales[k >> 5] = f16_roundtrip(d);
                     extra[k >> 5] = f16_roundtrip(csum * d);

@@ -313,9 +313,9 @@ __global__ __launch_bounds__(256) void fused_q41_kernel(FusedGemvArgs a) {
     constexpr int QC = 4;
     extern __shared__ int lds_f41[];
     const int K = a.K, N = a.N;
-    const int nb = K >> 5, nbc8 = (nb + 7) >> 3, nb8 = nbc8 * 8;
-    int* codes = lds_f41;                                // [MT][8][nb8] words
-    float* scales = (float*)(lds_f41 + MT * 8 * nb8);    // [MT][nb8]
+    const int nb = K >> 5, nbc8 = (nb + 7) >> 3, nb8 = nbc8 * 8, nbs8 = nb8 + 4;
+    int* codes = lds_f41;                                // [MT][8][nbs8] words (wg_prologue's Q8_1 layout)
+    float* scales = (float*)(lds_f41 + MT * 8 * nbs8);   // [MT][nb8]
     float* sums = scales + MT * nb8;                     // [MT][nb8]
     const int m0 = blockIdx.y * MT;
     const v4i* qs = (const v4i*)a.qs;
@@ -354,7 +354,7 @@ __global__ __launch_bounds__(256) void fused_q41_kernel(FusedGemvArgs a) {
             float xs[MT][8], xu[MT][8];
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                const v4i* cp = (const v4i*)(codes + (size_t)(m * 8 + l) * nb8 + 8 * c);
+                const v4i* cp = (const v4i*)(codes + (size_t)(m * 8 + l) * nbs8 + 8 * c);
                 const v4f* sp = (const v4f*)(scales + (size_t)m * nb8 + 8 * c);
                 const v4f* up = (const v4f*)(sums + (size_t)m * nb8 + 8 * c);
 #pragma unroll
@@ -394,7 +394,7 @@ __global__ __launch_bounds__(256) void fused_q41_kernel(FusedGemvArgs a) {
     wg_prologue_code<PRO, kCodecQ81, J>(a, m0 < a.M, pin, nullptr, codes, scales, sums);
 #pragma unroll
     for (int m = 1; m < MT; ++m)
-        wg_prologue<PRO, kCodecQ81, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + (size_t)m * 8 * nb8,
+        wg_prologue<PRO, kCodecQ81, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + (size_t)m * 8 * nbs8,
                                        scales + (size_t)m * nb8, sums + (size_t)m * nb8);
     for (int R = R0; R < groups; R += nwaves) {
         if (R != R0) load_chunk(R, 0, ca);
@@ -439,9 +439,9 @@ __global__ __launch_bounds__(256) void fused_q6k_kernel(FusedGemvArgs a) {
     // is not consumed.
     constexpr int QS = 4;
     extern __shared__ int lds_f6[];
-    const int K = a.K, N = a.N, nsb = K >> 8;
-    int* codes = lds_f6;                                 // [MT][K/4] words
-    float* dk = (float*)(lds_f6 + MT * (K >> 2));        // [MT][nsb]
+    const int K = a.K, N = a.N, nsb = K >> 8, ls = (K >> 5) + 4, ms = 8 * ls;
+    int* codes = lds_f6;                                 // [MT][8][K/32 + 4] words (wg_prologue's Q8_K layout)
+    float* dk = (float*)(lds_f6 + MT * ms);              // [MT][nsb]
     int* bs = (int*)(dk + MT * nsb);                     // [MT][K/16]
     const int m0 = blockIdx.y * MT;
     const uint32_t* qa = (const uint32_t*)a.qs;
@@ -490,7 +490,7 @@ __global__ __launch_bounds__(256) void fused_q6k_kernel(FusedGemvArgs a) {
             const int so0 = sbyte(ck.S[i], 2 * l), so1 = sbyte(ck.S[i], 2 * l + 1);
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                const int* cl = codes + m * (K >> 2) + (size_t)l * (K >> 5) + sb * 8;
+                const int* cl = codes + m * ms + (size_t)l * ls + sb * 8;
                 const v4i c0 = *(const v4i*)cl, c1 = *(const v4i*)(cl + 4);
                 const int cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
                 int iacc = 0;
@@ -514,7 +514,7 @@ __global__ __launch_bounds__(256) void fused_q6k_kernel(FusedGemvArgs a) {
     wg_prologue_code<PRO, kCodecQ8K, J>(a, m0 < a.M, pin, nullptr, codes, nullptr, dk, bs);
 #pragma unroll
     for (int m = 1; m < MT; ++m)
-        wg_prologue<PRO, kCodecQ8K, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * (K >> 2), nullptr,
+        wg_prologue<PRO, kCodecQ8K, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * ms, nullptr,
                                        dk + m * nsb, bs + m * (K >> 4));
     for (int R = R0; R < groups; R += nwaves) {
         if (R != R0) load_chunk(R, 0, ca);
@@ -601,8 +601,9 @@ hipError_t launch_codec(const FusedGemvArgs& a, int type, hipStream_t s) {
     const int K = a.K;
     const int mt = type == kF32 ? 1 : (a.M == 1 ? 1 : (a.M == 2 ? 2 : 4));
     size_t per;
-    if (type == kQ4_1) per = (size_t)((K / 32 + 7) / 8 * 8) * 40;  // codes 8 words + scale + sum per block
-    else if (type == kQ6_K) per = (size_t)K + (size_t)(K / 256) * 4 + (size_t)(K / 16) * 4;
+    // codes 8 words per block (lane rows padded by 4 words) + scale + sum per block
+    if (type == kQ4_1) per = (size_t)(8 * ((K / 32 + 7) / 8 * 8 + 4) + 2 * ((K / 32 + 7) / 8 * 8)) * 4;
+    else if (type == kQ6_K) per = (size_t)8 * (K / 32 + 4) * 4 + (size_t)(K / 256) * 4 + (size_t)(K / 16) * 4;
     else per = (size_t)K * 4;
     const size_t lds = per * mt;
     const size_t units = type == kF32 ? ((size_t)a.N + 1) / 2 : ((size_t)a.N + 7) / 8;
