@@ -22,7 +22,9 @@
 // register buffers, the next QC chunks requested before the current ones
 // are multiplied.  Every activation word read from LDS serves R weight rows
 // and every weight word MT activation rows: the fused kernels read all the
-// weights again for each group of four rows.
+// weights again for each group of four rows.  q8_mfma_kernel forms the same
+// per-word dots on the int8 matrix cores (below); launch_rows picks one of
+// the two by shape.
 #include <type_traits>
 
 #include "zg_decode_common.hpp"
@@ -185,16 +187,163 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
+// The same products on the int8 matrix cores (v_mfma_i32_16x16x32_i8, one
+// Q8_0 block per instruction).  A: row i = 8 mm + l is word l of activation
+// row 2 p + mm (pair p): its codes at k = 4l .. 4l+3 and zeros elsewhere,
+// so D[i][j] is exactly the int32 dot of word l with output row j's word l,
+// the reference's per-lane dot.  B: lane (j, kq) holds the block's words
+// 2kq and 2kq+1 of output row n0 + j; in the tile layout those are two
+// adjacent 16-byte pieces carrying the chunk's four blocks (one 32-byte
+// load, the tile's chunk read whole by the wave).  D: lane (j, kq) holds
+// rows 4kq .. 4kq+3, i.e. activation row 2p + kq/2 and words
+// l = 4(kq & 1) .. +3, which share one scale wd[n][b] * xs[m][b]: one
+// product per four fmas instead of one per fma.  After the last block,
+// lanes kq and kq ^ 1 (16 apart) add words l and l + 4, and the even lane
+// forms ((s0 + s2) + (s1 + s3)): the reference's tree, so the result is
+// q8_rows_kernel's bit for bit.
+template <int MP, int R, int EPI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void q8_mfma_kernel(
+    FusedGemvArgs a, const int8_t* __restrict__ aq, const float* __restrict__ ad) {
+    constexpr int MT = 2 * MP;
+    extern __shared__ int lds_q8m[];
+    const int K = a.K, N = a.N, M = a.M;
+    const int nb = K >> 5, nbc = (nb + 3) >> 2, nbp = nbc * 4, nbs = nbp + 4, kw = K >> 2;
+    int* codes = lds_q8m;                              // [MT][8][nbs] words
+    float* scales = (float*)(lds_q8m + MT * 8 * nbs);  // [MT][nbp]
+    const int m0 = blockIdx.y * MT;
+    const int lane = threadIdx.x & 63, j = lane & 15, kq = lane >> 4;
+    const int tiles = (N + 15) >> 4, tasks = (tiles + R - 1) / R;
+    const int nwaves = gridDim.x * 4;
+    const v4i* qs = (const v4i*)a.qs;
+    const uint16_t* hdr = (const uint16_t*)a.hdr;
+
+    struct Chunk {
+        v4i w0[R], w1[R];
+        uint2 h[R];
+    };
+    // rows past N re-read row N - 1, chunks past the end the last one:
+    // loaded, never consumed
+    auto load = [&](int T, int c, Chunk& ck) {
+        c = min(c, nbc - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = min(min(T * R + r, tiles - 1) * 16 + j, N - 1);
+            const v4i* p = qs + ((size_t)(n >> 3) * nbc + c) * 64 + (n & 7) * 8 + 2 * kq;
+            ck.w0[r] = load_nt(p);
+            ck.w1[r] = load_nt(p + 1);
+            ck.h[r] = *(const uint2*)(hdr + (size_t)n * nbp + 4 * c);
+        }
+    };
+    const int T0 = blockIdx.x * 4 + (threadIdx.x >> 6);
+    Chunk ca, cb;
+    if (T0 < tasks) load(T0, 0, ca);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- stage the MT activation rows (zero past M) into LDS
+    const int nq = MT * (kw >> 2);
+    for (int p = threadIdx.x; p < nq; p += blockDim.x) {
+        const int m = p / (kw >> 2), wd = 4 * (p - m * (kw >> 2));
+        v4i v = {0, 0, 0, 0};
+        if (m0 + m < M) v = *(const v4i*)(aq + (size_t)(m0 + m) * K + 4 * wd);
+        const int b = wd >> 3, l0 = wd & 7;
+        int* dst = codes + (m * 8 + l0) * nbs + b;
+        dst[0] = v.x;
+        dst[nbs] = v.y;
+        dst[2 * nbs] = v.z;
+        dst[3 * nbs] = v.w;
+    }
+    for (int i = threadIdx.x; i < MT * nbp; i += blockDim.x) {
+        const int m = i / nbp, b = i - m * nbp;
+        scales[i] = (m0 + m < M && b < nb) ? ad[(size_t)(m0 + m) * nb + b] : 0.0f;
+    }
+    __syncthreads();
+
+    const int l = j & 7, mm = j >> 3;  // this lane's A row: word l of activation row 2p + mm
+    const bool lo = l == 2 * kq, hi = l == 2 * kq + 1;
+    float acc[MP][R][4];
+    auto consume = [&](const Chunk& ck, int c) {
+        const int nbi = min(4, nb - 4 * c);
+        float wd[R][4];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            wd[r][0] = f16_to_f32((uint16_t)(ck.h[r].x & 0xffffu));
+            wd[r][1] = f16_to_f32((uint16_t)(ck.h[r].x >> 16));
+            wd[r][2] = f16_to_f32((uint16_t)(ck.h[r].y & 0xffffu));
+            wd[r][3] = f16_to_f32((uint16_t)(ck.h[r].y >> 16));
+        }
+        auto blocks = [&](auto full) {
+#pragma unroll
+            for (int p = 0; p < MP; ++p) {
+                const v4i xv = *(const v4i*)(codes + ((2 * p + mm) * 8 + l) * nbs + 4 * c);
+                const v4f sv = *(const v4f*)(scales + (2 * p + (kq >> 1)) * nbp + 4 * c);
+                const int xw[4] = {xv.x, xv.y, xv.z, xv.w};
+                const float xs[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+                for (int bi = 0; bi < 4; ++bi) {
+                    if (decltype(full)::value || bi < nbi) {
+                        const long av = (long)(uint64_t)(lo ? (uint32_t)xw[bi] : 0u) |
+                                        (long)((uint64_t)(hi ? (uint32_t)xw[bi] : 0u) << 32);
+#pragma unroll
+                        for (int r = 0; r < R; ++r) {
+                            const int w0 = bi == 0 ? ck.w0[r].x : bi == 1 ? ck.w0[r].y : bi == 2 ? ck.w0[r].z
+                                                                                                : ck.w0[r].w;
+                            const int w1 = bi == 0 ? ck.w1[r].x : bi == 1 ? ck.w1[r].y : bi == 2 ? ck.w1[r].z
+                                                                                                : ck.w1[r].w;
+                            const long bv = (long)(uint64_t)(uint32_t)w0 | (long)((uint64_t)(uint32_t)w1 << 32);
+                            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, v4i{0, 0, 0, 0}, 0, 0, 0);
+                            const float scale = wd[r][bi] * xs[bi];
+                            acc[p][r][0] = fmaf((float)d.x, scale, acc[p][r][0]);
+                            acc[p][r][1] = fmaf((float)d.y, scale, acc[p][r][1]);
+                            acc[p][r][2] = fmaf((float)d.z, scale, acc[p][r][2]);
+                            acc[p][r][3] = fmaf((float)d.w, scale, acc[p][r][3]);
+                        }
+                    }
+                }
+            }
+        };
+        if (nbi == 4) blocks(std::true_type{});
+        else blocks(std::false_type{});
+    };
+
+    for (int T = T0; T < tasks; T += nwaves) {
+        if (T != T0) load(T, 0, ca);
+#pragma unroll
+        for (int p = 0; p < MP; ++p)
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) acc[p][r][t] = 0.0f;
+        for (int c = 0; c < nbc; c += 2) {
+            if (c + 1 < nbc) load(T, c + 1, cb);
+            consume(ca, c);
+            if (c + 1 >= nbc) break;
+            if (c + 2 < nbc) load(T, c + 2, ca);
+            consume(cb, c + 1);
+        }
+#pragma unroll
+        for (int p = 0; p < MP; ++p)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float s[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) s[t] = acc[p][r][t] + __shfl_xor(acc[p][r][t], 16, 64);  // l + (l + 4)
+                const float v = (s[0] + s[2]) + (s[1] + s[3]);
+                const int tile = T * R + r, n = tile * 16 + j, m = m0 + 2 * p + (kq >> 1);
+                if (!(kq & 1) && tile < tiles && n < N && m < M) epilogue(a, m, n, v, EPI);
+            }
+    }
+}
+
 size_t rows_lds(int mt, int K) {
     const int nbp = ((K >> 5) + 3) & ~3;
     return (size_t)mt * (8 * (nbp + 4) + nbp) * 4;  // 8 code words (padded rows) and a scale per block
 }
 
 template <int EPI>
-hipError_t launch_rows(const FusedGemvArgs& a, const int8_t* aq, const float* ad, hipStream_t s) {
+hipError_t launch_valu_rows(const FusedGemvArgs& a, const int8_t* aq, const float* ad, hipStream_t s) {
     const int M = a.M, K = a.K;
     const size_t groups = ((size_t)a.N + 7) / 8;
-    // R rows groups per wave while the waves stay plentiful: an activation
+    // R row groups per wave while the waves stay plentiful: an activation
     // word read from LDS then serves R weight rows
     int R = groups >= 4 * 4096 ? 4 : (groups >= 2 * 2048 ? 2 : 1);
     // MT activation rows per workgroup: as many as M needs up to 16, within
@@ -230,6 +379,54 @@ hipError_t launch_rows(const FusedGemvArgs& a, const int8_t* aq, const float* ad
 #undef ZG_Q8R_R
 #undef ZG_Q8R
     return hipGetLastError();
+}
+
+template <int EPI>
+hipError_t launch_mfma_rows(const FusedGemvArgs& a, const int8_t* aq, const float* ad, hipStream_t s) {
+    const int M = a.M, K = a.K;
+    const size_t tiles = ((size_t)a.N + 15) / 16;
+    // R 16-row tiles per wave task while the waves stay plentiful
+    const int R = tiles >= 2 * 4096 ? 2 : 1;
+    const unsigned wgs = (unsigned)std::min<size_t>(((tiles + R - 1) / R + 3) / 4, 1024);
+    // MT activation rows per workgroup: as many as M needs up to 16, within
+    // 64 KB of LDS (two workgroups per CU), and fewer when the tiles alone
+    // would leave CUs idle (more workgroups along M, each re-reading the
+    // weights from cache)
+    int mt = 16;
+    while (mt > 4 && mt / 2 >= M) mt >>= 1;
+    while (mt > 4 && rows_lds(mt, K) > 65536) mt >>= 1;
+    while (mt > 4 && (size_t)wgs * ((M + mt - 1) / mt) < 256) mt >>= 1;
+    if (rows_lds(mt, K) > 65536) return hipErrorInvalidValue;
+    const unsigned gy = (unsigned)((M + mt - 1) / mt);
+    if (gy > 65535) return hipErrorInvalidValue;
+    const dim3 g(wgs, gy);
+    const size_t lds = rows_lds(mt, K);
+#define ZG_Q8M(MP_, R_) hipLaunchKernelGGL((q8_mfma_kernel<MP_, R_, EPI>), g, dim3(256), lds, s, a, aq, ad)
+#define ZG_Q8M_R(MP_)               \
+    if (R == 2) ZG_Q8M(MP_, 2);     \
+    else ZG_Q8M(MP_, 1);
+    if (mt == 16) {
+        ZG_Q8M_R(8)
+    } else if (mt == 8) {
+        ZG_Q8M_R(4)
+    } else {
+        ZG_Q8M_R(2)
+    }
+#undef ZG_Q8M_R
+#undef ZG_Q8M
+    return hipGetLastError();
+}
+
+// The matrix-core kernel takes 16-row tiles per wave task, the VALU kernel
+// 8-row groups: with few tiles the VALU kernel keeps twice the waves busy,
+// and with many rows or many tiles the matrix cores' cheaper products win
+// (measured per shape: the 2B-shaped projections and the LM head at 8, 16
+// and 32 rows).
+template <int EPI>
+hipError_t launch_rows(const FusedGemvArgs& a, const int8_t* aq, const float* ad, hipStream_t s) {
+    const size_t tiles = ((size_t)a.N + 15) / 16;
+    const bool mfma = tiles >= 512 || (a.M >= 16 && tiles >= 256) || (a.M >= 32 && tiles >= 128);
+    return mfma ? launch_mfma_rows<EPI>(a, aq, ad, s) : launch_valu_rows<EPI>(a, aq, ad, s);
 }
 
 template <int PRO>
