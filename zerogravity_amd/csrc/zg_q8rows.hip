@@ -278,24 +278,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 const v4f sv = *(const v4f*)(scales + (2 * p + (kq >> 1)) * nbp + 4 * c);
                 const int xw[4] = {xv.x, xv.y, xv.z, xv.w};
                 const float xs[4] = {sv.x, sv.y, sv.z, sv.w};
+                // the pair's four blocks go to the matrix cores together,
+                // then their products join the chains in block order
 #pragma unroll
-                for (int bi = 0; bi < 4; ++bi) {
-                    if (decltype(full)::value || bi < nbi) {
-                        const long av = (long)(uint64_t)(lo ? (uint32_t)xw[bi] : 0u) |
-                                        (long)((uint64_t)(hi ? (uint32_t)xw[bi] : 0u) << 32);
+                for (int r = 0; r < R; ++r) {
+                    v4i d[4];
 #pragma unroll
-                        for (int r = 0; r < R; ++r) {
+                    for (int bi = 0; bi < 4; ++bi) {
+                        if (decltype(full)::value || bi < nbi) {
+                            const long av = (long)(uint64_t)(lo ? (uint32_t)xw[bi] : 0u) |
+                                            (long)((uint64_t)(hi ? (uint32_t)xw[bi] : 0u) << 32);
                             const int w0 = bi == 0 ? ck.w0[r].x : bi == 1 ? ck.w0[r].y : bi == 2 ? ck.w0[r].z
                                                                                                 : ck.w0[r].w;
                             const int w1 = bi == 0 ? ck.w1[r].x : bi == 1 ? ck.w1[r].y : bi == 2 ? ck.w1[r].z
                                                                                                 : ck.w1[r].w;
                             const long bv = (long)(uint64_t)(uint32_t)w0 | (long)((uint64_t)(uint32_t)w1 << 32);
-                            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, v4i{0, 0, 0, 0}, 0, 0, 0);
+                            d[bi] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, v4i{0, 0, 0, 0}, 0, 0, 0);
+                        }
+                    }
+#pragma unroll
+                    for (int bi = 0; bi < 4; ++bi) {
+                        if (decltype(full)::value || bi < nbi) {
                             const float scale = wd[r][bi] * xs[bi];
-                            acc[p][r][0] = fmaf((float)d.x, scale, acc[p][r][0]);
-                            acc[p][r][1] = fmaf((float)d.y, scale, acc[p][r][1]);
-                            acc[p][r][2] = fmaf((float)d.z, scale, acc[p][r][2]);
-                            acc[p][r][3] = fmaf((float)d.w, scale, acc[p][r][3]);
+                            acc[p][r][0] = fmaf((float)d[bi].x, scale, acc[p][r][0]);
+                            acc[p][r][1] = fmaf((float)d[bi].y, scale, acc[p][r][1]);
+                            acc[p][r][2] = fmaf((float)d[bi].z, scale, acc[p][r][2]);
+                            acc[p][r][3] = fmaf((float)d[bi].w, scale, acc[p][r][3]);
                         }
                     }
                 }
