@@ -163,6 +163,42 @@ def test_gemv_device_f32_decode_kernels(kern, torch_cuda, kind, N, K, M):
     assert worst <= REL_TOL, worst
 
 
+# Q8_0 beyond 4 rows on ragged shapes: K not a multiple of 128 (a last
+# chunk of 1-3 blocks, checked per block), N not a multiple of 8 or 16 (a
+# last row group or tile past N), both row kernels (the int8 matrix-core
+# one takes 128+ tiles of 16 rows at 32+ rows, 256+ at 16+, 512+ at any
+# count; the v_dot4 one the rest), and K = 8192 (four rows per workgroup,
+# the LDS bound).  f32 input through the coded-once activation, bf16 through
+# the prepared activation; bit-exact against the oracle either way.
+@pytest.mark.parametrize("N,K,M", [(1001, 1056, 9), (777, 96, 33), (2050, 1056, 32), (8200, 96, 16),
+                                   (4100, 4128, 17), (600, 8192, 20)])
+@pytest.mark.parametrize("x_dtype", [L.F32, L.BF16])
+def test_q8_rows_ragged_shapes_bit_exact(kern, torch_cuda, N, K, M, x_dtype):
+    torch = torch_cuda
+    if x_dtype == L.BF16 and M > 64:
+        pytest.skip("bf16 activations take at most 64 rows")
+    w, h = weight(kern, synth.Q8_0, N, K)
+    rng = np.random.default_rng(N * 3 + K + M + x_dtype)
+    xf = rng.standard_normal((M, K)).astype(np.float32)
+    if x_dtype == L.BF16:
+        xf, xb = synth.bf16_round(xf)
+        x_d = torch.from_numpy(xb.view(np.int16)).cuda()
+    else:
+        x_d = torch.from_numpy(xf).cuda()
+    gamma = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    g_d = torch.from_numpy(gamma).cuda()
+    y_d = torch.full((M, N), np.nan, dtype=torch.float32, device="cuda")
+    stream = _stream(torch)
+    kern.ctx.check(L.lib().zg_gemv_device(kern.ctx.h, h.h, x_d.data_ptr(), x_dtype, M, g_d.data_ptr(), 1e-6,
+                                          y_d.data_ptr(), stream))
+    torch.cuda.synchronize()
+    y = y_d.cpu().numpy()
+    for m in range(M):
+        xn = O.rms_norm(xf[m], gamma, 1e-6)
+        ref = O.matvec(synth.Q8_0, w.reshape(-1), N, K, xn)
+        assert np.array_equal(y[m].view(np.uint32), ref.view(np.uint32)), (m, float(np.max(np.abs(y[m] - ref))))
+
+
 def test_q8_activation_codes_bit_exact(kern, torch_cuda):
     # The prepared Q8_0 activation (RMSNorm + dynamic coding) must equal the
     # oracle's codes and f16-rounded scales bit for bit.
