@@ -165,6 +165,28 @@ def test_mixed_integer_codec_batched_rows_bit_exact(kern):
     m.close()
 
 
+def test_q8_model_wide_batch_bit_exact(kern):
+    """An all-Q8_0 model at B = 33: every projection takes the coded-once
+    activation and the Q8_0 rows kernels (the 4096-row LM head the int8
+    matrix-core one, 256 tiles at 32+ rows; the narrower projections the
+    v_dot4 one), in the step's own prologue forms (RMS, gated RMS, SiLU
+    product) and epilogues; rows at either end and in the middle equal their
+    own oracle sessions bit for bit."""
+    g = dict(TINY, vocab=4096)
+    t = qwen35.synthetic_tensors(g, gguf.Q8_0, seed=34)
+    m = qwen35.QwenModelHip(g, t, kernel=kern)
+    B, steps = 33, 3
+    s = m.session(max_batch=B, max_context=64, kv_dtype=L.BF16)
+    toks = np.random.default_rng(8).integers(0, g["vocab"], (steps, B)).astype(np.uint32)
+    got = [s.step(toks[i])[0] for i in range(steps)]
+    for b in (0, 16, 32):
+        o = O.Model(g, t).session(kv_bf16=True)
+        for i in range(steps):
+            ref = o.forward(int(toks[i, b]))
+            assert same_bits(got[i][b], ref), (b, i, float(np.max(np.abs(got[i][b] - ref))))
+    m.close()
+
+
 @pytest.mark.parametrize("B", [3, 6])
 def test_mixed_q4k_model_greedy_matches_oracle(kern, B):
     """Q4_K projections beside the integer codecs, at B = 1 and B = 3 or 6
