@@ -511,8 +511,9 @@ def bench_decode(args):
 
 def bench_decode_q8(args, mixed=False):
     """The decode step of the 2B-shaped model with Q8_0 weights (the codec of
-    the reference's pinned checkpoints): B=1 and B=4 greedy positions after a
-    random 2048-token prefix, fused GEMVs in the reference's exact dot order.
+    the reference's pinned checkpoints): B=1, 4 and 32 greedy positions
+    after a random 2048-token prefix, GEMVs in the reference's exact dot
+    order (32 rows: the coded-once activation and the Q8_0 rows kernels).
     mixed: the mixed-quant layout (Q6_K embedding/LM head, V and FFN down,
     Q4_1 attention gate, F32 GDN alpha/beta) over Q8_0."""
     import torch
@@ -527,7 +528,7 @@ def bench_decode_q8(args, mixed=False):
     name = "Q8_0 + Q6_K/Q4_1/F32" if mixed else "Q8_0"
     log(f"2B {name} model resident ({time.perf_counter() - t0:.1f} s)")
     res = {}
-    for B in (1, 4):
+    for B in (1, 4, 32):
         total_ms, per = run_decode(model, torch, B, args.prefix, args.steps, args.warmup, seed=B)
         ms = total_ms / args.steps
         byts = step_bytes(g, gguf.Q8_0, B, args.prefix + args.warmup + args.steps // 2, tensors if mixed else None)
@@ -545,7 +546,7 @@ def bench_decode_q8(args, mixed=False):
         "scaling": "weak", "vs_baseline": None, "dtype": "integer codecs, int8 dots, f32 accumulate",
         "data": f"synthetic (seeded random-init {name} GGUF weights, random prefix state)",
         "config": {"workload": f"2B-shaped {name} greedy decode", "prefix": args.prefix, "kv_cache": "bf16",
-                   "b1": res[1], "b4": res[4]},
+                   "b1": res[1], "b4": res[4], "b32": res[32]},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "whole B=1 step (weights, GDN state, KV cache per step)"},
