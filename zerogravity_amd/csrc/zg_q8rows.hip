@@ -376,7 +376,8 @@ hipError_t launch_valu_rows(const FusedGemvArgs& a, const int8_t* aq, const floa
     else if (R == 2) ZG_Q8R(MT_, 2); \
     else ZG_Q8R(MT_, 1);
     if (mt == 16) {
-        // four row groups of 16 rows would spill: two
+        // 16 activation rows with four row groups per wave spill registers:
+        // two groups
         if (R >= 2) ZG_Q8R(16, 2);
         else ZG_Q8R(16, 1);
     } else if (mt == 8) {
