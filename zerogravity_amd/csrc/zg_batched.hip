@@ -381,14 +381,21 @@ __global__ __launch_bounds__(64 * kM16Waves) __attribute__((amdgpu_waves_per_eu(
         }
         if (UPW * MBW >= 10) reduce_ss();  // wide units: before the main loads hold their registers
     }
+    // lane l carries activation row m0 + 16 mb + l % 16 (xh16_index): rows
+    // past M are the tiles' zero padding, so those lanes take zeros without
+    // a load (a 2-row batch reads an eighth of the block)
     h8v xa[UPW][MBW][4];
 #pragma unroll
-    for (int u = 0; u < UPW; ++u)
+    for (int mb = 0; mb < MBW; ++mb) {
+        const bool live = m0 + 16 * mb + r16 < a.M;
 #pragma unroll
-        for (int mb = 0; mb < MBW; ++mb)
+        for (int u = 0; u < UPW; ++u)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                xa[u][mb][i] = xh[(((size_t)(MBW * blockIdx.y + mb) * nunits + ub + u) * 4 + i) * 64 + lane];
+            for (int i = 0; i < 4; ++i) {
+                xa[u][mb][i] = h8v{0, 0, 0, 0, 0, 0, 0, 0};
+                if (live) xa[u][mb][i] = xh[(((size_t)(MBW * blockIdx.y + mb) * nunits + ub + u) * 4 + i) * 64 + lane];
+            }
+    }
     auto wrow = [&](int vt) {
         if (EPI == EPI_GLU) {
             const int j = min(vt * 8 + (r16 & 7), nout - 1);
