@@ -567,8 +567,10 @@ def bench_gemv_one(kern, torch, handles, kind, N, K, M, steps, warmup, rng, path
     """One (codec, N, K, M) point of the sweep, rotating over the weight
     copies.  path "fused": zg_gemv_device on the f32 values of the bf16
     activation -- the decode step's kernels, the RMSNorm in their prologue
-    (one row: the int8-MFMA GEMV; 2-4 rows: the fused GEMV; more, Q4_K: the
-    f16 activation tiles and the f16 MFMA GEMM, two launches), all timed.
+    (Q4_K: one row the int8-MFMA GEMV, from two rows the f16 activation
+    tiles and the f16 MFMA GEMM, two launches; Q8_0: up to 4 rows the fused
+    GEMV, beyond the coded-once activation and the rows kernels, two
+    launches), all timed.
     path "prepared": the region path, the bf16 activation RMS-normalised and
     coded once (zg_act_prepare_device, untimed), then zg_gemv_prepared_device
     timed alone.  After a warm pass, `steps` launches are captured in one

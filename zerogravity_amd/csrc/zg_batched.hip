@@ -1,5 +1,5 @@
-// Batched-row decode projections on f16 MFMA (the session step's Q4_K rows
-// from 2 up; zg_gemv_device from 5) and the prompt-sized GEMMs.
+// Batched-row decode projections on f16 MFMA (Q4_K from 2 rows up, in the
+// session step and zg_gemv_device) and the prompt-sized GEMMs.
 #include "zg_decode_common.hpp"
 
 namespace zg {

@@ -1,7 +1,8 @@
 #pragma once
-// Kernels of the fused decode GEMV (one launch per projection at B <= 4,
-// except one Q4_K row, which takes the int8 GEMV, and a session step's 2-4
-// Q4_K rows, which take the batched f16 kernels)
+// Kernels of the fused decode GEMV (one launch per projection at B <= 4:
+// the codecs other than Q4_K, and Q4_K at 2-4 rows through
+// zg_gemv_device_fused; one Q4_K row takes the int8 GEMV, and 2+ Q4_K rows
+// of zg_gemv_device and the session step the batched f16 kernels)
 // and their launch templates; zg_fused_<prologue>.hip instantiate one
 // prologue each so that the instantiations compile in parallel.
 #include "zg_decode_common.hpp"
