@@ -501,9 +501,10 @@ size_t zg_gemv_greedy_parts(const zg_weight* w);
  * arguments, kernels and bit-identical results, with the activation scratch
  * in a static per-device array of 4 MiB (held until the process ends)
  * instead of a context buffer.  Limits: m_rows 1..64 and the prepared
- * activation within 4 MiB (ZG_E_LIMIT otherwise); Q4_K with f32 input and
- * more than 4 rows needs the weight's batched tile layout, which one
- * zg_gemv_device call with more than 4 rows builds (ZG_E_STATE otherwise).
+ * activation within 4 MiB (ZG_E_LIMIT otherwise); Q4_K with f32 input, 2
+ * or more rows and a shape the 16-row kernel does not take needs the
+ * weight's batched tile layout, which one zg_gemv_device call of that shape
+ * builds (ZG_E_STATE otherwise).
  * Every call on a device shares that device's array, which keeps the last
  * call's contents.  Calls are ordered on it: each waits on an event the
  * previous call on that device (any stream, thread or context) recorded

@@ -647,7 +647,7 @@ int zg_gemv_device_noalloc(zg_ctx* ctx, const zg_weight* w, const void* x, int x
     if (batched) {
         if (w->dw.type == zg::kQ4_K && !w->dw.qs_t && !zg::batched16_supported(m_rows, w->dw.K, w->dw.N, zg::EPI_STORE))
             return fail(ctx, ZG_E_STATE,
-                        "weight has no batched tile layout yet: a zg_gemv_device call with more than 4 rows builds it");
+                        "weight has no batched tile layout yet: a zg_gemv_device call of this shape with 2 or more rows builds it");
         if (zg::batched_scratch_bytes(m_rows, w->dw.K) > kStaticScratchBytes)
             return fail(ctx, ZG_E_LIMIT, "activation exceeds the 4 MiB static scratch");
     } else if (!fused) {
