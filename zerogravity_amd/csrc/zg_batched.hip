@@ -572,8 +572,8 @@ __global__ __launch_bounds__(64 * kM16Waves) __attribute__((amdgpu_waves_per_eu(
             }
             pass(wA, hA, tb);
         }
-    } else {
-        static_assert(LOOP != 2 || UPW <= 2, "two weight buffers fit the registers up to UPW = 2");
+    } else if constexpr (LOOP == 2) {
+        static_assert(UPW <= 2, "two weight buffers fit the registers up to UPW = 2");
         v4u wB[UPW][TMAX], hB[NH][TMAX];
         for (int tb = t0; tb < t1; tb += 2 * TMAX) {
             const int tb2 = tb + TMAX;
@@ -584,6 +584,25 @@ __global__ __launch_bounds__(64 * kM16Waves) __attribute__((amdgpu_waves_per_eu(
             issue(wA, hA, tb2 + TMAX);
             __builtin_amdgcn_sched_barrier(0);
             pass(wB, hB, tb2);
+        }
+    } else {
+        // LOOP 3: three buffers, the next two passes' weights in flight
+        // while one is multiplied (long runs: a 151936-row LM head)
+        static_assert(UPW <= 2, "three weight buffers fit the registers up to UPW = 2");
+        v4u wB[UPW][TMAX], hB[NH][TMAX], wC[UPW][TMAX], hC[NH][TMAX];
+        issue(wB, hB, t0 + TMAX);
+        for (int tb = t0; tb < t1; tb += 3 * TMAX) {
+            issue(wC, hC, tb + 2 * TMAX);
+            __builtin_amdgcn_sched_barrier(0);
+            pass(wA, hA, tb);
+            if (tb + TMAX >= t1) break;
+            issue(wA, hA, tb + 3 * TMAX);
+            __builtin_amdgcn_sched_barrier(0);
+            pass(wB, hB, tb + TMAX);
+            if (tb + 2 * TMAX >= t1) break;
+            issue(wB, hB, tb + 4 * TMAX);
+            __builtin_amdgcn_sched_barrier(0);
+            pass(wC, hC, tb + 2 * TMAX);
         }
     }
 }
@@ -600,7 +619,12 @@ static hipError_t launch_mfma16_m(const FusedGemvArgs& a, const _Float16* xh, hi
     const int upw = a.K / 1024, nout = EPI == EPI_GLU ? a.N / 2 : a.N, vr = EPI == EPI_GLU ? 8 : 16;
     const int gy = (a.M + 16 * MBW - 1) / (16 * MBW);
     const int nvt = (nout + vr - 1) / vr, G = std::min(nvt, std::max(1, 256 / gy)), per = (nvt + G - 1) / G;
-    const int loop = per <= m16_tiles_per_pass(upw, 0, MBW) ? 0 : (upw <= 2 ? 2 : 1);
+    const int tmax = m16_tiles_per_pass(upw, 0, MBW);
+    // one pass; passes with the next one's weights in flight; with the next
+    // two (four or more passes of a plain store: the residual and SwiGLU
+    // epilogues leave no room for a third buffer); one buffer where two do
+    // not fit (UPW > 2)
+    const int loop = per <= tmax ? 0 : (upw <= 2 ? (per >= 4 * tmax && EPI == EPI_STORE ? 3 : 2) : 1);
     const dim3 g((unsigned)G, (unsigned)gy);
     const h8v* x = (const h8v*)xh;
 #define ZG_M16(U)                                                                                                  \
@@ -609,9 +633,12 @@ static hipError_t launch_mfma16_m(const FusedGemvArgs& a, const _Float16* xh, hi
             hipLaunchKernelGGL((mfma16_q4k_kernel<EPI, U, 0, MBW>), g, dim3(64 * kM16Waves), 0, s, a, x);          \
         } else if (loop == 1) {                                                                                    \
             hipLaunchKernelGGL((mfma16_q4k_kernel<EPI, U, 1, MBW>), g, dim3(64 * kM16Waves), 0, s, a, x);          \
-        } else {                                                                                                   \
+        } else if (loop == 2) {                                                                                    \
             if constexpr (U <= 2)                                                                                  \
                 hipLaunchKernelGGL((mfma16_q4k_kernel<EPI, U, 2, MBW>), g, dim3(64 * kM16Waves), 0, s, a, x);      \
+        } else {                                                                                                   \
+            if constexpr (U <= 2 && EPI == EPI_STORE)                                                              \
+                hipLaunchKernelGGL((mfma16_q4k_kernel<EPI, U, 3, MBW>), g, dim3(64 * kM16Waves), 0, s, a, x);      \
         }                                                                                                          \
         break;
     switch (upw) {
