@@ -494,7 +494,8 @@ int zg_gemv_prepared_device(zg_ctx* ctx, const zg_weight* w, size_t m_rows, cons
 // rows takes the coded-once activation and one weight stream per 16 rows.
 static bool device_batched(const zg_weight* w, size_t m_rows, int pro) {
     return (m_rows >= 2 && w->dw.type == zg::kQ4_K) ||
-           (m_rows > 4 && w->dw.type == zg::kQ8_0 && zg::q8_rows_supported(w->dw.K, w->dw.N, pro));
+           (m_rows > 4 && w->dw.type == zg::kQ8_0 && zg::q8_rows_supported(w->dw.K, w->dw.N, pro)) ||
+           (m_rows > 4 && w->dw.type == zg::kQ6_K && zg::q6k_rows_supported(w->dw.K, w->dw.N, pro));
 }
 
 int zg_gemv_device(zg_ctx* ctx, const zg_weight* w, const void* x, int x_dtype, size_t m_rows, const float* gamma,

@@ -804,6 +804,7 @@ static void launch_act16(const FusedGemvArgs& a, int mpad, _Float16* xh, hipStre
 
 hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* scratch, hipStream_t s) {
     if (w.type == kQ8_0) return q8_rows_gemv(w, args, scratch, s);
+    if (w.type == kQ6_K) return q6k_rows_gemv(w, args, scratch, s);
     if (w.type != kQ4_K || w.K % 256 || w.K > 8192 || args.M <= 0 || args.M > 65535 * 32) return hipErrorInvalidValue;
     if (args.pro == PRO_GATED && args.group != 128) return hipErrorInvalidValue;
     const bool m16 = batched16_supported((size_t)args.M, w.K, w.N, args.epi);

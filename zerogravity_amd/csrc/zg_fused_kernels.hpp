@@ -430,7 +430,10 @@ __device__ __forceinline__ int sbyte(const v4u& v, int idx) {
 // int32 sum is sum(code * local scale * q8) (4-element dot products, one
 // local scale each) minus 32 * (bsum * scale) over the contiguous 16-groups
 // 2L and 2L+1; lane = fma((float)int, d_a * d_w, lane); the Q8_0 lane tree.
-template <int MT, int J, int PRO, int EPI>
+// STAGED: the MT activation rows come already coded (q6k_act_rows_kernel,
+// the same prologue function) from a.staged, one row per ms + nsb + K/16
+// words in the LDS layout below, instead of being coded per workgroup.
+template <int MT, int J, int PRO, int EPI, bool STAGED = false>
 __global__ __launch_bounds__(256) void fused_q6k_kernel(FusedGemvArgs a) {
     // superblocks stream in chunks of QS through two register buffers, the
     // next chunk's loads issued before the current one is consumed;
@@ -507,16 +510,32 @@ __global__ __launch_bounds__(256) void fused_q6k_kernel(FusedGemvArgs a) {
             }
         }
     };
-    ProIn<J> pin;
-    wg_prologue_load<PRO, J>(a, m0, m0 < a.M, pin);
     const int R0 = blockIdx.x * 4 + (threadIdx.x >> 6);
     Chunk ca, cb;
-    load_chunk(R0, 0, ca);
-    wg_prologue_code<PRO, kCodecQ8K, J>(a, m0 < a.M, pin, nullptr, codes, nullptr, dk, bs);
+    if constexpr (STAGED) {
+        // the first chunk's weights go out first, then the rows' copy (rows
+        // past M zero); the copy's words keep the LDS layout, so a row is
+        // one contiguous run of rw words
+        load_chunk(R0, 0, ca);
+        const int rw = ms + nsb + (K >> 4);
+        for (int i = threadIdx.x; i < MT * rw; i += blockDim.x) {
+            const int m = i / rw, o = i - m * rw;
+            const int v = m0 + m < a.M ? a.staged[(size_t)(m0 + m) * rw + o] : 0;
+            if (o < ms) codes[m * ms + o] = v;
+            else if (o < ms + nsb) ((int*)dk)[m * nsb + o - ms] = v;
+            else bs[m * (K >> 4) + o - ms - nsb] = v;
+        }
+        __syncthreads();
+    } else {
+        ProIn<J> pin;
+        wg_prologue_load<PRO, J>(a, m0, m0 < a.M, pin);
+        load_chunk(R0, 0, ca);
+        wg_prologue_code<PRO, kCodecQ8K, J>(a, m0 < a.M, pin, nullptr, codes, nullptr, dk, bs);
 #pragma unroll
-    for (int m = 1; m < MT; ++m)
-        wg_prologue<PRO, kCodecQ8K, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * ms, nullptr,
-                                       dk + m * nsb, bs + m * (K >> 4));
+        for (int m = 1; m < MT; ++m)
+            wg_prologue<PRO, kCodecQ8K, J>(a, m0 + m, m0 + m < a.M, nullptr, codes + m * ms, nullptr,
+                                           dk + m * nsb, bs + m * (K >> 4));
+    }
     for (int R = R0; R < groups; R += nwaves) {
         if (R != R0) load_chunk(R, 0, ca);
         const int row = R * 8 + rl;

@@ -220,6 +220,7 @@ struct FusedGemvArgs {
     double* rms_ss_out = nullptr;
     const double* rms_ss_in = nullptr;
     int rms_ss_n = 0;
+    const int* staged = nullptr;  // Q6_K beyond 4 rows: the rows coded once (q6k_rows_gemv)
     void* xh_out = nullptr;      // EPI_GLU, batched: f16 tiled product
     const void* xh_in = nullptr;  // batched: f16 tiled activation ready (no activation kernel)
     int xh_rows = 0;              // activation kernel: f16 row-major [M][K] instead of MFMA tiles
@@ -283,6 +284,12 @@ hipError_t batched_gemv(const DeviceWeight& w, const FusedGemvArgs& a, void* scr
 // PLAIN; epilogues STORE and RESID.  batched_gemv routes Q8_0 here.
 bool q8_rows_supported(size_t K, size_t N, int pro);
 hipError_t q8_rows_gemv(const DeviceWeight& w, const FusedGemvArgs& a, void* scratch, hipStream_t s);
+// Q6_K beyond 4 rows: each row coded once to Q8_K into `scratch` (within
+// batched_scratch_bytes), then the fused Q6_K kernel on up to 16 staged rows
+// per workgroup; bit-identical to the 1-4 row kernel.  batched_gemv routes
+// Q6_K here.
+bool q6k_rows_supported(size_t K, size_t N, int pro);
+hipError_t q6k_rows_gemv(const DeviceWeight& w, const FusedGemvArgs& a, void* scratch, hipStream_t s);
 // The same GEMV on an activation act_prepare_for already prepared.
 hipError_t q8_rows_prepared(const DeviceWeight& w, size_t M, const void* prepared, float* y, hipStream_t s);
 // The prompt-sized GEMM on f16 A tiles `xh` (act16_kernel's layout, or the

@@ -25,9 +25,15 @@
 // weights again for each group of four rows.  q8_mfma_kernel forms the same
 // per-word dots on the int8 matrix cores (below); launch_rows picks one of
 // the two by shape.
+//
+// Q6_K beyond 4 rows takes the same two-launch form: q6k_act_rows_kernel
+// codes each row once to Q8_K (the prologue function the fused Q6_K kernel
+// runs per workgroup), and fused_q6k_kernel in its staged mode copies up to
+// 16 coded rows per workgroup instead of coding them, so one weight stream
+// serves them all with the kernel's own per-row arithmetic.
 #include <type_traits>
 
-#include "zg_decode_common.hpp"
+#include "zg_fused_kernels.hpp"
 
 namespace zg {
 
@@ -452,6 +458,58 @@ hipError_t launch_act_rows(const FusedGemvArgs& a, int8_t* aq, float* ad, hipStr
     return hipGetLastError();
 }
 
+// One row of the Q8_K coding per workgroup: codes (lane rows padded), the
+// per-256 scales and the 16-element code sums, contiguous in the fused
+// Q6_K kernel's LDS order (its staged copy is one run of words per row).
+template <int PRO, int J>
+__global__ __launch_bounds__(256) void q6k_act_rows_kernel(FusedGemvArgs a, int* __restrict__ out) {
+    extern __shared__ int lds_q6a[];
+    const int K = a.K, nsb = K >> 8, ms = 8 * ((K >> 5) + 4), rw = ms + nsb + (K >> 4);
+    const int m = blockIdx.x;
+    wg_prologue<PRO, kCodecQ8K, J>(a, m, true, nullptr, lds_q6a, nullptr, (float*)(lds_q6a + ms),
+                                   lds_q6a + ms + nsb);  // ends with a barrier
+    int* o = out + (size_t)m * rw;
+    for (int i = threadIdx.x; i < rw; i += blockDim.x) o[i] = lds_q6a[i];
+}
+
+size_t q6k_row_bytes(int K) { return (size_t)(8 * ((K >> 5) + 4) + (K >> 8) + (K >> 4)) * 4; }
+
+template <int EPI>
+hipError_t launch_q6k_rows(const FusedGemvArgs& a, hipStream_t s) {
+    const int M = a.M, K = a.K;
+    const size_t groups = ((size_t)a.N + 7) / 8;
+    const unsigned wgs = (unsigned)std::min<size_t>((groups + 3) / 4, 256 * 8);
+    // up to 16 rows per workgroup within 64 KB of LDS, fewer when the row
+    // groups alone would leave CUs idle
+    int mt = 16;
+    while (mt > 4 && mt / 2 >= M) mt >>= 1;
+    while (mt > 4 && q6k_row_bytes(K) * mt > 65536) mt >>= 1;
+    while (mt > 4 && (size_t)wgs * ((M + mt - 1) / mt) < 256) mt >>= 1;
+    if (q6k_row_bytes(K) * mt > 65536) return hipErrorInvalidValue;
+    const unsigned gy = (unsigned)((M + mt - 1) / mt);
+    if (gy > 65535) return hipErrorInvalidValue;
+    const dim3 g(wgs, gy);
+    const size_t lds = q6k_row_bytes(K) * mt;
+    if (mt == 16) hipLaunchKernelGGL((fused_q6k_kernel<16, 1, PRO_PLAIN, EPI, true>), g, dim3(256), lds, s, a);
+    else if (mt == 8) hipLaunchKernelGGL((fused_q6k_kernel<8, 1, PRO_PLAIN, EPI, true>), g, dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((fused_q6k_kernel<4, 1, PRO_PLAIN, EPI, true>), g, dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int PRO>
+hipError_t launch_q6k_act_rows(const FusedGemvArgs& a, int* out, hipStream_t s) {
+    const int K = a.K;
+    const dim3 g((unsigned)a.M);
+    const size_t lds = q6k_row_bytes(K);
+#define ZG_Q6A(J) hipLaunchKernelGGL((q6k_act_rows_kernel<PRO, J>), g, dim3(256), lds, s, a, out)
+    if (K <= 1024) ZG_Q6A(1);
+    else if (K <= 2048) ZG_Q6A(2);
+    else if (K <= 4096) ZG_Q6A(4);
+    else ZG_Q6A(8);
+#undef ZG_Q6A
+    return hipGetLastError();
+}
+
 }  // namespace
 
 bool q8_rows_supported(size_t K, size_t N, int pro) {
@@ -501,6 +559,38 @@ hipError_t q8_rows_prepared(const DeviceWeight& w, size_t M, const void* prepare
     const int8_t* aq = (const int8_t*)prepared;
     const float* ad = (const float*)((const char*)prepared + ((M * w.K + 255) & ~(size_t)255));
     return launch_rows<EPI_STORE>(a, aq, ad, s);
+}
+
+bool q6k_rows_supported(size_t K, size_t N, int pro) {
+    return pro != PRO_GATED_PRE && fused_gemv_supported(kQ6_K, K, N, pro) && q6k_row_bytes((int)K) * 4 <= 65536;
+}
+
+hipError_t q6k_rows_gemv(const DeviceWeight& w, const FusedGemvArgs& args, void* scratch, hipStream_t s) {
+    if (w.type != kQ6_K || !q6k_rows_supported(w.K, w.N, args.pro) || args.M <= 0 || !scratch ||
+        (args.epi != EPI_STORE && args.epi != EPI_RESID) || args.xh_in || args.xh_out || args.rparts ||
+        (args.parts && args.splits > 1) || args.rms_tiles_out || args.rms_ss_in || args.amax || args.emb_qs ||
+        args.gate_dt)
+        return hipErrorInvalidValue;
+    if (args.pro == PRO_GATED && (args.group <= 0 || args.group > 1024 || (args.group & (args.group - 1)) ||
+                                  w.K % (size_t)args.group))
+        return hipErrorInvalidValue;
+    FusedGemvArgs a = args;
+    a.qs = w.qs;
+    a.hdr = w.hdr;
+    a.K = (int)w.K;
+    a.N = (int)w.N;
+    int* st = (int*)scratch;
+    hipError_t e;
+    switch (a.pro) {
+    case PRO_RMS: e = launch_q6k_act_rows<PRO_RMS>(a, st, s); break;
+    case PRO_GATED: e = launch_q6k_act_rows<PRO_GATED>(a, st, s); break;
+    case PRO_SILU_MUL: e = launch_q6k_act_rows<PRO_SILU_MUL>(a, st, s); break;
+    case PRO_PLAIN: e = launch_q6k_act_rows<PRO_PLAIN>(a, st, s); break;
+    default: return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return e;
+    a.staged = st;
+    return a.epi == EPI_RESID ? launch_q6k_rows<EPI_RESID>(a, s) : launch_q6k_rows<EPI_STORE>(a, s);
 }
 
 }  // namespace zg

@@ -437,10 +437,12 @@ int step(zg_session* s, size_t B, const uint32_t* tokens, float* logits, uint32_
             return zg::batched_gemv(w->dw, f, s->xh, st);
         }
         if (epi == zg::EPI_RESID && y == s->x) rms_ready = false;
-        // Q8_0 beyond four rows: the activation coded once into the scratch
-        // (no tiles are pending there: only Q4_K projections consume them),
-        // then one weight stream per 16 rows
-        if (B > 4 && w->dw.type == zg::kQ8_0 && !xh_in && !xh_out && zg::q8_rows_supported(w->dw.K, w->dw.N, pro))
+        // Q8_0 and Q6_K beyond four rows: the activation coded once into the
+        // scratch (no tiles are pending there: only Q4_K projections consume
+        // them), then one weight stream per 16 rows
+        if (B > 4 && !xh_in && !xh_out &&
+            ((w->dw.type == zg::kQ8_0 && zg::q8_rows_supported(w->dw.K, w->dw.N, pro)) ||
+             (w->dw.type == zg::kQ6_K && zg::q6k_rows_supported(w->dw.K, w->dw.N, pro))))
             return zg::batched_gemv(w->dw, f, s->xh, st);
         return zg::fused_gemv(w->dw, f, st);
     };
