@@ -446,8 +446,8 @@ int zg_session_fill_random(zg_session* s, size_t rows, size_t prefix, uint64_t s
  * for bf16 activations, M <= 65536 for f32.  f32 activations run the decode
  * step's own kernels: the prologue inside the GEMV (Q8_0, Q4_1, Q6_K and F32
  * bit-identical to the CPU at any M; Q4_K for one row, on the int8 matrix
- * cores; Q8_0 beyond 4 rows codes each activation row once and streams the
- * weights once per 16 rows), and for Q4_K with M >= 2 the activation rounded to f16 and an f16
+ * cores; Q8_0 and Q6_K beyond 4 rows code each activation row once and
+ * stream the weights once per 16 rows), and for Q4_K with M >= 2 the activation rounded to f16 and an f16
  * MFMA GEMM (f32 accumulate; within 1e-3 relative of the CPU), LDS-staged
  * for prompt-sized M >= 1024.
  * No counterpart in the reference beyond MatVecKernel::try_execute; this is
