@@ -99,6 +99,28 @@ def test_gemv_device_rms_prologue_bit_exact(kern, torch_cuda, kind, N, K, M):
         assert same_bits(y[m], ref), (m, float(np.max(np.abs(y[m] - ref))))
 
 
+@pytest.mark.parametrize("N,K,M", [(777, 512, 17), (3001, 1536, 33), (64, 8192, 6)])
+def test_q6k_staged_rows_bit_exact(kern, torch_cuda, N, K, M):
+    """Q6_K beyond 4 rows: each activation row coded once, then up to 16
+    staged rows per workgroup; N not a multiple of 8 (a last row group past
+    N), a partial last group of activation rows, K = 8192 (four rows per
+    workgroup, the LDS bound): bit-exact against the oracle."""
+    torch = torch_cuda
+    w, h = weight(kern, synth.Q6_K, N, K)
+    rng = np.random.default_rng(M * 17 + N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    x_d, g_d = torch.from_numpy(x).cuda(), torch.from_numpy(gamma).cuda()
+    y_d = torch.full((M, N), np.nan, dtype=torch.float32, device="cuda")
+    kern.ctx.check(L.lib().zg_gemv_device(kern.ctx.h, h.h, x_d.data_ptr(), L.F32, M, g_d.data_ptr(), 1e-6,
+                                          y_d.data_ptr(), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    y = y_d.cpu().numpy()
+    for m in range(M):
+        ref = O.matvec(synth.Q6_K, w.reshape(-1), N, K, O.rms_norm(x[m], gamma, 1e-6))
+        assert same_bits(y[m], ref), (m, float(np.max(np.abs(y[m] - ref))))
+
+
 def test_q8_k_coding_edge_blocks_bit_exact(kern):
     # an all-zero superblock (d = 0), a block whose largest magnitude appears
     # twice with opposite signs (the first wins), and ties at the rounding
