@@ -63,7 +63,7 @@ def _seeded_state(g, prefix, seed):
 
 
 STEPS = 128  # 128 greedy steps
-CHECKED = {1: (0,), 32: (0, 4, 9, 13, 18, 22, 27, 31)}
+CHECKED = {1: (0,), 3: (0, 2), 32: (0, 4, 9, 13, 18, 22, 27, 31)}  # B=3: the batched f16 kernels below 16 rows
 _RUNS = {}
 
 
@@ -105,7 +105,8 @@ def _device_run(model_2b, B):
     return _RUNS[B]
 
 
-@pytest.mark.parametrize("B,checked", [(1, (0,)), (32, (0, 4)), (32, (9, 13)), (32, (18, 22)), (32, (27, 31))])
+@pytest.mark.parametrize("B,checked", [(1, (0,)), (3, (0, 2)), (32, (0, 4)), (32, (9, 13)), (32, (18, 22)),
+                                       (32, (27, 31))])
 def test_config5_2b_q4k_decode_from_2048_prefix(model_2b, B, checked):
     """128 greedy steps, each checked row against its own oracle session
     (split over several tests so that each stays within the per-test time
